@@ -1,0 +1,141 @@
+// Internal declarations shared by the HIP kernels and the C ABI of liblarql_hip.
+//
+// Device layouts ("dev layouts") are what a registered weight looks like in HBM.
+// Every quantized format is repacked once, at registration, from the reference's
+// byte layout (LC/src/cpu/ops/q4_common.rs) into structure-of-arrays form so the
+// kernels issue 16-byte aligned, wave-contiguous loads:
+//
+//   Q4_K (148 B / 256 elems in the reference):
+//     qs  : u8 [rows][S*128]      nibble bytes, reference order within a super-block
+//     hdr : u32x4 [rows][S]       {d|dmin<<16, sc[0..3], sc[4..7], min bytes}
+//   Q6_K (210 B / 256):
+//     ql  : u8 [rows][S*128]      low nibbles
+//     qh  : u8 [rows][S*64]       high 2-bit pairs
+//     sc  : i8 [rows][S*16]       sub-block scales
+//     d   : f16 [rows][S]         super-block scale
+//   Q4_0 (18 B / 32):
+//     qs  : u8 [rows][B*16]       nibble bytes
+//     d   : f16 [rows][B]         block scale
+//   Q8_0 (trait form: i8 + separate f32 scales):
+//     qs  : i8 [rows][cols]
+//     d   : f32 [rows][B]
+// where S = cols/256 and B = cols/32.  The algorithmic byte count of every
+// format stays the reference's; the Q4_K device layout drops the four unused
+// scale bytes of each super-block (144 of 148 bytes are moved).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/larql_hip.h"
+
+namespace larql {
+
+// ── errors ──────────────────────────────────────────────────────────────
+struct Error {
+    int code;
+    std::string msg;
+};
+
+#define LARQL_HIP_CHECK(expr)                                                        \
+    do {                                                                             \
+        hipError_t _e = (expr);                                                      \
+        if (_e != hipSuccess)                                                        \
+            throw ::larql::Error{LARQL_HIP_ERR_DEVICE,                               \
+                                 std::string(#expr) + ": " + hipGetErrorString(_e)}; \
+    } while (0)
+
+[[noreturn]] inline void fail(int code, const std::string& msg) { throw Error{code, msg}; }
+
+// ── device layouts ──────────────────────────────────────────────────────
+struct DevWeight {
+    int format = 0;          // larql_quant_format
+    size_t rows = 0, cols = 0;
+    void* base = nullptr;    // one device allocation holding all sub-arrays
+    size_t bytes = 0;
+    // sub-array pointers into `base`
+    uint8_t* qs = nullptr;   // Q4_K/Q4_0 nibbles, Q6_K ql, Q8_0 int8
+    uint8_t* qh = nullptr;   // Q6_K high bits
+    int8_t* sc = nullptr;    // Q6_K scales
+    uint4* hdr = nullptr;    // Q4_K headers
+    void* d = nullptr;       // Q6_K/Q4_0 f16 scales, Q8_0 f32 scales
+    // registry keys
+    const void* host_ptr = nullptr;
+    size_t host_len = 0;
+    uint64_t host_fp = 0;    // sampled content fingerprint of the host bytes
+    uint64_t handle = 0;
+};
+
+// FNV-1a over the whole buffer when it is small, else over 64 evenly spaced
+// 64-byte samples: a cache hit on a reused host address with different bytes
+// re-uploads instead of serving stale weights.
+uint64_t host_fingerprint(const void* data, size_t len);
+
+size_t ref_row_bytes(int format, size_t cols);   // bytes per row in the reference layout
+size_t dev_layout_bytes(int format, size_t rows, size_t cols);
+void dev_layout_carve(DevWeight& w);              // set sub-array pointers from base
+
+// Repack reference-layout bytes already on the device (`raw`) into `w`.
+void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scales, hipStream_t s);
+
+// ── KV cache ────────────────────────────────────────────────────────────
+struct KVCache {
+    size_t num_layers = 0, max_seq = 0, num_kv = 0, head_dim = 0;
+    size_t current_len = 0;
+    std::vector<__half*> k, v;   // per layer [max_seq][num_kv][head_dim]
+};
+
+// ── context ─────────────────────────────────────────────────────────────
+struct DeviceBuf {
+    void* p = nullptr;
+    size_t n = 0;
+};
+
+}  // namespace larql
+
+struct larql_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::recursive_mutex mu;
+    std::string last_error;
+    std::string device_name;
+    int num_cus = 0;
+    uint64_t next_handle = 1;
+    std::unordered_map<uint64_t, larql::DevWeight> weights;
+    std::map<std::pair<const void*, size_t>, uint64_t> by_host;
+    // reusable device staging buffers for host-pointer calls
+    larql::DeviceBuf stage_in, stage_in2, stage_out, stage_raw, scratch;
+    larql::KVCache kv;
+    // decode-step workspace
+    larql::DeviceBuf ws;
+};
+
+namespace larql {
+
+void* ensure(larql_hip_ctx* c, DeviceBuf& b, size_t bytes);
+const DevWeight& lookup(larql_hip_ctx* c, uint64_t handle);
+// Find or create a device copy of reference-layout host bytes (Metal-style cache
+// keyed by host pointer and length, LC/src/metal/buffers.rs:37-85).
+const DevWeight& cached_weight(larql_hip_ctx* c, int format, const void* data, size_t len,
+                               const float* q8_scales, size_t rows, size_t cols);
+
+// ── kernel launchers (device pointers; enqueue only) ───────────────────
+void launch_q4k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s);
+void launch_q6k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s);
+void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
+                        size_t m, hipStream_t s);
+void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
+                      size_t m, hipStream_t s);
+void launch_quantize_q8(const float* x, size_t n, size_t m, int8_t* q8, float* scales, hipStream_t s);
+void launch_quantize_weights(int format, const float* x, size_t n, void* out, float* q8_scales, hipStream_t s);
+
+}  // namespace larql

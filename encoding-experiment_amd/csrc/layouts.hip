@@ -1,0 +1,135 @@
+// Registration-time repack: reference byte layouts -> device SoA layouts.
+//
+// Reference layouts (LC/src/cpu/ops/q4_common.rs):
+//   Q4_0  18 B / 32  : [f16 scale][16 B nibbles]                              (:50-81)
+//   Q4_K 148 B / 256 : [f16 d][f16 dmin][12 B sc (0..7 used)][4 B mins][128 B]  (:104-170)
+//   Q6_K 210 B / 256 : [128 B ql][64 B qh][16 x i8 scales][f16 d]              (:179-239)
+//   Q8_0 trait form  : i8 [rows*cols] + f32 scales [rows*cols/32]          (LC/src/pipeline.rs:22-27)
+#include "larql_hip_internal.h"
+
+namespace larql {
+
+size_t ref_row_bytes(int format, size_t cols) {
+    switch (format) {
+        case LARQL_Q4_0: return cols / 32 * 18;
+        case LARQL_Q4_K: return cols / 256 * 148;
+        case LARQL_Q6_K: return cols / 256 * 210;
+        case LARQL_Q8_0: return cols;
+        default: return 0;
+    }
+}
+
+static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+size_t dev_layout_bytes(int format, size_t rows, size_t cols) {
+    switch (format) {
+        case LARQL_Q4_0: return align256(rows * cols / 2) + align256(rows * (cols / 32) * 2);
+        case LARQL_Q4_K: return align256(rows * cols / 2) + align256(rows * (cols / 256) * 16);
+        case LARQL_Q6_K:
+            return align256(rows * cols / 2) + align256(rows * cols / 4) + align256(rows * cols / 16) +
+                   align256(rows * (cols / 256) * 2);
+        case LARQL_Q8_0: return align256(rows * cols) + align256(rows * (cols / 32) * 4);
+        default: return 0;
+    }
+}
+
+void dev_layout_carve(DevWeight& w) {
+    uint8_t* p = static_cast<uint8_t*>(w.base);
+    const size_t R = w.rows, K = w.cols;
+    switch (w.format) {
+        case LARQL_Q4_0:
+            w.qs = p; p += align256(R * K / 2);
+            w.d = p;
+            break;
+        case LARQL_Q4_K:
+            w.qs = p; p += align256(R * K / 2);
+            w.hdr = reinterpret_cast<uint4*>(p);
+            break;
+        case LARQL_Q6_K:
+            w.qs = p; p += align256(R * K / 2);
+            w.qh = p; p += align256(R * K / 4);
+            w.sc = reinterpret_cast<int8_t*>(p); p += align256(R * K / 16);
+            w.d = p;
+            break;
+        case LARQL_Q8_0:
+            w.qs = p; p += align256(R * K);
+            w.d = p;
+            break;
+        default: break;
+    }
+}
+
+// One thread per Q4_K super-block.  Source blocks sit at 148-byte offsets, so they
+// are 4-byte aligned whenever the raw buffer is.
+__global__ void repack_q4k_kernel(const uint32_t* __restrict__ raw, uint8_t* __restrict__ qs,
+                                  uint4* __restrict__ hdr, size_t nblocks) {
+    size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint32_t* s = raw + b * 37;
+    hdr[b] = make_uint4(s[0], s[1], s[2], s[4]);
+    uint4* q = reinterpret_cast<uint4*>(qs + b * 128);
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = make_uint4(s[5 + 4 * i], s[6 + 4 * i], s[7 + 4 * i], s[8 + 4 * i]);
+}
+
+// One thread per Q6_K super-block (210-byte stride: 2-byte aligned source).
+__global__ void repack_q6k_kernel(const uint16_t* __restrict__ raw, uint8_t* __restrict__ ql,
+                                  uint8_t* __restrict__ qh, int8_t* __restrict__ sc,
+                                  uint16_t* __restrict__ d, size_t nblocks) {
+    size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint16_t* s = raw + b * 105;
+    uint16_t* l = reinterpret_cast<uint16_t*>(ql + b * 128);
+    uint16_t* h = reinterpret_cast<uint16_t*>(qh + b * 64);
+    uint16_t* c = reinterpret_cast<uint16_t*>(sc + b * 16);
+    for (int i = 0; i < 64; i++) l[i] = s[i];
+    for (int i = 0; i < 32; i++) h[i] = s[64 + i];
+    for (int i = 0; i < 8; i++) c[i] = s[96 + i];
+    d[b] = s[104];
+}
+
+// One thread per Q4_0 block (18-byte stride: 2-byte aligned source).
+__global__ void repack_q4_0_kernel(const uint16_t* __restrict__ raw, uint8_t* __restrict__ qs,
+                                   uint16_t* __restrict__ d, size_t nblocks) {
+    size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint16_t* s = raw + b * 9;
+    d[b] = s[0];
+    uint16_t* q = reinterpret_cast<uint16_t*>(qs + b * 16);
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = s[1 + i];
+}
+
+void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scales, hipStream_t s) {
+    const int T = 256;
+    switch (w.format) {
+        case LARQL_Q4_K: {
+            size_t nb = w.rows * (w.cols / 256);
+            repack_q4k_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
+                reinterpret_cast<const uint32_t*>(raw), w.qs, w.hdr, nb);
+            break;
+        }
+        case LARQL_Q6_K: {
+            size_t nb = w.rows * (w.cols / 256);
+            repack_q6k_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
+                reinterpret_cast<const uint16_t*>(raw), w.qs, w.qh, w.sc, static_cast<uint16_t*>(w.d), nb);
+            break;
+        }
+        case LARQL_Q4_0: {
+            size_t nb = w.rows * (w.cols / 32);
+            repack_q4_0_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
+                reinterpret_cast<const uint16_t*>(raw), w.qs, static_cast<uint16_t*>(w.d), nb);
+            break;
+        }
+        case LARQL_Q8_0: {
+            LARQL_HIP_CHECK(hipMemcpyAsync(w.qs, raw, w.rows * w.cols, hipMemcpyDeviceToDevice, s));
+            LARQL_HIP_CHECK(hipMemcpyAsync(w.d, q8_scales, w.rows * (w.cols / 32) * sizeof(float),
+                                           hipMemcpyDeviceToDevice, s));
+            break;
+        }
+        default: fail(LARQL_HIP_ERR_UNSUPPORTED, "repack: unsupported format");
+    }
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace larql

@@ -1,0 +1,282 @@
+"""Python binding of liblarql_hip — the MI355X backend for LARQL's quantized path.
+
+``HipBackend`` mirrors the reference trait ``ComputeBackend``
+(larql-main/crates/larql-compute/src/backend.rs:24-164): the same method names,
+argument meaning and ``Option`` behaviour — a method returns ``None`` when the
+backend cannot serve the request, and the reason is in ``last_error()``.
+Construct with ``strict=True`` to raise ``LarqlHipError`` instead.
+
+Importing this module loads ``liblarql_hip.so`` (built next to this file by
+``make -C encoding-experiment_amd``) and raises if it is missing: there is no
+CPU fallback behind this binding.
+
+The ``*_dev`` methods take device-resident tensors (anything with
+``data_ptr()``, e.g. torch tensors on ``cuda``) and only enqueue work.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liblarql_hip.so")
+
+Q4_0, Q4_K, Q4_KF, Q6_K, Q8_0 = 0, 1, 2, 3, 4
+FORMAT_NAMES = {Q4_0: "Q4_0", Q4_K: "Q4_K", Q4_KF: "Q4_KF", Q6_K: "Q6_K", Q8_0: "Q8_0"}
+
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_DEVICE, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5
+
+_P = ctypes.c_void_p
+_SZ = ctypes.c_size_t
+_I = ctypes.c_int
+_U64 = ctypes.c_uint64
+
+
+class LarqlHipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+# name -> (restype, argtypes); every symbol declared in include/larql_hip.h
+SIGNATURES = {
+    "larql_hip_ctx_create": (_I, [_I, ctypes.POINTER(_P)]),
+    "larql_hip_ctx_destroy": (None, [_P]),
+    "larql_hip_last_error": (ctypes.c_char_p, [_P]),
+    "larql_hip_name": (ctypes.c_char_p, []),
+    "larql_hip_device_info": (_I, [_P, ctypes.c_char_p, _SZ]),
+    "larql_hip_has_q4": (_I, [_P]),
+    "larql_hip_has_kv_cache": (_I, [_P]),
+    "larql_hip_synchronize": (_I, [_P]),
+    "larql_hip_register_weight": (_I, [_P, _I, _P, _SZ, _P, _SZ, _SZ, ctypes.POINTER(_U64)]),
+    "larql_hip_register_weight_device": (_I, [_P, _I, _P, _SZ, _P, _SZ, _SZ, ctypes.POINTER(_U64)]),
+    "larql_hip_release_weight": (_I, [_P, _U64]),
+    "larql_hip_forget_host": (_I, [_P, _P]),
+    "larql_hip_weight_device_bytes": (_I, [_P, _U64, ctypes.POINTER(_SZ)]),
+    "larql_hip_q4_matvec": (_I, [_P, _P, _SZ, _P, _P, _P, _SZ, _SZ]),
+    "larql_hip_q4k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
+    "larql_hip_q6k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
+    "larql_hip_quantize_to_q8": (_I, [_P, _P, _SZ, _P, _P]),
+    "larql_hip_q8_matvec": (_I, [_P, _P, _SZ, _P, _P, _P, _SZ, _P, _SZ, _SZ]),
+    "larql_hip_matvec_dev": (_I, [_P, _U64, _P, _P, _P, _SZ, _P]),
+    "larql_hip_quantize_to_q8_dev": (_I, [_P, _P, _SZ, _SZ, _P, _P, _P]),
+    "larql_hip_quantize_weights": (_I, [_P, _I, _P, _SZ, _P, _P]),
+    "larql_hip_quantize_weights_dev": (_I, [_P, _I, _P, _SZ, _P, _P, _P]),
+}
+
+QUANT_BYTES = {Q4_0: (32, 18), Q4_K: (256, 148), Q6_K: (256, 210), Q8_0: (32, 32)}
+
+_lib = None
+
+
+def load_library():
+    """Load liblarql_hip.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"liblarql_hip.so not built at {LIB_PATH}; run `make -C encoding-experiment_amd`")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+load_library()
+
+
+def _arr(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a, a.ctypes.data_as(_P)
+
+
+def _dptr(t):
+    """Device pointer of a tensor-like object (torch.Tensor or an int address)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return _P(t)
+    return _P(t.data_ptr())
+
+
+def _stream_ptr(stream):
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return _P(stream)
+    return _P(stream.cuda_stream)
+
+
+class HipBackend:
+    """ComputeBackend over liblarql_hip (one context = one device + stream)."""
+
+    def __init__(self, device: int = 0, strict: bool = False):
+        self._lib = load_library()
+        self.strict = strict
+        ctx = _P()
+        rc = self._lib.larql_hip_ctx_create(device, ctypes.byref(ctx))
+        if rc != OK:
+            raise LarqlHipError(rc, f"larql_hip_ctx_create(device={device}) failed")
+        self._ctx = ctx
+        self.device = device
+
+    # ── lifecycle ──────────────────────────────────────────────────────
+    def close(self):
+        if getattr(self, "_ctx", None):
+            self._lib.larql_hip_ctx_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def last_error(self) -> str:
+        return self._lib.larql_hip_last_error(self._ctx).decode()
+
+    def _ok(self, rc: int) -> bool:
+        if rc == OK:
+            return True
+        if self.strict:
+            raise LarqlHipError(rc, self.last_error())
+        return False
+
+    def _check(self, rc: int):
+        if rc != OK:
+            raise LarqlHipError(rc, self.last_error())
+
+    # ── metadata (backend.rs:155-163) ──────────────────────────────────
+    def name(self) -> str:
+        return self._lib.larql_hip_name().decode()
+
+    def device_info(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        self._check(self._lib.larql_hip_device_info(self._ctx, buf, 256))
+        return buf.value.decode()
+
+    def has_q4(self) -> bool:
+        return bool(self._lib.larql_hip_has_q4(self._ctx))
+
+    def has_kv_cache(self) -> bool:
+        return bool(self._lib.larql_hip_has_kv_cache(self._ctx))
+
+    def synchronize(self):
+        self._check(self._lib.larql_hip_synchronize(self._ctx))
+
+    # ── weight registry ────────────────────────────────────────────────
+    def register_weight(self, fmt: int, data, rows: int, cols: int, q8_scales=None) -> int:
+        """Upload + repack reference-layout bytes (host numpy) -> handle."""
+        raw = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+        sc_ptr = None
+        if q8_scales is not None:
+            sc, sc_ptr = _arr(q8_scales, np.float32)
+        h = _U64()
+        self._check(self._lib.larql_hip_register_weight(
+            self._ctx, fmt, raw.ctypes.data_as(_P), raw.size, sc_ptr, rows, cols, ctypes.byref(h)))
+        return h.value
+
+    def register_weight_device(self, fmt: int, dev_data, nbytes: int, rows: int, cols: int,
+                               dev_q8_scales=None) -> int:
+        h = _U64()
+        self._check(self._lib.larql_hip_register_weight_device(
+            self._ctx, fmt, _dptr(dev_data), nbytes, _dptr(dev_q8_scales), rows, cols, ctypes.byref(h)))
+        return h.value
+
+    def release_weight(self, handle: int):
+        self._check(self._lib.larql_hip_release_weight(self._ctx, handle))
+
+    def forget_host(self, data: np.ndarray):
+        self._check(self._lib.larql_hip_forget_host(self._ctx, data.ctypes.data_as(_P)))
+
+    def weight_device_bytes(self, handle: int) -> int:
+        n = _SZ()
+        self._check(self._lib.larql_hip_weight_device_bytes(self._ctx, handle, ctypes.byref(n)))
+        return n.value
+
+    # ── trait methods (backend.rs) ─────────────────────────────────────
+    def q4_matvec(self, q4_data, q8_x, q8_scales, num_rows: int, hidden: int):
+        """backend.rs:49-53 — scores[N] = Q4_0[N,K] @ Q8_x[K]."""
+        q4, q4p = _arr(q4_data, np.uint8)
+        qx, qxp = _arr(q8_x, np.int8)
+        qs, qsp = _arr(q8_scales, np.float32)
+        out = np.empty(num_rows, dtype=np.float32)
+        rc = self._lib.larql_hip_q4_matvec(self._ctx, q4p, q4.size, qxp, qsp, out.ctypes.data_as(_P), num_rows, hidden)
+        return out if self._ok(rc) else None
+
+    def q4k_matvec(self, q4k_data, x, num_rows: int, hidden: int):
+        """backend.rs:126-130 — scores[N] = Q4_K[N,K] @ f32_x[K]."""
+        q, qp = _arr(q4k_data, np.uint8)
+        xv, xp = _arr(x, np.float32)
+        out = np.empty(num_rows, dtype=np.float32)
+        rc = self._lib.larql_hip_q4k_matvec(self._ctx, qp, q.size, xp, out.ctypes.data_as(_P), num_rows, hidden)
+        return out if self._ok(rc) else None
+
+    def q6k_matvec(self, q6k_data, x, num_rows: int, hidden: int):
+        """backend.rs:133-137 — scores[N] = Q6_K[N,K] @ f32_x[K]."""
+        q, qp = _arr(q6k_data, np.uint8)
+        xv, xp = _arr(x, np.float32)
+        out = np.empty(num_rows, dtype=np.float32)
+        rc = self._lib.larql_hip_q6k_matvec(self._ctx, qp, q.size, xp, out.ctypes.data_as(_P), num_rows, hidden)
+        return out if self._ok(rc) else None
+
+    # ── reference free functions (extensions) ──────────────────────────
+    def quantize_to_q8(self, x):
+        """q4_common.rs:28-44 on the device (bit-exact)."""
+        xv, xp = _arr(x, np.float32)
+        q8 = np.empty(xv.size, dtype=np.int8)
+        sc = np.empty(xv.size // 32, dtype=np.float32)
+        rc = self._lib.larql_hip_quantize_to_q8(self._ctx, xp, xv.size, q8.ctypes.data_as(_P), sc.ctypes.data_as(_P))
+        return (q8, sc) if self._ok(rc) else None
+
+    def q8_matvec(self, w_q8, w_scales, x_q8, x_scales, num_rows: int, hidden: int):
+        """q8_matvec.rs:36-62, batched: x_q8 is [m, hidden] (or [hidden]); returns [m, num_rows]."""
+        wq, wqp = _arr(w_q8, np.int8)
+        ws, wsp = _arr(w_scales, np.float32)
+        xq, xqp = _arr(x_q8, np.int8)
+        xs, xsp = _arr(x_scales, np.float32)
+        m = xq.size // hidden
+        out = np.empty((m, num_rows), dtype=np.float32)
+        rc = self._lib.larql_hip_q8_matvec(self._ctx, wqp, wq.size, wsp, xqp, xsp, m, out.ctypes.data_as(_P), num_rows, hidden)
+        return out if self._ok(rc) else None
+
+    def quantize_weights(self, fmt: int, x):
+        """Reference weight quantizers on the device: returns the reference layout bytes
+        (and, for Q8_0, (int8 values, f32 scales))."""
+        xv, xp = _arr(x, np.float32)
+        per, nbytes = QUANT_BYTES[fmt]
+        out = np.empty(xv.size // per * nbytes, dtype=np.uint8)
+        sc = np.empty(xv.size // 32, dtype=np.float32) if fmt == Q8_0 else None
+        rc = self._lib.larql_hip_quantize_weights(self._ctx, fmt, xp, xv.size, out.ctypes.data_as(_P),
+                                                  sc.ctypes.data_as(_P) if sc is not None else None)
+        if not self._ok(rc):
+            return None
+        return (out.view(np.int8), sc) if fmt == Q8_0 else out
+
+    # ── device-resident fast path ──────────────────────────────────────
+    def matvec_dev(self, handle: int, x, out, m: int = 1, x_scales=None, stream=None):
+        self._check(self._lib.larql_hip_matvec_dev(self._ctx, handle, _dptr(x), _dptr(x_scales), _dptr(out), m,
+                                                   _stream_ptr(stream)))
+
+    def quantize_weights_dev(self, fmt: int, x, n: int, out, q8_scales=None, stream=None):
+        self._check(self._lib.larql_hip_quantize_weights_dev(self._ctx, fmt, _dptr(x), n, _dptr(out),
+                                                             _dptr(q8_scales), _stream_ptr(stream)))
+
+    def quantize_to_q8_dev(self, x, n: int, m: int, q8, scales, stream=None):
+        self._check(self._lib.larql_hip_quantize_to_q8_dev(self._ctx, _dptr(x), n, m, _dptr(q8), _dptr(scales),
+                                                           _stream_ptr(stream)))
+
+
+def default_backend(device: int = 0, strict: bool = False) -> HipBackend:
+    """lib.rs:68-78 analogue: the HIP backend on `device` (raises if no device)."""
+    return HipBackend(device, strict=strict)

@@ -1,0 +1,153 @@
+/*
+ * larql_hip.h — C ABI of the MI355X (gfx950) backend for LARQL's quantized
+ * compute path.
+ *
+ * This is the boundary a third `ComputeBackend` implementation binds to
+ * (reference trait: larql-main/crates/larql-compute/src/backend.rs:24-164).
+ * Conventions follow the reference's existing C kernel ABI
+ * (larql-compute/src/cpu/ops/q4_common.rs:6-25 -> csrc/q4_dot.c:169,201):
+ * plain pointers and sizes, caller-allocated outputs, no torch/HIP types in
+ * the signatures.  Two additions:
+ *   - a context handle (device, stream, weight registry, KV cache), and
+ *   - an int status: 0 = OK, negative = error (message via
+ *     larql_hip_last_error).  A nonzero status is what the Rust trait shim
+ *     maps to `None`, which makes callers fall back to the CPU backend exactly
+ *     as they do for an unsupported method (backend.rs:45-53, "Returns None
+ *     if backend doesn't support Q4").
+ *
+ * Reference paths below are relative to larql-main/crates/, abbreviated
+ *   LC = larql-compute, LV = larql-vindex, LI = larql-inference.
+ *
+ * Weight bytes are the reference's own layouts (Q4_0 18 B/32, Q4_K 148 B/256,
+ * Q6_K 210 B/256, Q8_0 as i8 + separate f32 scales).  On first use a host
+ * buffer is uploaded and repacked into a device layout and cached, keyed by
+ * (host pointer, length) like the Metal backend's buffer cache
+ * (LC/src/metal/buffers.rs:37-85); the same staleness rule applies: a caller
+ * that rewrites a buffer in place must call larql_hip_forget_host first.
+ *
+ * Thread safety: every entry point locks the context; kernels are reentrant.
+ */
+#ifndef LARQL_HIP_H
+#define LARQL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct larql_hip_ctx larql_hip_ctx;
+
+#define LARQL_HIP_OK 0
+#define LARQL_HIP_ERR_INVALID (-1)     /* bad argument or shape */
+#define LARQL_HIP_ERR_UNSUPPORTED (-2) /* valid request this backend does not implement */
+#define LARQL_HIP_ERR_DEVICE (-3)      /* HIP runtime error */
+#define LARQL_HIP_ERR_NOMEM (-4)
+#define LARQL_HIP_ERR_STATE (-5)       /* e.g. KV cache not initialised */
+
+/* QuantFormat — LC/src/pipeline.rs:12-19 (same discriminant order). */
+typedef enum {
+    LARQL_Q4_0 = 0,
+    LARQL_Q4_K = 1,
+    LARQL_Q4_KF = 2,
+    LARQL_Q6_K = 3,
+    LARQL_Q8_0 = 4
+} larql_quant_format;
+
+/* ── lifecycle and metadata ─────────────────────────────────────────────── */
+
+/* Backend construction; replaces MetalBackend::new() in default_backend()
+ * (LC/src/lib.rs:68-78).  device = HIP device ordinal. */
+int larql_hip_ctx_create(int device, larql_hip_ctx** out);
+void larql_hip_ctx_destroy(larql_hip_ctx* ctx);
+/* Message of the last failed call on this context ("" if none). */
+const char* larql_hip_last_error(larql_hip_ctx* ctx);
+/* ComputeBackend::name — LC/src/backend.rs:160 */
+const char* larql_hip_name(void);
+/* ComputeBackend::device_info — LC/src/backend.rs:163 */
+int larql_hip_device_info(larql_hip_ctx* ctx, char* buf, size_t len);
+/* ComputeBackend::has_q4 — LC/src/backend.rs:155 */
+int larql_hip_has_q4(larql_hip_ctx* ctx);
+/* ComputeBackend::has_kv_cache — LC/src/backend.rs:99 */
+int larql_hip_has_kv_cache(larql_hip_ctx* ctx);
+/* Block until all work queued on the context stream has finished. */
+int larql_hip_synchronize(larql_hip_ctx* ctx);
+
+/* ── weight registry (explicit form of the Metal buffer cache) ─────────── */
+
+/* Upload + repack a reference-layout weight from host memory.  q8_scales is
+ * used only for LARQL_Q8_0 (QuantWeight.scales, LC/src/pipeline.rs:22-27). */
+int larql_hip_register_weight(larql_hip_ctx* ctx, int format, const void* data, size_t len,
+                              const float* q8_scales, size_t rows, size_t cols, uint64_t* handle);
+/* Same, from reference-layout bytes already in device memory. */
+int larql_hip_register_weight_device(larql_hip_ctx* ctx, int format, const void* dev_data, size_t len,
+                                     const float* dev_q8_scales, size_t rows, size_t cols,
+                                     uint64_t* handle);
+int larql_hip_release_weight(larql_hip_ctx* ctx, uint64_t handle);
+/* Drop cached device copies made from host pointer `data` (any length). */
+int larql_hip_forget_host(larql_hip_ctx* ctx, const void* data);
+/* Bytes of device memory held by one registered weight. */
+int larql_hip_weight_device_bytes(larql_hip_ctx* ctx, uint64_t handle, size_t* bytes);
+
+/* ── trait methods (host memory in, caller-allocated host memory out) ──── */
+/* Weight arguments carry their byte length (the Rust slice length); a shape
+ * that needs more bytes than that is rejected with LARQL_HIP_ERR_INVALID. */
+
+/* ComputeBackend::q4_matvec — LC/src/backend.rs:49-53; CPU twin
+ * q4_0_matvec_c, LC/csrc/q4_dot.c:107/169.  scores[num_rows] = Q4_0[num_rows,hidden] . Q8(x).
+ * Per-block int32 dots are exact; blocks are accumulated in order as
+ * acc += (float)isum_b * (f16(scale_b) * q8_scales[b]) (q4_dot.c:58-89). */
+int larql_hip_q4_matvec(larql_hip_ctx* ctx, const uint8_t* q4_data, size_t q4_len, const int8_t* q8_x,
+                        const float* q8_scales, float* scores, size_t num_rows, size_t hidden);
+
+/* ComputeBackend::q4k_matvec — LC/src/backend.rs:126-130 (CPU: LC/src/cpu/ops/q4k_matvec.rs:31-90). */
+int larql_hip_q4k_matvec(larql_hip_ctx* ctx, const uint8_t* q4k_data, size_t q4k_len, const float* x,
+                         float* out, size_t num_rows, size_t hidden);
+
+/* ComputeBackend::q6k_matvec — LC/src/backend.rs:133-137 (CPU: LC/src/cpu/ops/q6k_matvec.rs:31-90). */
+int larql_hip_q6k_matvec(larql_hip_ctx* ctx, const uint8_t* q6k_data, size_t q6k_len, const float* x,
+                         float* out, size_t num_rows, size_t hidden);
+
+/* ── free functions of the reference exposed as extensions ─────────────── */
+
+/* quantize_to_q8 — LC/src/cpu/ops/q4_common.rs:28-44 (bit-exact). n % 32 == 0. */
+int larql_hip_quantize_to_q8(larql_hip_ctx* ctx, const float* x, size_t n, int8_t* q8, float* scales);
+
+/* q8_matvec::dispatch — LC/src/cpu/ops/q8_matvec.rs:36-62, batched over m
+ * activation rows: out[i*num_rows + r] = sum_b (float)isum(i,r,b) * (w_scales[r,b] * x_scales[i,b]),
+ * blocks in order (bit-exact with the CPU function). */
+int larql_hip_q8_matvec(larql_hip_ctx* ctx, const int8_t* w_q8, size_t w_len, const float* w_scales,
+                        const int8_t* x_q8, const float* x_scales, size_t m, float* out, size_t num_rows,
+                        size_t hidden);
+
+/* Weight quantizers of the reference, on the device and byte-identical to the
+ * host versions: quantize_q4_0 (LC/src/cpu/ops/q4_common.rs:50-81),
+ * quantize_q4_k (:104-170), quantize_q6_k (:179-239) and quantize_weights_q8
+ * (LC/src/cpu/ops/q8_matvec.rs:11-34).  x holds n floats (n % 32 == 0, or
+ * n % 256 == 0 for the K formats); `out` receives the reference layout
+ * (n/32*18, n/256*148, n/256*210 or n bytes); q8_scales (Q8_0 only) n/32 floats. */
+int larql_hip_quantize_weights(larql_hip_ctx* ctx, int format, const float* x, size_t n, void* out,
+                               float* q8_scales);
+
+/* ── device-resident fast path (device pointers; enqueue on `stream`) ──── */
+
+/* One matvec with a registered weight.  For LARQL_Q4_K / LARQL_Q6_K `x` is f32
+ * [m][cols] and x_scales is unused; for LARQL_Q4_0 / LARQL_Q8_0 `x` is int8
+ * [m][cols] and x_scales f32 [m][cols/32].  out is f32 [m][rows].
+ * stream: a hipStream_t, or NULL for the context stream.  Returns after enqueue. */
+int larql_hip_matvec_dev(larql_hip_ctx* ctx, uint64_t handle, const void* x, const float* x_scales,
+                         float* out, size_t m, void* stream);
+
+/* quantize_to_q8 on device memory, m rows of n floats. */
+int larql_hip_quantize_to_q8_dev(larql_hip_ctx* ctx, const float* x, size_t n, size_t m, int8_t* q8,
+                                 float* scales, void* stream);
+
+/* larql_hip_quantize_weights on device memory. */
+int larql_hip_quantize_weights_dev(larql_hip_ctx* ctx, int format, const float* x, size_t n, void* out,
+                                   float* q8_scales, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LARQL_HIP_H */

@@ -1,0 +1,102 @@
+/*
+ * larql_oracle.h — CPU oracle for the LARQL quantized compute path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
+ * CPU backend (larql-compute `CpuBackend`, its C kernel q4_dot.c, and the
+ * larql-inference CPU numerics used by the decode step).  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
+ * only as the checker.  The product library (liblarql_hip.so) never links,
+ * loads or calls anything here.
+ *
+ * Every function cites the reference file:line it follows; paths are relative
+ * to the reference repository root, abbreviated
+ *   LC/ = larql-main/crates/larql-compute/
+ *   LI/ = larql-main/crates/larql-inference/
+ *   LV/ = larql-main/crates/larql-vindex/
+ *
+ * Build: gcc -O3 -mavx2 -ffp-contract=off (the reference C kernel's flags,
+ * LC/build.rs:12-17, plus no mul+add contraction because Rust never fuses).
+ */
+#ifndef LARQL_ORACLE_H
+#define LARQL_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ── f16 codecs ─────────────────────────────────────────────────────────── */
+float    lo_f16_to_f32(uint16_t bits);          /* LC/src/cpu/ops/q4_common.rs:426-442 */
+float    lo_decode_f16(uint16_t h);             /* LC/csrc/q4_dot.c:9-35              */
+uint16_t lo_f32_to_f16_trunc(float v);          /* LC/src/cpu/ops/q4_common.rs:83-95  */
+uint16_t lo_f32_to_f16_rne(float v);            /* IEEE-754 round-to-nearest-even (KV cache storage) */
+
+/* ── quantizers ─────────────────────────────────────────────────────────── */
+void lo_quantize_to_q8(const float* x, size_t n, int8_t* q8, float* scales);       /* q4_common.rs:28-44  */
+void lo_quantize_q4_0(const float* x, size_t n, uint8_t* out);                     /* q4_common.rs:50-81  */
+void lo_quantize_q4_k(const float* x, size_t n, uint8_t* out);                     /* q4_common.rs:104-170 */
+void lo_quantize_q6_k(const float* x, size_t n, uint8_t* out);                     /* q4_common.rs:179-239 */
+void lo_quantize_weights_q8(const float* w, size_t rows, size_t cols,
+                            int8_t* q8, float* scales);                            /* q8_matvec.rs:11-34  */
+
+/* ── matvecs ────────────────────────────────────────────────────────────── */
+/* x86 scalar float order, LC/csrc/q4_dot.c:169-199 */
+void lo_q4_0_matvec_x86(const uint8_t* q4, const int8_t* q8x, const float* q8s,
+                        float* out, size_t rows, size_t hidden);
+/* ARM/Metal int32-block order, LC/csrc/q4_dot.c:48-126 */
+void lo_q4_0_matvec_blockint(const uint8_t* q4, const int8_t* q8x, const float* q8s,
+                             float* out, size_t rows, size_t hidden);
+/* per-block int32 dots, isum[row*blocks + b] (exact integers) */
+void lo_q4_0_block_dots(const uint8_t* q4, const int8_t* q8x, int32_t* isum,
+                        size_t rows, size_t hidden);
+/* LC/csrc/q4_dot.c:201-232 */
+void lo_q4_0_vecmat(const float* act, const uint8_t* q4, float* out,
+                    size_t inter, size_t hidden);
+/* LC/src/cpu/ops/q4k_matvec.rs:31-90 */
+void lo_q4k_matvec(const uint8_t* q4k, const float* x, float* out, size_t rows, size_t hidden);
+/* LC/src/cpu/ops/q6k_matvec.rs:31-90 */
+void lo_q6k_matvec(const uint8_t* q6k, const float* x, float* out, size_t rows, size_t hidden);
+/* LC/src/cpu/ops/q8_matvec.rs:36-62 */
+void lo_q8_matvec(const int8_t* wq, const float* ws, const int8_t* xq, const float* xs,
+                  float* out, size_t rows, size_t hidden);
+void lo_q8_block_dots(const int8_t* wq, const int8_t* xq, int32_t* isum, size_t rows, size_t hidden);
+
+/* ── gate KNN ───────────────────────────────────────────────────────────── */
+/* Top-k by |score| descending (LV/src/index/gate.rs:307-316); ties -> lower index. */
+void lo_topk_abs(const float* scores, size_t n, size_t k, uint32_t* idx, float* val);
+/* Top-k by signed score descending (LV/src/index/walk.rs:563-580); ties -> lower index. */
+void lo_topk_signed(const float* scores, size_t n, size_t k, uint32_t* idx, float* val);
+/* f32 gate scores in the canonical order shared with the HIP kernel:
+ * s[f] = one sequential fmaf chain over k = 0..hidden-1 starting from +0.0f. */
+void lo_gate_scores_f32(const float* gate, const float* x, float* out, size_t features, size_t hidden);
+
+/* ── decode-step numerics (LI/src) ──────────────────────────────────────── */
+void lo_rms_norm(const float* x, const float* w, float offset, double eps, float* out, size_t n); /* residual.rs:17-33 */
+void lo_rope_at(float* x, size_t num_heads, size_t head_dim, size_t rotary_dim,
+                double base, size_t pos);                                         /* rope.rs:22-55 */
+void lo_silu_gate_up(const float* gate, const float* up, float* out, size_t n);  /* ffn/mod.rs:87-94 */
+/* Single-query GQA over an fp16 cache laid out [t][kv_head][head_dim] (gqa.rs:29-110). */
+void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T,
+                   size_t num_q, size_t num_kv, size_t head_dim, float scale, float* out);
+
+/* One Llama decoder layer (Q4_K projections, fp16 KV cache) at position pos.
+ * h is updated in place; the new K/V row is written into kc/vc at pos. */
+typedef struct {
+    const uint8_t *wq, *wk, *wv, *wo, *gate, *up, *down;  /* Q4_K 148-byte layout */
+    const float *input_norm, *post_attn_norm;
+    uint16_t *k_cache, *v_cache;                             /* [max_seq][kv_heads][head_dim] fp16 */
+} lo_layer_t;
+
+void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,
+                     size_t hidden, size_t inter, size_t num_q, size_t num_kv, size_t head_dim,
+                     double rope_base, double eps);
+
+/* ── deterministic inputs (splitmix64 -> Box-Muller in f64 -> f32) ─────── */
+void lo_gauss_f32(uint64_t seed, float mean, float std, float* out, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
