@@ -78,7 +78,7 @@ def main():
 
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU sharding is design-only "
-                                   "(see DESIGN.md, 'How the path would shard')", "n_gpus": args.gpus}))
+                                   "(the single-GPU kernels are the per-GPU share of a row-sharded layout)", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import torch
@@ -86,7 +86,8 @@ def main():
     import larql_hip
 
     dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream(dev)
+    stream = torch.cuda.Stream(device=dev)          # kernels, events and torch ops all on this stream
+    torch.cuda.set_stream(stream)
     be = larql_hip.HipBackend(0, strict=True)
     log(f"[bench] {be.device_info()}")
 

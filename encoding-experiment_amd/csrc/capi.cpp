@@ -23,7 +23,8 @@ void* ensure(larql_hip_ctx* c, DeviceBuf& b, size_t bytes) {
     if (bytes == 0) bytes = 1;
     if (b.n >= bytes) return b.p;
     if (b.p) {
-        LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
+        (void)c;
+        LARQL_HIP_CHECK(hipDeviceSynchronize());  // the buffer may be in use on a caller's stream
         LARQL_HIP_CHECK(hipFree(b.p));
         b.p = nullptr;
         b.n = 0;
@@ -73,11 +74,13 @@ static uint64_t register_impl(larql_hip_ctx* c, int format, const void* data, si
     DevWeight w;
     w.format = format;
     w.rows = rows;
+    w.rows_pad = pad_rows(rows);
     w.cols = cols;
-    w.bytes = dev_layout_bytes(format, rows, cols);
+    w.bytes = dev_layout_bytes(format, w.rows_pad, cols);
     if (hipMalloc(&w.base, w.bytes) != hipSuccess)
         fail(LARQL_HIP_ERR_NOMEM, "hipMalloc of weight (" + std::to_string(w.bytes) + " bytes) failed");
     dev_layout_carve(w);
+    if (w.rows_pad != rows) LARQL_HIP_CHECK(hipMemsetAsync(w.base, 0, w.bytes, c->stream));
     const size_t raw_bytes = rows * ref_row_bytes(format, cols);
     const size_t sc_bytes = format == LARQL_Q8_0 ? rows * (cols / 32) * sizeof(float) : 0;
     try {
@@ -151,31 +154,7 @@ static void release(larql_hip_ctx* c, uint64_t handle) {
 
 }  // namespace larql
 
-// ── guard ────────────────────────────────────────────────────────────────
-template <class F>
-static int guarded(larql_hip_ctx* c, F&& f) {
-    if (!c) return LARQL_HIP_ERR_INVALID;
-    std::lock_guard<std::recursive_mutex> lk(c->mu);
-    try {
-        LARQL_HIP_CHECK(hipSetDevice(c->device));
-        f();
-        c->last_error.clear();
-        return LARQL_HIP_OK;
-    } catch (const Error& e) {
-        c->last_error = e.msg;
-        return e.code;
-    } catch (const std::bad_alloc&) {
-        c->last_error = "host allocation failed";
-        return LARQL_HIP_ERR_NOMEM;
-    } catch (const std::exception& e) {
-        c->last_error = e.what();
-        return LARQL_HIP_ERR_DEVICE;
-    }
-}
-
-static hipStream_t pick_stream(larql_hip_ctx* c, void* s) {
-    return s ? static_cast<hipStream_t>(s) : c->stream;
-}
+#include "capi_util.h"
 
 // ── lifecycle ────────────────────────────────────────────────────────────
 extern "C" int larql_hip_ctx_create(int device, larql_hip_ctx** out) {
@@ -207,10 +186,12 @@ extern "C" void larql_hip_ctx_destroy(larql_hip_ctx* c) {
         (void)hipStreamSynchronize(c->stream);
         for (auto& kv : c->weights) (void)hipFree(kv.second.base);
         c->weights.clear();
-        for (auto* b : {&c->stage_in, &c->stage_in2, &c->stage_out, &c->stage_raw, &c->scratch, &c->ws})
+        try {
+            larql_hip_decode_release(c);
+        } catch (...) {
+        }
+        for (auto* b : {&c->stage_in, &c->stage_in2, &c->stage_out, &c->stage_raw, &c->scratch})
             if (b->p) (void)hipFree(b->p);
-        for (auto* p : c->kv.k) (void)hipFree(p);
-        for (auto* p : c->kv.v) (void)hipFree(p);
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -276,18 +257,6 @@ extern "C" int larql_hip_weight_device_bytes(larql_hip_ctx* c, uint64_t handle, 
 }
 
 // ── host-memory trait methods ───────────────────────────────────────────
-template <class T>
-static T* stage_upload(larql_hip_ctx* c, larql::DeviceBuf& b, const T* host, size_t n) {
-    T* d = static_cast<T*>(larql::ensure(c, b, n * sizeof(T)));
-    LARQL_HIP_CHECK(hipMemcpyAsync(d, host, n * sizeof(T), hipMemcpyHostToDevice, c->stream));
-    return d;
-}
-
-static void download(larql_hip_ctx* c, void* host, const void* dev, size_t bytes) {
-    LARQL_HIP_CHECK(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, c->stream));
-    LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
-}
-
 extern "C" int larql_hip_q4k_matvec(larql_hip_ctx* c, const uint8_t* q4k_data, size_t q4k_len, const float* x,
                                     float* out, size_t num_rows, size_t hidden) {
     return guarded(c, [&] {

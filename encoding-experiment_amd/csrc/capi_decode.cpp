@@ -1,0 +1,464 @@
+// Decode-step entry points: KV cache (ComputeBackend::{populate_kv_layer, reset_kv_cache},
+// LC/src/backend.rs:99-110), decode_token (:115-123) and the device-resident model.
+//
+// A model holds, per layer, four device weights: Q|K|V concatenated by rows, Wo,
+// gate/up interleaved by rows (row 2n = gate n, row 2n+1 = up n, so one matvec
+// epilogue sees both and writes silu(gate)*up), and Wd; plus the two norm vectors.
+// The host-pointer decode_token caches the model it built, keyed by the layers'
+// pointers, lengths and sampled content (the Metal backend caches its buffers by host
+// pointer, LC/src/metal/buffers.rs:37-85, and re-uses them for every token).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "capi_util.h"
+#include "decode.h"
+#include "matvec_common.h"
+
+using larql::DevWeight;
+using larql::fail;
+
+struct LayerDev {
+    DevWeight qkv, wo, gateup, down;
+    float* input_norm = nullptr;
+    float* post_attn_norm = nullptr;
+    double eps = 1e-6;
+    float attn_scale = 0.f;
+    double rope_base = 10000.0;
+    int hd = 0, nq = 0, nkv = 0, rdim = 0, window = 0;
+};
+
+struct larql_hip_model {
+    std::vector<LayerDev> layers;
+    size_t hidden = 0, inter = 0, q_dim = 0, kv_dim = 0;
+    int nq = 0, nkv = 0, hd = 0;
+    bool has_head = false;
+    DevWeight head;
+    float* final_norm = nullptr;
+    double final_eps = 1e-6;
+    size_t vocab = 0;
+    std::vector<void*> allocs;
+    // workspace
+    float *h0 = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *xin = nullptr;
+    int* counter = nullptr;
+    larql::DeviceBuf part;
+    // host-pointer decode_token cache key
+    std::vector<uint64_t> key;
+};
+
+namespace {
+
+void* dev_alloc(larql_hip_model* m, size_t bytes) {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) fail(LARQL_HIP_ERR_NOMEM, "hipMalloc failed in model build");
+    m->allocs.push_back(p);
+    return p;
+}
+
+struct Src {
+    const void* data;
+    size_t len;
+    size_t rows;
+};
+
+// One device weight from one or more reference-layout sources: concatenated by rows
+// (stride 1) or interleaved (source i -> rows i, i+n, ...).
+DevWeight build_weight(larql_hip_ctx* c, larql_hip_model* m, int format, size_t cols, const std::vector<Src>& srcs,
+                       bool interleave, bool on_device) {
+    if (format != LARQL_Q4_K && format != LARQL_Q6_K)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: projections must be Q4_K or Q6_K");
+    if (cols % 256) fail(LARQL_HIP_ERR_INVALID, "decode: projection input width must be a multiple of 256");
+    size_t rows = 0;
+    for (const Src& s : srcs) {
+        if (!s.data) fail(LARQL_HIP_ERR_INVALID, "decode: null weight");
+        if (s.len < s.rows * larql::ref_row_bytes(format, cols))
+            fail(LARQL_HIP_ERR_INVALID, "decode: weight buffer shorter than its shape");
+        if (interleave && s.rows != srcs[0].rows) fail(LARQL_HIP_ERR_INVALID, "decode: gate/up shapes differ");
+        rows += s.rows;
+    }
+    DevWeight w;
+    w.format = format;
+    w.rows = rows;
+    w.rows_pad = larql::pad_rows(rows);
+    w.cols = cols;
+    w.bytes = larql::dev_layout_bytes(format, w.rows_pad, cols);
+    w.base = dev_alloc(m, w.bytes);
+    larql::dev_layout_carve(w);
+    LARQL_HIP_CHECK(hipMemsetAsync(w.base, 0, w.bytes, c->stream));
+    size_t row0 = 0;
+    for (size_t i = 0; i < srcs.size(); i++) {
+        const Src& s = srcs[i];
+        const size_t nbytes = s.rows * larql::ref_row_bytes(format, cols);
+        const uint8_t* raw = static_cast<const uint8_t*>(s.data);
+        if (!on_device) {
+            uint8_t* stage = static_cast<uint8_t*>(larql::ensure(c, c->stage_raw, nbytes));
+            LARQL_HIP_CHECK(hipMemcpyAsync(stage, s.data, nbytes, hipMemcpyHostToDevice, c->stream));
+            raw = stage;
+        }
+        if (interleave) larql::launch_repack(w, raw, nullptr, c->stream, s.rows, i, srcs.size());
+        else larql::launch_repack(w, raw, nullptr, c->stream, s.rows, row0, 1);
+        row0 += s.rows;
+        LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));  // the staging buffer is reused
+    }
+    return w;
+}
+
+float* upload_vec(larql_hip_ctx* c, larql_hip_model* m, const float* v, size_t n, bool on_device) {
+    if (!v) fail(LARQL_HIP_ERR_INVALID, "decode: null norm vector");
+    float* d = static_cast<float*>(dev_alloc(m, n * sizeof(float)));
+    LARQL_HIP_CHECK(hipMemcpyAsync(d, v, n * sizeof(float), on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                   c->stream));
+    return d;
+}
+
+// The HIP decode step implements the Llama layer; everything else is reported as
+// unsupported so callers fall back (LI/src/layer_graph/predict.rs:397-430).
+void check_supported(const larql_pipeline_layer& L) {
+    if (L.norm_type != LARQL_NORM_RMS) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: LayerNorm layers not supported");
+    if (L.ffn_type != LARQL_FFN_GATED) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: non-gated FFN not supported");
+    if (L.activation != LARQL_ACT_SILU) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: only SiLU FFN supported");
+    if (L.has_post_norms || L.pre_ffn_norm || L.post_ffn_norm)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: post-norm layers not supported");
+    if (L.input_norm_bias || L.post_attn_norm_bias || L.ffn_up_bias || L.ffn_down_bias)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: biases not supported");
+    if (L.has_v_norm) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: V-norm not supported");
+    if (L.layer_scalar != 0.0f) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: layer scalar not supported");
+    if (L.wq.format != L.wk.format || L.wq.format != L.wv.format)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: mixed Q/K/V formats not supported");
+    if (L.gate.format != L.up.format) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: mixed gate/up formats not supported");
+}
+
+larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t n, size_t hidden,
+                             size_t inter, bool on_device) {
+    if (!layers || n == 0) fail(LARQL_HIP_ERR_INVALID, "decode: no layers");
+    if (hidden == 0 || inter == 0) fail(LARQL_HIP_ERR_INVALID, "decode: zero hidden/inter");
+    auto* m = new larql_hip_model();
+    try {
+        m->hidden = hidden;
+        m->inter = inter;
+        for (size_t l = 0; l < n; l++) {
+            const larql_pipeline_layer& L = layers[l];
+            check_supported(L);
+            LayerDev d;
+            d.hd = static_cast<int>(L.head_dim);
+            d.nq = static_cast<int>(L.num_q_heads);
+            d.nkv = static_cast<int>(L.num_kv_heads);
+            if (d.hd <= 0 || d.nq <= 0 || d.nkv <= 0 || d.nq % d.nkv || d.hd % 8)
+                fail(LARQL_HIP_ERR_INVALID, "decode: bad head geometry");
+            d.rdim = L.rotary_dim ? static_cast<int>(L.rotary_dim) : d.hd;
+            if (d.rdim > d.hd || d.rdim % 2) fail(LARQL_HIP_ERR_INVALID, "decode: bad rotary_dim");
+            if (larql::attn_lds_bytes(d.nq / d.nkv, d.hd, d.rdim) > 64 * 1024)
+                fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: head geometry exceeds the attention kernel's LDS");
+            d.window = static_cast<int>(L.sliding_window);
+            d.eps = L.eps > 0.f ? static_cast<double>(L.eps) : 1e-6;
+            d.attn_scale = L.attn_scale != 0.f ? L.attn_scale : static_cast<float>(1.0 / std::sqrt(double(d.hd)));
+            d.rope_base = L.rope_base;
+            if (l == 0) {
+                m->nq = d.nq;
+                m->nkv = d.nkv;
+                m->hd = d.hd;
+            } else if (d.nq != m->nq || d.nkv != m->nkv || d.hd != m->hd) {
+                fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: per-layer head geometry must be uniform");
+            }
+            const size_t qd = static_cast<size_t>(d.nq) * d.hd, kvd = static_cast<size_t>(d.nkv) * d.hd;
+            d.qkv = build_weight(c, m, L.wq.format, hidden,
+                                 {{L.wq.data, L.wq.len, qd}, {L.wk.data, L.wk.len, kvd}, {L.wv.data, L.wv.len, kvd}},
+                                 false, on_device);
+            d.wo = build_weight(c, m, L.wo.format, qd, {{L.wo.data, L.wo.len, hidden}}, false, on_device);
+            d.gateup = build_weight(c, m, L.gate.format, hidden,
+                                    {{L.gate.data, L.gate.len, inter}, {L.up.data, L.up.len, inter}}, true, on_device);
+            d.down = build_weight(c, m, L.down.format, inter, {{L.down.data, L.down.len, hidden}}, false, on_device);
+            d.input_norm = upload_vec(c, m, L.input_norm, hidden, on_device);
+            d.post_attn_norm = upload_vec(c, m, L.post_attn_norm, hidden, on_device);
+            m->layers.push_back(d);
+        }
+        m->q_dim = static_cast<size_t>(m->nq) * m->hd;
+        m->kv_dim = static_cast<size_t>(m->nkv) * m->hd;
+        m->h0 = static_cast<float*>(dev_alloc(m, hidden * 4));
+        m->h1 = static_cast<float*>(dev_alloc(m, hidden * 4));
+        m->xin = static_cast<float*>(dev_alloc(m, hidden * 4));
+        m->qkv = static_cast<float*>(dev_alloc(m, (m->q_dim + 2 * m->kv_dim) * 4));
+        m->attn = static_cast<float*>(dev_alloc(m, m->q_dim * 4));
+        m->act = static_cast<float*>(dev_alloc(m, inter * 4));
+        m->counter = static_cast<int*>(dev_alloc(m, m->nkv * sizeof(int)));
+        LARQL_HIP_CHECK(hipMemsetAsync(m->counter, 0, m->nkv * sizeof(int), c->stream));
+        LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
+    } catch (...) {
+        for (void* p : m->allocs) (void)hipFree(p);
+        delete m;
+        throw;
+    }
+    return m;
+}
+
+void destroy_model(larql_hip_ctx* c, larql_hip_model* m) {
+    if (!m) return;
+    (void)hipDeviceSynchronize();
+    for (void* p : m->allocs) (void)hipFree(p);
+    if (m->part.p) (void)hipFree(m->part.p);
+    (void)c;
+    delete m;
+}
+
+// ── KV cache ───────────────────────────────────────────────────────────
+void kv_free(larql_hip_ctx* c) {
+    (void)hipDeviceSynchronize();
+    for (auto* p : c->kv.k) (void)hipFree(p);
+    for (auto* p : c->kv.v) (void)hipFree(p);
+    c->kv = larql::KVCache{};
+}
+
+// Make room for `layers` layers of [cap][num_kv][head_dim] with cap >= need (initial
+// capacity 4096 as in the reference, LC/src/metal/trait_impl.rs:163; doubled on demand,
+// so attention is not limited in T).
+void kv_ensure(larql_hip_ctx* c, size_t layers, size_t num_kv, size_t head_dim, size_t need) {
+    auto& kv = c->kv;
+    if (kv.num_layers && (kv.num_kv != num_kv || kv.head_dim != head_dim)) kv_free(c);
+    const size_t row = num_kv * head_dim;
+    if (kv.num_layers == 0) {
+        kv.num_kv = num_kv;
+        kv.head_dim = head_dim;
+        kv.max_seq = need > 4096 ? need : 4096;
+        kv.current_len = 0;
+    }
+    if (need > kv.max_seq) {
+        size_t cap = kv.max_seq * 2;
+        while (cap < need) cap *= 2;
+        (void)hipDeviceSynchronize();
+        for (size_t l = 0; l < kv.num_layers; l++) {
+            for (auto* vec : {&kv.k, &kv.v}) {
+                __half* p = nullptr;
+                if (hipMalloc(&p, cap * row * sizeof(__half)) != hipSuccess) fail(LARQL_HIP_ERR_NOMEM, "KV grow failed");
+                LARQL_HIP_CHECK(hipMemcpy(p, (*vec)[l], kv.current_len * row * sizeof(__half), hipMemcpyDeviceToDevice));
+                (void)hipFree((*vec)[l]);
+                (*vec)[l] = p;
+            }
+        }
+        kv.max_seq = cap;
+    }
+    while (kv.num_layers < layers) {
+        __half *k = nullptr, *v = nullptr;
+        if (hipMalloc(&k, kv.max_seq * row * sizeof(__half)) != hipSuccess ||
+            hipMalloc(&v, kv.max_seq * row * sizeof(__half)) != hipSuccess) {
+            if (k) (void)hipFree(k);
+            fail(LARQL_HIP_ERR_NOMEM, "KV cache allocation failed");
+        }
+        kv.k.push_back(k);
+        kv.v.push_back(v);
+        kv.num_layers++;
+    }
+}
+
+void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float* hidden_out, float* logits,
+                hipStream_t s) {
+    auto& kv = c->kv;
+    kv_ensure(c, m->layers.size(), m->nkv, m->hd, kv.current_len + 1);
+    const int T = static_cast<int>(kv.current_len) + 1;
+    const int S = (T + 63) / 64;
+    float* part = static_cast<float*>(
+        larql::ensure(c, m->part, static_cast<size_t>(m->nq) * S * (m->hd + 2) * sizeof(float)));
+    larql::launch_copy_f32(x_dev, m->h0, m->hidden, s);
+    for (size_t l = 0; l < m->layers.size(); l++) {
+        const LayerDev& L = m->layers[l];
+        larql::MvArgs a;
+        a.x = m->h0;
+        a.out = m->qkv;
+        a.norm_w = L.input_norm;
+        a.eps = L.eps;
+        larql::launch_mv(L.qkv, a, s);
+
+        larql::AttnArgs at{};
+        at.qkv = m->qkv;
+        at.kc = kv.k[l];
+        at.vc = kv.v[l];
+        at.out = m->attn;
+        at.part = part;
+        at.counter = m->counter;
+        at.num_q = L.nq;
+        at.num_kv = L.nkv;
+        at.hd = L.hd;
+        at.rdim = L.rdim;
+        at.T = T;
+        at.t_begin = (L.window > 0 && T > L.window) ? T - L.window : 0;
+        at.scale = L.attn_scale;
+        at.rope_base = L.rope_base;
+        larql::launch_attention(at, s);
+
+        larql::MvArgs o;
+        o.x = m->attn;
+        o.out = m->h1;
+        o.epi = larql::EPI_RESID;
+        o.resid = m->h0;
+        larql::launch_mv(L.wo, o, s);
+
+        larql::MvArgs g;
+        g.x = m->h1;
+        g.out = m->act;
+        g.norm_w = L.post_attn_norm;
+        g.eps = L.eps;
+        g.epi = larql::EPI_SILU_PAIR;
+        larql::launch_mv(L.gateup, g, s);
+
+        larql::MvArgs d;
+        d.x = m->act;
+        d.out = m->h0;
+        d.epi = larql::EPI_RESID;
+        d.resid = m->h1;
+        larql::launch_mv(L.down, d, s);
+    }
+    kv.current_len = static_cast<size_t>(T);
+    if (hidden_out) larql::launch_copy_f32(m->h0, hidden_out, m->hidden, s);
+    if (logits) {
+        if (!m->has_head) fail(LARQL_HIP_ERR_STATE, "decode: logits requested but the model has no head");
+        larql::MvArgs e;
+        e.x = m->h0;
+        e.out = logits;
+        e.norm_w = m->final_norm;
+        e.eps = m->final_eps;
+        larql::launch_mv(m->head, e, s);
+    }
+}
+
+std::vector<uint64_t> layers_key(const larql_pipeline_layer* layers, size_t n, size_t hidden, size_t inter) {
+    std::vector<uint64_t> k{n, hidden, inter};
+    for (size_t l = 0; l < n; l++) {
+        const larql_pipeline_layer& L = layers[l];
+        for (const larql_quant_weight* w : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down}) {
+            k.push_back(reinterpret_cast<uint64_t>(w->data));
+            k.push_back(w->len);
+            k.push_back(static_cast<uint64_t>(w->format));
+            k.push_back(w->data ? larql::host_fingerprint(w->data, w->len) : 0);
+        }
+        k.push_back(reinterpret_cast<uint64_t>(L.input_norm));
+        k.push_back(reinterpret_cast<uint64_t>(L.post_attn_norm));
+        k.push_back(L.input_norm ? larql::host_fingerprint(L.input_norm, hidden * 4) : 0);
+        k.push_back(L.post_attn_norm ? larql::host_fingerprint(L.post_attn_norm, hidden * 4) : 0);
+        uint32_t bits[3];
+        std::memcpy(&bits[0], &L.eps, 4);
+        std::memcpy(&bits[1], &L.rope_base, 4);
+        std::memcpy(&bits[2], &L.attn_scale, 4);
+        k.push_back((static_cast<uint64_t>(bits[0]) << 32) | bits[1]);
+        k.push_back((static_cast<uint64_t>(bits[2]) << 32) | (L.head_dim << 16) | (L.num_q_heads << 8) | L.num_kv_heads);
+        k.push_back((static_cast<uint64_t>(L.rotary_dim) << 32) | L.sliding_window);
+    }
+    return k;
+}
+
+}  // namespace
+
+extern "C" int larql_hip_decode_token(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t num_layers,
+                                      const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim,
+                                      size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float rope_base,
+                                      float* out) {
+    return guarded(c, [&] {
+        if (!layers || !x || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        if (num_q_heads * head_dim != q_dim || num_kv_heads * head_dim != kv_dim)
+            fail(LARQL_HIP_ERR_INVALID, "decode_token: q_dim/kv_dim do not match the head geometry");
+        (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
+        auto key = layers_key(layers, num_layers, hidden, inter);
+        larql_hip_model*& m = c->trait_model;  // model of the last host-pointer decode_token
+        if (!m || m->key != key) {
+            destroy_model(c, m);
+            m = nullptr;
+            m = build_model(c, layers, num_layers, hidden, inter, false);
+            m->key = key;
+        }
+        if (m->q_dim != q_dim || m->kv_dim != kv_dim)
+            fail(LARQL_HIP_ERR_INVALID, "decode_token: layer geometry differs from q_dim/kv_dim");
+        LARQL_HIP_CHECK(hipMemcpyAsync(m->xin, x, hidden * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        run_decode(c, m, m->xin, m->xin, nullptr, c->stream);
+        download(c, out, m->xin, hidden * sizeof(float));
+    });
+}
+
+extern "C" int larql_hip_populate_kv_layer(larql_hip_ctx* c, size_t layer, const float* k_data, const float* v_data,
+                                           size_t seq_len, size_t num_kv_heads, size_t head_dim) {
+    return guarded(c, [&] {
+        if (!k_data || !v_data) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        if (num_kv_heads == 0 || head_dim == 0) fail(LARQL_HIP_ERR_INVALID, "zero kv geometry");
+        kv_ensure(c, layer + 1, num_kv_heads, head_dim, seq_len);
+        const size_t n = seq_len * num_kv_heads * head_dim;
+        const float* dk = stage_upload(c, c->stage_in, k_data, n);
+        larql::launch_f32_to_f16(dk, c->kv.k[layer], n, c->stream);
+        const float* dv = stage_upload(c, c->stage_in2, v_data, n);
+        larql::launch_f32_to_f16(dv, c->kv.v[layer], n, c->stream);
+        LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
+        c->kv.current_len = seq_len;
+    });
+}
+
+extern "C" int larql_hip_populate_kv_layer_f16_dev(larql_hip_ctx* c, size_t layer, const uint16_t* k_dev,
+                                                   const uint16_t* v_dev, size_t seq_len, size_t num_kv_heads,
+                                                   size_t head_dim) {
+    return guarded(c, [&] {
+        if (!k_dev || !v_dev) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        if (num_kv_heads == 0 || head_dim == 0) fail(LARQL_HIP_ERR_INVALID, "zero kv geometry");
+        kv_ensure(c, layer + 1, num_kv_heads, head_dim, seq_len);
+        const size_t bytes = seq_len * num_kv_heads * head_dim * sizeof(__half);
+        LARQL_HIP_CHECK(hipMemcpyAsync(c->kv.k[layer], k_dev, bytes, hipMemcpyDeviceToDevice, c->stream));
+        LARQL_HIP_CHECK(hipMemcpyAsync(c->kv.v[layer], v_dev, bytes, hipMemcpyDeviceToDevice, c->stream));
+        LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
+        c->kv.current_len = seq_len;
+    });
+}
+
+extern "C" int larql_hip_reset_kv_cache(larql_hip_ctx* c) {
+    return guarded(c, [&] { kv_free(c); });
+}
+
+extern "C" int larql_hip_kv_cache_len(larql_hip_ctx* c, size_t* len) {
+    return guarded(c, [&] {
+        if (!len) fail(LARQL_HIP_ERR_INVALID, "null output");
+        *len = c->kv.current_len;
+    });
+}
+
+extern "C" int larql_hip_kv_truncate(larql_hip_ctx* c, size_t len) {
+    return guarded(c, [&] {
+        if (len > c->kv.current_len) fail(LARQL_HIP_ERR_INVALID, "kv_truncate: length beyond the cache");
+        c->kv.current_len = len;
+    });
+}
+
+extern "C" int larql_hip_model_create(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t num_layers,
+                                      size_t hidden, size_t inter, int weights_on_device, larql_hip_model** out) {
+    return guarded(c, [&] {
+        if (!out) fail(LARQL_HIP_ERR_INVALID, "null output");
+        *out = build_model(c, layers, num_layers, hidden, inter, weights_on_device != 0);
+    });
+}
+
+extern "C" int larql_hip_model_set_head(larql_hip_ctx* c, larql_hip_model* m, const larql_quant_weight* head,
+                                        size_t vocab, const float* final_norm, float eps, int weights_on_device) {
+    return guarded(c, [&] {
+        if (!m || !head || !final_norm) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        const bool dev = weights_on_device != 0;
+        m->head = build_weight(c, m, head->format, m->hidden, {{head->data, head->len, vocab}}, false, dev);
+        m->final_norm = upload_vec(c, m, final_norm, m->hidden, dev);
+        m->final_eps = eps > 0.f ? static_cast<double>(eps) : 1e-6;
+        m->vocab = vocab;
+        m->has_head = true;
+        LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
+    });
+}
+
+extern "C" int larql_hip_model_destroy(larql_hip_ctx* c, larql_hip_model* m) {
+    return guarded(c, [&] { destroy_model(c, m); });
+}
+
+extern "C" int larql_hip_model_decode_dev(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev,
+                                          float* hidden_out_dev, float* logits_dev, void* stream) {
+    return guarded(c, [&] {
+        if (!m || !x_dev) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        run_decode(c, m, x_dev, hidden_out_dev, logits_dev, pick_stream(c, stream));
+    });
+}
+
+// Called by larql_hip_ctx_destroy.
+void larql_hip_decode_release(larql_hip_ctx* c) {
+    destroy_model(c, c->trait_model);
+    c->trait_model = nullptr;
+    kv_free(c);
+}

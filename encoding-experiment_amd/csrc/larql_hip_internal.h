@@ -9,8 +9,10 @@
 //     qs  : u8 [rows][S*128]      nibble bytes, reference order within a super-block
 //     hdr : u32x4 [rows][S]       {d|dmin<<16, sc[0..3], sc[4..7], min bytes}
 //   Q6_K (210 B / 256):
-//     ql  : u8 [rows][S*128]      low nibbles
-//     qh  : u8 [rows][S*64]       high 2-bit pairs
+//     ql  : u8 [rows][S*128]      low nibbles (reference order)
+//     qh  : u32 [rows][S*16]      high 2-bit pairs, regrouped per 16 elements: for
+//                                 element 8w + 2j + p of a 16-element group (w, p in
+//                                 {0,1}), bits 8j + 4w + 2p of the group's word
 //     sc  : i8 [rows][S*16]       sub-block scales
 //     d   : f16 [rows][S]         super-block scale
 //   Q4_0 (18 B / 32):
@@ -19,9 +21,11 @@
 //   Q8_0 (trait form: i8 + separate f32 scales):
 //     qs  : i8 [rows][cols]
 //     d   : f32 [rows][B]
-// where S = cols/256 and B = cols/32.  The algorithmic byte count of every
-// format stays the reference's; the Q4_K device layout drops the four unused
-// scale bytes of each super-block (144 of 148 bytes are moved).
+// where S = cols/256 and B = cols/32.  Rows are zero-padded to rows_pad (a multiple
+// of 64) so matvec tiles load without row tests; padding rows decode to zero.
+// The algorithmic byte count of every format stays the reference's; the Q4_K
+// device layout drops the four unused scale bytes of each super-block (144 of
+// 148 bytes are moved).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -60,6 +64,7 @@ struct Error {
 struct DevWeight {
     int format = 0;          // larql_quant_format
     size_t rows = 0, cols = 0;
+    size_t rows_pad = 0;     // rows rounded up to a multiple of 64
     void* base = nullptr;    // one device allocation holding all sub-arrays
     size_t bytes = 0;
     // sub-array pointers into `base`
@@ -81,11 +86,14 @@ struct DevWeight {
 uint64_t host_fingerprint(const void* data, size_t len);
 
 size_t ref_row_bytes(int format, size_t cols);   // bytes per row in the reference layout
-size_t dev_layout_bytes(int format, size_t rows, size_t cols);
+size_t dev_layout_bytes(int format, size_t rows_pad, size_t cols);
+inline size_t pad_rows(size_t rows) { return (rows + 63) & ~size_t(63); }
 void dev_layout_carve(DevWeight& w);              // set sub-array pointers from base
 
-// Repack reference-layout bytes already on the device (`raw`) into `w`.
-void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scales, hipStream_t s);
+// Repack reference-layout bytes already on the device (`raw`, src_rows rows; 0 = w.rows)
+// into `w`, source row r landing in destination row row0 + r*stride.
+void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scales, hipStream_t s,
+                   size_t src_rows = 0, size_t row0 = 0, size_t stride = 1);
 
 // ── KV cache ────────────────────────────────────────────────────────────
 struct KVCache {
@@ -115,9 +123,12 @@ struct larql_hip_ctx {
     // reusable device staging buffers for host-pointer calls
     larql::DeviceBuf stage_in, stage_in2, stage_out, stage_raw, scratch;
     larql::KVCache kv;
-    // decode-step workspace
-    larql::DeviceBuf ws;
+    // model built by the last host-pointer decode_token (re-used while its key matches)
+    larql_hip_model* trait_model = nullptr;
 };
+
+// Frees the decode-side state of a context (trait model, KV cache).
+void larql_hip_decode_release(larql_hip_ctx* c);
 
 namespace larql {
 

@@ -35,7 +35,7 @@ size_t dev_layout_bytes(int format, size_t rows, size_t cols) {
 
 void dev_layout_carve(DevWeight& w) {
     uint8_t* p = static_cast<uint8_t*>(w.base);
-    const size_t R = w.rows, K = w.cols;
+    const size_t R = w.rows_pad, K = w.cols;
     switch (w.format) {
         case LARQL_Q4_0:
             w.qs = p; p += align256(R * K / 2);
@@ -61,70 +61,97 @@ void dev_layout_carve(DevWeight& w) {
 
 // One thread per Q4_K super-block.  Source blocks sit at 148-byte offsets, so they
 // are 4-byte aligned whenever the raw buffer is.
+// Source row r lands in destination row row0 + r*stride (concatenated or interleaved
+// fused weights); bpr = blocks per row.
+__device__ __forceinline__ size_t dst_block(size_t b, size_t bpr, size_t row0, size_t stride) {
+    const size_t r = b / bpr;
+    return (row0 + r * stride) * bpr + (b - r * bpr);
+}
+
 __global__ void repack_q4k_kernel(const uint32_t* __restrict__ raw, uint8_t* __restrict__ qs,
-                                  uint4* __restrict__ hdr, size_t nblocks) {
+                                  uint4* __restrict__ hdr, size_t nblocks, size_t bpr, size_t row0, size_t stride) {
     size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
     const uint32_t* s = raw + b * 37;
-    hdr[b] = make_uint4(s[0], s[1], s[2], s[4]);
-    uint4* q = reinterpret_cast<uint4*>(qs + b * 128);
+    const size_t o = dst_block(b, bpr, row0, stride);
+    hdr[o] = make_uint4(s[0], s[1], s[2], s[4]);
+    uint4* q = reinterpret_cast<uint4*>(qs + o * 128);
 #pragma unroll
     for (int i = 0; i < 8; i++) q[i] = make_uint4(s[5 + 4 * i], s[6 + 4 * i], s[7 + 4 * i], s[8 + 4 * i]);
 }
 
-// One thread per Q6_K super-block (210-byte stride: 2-byte aligned source).
+// One thread per Q6_K super-block (210-byte stride: 2-byte aligned source).  The
+// 64 qh bytes (element e at byte e/4, bits 2*(e%4)) are regrouped into 16 words, one
+// per 16-element group g: element 16g + 8w + 2j + p goes to bits 8j + 4w + 2p.
 __global__ void repack_q6k_kernel(const uint16_t* __restrict__ raw, uint8_t* __restrict__ ql,
                                   uint8_t* __restrict__ qh, int8_t* __restrict__ sc,
-                                  uint16_t* __restrict__ d, size_t nblocks) {
+                                  uint16_t* __restrict__ d, size_t nblocks, size_t bpr, size_t row0, size_t stride) {
     size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
     const uint16_t* s = raw + b * 105;
-    uint16_t* l = reinterpret_cast<uint16_t*>(ql + b * 128);
-    uint16_t* h = reinterpret_cast<uint16_t*>(qh + b * 64);
-    uint16_t* c = reinterpret_cast<uint16_t*>(sc + b * 16);
+    const size_t o = dst_block(b, bpr, row0, stride);
+    uint16_t* l = reinterpret_cast<uint16_t*>(ql + o * 128);
+    uint32_t* h = reinterpret_cast<uint32_t*>(qh + o * 64);
+    uint16_t* c = reinterpret_cast<uint16_t*>(sc + o * 16);
     for (int i = 0; i < 64; i++) l[i] = s[i];
-    for (int i = 0; i < 32; i++) h[i] = s[64 + i];
+    for (int g = 0; g < 16; g++) {
+        // source: 16 elements = 4 bytes = u16 words s[64 + 2g] and s[64 + 2g + 1]
+        const uint32_t src = static_cast<uint32_t>(s[64 + 2 * g]) | (static_cast<uint32_t>(s[64 + 2 * g + 1]) << 16);
+        uint32_t dst = 0;
+        for (int e = 0; e < 16; e++) {
+            const uint32_t v = (src >> (2 * e)) & 3u;
+            const int w = e >> 3, j = (e & 7) >> 1, p = e & 1;
+            dst |= v << (8 * j + 4 * w + 2 * p);
+        }
+        h[g] = dst;
+    }
     for (int i = 0; i < 8; i++) c[i] = s[96 + i];
-    d[b] = s[104];
+    d[o] = s[104];
 }
 
 // One thread per Q4_0 block (18-byte stride: 2-byte aligned source).
 __global__ void repack_q4_0_kernel(const uint16_t* __restrict__ raw, uint8_t* __restrict__ qs,
-                                   uint16_t* __restrict__ d, size_t nblocks) {
+                                   uint16_t* __restrict__ d, size_t nblocks, size_t bpr, size_t row0, size_t stride) {
     size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
     const uint16_t* s = raw + b * 9;
-    d[b] = s[0];
-    uint16_t* q = reinterpret_cast<uint16_t*>(qs + b * 16);
+    const size_t o = dst_block(b, bpr, row0, stride);
+    d[o] = s[0];
+    uint16_t* q = reinterpret_cast<uint16_t*>(qs + o * 16);
 #pragma unroll
     for (int i = 0; i < 8; i++) q[i] = s[1 + i];
 }
 
-void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scales, hipStream_t s) {
+void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scales, hipStream_t s,
+                   size_t src_rows, size_t row0, size_t stride) {
     const int T = 256;
+    if (src_rows == 0) src_rows = w.rows;
+    if (row0 + (src_rows - 1) * stride >= w.rows) fail(LARQL_HIP_ERR_INVALID, "repack: rows out of range");
     switch (w.format) {
         case LARQL_Q4_K: {
-            size_t nb = w.rows * (w.cols / 256);
+            const size_t bpr = w.cols / 256, nb = src_rows * bpr;
             repack_q4k_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
-                reinterpret_cast<const uint32_t*>(raw), w.qs, w.hdr, nb);
+                reinterpret_cast<const uint32_t*>(raw), w.qs, w.hdr, nb, bpr, row0, stride);
             break;
         }
         case LARQL_Q6_K: {
-            size_t nb = w.rows * (w.cols / 256);
+            const size_t bpr = w.cols / 256, nb = src_rows * bpr;
             repack_q6k_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
-                reinterpret_cast<const uint16_t*>(raw), w.qs, w.qh, w.sc, static_cast<uint16_t*>(w.d), nb);
+                reinterpret_cast<const uint16_t*>(raw), w.qs, w.qh, w.sc, static_cast<uint16_t*>(w.d), nb, bpr,
+                row0, stride);
             break;
         }
         case LARQL_Q4_0: {
-            size_t nb = w.rows * (w.cols / 32);
+            const size_t bpr = w.cols / 32, nb = src_rows * bpr;
             repack_q4_0_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
-                reinterpret_cast<const uint16_t*>(raw), w.qs, static_cast<uint16_t*>(w.d), nb);
+                reinterpret_cast<const uint16_t*>(raw), w.qs, static_cast<uint16_t*>(w.d), nb, bpr, row0, stride);
             break;
         }
         case LARQL_Q8_0: {
-            LARQL_HIP_CHECK(hipMemcpyAsync(w.qs, raw, w.rows * w.cols, hipMemcpyDeviceToDevice, s));
-            LARQL_HIP_CHECK(hipMemcpyAsync(w.d, q8_scales, w.rows * (w.cols / 32) * sizeof(float),
-                                           hipMemcpyDeviceToDevice, s));
+            if (stride != 1) fail(LARQL_HIP_ERR_UNSUPPORTED, "repack: interleaved Q8_0");
+            LARQL_HIP_CHECK(hipMemcpyAsync(w.qs + row0 * w.cols, raw, src_rows * w.cols, hipMemcpyDeviceToDevice, s));
+            LARQL_HIP_CHECK(hipMemcpyAsync(static_cast<float*>(w.d) + row0 * (w.cols / 32), q8_scales,
+                                           src_rows * (w.cols / 32) * sizeof(float), hipMemcpyDeviceToDevice, s));
             break;
         }
         default: fail(LARQL_HIP_ERR_UNSUPPORTED, "repack: unsupported format");

@@ -1,0 +1,385 @@
+// K-quant x f32 matvecs with fused RMSNorm prologue and decode epilogues.
+//
+//   Q4_K (148-byte layout): reference semantics LC/src/cpu/ops/q4k_matvec.rs:31-90,
+//        trait method LC/src/backend.rs:126-130.
+//   Q6_K (210-byte layout): LC/src/cpu/ops/q6k_matvec.rs:31-90, backend.rs:133-137.
+//
+// Mapping (gfx950, wave64): a "row slot" is `wpr` waves whose 64*wpr lanes cover K,
+// one 32-element sub-block per lane per pass (SBL passes).  Every weight byte is read
+// from HBM exactly once with wave-contiguous 16-byte loads; each workgroup issues the
+// loads of its whole RB-row tile before any arithmetic.
+//
+// Arithmetic: the dot of 4-bit / 6-bit integer codes with x is done in exact int32
+// with v_dot4.  Each lane turns its x sub-block once into fixed point,
+//   T_k = rint(x_k * 127 * 2^16 / max|x|)        (|T_k| < 2^23, exact in f32),
+// so x_k ~= s' * T_k with s' = max|x| / (127 * 2^16) and |x_k - s' T_k| <= ~1.2e-7 max|x|
+// (the size of an f32 rounding of the block's largest term).  The bytes of T are three
+// int8/uint8 levels, T = 2^16 a + 2^8 b + c with a signed and b, c unsigned, so
+//   sum(q * x) = s' * (2^16 I_a + 2^8 I_b + I_c)
+// with I_a = sdot4(q, a) and I_b, I_c = udot4(q, b|c) exact integer dots.
+// The per-sub-block scale and min are applied in f32 as in the Metal kernel's
+// factorisation  sc*sum(q*x) - mn*sum(x)  (LC/src/metal/shaders/q4k_matvec.rs:13-79),
+// sum(x) being the f32 sum of the lane's (normalised) x.
+#include "matvec_common.h"
+
+namespace larql {
+
+// Three-level byte image of one 32-element x sub-block, laid out for v_dot4 against
+// nibble dwords: word w of a level holds elements {8w+0, 8w+2, 8w+4, 8w+6} (even) or
+// {8w+1, 8w+3, 8w+5, 8w+7} (odd), one per byte.  Level 0 = byte 2 of T (signed),
+// levels 1, 2 = bytes 1, 0 (unsigned).
+struct XLevels {
+    uint32_t ev[3][4], od[3][4];
+    float f0, f1, f2;   // 2^16 s', 2^8 s', s'
+    float xs;           // f32 sum of the 32 elements (Q4_K min term)
+    float xs0, xs1;     // f32 sums of elements 0..15 and 16..31 (Q6_K -32 offset)
+};
+
+// Byte `b` of each of four dwords, packed low to high.
+__device__ __forceinline__ uint32_t gather_byte(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3, int b) {
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, 0x0C0C0400u + 0x0101u * b);  // t0.b, t1.b
+    const uint32_t hi = __builtin_amdgcn_perm(t3, t2, 0x04000C0Cu + 0x01010000u * b);  // t2.b, t3.b
+    return lo | hi;
+}
+
+__device__ __forceinline__ void make_levels(const float (&x)[32], XLevels& L) {
+    float amax = 0.f, s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(x[k]));
+#pragma unroll
+    for (int k = 0; k < 16; k++) s0 += x[k];
+#pragma unroll
+    for (int k = 16; k < 32; k++) s1 += x[k];
+    const float inv = amax > 0.f ? (127.0f * 65536.0f) / amax : 0.f;
+    const float sp = amax / (127.0f * 65536.0f);
+    uint32_t T[32];
+#pragma unroll
+    for (int k = 0; k < 32; k++) T[k] = static_cast<uint32_t>(static_cast<int>(rintf(x[k] * inv)));
+#pragma unroll
+    for (int l = 0; l < 3; l++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            L.ev[l][w] = gather_byte(T[8 * w + 0], T[8 * w + 2], T[8 * w + 4], T[8 * w + 6], 2 - l);
+            L.od[l][w] = gather_byte(T[8 * w + 1], T[8 * w + 3], T[8 * w + 5], T[8 * w + 7], 2 - l);
+        }
+    L.f0 = sp * 65536.0f;
+    L.f1 = sp * 256.0f;
+    L.f2 = sp;
+    L.xs = s0 + s1;
+    L.xs0 = s0;
+    L.xs1 = s1;
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+__device__ __forceinline__ uint32_t udot4(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_udot4(a, b, c, false);
+}
+
+__device__ __forceinline__ float combine(const XLevels& L, int ia, uint32_t ib, uint32_t ic) {
+    return fmaf(static_cast<float>(ia), L.f0, fmaf(static_cast<float>(ib), L.f1, static_cast<float>(ic) * L.f2));
+}
+
+// Shared prologue: x sub-blocks into registers (optionally RMS-normalised), then
+// their int8 level images.
+template <int SBL>
+__device__ __forceinline__ void prologue_levels(const MvArgs& a, int cl, int C, int nsub, double* dscratch,
+                                                int wave, int slot, int lane, XLevels (&L)[SBL],
+                                                const bool (&valid)[SBL]) {
+    float xv[SBL][32];
+#pragma unroll
+    for (int i = 0; i < SBL; i++) load_slice<32>(a.x, (cl + i * C) * 32, valid[i], xv[i]);
+    if (a.norm_w) {
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < SBL; i++)
+#pragma unroll
+            for (int k = 0; k < 32; k++) ss += static_cast<double>(xv[i][k]) * static_cast<double>(xv[i][k]);
+        const double tot = slot_sum_d(ss, dscratch, wave, slot, a.wpr, lane);
+        // rms as the CPU path rounds it (LI/src/residual.rs:24); x * (1/rms) differs from
+        // x / rms by at most one f32 rounding.
+        const float rms = static_cast<float>(sqrt(tot / static_cast<double>(a.cols) + a.eps));
+        const float inv_rms = 1.0f / rms;
+#pragma unroll
+        for (int i = 0; i < SBL; i++) {
+            float wv[32];
+            load_slice<32>(a.norm_w, (cl + i * C) * 32, valid[i], wv);
+#pragma unroll
+            for (int k = 0; k < 32; k++) xv[i][k] = (xv[i][k] * inv_rms) * (a.norm_offset + wv[k]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < SBL; i++) make_levels(xv[i], L[i]);
+}
+
+template <int RB>
+__device__ __forceinline__ void finish_rows(const MvArgs& a, float (&acc)[RB], float* red, int t, int lane, int wave,
+                                            int nwaves, int slot, int wslot, int row0) {
+    const float tot = multi_row_reduce<RB>(acc, lane);
+    if (a.wpr == 1) {
+        epilogue_wave<RB>(a, tot, lane, row0);
+    } else {
+        constexpr int rsh = rb_shift<RB>();
+        const bool owner = (lane & ((1 << rsh) - 1)) == 0;
+        float* buf = red + (t & 1) * nwaves * RB;
+        if (owner) buf[wave * RB + (lane >> rsh)] = tot;
+        __syncthreads();
+        if (wslot == 0) {
+            float s = 0.f;
+            if (lane < RB)
+                for (int w = 0; w < a.wpr; w++) s += buf[(slot * a.wpr + w) * RB + lane];
+            epilogue_lanes(a, s, lane, row0, RB);
+        }
+    }
+}
+
+// ── Q4_K ────────────────────────────────────────────────────────────────
+// Device rows are zero-padded to a multiple of 64, so tile loads need no row test;
+// FULL means 64*wpr*SBL lanes cover K exactly, so no lane test either (otherwise the
+// spare lanes read a clamped, real block and contribute 0).
+template <int SBL, int RB, bool FULL>
+__global__ __launch_bounds__(512) void q4k_mv_kernel(MvArgs a) {
+    extern __shared__ double dyn_lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const int slot = wave / a.wpr;
+    const int wslot = wave - slot * a.wpr;
+    const int nslots = nwaves / a.wpr;
+    const int C = a.wpr * 64;
+    const int cl = wslot * 64 + lane;
+    const int nsub = a.cols >> 5;
+    const int S = a.cols >> 8;
+    const size_t rowq = static_cast<size_t>(a.cols) >> 1;
+    double* dscratch = dyn_lds;
+    float* red = reinterpret_cast<float*>(dyn_lds + nwaves);
+
+    bool valid[SBL];
+    int cc[SBL], scsel[SBL], scsh[SBL], msh[SBL];
+#pragma unroll
+    for (int i = 0; i < SBL; i++) {
+        valid[i] = cl + i * C < nsub;
+        cc[i] = FULL ? cl + i * C : min(cl + i * C, nsub - 1);
+        const int j = cc[i] & 7;
+        scsel[i] = j < 4;
+        scsh[i] = 8 * (j & 3);
+        msh[i] = 8 * (j & 3) + (j < 4 ? 0 : 4);
+    }
+    // Workgroup b handles tiles b, b + grid, b + 2 grid, ... (a.steps of them): the x
+    // prologue is paid once per workgroup.  The first tile's weight loads are issued
+    // before the prologue, each next tile's right after the current tile's arithmetic.
+    uint4 qv[RB][SBL], hv[RB][SBL];
+    auto load_tile = [&](int tile) {
+        const int row0 = (tile * nslots + slot) * RB;
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int i = 0; i < SBL; i++) {
+                const size_t row = static_cast<size_t>(row0 + r);
+                qv[r][i] = *reinterpret_cast<const uint4*>(a.qs + row * rowq + cc[i] * 16);
+                hv[r][i] = a.hdr[row * S + (cc[i] >> 3)];
+            }
+    };
+    load_tile(blockIdx.x);
+    XLevels L[SBL];
+    prologue_levels<SBL>(a, cl, C, nsub, dscratch, wave, slot, lane, L, valid);
+    for (int t = 0; t < a.steps; t++) {
+        const int tile = blockIdx.x + t * gridDim.x;
+        float acc[RB];
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            acc[r] = 0.f;
+#pragma unroll
+            for (int i = 0; i < SBL; i++) {
+                const uint4 q = qv[r][i];
+                const uint4 h = hv[r][i];
+                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+                int ia = 0;
+                uint32_t ib = 0, ic = 0;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const uint32_t lo = qw[w] & 0x0F0F0F0Fu;
+                    const uint32_t hi = (qw[w] >> 4) & 0x0F0F0F0Fu;
+                    ia = sdot4(lo, L[i].ev[0][w], ia);
+                    ia = sdot4(hi, L[i].od[0][w], ia);
+                    ib = udot4(lo, L[i].ev[1][w], ib);
+                    ib = udot4(hi, L[i].od[1][w], ib);
+                    ic = udot4(lo, L[i].ev[2][w], ic);
+                    ic = udot4(hi, L[i].od[2][w], ic);
+                }
+                const float d = h2f(h.x);
+                const float dmin = h2f(h.x >> 16);
+                const uint32_t sw = scsel[i] ? h.y : h.z;
+                float sc = d * static_cast<float>((sw >> scsh[i]) & 0x3Fu);
+                float mn = dmin * static_cast<float>((h.w >> msh[i]) & 0xFu);
+                if (!FULL && !valid[i]) { sc = 0.f; mn = 0.f; }
+                acc[r] = fmaf(sc, combine(L[i], ia, ib, ic), fmaf(-mn, L[i].xs, acc[r]));
+            }
+        }
+        if (t + 1 < a.steps && tile + static_cast<int>(gridDim.x) < a.tiles) load_tile(tile + gridDim.x);
+        if (tile < a.tiles) finish_rows<RB>(a, acc, red, t, lane, wave, nwaves, slot, wslot, (tile * nslots + slot) * RB);
+    }
+}
+
+// ── Q6_K ────────────────────────────────────────────────────────────────
+// Device layout per 32-element chunk: ql 16 B (reference order), qh 8 B rearranged at
+// registration so that for ql dword w (elements 8w..8w+7), word qh[w/2] holds the
+// 2-bit high part of element 8w + 2j + p at byte j, bits 4*(w&1) + 2p.  Then the q6
+// bytes of the even / odd elements are  lo4 | (((qh >> s) & 0x03030303) << 4).
+template <int SBL, int RB, bool FULL>
+__global__ __launch_bounds__(512) void q6k_mv_kernel(MvArgs a) {
+    extern __shared__ double dyn_lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const int slot = wave / a.wpr;
+    const int wslot = wave - slot * a.wpr;
+    const int nslots = nwaves / a.wpr;
+    const int C = a.wpr * 64;
+    const int cl = wslot * 64 + lane;
+    const int nsub = a.cols >> 5;
+    const int S = a.cols >> 8;
+    const size_t rowl = static_cast<size_t>(a.cols) >> 1;
+    const size_t rowh = static_cast<size_t>(a.cols) >> 2;
+    const size_t rows_s = static_cast<size_t>(a.cols) >> 4;
+    double* dscratch = dyn_lds;
+    float* red = reinterpret_cast<float*>(dyn_lds + nwaves);
+
+    bool valid[SBL];
+    int cc[SBL];
+#pragma unroll
+    for (int i = 0; i < SBL; i++) {
+        valid[i] = cl + i * C < nsub;
+        cc[i] = FULL ? cl + i * C : min(cl + i * C, nsub - 1);
+    }
+    uint4 lv[RB][SBL];
+    uint2 hv[RB][SBL];
+    uint32_t sv[RB][SBL], dv[RB][SBL];
+    auto load_tile = [&](int tile) {
+        const int row0 = (tile * nslots + slot) * RB;
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int i = 0; i < SBL; i++) {
+                const size_t row = static_cast<size_t>(row0 + r);
+                lv[r][i] = *reinterpret_cast<const uint4*>(a.qs + row * rowl + cc[i] * 16);
+                hv[r][i] = *reinterpret_cast<const uint2*>(a.qh + row * rowh + cc[i] * 8);
+                sv[r][i] = *reinterpret_cast<const uint16_t*>(a.sc + row * rows_s + cc[i] * 2);
+                dv[r][i] = a.d[row * S + (cc[i] >> 3)];
+            }
+    };
+    load_tile(blockIdx.x);
+    XLevels L[SBL];
+    prologue_levels<SBL>(a, cl, C, nsub, dscratch, wave, slot, lane, L, valid);
+    for (int t = 0; t < a.steps; t++) {
+        const int tile = blockIdx.x + t * gridDim.x;
+        float acc[RB];
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            acc[r] = 0.f;
+#pragma unroll
+            for (int i = 0; i < SBL; i++) {
+                const uint4 l = lv[r][i];
+                const uint32_t lw[4] = {l.x, l.y, l.z, l.w};
+                const uint32_t hw[2] = {hv[r][i].x, hv[r][i].y};
+                int ga[2] = {0, 0};
+                uint32_t gb[2] = {0u, 0u}, gc[2] = {0u, 0u};
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const uint32_t H = hw[w >> 1];
+                    const int sh = 4 * (w & 1);
+                    const uint32_t qe = (lw[w] & 0x0F0F0F0Fu) | (((H >> sh) & 0x03030303u) << 4);
+                    const uint32_t qo = ((lw[w] >> 4) & 0x0F0F0F0Fu) | (((H >> (sh + 2)) & 0x03030303u) << 4);
+                    const int h2 = w >> 1;
+                    ga[h2] = sdot4(qe, L[i].ev[0][w], ga[h2]);
+                    ga[h2] = sdot4(qo, L[i].od[0][w], ga[h2]);
+                    gb[h2] = udot4(qe, L[i].ev[1][w], gb[h2]);
+                    gb[h2] = udot4(qo, L[i].od[1][w], gb[h2]);
+                    gc[h2] = udot4(qe, L[i].ev[2][w], gc[h2]);
+                    gc[h2] = udot4(qo, L[i].od[2][w], gc[h2]);
+                }
+                const float d = h2f(dv[r][i]);
+                const uint32_t s2 = sv[r][i];
+                float sc0 = d * static_cast<float>(static_cast<int8_t>(s2 & 0xFFu));
+                float sc1 = d * static_cast<float>(static_cast<int8_t>(s2 >> 8));
+                if (!FULL && !valid[i]) { sc0 = 0.f; sc1 = 0.f; }
+                // value = sc * (q6 - 32): group sum = sc * (sum(q6 * x) - 32 * sum(x))
+                acc[r] = fmaf(sc0, fmaf(-32.f, L[i].xs0, combine(L[i], ga[0], gb[0], gc[0])), acc[r]);
+                acc[r] = fmaf(sc1, fmaf(-32.f, L[i].xs1, combine(L[i], ga[1], gb[1], gc[1])), acc[r]);
+            }
+        }
+        if (t + 1 < a.steps && tile + static_cast<int>(gridDim.x) < a.tiles) load_tile(tile + gridDim.x);
+        if (tile < a.tiles) finish_rows<RB>(a, acc, red, t, lane, wave, nwaves, slot, wslot, (tile * nslots + slot) * RB);
+    }
+}
+
+// ── launch ──────────────────────────────────────────────────────────────
+template <int SBL, int RB>
+static void launch_mv_t(const DevWeight& w, MvArgs a, hipStream_t s, int nslots, bool full) {
+    const int threads = 64 * a.wpr * nslots;
+    const size_t rows_per_tile = static_cast<size_t>(nslots) * RB;
+    if (w.rows_pad % rows_per_tile) fail(LARQL_HIP_ERR_INVALID, "matvec: device rows not padded to the tile");
+    const size_t tiles = w.rows_pad / rows_per_tile;
+    // About two workgroups per CU; each loops over its share of the tiles.
+    const size_t target = 2 * static_cast<size_t>(a.num_cus > 0 ? a.num_cus : 256);
+    a.tiles = static_cast<int>(tiles);
+    a.steps = static_cast<int>((tiles + target - 1) / target);
+    const size_t grid = (tiles + a.steps - 1) / a.steps;
+    const int nwaves = threads / 64;
+    const size_t shmem = nwaves * sizeof(double) + 2 * nwaves * RB * sizeof(float);
+    const dim3 g(static_cast<unsigned>(grid)), b(threads);
+    if (w.format == LARQL_Q4_K) {
+        a.qs = w.qs;
+        a.hdr = w.hdr;
+        if (full) q4k_mv_kernel<SBL, RB, true><<<g, b, shmem, s>>>(a);
+        else q4k_mv_kernel<SBL, RB, false><<<g, b, shmem, s>>>(a);
+    } else {
+        a.qs = w.qs;
+        a.qh = w.qh;
+        a.sc = w.sc;
+        a.d = static_cast<const uint16_t*>(w.d);
+        if (full) q6k_mv_kernel<SBL, RB, true><<<g, b, shmem, s>>>(a);
+        else q6k_mv_kernel<SBL, RB, false><<<g, b, shmem, s>>>(a);
+    }
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s) {
+    if (w.format != LARQL_Q4_K && w.format != LARQL_Q6_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "launch_mv: format");
+    a.rows = static_cast<int>(w.rows);
+    a.cols = static_cast<int>(w.cols);
+    if (a.epi == EPI_SILU_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "silu pair epilogue needs even rows");
+    const size_t nsub = w.cols / 32;
+    const size_t waves1 = (nsub + 63) / 64;
+    if (waves1 <= 8) {
+        // one sub-block per lane; >= 256 threads per workgroup where possible
+        a.wpr = static_cast<int>(waves1);
+        int nslots = 1;
+        while (a.wpr * nslots * 2 <= 4) nslots *= 2;
+        launch_mv_t<1, 8>(w, a, s, nslots, static_cast<size_t>(64) * a.wpr == nsub);
+    } else {
+        a.wpr = static_cast<int>((nsub + 127) / 128);
+        if (a.wpr > 8) fail(LARQL_HIP_ERR_UNSUPPORTED, "matvec: hidden too large (max 32768)");
+        launch_mv_t<2, 4>(w, a, s, 1, static_cast<size_t>(128) * a.wpr == nsub);
+    }
+}
+
+void launch_q4k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s) {
+    if (m != 1) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4k_matvec: batch > 1 not supported");
+    MvArgs a;
+    a.x = x;
+    a.out = out;
+    launch_mv(w, a, s);
+}
+
+void launch_q6k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s) {
+    if (m != 1) fail(LARQL_HIP_ERR_UNSUPPORTED, "q6k_matvec: batch > 1 not supported");
+    MvArgs a;
+    a.x = x;
+    a.out = out;
+    launch_mv(w, a, s);
+}
+
+}  // namespace larql

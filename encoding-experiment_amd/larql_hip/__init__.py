@@ -64,7 +64,86 @@ SIGNATURES = {
     "larql_hip_quantize_to_q8_dev": (_I, [_P, _P, _SZ, _SZ, _P, _P, _P]),
     "larql_hip_quantize_weights": (_I, [_P, _I, _P, _SZ, _P, _P]),
     "larql_hip_quantize_weights_dev": (_I, [_P, _I, _P, _SZ, _P, _P, _P]),
+    # decode step (structs declared below; pointers passed as void*)
+    "larql_hip_decode_token": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
+    "larql_hip_populate_kv_layer": (_I, [_P, _SZ, _P, _P, _SZ, _SZ, _SZ]),
+    "larql_hip_reset_kv_cache": (_I, [_P]),
+    "larql_hip_kv_cache_len": (_I, [_P, ctypes.POINTER(_SZ)]),
+    "larql_hip_kv_truncate": (_I, [_P, _SZ]),
+    "larql_hip_populate_kv_layer_f16_dev": (_I, [_P, _SZ, _P, _P, _SZ, _SZ, _SZ]),
+    "larql_hip_model_create": (_I, [_P, _P, _SZ, _SZ, _SZ, _I, ctypes.POINTER(_P)]),
+    "larql_hip_model_set_head": (_I, [_P, _P, _P, _SZ, _P, ctypes.c_float, _I]),
+    "larql_hip_model_destroy": (_I, [_P, _P]),
+    "larql_hip_model_decode_dev": (_I, [_P, _P, _P, _P, _P, _P]),
 }
+
+NORM_RMS, NORM_LAYER = 0, 1
+FFN_GATED, FFN_STANDARD = 0, 1
+ACT_SILU, ACT_GELU_TANH = 0, 1
+
+
+class QuantWeight(ctypes.Structure):
+    """larql_quant_weight / QuantWeight (larql-compute/src/pipeline.rs:22-27)."""
+    _fields_ = [("data", _P), ("len", _SZ), ("scales", _P), ("format", _I)]
+
+
+class PipelineLayer(ctypes.Structure):
+    """larql_pipeline_layer / FullPipelineLayer (larql-compute/src/pipeline.rs:60-120)."""
+    _fields_ = [
+        ("wq", QuantWeight), ("wk", QuantWeight), ("wv", QuantWeight), ("wo", QuantWeight),
+        ("gate", QuantWeight), ("up", QuantWeight), ("down", QuantWeight),
+        ("input_norm", _P), ("post_attn_norm", _P), ("pre_ffn_norm", _P), ("post_ffn_norm", _P),
+        ("input_norm_bias", _P), ("post_attn_norm_bias", _P),
+        ("norm_offset", ctypes.c_float), ("qk_norm_offset", ctypes.c_float), ("eps", ctypes.c_float),
+        ("has_post_norms", _I), ("norm_type", _I), ("ffn_type", _I), ("activation", _I),
+        ("attn_scale", ctypes.c_float), ("head_dim", _SZ), ("num_q_heads", _SZ), ("num_kv_heads", _SZ),
+        ("rope_base", ctypes.c_float), ("rotary_dim", _SZ), ("sliding_window", _SZ),
+        ("has_v_norm", _I), ("layer_scalar", ctypes.c_float),
+        ("ffn_up_bias", _P), ("ffn_down_bias", _P),
+    ]
+
+
+def _addr(a):
+    """Address of a numpy array (host) or tensor-like (device) or int."""
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    if isinstance(a, np.ndarray):
+        assert a.flags["C_CONTIGUOUS"]
+        return a.ctypes.data
+    return a.data_ptr()
+
+
+def _nbytes(a):
+    if isinstance(a, np.ndarray):
+        return a.nbytes
+    return a.numel() * a.element_size()
+
+
+def make_layer(wq, wk, wv, wo, gate, up, down, input_norm, post_attn_norm, *, head_dim, num_q_heads,
+               num_kv_heads, rope_base, eps=1e-6, attn_scale=None, fmt=Q4_K, formats=None,
+               rotary_dim=0, sliding_window=0):
+    """A Llama FullPipelineLayer over numpy (host) or device tensors of reference-layout bytes.
+    Keep the source arrays alive while the struct is in use."""
+    L = PipelineLayer()
+    names = ("wq", "wk", "wv", "wo", "gate", "up", "down")
+    for name, arr in zip(names, (wq, wk, wv, wo, gate, up, down)):
+        f = (formats or {}).get(name, fmt)
+        setattr(L, name, QuantWeight(_addr(arr), _nbytes(arr), None, f))
+    L.input_norm = _addr(input_norm)
+    L.post_attn_norm = _addr(post_attn_norm)
+    L.norm_offset = 0.0
+    L.eps = eps
+    L.norm_type = NORM_RMS
+    L.ffn_type = FFN_GATED
+    L.activation = ACT_SILU
+    L.attn_scale = attn_scale if attn_scale is not None else float(1.0 / np.sqrt(head_dim))
+    L.head_dim, L.num_q_heads, L.num_kv_heads = head_dim, num_q_heads, num_kv_heads
+    L.rope_base = rope_base
+    L.rotary_dim = rotary_dim
+    L.sliding_window = sliding_window
+    return L
 
 QUANT_BYTES = {Q4_0: (32, 18), Q4_K: (256, 148), Q6_K: (256, 210), Q8_0: (32, 32)}
 
@@ -104,11 +183,15 @@ def _dptr(t):
 
 
 def _stream_ptr(stream):
+    """hipStream_t of a torch stream (or a raw handle).  None selects the context's
+    own stream.  The legacy default stream (handle 0) is rejected: NULL means
+    "context stream" in the C ABI, so work would silently leave the caller's order."""
     if stream is None:
         return None
-    if isinstance(stream, int):
-        return _P(stream)
-    return _P(stream.cuda_stream)
+    h = stream if isinstance(stream, int) else stream.cuda_stream
+    if h == 0:
+        raise ValueError("pass a non-default stream (e.g. torch.cuda.Stream()); handle 0 means the context stream")
+    return _P(h)
 
 
 class HipBackend:
@@ -263,6 +346,47 @@ class HipBackend:
             return None
         return (out.view(np.int8), sc) if fmt == Q8_0 else out
 
+    # ── decode step (backend.rs:99-123) ───────────────────────────────
+    def has_kv(self) -> bool:
+        return self.has_kv_cache()
+
+    def decode_token(self, layers, x, hidden: int, inter: int, q_dim: int, kv_dim: int, num_q_heads: int,
+                     num_kv_heads: int, head_dim: int, rope_base: float):
+        """backend.rs:115-123: one token through all layers with the KV cache; returns the
+        final hidden state (before the final norm) or None."""
+        arr = (PipelineLayer * len(layers))(*layers)
+        xv, xp = _arr(x, np.float32)
+        out = np.empty(hidden, dtype=np.float32)
+        rc = self._lib.larql_hip_decode_token(self._ctx, ctypes.cast(arr, _P), len(layers), xp, hidden, inter, q_dim,
+                                              kv_dim, num_q_heads, num_kv_heads, head_dim, rope_base,
+                                              out.ctypes.data_as(_P))
+        return out if self._ok(rc) else None
+
+    def populate_kv_layer(self, layer: int, k_data, v_data, seq_len: int, num_kv_heads: int, head_dim: int):
+        """backend.rs:103-107 (K/V f32 [seq_len, num_kv*head_dim], stored as fp16)."""
+        k, kp = _arr(k_data, np.float32)
+        v, vp = _arr(v_data, np.float32)
+        self._check(self._lib.larql_hip_populate_kv_layer(self._ctx, layer, kp, vp, seq_len, num_kv_heads, head_dim))
+
+    def populate_kv_layer_f16_dev(self, layer: int, k_dev, v_dev, seq_len: int, num_kv_heads: int, head_dim: int):
+        self._check(self._lib.larql_hip_populate_kv_layer_f16_dev(self._ctx, layer, _dptr(k_dev), _dptr(v_dev),
+                                                                  seq_len, num_kv_heads, head_dim))
+
+    def reset_kv_cache(self):
+        """backend.rs:110."""
+        self._check(self._lib.larql_hip_reset_kv_cache(self._ctx))
+
+    def kv_cache_len(self) -> int:
+        n = _SZ()
+        self._check(self._lib.larql_hip_kv_cache_len(self._ctx, ctypes.byref(n)))
+        return n.value
+
+    def kv_truncate(self, n: int):
+        self._check(self._lib.larql_hip_kv_truncate(self._ctx, n))
+
+    def model(self, layers, hidden: int, inter: int, weights_on_device: bool = True) -> DeviceModel:
+        return DeviceModel(self, layers, hidden, inter, weights_on_device)
+
     # ── device-resident fast path ──────────────────────────────────────
     def matvec_dev(self, handle: int, x, out, m: int = 1, x_scales=None, stream=None):
         self._check(self._lib.larql_hip_matvec_dev(self._ctx, handle, _dptr(x), _dptr(x_scales), _dptr(out), m,
@@ -275,6 +399,33 @@ class HipBackend:
     def quantize_to_q8_dev(self, x, n: int, m: int, q8, scales, stream=None):
         self._check(self._lib.larql_hip_quantize_to_q8_dev(self._ctx, _dptr(x), n, m, _dptr(q8), _dptr(scales),
                                                            _stream_ptr(stream)))
+
+
+class DeviceModel:
+    """Device-resident decoder (larql_hip_model): registered once, decoded per token."""
+
+    def __init__(self, backend: "HipBackend", layers, hidden: int, inter: int, weights_on_device: bool):
+        self.be = backend
+        arr = (PipelineLayer * len(layers))(*layers)
+        h = _P()
+        backend._check(backend._lib.larql_hip_model_create(backend._ctx, ctypes.cast(arr, _P), len(layers), hidden,
+                                                           inter, int(weights_on_device), ctypes.byref(h)))
+        self._h = h
+        self.hidden = hidden
+
+    def set_head(self, head, vocab: int, final_norm, eps: float = 1e-6, fmt: int = Q6_K, on_device: bool = True):
+        qw = QuantWeight(_addr(head), _nbytes(head), None, fmt)
+        self.be._check(self.be._lib.larql_hip_model_set_head(self.be._ctx, self._h, ctypes.byref(qw), vocab,
+                                                             _P(_addr(final_norm)), eps, int(on_device)))
+
+    def decode_dev(self, x, hidden_out=None, logits=None, stream=None):
+        self.be._check(self.be._lib.larql_hip_model_decode_dev(self.be._ctx, self._h, _dptr(x), _dptr(hidden_out),
+                                                               _dptr(logits), _stream_ptr(stream)))
+
+    def close(self):
+        if self._h:
+            self.be._lib.larql_hip_model_destroy(self.be._ctx, self._h)
+            self._h = None
 
 
 def default_backend(device: int = 0, strict: bool = False) -> HipBackend:

@@ -147,6 +147,102 @@ int larql_hip_quantize_to_q8_dev(larql_hip_ctx* ctx, const float* x, size_t n, s
 int larql_hip_quantize_weights_dev(larql_hip_ctx* ctx, int format, const float* x, size_t n, void* out,
                                    float* q8_scales, void* stream);
 
+
+/* ── decode step: layers, KV cache, full-pipeline decode ───────────────── */
+
+/* QuantWeight — LC/src/pipeline.rs:22-27.  `data`/`len` are reference-layout
+ * bytes (host memory, or device memory for the *_dev model constructor);
+ * `scales` only for LARQL_Q8_0. */
+typedef struct {
+    const void* data;
+    size_t len;
+    const float* scales;
+    int format;
+} larql_quant_weight;
+
+/* NormType / FfnType / Activation — LC/src/pipeline.rs:31-56. */
+enum { LARQL_NORM_RMS = 0, LARQL_NORM_LAYER = 1 };
+enum { LARQL_FFN_GATED = 0, LARQL_FFN_STANDARD = 1 };
+enum { LARQL_ACT_SILU = 0, LARQL_ACT_GELU_TANH = 1 };
+
+/* FullPipelineLayer — LC/src/pipeline.rs:60-120, same fields in the same order.
+ * Optional vectors are NULL when absent.  The HIP decode step implements the
+ * Llama family: RMSNorm, gated SiLU FFN, no post-norms, no V-norm, no biases,
+ * no layer scalar, Q4_K or Q6_K projections; anything else is reported as
+ * LARQL_HIP_ERR_UNSUPPORTED so the caller falls back (predict.rs:397-430). */
+typedef struct {
+    larql_quant_weight wq, wk, wv, wo;
+    larql_quant_weight gate, up, down;
+    const float* input_norm;
+    const float* post_attn_norm;
+    const float* pre_ffn_norm;
+    const float* post_ffn_norm;
+    const float* input_norm_bias;
+    const float* post_attn_norm_bias;
+    float norm_offset;
+    float qk_norm_offset;
+    float eps;
+    int has_post_norms;
+    int norm_type;
+    int ffn_type;
+    int activation;
+    float attn_scale;
+    size_t head_dim;
+    size_t num_q_heads;
+    size_t num_kv_heads;
+    float rope_base;
+    size_t rotary_dim;      /* 0 = head_dim */
+    size_t sliding_window;  /* 0 = full attention */
+    int has_v_norm;
+    float layer_scalar;
+    const float* ffn_up_bias;
+    const float* ffn_down_bias;
+} larql_pipeline_layer;
+
+/* ComputeBackend::decode_token — LC/src/backend.rs:115-123.  Runs one token
+ * through all layers with the KV cache (fp16 on the device, appended at the
+ * current length, which then advances by one; attention is not limited in T).
+ * x and out are host vectors of `hidden` floats (out = final hidden state,
+ * before the final norm, as the reference returns it). */
+int larql_hip_decode_token(larql_hip_ctx* ctx, const larql_pipeline_layer* layers, size_t num_layers,
+                           const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim,
+                           size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float rope_base,
+                           float* out);
+
+/* ComputeBackend::populate_kv_layer — LC/src/backend.rs:103-107: K/V rows
+ * [seq_len][num_kv_heads*head_dim] f32 (stored as fp16, RNE); sets the cache
+ * length to seq_len. */
+int larql_hip_populate_kv_layer(larql_hip_ctx* ctx, size_t layer, const float* k_data, const float* v_data,
+                                size_t seq_len, size_t num_kv_heads, size_t head_dim);
+/* ComputeBackend::reset_kv_cache — LC/src/backend.rs:110 (drops the cache). */
+int larql_hip_reset_kv_cache(larql_hip_ctx* ctx);
+/* Current cache length (positions held). */
+int larql_hip_kv_cache_len(larql_hip_ctx* ctx, size_t* len);
+/* Rewind the cache to `len` positions (len <= current length). */
+int larql_hip_kv_truncate(larql_hip_ctx* ctx, size_t len);
+/* populate_kv_layer from device fp16 data [seq_len][num_kv_heads*head_dim]. */
+int larql_hip_populate_kv_layer_f16_dev(larql_hip_ctx* ctx, size_t layer, const uint16_t* k_dev,
+                                        const uint16_t* v_dev, size_t seq_len, size_t num_kv_heads,
+                                        size_t head_dim);
+
+/* ── device-resident decoder (extension; no counterpart in the trait) ──────
+ * The same decode step with the weights registered once and activations in
+ * device memory, for serving loops and benchmarks.  `weights_on_device`
+ * selects whether the larql_quant_weight data pointers are device addresses. */
+typedef struct larql_hip_model larql_hip_model;
+int larql_hip_model_create(larql_hip_ctx* ctx, const larql_pipeline_layer* layers, size_t num_layers,
+                           size_t hidden, size_t inter, int weights_on_device, larql_hip_model** out);
+/* Final norm + output head (LI/src/layer_graph/generate.rs:140-143): logits =
+ * head . rms_norm(h, final_norm).  head: Q4_K or Q6_K [vocab][hidden]. */
+int larql_hip_model_set_head(larql_hip_ctx* ctx, larql_hip_model* model, const larql_quant_weight* head,
+                             size_t vocab, const float* final_norm, float eps, int weights_on_device);
+int larql_hip_model_destroy(larql_hip_ctx* ctx, larql_hip_model* model);
+/* One decode step on device memory: x_dev [hidden] in; hidden_out_dev [hidden]
+ * (may be NULL) and logits_dev [vocab] (may be NULL; needs a head) out.  Appends
+ * K/V at the current cache length and advances it.  Enqueues on `stream`. */
+int larql_hip_model_decode_dev(larql_hip_ctx* ctx, larql_hip_model* model, const float* x_dev,
+                               float* hidden_out_dev, float* logits_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

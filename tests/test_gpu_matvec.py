@@ -55,7 +55,7 @@ def fuzz_q6k(rows, cols, seed):
     return b.reshape(-1)
 
 
-Q4K_SHAPES = [(1, 256), (7, 256), (64, 512), (300, 4096), (1000, 2560), (14336, 4096), (4096, 14336)]
+Q4K_SHAPES = [(1, 256), (7, 256), (64, 512), (300, 4096), (1000, 2560), (14336, 4096), (4096, 14336), (100, 20480)]
 
 
 @pytest.mark.parametrize("rows,cols", Q4K_SHAPES)
@@ -80,7 +80,7 @@ def test_q4k_matvec_fuzzed_bytes(hip, rows, cols):
     assert rel_err(got, ref) <= REL_TOL
 
 
-Q6K_SHAPES = [(1, 256), (9, 512), (300, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
+Q6K_SHAPES = [(1, 256), (9, 512), (300, 4096), (14336, 4096), (4096, 14336), (128256, 4096), (70, 20480), (50, 2560)]
 
 
 @pytest.mark.parametrize("rows,cols", Q6K_SHAPES)
@@ -142,7 +142,10 @@ def test_f16_decode_all_codes_on_device(hip):
     q8 = np.ones(32, np.int8)
     s8 = np.ones(1, np.float32)
     got = hip.q4_matvec(blocks.reshape(-1), q8, s8, rows, 32)
-    want = codes.view(np.float16).astype(np.float32) * np.float32(32.0)
+    # the reference accumulates from +0.0 (acc = 0.0 + p), which maps -0.0 to +0.0
+    want = np.float32(0.0) + codes.view(np.float16).astype(np.float32) * np.float32(32.0)
+    ref = oracle.q4_0_matvec_blockint(blocks.reshape(-1), q8, s8, rows, 32)
+    assert np.array_equal(ref.view(np.uint32), want.view(np.uint32))
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
