@@ -150,12 +150,24 @@ QUANT_BYTES = {Q4_0: (32, 18), Q4_K: (256, 148), Q6_K: (256, 210), Q8_0: (32, 32
 _lib = None
 
 
+def _share_torch_hip_runtime():
+    """PyTorch-ROCm ships its own libamdhip64 (soname libamdhip64.so.7).  If it is
+    loaded first, liblarql_hip binds to that copy; if liblarql_hip loaded the system
+    copy first, torch would load a second HIP/HSA runtime that cannot open the device.
+    Importing torch first keeps one runtime per process."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def load_library():
     """Load liblarql_hip.so once; raise if it has not been built."""
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise ImportError(f"liblarql_hip.so not built at {LIB_PATH}; run `make -C encoding-experiment_amd`")
+        _share_torch_hip_runtime()
         lib = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

@@ -56,3 +56,16 @@ def test_product_does_not_reference_oracle():
             if fn.endswith((".py", ".hip", ".cpp", ".h", ".hpp")):
                 text = open(os.path.join(dirpath, fn), errors="ignore").read()
                 assert "import oracle" not in text and "larql_oracle" not in text and "liblarql_oracle" not in text, fn
+
+
+def test_single_hip_runtime_in_process():
+    """The binding must not put a second libamdhip64 next to torch's."""
+    import subprocess
+    import sys
+
+    code = ("import sys; sys.path[:0] = [%r, %r]; import larql_hip, torch; "
+            "maps = [l.split()[-1] for l in open('/proc/self/maps') if 'libamdhip64' in l and 'r-xp' in l]; "
+            "print(len(set(maps)))") % (ROOT, os.path.join(ROOT, "encoding-experiment_amd"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "1", out.stdout
