@@ -5,6 +5,7 @@
 // failure into a negative status plus a message (larql_hip_last_error).  Nothing in
 // here falls back to a CPU computation: a failure is reported, and the caller decides
 // (the reference callers fall back to the CPU backend on None, LV/src/index/gate.rs:684-704).
+#include <atomic>
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -18,6 +19,19 @@ using larql::Error;
 using larql::fail;
 
 namespace larql {
+
+int current_device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    LARQL_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) fail(LARQL_HIP_ERR_DEVICE, "device index out of range");
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        LARQL_HIP_CHECK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
 
 void* ensure(larql_hip_ctx* c, DeviceBuf& b, size_t bytes) {
     if (bytes == 0) bytes = 1;

@@ -42,7 +42,6 @@ struct larql_hip_model {
     std::vector<void*> allocs;
     // workspace
     float *h0 = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *xin = nullptr;
-    int* counter = nullptr;
     larql::DeviceBuf part;
     // host-pointer decode_token cache key
     std::vector<uint64_t> key;
@@ -147,6 +146,7 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
             d.nkv = static_cast<int>(L.num_kv_heads);
             if (d.hd <= 0 || d.nq <= 0 || d.nkv <= 0 || d.nq % d.nkv || d.hd % 8)
                 fail(LARQL_HIP_ERR_INVALID, "decode: bad head geometry");
+            if (d.hd > 256) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: head_dim > 256");
             d.rdim = L.rotary_dim ? static_cast<int>(L.rotary_dim) : d.hd;
             if (d.rdim > d.hd || d.rdim % 2) fail(LARQL_HIP_ERR_INVALID, "decode: bad rotary_dim");
             if (larql::attn_lds_bytes(d.nq / d.nkv, d.hd, d.rdim) > 64 * 1024)
@@ -182,8 +182,6 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
         m->qkv = static_cast<float*>(dev_alloc(m, (m->q_dim + 2 * m->kv_dim) * 4));
         m->attn = static_cast<float*>(dev_alloc(m, m->q_dim * 4));
         m->act = static_cast<float*>(dev_alloc(m, inter * 4));
-        m->counter = static_cast<int*>(dev_alloc(m, m->nkv * sizeof(int)));
-        LARQL_HIP_CHECK(hipMemsetAsync(m->counter, 0, m->nkv * sizeof(int), c->stream));
         LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
     } catch (...) {
         for (void* p : m->allocs) (void)hipFree(p);
@@ -207,7 +205,33 @@ void kv_free(larql_hip_ctx* c) {
     (void)hipDeviceSynchronize();
     for (auto* p : c->kv.k) (void)hipFree(p);
     for (auto* p : c->kv.v) (void)hipFree(p);
+    for (auto& r : c->kv.rope) (void)hipFree(r.cs);
     c->kv = larql::KVCache{};
+}
+
+// RoPE cos/sin table for (base, rdim) covering the cache capacity; built once per
+// capacity (the cache only grows), on stream s, which is then synchronised so the
+// table may be used from any stream afterwards.
+const float2* rope_table(larql_hip_ctx* c, double base, int rdim, hipStream_t s) {
+    auto& kv = c->kv;
+    for (auto& r : kv.rope)
+        if (r.base == base && r.rdim == rdim && r.cap >= kv.max_seq) return r.cs;
+    larql::RopeTable t;
+    t.base = base;
+    t.rdim = rdim;
+    t.cap = kv.max_seq;
+    const size_t bytes = t.cap * static_cast<size_t>(rdim / 2) * sizeof(float2);
+    if (hipMalloc(&t.cs, bytes ? bytes : 1) != hipSuccess) fail(LARQL_HIP_ERR_NOMEM, "RoPE table allocation failed");
+    larql::launch_rope_table(t.cs, t.cap, rdim, base, s);
+    LARQL_HIP_CHECK(hipStreamSynchronize(s));
+    for (auto it = kv.rope.begin(); it != kv.rope.end(); ++it)
+        if (it->base == base && it->rdim == rdim) {
+            (void)hipFree(it->cs);
+            kv.rope.erase(it);
+            break;
+        }
+    kv.rope.push_back(t);
+    return t.cs;
 }
 
 // Make room for `layers` layers of [cap][num_kv][head_dim] with cap >= need (initial
@@ -275,7 +299,6 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
         at.vc = kv.v[l];
         at.out = m->attn;
         at.part = part;
-        at.counter = m->counter;
         at.num_q = L.nq;
         at.num_kv = L.nkv;
         at.hd = L.hd;
@@ -283,7 +306,7 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
         at.T = T;
         at.t_begin = (L.window > 0 && T > L.window) ? T - L.window : 0;
         at.scale = L.attn_scale;
-        at.rope_base = L.rope_base;
+        at.rope = rope_table(c, L.rope_base, L.rdim, s);
         larql::launch_attention(at, s);
 
         larql::MvArgs o;

@@ -88,6 +88,9 @@ uint64_t host_fingerprint(const void* data, size_t len);
 size_t ref_row_bytes(int format, size_t cols);   // bytes per row in the reference layout
 size_t dev_layout_bytes(int format, size_t rows_pad, size_t cols);
 inline size_t pad_rows(size_t rows) { return (rows + 63) & ~size_t(63); }
+
+// Compute units of the current device (queried once per device, then cached).
+int current_device_cus();
 void dev_layout_carve(DevWeight& w);              // set sub-array pointers from base
 
 // Repack reference-layout bytes already on the device (`raw`, src_rows rows; 0 = w.rows)
@@ -96,10 +99,19 @@ void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scale
                    size_t src_rows = 0, size_t row0 = 0, size_t stride = 1);
 
 // ── KV cache ────────────────────────────────────────────────────────────
+// cos / sin of the split-half RoPE angles for positions [0, cap): float2 [cap][rdim/2].
+struct RopeTable {
+    double base = 0.0;
+    int rdim = 0;
+    size_t cap = 0;
+    float2* cs = nullptr;
+};
+
 struct KVCache {
     size_t num_layers = 0, max_seq = 0, num_kv = 0, head_dim = 0;
     size_t current_len = 0;
     std::vector<__half*> k, v;   // per layer [max_seq][num_kv][head_dim]
+    std::vector<RopeTable> rope;  // one per (rope_base, rdim) in use, cap >= max_seq
 };
 
 // ── context ─────────────────────────────────────────────────────────────

@@ -31,36 +31,67 @@ struct MvArgs {
     // epilogue
     int epi = EPI_STORE;
     const float* resid = nullptr;
-    // launch shape: waves per row slot, row tiles, tiles per workgroup, CUs on the device
-    int wpr = 1, tiles = 0, steps = 1, num_cus = 256;
+    // launch shape: waves per row slot, row tiles, tiles per workgroup, CUs on the device,
+    // device rows (a multiple of 64; rows past `rows` decode to zero)
+    int wpr = 1, tiles = 0, steps = 1, num_cus = 0, rows_pad = 0;
 };
 
-// Reduce RB per-lane partials over the 64 lanes of a wave; on return lane
-// (r << (6 - log2 RB)) holds the total of row r.
+// Transposing reduction across 32- and 16-lane halves (gfx950 permlane swaps): after
+// swap(A, B) and A + B, the lower half of the result holds A's pair sums and the upper
+// half B's.  With A == B it is a plain butterfly step.
+__device__ __forceinline__ float swap32_add(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap16_add(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_ROW_MIRROR = 0x140;       // lane i <- 15 - i within 16 lanes
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i <- 7 - i within 8 lanes
+constexpr int DPP_QUAD_REV = 0x1B;          // quad_perm [3,2,1,0]
+constexpr int DPP_QUAD_SWAP = 0xB1;         // quad_perm [1,0,3,2]
+
+// Reduce RB per-lane partials (RB <= 8) over the 64 lanes of a wave; on return lane
+// (r << (6 - log2 RB)) holds the total of row r (every lane of that 64/RB block does).
+// Each halving step keeps RB/2 registers: rows of the lower half-block in the lower
+// lanes, rows of the upper half-block in the upper lanes.
 template <int RB>
 __device__ __forceinline__ float multi_row_reduce(float (&v)[RB], int lane) {
-    int n = RB;
-    int mask = 32;
+    static_assert(RB == 1 || RB == 2 || RB == 4 || RB == 8, "RB must be 1, 2, 4 or 8");
+    float w[4];
+    if constexpr (RB >= 2) {
 #pragma unroll
-    for (int step = 0; step < 6; step++) {
-        if (n > 1) {
-            const bool upper = (lane & mask) != 0;
-            const int half = n >> 1;
-#pragma unroll
-            for (int i = 0; i < RB / 2; i++) {
-                if (i < half) {
-                    float keep = upper ? v[i + half] : v[i];
-                    float send = upper ? v[i] : v[i + half];
-                    v[i] = keep + __shfl_xor(send, mask, 64);
-                }
-            }
-            n = half;
-        } else {
-            v[0] += __shfl_xor(v[0], mask, 64);
-        }
-        mask >>= 1;
+        for (int i = 0; i < RB / 2; i++) w[i] = swap32_add(v[i], v[i + RB / 2]);
+    } else {
+        w[0] = swap32_add(v[0], v[0]);
     }
-    return v[0];
+    constexpr int n32 = RB >= 2 ? RB / 2 : 1;
+    float u[2];
+    if constexpr (n32 >= 2) {
+#pragma unroll
+        for (int i = 0; i < n32 / 2; i++) u[i] = swap16_add(w[i], w[i + n32 / 2]);
+    } else {
+        u[0] = swap16_add(w[0], w[0]);
+    }
+    constexpr int n16 = n32 >= 2 ? n32 / 2 : 1;
+    float t;
+    if constexpr (n16 == 2) {
+        const bool upper = (lane & 8) != 0;
+        const float keep = upper ? u[1] : u[0];
+        const float send = upper ? u[0] : u[1];
+        t = keep + dpp_f<DPP_ROW_MIRROR>(send);
+    } else {
+        t = u[0] + dpp_f<DPP_ROW_MIRROR>(u[0]);
+    }
+    t += dpp_f<DPP_ROW_HALF_MIRROR>(t);
+    t += dpp_f<DPP_QUAD_REV>(t);
+    t += dpp_f<DPP_QUAD_SWAP>(t);
+    return t;
 }
 
 template <int RB>
@@ -126,5 +157,7 @@ __device__ __forceinline__ void load_slice(const float* __restrict__ base, int c
 }
 
 void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s);
+bool stream_mv_supported(const DevWeight& w);
+void launch_mv_stream(const DevWeight& w, MvArgs a, hipStream_t s);
 
 }  // namespace larql

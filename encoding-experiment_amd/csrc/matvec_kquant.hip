@@ -10,77 +10,17 @@
 // loads of its whole RB-row tile before any arithmetic.
 //
 // Arithmetic: the dot of 4-bit / 6-bit integer codes with x is done in exact int32
-// with v_dot4.  Each lane turns its x sub-block once into fixed point,
-//   T_k = rint(x_k * 127 * 2^16 / max|x|)        (|T_k| < 2^23, exact in f32),
-// so x_k ~= s' * T_k with s' = max|x| / (127 * 2^16) and |x_k - s' T_k| <= ~1.2e-7 max|x|
-// (the size of an f32 rounding of the block's largest term).  The bytes of T are three
-// int8/uint8 levels, T = 2^16 a + 2^8 b + c with a signed and b, c unsigned, so
-//   sum(q * x) = s' * (2^16 I_a + 2^8 I_b + I_c)
+// with v_dot4.  Each lane turns its x sub-block once into 23-bit fixed point
+// T = 65536 a + 256 b + c (three byte planes, x ~= s' T, error <= 1.2e-7 max|x|), so
+//   sum(q * x) = s' * (65536 I_a + 256 I_b + I_c)
 // with I_a = sdot4(q, a) and I_b, I_c = udot4(q, b|c) exact integer dots.
 // The per-sub-block scale and min are applied in f32 as in the Metal kernel's
 // factorisation  sc*sum(q*x) - mn*sum(x)  (LC/src/metal/shaders/q4k_matvec.rs:13-79),
 // sum(x) being the f32 sum of the lane's (normalised) x.
+#include "kquant_levels.h"
 #include "matvec_common.h"
 
 namespace larql {
-
-// Three-level byte image of one 32-element x sub-block, laid out for v_dot4 against
-// nibble dwords: word w of a level holds elements {8w+0, 8w+2, 8w+4, 8w+6} (even) or
-// {8w+1, 8w+3, 8w+5, 8w+7} (odd), one per byte.  Level 0 = byte 2 of T (signed),
-// levels 1, 2 = bytes 1, 0 (unsigned).
-struct XLevels {
-    uint32_t ev[3][4], od[3][4];
-    float f0, f1, f2;   // 2^16 s', 2^8 s', s'
-    float xs;           // f32 sum of the 32 elements (Q4_K min term)
-    float xs0, xs1;     // f32 sums of elements 0..15 and 16..31 (Q6_K -32 offset)
-};
-
-// Byte `b` of each of four dwords, packed low to high.
-__device__ __forceinline__ uint32_t gather_byte(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3, int b) {
-    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, 0x0C0C0400u + 0x0101u * b);  // t0.b, t1.b
-    const uint32_t hi = __builtin_amdgcn_perm(t3, t2, 0x04000C0Cu + 0x01010000u * b);  // t2.b, t3.b
-    return lo | hi;
-}
-
-__device__ __forceinline__ void make_levels(const float (&x)[32], XLevels& L) {
-    float amax = 0.f, s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(x[k]));
-#pragma unroll
-    for (int k = 0; k < 16; k++) s0 += x[k];
-#pragma unroll
-    for (int k = 16; k < 32; k++) s1 += x[k];
-    const float inv = amax > 0.f ? (127.0f * 65536.0f) / amax : 0.f;
-    const float sp = amax / (127.0f * 65536.0f);
-    uint32_t T[32];
-#pragma unroll
-    for (int k = 0; k < 32; k++) T[k] = static_cast<uint32_t>(static_cast<int>(rintf(x[k] * inv)));
-#pragma unroll
-    for (int l = 0; l < 3; l++)
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            L.ev[l][w] = gather_byte(T[8 * w + 0], T[8 * w + 2], T[8 * w + 4], T[8 * w + 6], 2 - l);
-            L.od[l][w] = gather_byte(T[8 * w + 1], T[8 * w + 3], T[8 * w + 5], T[8 * w + 7], 2 - l);
-        }
-    L.f0 = sp * 65536.0f;
-    L.f1 = sp * 256.0f;
-    L.f2 = sp;
-    L.xs = s0 + s1;
-    L.xs0 = s0;
-    L.xs1 = s1;
-}
-
-__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
-    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
-}
-
-__device__ __forceinline__ uint32_t udot4(uint32_t a, uint32_t b, uint32_t c) {
-    return __builtin_amdgcn_udot4(a, b, c, false);
-}
-
-__device__ __forceinline__ float combine(const XLevels& L, int ia, uint32_t ib, uint32_t ic) {
-    return fmaf(static_cast<float>(ia), L.f0, fmaf(static_cast<float>(ib), L.f1, static_cast<float>(ic) * L.f2));
-}
 
 // Shared prologue: x sub-blocks into registers (optionally RMS-normalised), then
 // their int8 level images.
@@ -143,7 +83,7 @@ template <int SBL, int RB, bool FULL>
 __global__ __launch_bounds__(512) void q4k_mv_kernel(MvArgs a) {
     extern __shared__ double dyn_lds[];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row addresses
     const int nwaves = blockDim.x >> 6;
     const int slot = wave / a.wpr;
     const int wslot = wave - slot * a.wpr;
@@ -168,25 +108,26 @@ __global__ __launch_bounds__(512) void q4k_mv_kernel(MvArgs a) {
         msh[i] = 8 * (j & 3) + (j < 4 ? 0 : 4);
     }
     // Workgroup b handles tiles b, b + grid, b + 2 grid, ... (a.steps of them): the x
-    // prologue is paid once per workgroup.  The first tile's weight loads are issued
-    // before the prologue, each next tile's right after the current tile's arithmetic.
-    uint4 qv[RB][SBL], hv[RB][SBL];
-    auto load_tile = [&](int tile) {
+    // prologue is paid once per workgroup.  Tiles are double-buffered in registers: the
+    // loads of tile t+1 are issued before tile t's arithmetic, so every wave keeps a
+    // tile in flight while it computes.
+    uint4 qa[RB][SBL], ha[RB][SBL], qb[RB][SBL], hb[RB][SBL];
+    auto load_tile = [&](uint4 (&qv)[RB][SBL], uint4 (&hv)[RB][SBL], int tile) __attribute__((always_inline)) {
         const int row0 = (tile * nslots + slot) * RB;
 #pragma unroll
         for (int r = 0; r < RB; r++)
 #pragma unroll
             for (int i = 0; i < SBL; i++) {
                 const size_t row = static_cast<size_t>(row0 + r);
-                qv[r][i] = *reinterpret_cast<const uint4*>(a.qs + row * rowq + cc[i] * 16);
-                hv[r][i] = a.hdr[row * S + (cc[i] >> 3)];
+                // wave-uniform row base + 32-bit lane offset: scalar-base loads
+                const uint8_t* qrow = a.qs + row * rowq;
+                const uint4* hrow = a.hdr + row * S;
+                qv[r][i] = *reinterpret_cast<const uint4*>(qrow + static_cast<uint32_t>(cc[i]) * 16u);
+                hv[r][i] = hrow[static_cast<uint32_t>(cc[i]) >> 3];
             }
     };
-    load_tile(blockIdx.x);
     XLevels L[SBL];
-    prologue_levels<SBL>(a, cl, C, nsub, dscratch, wave, slot, lane, L, valid);
-    for (int t = 0; t < a.steps; t++) {
-        const int tile = blockIdx.x + t * gridDim.x;
+    auto compute_tile = [&](const uint4 (&qv)[RB][SBL], const uint4 (&hv)[RB][SBL], int t, int tile) __attribute__((always_inline)) {
         float acc[RB];
 #pragma unroll
         for (int r = 0; r < RB; r++) {
@@ -215,11 +156,22 @@ __global__ __launch_bounds__(512) void q4k_mv_kernel(MvArgs a) {
                 float sc = d * static_cast<float>((sw >> scsh[i]) & 0x3Fu);
                 float mn = dmin * static_cast<float>((h.w >> msh[i]) & 0xFu);
                 if (!FULL && !valid[i]) { sc = 0.f; mn = 0.f; }
-                acc[r] = fmaf(sc, combine(L[i], ia, ib, ic), fmaf(-mn, L[i].xs, acc[r]));
+                acc[r] = fmaf(sc, combine(ia, ib, ic, L[i].sp), fmaf(-mn, L[i].xs, acc[r]));
             }
         }
-        if (t + 1 < a.steps && tile + static_cast<int>(gridDim.x) < a.tiles) load_tile(tile + gridDim.x);
-        if (tile < a.tiles) finish_rows<RB>(a, acc, red, t, lane, wave, nwaves, slot, wslot, (tile * nslots + slot) * RB);
+        finish_rows<RB>(a, acc, red, t, lane, wave, nwaves, slot, wslot, (tile * nslots + slot) * RB);
+    };
+    const int g = static_cast<int>(gridDim.x);
+    load_tile(qa, ha, blockIdx.x);
+    prologue_levels<SBL>(a, cl, C, nsub, dscratch, wave, slot, lane, L, valid);
+    for (int t = 0; t < a.steps; t += 2) {
+        const int t0 = blockIdx.x + t * g, t1 = t0 + g, t2 = t1 + g;
+        if (t + 1 < a.steps && t1 < a.tiles) load_tile(qb, hb, t1);
+        if (t0 < a.tiles) compute_tile(qa, ha, t, t0);
+        if (t + 1 < a.steps) {
+            if (t + 2 < a.steps && t2 < a.tiles) load_tile(qa, ha, t2);
+            if (t1 < a.tiles) compute_tile(qb, hb, t + 1, t1);
+        }
     }
 }
 
@@ -232,7 +184,7 @@ template <int SBL, int RB, bool FULL>
 __global__ __launch_bounds__(512) void q6k_mv_kernel(MvArgs a) {
     extern __shared__ double dyn_lds[];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row addresses
     const int nwaves = blockDim.x >> 6;
     const int slot = wave / a.wpr;
     const int wslot = wave - slot * a.wpr;
@@ -254,36 +206,37 @@ __global__ __launch_bounds__(512) void q6k_mv_kernel(MvArgs a) {
         valid[i] = cl + i * C < nsub;
         cc[i] = FULL ? cl + i * C : min(cl + i * C, nsub - 1);
     }
-    uint4 lv[RB][SBL];
-    uint2 hv[RB][SBL];
-    uint32_t sv[RB][SBL], dv[RB][SBL];
-    auto load_tile = [&](int tile) {
+    struct Tile {
+        uint4 l[RB][SBL];
+        uint2 h[RB][SBL];
+        uint32_t s[RB][SBL], d[RB][SBL];
+    };
+    Tile ta, tb;
+    auto load_tile = [&](Tile& T, int tile) __attribute__((always_inline)) {
         const int row0 = (tile * nslots + slot) * RB;
 #pragma unroll
         for (int r = 0; r < RB; r++)
 #pragma unroll
             for (int i = 0; i < SBL; i++) {
                 const size_t row = static_cast<size_t>(row0 + r);
-                lv[r][i] = *reinterpret_cast<const uint4*>(a.qs + row * rowl + cc[i] * 16);
-                hv[r][i] = *reinterpret_cast<const uint2*>(a.qh + row * rowh + cc[i] * 8);
-                sv[r][i] = *reinterpret_cast<const uint16_t*>(a.sc + row * rows_s + cc[i] * 2);
-                dv[r][i] = a.d[row * S + (cc[i] >> 3)];
+                const uint32_t c = static_cast<uint32_t>(cc[i]);
+                T.l[r][i] = *reinterpret_cast<const uint4*>(a.qs + row * rowl + c * 16u);
+                T.h[r][i] = *reinterpret_cast<const uint2*>(a.qh + row * rowh + c * 8u);
+                T.s[r][i] = *reinterpret_cast<const uint16_t*>(a.sc + row * rows_s + c * 2u);
+                T.d[r][i] = a.d[row * S + (c >> 3)];
             }
     };
-    load_tile(blockIdx.x);
     XLevels L[SBL];
-    prologue_levels<SBL>(a, cl, C, nsub, dscratch, wave, slot, lane, L, valid);
-    for (int t = 0; t < a.steps; t++) {
-        const int tile = blockIdx.x + t * gridDim.x;
+    auto compute_tile = [&](const Tile& T, int t, int tile) __attribute__((always_inline)) {
         float acc[RB];
 #pragma unroll
         for (int r = 0; r < RB; r++) {
             acc[r] = 0.f;
 #pragma unroll
             for (int i = 0; i < SBL; i++) {
-                const uint4 l = lv[r][i];
+                const uint4 l = T.l[r][i];
                 const uint32_t lw[4] = {l.x, l.y, l.z, l.w};
-                const uint32_t hw[2] = {hv[r][i].x, hv[r][i].y};
+                const uint32_t hw[2] = {T.h[r][i].x, T.h[r][i].y};
                 int ga[2] = {0, 0};
                 uint32_t gb[2] = {0u, 0u}, gc[2] = {0u, 0u};
 #pragma unroll
@@ -300,18 +253,29 @@ __global__ __launch_bounds__(512) void q6k_mv_kernel(MvArgs a) {
                     gc[h2] = udot4(qe, L[i].ev[2][w], gc[h2]);
                     gc[h2] = udot4(qo, L[i].od[2][w], gc[h2]);
                 }
-                const float d = h2f(dv[r][i]);
-                const uint32_t s2 = sv[r][i];
+                const float d = h2f(T.d[r][i]);
+                const uint32_t s2 = T.s[r][i];
                 float sc0 = d * static_cast<float>(static_cast<int8_t>(s2 & 0xFFu));
                 float sc1 = d * static_cast<float>(static_cast<int8_t>(s2 >> 8));
                 if (!FULL && !valid[i]) { sc0 = 0.f; sc1 = 0.f; }
                 // value = sc * (q6 - 32): group sum = sc * (sum(q6 * x) - 32 * sum(x))
-                acc[r] = fmaf(sc0, fmaf(-32.f, L[i].xs0, combine(L[i], ga[0], gb[0], gc[0])), acc[r]);
-                acc[r] = fmaf(sc1, fmaf(-32.f, L[i].xs1, combine(L[i], ga[1], gb[1], gc[1])), acc[r]);
+                acc[r] = fmaf(sc0, fmaf(-32.f, L[i].xs0, combine(ga[0], gb[0], gc[0], L[i].sp)), acc[r]);
+                acc[r] = fmaf(sc1, fmaf(-32.f, L[i].xs1, combine(ga[1], gb[1], gc[1], L[i].sp)), acc[r]);
             }
         }
-        if (t + 1 < a.steps && tile + static_cast<int>(gridDim.x) < a.tiles) load_tile(tile + gridDim.x);
-        if (tile < a.tiles) finish_rows<RB>(a, acc, red, t, lane, wave, nwaves, slot, wslot, (tile * nslots + slot) * RB);
+        finish_rows<RB>(a, acc, red, t, lane, wave, nwaves, slot, wslot, (tile * nslots + slot) * RB);
+    };
+    const int g = static_cast<int>(gridDim.x);
+    load_tile(ta, blockIdx.x);
+    prologue_levels<SBL>(a, cl, C, nsub, dscratch, wave, slot, lane, L, valid);
+    for (int t = 0; t < a.steps; t += 2) {
+        const int t0 = blockIdx.x + t * g, t1 = t0 + g, t2 = t1 + g;
+        if (t + 1 < a.steps && t1 < a.tiles) load_tile(tb, t1);
+        if (t0 < a.tiles) compute_tile(ta, t, t0);
+        if (t + 1 < a.steps) {
+            if (t + 2 < a.steps && t2 < a.tiles) load_tile(ta, t2);
+            if (t1 < a.tiles) compute_tile(tb, t + 1, t1);
+        }
     }
 }
 
@@ -323,7 +287,7 @@ static void launch_mv_t(const DevWeight& w, MvArgs a, hipStream_t s, int nslots,
     if (w.rows_pad % rows_per_tile) fail(LARQL_HIP_ERR_INVALID, "matvec: device rows not padded to the tile");
     const size_t tiles = w.rows_pad / rows_per_tile;
     // About two workgroups per CU; each loops over its share of the tiles.
-    const size_t target = 2 * static_cast<size_t>(a.num_cus > 0 ? a.num_cus : 256);
+    const size_t target = 2 * static_cast<size_t>(a.num_cus);
     a.tiles = static_cast<int>(tiles);
     a.steps = static_cast<int>((tiles + target - 1) / target);
     const size_t grid = (tiles + a.steps - 1) / a.steps;
@@ -348,6 +312,8 @@ static void launch_mv_t(const DevWeight& w, MvArgs a, hipStream_t s, int nslots,
 
 void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s) {
     if (w.format != LARQL_Q4_K && w.format != LARQL_Q6_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "launch_mv: format");
+    if (a.num_cus <= 0) a.num_cus = current_device_cus();
+    if (stream_mv_supported(w)) return launch_mv_stream(w, a, s);
     a.rows = static_cast<int>(w.rows);
     a.cols = static_cast<int>(w.cols);
     if (a.epi == EPI_SILU_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "silu pair epilogue needs even rows");

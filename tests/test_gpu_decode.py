@@ -3,8 +3,8 @@ reset_kv_cache; larql-compute/src/backend.rs:99-123) against the CPU oracle's
 Llama layer (oracle.decode_layer: LI/src/attention/{rope,gqa}.rs, LI/src/residual.rs,
 LI/src/ffn/mod.rs composed in the reference GPU decode's op order).
 
-Bar: max|gpu - cpu| / max|cpu| <= 1e-3 on the hidden state / logits (BASELINE north
-star, fp outputs), and the greedy next token (argmax of the logits) identical.
+Bar: max|gpu - cpu| / max|cpu| <= 1e-3 on the hidden state / logits (floating-point
+outputs), and the greedy next token (argmax of the logits) identical.
 The KV cache is fp16 on both sides (new rows rounded to nearest even).
 """
 import numpy as np

@@ -1,7 +1,7 @@
 """GPU parity: HIP matvec kernels (through the C ABI) vs the CPU oracle on the
 same seeded inputs.
 
-Bars:
+Bars (parity targets of the quantized compute path):
   * Q4_0 x Q8 and Q8_0 x Q8: BIT-EXACT outputs.  The reference's int32 block
     dot is exact and its block accumulation order (acc += (float)isum_b * cs_b,
     LC/csrc/q4_dot.c:58-89, LC/src/cpu/ops/q8_matvec.rs:44-57) is reproduced.
