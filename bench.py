@@ -1,27 +1,40 @@
 #!/usr/bin/env python3
 """Benchmark of the LARQL quantized compute path on one MI355X.
 
-Headline metric: "Q4_K matvec HBM GB/s (% of peak) + 8B-shape decode tokens/sec".
+Headline metric: "Q4_K matvec HBM GB/s (% of peak) + 8B-shape decode tokens/sec, 1 GPU".
 
-One step = one pass of the Llama-3-8B FFN matvec trio in 148-byte Q4_K
-(gate [14336x4096], up [14336x4096], down [4096x14336]), batch 1, f32
-activations, weights drawn N(0, 0.02) on the device and quantized by the
-library's device port of the reference quantizer.  Each launch uses one of
-16 distinct weight copies (16 x 3 x 34 MB) in rotation so the 256 MB
-Infinity Cache cannot serve repeats.  Inputs are resident in HBM before the
-timed region; the timed region is bracketed by synchronizations and HIP
-events recorded on the stream the kernels are launched on.
+Matvec part (the JSON `value`).  One step = one pass of the Llama-3-8B FFN matvec trio
+in 148-byte Q4_K (gate [14336x4096], up [14336x4096], down [4096x14336]), batch 1, f32
+activations, weights drawn N(0, 0.02) on the device and quantized by the library's
+device port of the reference quantizer.  Each launch uses one of 16 distinct weight
+copies (16 x 3 x 34 MB) in rotation so the 256 MB Infinity Cache cannot serve
+repeats.  Inputs are resident in HBM before the timed region; the timed region is
+bracketed by synchronizations and HIP events recorded on the stream the kernels are
+launched on.
 
-value        = algorithmic bytes of all launches / timed wall time (GB/s)
-roofline     = the same for the dominant kernel (q4k_matvec) vs 8 TB/s
-cpu_baseline = the oracle's port of the reference CPU q4k_matvec, one
-               thread, timed on a bounded sample on this host.
+Decode part (`decode`).  The full synthetic Llama-3-8B Q4_K decode step (32 layers,
+d 4096, 32/8 heads, hd 128, FFN 14336, Q6_K head over 128256, fp16 KV prefilled with
+2048 positions): the cache is truncated to 2048 before every step, so every timed
+step runs at pos 2048; tokens/s = 1 / median step time.
+
+value        = algorithmic bytes of all trio launches / timed wall time (GB/s)
+roofline     = the gate launch alone: algorithmic bytes / its average launch time,
+               vs 8 TB/s; traffic from the committed rocprofv3 PMC summary
+cpu_baseline = the oracle's port of the reference CPU q4k_matvec (q4k_matvec.rs),
+               one thread, timed on a bounded sample on this host.
+
+PMC helpers (used to produce profiles/q4k_matvec_traffic.json):
+  bench.py --pmc-pass calib   plain 64 MiB device copies (known bytes) for scaling
+  bench.py --pmc-pass gate    gate-shape Q4_K matvec launches
+  bench.py --pmc-report CALIB_FETCH CALIB_WRITE GATE_FETCH GATE_WRITE
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -34,11 +47,27 @@ for _p in (ROOT, PKG):
 METRIC = "Q4_K matvec HBM GB/s (% of peak) + 8B-shape decode tokens/sec, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 SHAPES = (("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336))
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "q4k_matvec_traffic.json")
+CALIB_BYTES = 64 << 20
 
 
 def q4k_algorithmic_bytes(rows: int, cols: int) -> int:
     """148-byte Q4_K weights + f32 x + f32 out (one launch)."""
     return rows * (cols // 256) * 148 + cols * 4 + rows * 4
+
+
+def decode_algorithmic_bytes(cfg: dict, kv_len: int) -> int:
+    """Bytes one decode step must move: Q4_K layer weights, the Q6_K head, the KV
+    cache read over T = kv_len + 1 positions, the new K/V row, norms, the embedding
+    row and the logits."""
+    h, i, nq, nkv, hd, L, V = (cfg[k] for k in ("hidden", "inter", "nq", "nkv", "hd", "n_layers", "vocab"))
+    qd, kvd = nq * hd, nkv * hd
+    per_layer = sum(r * (c // 256) * 148 for r, c in ((qd, h), (kvd, h), (kvd, h), (h, qd), (i, h), (i, h), (h, i)))
+    head = V * (h // 256) * 210
+    kv_read = L * (kv_len + 1) * kvd * 2 * 2
+    kv_write = L * kvd * 2 * 2
+    norms = (2 * L + 1) * h * 4
+    return L * per_layer + head + kv_read + kv_write + norms + h * 4 + V * 4
 
 
 def log(msg: str):
@@ -66,20 +95,162 @@ def cpu_baseline(raw_u8, x_np, rows, cols, budget_s: float):
     }
 
 
+def make_weights(be, torch, stream, copies):
+    import larql_hip
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    handles, xs, outs, raws = {}, {}, {}, {}
+    for i, (name, rows, cols) in enumerate(SHAPES):
+        gen.manual_seed(1000 + i)
+        w = torch.randn(rows, cols, device=dev, generator=gen, dtype=torch.float32) * 0.02
+        raw = torch.empty(rows * (cols // 256) * 148, dtype=torch.uint8, device=dev)
+        be.quantize_weights_dev(larql_hip.Q4_K, w, rows * cols, raw, stream=stream)
+        torch.cuda.synchronize()
+        del w
+        handles[name] = [be.register_weight_device(larql_hip.Q4_K, raw, raw.numel(), rows, cols)
+                         for _ in range(copies)]
+        raws[name] = raw
+        gen.manual_seed(2000 + i)
+        xs[name] = torch.randn(cols, device=dev, generator=gen, dtype=torch.float32)
+        outs[name] = torch.empty(rows, device=dev, dtype=torch.float32)
+    torch.cuda.synchronize()
+    return handles, xs, outs, raws
+
+
+def time_launches(torch, stream, fn, n):
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(n):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)  # ms
+
+
+def run_decode(be, torch, stream, steps, warmup):
+    from larql_hip.synth import LLAMA3_8B, build_llama
+
+    sm = build_llama(be, torch, **LLAMA3_8B)
+    kv_len = sm.kv_len
+
+    def step():
+        be.kv_truncate(kv_len)
+        sm.model.decode_dev(sm.x, logits=sm.logits, stream=stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    times = []
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record(stream)
+        step()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    times = [e0.elapsed_time(e1) for e0, e1 in ev]
+    med = statistics.median(times)
+    nbytes = decode_algorithmic_bytes(sm.cfg, kv_len)
+    sm.model.close()
+    return {
+        "tokens_per_s": round(1000.0 / med, 2),
+        "ms_per_step_median": round(med, 4),
+        "ms_per_step_min": round(min(times), 4),
+        "steps": steps,
+        "bytes_per_step": nbytes,
+        "achieved_GBs": round(nbytes / (med * 1e-3) / 1e9, 1),
+        "config": "Llama-3-8B shape, Q4_K linears, Q6_K head (vocab 128256), fp16 KV at pos 2048, batch 1",
+    }
+
+
+def pmc_pass(which: str, launches: int):
+    """Kernels only, for a rocprofv3 --pmc run (no timing output)."""
+    import torch
+
+    import larql_hip
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    torch.cuda.set_stream(stream)
+    if which == "calib":
+        src = torch.empty(CALIB_BYTES // 4, device=dev, dtype=torch.float32).uniform_()
+        dst = torch.empty_like(src)
+        for _ in range(launches):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return
+    be = larql_hip.HipBackend(0, strict=True)
+    handles, xs, outs, _ = make_weights(be, torch, stream, copies=16)
+    for i in range(launches):
+        be.matvec_dev(handles["gate"][i % 16], xs["gate"], outs["gate"], stream=stream)
+    torch.cuda.synchronize()
+    be.close()
+
+
+def _pmc_values(path: str, counter: str, name_part: str):
+    vals = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter and name_part in r["Kernel_Name"]:
+                vals.append(float(r["Counter_Value"]))
+    if not vals:
+        raise SystemExit(f"{path}: no {counter} rows for kernels matching {name_part!r}")
+    return vals
+
+
+def pmc_report(calib_fetch, calib_write, gate_fetch, gate_write):
+    """Scale the gate launches' FETCH_SIZE / WRITE_SIZE (KiB per dispatch) by what the
+    same counters read for a plain copy of CALIB_BYTES, and write the traffic summary."""
+    kib = CALIB_BYTES / 1024.0
+    cf = statistics.median(_pmc_values(calib_fetch, "FETCH_SIZE", "copy"))
+    cw = statistics.median(_pmc_values(calib_write, "WRITE_SIZE", "copy"))
+    gf = statistics.median(_pmc_values(gate_fetch, "FETCH_SIZE", "kq_stream_kernel"))
+    gw = statistics.median(_pmc_values(gate_write, "WRITE_SIZE", "kq_stream_kernel"))
+    f_fetch, f_write = kib / cf, kib / cw
+    traffic = (gf * f_fetch + gw * f_write) * 1024.0
+    alg = q4k_algorithmic_bytes(14336, 4096)
+    out = {
+        "kernel": "kq_stream_kernel (Q4_K, gate [14336x4096])",
+        "calibration": {"copy_bytes": CALIB_BYTES, "fetch_kib_read": cf, "write_kib_read": cw,
+                        "fetch_scale": round(f_fetch, 4), "write_scale": round(f_write, 4)},
+        "gate": {"fetch_kib_raw": gf, "write_kib_raw": gw},
+        "traffic_bytes_per_launch": int(traffic),
+        "algorithmic_bytes_per_launch": alg,
+        "traffic_over_algorithmic": round(traffic / alg, 4),
+    }
+    os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump(out, f, indent=2)
+    print(json.dumps(out, indent=2))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--copies", type=int, default=16)
+    ap.add_argument("--decode-steps", type=int, default=30)
+    ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-pass", choices=("calib", "gate"))
+    ap.add_argument("--pmc-launches", type=int, default=50)
+    ap.add_argument("--pmc-report", nargs=4, metavar=("CALIB_FETCH", "CALIB_WRITE", "GATE_FETCH", "GATE_WRITE"))
     args = ap.parse_args()
 
+    if args.pmc_report:
+        pmc_report(*args.pmc_report)
+        return
     if args.gpus != 1:
-        print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU sharding is design-only "
-                                   "(the single-GPU kernels are the per-GPU share of a row-sharded layout)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU; sharding is described in DESIGN.md and "
+                                   "not built (one GPU's share is the full single-GPU shape)", "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.pmc_pass:
+        pmc_pass(args.pmc_pass, args.pmc_launches)
+        return
 
     import torch
 
@@ -91,22 +262,7 @@ def main():
     be = larql_hip.HipBackend(0, strict=True)
     log(f"[bench] {be.device_info()}")
 
-    gen = torch.Generator(device=dev)
-    handles, xs, outs, raws = {}, {}, {}, {}
-    for i, (name, rows, cols) in enumerate(SHAPES):
-        gen.manual_seed(1000 + i)
-        w = torch.randn(rows, cols, device=dev, generator=gen, dtype=torch.float32) * 0.02
-        raw = torch.empty(rows * (cols // 256) * 148, dtype=torch.uint8, device=dev)
-        be.quantize_weights_dev(larql_hip.Q4_K, w, rows * cols, raw, stream=stream)
-        torch.cuda.synchronize()
-        del w
-        handles[name] = [be.register_weight_device(larql_hip.Q4_K, raw, raw.numel(), rows, cols)
-                         for _ in range(args.copies)]
-        raws[name] = raw
-        gen.manual_seed(2000 + i)
-        xs[name] = torch.randn(cols, device=dev, generator=gen, dtype=torch.float32)
-        outs[name] = torch.empty(rows, device=dev, dtype=torch.float32)
-    torch.cuda.synchronize()
+    handles, xs, outs, raws = make_weights(be, torch, stream, args.copies)
     log(f"[bench] weights ready: {len(SHAPES)} x {args.copies} copies")
 
     def step(i):
@@ -115,23 +271,23 @@ def main():
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record(stream)
-    for i in range(args.steps):
-        step(i)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1)
+    ms = time_launches(torch, stream, step, args.steps)
     ms_per_step = ms / args.steps
     bytes_per_step = sum(q4k_algorithmic_bytes(r, c) for _, r, c in SHAPES)
     gbs = bytes_per_step * args.steps / (ms * 1e-3) / 1e9
-    per_launch_us = ms * 1e3 / (args.steps * len(SHAPES))
-    log(f"[bench] {args.steps} steps in {ms:.3f} ms: {ms_per_step * 1e3:.2f} us/step, "
-        f"{per_launch_us:.2f} us/launch, {gbs:.1f} GB/s")
+    log(f"[bench] trio: {args.steps} steps in {ms:.3f} ms: {ms_per_step * 1e3:.2f} us/step, {gbs:.1f} GB/s")
+
+    # the dominant kernel alone: back-to-back gate launches
+    per_shape = {}
+    for name, rows, cols in SHAPES:
+        n = args.steps
+        ms_s = time_launches(torch, stream,
+                             lambda i: be.matvec_dev(handles[name][i % args.copies], xs[name], outs[name],
+                                                     stream=stream), n)
+        us = ms_s * 1e3 / n
+        per_shape[name] = {"us_per_launch": round(us, 3),
+                           "GBs": round(q4k_algorithmic_bytes(rows, cols) / (us * 1e-6) / 1e9, 1)}
+    log(f"[bench] per shape: {per_shape}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -139,7 +295,24 @@ def main():
         cpu = cpu_baseline(raws[name].cpu().numpy(), xs[name].cpu().numpy(), rows, cols, args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu}")
 
-    per_launch_bytes = q4k_algorithmic_bytes(14336, 4096)
+    for name in handles:
+        for h in handles[name]:
+            be.release_weight(h)
+    del raws
+    torch.cuda.empty_cache()
+
+    decode = None
+    if not args.no_decode:
+        decode = run_decode(be, torch, stream, args.decode_steps, warmup=5)
+        log(f"[bench] decode: {decode}")
+
+    gate_bytes = q4k_algorithmic_bytes(14336, 4096)
+    gate_us = per_shape["gate"]["us_per_launch"]
+    achieved = gate_bytes / (gate_us * 1e-6) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_JSON):
+        with open(TRAFFIC_JSON) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -151,25 +324,27 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "u8 (4-bit codes) x f32, int32 v_dot4",
         "data": "synthetic: W ~ N(0,0.02) quantized to 148-byte Q4_K on device, x ~ N(0,1)",
         "config": {
             "workload": "Q4_K matvec trio at Llama-3-8B FFN shapes: gate/up [14336x4096], down [4096x14336], batch 1",
             "weight_copies": args.copies,
             "launches_per_step": len(SHAPES),
+            "per_shape": per_shape,
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(per_launch_bytes / (per_launch_us * 1e-6) / 1e9, 2),
+            "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(per_launch_bytes / (per_launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "q4k_matvec_kernel",
-            "bytes_per_launch": per_launch_bytes,
-            "avg_launch_us": round(per_launch_us, 3),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "kq_stream_kernel<Q4_K> gate [14336x4096]",
+            "bytes_per_launch": gate_bytes,
+            "avg_launch_us": gate_us,
         },
         "cpu_baseline": cpu,
+        "decode": decode,
     }
     print(json.dumps(result), flush=True)
     be.close()
