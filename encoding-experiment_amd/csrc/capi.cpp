@@ -71,6 +71,9 @@ static void check_shape(int format, size_t len, size_t rows, size_t cols) {
             break;
         case LARQL_Q4_KF:
             fail(LARQL_HIP_ERR_UNSUPPORTED, "Q4_KF is not supported by the HIP backend");
+        case LARQL_F32:
+            if (cols % 16) fail(LARQL_HIP_ERR_INVALID, "f32 gate hidden must be a multiple of 16");
+            break;
         default: fail(LARQL_HIP_ERR_INVALID, "unknown quant format");
     }
     if (rows > 0x7FFFFFFF / 2) fail(LARQL_HIP_ERR_INVALID, "too many rows");
@@ -204,7 +207,8 @@ extern "C" void larql_hip_ctx_destroy(larql_hip_ctx* c) {
             larql_hip_decode_release(c);
         } catch (...) {
         }
-        for (auto* b : {&c->stage_in, &c->stage_in2, &c->stage_out, &c->stage_raw, &c->scratch})
+        for (auto* b : {&c->stage_in, &c->stage_in2, &c->stage_out, &c->stage_raw, &c->scratch, &c->knn_scores,
+                        &c->knn_q8, &c->knn_q8s, &c->knn_idx, &c->knn_val, &c->knn_handles})
             if (b->p) (void)hipFree(b->p);
         (void)hipStreamDestroy(c->stream);
     }

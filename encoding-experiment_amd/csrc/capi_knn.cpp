@@ -1,0 +1,125 @@
+// Gate-KNN entry points (vindex code in the reference, not trait methods):
+// VectorIndex::gate_knn / gate_knn_batch / gate_knn_q4 / top_k_from_scores,
+// LV/src/index/gate.rs:14-29, 108-134, 307-316, 500-537, 711-731.
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "capi_util.h"
+#include "knn.h"
+
+using larql::DevWeight;
+using larql::fail;
+
+namespace {
+
+struct KnnPlan {
+    int format = 0;
+    int F = 0, K = 0;
+    larql::KnnLayers a{}, b{};  // f32: a = rows; Q4_0: a = nibbles, b = f16 scales
+};
+
+KnnPlan plan_layers(larql_hip_ctx* c, const uint64_t* handles, size_t n_layers) {
+    if (!handles || n_layers == 0) fail(LARQL_HIP_ERR_INVALID, "gate KNN: no layers");
+    if (n_layers > static_cast<size_t>(larql::kMaxKnnLayers))
+        fail(LARQL_HIP_ERR_INVALID, "gate KNN: more than LARQL_HIP_KNN_MAX_LAYERS layers in one call");
+    KnnPlan p;
+    for (size_t l = 0; l < n_layers; l++) {
+        const DevWeight& w = larql::lookup(c, handles[l]);
+        if (w.format != LARQL_F32 && w.format != LARQL_Q4_0)
+            fail(LARQL_HIP_ERR_UNSUPPORTED, "gate KNN: gate weights must be LARQL_F32 or LARQL_Q4_0");
+        if (l == 0) {
+            p.format = w.format;
+            p.F = static_cast<int>(w.rows);
+            p.K = static_cast<int>(w.cols);
+        } else if (w.format != p.format || static_cast<int>(w.rows) != p.F || static_cast<int>(w.cols) != p.K) {
+            fail(LARQL_HIP_ERR_INVALID, "gate KNN: layers differ in format or shape");
+        }
+        p.a.p[l] = w.qs;
+        p.b.p[l] = w.d;
+    }
+    if (p.format == LARQL_Q4_0 && p.K % 64) fail(LARQL_HIP_ERR_INVALID, "gate KNN: Q4_0 hidden must be a multiple of 64");
+    return p;
+}
+
+// Scores [n_layers][nq][F] into `scores` (device).
+void run_scores(larql_hip_ctx* c, const KnnPlan& p, size_t n_layers, const float* queries, size_t nq, float* scores,
+                hipStream_t s) {
+    if (!queries || !scores || nq == 0) fail(LARQL_HIP_ERR_INVALID, "gate KNN: null queries/scores or nq == 0");
+    if (nq > 0x7FFFFFFF / static_cast<size_t>(p.K)) fail(LARQL_HIP_ERR_INVALID, "gate KNN: too many queries");
+    const int Q = static_cast<int>(nq);
+    if (p.format == LARQL_F32) {
+        larql::launch_gate_scores_f32(p.a, static_cast<int>(n_layers), queries, scores, p.F, p.K, Q, s);
+    } else {
+        int8_t* q8 = static_cast<int8_t*>(larql::ensure(c, c->knn_q8, nq * p.K));
+        float* q8s = static_cast<float*>(larql::ensure(c, c->knn_q8s, nq * (p.K / 32) * sizeof(float)));
+        larql::launch_quantize_q8(queries, static_cast<size_t>(p.K), nq, q8, q8s, s);
+        larql::launch_gate_scores_q4(p.a, p.b, static_cast<int>(n_layers), q8, q8s, scores, p.F, p.K, Q, s);
+    }
+}
+
+void check_k(size_t k, int F) {
+    if (k < 1 || k > static_cast<size_t>(larql::kTopkMaxK) || k > static_cast<size_t>(F))
+        fail(LARQL_HIP_ERR_INVALID, "gate KNN: need 1 <= top_k <= min(features, 64)");
+}
+
+}  // namespace
+
+extern "C" int larql_hip_gate_scores_dev(larql_hip_ctx* c, const uint64_t* handles, size_t n_layers,
+                                         const float* queries, size_t nq, float* scores, void* stream) {
+    return guarded(c, [&] {
+        const KnnPlan p = plan_layers(c, handles, n_layers);
+        run_scores(c, p, n_layers, queries, nq, scores, pick_stream(c, stream));
+    });
+}
+
+extern "C" int larql_hip_gate_knn_dev(larql_hip_ctx* c, const uint64_t* handles, size_t n_layers,
+                                      const float* queries, size_t nq, size_t top_k, uint32_t* idx, float* scores,
+                                      void* stream) {
+    return guarded(c, [&] {
+        const KnnPlan p = plan_layers(c, handles, n_layers);
+        check_k(top_k, p.F);
+        if (!idx || !scores) fail(LARQL_HIP_ERR_INVALID, "gate KNN: null outputs");
+        hipStream_t s = pick_stream(c, stream);
+        float* S = static_cast<float*>(larql::ensure(c, c->knn_scores, n_layers * nq * p.F * sizeof(float)));
+        run_scores(c, p, n_layers, queries, nq, S, s);
+        larql::launch_topk(S, n_layers * nq, static_cast<size_t>(p.F), p.F, static_cast<int>(top_k), 0, idx, scores, s);
+    });
+}
+
+extern "C" int larql_hip_topk_dev(larql_hip_ctx* c, const float* scores, size_t rows, size_t n, size_t k,
+                                  int signed_mode, uint32_t* idx, float* vals, void* stream) {
+    return guarded(c, [&] {
+        if (!scores || !idx || !vals) fail(LARQL_HIP_ERR_INVALID, "top-k: null pointer");
+        if (n == 0 || n > 0x7FFFFFFF) fail(LARQL_HIP_ERR_INVALID, "top-k: bad row length");
+        if (k < 1 || k > static_cast<size_t>(larql::kTopkMaxK) || k > n)
+            fail(LARQL_HIP_ERR_INVALID, "top-k: need 1 <= k <= min(n, 64)");
+        larql::launch_topk(scores, rows, n, static_cast<int>(n), static_cast<int>(k), signed_mode ? 1 : 0, idx, vals,
+                           pick_stream(c, stream));
+    });
+}
+
+extern "C" int larql_hip_gate_knn(larql_hip_ctx* c, int format, const void* gate, size_t gate_len, size_t features,
+                                  size_t hidden, const float* queries, size_t nq, size_t top_k, uint32_t* idx,
+                                  float* scores) {
+    return guarded(c, [&] {
+        if (format != LARQL_F32 && format != LARQL_Q4_0)
+            fail(LARQL_HIP_ERR_UNSUPPORTED, "gate KNN: format must be LARQL_F32 or LARQL_Q4_0");
+        if (!queries || !idx || !scores || nq == 0) fail(LARQL_HIP_ERR_INVALID, "gate KNN: null pointer or nq == 0");
+        const DevWeight& w = larql::cached_weight(c, format, gate, gate_len, nullptr, features, hidden);
+        const uint64_t h = w.handle;
+        const KnnPlan p = plan_layers(c, &h, 1);
+        check_k(top_k, p.F);
+        const size_t qbytes = nq * hidden * sizeof(float);
+        float* dq = static_cast<float*>(larql::ensure(c, c->stage_in, qbytes));
+        LARQL_HIP_CHECK(hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, c->stream));
+        float* S = static_cast<float*>(larql::ensure(c, c->knn_scores, nq * p.F * sizeof(float)));
+        run_scores(c, p, 1, dq, nq, S, c->stream);
+        uint32_t* di = static_cast<uint32_t*>(larql::ensure(c, c->knn_idx, nq * top_k * sizeof(uint32_t)));
+        float* dv = static_cast<float*>(larql::ensure(c, c->knn_val, nq * top_k * sizeof(float)));
+        larql::launch_topk(S, nq, static_cast<size_t>(p.F), p.F, static_cast<int>(top_k), 0, di, dv, c->stream);
+        LARQL_HIP_CHECK(hipMemcpyAsync(idx, di, nq * top_k * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+        LARQL_HIP_CHECK(hipMemcpyAsync(scores, dv, nq * top_k * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
+    });
+}

@@ -134,6 +134,8 @@ struct larql_hip_ctx {
     std::map<std::pair<const void*, size_t>, uint64_t> by_host;
     // reusable device staging buffers for host-pointer calls
     larql::DeviceBuf stage_in, stage_in2, stage_out, stage_raw, scratch;
+    // gate-KNN work buffers: scores [layers][nq][features], quantized queries
+    larql::DeviceBuf knn_scores, knn_q8, knn_q8s, knn_idx, knn_val, knn_handles;
     larql::KVCache kv;
     // model built by the last host-pointer decode_token (re-used while its key matches)
     larql_hip_model* trait_model = nullptr;

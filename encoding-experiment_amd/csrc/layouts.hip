@@ -15,6 +15,7 @@ size_t ref_row_bytes(int format, size_t cols) {
         case LARQL_Q4_K: return cols / 256 * 148;
         case LARQL_Q6_K: return cols / 256 * 210;
         case LARQL_Q8_0: return cols;
+        case LARQL_F32: return cols * 4;
         default: return 0;
     }
 }
@@ -29,6 +30,7 @@ size_t dev_layout_bytes(int format, size_t rows, size_t cols) {
             return align256(rows * cols / 2) + align256(rows * cols / 4) + align256(rows * cols / 16) +
                    align256(rows * (cols / 256) * 2);
         case LARQL_Q8_0: return align256(rows * cols) + align256(rows * (cols / 32) * 4);
+        case LARQL_F32: return align256(rows * cols * 4);
         default: return 0;
     }
 }
@@ -54,6 +56,9 @@ void dev_layout_carve(DevWeight& w) {
         case LARQL_Q8_0:
             w.qs = p; p += align256(R * K);
             w.d = p;
+            break;
+        case LARQL_F32:
+            w.qs = p;
             break;
         default: break;
     }
@@ -152,6 +157,12 @@ void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scale
             LARQL_HIP_CHECK(hipMemcpyAsync(w.qs + row0 * w.cols, raw, src_rows * w.cols, hipMemcpyDeviceToDevice, s));
             LARQL_HIP_CHECK(hipMemcpyAsync(static_cast<float*>(w.d) + row0 * (w.cols / 32), q8_scales,
                                            src_rows * (w.cols / 32) * sizeof(float), hipMemcpyDeviceToDevice, s));
+            break;
+        }
+        case LARQL_F32: {
+            if (stride != 1) fail(LARQL_HIP_ERR_UNSUPPORTED, "repack: interleaved f32");
+            LARQL_HIP_CHECK(hipMemcpyAsync(w.qs + row0 * w.cols * 4, raw, src_rows * w.cols * 4,
+                                           hipMemcpyDeviceToDevice, s));
             break;
         }
         default: fail(LARQL_HIP_ERR_UNSUPPORTED, "repack: unsupported format");

@@ -23,8 +23,9 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liblarql_hip.so")
 
-Q4_0, Q4_K, Q4_KF, Q6_K, Q8_0 = 0, 1, 2, 3, 4
-FORMAT_NAMES = {Q4_0: "Q4_0", Q4_K: "Q4_K", Q4_KF: "Q4_KF", Q6_K: "Q6_K", Q8_0: "Q8_0"}
+Q4_0, Q4_K, Q4_KF, Q6_K, Q8_0, F32 = 0, 1, 2, 3, 4, 5
+FORMAT_NAMES = {Q4_0: "Q4_0", Q4_K: "Q4_K", Q4_KF: "Q4_KF", Q6_K: "Q6_K", Q8_0: "Q8_0", F32: "F32"}
+TOPK_MAX, KNN_MAX_LAYERS = 64, 64
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_DEVICE, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5
 
@@ -64,6 +65,11 @@ SIGNATURES = {
     "larql_hip_quantize_to_q8_dev": (_I, [_P, _P, _SZ, _SZ, _P, _P, _P]),
     "larql_hip_quantize_weights": (_I, [_P, _I, _P, _SZ, _P, _P]),
     "larql_hip_quantize_weights_dev": (_I, [_P, _I, _P, _SZ, _P, _P, _P]),
+    # vindex gate-KNN
+    "larql_hip_gate_knn": (_I, [_P, _I, _P, _SZ, _SZ, _SZ, _P, _SZ, _SZ, _P, _P]),
+    "larql_hip_gate_knn_dev": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _P, _P, _P]),
+    "larql_hip_gate_scores_dev": (_I, [_P, _P, _SZ, _P, _SZ, _P, _P]),
+    "larql_hip_topk_dev": (_I, [_P, _P, _SZ, _SZ, _SZ, _I, _P, _P, _P]),
     # decode step (structs declared below; pointers passed as void*)
     "larql_hip_decode_token": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
     "larql_hip_populate_kv_layer": (_I, [_P, _SZ, _P, _P, _SZ, _SZ, _SZ]),
@@ -411,6 +417,39 @@ class HipBackend:
     def quantize_to_q8_dev(self, x, n: int, m: int, q8, scales, stream=None):
         self._check(self._lib.larql_hip_quantize_to_q8_dev(self._ctx, _dptr(x), n, m, _dptr(q8), _dptr(scales),
                                                            _stream_ptr(stream)))
+
+    # ── vindex gate-KNN (LV/src/index/gate.rs) ─────────────────────────
+    def gate_knn(self, gate, features: int, hidden: int, queries, top_k: int, fmt: int = F32):
+        """gate_knn (gate.rs:108-134) per query, or gate_knn_q4 (:711-731) with fmt=Q4_0.
+        queries: f32 [nq, hidden] (or [hidden]).  Returns (idx u32 [nq, k], scores f32
+        [nq, k]) by |score| descending, ties in index order; None if unsupported."""
+        g, gp = _arr(gate, np.float32 if fmt == F32 else np.uint8)
+        q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, hidden)
+        nq = q.shape[0]
+        idx = np.empty((nq, top_k), dtype=np.uint32)
+        val = np.empty((nq, top_k), dtype=np.float32)
+        rc = self._lib.larql_hip_gate_knn(self._ctx, fmt, gp, g.nbytes, features, hidden, q.ctypes.data_as(_P), nq,
+                                          top_k, idx.ctypes.data_as(_P), val.ctypes.data_as(_P))
+        return (idx, val) if self._ok(rc) else None
+
+    @staticmethod
+    def _handle_array(handles):
+        arr = (_U64 * len(handles))(*handles)
+        return arr, ctypes.cast(arr, _P)
+
+    def gate_knn_dev(self, handles, queries, nq: int, top_k: int, idx, scores, stream=None):
+        arr, ap = self._handle_array(handles)
+        self._check(self._lib.larql_hip_gate_knn_dev(self._ctx, ap, len(handles), _dptr(queries), nq, top_k,
+                                                     _dptr(idx), _dptr(scores), _stream_ptr(stream)))
+
+    def gate_scores_dev(self, handles, queries, nq: int, scores, stream=None):
+        arr, ap = self._handle_array(handles)
+        self._check(self._lib.larql_hip_gate_scores_dev(self._ctx, ap, len(handles), _dptr(queries), nq,
+                                                        _dptr(scores), _stream_ptr(stream)))
+
+    def topk_dev(self, scores, rows: int, n: int, k: int, idx, vals, signed: bool = False, stream=None):
+        self._check(self._lib.larql_hip_topk_dev(self._ctx, _dptr(scores), rows, n, k, int(signed), _dptr(idx),
+                                                 _dptr(vals), _stream_ptr(stream)))
 
 
 class DeviceModel:

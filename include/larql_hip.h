@@ -46,13 +46,16 @@ typedef struct larql_hip_ctx larql_hip_ctx;
 #define LARQL_HIP_ERR_NOMEM (-4)
 #define LARQL_HIP_ERR_STATE (-5)       /* e.g. KV cache not initialised */
 
-/* QuantFormat — LC/src/pipeline.rs:12-19 (same discriminant order). */
+/* QuantFormat — LC/src/pipeline.rs:12-19 (same discriminant order).  LARQL_F32 is an
+ * extension with no QuantFormat counterpart: plain f32 [rows][cols], the vindex's f32
+ * gate vectors (LV/src/index/gate.rs:14-29), usable only by the gate-KNN entry points. */
 typedef enum {
     LARQL_Q4_0 = 0,
     LARQL_Q4_K = 1,
     LARQL_Q4_KF = 2,
     LARQL_Q6_K = 3,
-    LARQL_Q8_0 = 4
+    LARQL_Q8_0 = 4,
+    LARQL_F32 = 5
 } larql_quant_format;
 
 /* ── lifecycle and metadata ─────────────────────────────────────────────── */
@@ -147,6 +150,38 @@ int larql_hip_quantize_to_q8_dev(larql_hip_ctx* ctx, const float* x, size_t n, s
 int larql_hip_quantize_weights_dev(larql_hip_ctx* ctx, int format, const float* x, size_t n, void* out,
                                    float* q8_scales, void* stream);
 
+
+/* ── vindex gate-KNN (vindex code, not trait methods: LV/src/index/gate.rs) ── */
+
+/* Largest top_k and number of layers per call. */
+#define LARQL_HIP_TOPK_MAX 64
+#define LARQL_HIP_KNN_MAX_LAYERS 64
+
+/* Gate KNN for one layer from host memory: VectorIndex::gate_knn (LV/src/index/gate.rs:108-134)
+ * for each of nq queries, i.e. the per-position lists of gate_knn_batch (:500-537) before
+ * their union.  format LARQL_F32: scores = gate[features, hidden] . q (gemv, :14-29);
+ * format LARQL_Q4_0: gate_knn_q4 (:711-731), q quantized by quantize_to_q8 and scored by
+ * q4_matvec.  Output per query: top_k (index, score) by |score| descending (top_k_from_scores,
+ * :307-316), ties in index order.  idx u32 and scores f32, [nq][top_k]. */
+int larql_hip_gate_knn(larql_hip_ctx* ctx, int format, const void* gate, size_t gate_len, size_t features,
+                       size_t hidden, const float* queries, size_t nq, size_t top_k, uint32_t* idx,
+                       float* scores);
+
+/* Device form over several layers in one launch: handles of registered gate matrices
+ * (all LARQL_F32, or all LARQL_Q4_0, with equal shapes), queries f32 [nq][hidden] in
+ * device memory, idx / scores [n_layers][nq][top_k] in device memory. */
+int larql_hip_gate_knn_dev(larql_hip_ctx* ctx, const uint64_t* handles, size_t n_layers, const float* queries,
+                           size_t nq, size_t top_k, uint32_t* idx, float* scores, void* stream);
+
+/* Scores only: scores f32 [n_layers][nq][features] (device). */
+int larql_hip_gate_scores_dev(larql_hip_ctx* ctx, const uint64_t* handles, size_t n_layers, const float* queries,
+                              size_t nq, float* scores, void* stream);
+
+/* Top-k of each row of a device score matrix [rows][n]: signed_mode 0 orders by |score|
+ * (gate.rs:307-316), 1 by the signed score (lm-head KNN, LV/src/index/walk.rs:563-580).
+ * Ties in index order.  idx / vals [rows][k] (device), 1 <= k <= min(n, 64). */
+int larql_hip_topk_dev(larql_hip_ctx* ctx, const float* scores, size_t rows, size_t n, size_t k, int signed_mode,
+                       uint32_t* idx, float* vals, void* stream);
 
 /* ── decode step: layers, KV cache, full-pipeline decode ───────────────── */
 

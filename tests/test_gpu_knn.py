@@ -1,0 +1,199 @@
+"""GPU parity of the vindex gate-KNN (LV/src/index/gate.rs) against the CPU oracle.
+
+Bars:
+  * f32 gate scores: BIT-EXACT with the oracle's canonical order (one fma chain per
+    (feature, query) over k from +0, lo_gate_scores_f32).  The reference hands the
+    order to matrixmultiply (parity of its bit patterns is unpinned); the kernel and
+    the oracle fix the same order, so indices are comparable bit for bit.
+  * Q4_0 gate scores (gate_knn_q4, gate.rs:711-731): BIT-EXACT with quantize_to_q8 +
+    q4_0 block-integer matvec (LC/csrc/q4_dot.c:58-89 order).
+  * top-k (top_k_from_scores, gate.rs:307-316; signed: walk.rs:563-580): indices and
+    values BIT-EXACT with the oracle's selection, ties in index order.
+"""
+import numpy as np
+import pytest
+
+import larql_hip
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_knn_f32(gate, queries, features, hidden, k):
+    idx, val = [], []
+    for q in queries:
+        s = oracle.gate_scores_f32(gate, q, features, hidden)
+        i, v = oracle.topk_abs(s, k)
+        idx.append(i)
+        val.append(v)
+    return np.array(idx), np.array(val)
+
+
+def oracle_knn_q4(q4, queries, features, hidden, k):
+    idx, val = [], []
+    for q in queries:
+        q8, q8s = oracle.quantize_to_q8(q)
+        s = oracle.q4_0_matvec_blockint(q4, q8, q8s, features, hidden)
+        i, v = oracle.topk_abs(s, k)
+        idx.append(i)
+        val.append(v)
+    return np.array(idx), np.array(val)
+
+
+@pytest.mark.parametrize("features,hidden,nq,k", [(1000, 2560, 37, 32), (10240, 2560, 8, 32), (64, 256, 300, 64),
+                                                  (130, 64, 3, 1)])
+def test_gate_knn_f32_bit_exact(hip, features, hidden, nq, k):
+    print(f"[knn f32] F={features} K={hidden} nq={nq} k={k}", flush=True)
+    gate = oracle.gauss(11, features * hidden, 0.0, 0.02).reshape(features, hidden)
+    queries = oracle.gauss(12, nq * hidden).reshape(nq, hidden)
+    got = hip.gate_knn(gate, features, hidden, queries, k, fmt=larql_hip.F32)
+    ref_i, ref_v = oracle_knn_f32(gate, queries, features, hidden, k)
+    np.testing.assert_array_equal(got[0], ref_i)
+    np.testing.assert_array_equal(got[1].view(np.uint32), ref_v.view(np.uint32))
+
+
+def test_gate_scores_f32_bit_exact(hip):
+    torch = pytest.importorskip("torch")
+    features, hidden, nq = 200, 512, 257   # partial feature tile and two query tiles
+    gate = oracle.gauss(21, features * hidden, 0.0, 0.02).reshape(features, hidden)
+    queries = oracle.gauss(22, nq * hidden).reshape(nq, hidden)
+    h = hip.register_weight(larql_hip.F32, gate, features, hidden)
+    try:
+        dq = torch.from_numpy(queries).cuda()
+        ds = torch.empty(nq * features, device="cuda", dtype=torch.float32)
+        hip.gate_scores_dev([h], dq, nq, ds)
+        hip.synchronize()
+        got = ds.cpu().numpy().reshape(nq, features)
+        ref = np.stack([oracle.gate_scores_f32(gate, q, features, hidden) for q in queries])
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    finally:
+        hip.release_weight(h)
+
+
+@pytest.mark.parametrize("features,hidden,nq,k", [(10240, 2560, 6, 32), (1000, 2560, 130, 17), (64, 64, 2, 64)])
+def test_gate_knn_q4_bit_exact(hip, features, hidden, nq, k):
+    print(f"[knn q4] F={features} K={hidden} nq={nq} k={k}", flush=True)
+    gate = oracle.gauss(31, features * hidden, 0.0, 0.02)
+    q4 = oracle.quantize_q4_0(gate)
+    queries = oracle.gauss(32, nq * hidden).reshape(nq, hidden)
+    got = hip.gate_knn(q4, features, hidden, queries, k, fmt=larql_hip.Q4_0)
+    ref_i, ref_v = oracle_knn_q4(q4, queries, features, hidden, k)
+    np.testing.assert_array_equal(got[0], ref_i)
+    np.testing.assert_array_equal(got[1].view(np.uint32), ref_v.view(np.uint32))
+
+
+def test_gate_knn_q4_fuzzed_bytes(hip):
+    """Random Q4_0 bytes (all nibbles, scales from a bounded f16 range)."""
+    features, hidden, nq, k = 300, 512, 5, 32
+    rng = np.random.default_rng(41)
+    q4 = rng.integers(0, 256, size=features * hidden // 32 * 18, dtype=np.uint8)
+    blocks = q4.reshape(-1, 18)
+    blocks[:, 0:2] = np.frombuffer(rng.uniform(-0.05, 0.05, blocks.shape[0]).astype(np.float16).tobytes(),
+                                   np.uint8).reshape(-1, 2)
+    queries = oracle.gauss(42, nq * hidden).reshape(nq, hidden)
+    got = hip.gate_knn(q4, features, hidden, queries, k, fmt=larql_hip.Q4_0)
+    ref_i, ref_v = oracle_knn_q4(q4, queries, features, hidden, k)
+    np.testing.assert_array_equal(got[0], ref_i)
+    np.testing.assert_array_equal(got[1].view(np.uint32), ref_v.view(np.uint32))
+
+
+def _topk_rows(hip, torch, rows, k, signed):
+    n = rows.shape[1]
+    ds = torch.from_numpy(np.ascontiguousarray(rows, dtype=np.float32)).cuda()
+    di = torch.empty(rows.shape[0] * k, device="cuda", dtype=torch.int32)
+    dv = torch.empty(rows.shape[0] * k, device="cuda", dtype=torch.float32)
+    hip.topk_dev(ds, rows.shape[0], n, k, di, dv, signed=signed)
+    hip.synchronize()
+    return di.cpu().numpy().view(np.uint32).reshape(-1, k), dv.cpu().numpy().reshape(-1, k)
+
+
+@pytest.mark.parametrize("signed", [False, True])
+def test_topk_ties_zeros_and_sizes(hip, signed):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(51)
+    cases = []
+    # duplicates, +-0, all equal, sign pairs with equal magnitude, huge values
+    r = rng.standard_normal(1000).astype(np.float32)
+    r[::7] = 0.0
+    r[3::11] = -0.0
+    r[5::13] = 1.5
+    r[6::13] = -1.5
+    cases.append(r)
+    cases.append(np.zeros(777, np.float32))
+    cases.append(np.full(500, -2.0, np.float32))
+    cases.append(np.concatenate([rng.standard_normal(300), [np.inf, -np.inf, 3e38, -3e38]]).astype(np.float32))
+    for n in (64, 12288, 12289, 128256):   # register path limit is 48 * 256 = 12288
+        cases.append(rng.standard_normal(n).astype(np.float32))
+    for row in cases:
+        for k in (1, 32, 64):
+            if k > row.size:
+                continue
+            gi, gv = _topk_rows(hip, torch, row[None, :], k, signed)
+            ri, rv = (oracle.topk_signed if signed else oracle.topk_abs)(row, k)
+            np.testing.assert_array_equal(gi[0], ri, err_msg=f"n={row.size} k={k} signed={signed}")
+            np.testing.assert_array_equal(gv[0].view(np.uint32), rv.view(np.uint32))
+
+
+def test_topk_invalid_k_returns_none():
+    be = larql_hip.HipBackend(0, strict=False)
+    try:
+        gate = np.zeros((8, 64), np.float32)
+        q = np.zeros(64, np.float32)
+        assert be.gate_knn(gate, 8, 64, q, 9, fmt=larql_hip.F32) is None      # k > features
+        assert be.gate_knn(gate, 8, 64, q, 65, fmt=larql_hip.F32) is None     # k > 64
+        assert be.gate_knn(gate, 8, 64, q, 4, fmt=larql_hip.Q4_K) is None     # unsupported format
+    finally:
+        be.close()
+
+
+def test_gate_knn_34_layers_full_size(hip):
+    """The vindex walk shape: 34 layers x gate [10240 x 2560], 256 queries, top-32, in
+    f32 and Q4_0, one launch each.  Four (layer, query) lists of each are checked against
+    the oracle bit for bit; every list is checked for the selection invariants."""
+    torch = pytest.importorskip("torch")
+    L, F, K, Q, k = 34, 10240, 2560, 256, 32
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gates, handles_f32, handles_q4, q4_host = [], [], [], {}
+    print("[knn 34] building gates", flush=True)
+    for l in range(L):
+        gen.manual_seed(9000 + l)
+        g = torch.randn(F, K, generator=gen, device=dev, dtype=torch.float32) * 0.02
+        handles_f32.append(hip.register_weight_device(larql_hip.F32, g, g.numel() * 4, F, K))
+        raw = torch.empty(F * K // 32 * 18, dtype=torch.uint8, device=dev)
+        hip.quantize_weights_dev(larql_hip.Q4_0, g, F * K, raw)
+        hip.synchronize()
+        handles_q4.append(hip.register_weight_device(larql_hip.Q4_0, raw, raw.numel(), F, K))
+        if l in (0, 33):
+            gates.append((l, g.cpu().numpy()))
+            q4_host[l] = raw.cpu().numpy()
+        del g, raw
+    gen.manual_seed(4)
+    queries = torch.randn(Q, K, generator=gen, device=dev, dtype=torch.float32)
+    qn = queries.cpu().numpy()
+    try:
+        for fmt, handles in (("f32", handles_f32), ("q4_0", handles_q4)):
+            di = torch.empty(L * Q * k, device=dev, dtype=torch.int32)
+            dv = torch.empty(L * Q * k, device=dev, dtype=torch.float32)
+            hip.gate_knn_dev(handles, queries, Q, k, di, dv)
+            hip.synchronize()
+            gi = di.cpu().numpy().view(np.uint32).reshape(L, Q, k)
+            gv = dv.cpu().numpy().reshape(L, Q, k)
+            print(f"[knn 34] {fmt}: checking invariants", flush=True)
+            a = np.abs(gv)
+            assert np.all(a[..., :-1] >= a[..., 1:])
+            assert all(len(set(r)) == k for r in gi.reshape(-1, k))
+            assert gi.max() < F
+            for l, g in gates:
+                for qi in (0, 255):
+                    if fmt == "f32":
+                        s = oracle.gate_scores_f32(g, qn[qi], F, K)
+                    else:
+                        q8, q8s = oracle.quantize_to_q8(qn[qi])
+                        s = oracle.q4_0_matvec_blockint(q4_host[l], q8, q8s, F, K)
+                    ri, rv = oracle.topk_abs(s, k)
+                    np.testing.assert_array_equal(gi[l, qi], ri, err_msg=f"{fmt} layer {l} query {qi}")
+                    np.testing.assert_array_equal(gv[l, qi].view(np.uint32), rv.view(np.uint32))
+    finally:
+        for h in handles_f32 + handles_q4:
+            hip.release_weight(h)
