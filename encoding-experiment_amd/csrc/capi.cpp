@@ -287,6 +287,18 @@ extern "C" int larql_hip_q4k_matvec(larql_hip_ctx* c, const uint8_t* q4k_data, s
     });
 }
 
+extern "C" int larql_hip_q4k_matmul(larql_hip_ctx* c, const uint8_t* q4k_data, size_t q4k_len, const float* x,
+                                    size_t m, float* out, size_t num_rows, size_t hidden) {
+    return guarded(c, [&] {
+        if (!q4k_data || !x || !out || m == 0) fail(LARQL_HIP_ERR_INVALID, "null pointer or m == 0");
+        const DevWeight& w = larql::cached_weight(c, LARQL_Q4_K, q4k_data, q4k_len, nullptr, num_rows, hidden);
+        const float* dx = stage_upload(c, c->stage_in, x, m * hidden);
+        float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, m * num_rows * sizeof(float)));
+        larql::launch_q4k_matvec(w, dx, dout, m, c->stream);
+        download(c, out, dout, m * num_rows * sizeof(float));
+    });
+}
+
 extern "C" int larql_hip_q6k_matvec(larql_hip_ctx* c, const uint8_t* q6k_data, size_t q6k_len, const float* x,
                                     float* out, size_t num_rows, size_t hidden) {
     return guarded(c, [&] {

@@ -156,6 +156,8 @@ const DevWeight& cached_weight(larql_hip_ctx* c, int format, const void* data, s
 // ── kernel launchers (device pointers; enqueue only) ───────────────────
 void launch_q4k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s);
 void launch_q6k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s);
+// Y[m][rows] = X[m][cols] . deq(W)^T, Q4_K, on MFMA (prefill.hip).
+void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, hipStream_t s);
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
                         size_t m, hipStream_t s);
 void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,

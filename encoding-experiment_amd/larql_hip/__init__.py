@@ -59,6 +59,7 @@ SIGNATURES = {
     "larql_hip_q4_matvec": (_I, [_P, _P, _SZ, _P, _P, _P, _SZ, _SZ]),
     "larql_hip_q4k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
     "larql_hip_q6k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
+    "larql_hip_q4k_matmul": (_I, [_P, _P, _SZ, _P, _SZ, _P, _SZ, _SZ]),
     "larql_hip_quantize_to_q8": (_I, [_P, _P, _SZ, _P, _P]),
     "larql_hip_q8_matvec": (_I, [_P, _P, _SZ, _P, _P, _P, _SZ, _P, _SZ, _SZ]),
     "larql_hip_matvec_dev": (_I, [_P, _U64, _P, _P, _P, _SZ, _P]),
@@ -321,6 +322,17 @@ class HipBackend:
         xv, xp = _arr(x, np.float32)
         out = np.empty(num_rows, dtype=np.float32)
         rc = self._lib.larql_hip_q4k_matvec(self._ctx, qp, q.size, xp, out.ctypes.data_as(_P), num_rows, hidden)
+        return out if self._ok(rc) else None
+
+    def q4k_matmul(self, q4k_data, x, num_rows: int, hidden: int):
+        """Prefill projection (Metal prefill loop, LC/src/metal/prefill.rs:21-110):
+        x f32 [m, hidden] -> out f32 [m, num_rows] = x . deq(Q4_K)^T (MFMA GEMM)."""
+        q, qp = _arr(q4k_data, np.uint8)
+        xv = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, hidden)
+        m = xv.shape[0]
+        out = np.empty((m, num_rows), dtype=np.float32)
+        rc = self._lib.larql_hip_q4k_matmul(self._ctx, qp, q.size, xv.ctypes.data_as(_P), m, out.ctypes.data_as(_P),
+                                            num_rows, hidden)
         return out if self._ok(rc) else None
 
     def q6k_matvec(self, q6k_data, x, num_rows: int, hidden: int):

@@ -108,6 +108,13 @@ int larql_hip_q4_matvec(larql_hip_ctx* ctx, const uint8_t* q4_data, size_t q4_le
 int larql_hip_q4k_matvec(larql_hip_ctx* ctx, const uint8_t* q4k_data, size_t q4k_len, const float* x,
                          float* out, size_t num_rows, size_t hidden);
 
+/* Prefill projection: out[m][num_rows] = x[m][hidden] . deq(Q4_K)^T for m tokens at once —
+ * the per-position q4k_matvec loop of the Metal prefill (LC/src/metal/prefill.rs:21-110,
+ * trait prefill_q4 LC/src/backend.rs:143-152) as one MFMA GEMM (fp16 operands, f32 sums).
+ * m = 1 is the matvec. */
+int larql_hip_q4k_matmul(larql_hip_ctx* ctx, const uint8_t* q4k_data, size_t q4k_len, const float* x, size_t m,
+                         float* out, size_t num_rows, size_t hidden);
+
 /* ComputeBackend::q6k_matvec — LC/src/backend.rs:133-137 (CPU: LC/src/cpu/ops/q6k_matvec.rs:31-90). */
 int larql_hip_q6k_matvec(larql_hip_ctx* ctx, const uint8_t* q6k_data, size_t q6k_len, const float* x,
                          float* out, size_t num_rows, size_t hidden);
@@ -136,7 +143,7 @@ int larql_hip_quantize_weights(larql_hip_ctx* ctx, int format, const float* x, s
 /* ── device-resident fast path (device pointers; enqueue on `stream`) ──── */
 
 /* One matvec with a registered weight.  For LARQL_Q4_K / LARQL_Q6_K `x` is f32
- * [m][cols] and x_scales is unused; for LARQL_Q4_0 / LARQL_Q8_0 `x` is int8
+ * [m][cols] and x_scales is unused (Q4_K with m > 1 runs the prefill GEMM, Q6_K needs m = 1); for LARQL_Q4_0 / LARQL_Q8_0 `x` is int8
  * [m][cols] and x_scales f32 [m][cols/32].  out is f32 [m][rows].
  * stream: a hipStream_t, or NULL for the context stream.  Returns after enqueue. */
 int larql_hip_matvec_dev(larql_hip_ctx* ctx, uint64_t handle, const void* x, const float* x_scales,
