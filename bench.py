@@ -165,6 +165,143 @@ def run_decode(be, torch, stream, steps, warmup):
     }
 
 
+def _time_us(torch, stream, fn, n, warm=5):
+    for i in range(warm):
+        fn(i)
+    return time_launches(torch, stream, fn, n) * 1e3 / n
+
+
+def bench_configs(be, torch, stream, copies: int):
+    """The other workloads of the path, each at its full single-GPU shape: Q4_0 x Q8
+    [10240x2560]; Q8_0 x Q8 [14336x4096] at M = 1, 4, 8; Q6_K [14336x4096] and
+    [4096x14336]; gate-KNN over 34 layers [10240x2560] x 256 queries, top-32, f32 and
+    Q4_0; Q4_K prefill GEMM 512 x [10240x2560]."""
+    import larql_hip
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    out = {}
+
+    def rnd(*shape, seed, std=1.0):
+        gen.manual_seed(seed)
+        return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std
+
+    def hbm(name, nbytes, us, extra=None):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        d = {"us_per_launch": round(us, 3), "bytes_per_launch": nbytes, "GBs": round(gbs, 1),
+             "roofline": {"bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+        if extra:
+            d.update(extra)
+        out[name] = d
+        log(f"[bench] {name}: {d}")
+
+    # Q4_0 x Q8, [10240 x 2560]
+    N, K = 10240, 2560
+    w = rnd(N, K, seed=11, std=0.02)
+    raw = torch.empty(N * K // 32 * 18, dtype=torch.uint8, device=dev)
+    be.quantize_weights_dev(larql_hip.Q4_0, w, N * K, raw, stream=stream)
+    torch.cuda.synchronize()
+    hs = [be.register_weight_device(larql_hip.Q4_0, raw, raw.numel(), N, K) for _ in range(copies)]
+    x = rnd(K, seed=12)
+    xq = torch.empty(K, dtype=torch.int8, device=dev)
+    xs = torch.empty(K // 32, dtype=torch.float32, device=dev)
+    be.quantize_to_q8_dev(x, K, 1, xq, xs, stream=stream)
+    y = torch.empty(N, device=dev)
+    us = _time_us(torch, stream, lambda i: be.matvec_dev(hs[i % copies], xq, y, x_scales=xs, stream=stream), 200)
+    hbm("q4_0_matvec_10240x2560", N * K // 32 * 18 + K + K // 32 * 4 + N * 4, us)
+    for h in hs:
+        be.release_weight(h)
+    del w, raw
+
+    # Q8_0 x Q8, [14336 x 4096], M in {1, 4, 8}
+    N, K = 14336, 4096
+    w = rnd(N, K, seed=21, std=0.02)
+    wq = torch.empty(N * K, dtype=torch.int8, device=dev)
+    wsc = torch.empty(N * K // 32, dtype=torch.float32, device=dev)
+    be.quantize_weights_dev(larql_hip.Q8_0, w, N * K, wq, q8_scales=wsc, stream=stream)
+    torch.cuda.synchronize()
+    hs = [be.register_weight_device(larql_hip.Q8_0, wq, wq.numel(), N, K, dev_q8_scales=wsc)
+          for _ in range(copies // 2)]
+    for m in (1, 4, 8):
+        x = rnd(m, K, seed=22)
+        xq = torch.empty(m * K, dtype=torch.int8, device=dev)
+        xs = torch.empty(m * K // 32, dtype=torch.float32, device=dev)
+        be.quantize_to_q8_dev(x, K, m, xq, xs, stream=stream)
+        y = torch.empty(m * N, device=dev)
+        us = _time_us(torch, stream, lambda i: be.matvec_dev(hs[i % len(hs)], xq, y, m=m, x_scales=xs, stream=stream),
+                      200)
+        hbm(f"q8_0_matvec_14336x4096_m{m}", N * K + N * K // 32 * 4 + m * (K + K // 32 * 4) + m * N * 4, us)
+    for h in hs:
+        be.release_weight(h)
+    del w, wq, wsc
+
+    # Q6_K [14336 x 4096] and [4096 x 14336]
+    for (N, K), seed in (((14336, 4096), 31), ((4096, 14336), 32)):
+        w = rnd(N, K, seed=seed, std=0.02)
+        raw = torch.empty(N * K // 256 * 210, dtype=torch.uint8, device=dev)
+        be.quantize_weights_dev(larql_hip.Q6_K, w, N * K, raw, stream=stream)
+        torch.cuda.synchronize()
+        hs = [be.register_weight_device(larql_hip.Q6_K, raw, raw.numel(), N, K) for _ in range(copies)]
+        x = rnd(K, seed=seed + 100)
+        y = torch.empty(N, device=dev)
+        us = _time_us(torch, stream, lambda i: be.matvec_dev(hs[i % copies], x, y, stream=stream), 200)
+        hbm(f"q6k_matvec_{N}x{K}", N * K // 256 * 210 + K * 4 + N * 4, us)
+        for h in hs:
+            be.release_weight(h)
+        del w, raw
+
+    # gate-KNN: 34 layers [10240 x 2560] x 256 queries, top-32
+    L, F, K, Q, k = 34, 10240, 2560, 256, 32
+    hf, hq = [], []
+    for l in range(L):
+        g = rnd(F, K, seed=9000 + l, std=0.02)
+        hf.append(be.register_weight_device(larql_hip.F32, g, g.numel() * 4, F, K))
+        raw = torch.empty(F * K // 32 * 18, dtype=torch.uint8, device=dev)
+        be.quantize_weights_dev(larql_hip.Q4_0, g, F * K, raw, stream=stream)
+        torch.cuda.synchronize()
+        hq.append(be.register_weight_device(larql_hip.Q4_0, raw, raw.numel(), F, K))
+        del g, raw
+    q = rnd(Q, K, seed=4)
+    di = torch.empty(L * Q * k, device=dev, dtype=torch.int32)
+    dv = torch.empty(L * Q * k, device=dev)
+    flops = 2.0 * L * F * K * Q
+    for name, hs, peak, unit in (("f32", hf, 157.3, "TFLOP/s"), ("q4_0", hq, 5000.0, "TOP/s")):
+        us = _time_us(torch, stream, lambda i: be.gate_knn_dev(hs, q, Q, k, di, dv, stream=stream), 10, warm=2)
+        t = flops / (us * 1e-6) / 1e12
+        bound = "valu-fp32" if name == "f32" else "int8-dot"
+        out[f"gate_knn_{name}_34x10240x2560_q256_top32"] = {
+            "ms_per_walk": round(us / 1e3, 3), "ops": flops, "achieved": round(t, 1), "unit": unit,
+            "roofline": {"bound": bound, "peak": peak, "unit": unit, "frac": round(t / peak, 4)},
+            "note": "f32 scores are canonical fma chains (bit-exact, no MFMA); Q4_0 int32 block dots "
+                    "on VALU v_dot4 vs the int8 MFMA peak"}
+        log(f"[bench] gate_knn {name}: {out[f'gate_knn_{name}_34x10240x2560_q256_top32']}")
+    for h in hf + hq:
+        be.release_weight(h)
+
+    # prefill: 512 tokens through Q4_K [10240 x 2560] on MFMA
+    N, K, M = 10240, 2560, 512
+    w = rnd(N, K, seed=51, std=0.02)
+    raw = torch.empty(N * K // 256 * 148, dtype=torch.uint8, device=dev)
+    be.quantize_weights_dev(larql_hip.Q4_K, w, N * K, raw, stream=stream)
+    torch.cuda.synchronize()
+    hs = [be.register_weight_device(larql_hip.Q4_K, raw, raw.numel(), N, K) for _ in range(copies)]
+    x = rnd(M, K, seed=52)
+    y = torch.empty(M * N, device=dev)
+    us = _time_us(torch, stream, lambda i: be.matvec_dev(hs[i % copies], x, y, m=M, stream=stream), 100)
+    fl = 2.0 * M * N * K
+    t = fl / (us * 1e-6) / 1e12
+    out["prefill_q4k_gemm_512x10240x2560"] = {
+        "us_per_launch": round(us, 2), "flops": fl, "achieved": round(t, 1), "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "peak": 2500.0, "unit": "TFLOP/s", "frac": round(t / 2500.0, 4)},
+        "bytes": N * K // 256 * 148 + M * K * 4 + M * N * 4}
+    log(f"[bench] prefill: {out['prefill_q4k_gemm_512x10240x2560']}")
+    for h in hs:
+        be.release_weight(h)
+    del w, raw
+    torch.cuda.empty_cache()
+    return out
+
+
 def pmc_pass(which: str, launches: int):
     """Kernels only, for a rocprofv3 --pmc run (no timing output)."""
     import torch
@@ -234,6 +371,7 @@ def main():
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--decode-steps", type=int, default=30)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the non-headline workloads")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-pass", choices=("calib", "gate"))
@@ -301,6 +439,10 @@ def main():
     del raws
     torch.cuda.empty_cache()
 
+    configs = None
+    if not args.no_configs:
+        configs = bench_configs(be, torch, stream, args.copies)
+
     decode = None
     if not args.no_decode:
         decode = run_decode(be, torch, stream, args.decode_steps, warmup=5)
@@ -345,6 +487,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "decode": decode,
+        "configs": configs,
     }
     print(json.dumps(result), flush=True)
     be.close()
