@@ -141,11 +141,21 @@ __global__ __launch_bounds__(256) void q4_0_matvec_kernel(const uint8_t* __restr
     }
 }
 
+// Rows per tile: enough tiles for ~4 workgroups per CU (the per-row block sums are
+// serial, so parallelism comes from tiles), a power of two in [4, 64].  Measured on
+// [10240 x 2560] Q4_0: 64 rows 15.8 us, 8 rows 7.8 us.
+static int tile_rows(size_t rows) {
+    const size_t want = rows / (4 * static_cast<size_t>(current_device_cus()));
+    int rw = 4;
+    while (rw < 64 && static_cast<size_t>(rw) * 2 <= want) rw *= 2;
+    return rw;
+}
+
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, size_t m,
                         hipStream_t s) {
     if (m != 1) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4_matvec: batch > 1 not supported");
     const int nb = static_cast<int>(w.cols / 32);
-    int rw = 64;
+    int rw = tile_rows(w.rows);
     const size_t fixed = static_cast<size_t>(nb) * (16 + 16 + 4 + 4);
     while (rw > 1 && fixed + static_cast<size_t>(rw) * nb * 4 > 60 * 1024) rw >>= 1;
     if (fixed + static_cast<size_t>(rw) * nb * 4 > 60 * 1024)
@@ -228,7 +238,7 @@ void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, f
     auto go = [&](auto mtag) {
         constexpr int M = decltype(mtag)::value;
         const size_t fixed = static_cast<size_t>(M) * nb * (32 + 4);
-        int rw = 64;
+        int rw = tile_rows(w.rows);
         while (rw > 1 && fixed + static_cast<size_t>(M) * rw * nb * 4 > 64 * 1024) rw >>= 1;
         if (fixed + static_cast<size_t>(M) * rw * nb * 4 > 64 * 1024)
             fail(LARQL_HIP_ERR_UNSUPPORTED, "q8_matvec: hidden too large for LDS staging");
