@@ -7,16 +7,27 @@
 //   Q8_0 x Q8 : q8_matvec::dispatch (LC/src/cpu/ops/q8_matvec.rs:36-62), same structure
 //               with an int8 weight block and a separate f32 weight scale.
 //
-// Both kernels reproduce that order bit for bit: a tile of (row, block) pairs is
-// mapped flat onto the workgroup (consecutive threads read consecutive 16/32-byte
-// blocks, so a tile is one contiguous stream), each pair's product
-// (float)isum * scale is written to LDS, and one thread per row then sums its
-// products in block order.  The activation (int8 values, re-ordered into even/odd
-// element dwords for v_dot4_i32_i8, plus its f32 block scales) is staged in LDS
+// Both reproduce that order bit for bit, for 1..8 activation rows at once (the
+// weights are read once for all of them):
+//   * int_mv_kernel: a group of G (4 or 16) consecutive lanes owns one weight row; at
+//     step s lane j holds block s*G + j, so a step reads G contiguous blocks of the
+//     row, and the block products (float)isum * scale are added to the row's running
+//     sum in block order by G v_add_f32 with a DPP broadcast of lane 0, 1, ..., G-1
+//     (every lane of the group carries the same sum; lane 0 stores it).  Lanes of a
+//     step that fall past the last block contribute +0, which leaves a sum that starts
+//     at +0 unchanged.
+//   * q8_mfma_kernel (Q8_0, 5..8 activation rows): the int32 block dots on the matrix
+//     cores, the products and sums per lane (described at the kernel).
+// Weight blocks stream through a register ring several steps deep.  The activation
+// rows (int8 values, for Q4_0 re-ordered into even/odd element dwords for
+// v_dot4_i32_i8 with the block's integer sum; f32 block scales) are staged in LDS
 // once per workgroup.
 //
 // quantize_to_q8 (LC/src/cpu/ops/q4_common.rs:28-44) is reproduced bit for bit:
 // IEEE division for amax/127 and 1/scale, round-half-away-from-zero, clamp.
+#include <algorithm>
+#include <utility>
+
 #include "device_common.h"
 #include "larql_hip_internal.h"
 
@@ -50,224 +61,480 @@ void launch_quantize_q8(const float* x, size_t n, size_t m, int8_t* q8, float* s
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
-// ── staging helpers ────────────────────────────────────────────────────
-// LDS image of one Q8 activation row: per block b, 16 bytes of even-index values,
-// 16 bytes of odd-index values, their integer sum, and the f32 scale.
-struct Q8Lds {
-    uint32_t* xe;   // [nb][4]
-    uint32_t* xo;   // [nb][4]
-    int* xsum;      // [nb]
-    float* xs;      // [nb]
+// ── the kernel ─────────────────────────────────────────────────────────
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kThreads = 256;
+
+template <int C>
+__device__ __forceinline__ float dpp_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), C, 0xF, 0xF, true));
+}
+
+// acc[m] + p[m](lane 0) + p[m](lane 1) + ... + p[m](lane G-1) of the lane's G-lane group,
+// left to right for every m: G = 16 broadcasts with row_newbcast:J (lane J of each
+// 16-lane row), G = 4 with quad_perm:[J,J,J,J].  The M sums advance together, so
+// consecutive adds are independent (no read-after-write stall between them).
+template <int G, int M, int J>
+__device__ __forceinline__ void chain_step(float (&acc)[M], const float (&p)[M]) {
+    static_assert(G == 16 || G == 4, "lane group of 4 or 16");
+#pragma unroll
+    for (int mi = 0; mi < M; mi++) acc[mi] = acc[mi] + dpp_bcast<G == 16 ? 0x150 + J : J * 0x55>(p[mi]);
+}
+
+template <int G, int M, int... J>
+__device__ __forceinline__ void chain_add(float (&acc)[M], const float (&p)[M], std::integer_sequence<int, J...>) {
+    (chain_step<G, M, J>(acc, p), ...);
+}
+
+// One raw Q8 activation block: 32 int8 values and the f32 scale.
+struct XRaw {
+    uint4 a, c;
+    float s;
+    __device__ __forceinline__ void load(const int8_t* xq, const float* xsc, int i) {
+        const uint4* p = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(i) * 32);
+        a = p[0];
+        c = p[1];
+        s = xsc[i];
+    }
 };
 
-__device__ __forceinline__ void stage_q8_row(const int8_t* __restrict__ xq, const float* __restrict__ xsc,
-                                             int nb, Q8Lds L) {
-    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-        const uint4* p = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(b) * 32);
-        const uint4 a = p[0], c = p[1];
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+template <int FMT>
+struct Blk;
+
+// Q4_0: 16 nibble bytes + the f16 scale.  LDS image per (activation row, block):
+// 8 dwords (even-element, odd-element dwords) and {-8 * sum(x_q), x scale}.
+template <>
+struct Blk<LARQL_Q4_0> {
+    uint4 q;
+    uint32_t d;
+    static constexpr int kXAux = 2;
+    __device__ __forceinline__ void load(const uint8_t* qs, const void* dsc, size_t blk) {
+        q = reinterpret_cast<const uint4*>(qs)[blk];
+        d = static_cast<const uint16_t*>(dsc)[blk];
+    }
+    __device__ __forceinline__ float product(const uint4* x0, const uint4* x1, const uint32_t* xa) const {
+        const uint4 e0 = *x0;
+        const uint4 e1 = *x1;
+        const uint2 a = *reinterpret_cast<const uint2*>(xa);
+        const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+        const uint32_t xe[4] = {e0.x, e0.y, e0.z, e0.w};
+        const uint32_t xo[4] = {e1.x, e1.y, e1.z, e1.w};
+        int isum = static_cast<int>(a.x);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            isum = __builtin_amdgcn_sdot4(static_cast<int>(qw[t] & 0x0F0F0F0Fu), static_cast<int>(xe[t]), isum, false);
+            isum = __builtin_amdgcn_sdot4(static_cast<int>((qw[t] >> 4) & 0x0F0F0F0Fu), static_cast<int>(xo[t]), isum,
+                                          false);
+        }
+        const float cs = h2f(d) * __uint_as_float(a.y);
+        return static_cast<float>(isum) * cs;
+    }
+    // one x block (flat index i over [M][nb]) -> LDS image
+    __device__ static void put_x(const XRaw& r, uint4* x0, uint4* x1, uint32_t* xa) {
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.c.x, r.c.y, r.c.z, r.c.w};
+        uint32_t ev[4], od[4];
         int s = 0;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            // dword t of the nibble block covers elements 8t..8t+7: bytes 2t, 2t+1 of x.
+            // nibble dword t covers elements 8t..8t+7 (byte i: elements 2i low, 2i+1 high),
+            // i.e. x dwords 2t and 2t+1: even elements go with the low nibbles.
             const uint32_t e0 = w[2 * t], e1 = w[2 * t + 1];
-            // even elements 8t+0,2,4,6 -> bytes 0,2 of e0 and 0,2 of e1
-            const uint32_t ev = __builtin_amdgcn_perm(e1, e0, 0x06040200u);
-            const uint32_t od = __builtin_amdgcn_perm(e1, e0, 0x07050301u);
-            L.xe[b * 4 + t] = ev;
-            L.xo[b * 4 + t] = od;
-            s += __builtin_amdgcn_sdot4(static_cast<int>(e0), 0x01010101, 0, false);
-            s += __builtin_amdgcn_sdot4(static_cast<int>(e1), 0x01010101, 0, false);
+            ev[t] = __builtin_amdgcn_perm(e1, e0, 0x06040200u);
+            od[t] = __builtin_amdgcn_perm(e1, e0, 0x07050301u);
+            s = __builtin_amdgcn_sdot4(static_cast<int>(e0), 0x01010101, s, false);
+            s = __builtin_amdgcn_sdot4(static_cast<int>(e1), 0x01010101, s, false);
         }
-        L.xsum[b] = s;
-        L.xs[b] = xsc[b];
+        *x0 = make_uint4(ev[0], ev[1], ev[2], ev[3]);
+        *x1 = make_uint4(od[0], od[1], od[2], od[3]);
+        xa[0] = static_cast<uint32_t>(-8 * s);
+        xa[1] = __float_as_uint(r.s);
     }
+};
+
+// Q8_0 (trait form): 32 int8 + an f32 scale.  LDS image: the 8 raw x dwords and the
+// x scale.
+template <>
+struct Blk<LARQL_Q8_0> {
+    uint4 a, c;
+    float ws;
+    static constexpr int kXAux = 1;
+    __device__ __forceinline__ void load(const uint8_t* qs, const void* dsc, size_t blk) {
+        const uint4* p = reinterpret_cast<const uint4*>(qs) + 2 * blk;
+        a = p[0];
+        c = p[1];
+        ws = static_cast<const float*>(dsc)[blk];
+    }
+    __device__ __forceinline__ float product(const uint4* xp0, const uint4* xp1, const uint32_t* xa) const {
+        const uint4 x0 = *xp0;
+        const uint4 x1 = *xp1;
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+        const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        int isum = 0;
+#pragma unroll
+        for (int t = 0; t < 8; t++) isum = __builtin_amdgcn_sdot4(static_cast<int>(w[t]), static_cast<int>(x[t]), isum, false);
+        const float cs = ws * __uint_as_float(xa[0]);
+        return static_cast<float>(isum) * cs;
+    }
+    __device__ static void put_x(const XRaw& r, uint4* x0, uint4* x1, uint32_t* xa) {
+        *x0 = r.a;
+        *x1 = r.c;
+        xa[0] = __float_as_uint(r.s);
+    }
+};
+
+template <int FMT>
+constexpr size_t x_lds_bytes(int m, int nb) {
+    return static_cast<size_t>(m) * nb * (32 + Blk<FMT>::kXAux * 4);
 }
 
-// ── Q4_0 x Q8 ──────────────────────────────────────────────────────────
-__global__ __launch_bounds__(256) void q4_0_matvec_kernel(const uint8_t* __restrict__ qs,
-                                                          const uint16_t* __restrict__ dsc,
+// Grid: one workgroup per 256 / G rows.  x: M activation rows of Q8 values (cols int8
+// each) and their scales (nb each); out: M rows of `rows` floats.
+template <int FMT, int M, int G, int D>
+__global__ __launch_bounds__(kThreads) void int_mv_kernel(const uint8_t* __restrict__ qs,
+                                                          const void* __restrict__ dsc,
                                                           const int8_t* __restrict__ xq,
                                                           const float* __restrict__ xsc,
-                                                          float* __restrict__ out, int rows, int cols,
-                                                          int rw, int tiles) {
-    extern __shared__ uint32_t lds[];
-    const int nb = cols >> 5;
-    Q8Lds L;
-    L.xe = lds;
-    L.xo = L.xe + nb * 4;
-    L.xsum = reinterpret_cast<int*>(L.xo + nb * 4);
-    L.xs = reinterpret_cast<float*>(L.xsum + nb);
-    float* p = L.xs + nb;  // [rw][nb]
-    stage_q8_row(xq, xsc, nb, L);
+                                                          float* __restrict__ out, int rows, int nb) {
+    using B = Blk<FMT>;
+    // x image: first and second 16 bytes of every block in separate arrays, so the 16
+    // lanes of a group read 256 contiguous bytes (no bank conflicts)
+    extern __shared__ uint4 lds4[];
+    uint4* xw0 = lds4;                                             // [M][nb]
+    uint4* xw1 = lds4 + M * nb;                                    // [M][nb]
+    uint32_t* xa = reinterpret_cast<uint32_t*>(lds4 + 2 * M * nb);  // [M][nb][kXAux]
+    const int j = threadIdx.x & (G - 1);
+    const int row = blockIdx.x * (kThreads / G) + threadIdx.x / G;
+    const size_t base = static_cast<size_t>(min(row, rows - 1)) * nb;
+    const int steps = (nb + G - 1) / G;
+    const int nx = M * nb;
+
+    // x loads first (the staging wait then covers them only), kXBatch blocks per thread
+    // in flight together, then the first D steps of weights, which stay in flight
+    // through the staging and the barrier
+    constexpr int kXBatch = (M * 128 + kThreads - 1) / kThreads;  // all of x for hidden <= 4096
+    XRaw xr[kXBatch];
+#pragma unroll
+    for (int k = 0; k < kXBatch; k++) xr[k].load(xq, xsc, min(static_cast<int>(threadIdx.x) + k * kThreads, nx - 1));
+    B ring[D];
+#pragma unroll
+    for (int u = 0; u < D; u++) ring[u].load(qs, dsc, base + min(u * G + j, nb - 1));
+#pragma unroll
+    for (int k = 0; k < kXBatch; k++) {
+        const int i = threadIdx.x + k * kThreads;
+        if (i < nx) B::put_x(xr[k], xw0 + i, xw1 + i, xa + i * B::kXAux);
+    }
+    for (int i0 = threadIdx.x + kXBatch * kThreads; i0 < nx; i0 += kXBatch * kThreads) {
+#pragma unroll
+        for (int k = 0; k < kXBatch; k++) xr[k].load(xq, xsc, min(i0 + k * kThreads, nx - 1));
+#pragma unroll
+        for (int k = 0; k < kXBatch; k++) {
+            const int i = i0 + k * kThreads;
+            if (i < nx) B::put_x(xr[k], xw0 + i, xw1 + i, xa + i * B::kXAux);
+        }
+    }
     __syncthreads();
 
-    const int pairs = rw * nb;
-    for (int tile = 0; tile < tiles; tile++) {
-        const int row0 = (blockIdx.x * tiles + tile) * rw;
-        int rl = threadIdx.x / nb;
-        int b = threadIdx.x - rl * nb;
-        for (int f = threadIdx.x; f < pairs; f += blockDim.x) {
-            const int row = row0 + rl;
-            if (row < rows) {
-                const size_t blk = static_cast<size_t>(row) * nb + b;
-                const uint4 q = reinterpret_cast<const uint4*>(qs)[blk];
-                const float cs = h2f(dsc[blk]) * L.xs[b];
-                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-                int isum = -8 * L.xsum[b];
+    float acc[M];
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    isum = __builtin_amdgcn_sdot4(static_cast<int>(qw[t] & 0x0F0F0F0Fu),
-                                                  static_cast<int>(L.xe[b * 4 + t]), isum, false);
-                    isum = __builtin_amdgcn_sdot4(static_cast<int>((qw[t] >> 4) & 0x0F0F0F0Fu),
-                                                  static_cast<int>(L.xo[b * 4 + t]), isum, false);
-                }
-                p[f] = static_cast<float>(isum) * cs;
-            }
-            b += blockDim.x;
-            while (b >= nb) { b -= nb; rl++; }
+    for (int mi = 0; mi < M; mi++) acc[mi] = 0.0f;
+    auto consume = [&](const B& blk, int s) __attribute__((always_inline)) {
+        const int b = s * G + j;
+        const int bc = min(b, nb - 1);
+        float p[M];
+#pragma unroll
+        for (int mi = 0; mi < M; mi++) {
+            const int xi = mi * nb + bc;
+            p[mi] = blk.product(xw0 + xi, xw1 + xi, xa + xi * B::kXAux);
+            p[mi] = b < nb ? p[mi] : 0.0f;
         }
-        __syncthreads();
-        for (int r = threadIdx.x; r < rw; r += blockDim.x) {
-            const int row = row0 + r;
-            if (row < rows) {
-                float acc = 0.0f;
-                const float* pr = p + r * nb;
-                for (int k = 0; k < nb; k++) acc += pr[k];
-                out[row] = acc;
-            }
+        chain_add<G, M>(acc, p, std::make_integer_sequence<int, G>{});
+    };
+    int s0 = 0;
+    for (; s0 + D <= steps; s0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            // consume, then refill the same registers (a copy of a slot whose load is
+            // still in flight would wait for it)
+            consume(ring[u], s0 + u);
+            ring[u].load(qs, dsc, base + min((s0 + u + D) * G + j, nb - 1));
+            // keep the refills in ring order: the wait for the next step then leaves the
+            // younger steps in flight
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < D; u++)
+        if (s0 + u < steps) consume(ring[u], s0 + u);
+
+    if (j == 0 && row < rows) {
+#pragma unroll
+        for (int mi = 0; mi < M; mi++) out[static_cast<size_t>(mi) * rows + row] = acc[mi];
     }
 }
 
-// Rows per tile: enough tiles for ~4 workgroups per CU (the per-row block sums are
-// serial, so parallelism comes from tiles), a power of two in [4, 64].  Measured on
-// [10240 x 2560] Q4_0: 64 rows 15.8 us, 8 rows 7.8 us.
-static int tile_rows(size_t rows) {
-    const size_t want = rows / (4 * static_cast<size_t>(current_device_cus()));
-    int rw = 4;
-    while (rw < 64 && static_cast<size_t>(rw) * 2 <= want) rw *= 2;
-    return rw;
+// ── Q8_0 x Q8 for 2..8 activation rows on the matrix cores ─────────────
+// v_mfma_i32_16x16x64_i8 gives exact int32 block dots for 16 weight rows x 8
+// activation rows x one block pair at once:
+//   B (64 x 16): the lane with column c and k-group g (l = 16 g + c) holds weight row
+//     c, bytes 16 g .. 16 g + 15 of the pair, i.e. block 2bp + g/2, half g % 2;
+//   A (16 x 64): row i = 2 mi + h holds x_mi's block 2bp + h in the two k-groups of
+//     that block and zeros in the other two,
+// so D[2 mi + h][c] is exactly the int32 dot of block 2bp + h of weight row c with
+// x_mi.  D lane l holds rows 4 g + t (t = 0..3): activation rows 2g and 2g + 1, both
+// blocks of the pair, for weight row c — the lane forms the four products
+// (float)isum * (ws * xs) and adds them to its two running sums in block order,
+// exactly as the serial loop does.  Requires an even block count (hidden % 64 == 0).
+// Weights stream through buffer loads (a prefetch past the end of the array reads 0);
+// weight scales through clamped global loads.
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaMaxM = 8;
+constexpr int kBufDword3 = 0x00020000;  // raw buffer descriptor word 3 (32-bit data format)
+
+constexpr size_t mfma_lds_bytes(int nb) {
+    return (static_cast<size_t>(nb) * 16 + 1) * 16 + static_cast<size_t>(nb) * 8 * 4;
 }
+
+template <int D, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void q8_mfma_kernel(const uint8_t* __restrict__ wq,
+                                                              const float* __restrict__ wsc,
+                                                              const int8_t* __restrict__ xq,
+                                                              const float* __restrict__ xsc,
+                                                              float* __restrict__ out, int rows, int nb, int m) {
+    constexpr int kT = 64 * WAVES;
+    extern __shared__ uint4 lds4[];
+    const int npair = nb >> 1;
+    const int nchunk = nb * 16;
+    uint4* xl = lds4;                                           // [npair][16 A rows][2 halves], then a zero chunk
+    float* xsl = reinterpret_cast<float*>(lds4 + nchunk + 1);   // [npair][8 mi][2 blocks]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int rbase = (blockIdx.x * WAVES + wave) * 16;
+    const uint32_t wr = static_cast<uint32_t>(min(rbase + c, rows - 1));
+
+    // x image item j: pair j >> 5, A row i = (j >> 1) & 15 (mi = i >> 1, block 2bp + (i & 1)),
+    // half j & 1 of the block; zero for mi >= m
+    auto xchunk = [&](int j) __attribute__((always_inline)) {
+        const int mi = min((j >> 2) & 7, m - 1);
+        const int blk = 2 * (j >> 5) + ((j >> 1) & 1);
+        return reinterpret_cast<const uint4*>(xq + (static_cast<size_t>(mi) * nb + blk) * 32)[j & 1];
+    };
+    // x scale item j: pair j >> 4, mi (j >> 1) & 7, block 2bp + (j & 1)
+    auto xscale = [&](int j) __attribute__((always_inline)) {
+        const int mi = min((j >> 1) & 7, m - 1);
+        return xsc[static_cast<size_t>(mi) * nb + 2 * (j >> 4) + (j & 1)];
+    };
+
+    // x loads first, all in flight together (the staging wait then covers them only),
+    // then the first D steps of weights
+    constexpr int kXB = 2048 / kT, kSB = 1024 / kT;  // one batch covers x for hidden <= 4096
+    const uint4 zero = make_uint4(0, 0, 0, 0);
+    auto put_chunk = [&](int j, uint4 v) __attribute__((always_inline)) {
+        if (((j >> 2) & 7) >= m) v = make_uint4(0, 0, 0, 0);
+        if (j < nchunk) xl[j] = v;
+    };
+    auto put_scale = [&](int j, float v) __attribute__((always_inline)) {
+        if (j < nb * 8) xsl[j] = ((j >> 1) & 7) < m ? v : 0.0f;
+    };
+    const int t0 = threadIdx.x;
+    uint4 x0[kXB];
+    float s0[kSB];
+#pragma unroll
+    for (int k = 0; k < kXB; k++) x0[k] = xchunk(min(t0 + k * kT, nchunk - 1));
+#pragma unroll
+    for (int k = 0; k < kSB; k++) s0[k] = xscale(min(t0 + k * kT, nb * 8 - 1));
+
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wq), 0, rows * nb * 32, kBufDword3);
+    const uint32_t voff_w = wr * static_cast<uint32_t>(nb) * 32 + 16 * g;
+    const float2* wsrow = reinterpret_cast<const float2*>(wsc + static_cast<size_t>(wr) * nb);
+    v4i wv[D];
+    float2 ws[D];
+    auto refill = [&](int u, int bp) __attribute__((always_inline)) {
+        wv[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w + 64 * bp, 0, 0);
+        ws[u] = wsrow[min(bp, npair - 1)];
+    };
+#pragma unroll
+    for (int u = 0; u < D; u++) refill(u, u);
+
+#pragma unroll
+    for (int k = 0; k < kXB; k++) put_chunk(t0 + k * kT, x0[k]);
+#pragma unroll
+    for (int k = 0; k < kSB; k++) put_scale(t0 + k * kT, s0[k]);
+    // hidden > 4096: further batches, each loaded whole before it is stored
+    for (int j0 = t0 + kXB * kT; j0 < nchunk; j0 += kXB * kT) {
+        uint4 xb[kXB];
+#pragma unroll
+        for (int k = 0; k < kXB; k++) xb[k] = xchunk(min(j0 + k * kT, nchunk - 1));
+#pragma unroll
+        for (int k = 0; k < kXB; k++) put_chunk(j0 + k * kT, xb[k]);
+    }
+    for (int j0 = t0 + kSB * kT; j0 < nb * 8; j0 += kSB * kT) {
+        float sb[kSB];
+#pragma unroll
+        for (int k = 0; k < kSB; k++) sb[k] = xscale(min(j0 + k * kT, nb * 8 - 1));
+#pragma unroll
+        for (int k = 0; k < kSB; k++) put_scale(j0 + k * kT, sb[k]);
+    }
+    if (threadIdx.x == 0) xl[nchunk] = zero;
+    __syncthreads();
+
+    // A operand of this lane: row c (mi = c >> 1, block half c & 1) at k-group g; the
+    // k-groups of the other block of the pair read the zero chunk
+    const bool a_on = (c & 1) == (g >> 1) && (c >> 1) < m;
+    const uint4* abase = a_on ? xl + c * 2 + (g & 1) : xl + nchunk;
+    const int astride = a_on ? 32 : 0;
+    const float* xsbase = xsl + 4 * g;
+
+    float acc[2] = {0.0f, 0.0f};
+    auto dots = [&](const v4i& w, int bp, v4i& d, float4& xs4) __attribute__((always_inline)) {
+        const uint4 av = abase[bp * astride];
+        const v4i a = {static_cast<int>(av.x), static_cast<int>(av.y), static_cast<int>(av.z), static_cast<int>(av.w)};
+        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w, v4i{0, 0, 0, 0}, 0, 0, 0);
+        xs4 = *reinterpret_cast<const float4*>(xsbase + bp * 16);
+    };
+    auto chain = [&](const v4i& d, const float4& xs4, const float2& w2) __attribute__((always_inline)) {
+        // d[2j + h] = block 2bp + h of activation row 2g + j
+        const float p0 = static_cast<float>(d[0]) * (w2.x * xs4.x);
+        const float p1 = static_cast<float>(d[1]) * (w2.y * xs4.y);
+        const float p2 = static_cast<float>(d[2]) * (w2.x * xs4.z);
+        const float p3 = static_cast<float>(d[3]) * (w2.y * xs4.w);
+        acc[0] = acc[0] + p0;
+        acc[0] = acc[0] + p1;
+        acc[1] = acc[1] + p2;
+        acc[1] = acc[1] + p3;
+    };
+    // the ring is processed in halves of DB steps: all dots of a half, then its sums,
+    // then its refill, while the other half's loads are in flight
+    constexpr int DB = D / 2;
+    int bp0 = 0;
+    for (; bp0 + D <= npair; bp0 += D) {
+#pragma unroll
+        for (int h = 0; h < D; h += DB) {
+            v4i dd[DB];
+            float4 xx[DB];
+#pragma unroll
+            for (int k = 0; k < DB; k++) dots(wv[h + k], bp0 + h + k, dd[k], xx[k]);
+#pragma unroll
+            for (int k = 0; k < DB; k++) chain(dd[k], xx[k], ws[h + k]);
+#pragma unroll
+            for (int k = 0; k < DB; k++) refill(h + k, bp0 + h + k + D);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < D; u++)
+        if (bp0 + u < npair) {
+            v4i d;
+            float4 xs4;
+            dots(wv[u], bp0 + u, d, xs4);
+            chain(d, xs4, ws[u]);
+        }
+
+    const int row = rbase + c;
+    if (row < rows) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int mi = 2 * g + j;
+            if (mi < m) out[static_cast<size_t>(mi) * rows + row] = acc[j];
+        }
+    }
+}
+
+template <int D, int WAVES>
+void launch_q8_mfma_t(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s) {
+    const int nb = static_cast<int>(w.cols / 32);
+    const size_t rows_per_wg = 16 * WAVES;
+    const size_t grid = (w.rows + rows_per_wg - 1) / rows_per_wg;
+    q8_mfma_kernel<D, WAVES><<<dim3(static_cast<unsigned>(grid)), dim3(64 * WAVES), mfma_lds_bytes(nb), s>>>(
+        w.qs, static_cast<const float*>(w.d), q8x, q8s, out, static_cast<int>(w.rows), nb, m);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_q8_mfma(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s) {
+    launch_q8_mfma_t<8, 4>(w, q8x, q8s, out, m, s);
+}
+
+constexpr size_t kLdsLimit = 64 * 1024;
+
+template <int FMT, int M, int G, int D>
+void launch_int_mv_g(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, hipStream_t s) {
+    const int nb = static_cast<int>(w.cols / 32);
+    const size_t rows_per_wg = kThreads / G;
+    const size_t grid = (w.rows + rows_per_wg - 1) / rows_per_wg;
+    int_mv_kernel<FMT, M, G, D><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), x_lds_bytes<FMT>(M, nb), s>>>(
+        w.qs, w.d, q8x, q8s, out, static_cast<int>(w.rows), nb);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+// Lane groups of 4 when the matrix has enough 64-row workgroups to cover the chip
+// (fewer DPP adds per block), else of 16 (four times the workgroups).  Measured on
+// Q8_0 [14336 x 4096]: 16.1 us (G = 4) vs 17.2 us (G = 16); on Q4_0 [10240 x 2560]:
+// 5.2 us (G = 16) vs 5.3 us (G = 4).
+template <int FMT, int M>
+void launch_int_mv(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, hipStream_t s) {
+    if ((w.rows + 63) / 64 * 4 >= static_cast<size_t>(current_device_cus()) * 3)
+        launch_int_mv_g<FMT, M, 4, 4>(w, q8x, q8s, out, s);
+    else
+        launch_int_mv_g<FMT, M, 16, 4>(w, q8x, q8s, out, s);
+}
+
+// M activation rows in chunks of 8/4/2/1, each chunk as large as the LDS image allows.
+template <int FMT>
+void launch_int_mv_batched(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, size_t m,
+                           hipStream_t s) {
+    const int nb = static_cast<int>(w.cols / 32);
+    if (x_lds_bytes<FMT>(1, nb) > kLdsLimit) fail(LARQL_HIP_ERR_UNSUPPORTED, "int matvec: hidden too large for LDS staging");
+    size_t done = 0;
+    while (done < m) {
+        const size_t left = m - done;
+        int take = 1;
+        for (int c : {8, 4, 2})
+            if (left >= static_cast<size_t>(c) && x_lds_bytes<FMT>(c, nb) <= kLdsLimit) { take = c; break; }
+        const int8_t* xq = q8x + done * w.cols;
+        const float* xs = q8s + done * nb;
+        float* o = out + done * w.rows;
+        switch (take) {
+            case 8: launch_int_mv<FMT, 8>(w, xq, xs, o, s); break;
+            case 4: launch_int_mv<FMT, 4>(w, xq, xs, o, s); break;
+            case 2: launch_int_mv<FMT, 2>(w, xq, xs, o, s); break;
+            default: launch_int_mv<FMT, 1>(w, xq, xs, o, s); break;
+        }
+        done += take;
+    }
+}
+
+}  // namespace
 
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, size_t m,
                         hipStream_t s) {
-    if (m != 1) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4_matvec: batch > 1 not supported");
-    const int nb = static_cast<int>(w.cols / 32);
-    int rw = tile_rows(w.rows);
-    const size_t fixed = static_cast<size_t>(nb) * (16 + 16 + 4 + 4);
-    while (rw > 1 && fixed + static_cast<size_t>(rw) * nb * 4 > 60 * 1024) rw >>= 1;
-    if (fixed + static_cast<size_t>(rw) * nb * 4 > 60 * 1024)
-        fail(LARQL_HIP_ERR_UNSUPPORTED, "q4_matvec: hidden too large for LDS staging");
-    const size_t ntiles = (w.rows + rw - 1) / rw;
-    const size_t target = 2048;
-    const int tiles = static_cast<int>((ntiles + target - 1) / target);
-    const size_t grid = (ntiles + tiles - 1) / tiles;
-    const size_t shmem = fixed + static_cast<size_t>(rw) * nb * 4;
-    q4_0_matvec_kernel<<<dim3(grid), dim3(256), shmem, s>>>(
-        w.qs, static_cast<const uint16_t*>(w.d), q8x, q8s, out, static_cast<int>(w.rows),
-        static_cast<int>(w.cols), rw, tiles);
-    LARQL_HIP_CHECK(hipGetLastError());
+    launch_int_mv_batched<LARQL_Q4_0>(w, q8x, q8s, out, m, s);
 }
 
-// ── Q8_0 x Q8, batched over M activation rows ──────────────────────────
-template <int M>
-__global__ __launch_bounds__(256) void q8_matvec_kernel(const int8_t* __restrict__ wq,
-                                                        const float* __restrict__ wsc,
-                                                        const int8_t* __restrict__ xq,
-                                                        const float* __restrict__ xsc,
-                                                        float* __restrict__ out, int rows, int cols,
-                                                        int rw, int tiles) {
-    extern __shared__ uint32_t lds[];
-    const int nb = cols >> 5;
-    uint32_t* xw = lds;                                                  // [M][nb*8] raw int8 dwords
-    float* xs = reinterpret_cast<float*>(xw + M * nb * 8);              // [M][nb]
-    float* p = xs + M * nb;                                              // [M][rw*nb]
-    for (int i = threadIdx.x; i < M * nb * 8; i += blockDim.x)
-        xw[i] = reinterpret_cast<const uint32_t*>(xq)[i];
-    for (int i = threadIdx.x; i < M * nb; i += blockDim.x) xs[i] = xsc[i];
-    __syncthreads();
-
-    const int pairs = rw * nb;
-    for (int tile = 0; tile < tiles; tile++) {
-        const int row0 = (blockIdx.x * tiles + tile) * rw;
-        int rl = threadIdx.x / nb;
-        int b = threadIdx.x - rl * nb;
-        for (int f = threadIdx.x; f < pairs; f += blockDim.x) {
-            const int row = row0 + rl;
-            if (row < rows) {
-                const size_t blk = static_cast<size_t>(row) * nb + b;
-                const uint4* wp = reinterpret_cast<const uint4*>(wq + blk * 32);
-                const uint4 a = wp[0], c = wp[1];
-                const uint32_t ww[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-                const float ws = wsc[blk];
-#pragma unroll
-                for (int mi = 0; mi < M; mi++) {
-                    const uint32_t* xr = xw + (mi * nb + b) * 8;
-                    int isum = 0;
-#pragma unroll
-                    for (int t = 0; t < 8; t++)
-                        isum = __builtin_amdgcn_sdot4(static_cast<int>(ww[t]), static_cast<int>(xr[t]), isum, false);
-                    const float cs = ws * xs[mi * nb + b];
-                    p[mi * pairs + f] = static_cast<float>(isum) * cs;
-                }
-            }
-            b += blockDim.x;
-            while (b >= nb) { b -= nb; rl++; }
-        }
-        __syncthreads();
-        for (int q = threadIdx.x; q < M * rw; q += blockDim.x) {
-            const int mi = q / rw;
-            const int r = q - mi * rw;
-            const int row = row0 + r;
-            if (row < rows) {
-                float acc = 0.0f;
-                const float* pr = p + mi * pairs + r * nb;
-                for (int k = 0; k < nb; k++) acc += pr[k];
-                out[static_cast<size_t>(mi) * rows + row] = acc;
-            }
-        }
-        __syncthreads();
-    }
-}
-
+// 1..4 activation rows: the lane-group kernel (one pass over the weights); 5..8: the
+// matrix-core kernel; more: chunks of 8 (a single leftover row takes the one-row
+// kernel).  Measured on Q8_0 [14336 x 4096]: M = 4 16.9 us (lane groups) vs 20.1 us
+// (matrix cores); M = 8 27.1 us vs 20.1 us.
 void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, size_t m,
                       hipStream_t s) {
     const int nb = static_cast<int>(w.cols / 32);
-    auto go = [&](auto mtag) {
-        constexpr int M = decltype(mtag)::value;
-        const size_t fixed = static_cast<size_t>(M) * nb * (32 + 4);
-        int rw = tile_rows(w.rows);
-        while (rw > 1 && fixed + static_cast<size_t>(M) * rw * nb * 4 > 64 * 1024) rw >>= 1;
-        if (fixed + static_cast<size_t>(M) * rw * nb * 4 > 64 * 1024)
-            fail(LARQL_HIP_ERR_UNSUPPORTED, "q8_matvec: hidden too large for LDS staging");
-        const size_t ntiles = (w.rows + rw - 1) / rw;
-        const size_t target = 2048;
-        const int tiles = static_cast<int>((ntiles + target - 1) / target);
-        const size_t grid = (ntiles + tiles - 1) / tiles;
-        const size_t shmem = fixed + static_cast<size_t>(M) * rw * nb * 4;
-        q8_matvec_kernel<M><<<dim3(grid), dim3(256), shmem, s>>>(
-            reinterpret_cast<const int8_t*>(w.qs), static_cast<const float*>(w.d), q8x, q8s, out,
-            static_cast<int>(w.rows), static_cast<int>(w.cols), rw, tiles);
-    };
-    switch (m) {
-        case 1: go(std::integral_constant<int, 1>{}); break;
-        case 2: go(std::integral_constant<int, 2>{}); break;
-        case 4: go(std::integral_constant<int, 4>{}); break;
-        case 8: go(std::integral_constant<int, 8>{}); break;
-        default: {
-            // Arbitrary M: run in chunks of 8/4/2/1 rows of activations.
-            size_t done = 0;
-            while (done < m) {
-                size_t left = m - done, take = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
-                launch_q8_matvec(w, q8x + done * w.cols, q8s + done * nb, out + done * w.rows, take, s);
-                done += take;
-            }
-            return;
-        }
+    const bool mfma_ok = nb % 2 == 0 && mfma_lds_bytes(nb) <= kLdsLimit && w.rows * w.cols < (size_t{1} << 31);
+    if (m <= 4 || !mfma_ok) {
+        launch_int_mv_batched<LARQL_Q8_0>(w, q8x, q8s, out, m, s);
+        return;
     }
-    LARQL_HIP_CHECK(hipGetLastError());
+    size_t done = 0;
+    while (done < m) {
+        const size_t take = std::min<size_t>(m - done, kMfmaMaxM);
+        if (take == 1)
+            launch_int_mv_batched<LARQL_Q8_0>(w, q8x + done * w.cols, q8s + done * nb, out + done * w.rows, 1, s);
+        else
+            launch_q8_mfma(w, q8x + done * w.cols, q8s + done * nb, out + done * w.rows, static_cast<int>(take), s);
+        done += take;
+    }
 }
 
 }  // namespace larql

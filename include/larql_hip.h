@@ -143,8 +143,10 @@ int larql_hip_quantize_weights(larql_hip_ctx* ctx, int format, const float* x, s
 /* ── device-resident fast path (device pointers; enqueue on `stream`) ──── */
 
 /* One matvec with a registered weight.  For LARQL_Q4_K / LARQL_Q6_K `x` is f32
- * [m][cols] and x_scales is unused (Q4_K with m > 1 runs the prefill GEMM, Q6_K needs m = 1); for LARQL_Q4_0 / LARQL_Q8_0 `x` is int8
- * [m][cols] and x_scales f32 [m][cols/32].  out is f32 [m][rows].
+ * [m][cols] and x_scales is unused (Q4_K with m > 1 runs the prefill GEMM, Q6_K needs
+ * m = 1); for LARQL_Q4_0 / LARQL_Q8_0 `x` is int8 [m][cols] and x_scales f32
+ * [m][cols/32], any m (each output row in the single-row order, bit for bit).
+ * out is f32 [m][rows].
  * stream: a hipStream_t, or NULL for the context stream.  Returns after enqueue. */
 int larql_hip_matvec_dev(larql_hip_ctx* ctx, uint64_t handle, const void* x, const float* x_scales,
                          float* out, size_t m, void* stream);

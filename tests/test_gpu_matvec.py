@@ -164,6 +164,44 @@ def test_q8_matvec_bit_exact(hip, m, rows, cols):
         assert np.array_equal(got[i].view(np.uint32), ref.view(np.uint32)), i
 
 
+@pytest.mark.parametrize("m,rows,cols", [(3, 37, 160), (5, 250, 544), (8, 17, 14336), (2, 1, 32)])
+def test_q8_matvec_ragged_bit_exact(hip, m, rows, cols):
+    """Odd batch sizes (run as 8/4/2/1 chunks), block counts that leave part of the last
+    16-block step empty, row counts off the 16-row tile, and a hidden size whose x image
+    only fits LDS two activation rows at a time."""
+    print(f"[q8 ragged] m={m} rows={rows} cols={cols}", flush=True)
+    w = oracle.gauss(710 + rows, rows * cols, 0.0, 0.02)
+    wq, ws = oracle.quantize_weights_q8(w, rows, cols)
+    xs = [oracle.quantize_to_q8(oracle.gauss(810 + i, cols)) for i in range(m)]
+    got = hip.q8_matvec(wq, ws, np.concatenate([a for a, _ in xs]), np.concatenate([b for _, b in xs]), rows, cols)
+    for i in range(m):
+        ref = oracle.q8_matvec(wq, ws, xs[i][0], xs[i][1], rows, cols)
+        assert np.array_equal(got[i].view(np.uint32), ref.view(np.uint32)), i
+
+
+@pytest.mark.parametrize("m,rows,cols", [(3, 1000, 2560), (8, 33, 160)])
+def test_q4_0_matvec_batched_dev_bit_exact(hip, m, rows, cols):
+    """Q4_0 x Q8 over several activation rows through the device entry point: each row
+    equals the single-row block-integer order."""
+    torch = pytest.importorskip("torch")
+    print(f"[q4_0 batched] m={m} rows={rows} cols={cols}", flush=True)
+    q = weights("q4_0", rows, cols, seed=520 + rows)
+    xs = [oracle.quantize_to_q8(oracle.gauss(620 + i, cols)) for i in range(m)]
+    h = hip.register_weight(larql_hip.Q4_0, q, rows, cols)
+    try:
+        dq = torch.from_numpy(np.concatenate([a for a, _ in xs])).cuda()
+        ds = torch.from_numpy(np.concatenate([b for _, b in xs])).cuda()
+        dy = torch.empty(m * rows, device="cuda", dtype=torch.float32)
+        hip.matvec_dev(h, dq, dy, m=m, x_scales=ds)
+        hip.synchronize()
+        got = dy.cpu().numpy().reshape(m, rows)
+    finally:
+        hip.release_weight(h)
+    for i in range(m):
+        ref = oracle.q4_0_matvec_blockint(q, xs[i][0], xs[i][1], rows, cols)
+        assert np.array_equal(got[i].view(np.uint32), ref.view(np.uint32)), i
+
+
 def test_quantize_to_q8_bit_exact(hip):
     x = oracle.gauss(901, 32 * 1000)
     x[:32] = 0.0                                     # zero block -> scale 0, q 0
