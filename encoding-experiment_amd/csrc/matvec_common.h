@@ -55,6 +55,8 @@ constexpr int DPP_ROW_MIRROR = 0x140;       // lane i <- 15 - i within 16 lanes
 constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i <- 7 - i within 8 lanes
 constexpr int DPP_QUAD_REV = 0x1B;          // quad_perm [3,2,1,0]
 constexpr int DPP_QUAD_SWAP = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_1032 = DPP_QUAD_SWAP;
+constexpr int DPP_QUAD_2301 = 0x4E;         // quad_perm [2,3,0,1]
 
 // Reduce RB per-lane partials (RB <= 8) over the 64 lanes of a wave; on return lane
 // (r << (6 - log2 RB)) holds the total of row r (every lane of that 64/RB block does).

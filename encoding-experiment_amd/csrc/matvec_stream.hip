@@ -7,8 +7,9 @@
 // Shape of the launch (gfx950): a persistent grid of a few 256-thread workgroups per
 // CU.  Each workgroup first builds the fixed-point image of the whole activation
 // (optionally RMS-normalised) in LDS, 112 bytes per 32-element sub-block, while the
-// first weight loads are already in flight.  Each wave owns a contiguous, balanced range of RB-row groups and sweeps them in "units"
-// of one row group x 64 sub-blocks (one per lane).  Units stream through a ring of D
+// first weight loads are already in flight.  Row groups (RB rows) are dealt to the
+// waves grid-strided, and each wave sweeps its groups in "units" of one row group x
+// 64 sub-blocks (one per lane).  Units stream through a ring of D
 // register buffers: the loads of unit u + D - 1 are issued before unit u's arithmetic,
 // so every wave keeps D - 1 units of weight bytes in flight at all times.  Each
 // weight byte is read from HBM once, with wave-contiguous 16-byte loads from a
@@ -36,15 +37,6 @@ struct LvSlot {
     float4 s;
 };
 static_assert(sizeof(LvSlot) == 112, "LDS level slot");
-
-__device__ __forceinline__ void store_slot(LvSlot* dst, const XLevels& L) {
-#pragma unroll
-    for (int l = 0; l < 3; l++) {
-        dst->e[l] = make_uint4(L.ev[l][0], L.ev[l][1], L.ev[l][2], L.ev[l][3]);
-        dst->o[l] = make_uint4(L.od[l][0], L.od[l][1], L.od[l][2], L.od[l][3]);
-    }
-    dst->s = make_float4(L.sp, L.xs, L.xs0, L.xs1);
-}
 
 // Sum of a double over the workgroup (all threads get the total).
 __device__ __forceinline__ double block_sum_d(double v, double* scratch) {
@@ -96,11 +88,44 @@ __device__ __forceinline__ void epilogue_rv(const MvArgs& a, float tot, float rv
     }
 }
 
+// Levels of R x 8-element slices, four lanes (a DPP quad) per 32-element sub-block:
+// slice sl is quarter sl & 3 (elements 8q..8q+7) of sub-block sl >> 2.  The result is
+// bit-identical to make_levels on the whole sub-block: the max is exact, and the sums
+// keep its tree (sum of 8, plus the neighbour's 8 for the half, plus the other half).
+template <int R>
+__device__ __forceinline__ void store_levels_quads(float (&xv)[R][8], int nsl, int nt, LvSlot* lv) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int sl = static_cast<int>(threadIdx.x) + nt * r;
+        float m = tree_max_abs<8>(xv[r]);
+        m = fmaxf(m, dpp_f<DPP_QUAD_1032>(m));
+        m = fmaxf(m, dpp_f<DPP_QUAD_2301>(m));
+        const float sl8 = tree_sum<8>(xv[r]);
+        const float half = sl8 + dpp_f<DPP_QUAD_1032>(sl8);    // elements 0..15 (q < 2) or 16..31
+        const float other = dpp_f<DPP_QUAD_2301>(half);
+        const float inv = m > 0.f ? kLevelScale / m : 0.f;
+        uint32_t T[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) T[k] = __float_as_uint(fmaf(xv[r][k], inv, 12582912.0f)) - 0x4B400000u;
+        if (sl < nsl) {
+            const int q = sl & 3;
+            LvSlot* slot = lv + (sl >> 2);
+#pragma unroll
+            for (int l = 0; l < 3; l++) {
+                reinterpret_cast<uint32_t*>(&slot->e[l])[q] = gather_byte(T[0], T[2], T[4], T[6], 2 - l);
+                reinterpret_cast<uint32_t*>(&slot->o[l])[q] = gather_byte(T[1], T[3], T[5], T[7], 2 - l);
+            }
+            if (q == 0) slot->s = make_float4(m / kLevelScale, half + other, half, other);
+        }
+    }
+}
+
 // Memory-op discipline (what keeps D - 1 units in flight): every global load in the
 // main loop is unconditional and issued in program order (unit indices are clamped in
 // scalar code), and no load is issued whose value is needed before older loads return,
 // so the compiler's waits are vmcnt(N) with N = the loads issued after the one needed.
-template <int FMT, int RB, int D, int NT, int OCC>
+// R = 8-element x slices per thread (4 nsub <= R NT); NORM: fused RMSNorm of x.
+template <int FMT, int RB, int D, int NT, int OCC, int R, bool NORM>
 __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
     extern __shared__ double dyn_lds[];
     double* scratch = dyn_lds;                                    // kMaxWaves doubles
@@ -109,25 +134,32 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nsub = a.cols >> 5;  // <= NT: one sub-block per thread in the prologue
+    const int nsub = a.cols >> 5;
+    const int nsl = 4 * nsub;      // 8-element x slices, <= R * NT
     const int npass = (nsub + 63) >> 6;
     const int S = a.cols >> 8;
     const int gw = blockIdx.x * (NT / 64) + wave;
     const int W = gridDim.x * (NT / 64);
-    // Row groups per wave: contiguous, balanced ranges.  With RB == 1 and the gate/up
-    // pair epilogue, ranges are split on row pairs so a pair never straddles two waves.
+    // Row groups are dealt out grid-strided: wave gw takes super-groups gw, gw + W, ...
+    // (a super-group is `pairs` consecutive RB-row groups; with RB == 1 and the gate/up
+    // pair epilogue a pair never straddles two waves).  At any moment the requests in
+    // flight over the whole GPU then cover one contiguous window of the weights, which
+    // HBM serves far better than one separate stream per wave (measured: 33 MB in
+    // ~7 us instead of ~9 us at the same depth).
     const int pairs = (RB == 1 && a.epi == EPI_SILU_PAIR) ? 2 : 1;
-    const int NG = a.rows_pad / (RB * pairs);
-    const int g0 = static_cast<int>(static_cast<long long>(gw) * NG / W) * pairs;
-    const int g1 = static_cast<int>(static_cast<long long>(gw + 1) * NG / W) * pairs;
-    const int U = (g1 - g0) * npass;  // g0 <= rows_pad / RB - 1 even when the range is empty
+    const int NSG = a.rows_pad / (RB * pairs);
+    const int nsg = gw < NSG ? (NSG - gw + W - 1) / W : 0;
+    const int U = nsg * pairs * npass;
 
-    // 1. x (and the norm weights) of this thread's sub-block: issued first.
-    const int sb = min(static_cast<int>(threadIdx.x), nsub - 1);
-    const bool has_sb = static_cast<int>(threadIdx.x) < nsub;
-    float xv[32], wv[32];
-    load_slice<32>(a.x, sb * 32, true, xv);
-    load_slice<32>(a.norm_w ? a.norm_w : a.x, sb * 32, true, wv);
+    // 1. x (and the norm weights) of this thread's slices: issued first, spread evenly
+    // over the workgroup (two 16-byte loads per slice).
+    float xv[R][8], wv[NORM ? R : 1][8];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int sl = min(static_cast<int>(threadIdx.x) + NT * r, nsl - 1);
+        load_slice<8>(a.x, sl * 8, true, xv[r]);
+        if constexpr (NORM) load_slice<8>(a.norm_w, sl * 8, true, wv[r]);
+    }
 
     // 2. The first D - 1 units.
     const int j = lane & 7;  // sub-block index within its super-block, the same in every pass
@@ -137,8 +169,10 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
     const float* rsrc = a.resid ? a.resid : a.x;
 
     Unit<FMT, RB> buf[D];
-    int lu = 0, lg = g0, lp = 0;  // next unit to load (clamped to the last one)
-    int cg = g0, cp = 0;          // next unit to compute
+    // next unit to load (clamped to the last one; a wave without units loads from a
+    // valid super-group and computes nothing) and next unit to compute
+    int lu = 0, lsg = min(gw, NSG - 1), lgi = 0, lp = 0;
+    int csg = lsg, cgi = 0, cp = 0;
     float acc[RB];
 #pragma unroll
     for (int r = 0; r < RB; r++) acc[r] = 0.f;
@@ -148,7 +182,7 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
         const uint32_t c = static_cast<uint32_t>(min(lp * 64 + lane, nsub - 1));
 #pragma unroll
         for (int r = 0; r < RB; r++) {
-            const size_t row = static_cast<size_t>(lg) * RB + r;
+            const size_t row = static_cast<size_t>(lsg * pairs + lgi) * RB + r;
             if constexpr (FMT == LARQL_Q4_K) {
                 const uint8_t* qrow = a.qs + row * (static_cast<size_t>(a.cols) >> 1);
                 B.r[r].q = *reinterpret_cast<const uint4*>(qrow + c * 16u);
@@ -164,11 +198,14 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
                 B.r[r].sd = s2 | (d << 16);
             }
         }
-        const int rrow = a.resid ? min(lg * RB + (lane >> rsh), a.rows - 1) : 0;
+        const int rrow = a.resid ? min((lsg * pairs + lgi) * RB + (lane >> rsh), a.rows - 1) : 0;
         B.rs = rsrc[rrow];
         if (lu < U - 1) {
             ++lu;
-            if (++lp == npass) { lp = 0; ++lg; }
+            if (++lp == npass) {
+                lp = 0;
+                if (++lgi == pairs) { lgi = 0; lsg += W; }
+            }
         }
     };
 
@@ -176,27 +213,27 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
     for (int d = 0; d < D - 1; d++) load_unit(buf[d]);
 
     // 3. Levels of the (normalised, LI/src/residual.rs:17-33) activation into LDS.
-    if (a.norm_w) {
-        double ss = 0.0;
-        if (has_sb) {
-            double part[4] = {0.0, 0.0, 0.0, 0.0};  // four chains of eight: latency, not order
+    if constexpr (NORM) {
+        double part[2] = {0.0, 0.0};  // two chains: latency, not order
 #pragma unroll
-            for (int k = 0; k < 32; k++) part[k & 3] = fma(static_cast<double>(xv[k]), static_cast<double>(xv[k]), part[k & 3]);
-            ss = (part[0] + part[1]) + (part[2] + part[3]);
+        for (int r = 0; r < R; r++) {
+            if (static_cast<int>(threadIdx.x) + NT * r < nsl) {
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    part[k & 1] = fma(static_cast<double>(xv[r][k]), static_cast<double>(xv[r][k]), part[k & 1]);
+            }
         }
-        const double tot = block_sum_d(ss, scratch);
+        const double tot = block_sum_d(part[0] + part[1], scratch);
         // rms as the CPU path rounds it (LI/src/residual.rs:24); x * (1/rms) differs from
         // x / rms by at most one f32 rounding.
         const float rms = static_cast<float>(sqrt(tot / static_cast<double>(a.cols) + a.eps));
         const float inv_rms = 1.0f / rms;
 #pragma unroll
-        for (int k = 0; k < 32; k++) xv[k] = (xv[k] * inv_rms) * (a.norm_offset + wv[k]);
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int k = 0; k < 8; k++) xv[r][k] = (xv[r][k] * inv_rms) * (a.norm_offset + wv[r][k]);
     }
-    if (has_sb) {
-        XLevels L;
-        make_levels(xv, L);
-        store_slot(lv + sb, L);
-    }
+    store_levels_quads<R>(xv, nsl, NT, lv);
     __syncthreads();
 
     // 4. Stream the units.
@@ -290,6 +327,7 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
             }
         }
         if (++cp == npass) {
+            const int cg = csg * pairs + cgi;
             const float tot = multi_row_reduce<RB>(acc, lane);
             if constexpr (RB == 1) {
                 // single-row groups: the gate row's total waits in a register for its up row
@@ -305,7 +343,7 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
 #pragma unroll
             for (int r = 0; r < RB; r++) acc[r] = 0.f;
             cp = 0;
-            ++cg;
+            if (++cgi == pairs) { cgi = 0; csg += W; }
         }
     };
 
@@ -326,7 +364,20 @@ void launch_stream_t(const DevWeight& w, MvArgs a, hipStream_t s, int wg_per_cu)
     size_t grid = std::min(cus * static_cast<size_t>(wg_per_cu), (ng + NT / 64 - 1) / (NT / 64));
     if (grid == 0) grid = 1;
     const size_t shmem = kMaxWaves * sizeof(double) + (w.cols / 32) * sizeof(LvSlot);
-    kq_stream_kernel<FMT, RB, D, NT, OCC><<<dim3(static_cast<unsigned>(grid)), dim3(NT), shmem, s>>>(a);
+    const size_t nsl = w.cols / 8;
+    const dim3 g(static_cast<unsigned>(grid)), b(NT);
+    const bool norm = a.norm_w != nullptr;
+    if (nsl <= NT) {
+        if (norm) kq_stream_kernel<FMT, RB, D, NT, OCC, 1, true><<<g, b, shmem, s>>>(a);
+        else kq_stream_kernel<FMT, RB, D, NT, OCC, 1, false><<<g, b, shmem, s>>>(a);
+    } else if (nsl <= 2 * NT) {
+        if (norm) kq_stream_kernel<FMT, RB, D, NT, OCC, 2, true><<<g, b, shmem, s>>>(a);
+        else kq_stream_kernel<FMT, RB, D, NT, OCC, 2, false><<<g, b, shmem, s>>>(a);
+    } else {
+        if (nsl > 4 * NT) fail(LARQL_HIP_ERR_UNSUPPORTED, "stream matvec: hidden too large for the workgroup");
+        if (norm) kq_stream_kernel<FMT, RB, D, NT, OCC, 4, true><<<g, b, shmem, s>>>(a);
+        else kq_stream_kernel<FMT, RB, D, NT, OCC, 4, false><<<g, b, shmem, s>>>(a);
+    }
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
@@ -335,7 +386,7 @@ void launch_stream_t(const DevWeight& w, MvArgs a, hipStream_t s, int wg_per_cu)
 // Largest K the streaming kernel takes (LDS holds 112 bytes per 32 columns).
 constexpr size_t kStreamMaxCols = 16384;
 
-static_assert(kStreamMaxCols / 32 <= 512, "prologue: one sub-block per thread of a 512-thread workgroup");
+static_assert(kStreamMaxCols / 8 <= 4 * 512, "prologue: at most four 8-element slices per thread of 512");
 
 // Very tall matrices (a vocabulary head) stream faster through the tiled kernel, whose
 // many small workgroups keep more rows in flight (measured: 128256 x 4096 Q6_K,
@@ -363,9 +414,29 @@ void launch_mv_stream(const DevWeight& w, MvArgs a, hipStream_t s) {
         a.sc = w.sc;
         a.d = static_cast<const uint16_t*>(w.d);
     }
-    // One 512-thread workgroup per CU, two rows per unit, four units in the ring.
-    if (w.format == LARQL_Q4_K) launch_stream_t<LARQL_Q4_K, 2, 4, 512, 2>(w, a, s, 1);
-    else launch_stream_t<LARQL_Q6_K, 2, 4, 512, 2>(w, a, s, 1);
+    // One workgroup per CU, two rows per unit, four units in the ring.  The workgroup
+    // has 8, 7 or 6 waves, whichever deals the row groups out most evenly (every wave
+    // finishes with the last one): e.g. 7168 groups (14336 rows) -> 7 waves per CU,
+    // four groups each; 3072 (a fused Q|K|V of 6144 rows) -> 6 waves, two each.
+    // Measured on Q4_K [14336 x 4096]: 9.2 us with 7 waves vs 9.6 us with 8.
+    const long long ng = static_cast<long long>(w.rows_pad) / 2;  // RB = 2: a group holds a gate/up pair
+    int best_nt = 512;
+    long long best_slots = 0;
+    for (int nt : {512, 448, 384}) {
+        if (w.cols / 8 > static_cast<size_t>(4 * nt)) continue;  // prologue: <= 4 x slices per thread
+        const long long W = static_cast<long long>(a.num_cus) * (nt / 64);
+        const long long slots = (ng + W - 1) / W * W;  // group slots incl. idle ones
+        if (best_slots == 0 || slots < best_slots) best_slots = slots, best_nt = nt;
+    }
+    if (w.format == LARQL_Q4_K) {
+        if (best_nt == 448) launch_stream_t<LARQL_Q4_K, 2, 4, 448, 1>(w, a, s, 1);
+        else if (best_nt == 384) launch_stream_t<LARQL_Q4_K, 2, 4, 384, 1>(w, a, s, 1);
+        else launch_stream_t<LARQL_Q4_K, 2, 4, 512, 2>(w, a, s, 1);
+    } else {
+        if (best_nt == 448) launch_stream_t<LARQL_Q6_K, 2, 4, 448, 1>(w, a, s, 1);
+        else if (best_nt == 384) launch_stream_t<LARQL_Q6_K, 2, 4, 384, 1>(w, a, s, 1);
+        else launch_stream_t<LARQL_Q6_K, 2, 4, 512, 2>(w, a, s, 1);
+    }
 }
 
 }  // namespace larql
