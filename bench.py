@@ -173,7 +173,8 @@ def _time_us(torch, stream, fn, n, warm=5):
 
 def bench_configs(be, torch, stream, copies: int):
     """The other workloads of the path, each at its full single-GPU shape: Q4_0 x Q8
-    [10240x2560]; Q8_0 x Q8 [14336x4096] at M = 1, 4, 8; Q6_K [14336x4096] and
+    [10240x2560]; Q4_0 vecmat [10240x2560] and gate/up pair batch (6 positions);
+    Q8_0 x Q8 [14336x4096] at M = 1, 4, 8; Q6_K [14336x4096] and
     [4096x14336]; gate-KNN over 34 layers [10240x2560] x 256 queries, top-32, f32 and
     Q4_0; Q4_K prefill GEMM 512 x [10240x2560]."""
     import larql_hip
@@ -212,6 +213,33 @@ def bench_configs(be, torch, stream, copies: int):
     for h in hs:
         be.release_weight(h)
     del w, raw
+
+    # Q4_0 walk FFN at [10240 x 2560]: vecmat (down, act [10240] -> out [2560]) and the
+    # gate/up pair batch over 6 positions (the reference's profile shape)
+    N, K = 10240, 2560
+    hs = []
+    for c in range(copies):
+        w = rnd(N, K, seed=60 + c % 2, std=0.02)
+        raw = torch.empty(N * K // 32 * 18, dtype=torch.uint8, device=dev)
+        be.quantize_weights_dev(larql_hip.Q4_0, w, N * K, raw, stream=stream)
+        torch.cuda.synchronize()
+        hs.append(be.register_weight_device(larql_hip.Q4_0, raw, raw.numel(), N, K))
+        del w, raw
+    act = rnd(N, seed=62)
+    y = torch.empty(K, device=dev)
+    us = _time_us(torch, stream, lambda i: be.vecmat_dev(hs[i % copies], act, y, stream=stream), 200)
+    hbm("q4_0_vecmat_10240x2560", N * K // 32 * 18 + N * 4 + K * 4, us,
+        {"note": "reference published: CPU 1.35 ms, Metal 1.84 ms on M3 Max (LC/PERFORMANCE.md:60)"})
+    seq = 6
+    xs6 = rnd(seq, K, seed=63)
+    g6 = torch.empty(seq * N, device=dev)
+    u6 = torch.empty(seq * N, device=dev)
+    us = _time_us(torch, stream,
+                  lambda i: be.pair_batch_dev(hs[i % copies], hs[(i + 1) % copies], xs6, seq, g6, u6, stream=stream), 200)
+    hbm("q4_0_pair_batch_6x10240x2560", 2 * (N * K // 32 * 18) + seq * K * 4 + 2 * seq * N * 4, us,
+        {"launches": 3, "note": "quantize 6 rows + gate and up Q4_0 matvecs over all 6 rows (one pass each)"})
+    for h in hs:
+        be.release_weight(h)
 
     # Q8_0 x Q8, [14336 x 4096], M in {1, 4, 8}
     N, K = 14336, 4096

@@ -208,7 +208,8 @@ extern "C" void larql_hip_ctx_destroy(larql_hip_ctx* c) {
         } catch (...) {
         }
         for (auto* b : {&c->stage_in, &c->stage_in2, &c->stage_out, &c->stage_raw, &c->scratch, &c->knn_scores,
-                        &c->knn_q8, &c->knn_q8s, &c->knn_idx, &c->knn_val, &c->knn_handles})
+                        &c->knn_q8, &c->knn_q8s, &c->knn_idx, &c->knn_val, &c->knn_handles, &c->vecmat_part,
+                        &c->pair_q8, &c->pair_q8s})
             if (b->p) (void)hipFree(b->p);
         (void)hipStreamDestroy(c->stream);
     }
@@ -321,6 +322,77 @@ extern "C" int larql_hip_q4_matvec(larql_hip_ctx* c, const uint8_t* q4_data, siz
         float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, num_rows * sizeof(float)));
         larql::launch_q4_0_matvec(w, dq, ds, dout, 1, c->stream);
         download(c, scores, dout, num_rows * sizeof(float));
+    });
+}
+
+// ── Q4_0 walk-FFN: vecmat and gate/up pair batch ────────────────────────
+static void run_vecmat(larql_hip_ctx* c, const DevWeight& w, const float* act, float* out, hipStream_t s) {
+    const size_t chunks = larql::q4_vecmat_chunks(w.rows, w.cols);
+    float* part = static_cast<float*>(larql::ensure(c, c->vecmat_part, chunks * w.cols * sizeof(float)));
+    larql::launch_q4_vecmat(w, act, out, part, chunks, s);
+}
+
+extern "C" int larql_hip_q4_vecmat(larql_hip_ctx* c, const float* activation, const uint8_t* q4_data, size_t q4_len,
+                                   float* out, size_t intermediate, size_t hidden) {
+    return guarded(c, [&] {
+        if (!activation || !q4_data || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        const DevWeight& w = larql::cached_weight(c, LARQL_Q4_0, q4_data, q4_len, nullptr, intermediate, hidden);
+        const float* da = stage_upload(c, c->stage_in, activation, intermediate);
+        float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, hidden * sizeof(float)));
+        run_vecmat(c, w, da, dout, c->stream);
+        download(c, out, dout, hidden * sizeof(float));
+    });
+}
+
+extern "C" int larql_hip_vecmat_dev(larql_hip_ctx* c, uint64_t handle, const float* activation, float* out,
+                                    void* stream) {
+    return guarded(c, [&] {
+        if (!activation || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        const DevWeight& w = larql::lookup(c, handle);
+        if (w.format != LARQL_Q4_0) fail(LARQL_HIP_ERR_UNSUPPORTED, "vecmat: Q4_0 weights only");
+        run_vecmat(c, w, activation, out, pick_stream(c, stream));
+    });
+}
+
+static void run_pair_batch(larql_hip_ctx* c, const DevWeight& g, const DevWeight& u, const float* x, size_t seq,
+                           float* gate_out, float* up_out, hipStream_t s) {
+    if (g.format != LARQL_Q4_0 || u.format != LARQL_Q4_0) fail(LARQL_HIP_ERR_UNSUPPORTED, "pair batch: Q4_0 weights");
+    if (g.rows != u.rows || g.cols != u.cols) fail(LARQL_HIP_ERR_INVALID, "pair batch: gate and up shapes differ");
+    if (seq == 0) return;
+    const size_t hidden = g.cols;
+    int8_t* q8 = static_cast<int8_t*>(larql::ensure(c, c->pair_q8, seq * hidden));
+    float* q8s = static_cast<float*>(larql::ensure(c, c->pair_q8s, seq * (hidden / 32) * sizeof(float)));
+    larql::launch_quantize_q8(x, hidden, seq, q8, q8s, s);
+    larql::launch_q4_0_matvec(g, q8, q8s, gate_out, seq, s);
+    larql::launch_q4_0_matvec(u, q8, q8s, up_out, seq, s);
+}
+
+extern "C" int larql_hip_q4_matvec_pair_batch(larql_hip_ctx* c, const uint8_t* gate_q4, size_t gate_len,
+                                              const uint8_t* up_q4, size_t up_len, const float* x_matrix,
+                                              size_t seq_len, float* gate_out, float* up_out, size_t num_rows,
+                                              size_t hidden) {
+    return guarded(c, [&] {
+        if (!gate_q4 || !up_q4 || !x_matrix || !gate_out || !up_out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        if (seq_len == 0) return;
+        // copies: the second lookup may insert into the registry
+        const DevWeight g = larql::cached_weight(c, LARQL_Q4_0, gate_q4, gate_len, nullptr, num_rows, hidden);
+        const DevWeight u = larql::cached_weight(c, LARQL_Q4_0, up_q4, up_len, nullptr, num_rows, hidden);
+        const float* dx = stage_upload(c, c->stage_in, x_matrix, seq_len * hidden);
+        float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, 2 * seq_len * num_rows * sizeof(float)));
+        run_pair_batch(c, g, u, dx, seq_len, dout, dout + seq_len * num_rows, c->stream);
+        LARQL_HIP_CHECK(hipMemcpyAsync(gate_out, dout, seq_len * num_rows * sizeof(float), hipMemcpyDeviceToHost,
+                                       c->stream));
+        download(c, up_out, dout + seq_len * num_rows, seq_len * num_rows * sizeof(float));
+    });
+}
+
+extern "C" int larql_hip_pair_batch_dev(larql_hip_ctx* c, uint64_t gate, uint64_t up, const float* x, size_t seq_len,
+                                        float* gate_out, float* up_out, void* stream) {
+    return guarded(c, [&] {
+        if (!x || !gate_out || !up_out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        const DevWeight g = larql::lookup(c, gate);
+        const DevWeight u = larql::lookup(c, up);
+        run_pair_batch(c, g, u, x, seq_len, gate_out, up_out, pick_stream(c, stream));
     });
 }
 

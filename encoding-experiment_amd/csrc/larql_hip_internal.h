@@ -136,6 +136,8 @@ struct larql_hip_ctx {
     larql::DeviceBuf stage_in, stage_in2, stage_out, stage_raw, scratch;
     // gate-KNN work buffers: scores [layers][nq][features], quantized queries
     larql::DeviceBuf knn_scores, knn_q8, knn_q8s, knn_idx, knn_val, knn_handles;
+    // q4_vecmat chunk partials; pair-batch quantized activations
+    larql::DeviceBuf vecmat_part, pair_q8, pair_q8s;
     larql::KVCache kv;
     // model built by the last host-pointer decode_token (re-used while its key matches)
     larql_hip_model* trait_model = nullptr;
@@ -163,6 +165,10 @@ void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s,
 void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
                       size_t m, hipStream_t s);
 void launch_quantize_q8(const float* x, size_t n, size_t m, int8_t* q8, float* scales, hipStream_t s);
+// q4_vecmat: chunks of rows per partial (q4_vecmat_chunks) and the two-pass launch;
+// part holds chunks x cols floats.
+size_t q4_vecmat_chunks(size_t inter, size_t hidden);
+void launch_q4_vecmat(const DevWeight& w, const float* act, float* out, float* part, size_t chunks, hipStream_t s);
 void launch_quantize_weights(int format, const float* x, size_t n, void* out, float* q8_scales, hipStream_t s);
 
 }  // namespace larql

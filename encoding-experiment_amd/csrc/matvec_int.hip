@@ -190,14 +190,15 @@ constexpr size_t x_lds_bytes(int m, int nb) {
     return static_cast<size_t>(m) * nb * (32 + Blk<FMT>::kXAux * 4);
 }
 
-// Grid: one workgroup per 256 / G rows.  x: M activation rows of Q8 values (cols int8
-// each) and their scales (nb each); out: M rows of `rows` floats.
+// Grid: one workgroup per 256 / G rows.  x: m <= M activation rows of Q8 values (cols
+// int8 each) and their scales (nb each); out: m rows of `rows` floats.  Rows m..M-1 of
+// the x image are left unset: their sums are formed and discarded.
 template <int FMT, int M, int G, int D>
 __global__ __launch_bounds__(kThreads) void int_mv_kernel(const uint8_t* __restrict__ qs,
                                                           const void* __restrict__ dsc,
                                                           const int8_t* __restrict__ xq,
                                                           const float* __restrict__ xsc,
-                                                          float* __restrict__ out, int rows, int nb) {
+                                                          float* __restrict__ out, int rows, int nb, int m) {
     using B = Blk<FMT>;
     // x image: first and second 16 bytes of every block in separate arrays, so the 16
     // lanes of a group read 256 contiguous bytes (no bank conflicts)
@@ -209,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void int_mv_kernel(const uint8_t* __restr
     const int row = blockIdx.x * (kThreads / G) + threadIdx.x / G;
     const size_t base = static_cast<size_t>(min(row, rows - 1)) * nb;
     const int steps = (nb + G - 1) / G;
-    const int nx = M * nb;
+    const int nx = m * nb;
 
     // x loads first (the staging wait then covers them only), kXBatch blocks per thread
     // in flight together, then the first D steps of weights, which stay in flight
@@ -271,7 +272,8 @@ __global__ __launch_bounds__(kThreads) void int_mv_kernel(const uint8_t* __restr
 
     if (j == 0 && row < rows) {
 #pragma unroll
-        for (int mi = 0; mi < M; mi++) out[static_cast<size_t>(mi) * rows + row] = acc[mi];
+        for (int mi = 0; mi < M; mi++)
+            if (mi < m) out[static_cast<size_t>(mi) * rows + row] = acc[mi];
     }
 }
 
@@ -461,12 +463,12 @@ void launch_q8_mfma(const DevWeight& w, const int8_t* q8x, const float* q8s, flo
 constexpr size_t kLdsLimit = 64 * 1024;
 
 template <int FMT, int M, int G, int D>
-void launch_int_mv_g(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, hipStream_t s) {
+void launch_int_mv_g(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s) {
     const int nb = static_cast<int>(w.cols / 32);
     const size_t rows_per_wg = kThreads / G;
     const size_t grid = (w.rows + rows_per_wg - 1) / rows_per_wg;
     int_mv_kernel<FMT, M, G, D><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), x_lds_bytes<FMT>(M, nb), s>>>(
-        w.qs, w.d, q8x, q8s, out, static_cast<int>(w.rows), nb);
+        w.qs, w.d, q8x, q8s, out, static_cast<int>(w.rows), nb, m);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
@@ -475,14 +477,16 @@ void launch_int_mv_g(const DevWeight& w, const int8_t* q8x, const float* q8s, fl
 // Q8_0 [14336 x 4096]: 16.1 us (G = 4) vs 17.2 us (G = 16); on Q4_0 [10240 x 2560]:
 // 5.2 us (G = 16) vs 5.3 us (G = 4).
 template <int FMT, int M>
-void launch_int_mv(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, hipStream_t s) {
+void launch_int_mv(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s) {
     if ((w.rows + 63) / 64 * 4 >= static_cast<size_t>(current_device_cus()) * 3)
-        launch_int_mv_g<FMT, M, 4, 4>(w, q8x, q8s, out, s);
+        launch_int_mv_g<FMT, M, 4, 4>(w, q8x, q8s, out, m, s);
     else
-        launch_int_mv_g<FMT, M, 16, 4>(w, q8x, q8s, out, s);
+        launch_int_mv_g<FMT, M, 16, 4>(w, q8x, q8s, out, m, s);
 }
 
-// M activation rows in chunks of 8/4/2/1, each chunk as large as the LDS image allows.
+// M activation rows in passes of up to 8 (one pass over the weights per pass): each pass
+// takes the kernel with 1, 2, 4 or 8 x rows that holds the rows left, or the largest
+// whose x image fits LDS.
 template <int FMT>
 void launch_int_mv_batched(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, size_t m,
                            hipStream_t s) {
@@ -491,17 +495,20 @@ void launch_int_mv_batched(const DevWeight& w, const int8_t* q8x, const float* q
     size_t done = 0;
     while (done < m) {
         const size_t left = m - done;
-        int take = 1;
+        int cap = 1;  // the largest kernel whose x image fits
         for (int c : {8, 4, 2})
-            if (left >= static_cast<size_t>(c) && x_lds_bytes<FMT>(c, nb) <= kLdsLimit) { take = c; break; }
+            if (x_lds_bytes<FMT>(c, nb) <= kLdsLimit) { cap = c; break; }
+        int kern = 1;
+        while (kern < cap && static_cast<size_t>(kern) < left) kern *= 2;
+        const int take = static_cast<int>(std::min<size_t>(left, kern));
         const int8_t* xq = q8x + done * w.cols;
         const float* xs = q8s + done * nb;
         float* o = out + done * w.rows;
-        switch (take) {
-            case 8: launch_int_mv<FMT, 8>(w, xq, xs, o, s); break;
-            case 4: launch_int_mv<FMT, 4>(w, xq, xs, o, s); break;
-            case 2: launch_int_mv<FMT, 2>(w, xq, xs, o, s); break;
-            default: launch_int_mv<FMT, 1>(w, xq, xs, o, s); break;
+        switch (kern) {
+            case 8: launch_int_mv<FMT, 8>(w, xq, xs, o, take, s); break;
+            case 4: launch_int_mv<FMT, 4>(w, xq, xs, o, take, s); break;
+            case 2: launch_int_mv<FMT, 2>(w, xq, xs, o, take, s); break;
+            default: launch_int_mv<FMT, 1>(w, xq, xs, o, take, s); break;
         }
         done += take;
     }

@@ -57,6 +57,10 @@ SIGNATURES = {
     "larql_hip_forget_host": (_I, [_P, _P]),
     "larql_hip_weight_device_bytes": (_I, [_P, _U64, ctypes.POINTER(_SZ)]),
     "larql_hip_q4_matvec": (_I, [_P, _P, _SZ, _P, _P, _P, _SZ, _SZ]),
+    "larql_hip_q4_vecmat": (_I, [_P, _P, _P, _SZ, _P, _SZ, _SZ]),
+    "larql_hip_q4_matvec_pair_batch": (_I, [_P, _P, _SZ, _P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ]),
+    "larql_hip_vecmat_dev": (_I, [_P, _U64, _P, _P, _P]),
+    "larql_hip_pair_batch_dev": (_I, [_P, _U64, _U64, _P, _SZ, _P, _P, _P]),
     "larql_hip_q4k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
     "larql_hip_q6k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
     "larql_hip_q4k_matmul": (_I, [_P, _P, _SZ, _P, _SZ, _P, _SZ, _SZ]),
@@ -316,6 +320,26 @@ class HipBackend:
         rc = self._lib.larql_hip_q4_matvec(self._ctx, q4p, q4.size, qxp, qsp, out.ctypes.data_as(_P), num_rows, hidden)
         return out if self._ok(rc) else None
 
+    def q4_vecmat(self, activation, q4_data, intermediate: int, hidden: int):
+        """backend.rs:56-60 — out[hidden] = activation[intermediate] @ Q4_0[intermediate, hidden]."""
+        a, ap = _arr(activation, np.float32)
+        q4, q4p = _arr(q4_data, np.uint8)
+        out = np.empty(hidden, dtype=np.float32)
+        rc = self._lib.larql_hip_q4_vecmat(self._ctx, ap, q4p, q4.size, out.ctypes.data_as(_P), intermediate, hidden)
+        return out if self._ok(rc) else None
+
+    def q4_matvec_pair_batch(self, gate_q4, up_q4, x_matrix, seq_len: int, num_rows: int, hidden: int):
+        """backend.rs:64-69 — per position: quantize_to_q8, then gate and up Q4_0 matvecs.
+        Returns (gate [seq_len, num_rows], up [seq_len, num_rows])."""
+        g, gp = _arr(gate_q4, np.uint8)
+        u, up = _arr(up_q4, np.uint8)
+        x, xp = _arr(x_matrix, np.float32)
+        go = np.empty((seq_len, num_rows), dtype=np.float32)
+        uo = np.empty((seq_len, num_rows), dtype=np.float32)
+        rc = self._lib.larql_hip_q4_matvec_pair_batch(self._ctx, gp, g.size, up, u.size, xp, seq_len,
+                                                      go.ctypes.data_as(_P), uo.ctypes.data_as(_P), num_rows, hidden)
+        return (go, uo) if self._ok(rc) else None
+
     def q4k_matvec(self, q4k_data, x, num_rows: int, hidden: int):
         """backend.rs:126-130 — scores[N] = Q4_K[N,K] @ f32_x[K]."""
         q, qp = _arr(q4k_data, np.uint8)
@@ -448,6 +472,14 @@ class HipBackend:
     def _handle_array(handles):
         arr = (_U64 * len(handles))(*handles)
         return arr, ctypes.cast(arr, _P)
+
+    def vecmat_dev(self, handle: int, activation, out, stream=None):
+        self._check(self._lib.larql_hip_vecmat_dev(self._ctx, handle, _dptr(activation), _dptr(out),
+                                                   _stream_ptr(stream)))
+
+    def pair_batch_dev(self, gate: int, up: int, x, seq_len: int, gate_out, up_out, stream=None):
+        self._check(self._lib.larql_hip_pair_batch_dev(self._ctx, gate, up, _dptr(x), seq_len, _dptr(gate_out),
+                                                       _dptr(up_out), _stream_ptr(stream)))
 
     def gate_knn_dev(self, handles, queries, nq: int, top_k: int, idx, scores, stream=None):
         arr, ap = self._handle_array(handles)

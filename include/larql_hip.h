@@ -104,6 +104,23 @@ int larql_hip_weight_device_bytes(larql_hip_ctx* ctx, uint64_t handle, size_t* b
 int larql_hip_q4_matvec(larql_hip_ctx* ctx, const uint8_t* q4_data, size_t q4_len, const int8_t* q8_x,
                         const float* q8_scales, float* scores, size_t num_rows, size_t hidden);
 
+/* ComputeBackend::q4_vecmat — LC/src/backend.rs:56-60 (CPU: LC/src/cpu/ops/q4_vecmat.rs:8-18 ->
+ * LC/csrc/q4_dot.c:201-232).  out[hidden] = activation[intermediate] . deq(Q4_0[intermediate, hidden]);
+ * rows whose activation lies in (-1e-10, 1e-10) are skipped and each term is
+ * (float)(nib - 8) * (f16(d) * act), as in the reference.  The rows are summed in chunks
+ * (deterministic) rather than in one serial chain per column: results agree with the
+ * reference to f32 rounding, not bit for bit. */
+int larql_hip_q4_vecmat(larql_hip_ctx* ctx, const float* activation, const uint8_t* q4_data, size_t q4_len,
+                        float* out, size_t intermediate, size_t hidden);
+
+/* ComputeBackend::q4_matvec_pair_batch — LC/src/backend.rs:64-69 (Metal LC/src/metal/ops/q4_batched.rs:19-80):
+ * for each of the seq_len rows x_s of x_matrix [seq_len][hidden], q = quantize_to_q8(x_s),
+ * gate_out[s] = q4_matvec(gate, q), up_out[s] = q4_matvec(up, q); bit-exact with
+ * larql_hip_q4_matvec.  gate_out and up_out are [seq_len][num_rows]. */
+int larql_hip_q4_matvec_pair_batch(larql_hip_ctx* ctx, const uint8_t* gate_q4, size_t gate_len, const uint8_t* up_q4,
+                                   size_t up_len, const float* x_matrix, size_t seq_len, float* gate_out,
+                                   float* up_out, size_t num_rows, size_t hidden);
+
 /* ComputeBackend::q4k_matvec — LC/src/backend.rs:126-130 (CPU: LC/src/cpu/ops/q4k_matvec.rs:31-90). */
 int larql_hip_q4k_matvec(larql_hip_ctx* ctx, const uint8_t* q4k_data, size_t q4k_len, const float* x,
                          float* out, size_t num_rows, size_t hidden);
@@ -150,6 +167,17 @@ int larql_hip_quantize_weights(larql_hip_ctx* ctx, int format, const float* x, s
  * stream: a hipStream_t, or NULL for the context stream.  Returns after enqueue. */
 int larql_hip_matvec_dev(larql_hip_ctx* ctx, uint64_t handle, const void* x, const float* x_scales,
                          float* out, size_t m, void* stream);
+
+/* q4_vecmat with a registered Q4_0 weight (rows = intermediate, cols = hidden), device
+ * activation f32 [rows] and output f32 [cols].  Uses a partials buffer owned by the
+ * context: device calls on one context must not overlap on different streams. */
+int larql_hip_vecmat_dev(larql_hip_ctx* ctx, uint64_t handle, const float* activation, float* out, void* stream);
+
+/* q4_matvec_pair_batch with registered Q4_0 gate and up weights of equal shape: x f32
+ * [seq_len][cols] (device), gate_out / up_out f32 [seq_len][rows] (device).  Quantizes x
+ * into a context-owned buffer (same overlap rule as larql_hip_vecmat_dev). */
+int larql_hip_pair_batch_dev(larql_hip_ctx* ctx, uint64_t gate, uint64_t up, const float* x, size_t seq_len,
+                             float* gate_out, float* up_out, void* stream);
 
 /* quantize_to_q8 on device memory, m rows of n floats. */
 int larql_hip_quantize_to_q8_dev(larql_hip_ctx* ctx, const float* x, size_t n, size_t m, int8_t* q8,

@@ -1,0 +1,153 @@
+"""GPU parity of the Q4_0 walk-FFN pair: q4_vecmat (LC/src/backend.rs:56-60 ->
+LC/csrc/q4_dot.c:201-232) and q4_matvec_pair_batch (backend.rs:64-69, Metal
+LC/src/metal/ops/q4_batched.rs:19-80), as the vindex walk FFN calls them
+(LI/src/vindex/walk_ffn.rs:233-330).
+
+Bars:
+  * vecmat: max|gpu - cpu| / max|cpu| <= 1e-3 against the oracle's x86 order (the
+    reference sums each column over the rows in one serial chain; the kernel sums row
+    chunks and adds the chunk totals in order, so only f32 rounding differs — measured
+    ~1e-7).  The skip of rows with |act| < 1e-10 is checked with rows whose weights
+    would dominate the result if they were not skipped.
+  * pair batch: BIT-EXACT with quantize_to_q8 + the block-integer Q4_0 matvec per row.
+"""
+import numpy as np
+import pytest
+
+import larql_hip
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+def rel_err(got, ref):
+    return float(np.max(np.abs(got.astype(np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+@pytest.mark.parametrize("inter,hidden", [(10240, 2560), (1, 32), (7, 64), (300, 544), (14336, 4096), (4099, 1056)])
+def test_q4_vecmat_matches_oracle(hip, inter, hidden):
+    print(f"[vecmat] inter={inter} hidden={hidden}", flush=True)
+    q4 = oracle.quantize_q4_0(oracle.gauss(900 + inter, inter * hidden, 0.0, 0.02))
+    act = oracle.gauss(901 + hidden, inter)
+    act[::5] = 0.0                      # the walk FFN's activations are mostly zero
+    got = hip.q4_vecmat(act, q4, inter, hidden)
+    ref = oracle.q4_0_vecmat(act, q4, inter, hidden)
+    e = rel_err(got, ref)
+    print(f"  rel_err {e:.2e}", flush=True)
+    assert e <= REL_TOL, e
+    # the reference's own C kernel, where it was built, agrees with the oracle exactly
+    r2 = oracle.ref_q4_0_vecmat(act, q4, inter, hidden)
+    if r2 is not None:
+        assert np.array_equal(r2.view(np.uint32), ref.view(np.uint32))
+
+
+def test_q4_vecmat_skips_tiny_activations(hip):
+    """Rows with |act| just below 1e-10 carry scales of 6e4 (f16 max): if they were added,
+    they would outweigh every other row by ~1e4."""
+    inter, hidden = 1000, 256
+    rng = np.random.default_rng(7)
+    q4 = oracle.quantize_q4_0(oracle.gauss(17, inter * hidden, 0.0, 0.02))
+    blocks = q4.reshape(inter, hidden // 32, 18)
+    act = oracle.gauss(18, inter)
+    tiny = rng.choice(inter, 50, replace=False)
+    act[tiny[:25]] = 9.9e-11
+    act[tiny[25:]] = -9.9e-11
+    blocks[tiny, :, 0:2] = np.frombuffer(np.float16(65504.0).tobytes(), np.uint8)
+    blocks[tiny, :, 2:] = 0xFF
+    act[3] = 1.0001e-10               # just outside the band: kept
+    got = hip.q4_vecmat(act, q4, inter, hidden)
+    ref = oracle.q4_0_vecmat(act, q4, inter, hidden)
+    assert rel_err(got, ref) <= REL_TOL
+    # and the big rows really are absent from both
+    assert np.max(np.abs(ref)) < 100.0
+
+
+def test_q4_vecmat_all_zero_activation(hip):
+    inter, hidden = 64, 128
+    q4 = oracle.quantize_q4_0(oracle.gauss(19, inter * hidden))
+    got = hip.q4_vecmat(np.zeros(inter, np.float32), q4, inter, hidden)
+    assert np.array_equal(got, np.zeros(hidden, np.float32))
+
+
+def test_q4_vecmat_fuzzed_bytes(hip):
+    inter, hidden = 777, 1024
+    rng = np.random.default_rng(23)
+    q4 = rng.integers(0, 256, inter * hidden // 32 * 18, dtype=np.uint8)
+    blocks = q4.reshape(-1, 18)
+    blocks[:, 0:2] = np.frombuffer(rng.uniform(-0.05, 0.05, blocks.shape[0]).astype(np.float16).tobytes(),
+                                   np.uint8).reshape(-1, 2)
+    act = oracle.gauss(24, inter)
+    got = hip.q4_vecmat(act, q4, inter, hidden)
+    ref = oracle.q4_0_vecmat(act, q4, inter, hidden)
+    assert rel_err(got, ref) <= REL_TOL
+
+
+def test_vecmat_dev_matches_host_entry(hip):
+    torch = pytest.importorskip("torch")
+    inter, hidden = 10240, 2560
+    q4 = oracle.quantize_q4_0(oracle.gauss(31, inter * hidden, 0.0, 0.02))
+    act = oracle.gauss(32, inter)
+    h = hip.register_weight(larql_hip.Q4_0, q4, inter, hidden)
+    try:
+        da = torch.from_numpy(act).cuda()
+        do = torch.empty(hidden, device="cuda", dtype=torch.float32)
+        hip.vecmat_dev(h, da, do)
+        hip.synchronize()
+        dev = do.cpu().numpy()
+    finally:
+        hip.release_weight(h)
+    host = hip.q4_vecmat(act, q4, inter, hidden)
+    assert np.array_equal(dev.view(np.uint32), host.view(np.uint32))   # same kernels, same order
+
+
+@pytest.mark.parametrize("seq,rows,hidden", [(6, 10240, 2560), (1, 64, 32), (9, 300, 544)])
+def test_pair_batch_bit_exact(hip, seq, rows, hidden):
+    print(f"[pair batch] seq={seq} rows={rows} hidden={hidden}", flush=True)
+    gate = oracle.quantize_q4_0(oracle.gauss(41 + seq, rows * hidden, 0.0, 0.02))
+    up = oracle.quantize_q4_0(oracle.gauss(42 + seq, rows * hidden, 0.0, 0.02))
+    x = oracle.gauss(43, seq * hidden).reshape(seq, hidden)
+    g, u = hip.q4_matvec_pair_batch(gate, up, x, seq, rows, hidden)
+    for s in range(seq):
+        q8, q8s = oracle.quantize_to_q8(x[s])
+        rg = oracle.q4_0_matvec_blockint(gate, q8, q8s, rows, hidden)
+        ru = oracle.q4_0_matvec_blockint(up, q8, q8s, rows, hidden)
+        assert np.array_equal(g[s].view(np.uint32), rg.view(np.uint32)), s
+        assert np.array_equal(u[s].view(np.uint32), ru.view(np.uint32)), s
+
+
+def test_pair_batch_dev(hip):
+    torch = pytest.importorskip("torch")
+    seq, rows, hidden = 4, 2048, 1024
+    gate = oracle.quantize_q4_0(oracle.gauss(51, rows * hidden, 0.0, 0.02))
+    up = oracle.quantize_q4_0(oracle.gauss(52, rows * hidden, 0.0, 0.02))
+    x = oracle.gauss(53, seq * hidden).reshape(seq, hidden)
+    hg = hip.register_weight(larql_hip.Q4_0, gate, rows, hidden)
+    hu = hip.register_weight(larql_hip.Q4_0, up, rows, hidden)
+    try:
+        dx = torch.from_numpy(x).cuda()
+        dg = torch.empty(seq * rows, device="cuda", dtype=torch.float32)
+        du = torch.empty(seq * rows, device="cuda", dtype=torch.float32)
+        hip.pair_batch_dev(hg, hu, dx, seq, dg, du)
+        hip.synchronize()
+        g = dg.cpu().numpy().reshape(seq, rows)
+        u = du.cpu().numpy().reshape(seq, rows)
+    finally:
+        hip.release_weight(hg)
+        hip.release_weight(hu)
+    for s in range(seq):
+        q8, q8s = oracle.quantize_to_q8(x[s])
+        assert np.array_equal(g[s].view(np.uint32), oracle.q4_0_matvec_blockint(gate, q8, q8s, rows, hidden).view(np.uint32))
+        assert np.array_equal(u[s].view(np.uint32), oracle.q4_0_matvec_blockint(up, q8, q8s, rows, hidden).view(np.uint32))
+
+
+def test_pair_batch_shape_mismatch_is_an_error():
+    be = larql_hip.HipBackend(0, strict=False)
+    try:
+        g = oracle.quantize_q4_0(oracle.gauss(1, 64 * 64))
+        u = oracle.quantize_q4_0(oracle.gauss(2, 32 * 64))
+        x = np.zeros((1, 64), np.float32)
+        assert be.q4_matvec_pair_batch(g, u, x, 1, 64, 64) is None   # up is too short for 64 rows
+    finally:
+        be.close()
