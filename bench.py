@@ -171,6 +171,30 @@ def _time_us(torch, stream, fn, n, warm=5):
     return time_launches(torch, stream, fn, n) * 1e3 / n
 
 
+def _graph_us(torch, stream, fn, n, reps=10, warm=5):
+    """Per-call device time of an entry point that launches several kernels: n calls are
+    captured into one HIP graph (every device buffer is allocated by the warm-up calls,
+    so the capture holds only kernel launches) and replayed `reps` times.  A Python loop
+    of such calls measures the interpreter, not the GPU."""
+    for i in range(warm):
+        fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(n):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * n)
+
+
 def bench_configs(be, torch, stream, copies: int):
     """The other workloads of the path, each at its full single-GPU shape: Q4_0 x Q8
     [10240x2560]; Q4_0 vecmat [10240x2560] and gate/up pair batch (6 positions);
@@ -227,17 +251,19 @@ def bench_configs(be, torch, stream, copies: int):
         del w, raw
     act = rnd(N, seed=62)
     y = torch.empty(K, device=dev)
-    us = _time_us(torch, stream, lambda i: be.vecmat_dev(hs[i % copies], act, y, stream=stream), 200)
+    us = _graph_us(torch, stream, lambda i: be.vecmat_dev(hs[i % copies], act, y, stream=stream), 64)
     hbm("q4_0_vecmat_10240x2560", N * K // 32 * 18 + N * 4 + K * 4, us,
-        {"note": "reference published: CPU 1.35 ms, Metal 1.84 ms on M3 Max (LC/PERFORMANCE.md:60)"})
+        {"launches": 2, "timing": "HIP graph replay of 64 calls",
+         "note": "reference published: CPU 1.35 ms, Metal 1.84 ms on M3 Max (LC/PERFORMANCE.md:60)"})
     seq = 6
     xs6 = rnd(seq, K, seed=63)
     g6 = torch.empty(seq * N, device=dev)
     u6 = torch.empty(seq * N, device=dev)
-    us = _time_us(torch, stream,
-                  lambda i: be.pair_batch_dev(hs[i % copies], hs[(i + 1) % copies], xs6, seq, g6, u6, stream=stream), 200)
+    us = _graph_us(torch, stream,
+                   lambda i: be.pair_batch_dev(hs[i % copies], hs[(i + 1) % copies], xs6, seq, g6, u6, stream=stream), 64)
     hbm("q4_0_pair_batch_6x10240x2560", 2 * (N * K // 32 * 18) + seq * K * 4 + 2 * seq * N * 4, us,
-        {"launches": 3, "note": "quantize 6 rows + gate and up Q4_0 matvecs over all 6 rows (one pass each)"})
+        {"launches": 3, "timing": "HIP graph replay of 64 calls",
+         "note": "quantize 6 rows + gate and up Q4_0 matvecs over all 6 rows (one pass each)"})
     for h in hs:
         be.release_weight(h)
 

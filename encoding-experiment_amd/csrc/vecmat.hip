@@ -8,15 +8,16 @@
 // one long serial chain per column (and its ARM build contracts the add into an fma,
 // so its two builds already disagree in the last bits); here the rows are summed in
 // chunks — sequentially within a wave, the four waves of a workgroup in order, then
-// the chunk partials in order — so the result is deterministic and within f32
-// rounding of the reference (the bar is relative, 1e-3).
+// the chunk partials in a fixed grouping — so the result is deterministic and within
+// f32 rounding of the reference (the bar is relative, 1e-3).
 //
 // Pass 1 (q4_vecmat_part_kernel): workgroup (tile, chunk) = 512 output columns x one
 // chunk of rows, four waves each owning a quarter of the chunk's rows.  Lane l holds
 // dword l % 4 of block l / 4 of the tile (8 outputs), so one row is a 256-byte
 // contiguous read per wave.  The row's activation is wave-uniform (a scalar load),
 // which makes the skip a uniform branch.
-// Pass 2 (q4_vecmat_sum_kernel): out[k] = sum over chunks of part[chunk][k].
+// Pass 2 (q4_vecmat_sum_kernel): out[k] = sum over chunks of part[chunk][k], chunk
+// groups in parallel and their totals added in a fixed order.
 #include "device_common.h"
 #include "larql_hip_internal.h"
 
@@ -29,7 +30,7 @@ namespace {
 constexpr int kVmThreads = 256;
 constexpr int kVmWaves = kVmThreads / 64;
 constexpr int kVmTileCols = 512;   // 64 lanes x 8 outputs
-constexpr int kVmRowsPerWave = 16;  // rows in flight per wave (all loaded before any arithmetic)
+constexpr int kVmRowsPerWave = 32;  // rows in flight per wave (all loaded before any arithmetic)
 
 // Grid (ceil(hidden / 512), chunks).  part: [chunks][hidden].
 __global__ __launch_bounds__(kVmThreads) void q4_vecmat_part_kernel(const uint32_t* __restrict__ qs,
@@ -102,35 +103,43 @@ __global__ __launch_bounds__(kVmThreads) void q4_vecmat_part_kernel(const uint32
     }
 }
 
-// out[k] = part[0][k] + part[1][k] + ... in chunk order; four chunks in flight per step.
+// out[k] = sum over chunks of part[c][k]: workgroup = 16 columns x 16 chunk groups;
+// group g sums chunks g, g + 16, ... (eight loads in flight at a time), then the 16
+// group totals are added in group order.
+constexpr int kSumCols = 16, kSumGroups = 16;
 __global__ __launch_bounds__(256) void q4_vecmat_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                            int hidden, int chunks) {
-    const int k = blockIdx.x * 256 + threadIdx.x;
-    if (k >= hidden) return;
+    __shared__ float red[kSumGroups][kSumCols];
+    const int col = threadIdx.x & (kSumCols - 1), g = threadIdx.x / kSumCols;
+    const int k = blockIdx.x * kSumCols + col;
+    const int kc = min(k, hidden - 1);
     float s = 0.0f;
-    int c = 0;
-    for (; c + 4 <= chunks; c += 4) {
-        const float v0 = part[static_cast<size_t>(c) * hidden + k];
-        const float v1 = part[static_cast<size_t>(c + 1) * hidden + k];
-        const float v2 = part[static_cast<size_t>(c + 2) * hidden + k];
-        const float v3 = part[static_cast<size_t>(c + 3) * hidden + k];
-        s = s + v0;
-        s = s + v1;
-        s = s + v2;
-        s = s + v3;
+    for (int c0 = g; c0 < chunks; c0 += 8 * kSumGroups) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = part[static_cast<size_t>(min(c0 + u * kSumGroups, chunks - 1)) * hidden + kc];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (c0 + u * kSumGroups < chunks) s = s + v[u];
     }
-    for (; c < chunks; c++) s = s + part[static_cast<size_t>(c) * hidden + k];
-    out[k] = s;
+    red[g][col] = s;
+    __syncthreads();
+    if (g == 0 && k < hidden) {
+        float t = red[0][col];
+#pragma unroll
+        for (int i = 1; i < kSumGroups; i++) t = t + red[i][col];
+        out[k] = t;
+    }
 }
 
 }  // namespace
 
-// Chunks: enough workgroups to cover the chip (about 8 waves per CU) without letting
+// Chunks: enough workgroups to cover the chip (about 16 waves per CU) without letting
 // the partials (4 bytes x chunks x hidden, written and read once) pass ~1/8 of the
 // weight bytes (18/32 bytes per weight).
 size_t q4_vecmat_chunks(size_t inter, size_t hidden) {
     const size_t tiles = (hidden + kVmTileCols - 1) / kVmTileCols;
-    const size_t want = std::max<size_t>(1, (static_cast<size_t>(current_device_cus()) * 2 + tiles - 1) / tiles);
+    const size_t want = std::max<size_t>(1, (static_cast<size_t>(current_device_cus()) * 4 + tiles - 1) / tiles);
     const size_t cap = std::max<size_t>(1, inter * 18 / (32 * 4 * 8));  // partials <= weights / 8
     return std::max<size_t>(1, std::min({want, cap, (inter + kVmWaves - 1) / kVmWaves}));
 }
@@ -147,7 +156,8 @@ void launch_q4_vecmat(const DevWeight& w, const float* act, float* out, float* p
                                                           static_cast<const uint16_t*>(w.d), act, part, inter, hidden,
                                                           rows_per_chunk);
     LARQL_HIP_CHECK(hipGetLastError());
-    q4_vecmat_sum_kernel<<<dim3(static_cast<unsigned>((hidden + 255) / 256)), dim3(256), 0, s>>>(part, out, hidden, nch);
+    q4_vecmat_sum_kernel<<<dim3(static_cast<unsigned>((hidden + kSumCols - 1) / kSumCols)), dim3(256), 0, s>>>(
+        part, out, hidden, nch);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
