@@ -5,9 +5,14 @@
 // byte layout (LC/src/cpu/ops/q4_common.rs) into structure-of-arrays form so the
 // kernels issue 16-byte aligned, wave-contiguous loads:
 //
-//   Q4_K (148 B / 256 elems in the reference):
-//     qs  : u8 [rows][S*128]      nibble bytes, reference order within a super-block
-//     hdr : u32x4 [rows][S]       {d|dmin<<16, sc[0..3], sc[4..7], min bytes}
+//   Q4_K (148 B / 256 elems in the reference), tile-major over 16-row tiles:
+//     qs  : u8 [rows/16][S][2][64][16]  nibble bytes: for row 16t + c, sub-block j of
+//                                       super-block sb sits at [t][sb][j/4][16(j%4) + c],
+//                                       16 bytes in reference order (element 2i low,
+//                                       2i+1 high nibble of byte i)
+//     hdr : u32x4 [rows/16][S][16]      {d|dmin<<16, sc[0..3], sc[4..7], min bytes}
+//   so that one wave-wide 16-byte load of a (tile, super-block) reads 1 KB of
+//   contiguous memory (the matrix-core matvec's B operand, one sub-block per lane).
 //   Q6_K (210 B / 256):
 //     ql  : u8 [rows][S*128]      low nibbles (reference order)
 //     qh  : u32 [rows][S*16]      high 2-bit pairs, regrouped per 16 elements: for
@@ -88,6 +93,16 @@ uint64_t host_fingerprint(const void* data, size_t len);
 size_t ref_row_bytes(int format, size_t cols);   // bytes per row in the reference layout
 size_t dev_layout_bytes(int format, size_t rows_pad, size_t cols);
 inline size_t pad_rows(size_t rows) { return (rows + 63) & ~size_t(63); }
+
+// Q4_K tile-major layout: byte offset of sub-block j (0..7) of super-block sb of `row`
+// in qs, and the index of its header in hdr (S = super-blocks per row).
+__host__ __device__ inline size_t q4k_sub_offset(size_t row, size_t sb, int j, size_t S) {
+    return ((((row >> 4) * S + sb) * 2 + static_cast<size_t>(j >> 2)) << 10) +
+           ((16 * static_cast<size_t>(j & 3) + (row & 15)) << 4);
+}
+__host__ __device__ inline size_t q4k_hdr_index(size_t row, size_t sb, size_t S) {
+    return ((row >> 4) * S + sb) * 16 + (row & 15);
+}
 
 // Compute units of the current device (queried once per device, then cached).
 int current_device_cus();

@@ -79,10 +79,12 @@ __global__ void repack_q4k_kernel(const uint32_t* __restrict__ raw, uint8_t* __r
     if (b >= nblocks) return;
     const uint32_t* s = raw + b * 37;
     const size_t o = dst_block(b, bpr, row0, stride);
-    hdr[o] = make_uint4(s[0], s[1], s[2], s[4]);
-    uint4* q = reinterpret_cast<uint4*>(qs + o * 128);
+    const size_t row = o / bpr, sb = o - row * bpr;
+    hdr[q4k_hdr_index(row, sb, bpr)] = make_uint4(s[0], s[1], s[2], s[4]);
 #pragma unroll
-    for (int i = 0; i < 8; i++) q[i] = make_uint4(s[5 + 4 * i], s[6 + 4 * i], s[7 + 4 * i], s[8 + 4 * i]);
+    for (int j = 0; j < 8; j++)
+        *reinterpret_cast<uint4*>(qs + q4k_sub_offset(row, sb, j, bpr)) =
+            make_uint4(s[5 + 4 * j], s[6 + 4 * j], s[7 + 4 * j], s[8 + 4 * j]);
 }
 
 // One thread per Q6_K super-block (210-byte stride: 2-byte aligned source).  The

@@ -1,7 +1,7 @@
-// K-quant x f32 matvecs with fused RMSNorm prologue and decode epilogues.
+// Q6_K x f32 matvec (tiled form for tall or very long matrices) with fused RMSNorm
+// prologue and decode epilogues, and the matvec dispatch for both K-quant formats
+// (Q4_K goes to the matrix-core kernel of matvec_q4k_mfma.hip).
 //
-//   Q4_K (148-byte layout): reference semantics LC/src/cpu/ops/q4k_matvec.rs:31-90,
-//        trait method LC/src/backend.rs:126-130.
 //   Q6_K (210-byte layout): LC/src/cpu/ops/q6k_matvec.rs:31-90, backend.rs:133-137.
 //
 // Mapping (gfx950, wave64): a "row slot" is `wpr` waves whose 64*wpr lanes cover K,
@@ -71,106 +71,6 @@ __device__ __forceinline__ void finish_rows(const MvArgs& a, float (&acc)[RB], f
             if (lane < RB)
                 for (int w = 0; w < a.wpr; w++) s += buf[(slot * a.wpr + w) * RB + lane];
             epilogue_lanes(a, s, lane, row0, RB);
-        }
-    }
-}
-
-// ── Q4_K ────────────────────────────────────────────────────────────────
-// Device rows are zero-padded to a multiple of 64, so tile loads need no row test;
-// FULL means 64*wpr*SBL lanes cover K exactly, so no lane test either (otherwise the
-// spare lanes read a clamped, real block and contribute 0).
-template <int SBL, int RB, bool FULL>
-__global__ __launch_bounds__(512) void q4k_mv_kernel(MvArgs a) {
-    extern __shared__ double dyn_lds[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar row addresses
-    const int nwaves = blockDim.x >> 6;
-    const int slot = wave / a.wpr;
-    const int wslot = wave - slot * a.wpr;
-    const int nslots = nwaves / a.wpr;
-    const int C = a.wpr * 64;
-    const int cl = wslot * 64 + lane;
-    const int nsub = a.cols >> 5;
-    const int S = a.cols >> 8;
-    const size_t rowq = static_cast<size_t>(a.cols) >> 1;
-    double* dscratch = dyn_lds;
-    float* red = reinterpret_cast<float*>(dyn_lds + nwaves);
-
-    bool valid[SBL];
-    int cc[SBL], scsel[SBL], scsh[SBL], msh[SBL];
-#pragma unroll
-    for (int i = 0; i < SBL; i++) {
-        valid[i] = cl + i * C < nsub;
-        cc[i] = FULL ? cl + i * C : min(cl + i * C, nsub - 1);
-        const int j = cc[i] & 7;
-        scsel[i] = j < 4;
-        scsh[i] = 8 * (j & 3);
-        msh[i] = 8 * (j & 3) + (j < 4 ? 0 : 4);
-    }
-    // Workgroup b handles tiles b, b + grid, b + 2 grid, ... (a.steps of them): the x
-    // prologue is paid once per workgroup.  Tiles are double-buffered in registers: the
-    // loads of tile t+1 are issued before tile t's arithmetic, so every wave keeps a
-    // tile in flight while it computes.
-    uint4 qa[RB][SBL], ha[RB][SBL], qb[RB][SBL], hb[RB][SBL];
-    auto load_tile = [&](uint4 (&qv)[RB][SBL], uint4 (&hv)[RB][SBL], int tile) __attribute__((always_inline)) {
-        const int row0 = (tile * nslots + slot) * RB;
-#pragma unroll
-        for (int r = 0; r < RB; r++)
-#pragma unroll
-            for (int i = 0; i < SBL; i++) {
-                const size_t row = static_cast<size_t>(row0 + r);
-                // wave-uniform row base + 32-bit lane offset: scalar-base loads
-                const uint8_t* qrow = a.qs + row * rowq;
-                const uint4* hrow = a.hdr + row * S;
-                qv[r][i] = *reinterpret_cast<const uint4*>(qrow + static_cast<uint32_t>(cc[i]) * 16u);
-                hv[r][i] = hrow[static_cast<uint32_t>(cc[i]) >> 3];
-            }
-    };
-    XLevels L[SBL];
-    auto compute_tile = [&](const uint4 (&qv)[RB][SBL], const uint4 (&hv)[RB][SBL], int t, int tile) __attribute__((always_inline)) {
-        float acc[RB];
-#pragma unroll
-        for (int r = 0; r < RB; r++) {
-            acc[r] = 0.f;
-#pragma unroll
-            for (int i = 0; i < SBL; i++) {
-                const uint4 q = qv[r][i];
-                const uint4 h = hv[r][i];
-                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-                int ia = 0;
-                uint32_t ib = 0, ic = 0;
-#pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    const uint32_t lo = qw[w] & 0x0F0F0F0Fu;
-                    const uint32_t hi = (qw[w] >> 4) & 0x0F0F0F0Fu;
-                    ia = sdot4(lo, L[i].ev[0][w], ia);
-                    ia = sdot4(hi, L[i].od[0][w], ia);
-                    ib = udot4(lo, L[i].ev[1][w], ib);
-                    ib = udot4(hi, L[i].od[1][w], ib);
-                    ic = udot4(lo, L[i].ev[2][w], ic);
-                    ic = udot4(hi, L[i].od[2][w], ic);
-                }
-                const float d = h2f(h.x);
-                const float dmin = h2f(h.x >> 16);
-                const uint32_t sw = scsel[i] ? h.y : h.z;
-                float sc = d * static_cast<float>((sw >> scsh[i]) & 0x3Fu);
-                float mn = dmin * static_cast<float>((h.w >> msh[i]) & 0xFu);
-                if (!FULL && !valid[i]) { sc = 0.f; mn = 0.f; }
-                acc[r] = fmaf(sc, combine(ia, ib, ic, L[i].sp), fmaf(-mn, L[i].xs, acc[r]));
-            }
-        }
-        finish_rows<RB>(a, acc, red, t, lane, wave, nwaves, slot, wslot, (tile * nslots + slot) * RB);
-    };
-    const int g = static_cast<int>(gridDim.x);
-    load_tile(qa, ha, blockIdx.x);
-    prologue_levels<SBL>(a, cl, C, nsub, dscratch, wave, slot, lane, L, valid);
-    for (int t = 0; t < a.steps; t += 2) {
-        const int t0 = blockIdx.x + t * g, t1 = t0 + g, t2 = t1 + g;
-        if (t + 1 < a.steps && t1 < a.tiles) load_tile(qb, hb, t1);
-        if (t0 < a.tiles) compute_tile(qa, ha, t, t0);
-        if (t + 1 < a.steps) {
-            if (t + 2 < a.steps && t2 < a.tiles) load_tile(qa, ha, t2);
-            if (t1 < a.tiles) compute_tile(qb, hb, t + 1, t1);
         }
     }
 }
@@ -294,12 +194,7 @@ static void launch_mv_t(const DevWeight& w, MvArgs a, hipStream_t s, int nslots,
     const int nwaves = threads / 64;
     const size_t shmem = nwaves * sizeof(double) + 2 * nwaves * RB * sizeof(float);
     const dim3 g(static_cast<unsigned>(grid)), b(threads);
-    if (w.format == LARQL_Q4_K) {
-        a.qs = w.qs;
-        a.hdr = w.hdr;
-        if (full) q4k_mv_kernel<SBL, RB, true><<<g, b, shmem, s>>>(a);
-        else q4k_mv_kernel<SBL, RB, false><<<g, b, shmem, s>>>(a);
-    } else {
+    {
         a.qs = w.qs;
         a.qh = w.qh;
         a.sc = w.sc;
@@ -311,7 +206,8 @@ static void launch_mv_t(const DevWeight& w, MvArgs a, hipStream_t s, int nslots,
 }
 
 void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s) {
-    if (w.format != LARQL_Q4_K && w.format != LARQL_Q6_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "launch_mv: format");
+    if (w.format == LARQL_Q4_K) return launch_q4k_mfma(w, a, s);
+    if (w.format != LARQL_Q6_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "launch_mv: format");
     if (a.num_cus <= 0) a.num_cus = current_device_cus();
     if (stream_mv_supported(w)) return launch_mv_stream(w, a, s);
     a.rows = static_cast<int>(w.rows);

@@ -1,0 +1,302 @@
+// Q4_K x f32 matvec with the integer block dots on the matrix cores.
+//
+//   Reference semantics: LC/src/cpu/ops/q4k_matvec.rs:31-90 (trait method
+//   LC/src/backend.rs:126-130): out[n] = sum_sb sum_j sum_i (d*sc_j*q - dmin*m_j) * x,
+//   computed here in the factorised form sc * sum(q x) - mn * sum(x) per 32-element
+//   sub-block (LC/src/metal/shaders/q4k_matvec.rs:13-79).
+//
+// Work split.  A workgroup owns a tile of 16 consecutive weight rows; its KS waves split
+// the super-blocks of the rows into contiguous parts of P = UR * R super-blocks (wave w
+// takes [wP, wP + P)), walked in R rounds of UR.  At the start of a round a wave issues
+// every load of the round (its x slice, then UR units of two 1 KB nibble loads and one
+// 256 B header load), so with R = 1 the whole matrix is requested from HBM within the
+// first microsecond of the launch and the arithmetic of every wave overlaps the
+// streaming of all the others.  The weights are stored tile-major (layouts.hip): each
+// of those loads reads contiguous memory.
+//
+// Per unit (one super-block of the 16 rows), lane (g, c) = lane 16 g + c holds
+// sub-blocks g and g + 4 of row c.  Four v_mfma_i32_16x16x64_i8 take the nibbles
+// (unpacked to bytes) as B, column c = row c, and the activation as A, with A row
+// 4 s + p = digit plane p of the x sub-block held by k-group s (zero in the other
+// k-groups).  Result lane 16 g + c, register p, is then exactly the int32 dot of plane p
+// of x with sub-block g (first accumulator) or g + 4 (second) of row c: no cross-lane
+// traffic until the end of the row.
+//
+// x digit planes: per 32-element sub-block, T = rint(x * (2^22 - 1) / max|x|) is split
+// into balanced signed bytes T = 65536 a + 256 b + c (a, b, c in [-128, 127]) taken from
+// the bytes of T + 0x808080 with their top bits flipped.  |x - s' T| <= s'/2 with
+// s' = max|x| / (2^22 - 1): the size of one f32 rounding of the sub-block's largest
+// element.  Each wave builds the planes of its own part in its own LDS area (no
+// workgroup barrier before the loop); a fused RMSNorm adds one barrier for sum(x^2).
+#include "kquant_levels.h"
+#include "matvec_common.h"
+
+namespace larql {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// One sub-block's planes in LDS: [MFMA half m][plane p] x 16 bytes, then
+// {s', 65536 s', sum x, 0}.  Within a unit, sub-block j sits in slot 2 (j % 4) + j / 4,
+// so the two sub-blocks of a lane (g and g + 4) are adjacent.
+struct PlSlot {
+    uint4 pl[2][3];
+    float4 s;
+};
+static_assert(sizeof(PlSlot) == 112, "LDS plane slot");
+
+constexpr int kZeroBytes = 256;  // per-wave zero area read by the idle A lanes (offsets < 176)
+constexpr int kMaxKS = 16;
+
+template <int UR>
+__host__ __device__ constexpr int wave_lds_bytes() {
+    return kZeroBytes + 8 * UR * static_cast<int>(sizeof(PlSlot));
+}
+
+// Byte b (b = 0, 1, 2) of each of u0..u3 -> dword b, top bits flipped: the signed digit
+// planes of four elements, low to high.
+__device__ __forceinline__ void pack_planes(uint32_t u0, uint32_t u1, uint32_t u2, uint32_t u3, uint32_t (&pl)[3]) {
+    const uint32_t p01 = __builtin_amdgcn_perm(u1, u0, 0x05010400u);  // u0.b0 u1.b0 u0.b1 u1.b1
+    const uint32_t q01 = __builtin_amdgcn_perm(u1, u0, 0x0C0C0602u);  // u0.b2 u1.b2 0 0
+    const uint32_t p23 = __builtin_amdgcn_perm(u3, u2, 0x05010400u);
+    const uint32_t q23 = __builtin_amdgcn_perm(u3, u2, 0x0C0C0602u);
+    pl[0] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;
+    pl[1] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
+    pl[2] = __builtin_amdgcn_perm(q23, q01, 0x05040100u) ^ 0x80808080u;
+}
+
+// Nibble dword (element 2i in the low, 2i + 1 in the high nibble of byte i) -> bytes of
+// its even / odd elements.
+__device__ __forceinline__ int lo_nib(uint32_t w) { return static_cast<int>(w & 0x0F0F0F0Fu); }
+__device__ __forceinline__ int hi_nib(uint32_t w) { return static_cast<int>((w >> 4) & 0x0F0F0F0Fu); }
+
+// UR: super-blocks per round (2 or 4); a.steps = R rounds; KS = blockDim.x / 64 waves.
+template <int UR, bool NORM>
+__global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int EL = 4 * UR;  // x elements per lane and round
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int KS = blockDim.x >> 6;
+    const int R = a.steps;
+    const int S = a.cols >> 8;
+    const int sb0 = wave * UR * R;                  // first super-block of this wave
+    const int nsb = max(0, min(UR * R, S - sb0));   // super-blocks of this wave
+    const int g = lane >> 4, c = lane & 15;
+    const int row = blockIdx.x * 16 + c;            // < rows_pad: the grid is rows_pad / 16
+    const uint8_t* tq = a.qs + static_cast<size_t>(blockIdx.x) * S * 2048 + lane * 16;
+    const uint4* th = a.hdr + static_cast<size_t>(blockIdx.x) * S * 16 + c;
+
+    uint8_t* wl = lds + wave * wave_lds_bytes<UR>();
+    PlSlot* slots = reinterpret_cast<PlSlot*>(wl + kZeroBytes);
+    float* red = reinterpret_cast<float*>(lds + KS * wave_lds_bytes<UR>());  // [KS][16], then NORM scratch
+
+    float xv[EL], wv[NORM ? EL : 1];
+    uint4 n0[UR], n1[UR], hd[UR];
+    // Loads of round r: this lane's x slice (element e0), then the units' weights
+    // (super-block indices clamped: a short last round re-reads a real block).
+    auto load_round = [&](int r) __attribute__((always_inline)) {
+        const int e0 = (sb0 + r * UR) * 256 + lane * EL;
+        load_slice<EL>(a.x, min(e0, a.cols - EL), true, xv);
+        if constexpr (NORM) load_slice<EL>(a.norm_w, min(e0, a.cols - EL), true, wv);
+#pragma unroll
+        for (int u = 0; u < UR; u++) {
+            const int sb = min(sb0 + r * UR + u, S - 1);
+            const uint8_t* q = tq + static_cast<size_t>(sb) * 2048;
+            n0[u] = *reinterpret_cast<const uint4*>(q);
+            n1[u] = *reinterpret_cast<const uint4*>(q + 1024);
+            hd[u] = th[static_cast<size_t>(sb) * 16];
+        }
+    };
+    load_round(0);
+
+    // Fused RMSNorm (LI/src/residual.rs:17-33): sum(x^2) over all of x, in f64.
+    float inv_rms = 1.f;
+    if constexpr (NORM) {
+        double part[2] = {0.0, 0.0};
+        for (int r = 0; r < R; r++) {
+            float xs[EL];
+            const int e0 = (sb0 + r * UR) * 256 + lane * EL;
+            if (r == 0) {
+#pragma unroll
+                for (int k = 0; k < EL; k++) xs[k] = xv[k];
+            } else {
+                load_slice<EL>(a.x, min(e0, a.cols - EL), true, xs);
+            }
+            if (e0 < sb0 * 256 + nsb * 256) {
+#pragma unroll
+                for (int k = 0; k < EL; k++)
+                    part[k & 1] = fma(static_cast<double>(xs[k]), static_cast<double>(xs[k]), part[k & 1]);
+            }
+        }
+        const double v = wave_sum_d(part[0] + part[1]);
+        double* dscr = reinterpret_cast<double*>(red + KS * 16);
+        if (lane == 0) dscr[wave] = v;
+        __syncthreads();
+        double tot = 0.0;
+        for (int w = 0; w < KS; w++) tot += dscr[w];
+        // rms as the CPU path rounds it (LI/src/residual.rs:24); x * (1/rms) differs from
+        // x / rms by at most one f32 rounding.
+        const float rms = static_cast<float>(sqrt(tot / static_cast<double>(a.cols) + a.eps));
+        inv_rms = 1.0f / rms;
+    }
+
+    // A lane (g, i): A row i = 4 s + p is live in k-group g iff s == g and p < 3; the
+    // others read the zero area (same immediate offsets, all inside it).
+    const int ia = lane & 15;
+    const bool alive = (ia >> 2) == g && (ia & 3) < 3;
+    const uint32_t abase = alive ? static_cast<uint32_t>(kZeroBytes + 2 * g * sizeof(PlSlot) + (ia & 3) * 16) : 0u;
+    const uint32_t astep = alive ? 8u * sizeof(PlSlot) : 0u;
+    const int scsh = 8 * g;
+    float acc = 0.f;
+
+    for (int r = 0; r < R; r++) {
+        const int nr = min(UR, nsb - r * UR);  // units of this round (wave-uniform)
+        if (nr <= 0) break;
+        if (r > 0) load_round(r);
+        // Digit planes of this lane's EL elements (one sub-block of 32 spans 32 / EL lanes).
+        {
+            if constexpr (NORM) {
+#pragma unroll
+                for (int k = 0; k < EL; k++) xv[k] = (xv[k] * inv_rms) * (a.norm_offset + wv[k]);
+            }
+            float m = tree_max_abs<EL>(xv);
+            float s = tree_sum<EL>(xv);
+            m = fmaxf(m, dpp_f<DPP_QUAD_1032>(m));
+            s = s + dpp_f<DPP_QUAD_1032>(s);
+            if constexpr (UR == 2) {
+                m = fmaxf(m, dpp_f<DPP_QUAD_2301>(m));
+                s = s + dpp_f<DPP_QUAD_2301>(s);
+            }
+            const float inv = m > 0.f ? kLevelScale / m : 0.f;
+            uint32_t u[EL];
+#pragma unroll
+            for (int k = 0; k < EL; k++)
+                u[k] = __float_as_uint(fmaf(xv[k], inv, 12582912.0f)) + (0x808080u - 0x4B400000u);
+            const int sub = (lane * EL) >> 5;  // sub-block within the round: unit sub / 8, j = sub % 8
+            const int ofs = (lane * EL) & 31;  // first element of the lane within it
+            if (sub < 8 * nr) {
+                const int j = sub & 7;
+                PlSlot& sl = slots[(sub & ~7) + 2 * (j & 3) + (j >> 2)];
+                const int hm = ofs >> 4;
+                const int dw0 = (ofs & 15) >> 2;  // first dword of the half this lane fills (0 or 2)
+#pragma unroll
+                for (int q8 = 0; q8 < EL / 8; q8++) {
+                    uint32_t pe[3], po[3];
+                    pack_planes(u[8 * q8 + 0], u[8 * q8 + 2], u[8 * q8 + 4], u[8 * q8 + 6], pe);
+                    pack_planes(u[8 * q8 + 1], u[8 * q8 + 3], u[8 * q8 + 5], u[8 * q8 + 7], po);
+#pragma unroll
+                    for (int p = 0; p < 3; p++) {
+                        uint32_t* d = reinterpret_cast<uint32_t*>(&sl.pl[hm][p]) + dw0 + 2 * q8;
+                        *reinterpret_cast<uint2*>(d) = make_uint2(pe[p], po[p]);
+                    }
+                }
+                if (ofs == 0) sl.s = make_float4(m / kLevelScale, m * (65536.0f / kLevelScale), s, 0.f);
+            }
+            if (r == 0 && lane < kZeroBytes / 16) reinterpret_cast<uint4*>(wl)[lane] = make_uint4(0, 0, 0, 0);
+        }
+        // the wave reads what its own lanes wrote: keep the LDS accesses in program order
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+#pragma unroll
+        for (int u = 0; u < UR; u++) {
+            if (u < nr) {
+                const uint8_t* ab = wl + abase + u * astep;
+                const uint4 a0 = *reinterpret_cast<const uint4*>(ab);
+                const uint4 a1 = *reinterpret_cast<const uint4*>(ab + 48);
+                const uint4 a2 = *reinterpret_cast<const uint4*>(ab + sizeof(PlSlot));
+                const uint4 a3 = *reinterpret_cast<const uint4*>(ab + sizeof(PlSlot) + 48);
+                const v4i A0 = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w};
+                const v4i A1 = {(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                const v4i A2 = {(int)a2.x, (int)a2.y, (int)a2.z, (int)a2.w};
+                const v4i A3 = {(int)a3.x, (int)a3.y, (int)a3.z, (int)a3.w};
+                const v4i B0 = {lo_nib(n0[u].x), hi_nib(n0[u].x), lo_nib(n0[u].y), hi_nib(n0[u].y)};
+                const v4i B1 = {lo_nib(n0[u].z), hi_nib(n0[u].z), lo_nib(n0[u].w), hi_nib(n0[u].w)};
+                const v4i B2 = {lo_nib(n1[u].x), hi_nib(n1[u].x), lo_nib(n1[u].y), hi_nib(n1[u].y)};
+                const v4i B3 = {lo_nib(n1[u].z), hi_nib(n1[u].z), lo_nib(n1[u].w), hi_nib(n1[u].w)};
+                v4i Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, v4i{0, 0, 0, 0}, 0, 0, 0);
+                v4i Db = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, v4i{0, 0, 0, 0}, 0, 0, 0);
+                Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, Da, 0, 0, 0);
+                Db = __builtin_amdgcn_mfma_i32_16x16x64_i8(A3, B3, Db, 0, 0, 0);
+                // scales of sub-blocks g and g + 4 of row c
+                const PlSlot* sl = slots + 8 * u + 2 * g;
+                const float4 sa = sl[0].s, sb = sl[1].s;
+                const uint4 h = hd[u];
+                const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+                const float sc0 = d * static_cast<float>((h.y >> scsh) & 0x3Fu);
+                const float sc1 = d * static_cast<float>((h.z >> scsh) & 0x3Fu);
+                const float mn0 = dmin * static_cast<float>((h.w >> scsh) & 0xFu);
+                const float mn1 = dmin * static_cast<float>((h.w >> (scsh + 4)) & 0xFu);
+                // s' (65536 a + 256 b + c): 256 b + c is exact in int32 and in f32 (< 2^24)
+                const float dot0 = fmaf(static_cast<float>(Da[2]), sa.y, sa.x * static_cast<float>(Da[1] * 256 + Da[0]));
+                const float dot1 = fmaf(static_cast<float>(Db[2]), sb.y, sb.x * static_cast<float>(Db[1] * 256 + Db[0]));
+                acc = fmaf(sc0, dot0, fmaf(-mn0, sa.z, acc));
+                acc = fmaf(sc1, dot1, fmaf(-mn1, sb.z, acc));
+            }
+        }
+        if (r + 1 < R) {
+            // the next round rewrites the planes this round's MFMA operands came from
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+
+    // Row totals: over the four k-groups of the wave, then over the waves in order.
+    acc = swap32_add(acc, acc);
+    acc = swap16_add(acc, acc);
+    if (lane < 16) red[wave * 16 + lane] = acc;
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+        float tot = red[lane];
+        for (int w = 1; w < KS; w++) tot += red[w * 16 + lane];
+        if (a.epi == EPI_SILU_PAIR) {
+            const float up = __shfl_down(tot, 1, 16);
+            if ((lane & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
+        } else if (row < a.rows) {
+            a.out[row] = a.epi == EPI_RESID ? a.resid[row] + tot : tot;
+        }
+    }
+}
+
+template <int UR>
+void launch_q4k_mfma_t(const DevWeight& w, MvArgs a, int R, hipStream_t s) {
+    const int S = static_cast<int>(w.cols / 256);
+    const int KS = (S + UR * R - 1) / (UR * R);
+    a.steps = R;
+    const size_t shmem = static_cast<size_t>(KS) * (wave_lds_bytes<UR>() + 16 * sizeof(float)) +
+                         (a.norm_w ? kMaxKS * sizeof(double) : 0);
+    const dim3 grid(static_cast<unsigned>(w.rows_pad / 16)), block(64 * KS);
+    if (a.norm_w) q4k_mfma_kernel<UR, true><<<grid, block, shmem, s>>>(a);
+    else q4k_mfma_kernel<UR, false><<<grid, block, shmem, s>>>(a);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace
+
+void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s) {
+    if (w.format != LARQL_Q4_K || w.cols % 256 != 0 || w.cols == 0 || w.rows_pad % 16 != 0 ||
+        w.cols > (size_t{1} << 24) || w.rows_pad / 16 > 0x7FFFFFFFu)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "q4k matvec: shape");
+    if (a.num_cus <= 0) a.num_cus = current_device_cus();
+    a.rows = static_cast<int>(w.rows);
+    a.cols = static_cast<int>(w.cols);
+    a.rows_pad = static_cast<int>(w.rows_pad);
+    a.qs = w.qs;
+    a.hdr = w.hdr;
+    if (a.epi == EPI_SILU_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "silu pair epilogue needs even rows");
+    // Four super-blocks per round; two when that leaves fewer than ~12 waves per CU
+    // (small matrices: the fused Q|K|V and O projections of a decode layer).  Rows
+    // longer than 16 waves x 4 super-blocks (K > 16384) take several rounds.
+    const size_t S = w.cols / 256;
+    const size_t tiles = w.rows_pad / 16;
+    if (S <= 2 * kMaxKS && tiles * ((S + 3) / 4) < 12 * static_cast<size_t>(a.num_cus))
+        launch_q4k_mfma_t<2>(w, a, 1, s);
+    else
+        launch_q4k_mfma_t<4>(w, a, static_cast<int>((S + 4 * kMaxKS - 1) / (4 * kMaxKS)), s);
+}
+
+}  // namespace larql

@@ -1,7 +1,5 @@
-// Streaming K-quant x f32 matvec: the decode-time weight sweep.
+// Streaming Q6_K x f32 matvec: the decode-time weight sweep.
 //
-//   Q4_K (148-byte layout): reference semantics LC/src/cpu/ops/q4k_matvec.rs:31-90,
-//        trait method LC/src/backend.rs:126-130.
 //   Q6_K (210-byte layout): LC/src/cpu/ops/q6k_matvec.rs:31-90, backend.rs:133-137.
 //
 // Shape of the launch (gfx950): a persistent grid of a few 256-thread workgroups per
@@ -15,7 +13,7 @@
 // weight byte is read from HBM once, with wave-contiguous 16-byte loads from a
 // wave-uniform row base.
 //
-// Arithmetic per lane and row: exact int32 v_dot4 of the 4/6-bit codes with the two
+// Arithmetic per lane and row: exact int32 v_dot4 of the 6-bit codes with the three
 // x byte planes, then the f32 sub-block scale / min as in the reference factorisation
 // sc * sum(q x) - mn * sum(x)  (LC/src/metal/shaders/q4k_matvec.rs:13-79).  Row sums
 // over lanes use the permlane-swap transposing reduction; the epilogue is fused.
@@ -53,10 +51,6 @@ __device__ __forceinline__ double block_sum_d(double v, double* scratch) {
 // Per-unit weight registers of one row.
 template <int FMT>
 struct RowRegs;
-template <>
-struct RowRegs<LARQL_Q4_K> {
-    uint4 q, h;  // 16 nibble bytes of the lane's sub-block; super-block header
-};
 template <>
 struct RowRegs<LARQL_Q6_K> {
     uint4 l;      // 16 low-nibble bytes
@@ -183,11 +177,7 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
 #pragma unroll
         for (int r = 0; r < RB; r++) {
             const size_t row = static_cast<size_t>(lsg * pairs + lgi) * RB + r;
-            if constexpr (FMT == LARQL_Q4_K) {
-                const uint8_t* qrow = a.qs + row * (static_cast<size_t>(a.cols) >> 1);
-                B.r[r].q = *reinterpret_cast<const uint4*>(qrow + c * 16u);
-                B.r[r].h = (a.hdr + row * S)[c >> 3];
-            } else {
+            {
                 const uint8_t* lrow = a.qs + row * (static_cast<size_t>(a.cols) >> 1);
                 const uint8_t* hrow = a.qh + row * (static_cast<size_t>(a.cols) >> 2);
                 const int8_t* srow = a.sc + row * (static_cast<size_t>(a.cols) >> 4);
@@ -251,43 +241,7 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
         const float4 st = L.s;
         // Integer dots first, rows interleaved and each level split over two
         // accumulators: 6 * RB independent chains of length 4.
-        if constexpr (FMT == LARQL_Q4_K) {
-            int ia[RB][2];
-            uint32_t ib[RB][2], ic[RB][2];
-#pragma unroll
-            for (int r = 0; r < RB; r++)
-#pragma unroll
-                for (int p = 0; p < 2; p++) ia[r][p] = 0, ib[r][p] = 0u, ic[r][p] = 0u;
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-#pragma unroll
-                for (int r = 0; r < RB; r++) {
-                    const uint4 q = B.r[r].q;
-                    const uint32_t qw = w == 0 ? q.x : w == 1 ? q.y : w == 2 ? q.z : q.w;
-                    const uint32_t lo = qw & 0x0F0F0F0Fu;
-                    const uint32_t hi = (qw >> 4) & 0x0F0F0F0Fu;
-                    const int p = w & 1;
-                    ia[r][p] = sdot4(lo, ev[0][w], ia[r][p]);
-                    ib[r][p] = udot4(lo, ev[1][w], ib[r][p]);
-                    ic[r][p] = udot4(lo, ev[2][w], ic[r][p]);
-                    ia[r][p] = sdot4(hi, od[0][w], ia[r][p]);
-                    ib[r][p] = udot4(hi, od[1][w], ib[r][p]);
-                    ic[r][p] = udot4(hi, od[2][w], ic[r][p]);
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < RB; r++) {
-                const uint4 h = B.r[r].h;
-                const float d = h2f(h.x);
-                const float dmin = h2f(h.x >> 16);
-                const uint32_t sw = scsel ? h.y : h.z;
-                float sc = d * static_cast<float>((sw >> scsh) & 0x3Fu);
-                float mn = dmin * static_cast<float>((h.w >> msh) & 0xFu);
-                if (!valid) { sc = 0.f; mn = 0.f; }
-                const float dot = combine(ia[r][0] + ia[r][1], ib[r][0] + ib[r][1], ic[r][0] + ic[r][1], st.x);
-                acc[r] = fmaf(sc, dot, fmaf(-mn, st.y, acc[r]));
-            }
-        } else {
+        {
             int ga[RB][2];
             uint32_t gb[RB][2], gc[RB][2];
 #pragma unroll
@@ -394,7 +348,7 @@ static_assert(kStreamMaxCols / 8 <= 4 * 512, "prologue: at most four 8-element s
 constexpr size_t kStreamMaxRows = 65536;
 
 bool stream_mv_supported(const DevWeight& w) {
-    return (w.format == LARQL_Q4_K || w.format == LARQL_Q6_K) && w.cols % 256 == 0 && w.cols <= kStreamMaxCols &&
+    return w.format == LARQL_Q6_K && w.cols % 256 == 0 && w.cols <= kStreamMaxCols &&
            w.rows_pad % 8 == 0 && w.rows_pad < kStreamMaxRows;
 }
 
@@ -405,20 +359,16 @@ void launch_mv_stream(const DevWeight& w, MvArgs a, hipStream_t s) {
     a.cols = static_cast<int>(w.cols);
     a.rows_pad = static_cast<int>(w.rows_pad);
     if (a.epi == EPI_SILU_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "silu pair epilogue needs even rows");
-    if (w.format == LARQL_Q4_K) {
-        a.qs = w.qs;
-        a.hdr = w.hdr;
-    } else {
-        a.qs = w.qs;
-        a.qh = w.qh;
-        a.sc = w.sc;
-        a.d = static_cast<const uint16_t*>(w.d);
-    }
+    a.qs = w.qs;
+    a.qh = w.qh;
+    a.sc = w.sc;
+    a.d = static_cast<const uint16_t*>(w.d);
     // One workgroup per CU, two rows per unit, four units in the ring.  The workgroup
     // has 8, 7 or 6 waves, whichever deals the row groups out most evenly (every wave
     // finishes with the last one): e.g. 7168 groups (14336 rows) -> 7 waves per CU,
     // four groups each; 3072 (a fused Q|K|V of 6144 rows) -> 6 waves, two each.
-    // Measured on Q4_K [14336 x 4096]: 9.2 us with 7 waves vs 9.6 us with 8.
+    // Measured (on the 4-bit form of this kernel, [14336 x 4096]): 9.2 us with 7 waves
+    // vs 9.6 us with 8.
     const long long ng = static_cast<long long>(w.rows_pad) / 2;  // RB = 2: a group holds a gate/up pair
     int best_nt = 512;
     long long best_slots = 0;
@@ -428,11 +378,7 @@ void launch_mv_stream(const DevWeight& w, MvArgs a, hipStream_t s) {
         const long long slots = (ng + W - 1) / W * W;  // group slots incl. idle ones
         if (best_slots == 0 || slots < best_slots) best_slots = slots, best_nt = nt;
     }
-    if (w.format == LARQL_Q4_K) {
-        if (best_nt == 448) launch_stream_t<LARQL_Q4_K, 2, 4, 448, 1>(w, a, s, 1);
-        else if (best_nt == 384) launch_stream_t<LARQL_Q4_K, 2, 4, 384, 1>(w, a, s, 1);
-        else launch_stream_t<LARQL_Q4_K, 2, 4, 512, 2>(w, a, s, 1);
-    } else {
+    {
         if (best_nt == 448) launch_stream_t<LARQL_Q6_K, 2, 4, 448, 1>(w, a, s, 1);
         else if (best_nt == 384) launch_stream_t<LARQL_Q6_K, 2, 4, 384, 1>(w, a, s, 1);
         else launch_stream_t<LARQL_Q6_K, 2, 4, 512, 2>(w, a, s, 1);

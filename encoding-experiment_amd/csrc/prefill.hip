@@ -61,16 +61,15 @@ __global__ __launch_bounds__(kThreads, 2) void q4k_gemm_kernel(const uint8_t* __
     const int lr = tid >> 1, lh = (tid & 1) * 16;
     const float* xp = X + static_cast<size_t>(min(m0 + lr, M - 1)) * K + lh;
     const size_t wrow = static_cast<size_t>(min(n0 + lr, N - 1));
-    const uint8_t* wq = qs + wrow * (K / 2) + lh / 2;
-    const uint4* wh = hdr + wrow * (K / 256);
+    const size_t S = static_cast<size_t>(K / 256);
     float4 xr[4];
     uint2 wqv;
     uint4 whv;
     auto gload = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 4; i++) xr[i] = *reinterpret_cast<const float4*>(xp + k0 + 4 * i);
-        wqv = *reinterpret_cast<const uint2*>(wq + (k0 >> 5) * 16);
-        whv = wh[k0 >> 8];
+        wqv = *reinterpret_cast<const uint2*>(qs + q4k_sub_offset(wrow, k0 >> 8, (k0 >> 5) & 7, S) + lh / 2);
+        whv = hdr[q4k_hdr_index(wrow, k0 >> 8, S)];
     };
     auto lstore = [&](int b, int k0) __attribute__((always_inline)) {
         *reinterpret_cast<half8*>(&Xs[b][lr][lh]) = to_half8(xr[0], xr[1]);
