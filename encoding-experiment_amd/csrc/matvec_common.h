@@ -161,7 +161,6 @@ __device__ __forceinline__ void load_slice(const float* __restrict__ base, int c
 void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s);
 bool stream_mv_supported(const DevWeight& w);
 void launch_mv_stream(const DevWeight& w, MvArgs a, hipStream_t s);
-bool q4k_mfma_supported(const DevWeight& w);
 void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s);
 
 }  // namespace larql

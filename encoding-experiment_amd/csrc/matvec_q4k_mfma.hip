@@ -5,14 +5,14 @@
 //   computed here in the factorised form sc * sum(q x) - mn * sum(x) per 32-element
 //   sub-block (LC/src/metal/shaders/q4k_matvec.rs:13-79).
 //
-// Work split.  A workgroup owns a tile of 16 consecutive weight rows; its KS waves split
-// the super-blocks of the rows into contiguous parts of P = UR * R super-blocks (wave w
-// takes [wP, wP + P)), walked in R rounds of UR.  At the start of a round a wave issues
-// every load of the round (its x slice, then UR units of two 1 KB nibble loads and one
-// 256 B header load), so with R = 1 the whole matrix is requested from HBM within the
-// first microsecond of the launch and the arithmetic of every wave overlaps the
-// streaming of all the others.  The weights are stored tile-major (layouts.hip): each
-// of those loads reads contiguous memory.
+// Work split.  A workgroup owns T tiles of 16 consecutive weight rows; its KS waves
+// split the super-blocks of the rows into contiguous parts of P = UR * R super-blocks
+// (wave w takes [wP, wP + P) of every tile), walked in R rounds of UR.  A round's loads
+// are its x slice, then UR units per tile of two 1 KB nibble loads and one 256 B header
+// load: with R = 1 every weight byte is requested within the first microsecond or two of
+// the launch and the arithmetic of every wave overlaps the streaming of all the others.
+// The weights are stored tile-major (layouts.hip), so each of those loads reads
+// contiguous memory, and they are non-temporal (each byte is used once).
 //
 // Per unit (one super-block of the 16 rows), lane (g, c) = lane 16 g + c holds
 // sub-blocks g and g + 4 of row c.  Four v_mfma_i32_16x16x64_i8 take the nibbles
@@ -30,6 +30,7 @@
 // workgroup barrier before the loop); a fused RMSNorm adds one barrier for sum(x^2).
 #include "kquant_levels.h"
 #include "matvec_common.h"
+
 
 namespace larql {
 
@@ -66,14 +67,29 @@ __device__ __forceinline__ void pack_planes(uint32_t u0, uint32_t u1, uint32_t u
     pl[2] = __builtin_amdgcn_perm(q23, q01, 0x05040100u) ^ 0x80808080u;
 }
 
+// Weight bytes are read exactly once: non-temporal loads keep them from displacing x and
+// the planes in the caches (measured: 8.4 -> 7.9 us on [14336 x 4096]).
+__device__ __forceinline__ uint4 load_nt(const void* p) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_nontemporal_load(static_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Nibble dword (element 2i in the low, 2i + 1 in the high nibble of byte i) -> bytes of
 // its even / odd elements.
 __device__ __forceinline__ int lo_nib(uint32_t w) { return static_cast<int>(w & 0x0F0F0F0Fu); }
 __device__ __forceinline__ int hi_nib(uint32_t w) { return static_cast<int>((w >> 4) & 0x0F0F0F0Fu); }
 
-// UR: super-blocks per round (2 or 4); a.steps = R rounds; KS = blockDim.x / 64 waves.
-template <int UR, bool NORM>
-__global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
+// UR: super-blocks per round (2 or 4); T: 16-row tiles per workgroup (rows
+// 16 T blockIdx.x ...), all sharing the wave's x planes; a.steps = R rounds;
+// KS = blockDim.x / 64 waves.
+template <int UR, int T>
+constexpr int max_waves() {
+    return UR * T >= 8 ? kMaxKS / 2 : kMaxKS;  // 8 units in flight need more than 128 VGPRs
+}
+
+template <int UR, int T, bool NORM>
+__global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int EL = 4 * UR;  // x elements per lane and round
     const int lane = threadIdx.x & 63;
@@ -84,32 +100,43 @@ __global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
     const int sb0 = wave * UR * R;                  // first super-block of this wave
     const int nsb = max(0, min(UR * R, S - sb0));   // super-blocks of this wave
     const int g = lane >> 4, c = lane & 15;
-    const int row = blockIdx.x * 16 + c;            // < rows_pad: the grid is rows_pad / 16
-    const uint8_t* tq = a.qs + static_cast<size_t>(blockIdx.x) * S * 2048 + lane * 16;
-    const uint4* th = a.hdr + static_cast<size_t>(blockIdx.x) * S * 16 + c;
+    const size_t tile0 = static_cast<size_t>(blockIdx.x) * T;  // < rows_pad / 16: the grid is rows_pad / (16 T)
+    const uint8_t* tq = a.qs + tile0 * S * 2048 + lane * 16;
+    const uint4* th = a.hdr + tile0 * S * 16 + c;
 
     uint8_t* wl = lds + wave * wave_lds_bytes<UR>();
     PlSlot* slots = reinterpret_cast<PlSlot*>(wl + kZeroBytes);
-    float* red = reinterpret_cast<float*>(lds + KS * wave_lds_bytes<UR>());  // [KS][16], then NORM scratch
+    float* red = reinterpret_cast<float*>(lds + KS * wave_lds_bytes<UR>());  // [KS][16 T], then NORM scratch
 
     float xv[EL], wv[NORM ? EL : 1];
-    uint4 n0[UR], n1[UR], hd[UR];
+    uint4 n0[T][UR], n1[T][UR], hd[T][UR];
     // Loads of round r: this lane's x slice (element e0), then the units' weights
-    // (super-block indices clamped: a short last round re-reads a real block).
-    auto load_round = [&](int r) __attribute__((always_inline)) {
+    // (super-block indices clamped: a short last round re-reads a real block).  The
+    // first PRE units are issued with x; the rest after the planes are built, so that a
+    // wave held up issuing loads into a full memory system has its planes ready when
+    // its data arrives.
+    auto load_x = [&](int r) __attribute__((always_inline)) {
         const int e0 = (sb0 + r * UR) * 256 + lane * EL;
         load_slice<EL>(a.x, min(e0, a.cols - EL), true, xv);
         if constexpr (NORM) load_slice<EL>(a.norm_w, min(e0, a.cols - EL), true, wv);
-#pragma unroll
-        for (int u = 0; u < UR; u++) {
-            const int sb = min(sb0 + r * UR + u, S - 1);
-            const uint8_t* q = tq + static_cast<size_t>(sb) * 2048;
-            n0[u] = *reinterpret_cast<const uint4*>(q);
-            n1[u] = *reinterpret_cast<const uint4*>(q + 1024);
-            hd[u] = th[static_cast<size_t>(sb) * 16];
-        }
     };
-    load_round(0);
+    // units are numbered t * UR + u (tile t, super-block u of the round)
+    auto load_units = [&](int r, int i0, int i1) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int u = 0; u < UR; u++) {
+                if (t * UR + u < i0 || t * UR + u >= i1) continue;
+                const size_t sb = static_cast<size_t>(t) * S + min(sb0 + r * UR + u, S - 1);
+                const uint8_t* q = tq + sb * 2048;
+                n0[t][u] = load_nt(q);
+                n1[t][u] = load_nt(q + 1024);
+                hd[t][u] = load_nt(th + sb * 16);
+            }
+    };
+    constexpr int PRE = 1;
+    load_x(0);
+    load_units(0, 0, PRE);
 
     // Fused RMSNorm (LI/src/residual.rs:17-33): sum(x^2) over all of x, in f64.
     float inv_rms = 1.f;
@@ -149,12 +176,17 @@ __global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
     const uint32_t abase = alive ? static_cast<uint32_t>(kZeroBytes + 2 * g * sizeof(PlSlot) + (ia & 3) * 16) : 0u;
     const uint32_t astep = alive ? 8u * sizeof(PlSlot) : 0u;
     const int scsh = 8 * g;
-    float acc = 0.f;
+    float acc[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[t] = 0.f;
 
     for (int r = 0; r < R; r++) {
         const int nr = min(UR, nsb - r * UR);  // units of this round (wave-uniform)
         if (nr <= 0) break;
-        if (r > 0) load_round(r);
+        if (r > 0) {
+            load_x(r);
+            load_units(r, 0, PRE);
+        }
         // Digit planes of this lane's EL elements (one sub-block of 32 spans 32 / EL lanes).
         {
             if constexpr (NORM) {
@@ -196,11 +228,14 @@ __global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
             }
             if (r == 0 && lane < kZeroBytes / 16) reinterpret_cast<uint4*>(wl)[lane] = make_uint4(0, 0, 0, 0);
         }
+        load_units(r, PRE, T * UR);
         // the wave reads what its own lanes wrote: keep the LDS accesses in program order
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+#pragma unroll
+        for (int t = 0; t < T; t++)
 #pragma unroll
         for (int u = 0; u < UR; u++) {
             if (u < nr) {
@@ -213,10 +248,10 @@ __global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
                 const v4i A1 = {(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
                 const v4i A2 = {(int)a2.x, (int)a2.y, (int)a2.z, (int)a2.w};
                 const v4i A3 = {(int)a3.x, (int)a3.y, (int)a3.z, (int)a3.w};
-                const v4i B0 = {lo_nib(n0[u].x), hi_nib(n0[u].x), lo_nib(n0[u].y), hi_nib(n0[u].y)};
-                const v4i B1 = {lo_nib(n0[u].z), hi_nib(n0[u].z), lo_nib(n0[u].w), hi_nib(n0[u].w)};
-                const v4i B2 = {lo_nib(n1[u].x), hi_nib(n1[u].x), lo_nib(n1[u].y), hi_nib(n1[u].y)};
-                const v4i B3 = {lo_nib(n1[u].z), hi_nib(n1[u].z), lo_nib(n1[u].w), hi_nib(n1[u].w)};
+                const v4i B0 = {lo_nib(n0[t][u].x), hi_nib(n0[t][u].x), lo_nib(n0[t][u].y), hi_nib(n0[t][u].y)};
+                const v4i B1 = {lo_nib(n0[t][u].z), hi_nib(n0[t][u].z), lo_nib(n0[t][u].w), hi_nib(n0[t][u].w)};
+                const v4i B2 = {lo_nib(n1[t][u].x), hi_nib(n1[t][u].x), lo_nib(n1[t][u].y), hi_nib(n1[t][u].y)};
+                const v4i B3 = {lo_nib(n1[t][u].z), hi_nib(n1[t][u].z), lo_nib(n1[t][u].w), hi_nib(n1[t][u].w)};
                 v4i Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, v4i{0, 0, 0, 0}, 0, 0, 0);
                 v4i Db = __builtin_amdgcn_mfma_i32_16x16x64_i8(A2, B2, v4i{0, 0, 0, 0}, 0, 0, 0);
                 Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, Da, 0, 0, 0);
@@ -224,7 +259,7 @@ __global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
                 // scales of sub-blocks g and g + 4 of row c
                 const PlSlot* sl = slots + 8 * u + 2 * g;
                 const float4 sa = sl[0].s, sb = sl[1].s;
-                const uint4 h = hd[u];
+                const uint4 h = hd[t][u];
                 const float d = h2f(h.x), dmin = h2f(h.x >> 16);
                 const float sc0 = d * static_cast<float>((h.y >> scsh) & 0x3Fu);
                 const float sc1 = d * static_cast<float>((h.z >> scsh) & 0x3Fu);
@@ -233,8 +268,8 @@ __global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
                 // s' (65536 a + 256 b + c): 256 b + c is exact in int32 and in f32 (< 2^24)
                 const float dot0 = fmaf(static_cast<float>(Da[2]), sa.y, sa.x * static_cast<float>(Da[1] * 256 + Da[0]));
                 const float dot1 = fmaf(static_cast<float>(Db[2]), sb.y, sb.x * static_cast<float>(Db[1] * 256 + Db[0]));
-                acc = fmaf(sc0, dot0, fmaf(-mn0, sa.z, acc));
-                acc = fmaf(sc1, dot1, fmaf(-mn1, sb.z, acc));
+                acc[t] = fmaf(sc0, dot0, fmaf(-mn0, sa.z, acc[t]));
+                acc[t] = fmaf(sc1, dot1, fmaf(-mn1, sb.z, acc[t]));
             }
         }
         if (r + 1 < R) {
@@ -246,15 +281,19 @@ __global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
     }
 
     // Row totals: over the four k-groups of the wave, then over the waves in order.
-    acc = swap32_add(acc, acc);
-    acc = swap16_add(acc, acc);
-    if (lane < 16) red[wave * 16 + lane] = acc;
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        float v = swap32_add(acc[t], acc[t]);
+        v = swap16_add(v, v);
+        if (lane < 16) red[(wave * T + t) * 16 + lane] = v;
+    }
     __syncthreads();
-    if (wave == 0 && lane < 16) {
+    if (wave == 0 && lane < 16 * T) {
         float tot = red[lane];
-        for (int w = 1; w < KS; w++) tot += red[w * 16 + lane];
+        for (int w = 1; w < KS; w++) tot += red[w * 16 * T + lane];
+        const int row = static_cast<int>(tile0 * 16) + lane;
         if (a.epi == EPI_SILU_PAIR) {
-            const float up = __shfl_down(tot, 1, 16);
+            const float up = __shfl_down(tot, 1, 64);  // rows 2i, 2i + 1 sit in adjacent lanes of one tile
             if ((lane & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
         } else if (row < a.rows) {
             a.out[row] = a.epi == EPI_RESID ? a.resid[row] + tot : tot;
@@ -262,16 +301,19 @@ __global__ __launch_bounds__(64 * kMaxKS) void q4k_mfma_kernel(MvArgs a) {
     }
 }
 
-template <int UR>
+
+
+template <int UR, int T>
 void launch_q4k_mfma_t(const DevWeight& w, MvArgs a, int R, hipStream_t s) {
     const int S = static_cast<int>(w.cols / 256);
     const int KS = (S + UR * R - 1) / (UR * R);
     a.steps = R;
-    const size_t shmem = static_cast<size_t>(KS) * (wave_lds_bytes<UR>() + 16 * sizeof(float)) +
+    if (KS > max_waves<UR, T>()) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4k matvec: row too long for this split");
+    const size_t shmem = static_cast<size_t>(KS) * (wave_lds_bytes<UR>() + 16 * T * sizeof(float)) +
                          (a.norm_w ? kMaxKS * sizeof(double) : 0);
-    const dim3 grid(static_cast<unsigned>(w.rows_pad / 16)), block(64 * KS);
-    if (a.norm_w) q4k_mfma_kernel<UR, true><<<grid, block, shmem, s>>>(a);
-    else q4k_mfma_kernel<UR, false><<<grid, block, shmem, s>>>(a);
+    const dim3 grid(static_cast<unsigned>(w.rows_pad / (16 * T))), block(64 * KS);
+    if (a.norm_w) q4k_mfma_kernel<UR, T, true><<<grid, block, shmem, s>>>(a);
+    else q4k_mfma_kernel<UR, T, false><<<grid, block, shmem, s>>>(a);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
@@ -288,15 +330,17 @@ void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s) {
     a.qs = w.qs;
     a.hdr = w.hdr;
     if (a.epi == EPI_SILU_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "silu pair epilogue needs even rows");
-    // Four super-blocks per round; two when that leaves fewer than ~12 waves per CU
-    // (small matrices: the fused Q|K|V and O projections of a decode layer).  Rows
-    // longer than 16 waves x 4 super-blocks (K > 16384) take several rounds.
+    // Measured (MI355X, 256 CUs, 16 rotating weight copies): [14336 x 4096] 7.5 us with
+    // two super-blocks per round and four tiles per workgroup (7.7 with 4 x 2, 8.1 with
+    // 4 x 1); [28672 x 4096] 12.8 us, [4096 x 14336] 8.0 us, [6144 x 4096] 4.8 us and
+    // [4096 x 4096] 4.0 us with 4 x 1 (every other split slower).  Rows longer than 16
+    // waves x 4 super-blocks (K > 16384) take several rounds.
     const size_t S = w.cols / 256;
-    const size_t tiles = w.rows_pad / 16;
-    if (S <= 2 * kMaxKS && tiles * ((S + 3) / 4) < 12 * static_cast<size_t>(a.num_cus))
-        launch_q4k_mfma_t<2>(w, a, 1, s);
+    const size_t tiles = w.rows_pad / 16, cus = static_cast<size_t>(a.num_cus);
+    if (S <= 16 && tiles >= 3 * cus && tiles < 6 * cus && w.rows_pad % 64 == 0)
+        launch_q4k_mfma_t<2, 4>(w, a, 1, s);
     else
-        launch_q4k_mfma_t<4>(w, a, static_cast<int>((S + 4 * kMaxKS - 1) / (4 * kMaxKS)), s);
+        launch_q4k_mfma_t<4, 1>(w, a, static_cast<int>((S + 4 * kMaxKS - 1) / (4 * kMaxKS)), s);
 }
 
 }  // namespace larql
