@@ -54,7 +54,9 @@ void run_scores(larql_hip_ctx* c, const KnnPlan& p, size_t n_layers, const float
         int8_t* q8 = static_cast<int8_t*>(larql::ensure(c, c->knn_q8, nq * p.K));
         float* q8s = static_cast<float*>(larql::ensure(c, c->knn_q8s, nq * (p.K / 32) * sizeof(float)));
         larql::launch_quantize_q8(queries, static_cast<size_t>(p.K), nq, q8, q8s, s);
-        larql::launch_gate_scores_q4(p.a, p.b, static_cast<int>(n_layers), q8, q8s, scores, p.F, p.K, Q, s);
+        uint4* xa = static_cast<uint4*>(larql::ensure(c, c->knn_xa, larql::q4_xa_bytes(p.K, Q)));
+        float* xsp = static_cast<float*>(larql::ensure(c, c->knn_xsp, larql::q4_xsp_bytes(p.K, Q)));
+        larql::launch_gate_scores_q4(p.a, p.b, static_cast<int>(n_layers), q8, q8s, xa, xsp, scores, p.F, p.K, Q, s);
     }
 }
 

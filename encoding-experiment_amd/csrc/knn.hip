@@ -106,145 +106,140 @@ __global__ __launch_bounds__(kThreads, 3) void gate_scores_f32_kernel(KnnLayers 
     }
 }
 
-// ── Q4_0 x Q8 scores ───────────────────────────────────────────────────────
-// Workgroup tile: 64 features x 128 queries; thread tile 8 features x 4 queries.
-// Each LDS stage holds two 32-element blocks: the features' nibble bytes and f16
-// scales, and the queries' int8 blocks re-laid out as even / odd element dwords
-// (matching lo / hi nibbles), their f32 scales and their element sums (for the -8
-// offset: isum = sum(nib * x) - 8 sum(x), exact).
-constexpr int kQ4TileF = 64, kQ4TileQ = 128, kQ4Bps = 2;
+// ── Q4_0 x Q8 scores on the matrix cores ───────────────────────────────────
+// v_mfma_i32_16x16x64_i8 gives exact int32 block dots for 16 features x 8 queries x one
+// block pair: B (64 x 16) = the features' codes minus 8 (column c = feature c, k-group g
+// = block g / 2, half g % 2), A (16 x 64) = row 2m + h holding query m's int8 block
+// 2bp + h in that block's k-groups and zeros in the other block's, so D[2m + h][c] is
+// block 2bp + h's dot sum((nib - 8) * x) for query m and feature c.  D lane (g, c)
+// holds queries 2g and 2g + 1 of the group, both blocks of the pair: the lane forms
+// (float)isum * (f16(d) * xs) and adds it to the query's running sum in block order,
+// exactly as the reference's serial loop (product and sum rounded separately).
+// The queries are laid out once per walk (q4_xa_kernel) as the A operands of every
+// (block pair, group of 8 queries), zeros included, plus their block scales; a
+// workgroup (64 features x 128 queries) stages one block pair of them in LDS per step.
+constexpr int kQ4TileF = 64, kQ4TileG = 16;  // features, groups of 8 queries
 
-__device__ __forceinline__ uint32_t pick4(uint32_t a, uint32_t b, uint32_t sel) {
-    return __builtin_amdgcn_perm(b, a, sel);
+// XA[bp][G][lane][16 B], XSP[bp][G][8 m][2 h] = xs of query 8G + m, block 2bp + h.
+// One thread per (bp, G, lane).  Element order within a 16-element half block matches
+// the nibble unpack: even elements 0..6, odd 1..7, even 8..14, odd 9..15.
+__global__ void q4_xa_kernel(const int8_t* __restrict__ X8, const float* __restrict__ XS, uint4* __restrict__ XA,
+                             float* __restrict__ XSP, int K, int Q, int ng) {
+    const size_t t = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    const int nbp = K / 64, nb = K / 32;
+    if (t >= static_cast<size_t>(nbp) * ng * 64) return;
+    const int lane = static_cast<int>(t & 63);
+    const size_t bg = t >> 6;
+    const int G = static_cast<int>(bg % ng), bp = static_cast<int>(bg / ng);
+    const int g = lane >> 4, i = lane & 15, m = i >> 1, h = i & 1;
+    const int q = 8 * G + m;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if ((g >> 1) == h && q < Q) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(X8 + static_cast<size_t>(q) * K + (2 * bp + h) * 32 + 16 * (g & 1));
+        v.x = __builtin_amdgcn_perm(raw.y, raw.x, 0x06040200u);  // elements 0, 2, 4, 6
+        v.y = __builtin_amdgcn_perm(raw.y, raw.x, 0x07050301u);  // 1, 3, 5, 7
+        v.z = __builtin_amdgcn_perm(raw.w, raw.z, 0x06040200u);  // 8 .. 14
+        v.w = __builtin_amdgcn_perm(raw.w, raw.z, 0x07050301u);  // 9 .. 15
+    }
+    XA[t] = v;
+    if (lane < 16) XSP[bg * 16 + lane] = q < Q ? XS[static_cast<size_t>(q) * nb + 2 * bp + h] : 0.f;
 }
 
-__global__ __launch_bounds__(kThreads, 2) void gate_scores_q4_kernel(KnnLayers g, KnnLayers gd, const int8_t* __restrict__ X8,
-                                                                  const float* __restrict__ XS, float* __restrict__ S,
-                                                                  int F, int K, int Q) {
-    __shared__ uint4 Gn[2][kQ4Bps][kQ4TileF];        // nibble bytes
-    __shared__ float Gd[2][kQ4Bps][kQ4TileF];        // decoded scales
-    __shared__ uint4 Xb[2][kQ4Bps][kQ4TileQ][2];     // even dwords, odd dwords
-    __shared__ float Xsc[2][kQ4Bps][kQ4TileQ];
-    __shared__ int Xsum[2][kQ4Bps][kQ4TileQ];
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+// Bytes of the codes minus 8 (signed), without borrows between bytes.
+__device__ __forceinline__ int nib_s8(uint32_t w4) {
+    return static_cast<int>(((w4 | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+}
+
+// Grid (F / 64, ceil(groups / 16), layers); wave w: features f0 + 16 w + c.
+__global__ __launch_bounds__(kThreads, 2) void gate_scores_q4_kernel(KnnLayers g, KnnLayers gd,
+                                                                  const uint4* __restrict__ XA,
+                                                                  const float* __restrict__ XSP, float* __restrict__ S,
+                                                                  int F, int K, int Q, int ng) {
+    __shared__ uint4 As[2][kQ4TileG][64];
+    __shared__ float4 Xs[2][kQ4TileG][4];
     const int l = blockIdx.z;
     const uint8_t* __restrict__ nib = static_cast<const uint8_t*>(g.p[l]);
     const uint16_t* __restrict__ dsc = static_cast<const uint16_t*>(gd.p[l]);
-    const int f0 = blockIdx.x * kQ4TileF, q0 = blockIdx.y * kQ4TileQ;
-    const int tid = threadIdx.x;
-    const int tf = tid >> 5, tq = tid & 31;  // features f0 + 8 tf .., queries q0 + 4 tq ..
-    const int nb = K / 32;
-    // global -> LDS mapping: features: threads 0..127 -> (block tid >> 6, feature tid & 63);
-    // queries: all 256 threads -> (block tid >> 7, query tid & 127)
-    const int gfb = (tid >> 6) & 1, gff = tid & 63;
-    const size_t grow = static_cast<size_t>(min(f0 + gff, F - 1));
-    const int xqb = tid >> 7, xqq = tid & 127;
-    const size_t xrow = static_cast<size_t>(min(q0 + xqq, Q - 1));
-    uint4 gr = make_uint4(0, 0, 0, 0);
-    uint16_t gdr = 0;
-    uint4 xr0, xr1;
-    float xsr;
-    auto gload = [&](int b0) __attribute__((always_inline)) {
-        if (tid < 128) {
-            const int b = b0 + gfb;
-            gr = *reinterpret_cast<const uint4*>(nib + grow * (K / 2) + static_cast<size_t>(b) * 16);
-            gdr = dsc[grow * nb + b];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int gl = lane >> 4, c = lane & 15;
+    const int G0 = blockIdx.y * kQ4TileG, nG = min(kQ4TileG, ng - G0);
+    const int f = min(blockIdx.x * kQ4TileF + 16 * wave + c, F - 1);
+    const int nbp = K / 64, nb = K / 32;
+    const uint8_t* wrow = nib + static_cast<size_t>(f) * (K / 2) + (gl >> 1) * 16 + (gl & 1) * 8;
+    const uint32_t* drow = reinterpret_cast<const uint32_t*>(dsc + static_cast<size_t>(f) * nb);
+
+    // staging: thread tid covers A items tid + 256 j of the tile's 16 x 64, and (tid < 64)
+    // one float4 of the scales
+    uint4 ar[4];
+    float4 xr = make_float4(0.f, 0.f, 0.f, 0.f);
+    uint2 wr;
+    uint32_t dr;
+    auto gload = [&](int bp) __attribute__((always_inline)) {
+        const uint4* src = XA + (static_cast<size_t>(bp) * ng + G0) * 64;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int it = tid + 256 * j;
+            ar[j] = (it >> 6) < nG ? src[it] : make_uint4(0, 0, 0, 0);
         }
-        const int b = b0 + xqb;
-        const uint4* xp = reinterpret_cast<const uint4*>(X8 + xrow * K + static_cast<size_t>(b) * 32);
-        xr0 = xp[0];
-        xr1 = xp[1];
-        xsr = XS[xrow * nb + b];
+        if (tid < 64 && (tid >> 2) < nG)
+            xr = reinterpret_cast<const float4*>(XSP + (static_cast<size_t>(bp) * ng + G0) * 16)[tid];
+        wr = *reinterpret_cast<const uint2*>(wrow + static_cast<size_t>(bp) * 32);
+        dr = drow[bp];
     };
     auto lstore = [&](int s) __attribute__((always_inline)) {
-        if (tid < 128) {
-            Gn[s][gfb][gff] = gr;
-            Gd[s][gfb][gff] = h2f(gdr);
-        }
-        // natural order dwords w0..w7 hold elements 4w..4w+3; even dword i needs elements
-        // 8i, 8i+2, 8i+4, 8i+6 = bytes 0, 2 of w(2i) and bytes 0, 2 of w(2i+1)
-        const uint32_t w[8] = {xr0.x, xr0.y, xr0.z, xr0.w, xr1.x, xr1.y, xr1.z, xr1.w};
-        uint32_t ev[4], od[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            ev[i] = pick4(w[2 * i], w[2 * i + 1], 0x06040200u);
-            od[i] = pick4(w[2 * i], w[2 * i + 1], 0x07050301u);
+        for (int j = 0; j < 4; j++) {
+            const int it = tid + 256 * j;
+            As[s][it >> 6][it & 63] = ar[j];
         }
-        int sum = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) sum = __builtin_amdgcn_sdot4(static_cast<int>(w[i]), 0x01010101, sum, false);
-        Xb[s][xqb][xqq][0] = make_uint4(ev[0], ev[1], ev[2], ev[3]);
-        Xb[s][xqb][xqq][1] = make_uint4(od[0], od[1], od[2], od[3]);
-        Xsc[s][xqb][xqq] = xsr;
-        Xsum[s][xqb][xqq] = sum;
+        if (tid < 64) Xs[s][tid >> 2][tid & 3] = xr;
     };
 
-    float acc[8][4];
+    float acc[kQ4TileG][2];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = 0.f;
+    for (int G = 0; G < kQ4TileG; G++) acc[G][0] = acc[G][1] = 0.f;
 
-    const int ns = nb / kQ4Bps;
     gload(0);
     lstore(0);
     __syncthreads();
-    for (int st = 0; st < ns; st++) {
-        const int s = st & 1;
-        if (st + 1 < ns) gload((st + 1) * kQ4Bps);
+    for (int bp = 0; bp < nbp; bp++) {
+        const int s = bp & 1;
+        const uint2 w = wr;
+        const uint32_t dw = dr;
+        if (bp + 1 < nbp) gload(bp + 1);
+        const v4i_t B = {nib_s8(w.x & 0x0F0F0F0Fu), nib_s8((w.x >> 4) & 0x0F0F0F0Fu), nib_s8(w.y & 0x0F0F0F0Fu),
+                         nib_s8((w.y >> 4) & 0x0F0F0F0Fu)};
+        const float d0 = h2f(dw), d1 = h2f(dw >> 16);
 #pragma unroll
-        for (int bb = 0; bb < kQ4Bps; bb++) {
-            // the four queries' x words, then one feature at a time
-            uint32_t ew[4][4], ow[4][4];
-            float xs[4];
-            int off[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int qq = tq * 4 + j;
-                const uint4 e = Xb[s][bb][qq][0], o = Xb[s][bb][qq][1];
-                ew[j][0] = e.x; ew[j][1] = e.y; ew[j][2] = e.z; ew[j][3] = e.w;
-                ow[j][0] = o.x; ow[j][1] = o.y; ow[j][2] = o.z; ow[j][3] = o.w;
-                xs[j] = Xsc[s][bb][qq];
-                off[j] = 8 * Xsum[s][bb][qq];
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const uint4 v = Gn[s][bb][tf * 8 + i];
-                const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-                uint32_t lo[4], hi[4];
-#pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    lo[w] = vw[w] & 0x0F0F0F0Fu;
-                    hi[w] = (vw[w] >> 4) & 0x0F0F0F0Fu;
-                }
-                const float d = Gd[s][bb][tf * 8 + i];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    int isum = 0;
-#pragma unroll
-                    for (int w = 0; w < 4; w++) {
-                        isum = __builtin_amdgcn_sdot4(static_cast<int>(lo[w]), static_cast<int>(ew[j][w]), isum, false);
-                        isum = __builtin_amdgcn_sdot4(static_cast<int>(hi[w]), static_cast<int>(ow[j][w]), isum, false);
-                    }
-                    // reference order: cs = f16(s) * q8s; acc += (float)isum * cs, product and
-                    // sum rounded separately (fp contract is off in this file)
-                    const float cs = d * xs[j];
-                    const float prod = static_cast<float>(isum - off[j]) * cs;
-                    acc[i][j] = acc[i][j] + prod;
-                }
+        for (int G = 0; G < kQ4TileG; G++) {
+            if (G < nG) {
+                const uint4 av = As[s][G][lane];
+                const v4i_t A = {static_cast<int>(av.x), static_cast<int>(av.y), static_cast<int>(av.z),
+                                 static_cast<int>(av.w)};
+                const v4i_t D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, v4i_t{0, 0, 0, 0}, 0, 0, 0);
+                const float4 xs = Xs[s][G][gl];  // xs of queries 2g, 2g + 1, blocks 2bp, 2bp + 1
+                // reference order: cs = f16(s) * q8s; acc += (float)isum * cs
+                acc[G][0] = acc[G][0] + static_cast<float>(D[0]) * (d0 * xs.x);
+                acc[G][0] = acc[G][0] + static_cast<float>(D[1]) * (d1 * xs.y);
+                acc[G][1] = acc[G][1] + static_cast<float>(D[2]) * (d0 * xs.z);
+                acc[G][1] = acc[G][1] + static_cast<float>(D[3]) * (d1 * xs.w);
             }
         }
-        if (st + 1 < ns) lstore(s ^ 1);
+        // buffer s ^ 1 was last read in step bp - 1, before that step's barrier
+        if (bp + 1 < nbp) lstore(s ^ 1);
         __syncthreads();
     }
+    const int fo = blockIdx.x * kQ4TileF + 16 * wave + c;
+    if (fo >= F) return;
     float* Sl = S + static_cast<size_t>(l) * Q * F;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int q = q0 + tq * 4 + j;
-        if (q >= Q) continue;
+    for (int G = 0; G < kQ4TileG; G++) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int f = f0 + tf * 8 + i;
-            if (f < F) Sl[static_cast<size_t>(q) * F + f] = acc[i][j];
+        for (int j = 0; j < 2; j++) {
+            const int q = 8 * (G0 + G) + 2 * gl + j;
+            if (G < nG && q < Q) Sl[static_cast<size_t>(q) * F + fo] = acc[G][j];
         }
     }
 }
@@ -379,12 +374,19 @@ void launch_gate_scores_f32(const KnnLayers& g, int n_layers, const float* X, fl
 }
 
 void launch_gate_scores_q4(const KnnLayers& nib, const KnnLayers& scales, int n_layers, const int8_t* X8,
-                           const float* XS, float* S, int F, int K, int Q, hipStream_t s) {
-    if (K % (32 * kQ4Bps)) fail(LARQL_HIP_ERR_INVALID, "gate scores: Q4_0 hidden must be a multiple of 64");
-    const dim3 grid((F + kQ4TileF - 1) / kQ4TileF, (Q + kQ4TileQ - 1) / kQ4TileQ, n_layers);
-    gate_scores_q4_kernel<<<grid, dim3(kThreads), 0, s>>>(nib, scales, X8, XS, S, F, K, Q);
+                           const float* XS, uint4* XA, float* XSP, float* S, int F, int K, int Q, hipStream_t s) {
+    if (K % 64) fail(LARQL_HIP_ERR_INVALID, "gate scores: Q4_0 hidden must be a multiple of 64");
+    const int ng = (Q + 7) / 8;
+    const size_t nxa = static_cast<size_t>(K / 64) * ng * 64;
+    q4_xa_kernel<<<dim3(static_cast<unsigned>((nxa + 255) / 256)), dim3(256), 0, s>>>(X8, XS, XA, XSP, K, Q, ng);
+    LARQL_HIP_CHECK(hipGetLastError());
+    const dim3 grid((F + kQ4TileF - 1) / kQ4TileF, (ng + kQ4TileG - 1) / kQ4TileG, n_layers);
+    gate_scores_q4_kernel<<<grid, dim3(kThreads), 0, s>>>(nib, scales, XA, XSP, S, F, K, Q, ng);
     LARQL_HIP_CHECK(hipGetLastError());
 }
+
+size_t q4_xa_bytes(int K, int Q) { return static_cast<size_t>(K / 64) * ((Q + 7) / 8) * 64 * sizeof(uint4); }
+size_t q4_xsp_bytes(int K, int Q) { return static_cast<size_t>(K / 64) * ((Q + 7) / 8) * 16 * sizeof(float); }
 
 void launch_topk(const float* S, size_t rows, size_t row_stride, int n, int k, int signed_mode, uint32_t* idx,
                  float* val, hipStream_t s) {

@@ -150,7 +150,7 @@ struct larql_hip_ctx {
     // reusable device staging buffers for host-pointer calls
     larql::DeviceBuf stage_in, stage_in2, stage_out, stage_raw, scratch;
     // gate-KNN work buffers: scores [layers][nq][features], quantized queries
-    larql::DeviceBuf knn_scores, knn_q8, knn_q8s, knn_idx, knn_val, knn_handles;
+    larql::DeviceBuf knn_scores, knn_q8, knn_q8s, knn_idx, knn_val, knn_handles, knn_xa, knn_xsp;
     // q4_vecmat chunk partials; pair-batch quantized activations
     larql::DeviceBuf vecmat_part, pair_q8, pair_q8s;
     larql::KVCache kv;
