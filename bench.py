@@ -351,12 +351,12 @@ def bench_configs(be, torch, stream, copies: int):
     for name, hs, peak, unit in (("f32", hf, 157.3, "TFLOP/s"), ("q4_0", hq, 5000.0, "TOP/s")):
         us = _time_us(torch, stream, lambda i: be.gate_knn_dev(hs, q, Q, k, di, dv, stream=stream), 10, warm=2)
         t = flops / (us * 1e-6) / 1e12
-        bound = "valu-fp32" if name == "f32" else "int8-dot"
+        bound = "valu-fp32" if name == "f32" else "mfma-int8"
         out[f"gate_knn_{name}_34x10240x2560_q256_top32"] = {
             "ms_per_walk": round(us / 1e3, 3), "ops": flops, "achieved": round(t, 1), "unit": unit,
             "roofline": {"bound": bound, "peak": peak, "unit": unit, "frac": round(t / peak, 4)},
             "note": "f32 scores are canonical fma chains (bit-exact, no MFMA); Q4_0 int32 block dots "
-                    "on VALU v_dot4 vs the int8 MFMA peak"}
+                    "on v_mfma_i32_16x16x64_i8 vs the int8 MFMA peak; walk includes top-32 selection"}
         log(f"[bench] gate_knn {name}: {out[f'gate_knn_{name}_34x10240x2560_q256_top32']}")
     for h in hf + hq:
         be.release_weight(h)
@@ -555,7 +555,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8 (4-bit codes) x f32, int32 v_dot4",
+        "dtype": "u8 (4-bit codes) x i8 digit planes of f32 x, int32 MFMA",
         "data": "synthetic: W ~ N(0,0.02) quantized to 148-byte Q4_K on device, x ~ N(0,1)",
         "config": {
             "workload": "Q4_K matvec trio at Llama-3-8B FFN shapes: gate/up [14336x4096], down [4096x14336], batch 1",

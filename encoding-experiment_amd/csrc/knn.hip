@@ -257,45 +257,35 @@ __device__ __forceinline__ uint32_t order_key(float v, int signed_mode) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-template <int PER>
-__global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ S, size_t row_stride, int n, int k,
-                                                        int signed_mode, uint32_t* __restrict__ idx_out,
-                                                        float* __restrict__ val_out) {
-    __shared__ uint32_t hist[kThreads / 64][256];
-    __shared__ uint64_t sel_prefix;
-    __shared__ int sel_remaining;
-    __shared__ int cnt;
-    __shared__ uint64_t cand_c[kTopkMaxK];
-    __shared__ float cand_v[kTopkMaxK];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float* __restrict__ s = S + static_cast<size_t>(blockIdx.x) * row_stride;
-    // element i = tid + kThreads * j (coalesced); held in registers when PER > 0
-    uint32_t key[PER > 0 ? PER : 1];
-    if constexpr (PER > 0) {
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int i = tid + kThreads * j;
-            key[j] = i < n ? order_key(s[i], signed_mode) : 0u;
-        }
-    }
-    auto comp = [&](int j, int i) __attribute__((always_inline)) -> uint64_t {
-        const uint32_t kk = PER > 0 ? key[j] : order_key(s[i], signed_mode);
-        return (static_cast<uint64_t>(kk) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(i));
-    };
-    const int nper = PER > 0 ? PER : (n + kThreads - 1) / kThreads;
+// Inclusive scan of one value per lane over the wave (DPP within rows of 16, then the
+// row totals through SGPRs).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    const int lane = threadIdx.x & 63;
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    const uint32_t r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+                   r2 = __builtin_amdgcn_readlane(v, 47);
+    const int row = lane >> 4;
+    return v + (row >= 1 ? r0 : 0u) + (row >= 2 ? r1 : 0u) + (row >= 3 ? r2 : 0u);
+}
 
-    uint64_t prefix = 0, pmask = 0;
+// Radix select of the k-th largest 32-bit key among the values every thread visits
+// (gen(visit) makes the same visits in every pass): four passes of 8-bit digits.
+// Returns the key; *above = number of visited values strictly greater than it.
+template <class Gen>
+__device__ __forceinline__ uint32_t select_kth32(int k, Gen gen, uint32_t (*hist)[256], uint32_t* sel, int* above) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t prefix = 0, pmask = 0;
     int remaining = k;
-    for (int pass = 0; pass < 8; pass++) {
-        const int shift = 56 - 8 * pass;
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
         for (int i = tid; i < (kThreads / 64) * 256; i += kThreads) (&hist[0][0])[i] = 0u;
         __syncthreads();
-        for (int j = 0; j < nper; j++) {
-            const int i = tid + kThreads * j;
-            if (i >= n) break;
-            const uint64_t c = comp(j, i);
+        gen([&](uint32_t c) __attribute__((always_inline)) {
             if ((c & pmask) == prefix) atomicAdd(&hist[wave][(c >> shift) & 0xFF], 1u);
-        }
+        });
         __syncthreads();
         if (wave == 0) {
             // lane covers digits 255 - 4 lane .. 252 - 4 lane (descending)
@@ -306,16 +296,9 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
                 h[u] = hist[0][dgt] + hist[1][dgt] + hist[2][dgt] + hist[3][dgt];
                 tot += h[u];
             }
-            // inclusive scan over lanes (descending digit order)
-            uint32_t incl = tot;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t v = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += v;
-            }
+            const uint32_t incl = wave_incl_scan(tot);
             const uint32_t excl = incl - tot;
-            const bool here = excl < static_cast<uint32_t>(remaining) && incl >= static_cast<uint32_t>(remaining);
-            if (here) {
+            if (excl < static_cast<uint32_t>(remaining) && incl >= static_cast<uint32_t>(remaining)) {
                 uint32_t cum = excl;
                 int dsel = 0, rem = remaining;
 #pragma unroll
@@ -327,39 +310,146 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
                     }
                     cum += h[u];
                 }
-                sel_prefix = prefix | (static_cast<uint64_t>(dsel) << shift);
-                sel_remaining = rem;
+                sel[0] = prefix | (static_cast<uint32_t>(dsel) << shift);
+                sel[1] = static_cast<uint32_t>(rem);
             }
         }
         __syncthreads();
-        prefix = sel_prefix;
-        remaining = sel_remaining;
-        pmask |= static_cast<uint64_t>(0xFF) << shift;
+        prefix = sel[0];
+        remaining = static_cast<int>(sel[1]);
+        pmask |= 0xFFu << shift;
         __syncthreads();
     }
-    // prefix is now the k-th largest composite: collect the k elements >= it
-    if (tid == 0) cnt = 0;
-    __syncthreads();
-    for (int j = 0; j < nper; j++) {
-        const int i = tid + kThreads * j;
-        if (i >= n) break;
-        const uint64_t c = comp(j, i);
-        if (c >= prefix) {
-            const int p = atomicAdd(&cnt, 1);
-            if (p < kTopkMaxK) {
-                cand_c[p] = c;
-                cand_v[p] = s[i];
+    *above = k - remaining;
+    return prefix;
+}
+
+constexpr int kTopkCap = 2048;  // candidates kept in LDS
+
+// One workgroup per row.  Order: key descending, index ascending (the composite
+// key << 32 | (0xFFFFFFFF - index), unique per element).  T, the k-th largest of the 256
+// per-thread maximum keys, is a lower bound of the k-th largest key (k distinct threads
+// hold an element >= T), so the elements with key >= T are compacted into LDS (the
+// score magnitudes of a row share their top key bits: a select over every element would
+// spend its passes on them) and the exact select runs there: the k-th largest key K,
+// every element above it, then the elements equal to K in index order.  Rows whose
+// candidates overflow the LDS list run the select over all elements instead.
+template <int PER>
+__global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ S, size_t row_stride, int n, int k,
+                                                        int signed_mode, uint32_t* __restrict__ idx_out,
+                                                        float* __restrict__ val_out) {
+    __shared__ uint32_t hist[kThreads / 64][256];
+    __shared__ uint32_t sel[2];
+    __shared__ int cnt, nout;
+    __shared__ uint32_t ckey[kTopkCap], cidx[kTopkCap];
+    __shared__ uint64_t out_c[kTopkMaxK];
+    __shared__ float out_v[kTopkMaxK];
+    const int tid = threadIdx.x;
+    const float* __restrict__ s = S + static_cast<size_t>(blockIdx.x) * row_stride;
+    // element i = tid + kThreads * j (coalesced); held in registers when PER > 0
+    uint32_t key[PER > 0 ? PER : 1];
+    if constexpr (PER > 0) {
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int i = tid + kThreads * j;
+            key[j] = i < n ? order_key(s[i], signed_mode) : 0u;
+        }
+    }
+    const int nper = (n + kThreads - 1) / kThreads;
+    // f(key, i) for this thread's elements i = tid + kThreads * j < n
+    auto each = [&](auto f) __attribute__((always_inline)) {
+        if constexpr (PER > 0) {
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int i = tid + kThreads * j;
+                if (i < n) f(key[j], i);
+            }
+        } else {
+            for (int j = 0; j < nper; j++) {
+                const int i = tid + kThreads * j;
+                if (i >= n) break;
+                f(order_key(s[i], signed_mode), i);
             }
         }
+    };
+
+    // 1. T: the k-th largest per-thread maximum key (threads without elements do not vote)
+    uint32_t kmax = 0;
+    bool has = false;
+    each([&](uint32_t kk, int) __attribute__((always_inline)) {
+        kmax = max(kmax, kk);
+        has = true;
+    });
+    int above = 0;
+    const uint32_t T = select_kth32(
+        k, [&](auto visit) __attribute__((always_inline)) { if (has) visit(kmax); }, hist, sel, &above);
+
+    // 2. candidates (key >= T) into LDS
+    if (tid == 0) cnt = 0;
+    __syncthreads();
+    each([&](uint32_t kk, int i) __attribute__((always_inline)) {
+        if (kk >= T) {
+            const int p = atomicAdd(&cnt, 1);
+            if (p < kTopkCap) {
+                ckey[p] = kk;
+                cidx[p] = static_cast<uint32_t>(i);
+            }
+        }
+    });
+    __syncthreads();
+    const int nc = cnt;
+    const bool inlds = nc <= kTopkCap;
+
+    // 3. K = the k-th largest key; `above` elements are strictly greater
+    const uint32_t K = inlds ? select_kth32(
+                                   k,
+                                   [&](auto visit) __attribute__((always_inline)) {
+                                       for (int p = tid; p < nc; p += kThreads) visit(ckey[p]);
+                                   },
+                                   hist, sel, &above)
+                             : select_kth32(
+                                   k,
+                                   [&](auto visit) __attribute__((always_inline)) {
+                                       each([&](uint32_t kk, int) __attribute__((always_inline)) { visit(kk); });
+                                   },
+                                   hist, sel, &above);
+
+    // 4. the k winners: every key > K, then the (k - above) lowest indices with key == K
+    if (tid == 0) nout = 0;
+    __syncthreads();
+    auto consider = [&](uint32_t kk, uint32_t i) __attribute__((always_inline)) {
+        if (kk > K) {
+            const int p = atomicAdd(&nout, 1);
+            out_c[p] = (static_cast<uint64_t>(kk) << 32) | (0xFFFFFFFFu - i);
+            out_v[p] = s[i];
+        } else if (kk == K) {
+            // rank among the ties by index; only the first (k - above) are kept
+            int r = 0;
+            if (inlds) {
+                for (int p = 0; p < nc; p++) r += (ckey[p] == K) & (cidx[p] < i);
+            } else {  // more than kTopkCap candidates: count over the row itself
+                for (int i2 = 0; i2 < static_cast<int>(i); i2++) r += order_key(s[i2], signed_mode) == K;
+            }
+            if (r < k - above) {
+                const int p = above + r;
+                out_c[p] = (static_cast<uint64_t>(kk) << 32) | (0xFFFFFFFFu - i);
+                out_v[p] = s[i];
+            }
+        }
+    };
+    if (inlds) {
+        for (int p = tid; p < nc; p += kThreads) consider(ckey[p], cidx[p]);
+    } else {
+        each([&](uint32_t kk, int i) __attribute__((always_inline)) { consider(kk, static_cast<uint32_t>(i)); });
     }
     __syncthreads();
     if (tid < k) {
-        const uint64_t me = cand_c[tid];
+        const uint64_t me = out_c[tid];
         int rank = 0;
-        for (int j = 0; j < k; j++) rank += cand_c[j] > me;
+        for (int j = 0; j < k; j++) rank += out_c[j] > me;
         const size_t o = static_cast<size_t>(blockIdx.x) * k + rank;
         idx_out[o] = 0xFFFFFFFFu - static_cast<uint32_t>(me & 0xFFFFFFFFu);
-        val_out[o] = cand_v[tid];
+        val_out[o] = out_v[tid];
     }
 }
 
