@@ -209,7 +209,7 @@ extern "C" void larql_hip_ctx_destroy(larql_hip_ctx* c) {
         }
         for (auto* b : {&c->stage_in, &c->stage_in2, &c->stage_out, &c->stage_raw, &c->scratch, &c->knn_scores,
                         &c->knn_q8, &c->knn_q8s, &c->knn_idx, &c->knn_val, &c->knn_handles, &c->vecmat_part,
-                        &c->pair_q8, &c->pair_q8s, &c->knn_xa, &c->knn_xsp})
+                        &c->pair_q8, &c->pair_q8s, &c->knn_xa, &c->knn_xsp, &c->gemm_x16})
             if (b->p) (void)hipFree(b->p);
         (void)hipStreamDestroy(c->stream);
     }
@@ -283,7 +283,7 @@ extern "C" int larql_hip_q4k_matvec(larql_hip_ctx* c, const uint8_t* q4k_data, s
         const DevWeight& w = larql::cached_weight(c, LARQL_Q4_K, q4k_data, q4k_len, nullptr, num_rows, hidden);
         const float* dx = stage_upload(c, c->stage_in, x, hidden);
         float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, num_rows * sizeof(float)));
-        larql::launch_q4k_matvec(w, dx, dout, 1, c->stream);
+        larql::launch_q4k_matvec(w, dx, dout, 1, nullptr, c->stream);
         download(c, out, dout, num_rows * sizeof(float));
     });
 }
@@ -295,7 +295,8 @@ extern "C" int larql_hip_q4k_matmul(larql_hip_ctx* c, const uint8_t* q4k_data, s
         const DevWeight& w = larql::cached_weight(c, LARQL_Q4_K, q4k_data, q4k_len, nullptr, num_rows, hidden);
         const float* dx = stage_upload(c, c->stage_in, x, m * hidden);
         float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, m * num_rows * sizeof(float)));
-        larql::launch_q4k_matvec(w, dx, dout, m, c->stream);
+        void* ws = m > 1 ? larql::ensure(c, c->gemm_x16, larql::q4k_gemm_ws_bytes(m, hidden)) : nullptr;
+        larql::launch_q4k_matvec(w, dx, dout, m, ws, c->stream);
         download(c, out, dout, m * num_rows * sizeof(float));
     });
 }
@@ -432,7 +433,11 @@ extern "C" int larql_hip_matvec_dev(larql_hip_ctx* c, uint64_t handle, const voi
         if (!x || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
         hipStream_t s = pick_stream(c, stream);
         switch (w.format) {
-            case LARQL_Q4_K: larql::launch_q4k_matvec(w, static_cast<const float*>(x), out, m, s); break;
+            case LARQL_Q4_K: {
+                void* ws = m > 1 ? larql::ensure(c, c->gemm_x16, larql::q4k_gemm_ws_bytes(m, w.cols)) : nullptr;
+                larql::launch_q4k_matvec(w, static_cast<const float*>(x), out, m, ws, s);
+                break;
+            }
             case LARQL_Q6_K: larql::launch_q6k_matvec(w, static_cast<const float*>(x), out, m, s); break;
             case LARQL_Q4_0:
                 if (!x_scales) fail(LARQL_HIP_ERR_INVALID, "Q4_0 matvec needs Q8 activation scales");

@@ -153,6 +153,8 @@ struct larql_hip_ctx {
     larql::DeviceBuf knn_scores, knn_q8, knn_q8s, knn_idx, knn_val, knn_handles, knn_xa, knn_xsp;
     // q4_vecmat chunk partials; pair-batch quantized activations
     larql::DeviceBuf vecmat_part, pair_q8, pair_q8s;
+    // prefill GEMM: X as fp16 MFMA operands
+    larql::DeviceBuf gemm_x16;
     larql::KVCache kv;
     // model built by the last host-pointer decode_token (re-used while its key matches)
     larql_hip_model* trait_model = nullptr;
@@ -171,10 +173,13 @@ const DevWeight& cached_weight(larql_hip_ctx* c, int format, const void* data, s
                                const float* q8_scales, size_t rows, size_t cols);
 
 // ── kernel launchers (device pointers; enqueue only) ───────────────────
-void launch_q4k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s);
+// m > 1 runs the prefill GEMM and needs `ws` of q4k_gemm_ws_bytes(m, cols) bytes.
+void launch_q4k_matvec(const DevWeight& w, const float* x, float* out, size_t m, void* ws, hipStream_t s);
 void launch_q6k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s);
-// Y[m][rows] = X[m][cols] . deq(W)^T, Q4_K, on MFMA (prefill.hip).
-void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, hipStream_t s);
+// Y[m][rows] = X[m][cols] . deq(W)^T, Q4_K, on MFMA (prefill.hip); ws holds X as fp16
+// MFMA operands.
+size_t q4k_gemm_ws_bytes(size_t m, size_t cols);
+void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, void* ws, hipStream_t s);
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
                         size_t m, hipStream_t s);
 void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,

@@ -228,8 +228,8 @@ void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s) {
     }
 }
 
-void launch_q4k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s) {
-    if (m > 1) return launch_q4k_gemm(w, x, out, m, s);  // prefill: m tokens on the matrix cores
+void launch_q4k_matvec(const DevWeight& w, const float* x, float* out, size_t m, void* ws, hipStream_t s) {
+    if (m > 1) return launch_q4k_gemm(w, x, out, m, ws, s);  // prefill: m tokens on the matrix cores
     MvArgs a;
     a.x = x;
     a.out = out;

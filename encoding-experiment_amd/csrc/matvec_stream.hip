@@ -156,10 +156,6 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
     }
 
     // 2. The first D - 1 units.
-    const int j = lane & 7;  // sub-block index within its super-block, the same in every pass
-    const int scsh = 8 * (j & 3);
-    const int msh = 8 * (j & 3) + (j < 4 ? 0 : 4);
-    const bool scsel = j < 4;
     const float* rsrc = a.resid ? a.resid : a.x;
 
     Unit<FMT, RB> buf[D];

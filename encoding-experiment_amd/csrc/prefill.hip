@@ -4,10 +4,18 @@
 // Reference semantics: the trait's prefill (LC/src/backend.rs:143-152) runs, per token,
 // the Q4_K matvec (LC/src/cpu/ops/q4k_matvec.rs:31-90; the Metal prefill is that matvec
 // in a loop over positions, LC/src/metal/prefill.rs:21-110).  Here the M matvecs are one
-// GEMM on the matrix cores:
-//   * the loaders dequantize each 32-element sub-block of W (d * sc_j * q - dmin * m_j in
-//     f32, then fp16) and convert X to fp16, straight into LDS (double-buffered);
-//   * v_mfma_f32_16x16x32_f16 accumulates in f32.
+// GEMM on the matrix cores, v_mfma_f32_16x16x32_f16 with f32 accumulation:
+//   * x16_pack_kernel converts X to fp16 once, laid out as ready-made A operands:
+//     one 1 KB block (64 lanes x 8 halves) per (16 tokens, super-block, half, step);
+//   * the GEMM streams the tile-major Q4_K weights (one coalesced 1 KB load per 16 rows
+//     and half super-block) and dequantizes them in registers into B operands,
+//     w = (1024 + q) * (d sc_j) - (1024 d sc_j + dmin m_j) in one f32 fma per element,
+//     rounded to fp16 (the same value as d sc_j q - dmin m_j, to ~2^-14 d sc_j);
+//   * the A blocks of a workgroup's 64 tokens go through LDS, double-buffered, and are
+//     shared by its four waves; each wave owns 80 weight rows.
+// The MFMA k order within a step is free as long as A and B agree: lane (g, c) of step s
+// in half h supplies elements 8s + {0,4,1,5,2,6,3,7} of sub-block 4h + g (the order in
+// which the nibble bytes unpack), and x16_pack_kernel writes X in that order.
 // fp16 operands carry 11 significant bits: over K = 2560 random terms the error is
 // ~1e-4 of max|Y|, inside the 1e-3 bar.
 #include "device_common.h"
@@ -19,120 +27,240 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
-constexpr int kMt = 128, kNt = 128, kKs = 32;
-constexpr int kRow = kKs + 8;  // LDS row pitch in halves (80 bytes: conflict-free 16-lane reads)
+constexpr int kMt = 4;                 // 16-token tiles per workgroup (64 tokens)
+constexpr int kNT = 5;                 // 16-row weight tiles per wave (80 rows)
+constexpr int kWaves = 4;              // waves per workgroup, side by side along N
+constexpr int kThreads = 64 * kWaves;
+constexpr int kNwg = 16 * kNT * kWaves;  // 320 weight rows per workgroup
+constexpr int kXUnit = kMt * 4 * 64;     // uint4 of A operands per unit (16 KB)
 
-__device__ __forceinline__ half8 to_half8(float4 a, float4 b) {
-    half8 h;
-    h[0] = static_cast<_Float16>(a.x); h[1] = static_cast<_Float16>(a.y);
-    h[2] = static_cast<_Float16>(a.z); h[3] = static_cast<_Float16>(a.w);
-    h[4] = static_cast<_Float16>(b.x); h[5] = static_cast<_Float16>(b.y);
-    h[6] = static_cast<_Float16>(b.z); h[7] = static_cast<_Float16>(b.w);
-    return h;
-}
-
-// Eight weights from four nibble bytes: byte i holds elements 2i (low) and 2i+1 (high).
-__device__ __forceinline__ half8 deq8(uint32_t bytes, float sc, float mn) {
-    half8 h;
+// X [M x K] f32 -> XP[mt][sb][h][s][lane] (uint4 = 8 halves); rows >= M are zeros.
+// Workgroup (sb, mt): the 16 x 256 block of X, read row-major into LDS, written out as
+// its 512 operand uint4 in order.
+__global__ __launch_bounds__(256) void x16_pack_kernel(const float* __restrict__ X, v4u* __restrict__ XP, int M,
+                                                       int K) {
+    __shared__ float xs[16][256 + 4];
+    const int sb = blockIdx.x, S = gridDim.x, mt = blockIdx.y, tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t b = (bytes >> (8 * i)) & 0xFFu;
-        h[2 * i] = static_cast<_Float16>(fmaf(sc, static_cast<float>(b & 0xFu), -mn));
-        h[2 * i + 1] = static_cast<_Float16>(fmaf(sc, static_cast<float>(b >> 4), -mn));
+    for (int r = 0; r < 4; r++) {
+        const int idx = tid + 256 * r, row = idx >> 6, c4 = idx & 63;
+        const size_t m = static_cast<size_t>(mt) * 16 + row;
+        const float4 v = m < static_cast<size_t>(M)
+                             ? *reinterpret_cast<const float4*>(X + m * K + 256 * sb + 4 * c4)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4*>(&xs[row][4 * c4]) = v;
     }
-    return h;
+    __syncthreads();
+    auto pk = [](float lo, float hi) __attribute__((always_inline)) {
+        return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
+               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+    };
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int t = tid + 256 * q, h = t >> 8, s = (t >> 6) & 3, lane = t & 63;
+        const int g = lane >> 4, i = lane & 15;
+        const float* p = &xs[i][32 * (4 * h + g) + 8 * s];
+        const float4 a = *reinterpret_cast<const float4*>(p);
+        const float4 b = *reinterpret_cast<const float4*>(p + 4);
+        // element order 0, 4, 1, 5, 2, 6, 3, 7
+        const v4u out = {pk(a.x, b.x), pk(a.y, b.y), pk(a.z, b.z), pk(a.w, b.w)};
+        XP[(static_cast<size_t>(mt) * S + sb) * 512 + t] = out;
+    }
 }
 
-// Grid (ceil(N / 128), ceil(M / 128)); four waves, each a 64 x 64 block of Y as 4 x 4
-// MFMA tiles of 16 x 16.
-__global__ __launch_bounds__(kThreads, 2) void q4k_gemm_kernel(const uint8_t* __restrict__ qs,
-                                                               const uint4* __restrict__ hdr,
-                                                               const float* __restrict__ X, float* __restrict__ Y,
-                                                               int M, int N, int K) {
-    __shared__ _Float16 Xs[2][kMt][kRow];
-    __shared__ _Float16 Ws[2][kNt][kRow];
+// Two weights from a dword holding two fp16 values v: (v * sc + c) in f32, each rounded
+// to fp16 (v_fma_mix, fp16 source operand with f32 scale and offset).
+__device__ __forceinline__ uint32_t mix2(uint32_t p, float sc, float c) {
+    uint32_t r;
+    asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=&v"(r) : "v"(p), "v"(sc), "v"(c));
+    asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(r) : "v"(p), "v"(sc), "v"(c));
+    return r;
+}
+
+// (m & x) | magic for a magic with no bits under m.
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t magic) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(x), "s"(magic));
+    return r;
+}
+
+// Scale and offsets of one sub-block for the two nibble positions of a byte: the low
+// nibble q becomes the fp16 1024 + q, the high nibble (left in place) 1024 + 16 q, so
+//   w = (1024 + q) sc - (1024 sc + mn) = (1024 + 16 q) (sc / 16) - (64 sc + mn).
+struct SubScale {
+    float sc, c_lo, sc16, c_hi;
+};
+
+// Eight weights (elements 8s + 0, 4, 1, 5, 2, 6, 3, 7) from the nibble dword of step s;
+// byte i holds elements 2i (low nibble) and 2i + 1 (high nibble).
+__device__ __forceinline__ half8 deq8(uint32_t u, const SubScale& k, uint32_t m_lo, uint32_t m_hi) {
+    constexpr uint32_t kMagic = 0x64006400u;  // fp16 1024 in both halves
+    const uint32_t u8 = u >> 8;
+    v4u r;
+    r.x = mix2(bfi(m_lo, u, kMagic), k.sc, k.c_lo);     // elements 0, 4
+    r.y = mix2(bfi(m_hi, u, kMagic), k.sc16, k.c_hi);   // 1, 5
+    r.z = mix2(bfi(m_lo, u8, kMagic), k.sc, k.c_lo);    // 2, 6
+    r.w = mix2(bfi(m_hi, u8, kMagic), k.sc16, k.c_hi);  // 3, 7
+    return __builtin_bit_cast(half8, r);
+}
+
+// Grid (ceil(N / 320), ceil(M / 64)): workgroups that share weight rows are 8 apart in
+// launch order when gridDim.x is a multiple of 8, i.e. on one XCD.  One wave per SIMD
+// (the accumulators, two units of staged weights and the operands need ~380 registers).
+__global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const uint8_t* __restrict__ qs,
+                                                            const v4u* __restrict__ hdr,
+                                                            const v4u* __restrict__ XP, float* __restrict__ Y,
+                                                            int M, int N, int K, int ntiles) {
+    __shared__ v4u As[2 * kXUnit];  // A operands of two units
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * kNt, m0 = blockIdx.y * kMt;
-    const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
+    const int g = lane >> 4, c = lane & 15;
+    const int S = K / 256;
+    const int n = 2 * S;  // units: (super-block u / 2, half u % 2)
+    const int mt0 = blockIdx.y * kMt;
+    const int nt0 = (blockIdx.x * kWaves + wave) * kNT;  // first 16-row weight tile of this wave
 
-    // loaders: two threads per row, 16 consecutive k each
-    const int lr = tid >> 1, lh = (tid & 1) * 16;
-    const float* xp = X + static_cast<size_t>(min(m0 + lr, M - 1)) * K + lh;
-    const size_t wrow = static_cast<size_t>(min(n0 + lr, N - 1));
-    const size_t S = static_cast<size_t>(K / 256);
-    float4 xr[4];
-    uint2 wqv;
-    uint4 whv;
-    auto gload = [&](int k0) __attribute__((always_inline)) {
+    // wave-uniform byte offsets of tile j's qs block (sb 0, half 0) and header block;
+    // the lane adds its 16-byte slot (qs) or header row c
+    uint32_t qo[kNT], ho[kNT];
 #pragma unroll
-        for (int i = 0; i < 4; i++) xr[i] = *reinterpret_cast<const float4*>(xp + k0 + 4 * i);
-        wqv = *reinterpret_cast<const uint2*>(qs + q4k_sub_offset(wrow, k0 >> 8, (k0 >> 5) & 7, S) + lh / 2);
-        whv = hdr[q4k_hdr_index(wrow, k0 >> 8, S)];
+    for (int j = 0; j < kNT; j++) {
+        const uint32_t t = static_cast<uint32_t>(min(nt0 + j, ntiles - 1));
+        qo[j] = __builtin_amdgcn_readfirstlane(t * S * 2048u);
+        ho[j] = __builtin_amdgcn_readfirstlane(t * S * 256u);
+    }
+    const v4u* xb = XP + static_cast<size_t>(mt0) * S * 512 + tid;
+
+    // A: 1024 uint4 per unit, four per thread: idx = tid + 256 r -> (tile r, step, lane)
+    v4u xr[4];
+    auto load_x = [&](int u) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) xr[r] = xb[static_cast<size_t>(r) * S * 512 + u * 256];
     };
-    auto lstore = [&](int b, int k0) __attribute__((always_inline)) {
-        *reinterpret_cast<half8*>(&Xs[b][lr][lh]) = to_half8(xr[0], xr[1]);
-        *reinterpret_cast<half8*>(&Xs[b][lr][lh + 8]) = to_half8(xr[2], xr[3]);
-        const int j = (k0 >> 5) & 7;  // sub-block within the super-block
-        const float d = h2f(whv.x), dmin = h2f(whv.x >> 16);
-        const uint32_t scw = j < 4 ? whv.y : whv.z;
-        const float sc = d * static_cast<float>((scw >> (8 * (j & 3))) & 0x3Fu);
-        const float mn = dmin * static_cast<float>((whv.w >> (8 * (j & 3) + (j < 4 ? 0 : 4))) & 0xFu);
-        *reinterpret_cast<half8*>(&Ws[b][lr][lh]) = deq8(wqv.x, sc, mn);
-        *reinterpret_cast<half8*>(&Ws[b][lr][lh + 8]) = deq8(wqv.y, sc, mn);
+    auto store_x = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) As[b * kXUnit + r * 256 + tid] = xr[r];
     };
-
-    floatx4 acc[4][4];
+    // nibbles of the unit and the three header words it needs: d | dmin, the scale word
+    // of its half, the mins word
+    struct Wu {
+        v4u q[kNT];
+        uint32_t dm[kNT], scw[kNT], mw[kNT];
+    };
+    const uint8_t* hdrb = reinterpret_cast<const uint8_t*>(hdr) + c * 16;
+    auto load_w = [&](int u, Wu& w) __attribute__((always_inline)) {
+        const int h = u & 1;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    const int nk = K / kKs;
-    const int fr = lane & 15, fk = 8 * (lane >> 4);
-    gload(0);
-    lstore(0, 0);
-    __syncthreads();
-    for (int s = 0; s < nk; s++) {
-        const int b = s & 1;
-        if (s + 1 < nk) gload((s + 1) * kKs);
-        half8 a[4], w[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            a[t] = *reinterpret_cast<const half8*>(&Xs[b][wm + 16 * t + fr][fk]);
-            w[t] = *reinterpret_cast<const half8*>(&Ws[b][wn + 16 * t + fr][fk]);
+        for (int j = 0; j < kNT; j++) {
+            w.q[j] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4u*>(qs + qo[j] + static_cast<uint32_t>(u) * 1024u) + lane);
+            const uint32_t* hw = reinterpret_cast<const uint32_t*>(hdrb + ho[j] + static_cast<uint32_t>(u >> 1) * 256u);
+            w.dm[j] = hw[0];
+            w.scw[j] = hw[1 + h];
+            w.mw[j] = hw[3];
         }
+    };
+
+    floatx4 acc[kMt][kNT];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+    for (int i = 0; i < kMt; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], w[j], acc[i][j], 0, 0, 0);
-        // buffer b ^ 1 was last read in step s - 1, before that step's barrier
-        if (s + 1 < nk) lstore(b ^ 1, (s + 1) * kKs);
+        for (int j = 0; j < kNT; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u;
+    asm volatile("" : "+v"(m_lo), "+v"(m_hi));  // keep the masks in VGPRs
+    auto compute = [&](int b, int u, const Wu& w) __attribute__((always_inline)) {
+        const int h = u & 1;
+        SubScale k[kNT];
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+            const float d = h2f(w.dm[j] & 0xFFFFu), dmin = h2f(w.dm[j] >> 16);
+            const float sc = d * static_cast<float>((w.scw[j] >> (8 * g)) & 0x3Fu);
+            const float mn = dmin * static_cast<float>((w.mw[j] >> (8 * g + 4 * h)) & 0xFu);
+            k[j].sc = sc;
+            k[j].c_lo = -__builtin_fmaf(1024.f, sc, mn);
+            k[j].sc16 = sc * 0.0625f;
+            k[j].c_hi = -__builtin_fmaf(64.f, sc, mn);
+        }
+        const v4u* Ab = As + b * kXUnit;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            half8 bq[kNT], aq[kMt];
+#pragma unroll
+            for (int j = 0; j < kNT; j++) bq[j] = deq8(w.q[j][s], k[j], m_lo, m_hi);
+#pragma unroll
+            for (int i = 0; i < kMt; i++) aq[i] = __builtin_bit_cast(half8, Ab[(i * 4 + s) * 64 + lane]);
+#pragma unroll
+            for (int i = 0; i < kMt; i++)
+#pragma unroll
+                for (int j = 0; j < kNT; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[i], bq[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Unit u uses LDS buffer u % 2 and register set wa (even u) or wb (odd u); n is even.
+    // X of unit u + 1 is stored to LDS once unit u is consumed; X and W of unit u + 2 are
+    // in flight during unit u + 1.
+    Wu wa, wb;
+    load_x(0);
+    load_w(0, wa);
+    store_x(0);
+    load_x(1);
+    load_w(1, wb);
+    __syncthreads();
+    for (int u = 0; u < n; u += 2) {
+        compute(0, u, wa);
+        store_x(1);
+        if (u + 2 < n) {
+            load_x(u + 2);
+            load_w(u + 2, wa);
+        }
+        __syncthreads();
+        compute(1, u + 1, wb);
+        if (u + 2 < n) store_x(0);
+        if (u + 3 < n) {
+            load_x(u + 3);
+            load_w(u + 3, wb);
+        }
         __syncthreads();
     }
+
+    // D lane (g, c) holds rows 4g .. 4g + 3 of column c of each 16 x 16 tile
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < kMt; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int n = n0 + wn + 16 * j + fr;
+        for (int j = 0; j < kNT; j++) {
+            const int col = (nt0 + j) * 16 + c;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm + 16 * i + 4 * (lane >> 4) + r;
-                if (m < M && n < N) Y[static_cast<size_t>(m) * N + n] = acc[i][j][r];
+                const int m = (mt0 + i) * 16 + 4 * g + r;
+                if (m < M && col < N) Y[static_cast<size_t>(m) * N + col] = acc[i][j][r];
             }
         }
 }
 
 }  // namespace
 
-void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, hipStream_t s) {
+size_t q4k_gemm_ws_bytes(size_t m, size_t cols) {
+    const size_t m_pad = (m + 16 * kMt - 1) / (16 * kMt) * (16 * kMt);
+    return m_pad * cols * sizeof(uint16_t);
+}
+
+void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, void* ws, hipStream_t s) {
     if (w.format != LARQL_Q4_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: Q4_K weights only");
     if (m == 0) return;
+    if (!ws) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: no workspace");
     if (m > 0x7FFFFFFF / w.cols) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: too many tokens");
-    const dim3 grid(static_cast<unsigned>((w.rows + kNt - 1) / kNt), static_cast<unsigned>((m + kMt - 1) / kMt));
-    q4k_gemm_kernel<<<grid, dim3(kThreads), 0, s>>>(w.qs, w.hdr, X, Y, static_cast<int>(m), static_cast<int>(w.rows),
-                                                     static_cast<int>(w.cols));
+    const size_t mtiles = (m + 16 * kMt - 1) / (16 * kMt) * kMt;  // 16-token tiles, padded
+    x16_pack_kernel<<<dim3(static_cast<unsigned>(w.cols / 256), static_cast<unsigned>(mtiles)), dim3(256), 0, s>>>(
+        X, static_cast<v4u*>(ws), static_cast<int>(m), static_cast<int>(w.cols));
+    LARQL_HIP_CHECK(hipGetLastError());
+    const dim3 grid(static_cast<unsigned>((w.rows + kNwg - 1) / kNwg), static_cast<unsigned>(mtiles / kMt));
+    q4k_gemm_kernel<<<grid, dim3(kThreads), 0, s>>>(w.qs, reinterpret_cast<const v4u*>(w.hdr),
+                                                     static_cast<const v4u*>(ws), Y, static_cast<int>(m),
+                                                     static_cast<int>(w.rows), static_cast<int>(w.cols),
+                                                     static_cast<int>(w.rows_pad / 16));
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
