@@ -146,11 +146,11 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
             d.nkv = static_cast<int>(L.num_kv_heads);
             if (d.hd <= 0 || d.nq <= 0 || d.nkv <= 0 || d.nq % d.nkv || d.hd % 8)
                 fail(LARQL_HIP_ERR_INVALID, "decode: bad head geometry");
-            if (d.hd > 256) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: head_dim > 256");
+            if (!larql::attn_supported(d.nq / d.nkv, d.hd))
+                fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: attention takes head_dim a multiple of 32 up to 256 and "
+                                                "1..8 query heads per kv head");
             d.rdim = L.rotary_dim ? static_cast<int>(L.rotary_dim) : d.hd;
             if (d.rdim > d.hd || d.rdim % 2) fail(LARQL_HIP_ERR_INVALID, "decode: bad rotary_dim");
-            if (larql::attn_lds_bytes(d.nq / d.nkv, d.hd, d.rdim) > 64 * 1024)
-                fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: head geometry exceeds the attention kernel's LDS");
             d.window = static_cast<int>(L.sliding_window);
             d.eps = L.eps > 0.f ? static_cast<double>(L.eps) : 1e-6;
             d.attn_scale = L.attn_scale != 0.f ? L.attn_scale : static_cast<float>(1.0 / std::sqrt(double(d.hd)));
@@ -244,7 +244,7 @@ void kv_ensure(larql_hip_ctx* c, size_t layers, size_t num_kv, size_t head_dim, 
     if (kv.num_layers == 0) {
         kv.num_kv = num_kv;
         kv.head_dim = head_dim;
-        kv.max_seq = need > 4096 ? need : 4096;
+        kv.max_seq = need > 4096 ? (need + 7) & ~size_t(7) : 4096;  // V blocks of 8 positions
         kv.current_len = 0;
     }
     if (need > kv.max_seq) {
@@ -255,7 +255,9 @@ void kv_ensure(larql_hip_ctx* c, size_t layers, size_t num_kv, size_t head_dim, 
             for (auto* vec : {&kv.k, &kv.v}) {
                 __half* p = nullptr;
                 if (hipMalloc(&p, cap * row * sizeof(__half)) != hipSuccess) fail(LARQL_HIP_ERR_NOMEM, "KV grow failed");
-                LARQL_HIP_CHECK(hipMemcpy(p, (*vec)[l], kv.current_len * row * sizeof(__half), hipMemcpyDeviceToDevice));
+                // V blocks hold 8 positions: copy whole blocks (K rows up to the same bound)
+                const size_t len8 = (kv.current_len + 7) & ~size_t(7);
+                LARQL_HIP_CHECK(hipMemcpy(p, (*vec)[l], len8 * row * sizeof(__half), hipMemcpyDeviceToDevice));
                 (void)hipFree((*vec)[l]);
                 (*vec)[l] = p;
             }
@@ -406,7 +408,8 @@ extern "C" int larql_hip_populate_kv_layer(larql_hip_ctx* c, size_t layer, const
         const float* dk = stage_upload(c, c->stage_in, k_data, n);
         larql::launch_f32_to_f16(dk, c->kv.k[layer], n, c->stream);
         const float* dv = stage_upload(c, c->stage_in2, v_data, n);
-        larql::launch_f32_to_f16(dv, c->kv.v[layer], n, c->stream);
+        larql::launch_v_to_cache(dv, true, c->kv.v[layer], seq_len, static_cast<int>(num_kv_heads),
+                                 static_cast<int>(head_dim), c->stream);
         LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
         c->kv.current_len = seq_len;
     });
@@ -421,7 +424,8 @@ extern "C" int larql_hip_populate_kv_layer_f16_dev(larql_hip_ctx* c, size_t laye
         kv_ensure(c, layer + 1, num_kv_heads, head_dim, seq_len);
         const size_t bytes = seq_len * num_kv_heads * head_dim * sizeof(__half);
         LARQL_HIP_CHECK(hipMemcpyAsync(c->kv.k[layer], k_dev, bytes, hipMemcpyDeviceToDevice, c->stream));
-        LARQL_HIP_CHECK(hipMemcpyAsync(c->kv.v[layer], v_dev, bytes, hipMemcpyDeviceToDevice, c->stream));
+        larql::launch_v_to_cache(v_dev, false, c->kv.v[layer], seq_len, static_cast<int>(num_kv_heads),
+                                 static_cast<int>(head_dim), c->stream);
         LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
         c->kv.current_len = seq_len;
     });

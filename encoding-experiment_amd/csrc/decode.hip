@@ -20,7 +20,11 @@
 namespace larql {
 
 constexpr int kAttnThreads = 256;
-constexpr int kAttnChunk = 64;   // positions per workgroup (= wave size: one score per lane)
+constexpr int kAttnChunk = 64;  // positions per workgroup
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 // Split-half RoPE of element d of head vector x (LI/src/attention/rope.rs:22-55):
 // pairs (i, i + rdim/2), dims >= rdim untouched.  cs[i] = (cos, sin) of pair i.
@@ -30,10 +34,39 @@ __device__ __forceinline__ float rope_elem(const float* x, int d, int half, cons
     return x[d];
 }
 
+// Wave max / sum without LDS traffic: DPP butterflies inside each row of 16 lanes, then
+// the four row results through SGPRs.  Every lane gets the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));   // quad_perm 1,0,3,2
+    v = fmaxf(v, dpp<0x4E>(v));   // quad_perm 2,3,0,1
+    v = fmaxf(v, dpp<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp<0x140>(v));  // row_mirror
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x140>(v);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (a + b) + (c + d);
+}
+
 // Workgroup-wide max / sum through `scratch` (>= kAttnThreads / 64 floats); every
 // thread gets the result.
 __device__ __forceinline__ float block_max(float v, float* scratch) {
-    v = wave_max(v);
+    v = wave_max_dpp(v);
     if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
     __syncthreads();
     float r = scratch[0];
@@ -42,7 +75,7 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
     return r;
 }
 __device__ __forceinline__ float block_sum(float v, float* scratch) {
-    v = wave_sum(v);
+    v = wave_sum_dpp(v);
     if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
     __syncthreads();
     float r = scratch[0];
@@ -51,205 +84,294 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
     return r;
 }
 
-__device__ __forceinline__ float2 h2_to_f2(uint32_t v) {
-    return make_float2(h2f(v & 0xFFFFu), h2f(v >> 16));
+// Value of lane (this lane + R) within its row of 16 (row_shl:R).
+template <int R>
+__device__ __forceinline__ float from_lane_plus(float v) {
+    return dpp<0x100 + R>(v);
+}
+__device__ __forceinline__ floatx4 add_lane_plus(floatx4 v, int reps) {
+    floatx4 o = v;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float w;
+        switch (reps) {
+            case 1: w = from_lane_plus<1>(v[r]); break;
+            case 2: w = from_lane_plus<2>(v[r]); break;
+            case 3: w = from_lane_plus<3>(v[r]); break;
+            case 4: w = from_lane_plus<4>(v[r]); break;
+            case 5: w = from_lane_plus<5>(v[r]); break;
+            case 6: w = from_lane_plus<6>(v[r]); break;
+            case 7: w = from_lane_plus<7>(v[r]); break;
+            default: w = from_lane_plus<8>(v[r]); break;
+        }
+        o[r] = v[r] + w;
+    }
+    return o;
 }
 
 __device__ __forceinline__ uint32_t f2_to_h2(float a, float b) {
-    const uint32_t lo = __half_as_ushort(__float2half_rn(a));
-    const uint32_t hi = __half_as_ushort(__float2half_rn(b));
-    return lo | (hi << 16);
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
 }
 
-// Grid (S, num_kv).  Workgroup (s, kvh) covers positions [t_begin + 64 s, ...) for the
-// reps = num_q/num_kv query heads of kv head kvh (GQA: kv_h = h / reps,
-// LI/src/attention/gqa.rs:53).  Every stage gives each thread one independent item
-// with split accumulators (a dependent VALU result is ~32 cycles away on gfx950):
-// scores = one (head, position) per thread, P.V = one (head, dim pair) per thread.
+// Eight f32 values as fp16 pairs: the rounded value (part 0) or the rounding residue
+// (part 1); the two parts sum to the value within 2^-22 of it.
+__device__ __forceinline__ v4u split8(const float* x, int part) {
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float hi = static_cast<float>(static_cast<_Float16>(x[e]));
+        y[e] = part ? x[e] - hi : hi;
+    }
+    return v4u{f2_to_h2(y[0], y[1]), f2_to_h2(y[2], y[3]), f2_to_h2(y[4], y[5]), f2_to_h2(y[6], y[7])};
+}
+
+// Grid (S, num_kv).  Workgroup (s, kvh) covers positions [t0, t0 + 64), t0 = t_begin
+// rounded down to a multiple of 8, plus 64 s, for the reps = num_q / num_kv query heads
+// of kv head kvh (GQA: kv_h = h / reps, LI/src/attention/gqa.rs:53).  Both products run
+// on v_mfma_f32_16x16x32_f16 with f32 accumulation; the fp16 operands are exact: the
+// cached K and V are fp16, and each f32 query element or probability is split into two
+// fp16 parts, placed in two operand columns and summed after the product.
+//   scores: D[t][col] = sum_d K[t][d] Qx[d][col], col = head (rounded part) or reps +
+//           head (residue); wave w takes positions 16 w .. 16 w + 15 of the chunk.
+//   P.V:    D[d][col] = sum_t Vt[d][t] Px[t][col]; wave w takes the 16-dim tiles
+//           w, w + 4, ...; the V cache is stored as [t / 8][kv][hd][8] so that a lane's
+//           eight consecutive positions of one dim are one 16-byte load.
+// The row at pos = T - 1 comes from the fresh projections: RoPE'd, rounded to fp16 and
+// written to the cache by the workgroup that owns it, which uses it from LDS.
 // attn_combine_kernel merges the S softmax partials of each head.
+template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
-    extern __shared__ float lds[];
+    constexpr int KS = HD / 32;                 // score k-steps
+    constexpr int NDT = HD / 16;                // P.V dim tiles
+    constexpr int DTW = (NDT + 3) / 4;          // dim tiles per wave (upper bound)
+    __shared__ float qr_s[8 * HD];              // raw query heads
+    __shared__ float q_s[8 * HD];               // RoPE'd query heads
+    __shared__ float kr_s[HD];                  // raw new key
+    __shared__ float2 cs_s[HD / 2];
+    __shared__ v4u qop[KS * 64];                // score B operands
+    __shared__ float p_s[8][kAttnChunk];
+    __shared__ float ml_s[16];
+    __shared__ v4u pop[2 * 64];                 // P.V B operands
+    __shared__ __attribute__((aligned(16))) uint16_t knew[HD];
+    __shared__ uint16_t vnew[HD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int nw = kAttnThreads / 64;
+    const int g = lane >> 4, c = lane & 15;
     const int s = blockIdx.x, kvh = blockIdx.y;
-    const int reps = a.num_q / a.num_kv;
-    const int hd = a.hd, hd2 = hd / 2, half = a.rdim / 2;
-    const int q_dim = a.num_q * hd, kv_dim = a.num_kv * hd;
-    float* q_s = lds;                                               // reps * hd
-    float2* cs_s = reinterpret_cast<float2*>(q_s + reps * hd);      // half
-    uint32_t* k_s = reinterpret_cast<uint32_t*>(cs_s + half);       // chunk * (hd2 + 1), padded rows
-    uint32_t* v_s = k_s + kAttnChunk * (hd2 + 1);                   // chunk * hd2
-    float* p_s = reinterpret_cast<float*>(v_s + kAttnChunk * hd2);  // reps * max(chunk, hd)
-    float* ml_s = p_s + reps * max(kAttnChunk, hd);                 // reps * 2
-
-    const int t0 = a.t_begin + s * kAttnChunk;
-    const int t1 = min(a.T, t0 + kAttnChunk);
-    const int nt = t1 - t0;
+    const int reps = a.num_q / a.num_kv, half = a.rdim / 2;
+    const int q_dim = a.num_q * HD, kv_dim = a.num_kv * HD;
+    const int t0 = (a.t_begin & ~7) + s * kAttnChunk;
     const int pos = a.T - 1;
+    const bool owner = pos < t0 + kAttnChunk;  // the last chunk holds pos
 
-    // Every global load of the workgroup is issued up front: the K/V tile (into
-    // registers), the raw query heads and this position's RoPE row (into LDS); one
-    // barrier then covers all of them.
-    const int c8n = hd / 8;
-    constexpr int kMaxItems = 8;  // nt * c8n <= 64 * 32 = kMaxItems * kAttnThreads (hd <= 256)
-    uint4 kk[kMaxItems], vv[kMaxItems];
+    // 1. Global loads, all issued up front.  K rows below pos as score A operands
+    // (lane (g, c) of wave w: position t0 + 16 w + c, dims 32 ks + 8 g ..); V blocks at or
+    // below pos as P.V A operands (dims 16 dt + c, positions t0 + 32 ts + 8 g ..).
+    const int tk = t0 + 16 * wave + c;
+    v4u kA[KS];
 #pragma unroll
-    for (int it = 0; it < kMaxItems; it++) {
-        const int idx = tid + it * kAttnThreads;
-        const int tl = idx / c8n, c8 = idx - tl * c8n, t = t0 + tl;
-        if (idx < nt * c8n && t != pos) {
-            const size_t off = (static_cast<size_t>(t) * a.num_kv + kvh) * hd + c8 * 8;
-            kk[it] = *reinterpret_cast<const uint4*>(a.kc + off);
-            vv[it] = *reinterpret_cast<const uint4*>(a.vc + off);
+    for (int ks = 0; ks < KS; ks++)
+        kA[ks] = tk < pos ? *reinterpret_cast<const v4u*>(a.kc + (static_cast<size_t>(tk) * a.num_kv + kvh) * HD +
+                                                          32 * ks + 8 * g)
+                          : v4u{0u, 0u, 0u, 0u};
+    v4u vA[DTW][2];
+#pragma unroll
+    for (int i = 0; i < DTW; i++) {
+        const int dt = wave + 4 * i;
+#pragma unroll
+        for (int ts = 0; ts < 2; ts++) {
+            const int tv = t0 + 32 * ts + 8 * g;
+            vA[i][ts] = (dt < NDT && tv <= pos)
+                            ? *reinterpret_cast<const v4u*>(
+                                  a.vc + ((static_cast<size_t>(tv >> 3) * a.num_kv + kvh) * HD + 16 * dt + c) * 8)
+                            : v4u{0u, 0u, 0u, 0u};
         }
     }
-    float* qraw_s = p_s;  // reps * hd floats, free until the scores are written
-    for (int idx = tid; idx < reps * hd; idx += kAttnThreads)
-        qraw_s[idx] = a.qkv[static_cast<size_t>(kvh * reps) * hd + idx];
+    for (int i = tid; i < reps * HD; i += kAttnThreads) qr_s[i] = a.qkv[static_cast<size_t>(kvh * reps) * HD + i];
     for (int i = tid; i < half; i += kAttnThreads) cs_s[i] = a.rope[static_cast<size_t>(pos) * half + i];
-    __syncthreads();
-    for (int idx = tid; idx < reps * hd; idx += kAttnThreads) {
-        const int g = idx / hd, d = idx - g * hd;
-        q_s[idx] = rope_elem(qraw_s + g * hd, d, half, cs_s);
-    }
-    // K/V tile into LDS.  The row at pos comes from the fresh projections: RoPE'd,
-    // rounded to fp16 and appended to the cache by the one workgroup that owns it.
-#pragma unroll
-    for (int it = 0; it < kMaxItems; it++) {
-        const int idx = tid + it * kAttnThreads;
-        if (idx >= nt * c8n) continue;
-        const int tl = idx / c8n, c8 = idx - tl * c8n, t = t0 + tl;
-        uint32_t kw[4], vw[4];
-        if (t == pos) {
-            const float* kh = a.qkv + q_dim + static_cast<size_t>(kvh) * hd;
-            const float* vh = a.qkv + q_dim + kv_dim + static_cast<size_t>(kvh) * hd;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int d = c8 * 8 + 2 * j;
-                kw[j] = f2_to_h2(rope_elem(kh, d, half, cs_s), rope_elem(kh, d + 1, half, cs_s));
-                vw[j] = f2_to_h2(vh[d], vh[d + 1]);
-            }
-            const size_t off = (static_cast<size_t>(t) * a.num_kv + kvh) * hd + c8 * 8;
-            *reinterpret_cast<uint4*>(a.kc + off) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
-            *reinterpret_cast<uint4*>(a.vc + off) = make_uint4(vw[0], vw[1], vw[2], vw[3]);
-        } else {
-            kw[0] = kk[it].x; kw[1] = kk[it].y; kw[2] = kk[it].z; kw[3] = kk[it].w;
-            vw[0] = vv[it].x; vw[1] = vv[it].y; vw[2] = vv[it].z; vw[3] = vv[it].w;
+    if (owner)
+        for (int i = tid; i < HD; i += kAttnThreads) {
+            kr_s[i] = a.qkv[q_dim + static_cast<size_t>(kvh) * HD + i];
+            vnew[i] = __builtin_bit_cast(uint16_t,
+                                         static_cast<_Float16>(a.qkv[q_dim + kv_dim + static_cast<size_t>(kvh) * HD + i]));
         }
+    __syncthreads();
+    for (int i = tid; i < reps * HD; i += kAttnThreads) {
+        const int h = i / HD, d = i - h * HD;
+        q_s[i] = rope_elem(qr_s + h * HD, d, half, cs_s);
+    }
+    if (owner)
+        for (int d = tid; d < HD; d += kAttnThreads) {
+            const uint16_t kh = __builtin_bit_cast(uint16_t, static_cast<_Float16>(rope_elem(kr_s, d, half, cs_s)));
+            knew[d] = kh;
+            // append the new row to the cache
+            a.kc[(static_cast<size_t>(pos) * a.num_kv + kvh) * HD + d] = __ushort_as_half(kh);
+            a.vc[((static_cast<size_t>(pos >> 3) * a.num_kv + kvh) * HD + d) * 8 + (pos & 7)] = __ushort_as_half(vnew[d]);
+        }
+    __syncthreads();
+    // score B operands: lane (g, col) of k-step ks holds dims 32 ks + 8 g .. of column col
+    for (int i = tid; i < KS * 64; i += kAttnThreads) {
+        const int ks = i >> 6, l = i & 63, lg = l >> 4, col = l & 15;
+        v4u op = {0u, 0u, 0u, 0u};
+        if (col < 2 * reps) {
+            const int h = col < reps ? col : col - reps;
+            op = split8(q_s + h * HD + 32 * ks + 8 * lg, col >= reps);
+        }
+        qop[i] = op;
+    }
+    if (owner) {
+        if (tk == pos) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            k_s[tl * (hd2 + 1) + c8 * 4 + j] = kw[j];
-            v_s[tl * hd2 + c8 * 4 + j] = vw[j];
+            for (int ks = 0; ks < KS; ks++) kA[ks] = *reinterpret_cast<const v4u*>(&knew[32 * ks + 8 * g]);
+        }
+        // the block holding pos: the new value at pos, zeros above it (beyond the cache)
+#pragma unroll
+        for (int i = 0; i < DTW; i++) {
+            const int dt = wave + 4 * i;
+#pragma unroll
+            for (int ts = 0; ts < 2; ts++) {
+                const int tv = t0 + 32 * ts + 8 * g;
+                if (dt < NDT && tv <= pos && pos < tv + 8) {
+                    const int e = pos - tv;
+                    const uint32_t vn = vnew[16 * dt + c];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const uint32_t w = vA[i][ts][k];
+                        const uint32_t lo = 2 * k < e ? (w & 0xFFFFu) : (2 * k == e ? vn : 0u);
+                        const uint32_t hi = 2 * k + 1 < e ? (w >> 16) : (2 * k + 1 == e ? vn : 0u);
+                        vA[i][ts][k] = lo | (hi << 16);
+                    }
+                }
+            }
         }
     }
     __syncthreads();
 
-    // Scores: thread (g, t), four accumulators over the head dimension.
-    for (int idx = tid; idx < reps * kAttnChunk; idx += kAttnThreads) {
-        const int g = idx / kAttnChunk, t = idx - g * kAttnChunk;
-        float sc = -INFINITY;
-        if (t < nt) {
-            const uint32_t* kr = k_s + t * (hd2 + 1);
-            const float2* qg = reinterpret_cast<const float2*>(q_s + g * hd);
-            float acc[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int j = 0; j < hd2; j += 2) {
-                const float2 k0 = h2_to_f2(kr[j]), k1 = h2_to_f2(kr[j + 1]);
-                const float2 q0 = qg[j], q1 = qg[j + 1];
-                acc[0] = fmaf(k0.x, q0.x, acc[0]);
-                acc[1] = fmaf(k0.y, q0.y, acc[1]);
-                acc[2] = fmaf(k1.x, q1.x, acc[2]);
-                acc[3] = fmaf(k1.y, q1.y, acc[3]);
-            }
-            sc = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * a.scale;
+    // 2. Scores of positions t0 + 16 w + 4 g + r for lanes (g, col < reps).
+    floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++)
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, kA[ks]),
+                                                      __builtin_bit_cast(half8, qop[ks * 64 + lane]), sacc, 0, 0, 0);
+    sacc = add_lane_plus(sacc, reps);
+    if (c < reps) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int tl = 16 * wave + 4 * g + r, t = t0 + tl;
+            p_s[c][tl] = (t >= a.t_begin && t <= pos) ? sacc[r] * a.scale : -INFINITY;
         }
-        p_s[idx] = sc;
     }
     __syncthreads();
-    // Softmax partials of the chunk: one wave per head.
-    for (int g = wave; g < reps; g += nw) {
-        const float sc = p_s[g * kAttnChunk + lane];
-        const float m = wave_max(sc);
-        const float p = lane < nt ? expf(sc - m) : 0.f;
-        const float l = wave_sum(p);
-        p_s[g * kAttnChunk + lane] = p;
+    // 3. Softmax partials of the chunk: one wave per head.
+    for (int h = wave; h < reps; h += kAttnThreads / 64) {
+        const float sc = p_s[h][lane];
+        const float m = wave_max_dpp(sc);
+        const float p = sc == -INFINITY ? 0.f : expf(sc - m);
+        const float l = wave_sum_dpp(p);
+        p_s[h][lane] = p;
         if (lane == 0) {
-            ml_s[2 * g] = m;
-            ml_s[2 * g + 1] = l;
+            ml_s[2 * h] = m;
+            ml_s[2 * h + 1] = l;
         }
     }
     __syncthreads();
-    // Unnormalised P.V: thread (g, dim pair j), even / odd positions on separate chains.
-    for (int idx = tid; idx < reps * hd2; idx += kAttnThreads) {
-        const int g = idx / hd2, j = idx - g * hd2;
-        const int h = kvh * reps + g;
-        const float* pg = p_s + g * kAttnChunk;
-        float ox[2] = {0.f, 0.f}, oy[2] = {0.f, 0.f};
-        int t = 0;
-        for (; t + 1 < nt; t += 2) {
-            const float2 v0 = h2_to_f2(v_s[t * hd2 + j]), v1 = h2_to_f2(v_s[(t + 1) * hd2 + j]);
-            ox[0] = fmaf(pg[t], v0.x, ox[0]);
-            oy[0] = fmaf(pg[t], v0.y, oy[0]);
-            ox[1] = fmaf(pg[t + 1], v1.x, ox[1]);
-            oy[1] = fmaf(pg[t + 1], v1.y, oy[1]);
+    // P.V B operands: lane (g, col) of position step ts holds positions 32 ts + 8 g ..
+    if (tid < 2 * 64) {
+        const int ts = tid >> 6, lg = (tid >> 4) & 3, col = tid & 15;
+        v4u op = {0u, 0u, 0u, 0u};
+        if (col < 2 * reps) {
+            const int h = col < reps ? col : col - reps;
+            op = split8(&p_s[h][32 * ts + 8 * lg], col >= reps);
         }
-        if (t < nt) {
-            const float2 v0 = h2_to_f2(v_s[t * hd2 + j]);
-            ox[0] = fmaf(pg[t], v0.x, ox[0]);
-            oy[0] = fmaf(pg[t], v0.y, oy[0]);
+        pop[tid] = op;
+    }
+    __syncthreads();
+    // 4. Unnormalised P.V: dims 16 dt + 4 g + r for lanes (g, col < reps).
+#pragma unroll
+    for (int i = 0; i < DTW; i++) {
+        const int dt = wave + 4 * i;
+        if (dt >= NDT) break;
+        floatx4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ts = 0; ts < 2; ts++)
+            o = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, vA[i][ts]),
+                                                       __builtin_bit_cast(half8, pop[ts * 64 + lane]), o, 0, 0, 0);
+        o = add_lane_plus(o, reps);
+        if (c < reps) {
+            float* dst = a.part + (static_cast<size_t>(kvh * reps + c) * a.S + s) * (HD + 2);
+#pragma unroll
+            for (int r = 0; r < 4; r++) dst[16 * dt + 4 * g + r] = o[r];
         }
-        float* dst = a.part + (static_cast<size_t>(h) * a.S + s) * (hd + 2);
-        dst[2 * j] = ox[0] + ox[1];
-        dst[2 * j + 1] = oy[0] + oy[1];
-        if (j == 0) {
-            dst[hd] = ml_s[2 * g];
-            dst[hd + 1] = ml_s[2 * g + 1];
-        }
+    }
+    if (tid < reps) {
+        float* dst = a.part + (static_cast<size_t>(kvh * reps + tid) * a.S + s) * (HD + 2);
+        dst[HD] = ml_s[2 * tid];
+        dst[HD + 1] = ml_s[2 * tid + 1];
     }
 }
 
 // Merge of the S softmax partials of each head (a second launch: the kernel boundary
-// makes every partial visible, with no device-scope fences in the split kernel):
+// makes every partial visible; a device-scope release/acquire inside the split kernel
+// measured ~25 us per launch here):
 //   o = sum_s e_s o_s / sum_s e_s l_s,   e_s = exp(m_s - max_s m_s).
-// Grid (num_q); thread (group g, dim pair j) sums splits g, g + 256/(hd/2), ... with
-// the per-split weights computed once per workgroup in LDS.
+// Grid (num_q); thread (group g, dim pair j) sums splits g, g + ngrp, ... with the
+// per-split weights computed once per workgroup in LDS.  The first 16 partial vectors of
+// every thread and the split maxima and sums are loaded before any reduction, so the
+// merge waits on global memory once.
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a) {
     extern __shared__ float lds[];
     const int h = blockIdx.x, tid = threadIdx.x, hd = a.hd, hd2 = hd / 2;
-    const int ngrp = kAttnThreads / hd2;                 // split groups (hd2 divides 256)
+    const int ngrp = kAttnThreads / hd2;                 // split groups
     float* e_s = lds;                                    // S weights
     float2* o_s = reinterpret_cast<float2*>(e_s + a.S);  // ngrp * hd2 partial outputs
     float* red = reinterpret_cast<float*>(o_s + ngrp * hd2);
     const float* src = a.part + static_cast<size_t>(h) * a.S * (hd + 2);
-    float M = -INFINITY;
-    for (int s2 = tid; s2 < a.S; s2 += kAttnThreads) M = fmaxf(M, src[s2 * (hd + 2) + hd]);
+    const int grp = tid / hd2, j = tid - grp * hd2;
+    const bool act = grp < ngrp;
+    constexpr int PF = 16;
+    float2 ov[PF];
+#pragma unroll
+    for (int u = 0; u < PF; u++) {
+        const int s2 = grp + u * ngrp;
+        ov[u] = act && s2 < a.S ? *reinterpret_cast<const float2*>(src + s2 * (hd + 2) + 2 * j) : make_float2(0.f, 0.f);
+    }
+    float M = -INFINITY, m0 = -INFINITY, l0 = 0.f;
+    if (tid < a.S) {
+        m0 = src[tid * (hd + 2) + hd];
+        l0 = src[tid * (hd + 2) + hd + 1];
+    }
+    M = m0;
+    for (int s2 = tid + kAttnThreads; s2 < a.S; s2 += kAttnThreads) M = fmaxf(M, src[s2 * (hd + 2) + hd]);
     M = block_max(M, red);
     float L = 0.f;
-    for (int s2 = tid; s2 < a.S; s2 += kAttnThreads) {
+    if (tid < a.S) {
+        const float e = expf(m0 - M);
+        e_s[tid] = e;
+        L = l0 * e;
+    }
+    for (int s2 = tid + kAttnThreads; s2 < a.S; s2 += kAttnThreads) {
         const float e = expf(src[s2 * (hd + 2) + hd] - M);
         e_s[s2] = e;
         L = fmaf(src[s2 * (hd + 2) + hd + 1], e, L);
     }
     L = block_sum(L, red);  // also orders the e_s writes before their reads
-    // thread (grp, j): splits grp, grp + ngrp, ...; loads unrolled by four
-    const int grp = tid / hd2, j = tid - grp * hd2;
     float2 o = make_float2(0.f, 0.f);
-    int s2 = grp;
-    for (; s2 + 3 * ngrp < a.S; s2 += 4 * ngrp) {
-        float2 v[4];
+    if (act) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = *reinterpret_cast<const float2*>(src + (s2 + u * ngrp) * (hd + 2) + 2 * j);
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            o.x = fmaf(v[u].x, e_s[s2 + u * ngrp], o.x);
-            o.y = fmaf(v[u].y, e_s[s2 + u * ngrp], o.y);
+        for (int u = 0; u < PF; u++) {
+            const int s2 = grp + u * ngrp;
+            if (s2 < a.S) {
+                o.x = fmaf(ov[u].x, e_s[s2], o.x);
+                o.y = fmaf(ov[u].y, e_s[s2], o.y);
+            }
         }
+        for (int s2 = grp + PF * ngrp; s2 < a.S; s2 += ngrp) {
+            const float2 v = *reinterpret_cast<const float2*>(src + s2 * (hd + 2) + 2 * j);
+            o.x = fmaf(v.x, e_s[s2], o.x);
+            o.y = fmaf(v.y, e_s[s2], o.y);
+        }
+        o_s[grp * hd2 + j] = o;
     }
-    for (; s2 < a.S; s2 += ngrp) {
-        const float2 v = *reinterpret_cast<const float2*>(src + s2 * (hd + 2) + 2 * j);
-        o.x = fmaf(v.x, e_s[s2], o.x);
-        o.y = fmaf(v.y, e_s[s2], o.y);
-    }
-    o_s[grp * hd2 + j] = o;
     __syncthreads();
     if (tid < hd2) {
         float2 t = o_s[tid];
@@ -262,11 +384,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a) 
     }
 }
 
-size_t attn_lds_bytes(int reps, int hd, int rdim) {
-    return sizeof(float) * reps * hd + sizeof(float2) * (rdim / 2) +
-           sizeof(uint32_t) * (kAttnChunk * (hd / 2 + 1) + kAttnChunk * hd / 2) +
-           sizeof(float) * (reps * std::max(kAttnChunk, hd) + 2 * reps);
-}
+bool attn_supported(int reps, int hd) { return reps >= 1 && reps <= 8 && hd % 32 == 0 && hd >= 32 && hd <= 256; }
 
 __global__ void rope_table_kernel(float2* cs, size_t n, int half, int rdim, double base) {
     const size_t idx = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
@@ -296,6 +414,29 @@ __global__ void f32_to_f16_kernel(const float* __restrict__ src, __half* __restr
     if (i < n) dst[i] = __float2half_rn(src[i]);
 }
 
+// [seq][num_kv][hd] rows (f32, or fp16 bits) -> the V cache layout [t / 8][num_kv][hd][8].
+template <typename T>
+__global__ void v_to_cache_kernel(const T* __restrict__ src, __half* __restrict__ dst, size_t seq, int num_kv,
+                                  int hd) {
+    const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    const size_t row = static_cast<size_t>(num_kv) * hd;
+    if (i >= seq * row) return;
+    const size_t t = i / row, j = i - t * row;  // j = kvh * hd + d
+    __half v;
+    if constexpr (sizeof(T) == 4) v = __float2half_rn(src[i]);
+    else v = __ushort_as_half(src[i]);
+    dst[((t >> 3) * row + j) * 8 + (t & 7)] = v;
+}
+
+void launch_v_to_cache(const void* src, bool src_f32, __half* dst, size_t seq, int num_kv, int hd, hipStream_t s) {
+    const size_t n = seq * static_cast<size_t>(num_kv) * hd;
+    if (n == 0) return;
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+    if (src_f32) v_to_cache_kernel<float><<<grid, dim3(256), 0, s>>>(static_cast<const float*>(src), dst, seq, num_kv, hd);
+    else v_to_cache_kernel<uint16_t><<<grid, dim3(256), 0, s>>>(static_cast<const uint16_t*>(src), dst, seq, num_kv, hd);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
 void launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s) {
     if (n == 0) return;
     copy_f32_kernel<<<dim3((n + 255) / 256), dim3(256), 0, s>>>(src, dst, n);
@@ -310,10 +451,20 @@ void launch_f32_to_f16(const float* src, __half* dst, size_t n, hipStream_t s) {
 
 void launch_attention(const AttnArgs& a0, hipStream_t s) {
     AttnArgs a = a0;
-    a.S = (a.T - a.t_begin + kAttnChunk - 1) / kAttnChunk;
     const int reps = a.num_q / a.num_kv;
-    const size_t lds = attn_lds_bytes(reps, a.hd, a.rdim);
-    attn_decode_kernel<<<dim3(a.S, a.num_kv), dim3(kAttnThreads), lds, s>>>(a);
+    if (!attn_supported(reps, a.hd)) fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: head geometry");
+    a.S = (a.T - (a.t_begin & ~7) + kAttnChunk - 1) / kAttnChunk;
+    const dim3 grid(a.S, a.num_kv), block(kAttnThreads);
+    switch (a.hd) {
+        case 32: attn_decode_kernel<32><<<grid, block, 0, s>>>(a); break;
+        case 64: attn_decode_kernel<64><<<grid, block, 0, s>>>(a); break;
+        case 96: attn_decode_kernel<96><<<grid, block, 0, s>>>(a); break;
+        case 128: attn_decode_kernel<128><<<grid, block, 0, s>>>(a); break;
+        case 160: attn_decode_kernel<160><<<grid, block, 0, s>>>(a); break;
+        case 192: attn_decode_kernel<192><<<grid, block, 0, s>>>(a); break;
+        case 224: attn_decode_kernel<224><<<grid, block, 0, s>>>(a); break;
+        default: attn_decode_kernel<256><<<grid, block, 0, s>>>(a); break;
+    }
     LARQL_HIP_CHECK(hipGetLastError());
     // combine: S split weights + block-reduction scratch
     const size_t lds2 = sizeof(float) * (static_cast<size_t>(a.S) + 2 * kAttnThreads + kAttnThreads / 64);
