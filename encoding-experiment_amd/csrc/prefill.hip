@@ -108,12 +108,12 @@ __device__ __forceinline__ half8 deq8(uint32_t u, const SubScale& k, uint32_t m_
 
 // Grid (ceil(N / 320), ceil(M / 64)): workgroups that share weight rows are 8 apart in
 // launch order when gridDim.x is a multiple of 8, i.e. on one XCD.  One wave per SIMD
-// (the accumulators, two units of staged weights and the operands need ~380 registers).
+// (the accumulators, three units of staged weights and the operands take ~410 registers).
 __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const uint8_t* __restrict__ qs,
                                                             const v4u* __restrict__ hdr,
                                                             const v4u* __restrict__ XP, float* __restrict__ Y,
                                                             int M, int N, int K, int ntiles) {
-    __shared__ v4u As[2 * kXUnit];  // A operands of two units
+    __shared__ v4u As[3 * kXUnit];  // A operands of three units
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int S = K / 256;
@@ -133,32 +133,29 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const uint8_t* __res
     const v4u* xb = XP + static_cast<size_t>(mt0) * S * 512 + tid;
 
     // A: 1024 uint4 per unit, four per thread: idx = tid + 256 r -> (tile r, step, lane)
-    v4u xr[4];
-    auto load_x = [&](int u) __attribute__((always_inline)) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) xr[r] = xb[static_cast<size_t>(r) * S * 512 + u * 256];
+    struct Xu {
+        v4u v[4];
     };
-    auto store_x = [&](int b) __attribute__((always_inline)) {
+    auto load_x = [&](int u, Xu& x) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) As[b * kXUnit + r * 256 + tid] = xr[r];
+        for (int r = 0; r < 4; r++) x.v[r] = xb[static_cast<size_t>(r) * S * 512 + u * 256];
     };
-    // nibbles of the unit and the three header words it needs: d | dmin, the scale word
-    // of its half, the mins word
+    auto store_x = [&](int b, const Xu& x) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) As[b * kXUnit + r * 256 + tid] = x.v[r];
+    };
+    // nibbles and super-block header of the unit (the half's scale word is chosen when
+    // the unit is consumed: selecting at load time would wait for the load)
     struct Wu {
-        v4u q[kNT];
-        uint32_t dm[kNT], scw[kNT], mw[kNT];
+        v4u q[kNT], hd[kNT];
     };
     const uint8_t* hdrb = reinterpret_cast<const uint8_t*>(hdr) + c * 16;
     auto load_w = [&](int u, Wu& w) __attribute__((always_inline)) {
-        const int h = u & 1;
 #pragma unroll
         for (int j = 0; j < kNT; j++) {
             w.q[j] = __builtin_nontemporal_load(
                 reinterpret_cast<const v4u*>(qs + qo[j] + static_cast<uint32_t>(u) * 1024u) + lane);
-            const uint32_t* hw = reinterpret_cast<const uint32_t*>(hdrb + ho[j] + static_cast<uint32_t>(u >> 1) * 256u);
-            w.dm[j] = hw[0];
-            w.scw[j] = hw[1 + h];
-            w.mw[j] = hw[3];
+            w.hd[j] = *reinterpret_cast<const v4u*>(hdrb + ho[j] + static_cast<uint32_t>(u >> 1) * 256u);
         }
     };
 
@@ -175,9 +172,10 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const uint8_t* __res
         SubScale k[kNT];
 #pragma unroll
         for (int j = 0; j < kNT; j++) {
-            const float d = h2f(w.dm[j] & 0xFFFFu), dmin = h2f(w.dm[j] >> 16);
-            const float sc = d * static_cast<float>((w.scw[j] >> (8 * g)) & 0x3Fu);
-            const float mn = dmin * static_cast<float>((w.mw[j] >> (8 * g + 4 * h)) & 0xFu);
+            const float d = h2f(w.hd[j].x & 0xFFFFu), dmin = h2f(w.hd[j].x >> 16);
+            const uint32_t scw = h ? w.hd[j].z : w.hd[j].y;
+            const float sc = d * static_cast<float>((scw >> (8 * g)) & 0x3Fu);
+            const float mn = dmin * static_cast<float>((w.hd[j].w >> (8 * g + 4 * h)) & 0xFu);
             k[j].sc = sc;
             k[j].c_lo = -__builtin_fmaf(1024.f, sc, mn);
             k[j].sc16 = sc * 0.0625f;
@@ -199,32 +197,35 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const uint8_t* __res
         }
     };
 
-    // Unit u uses LDS buffer u % 2 and register set wa (even u) or wb (odd u); n is even.
-    // X of unit u + 1 is stored to LDS once unit u is consumed; X and W of unit u + 2 are
-    // in flight during unit u + 1.
-    Wu wa, wb;
-    load_x(0);
-    load_w(0, wa);
-    store_x(0);
-    load_x(1);
-    load_w(1, wb);
+    // Three-stage ring: unit u uses LDS buffer u % 3 and register sets u % 3.  After unit
+    // u is consumed, X of unit u + 1 goes to LDS and X and W of unit u + 3 are requested,
+    // so every load has two units of compute to arrive.  Loads past the last unit re-read
+    // it (unused), keeping the count of loads in flight the same in every stage.
+    Wu w0, w1, w2;
+    Xu x0, x1, x2;
+    load_x(0, x0);
+    load_w(0, w0);
+    load_x(min(1, n - 1), x1);
+    load_w(min(1, n - 1), w1);
+    load_x(min(2, n - 1), x2);
+    load_w(min(2, n - 1), w2);
+    store_x(0, x0);
     __syncthreads();
-    for (int u = 0; u < n; u += 2) {
-        compute(0, u, wa);
-        store_x(1);
-        if (u + 2 < n) {
-            load_x(u + 2);
-            load_w(u + 2, wa);
-        }
+    auto stage = [&](int u, int b, Wu& w, Xu& xnext, Xu& xload) __attribute__((always_inline)) {
+        compute(b, u, w);
+        store_x(b == 2 ? 0 : b + 1, xnext);
+        load_x(min(u + 3, n - 1), xload);
+        load_w(min(u + 3, n - 1), w);
         __syncthreads();
-        compute(1, u + 1, wb);
-        if (u + 2 < n) store_x(0);
-        if (u + 3 < n) {
-            load_x(u + 3);
-            load_w(u + 3, wb);
-        }
-        __syncthreads();
+    };
+    int u = 0;
+    for (; u + 3 <= n; u += 3) {
+        stage(u, 0, w0, x1, x0);
+        stage(u + 1, 1, w1, x2, x1);
+        stage(u + 2, 2, w2, x0, x2);
     }
+    if (u < n) stage(u, 0, w0, x1, x0);
+    if (u + 1 < n) stage(u + 1, 1, w1, x2, x1);
 
     // D lane (g, c) holds rows 4g .. 4g + 3 of column c of each 16 x 16 tile
 #pragma unroll
