@@ -164,6 +164,9 @@ int larql_hip_quantize_weights(larql_hip_ctx* ctx, int format, const float* x, s
  * m = 1); for LARQL_Q4_0 / LARQL_Q8_0 `x` is int8 [m][cols] and x_scales f32
  * [m][cols/32], any m (each output row in the single-row order, bit for bit).
  * out is f32 [m][rows].
+ * The prefill GEMM packs x as fp16 into a workspace owned by the context; a call with a
+ * larger m than any before on the context grows it (device synchronize + allocation), so
+ * device calls on one context must not overlap on different streams.
  * stream: a hipStream_t, or NULL for the context stream.  Returns after enqueue. */
 int larql_hip_matvec_dev(larql_hip_ctx* ctx, uint64_t handle, const void* x, const float* x_scales,
                          float* out, size_t m, void* stream);
