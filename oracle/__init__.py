@@ -61,6 +61,8 @@ def _load():
             "lo_silu_gate_up": (None, [_P, _P, _P, _SZ]),
             "lo_attend_f16": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
             "lo_decode_layer": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, ctypes.c_double]),
+            "lo_decode_layer_window": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, ctypes.c_double,
+                                              _SZ]),
             "lo_gauss_f32": (None, [ctypes.c_uint64, ctypes.c_float, ctypes.c_float, _P, _SZ]),
         }
         for name, (res, args) in sig.items():
@@ -268,10 +270,15 @@ def silu_gate_up(g, u):
     return out
 
 
-def attend_f16(q, kc, vc, T: int, num_q: int, num_kv: int, head_dim: int, scale: float):
-    q, kc, vc = _c(q, np.float32), _c(kc, np.uint16), _c(vc, np.uint16)
+def attend_f16(q, kc, vc, T: int, num_q: int, num_kv: int, head_dim: int, scale: float, t_start: int = 0):
+    """Attention of the last query row over cache positions t_start .. T-1 (t_start > 0 is
+    the sliding window, LC/src/metal/shaders/kv_attention.rs:35)."""
+    kvd = num_kv * head_dim
+    q = _c(q, np.float32)
+    kc = _c(np.asarray(kc)[t_start * kvd:T * kvd], np.uint16)
+    vc = _c(np.asarray(vc)[t_start * kvd:T * kvd], np.uint16)
     out = np.empty(num_q * head_dim, dtype=np.float32)
-    _load().lo_attend_f16(_ptr(q), _ptr(kc), _ptr(vc), T, num_q, num_kv, head_dim, scale, _ptr(out))
+    _load().lo_attend_f16(_ptr(q), _ptr(kc), _ptr(vc), T - t_start, num_q, num_kv, head_dim, scale, _ptr(out))
     return out
 
 
@@ -282,9 +289,10 @@ class _Layer(ctypes.Structure):
 
 
 def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, num_kv: int,
-                 head_dim: int, rope_base: float, eps: float = 1e-6):
+                 head_dim: int, rope_base: float, eps: float = 1e-6, window: int = 0):
     """One Llama decoder layer on the CPU.  ``layer`` holds numpy arrays keyed as
-    the lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits) are updated in place."""
+    the lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits) are updated in place.
+    window > 0 attends over the last `window` positions only."""
     keep = {}
     st = _Layer()
     for name, dt in (("wq", np.uint8), ("wk", np.uint8), ("wv", np.uint8), ("wo", np.uint8),
@@ -298,8 +306,8 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
         assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]
         setattr(st, name, a.ctypes.data)
     h = np.array(h, dtype=np.float32, copy=True)
-    _load().lo_decode_layer(ctypes.byref(st), _ptr(h), pos, hidden, inter, num_q, num_kv,
-                            head_dim, rope_base, eps)
+    _load().lo_decode_layer_window(ctypes.byref(st), _ptr(h), pos, hidden, inter, num_q, num_kv,
+                                   head_dim, rope_base, eps, window)
     return h
 
 

@@ -583,6 +583,14 @@ void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_
 void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,
                      size_t hidden, size_t inter, size_t num_q, size_t num_kv, size_t head_dim,
                      double rope_base, double eps) {
+    lo_decode_layer_window(L, h, pos, hidden, inter, num_q, num_kv, head_dim, rope_base, eps, 0);
+}
+
+/* Same, attending over the last `window` positions only when window > 0 and T = pos + 1
+ * exceeds it: t_start = T - window (LC/src/metal/shaders/kv_attention.rs:35). */
+void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
+                            size_t hidden, size_t inter, size_t num_q, size_t num_kv, size_t head_dim,
+                            double rope_base, double eps, size_t window) {
     size_t qd = num_q * head_dim, kvd = num_kv * head_dim;
     float* xn = (float*)malloc(hidden * sizeof(float));
     float* q = (float*)malloc(qd * sizeof(float));
@@ -605,7 +613,8 @@ void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,
         L->v_cache[pos * kvd + i] = lo_f32_to_f16_rne(v[i]);
     }
     float scale = (float)(1.0 / sqrt((double)head_dim));
-    lo_attend_f16(q, L->k_cache, L->v_cache, pos + 1, num_q, num_kv, head_dim, scale, att);
+    const size_t T = pos + 1, t0 = (window > 0 && T > window) ? T - window : 0;
+    lo_attend_f16(q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, T - t0, num_q, num_kv, head_dim, scale, att);
     lo_q4k_matvec(L->wo, att, o, hidden, qd);
     for (size_t i = 0; i < hidden; i++) h[i] = h[i] + o[i];
 

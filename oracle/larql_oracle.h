@@ -92,6 +92,9 @@ typedef struct {
 void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,
                      size_t hidden, size_t inter, size_t num_q, size_t num_kv, size_t head_dim,
                      double rope_base, double eps);
+void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
+                            size_t hidden, size_t inter, size_t num_q, size_t num_kv, size_t head_dim,
+                            double rope_base, double eps, size_t window);
 
 /* ── deterministic inputs (splitmix64 -> Box-Muller in f64 -> f32) ─────── */
 void lo_gauss_f32(uint64_t seed, float mean, float std, float* out, size_t n);

@@ -41,15 +41,18 @@ class SmallModel:
                 post_attn_norm=(1.0 + 0.1 * oracle.gauss(s + 9, hidden)).astype(np.float32),
                 k_cache=np.zeros(cap * kvd, np.uint16), v_cache=np.zeros(cap * kvd, np.uint16)))
 
-    def hip_layers(self, rope_base):
+    def hip_layers(self, rope_base, window=0):
         return [larql_hip.make_layer(L["wq"], L["wk"], L["wv"], L["wo"], L["gate"], L["up"], L["down"],
                                      L["input_norm"], L["post_attn_norm"], head_dim=self.hd,
-                                     num_q_heads=self.nq, num_kv_heads=self.nkv, rope_base=rope_base)
+                                     num_q_heads=self.nq, num_kv_heads=self.nkv, rope_base=rope_base,
+                                     sliding_window=window)
                 for L in self.layers]
 
 
-def run_sequence(hip, T0, n_tokens, n_layers=2, hidden=512, inter=1024, nq=8, nkv=2, hd=64, rope=500000.0):
-    print(f"[decode] layers={n_layers} hidden={hidden} T0={T0} tokens={n_tokens}", flush=True)
+def run_sequence(hip, T0, n_tokens, n_layers=2, hidden=512, inter=1024, nq=8, nkv=2, hd=64, rope=500000.0,
+                 window=0):
+    print(f"[decode] layers={n_layers} hidden={hidden} nq={nq} nkv={nkv} hd={hd} T0={T0} tokens={n_tokens} "
+          f"window={window}", flush=True)
     m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=T0 + n_tokens + 1, seed=T0)
     kvd = nkv * hd
     hip.reset_kv_cache()
@@ -60,14 +63,14 @@ def run_sequence(hip, T0, n_tokens, n_layers=2, hidden=512, inter=1024, nq=8, nk
         L["k_cache"][: T0 * kvd] = k.astype(np.float16).view(np.uint16)
         L["v_cache"][: T0 * kvd] = v.astype(np.float16).view(np.uint16)
     assert hip.kv_cache_len() == T0
-    layers = m.hip_layers(rope)
+    layers = m.hip_layers(rope, window)
     errs = []
     for i in range(n_tokens):
         x = oracle.gauss(7000 + i, hidden)
         got = hip.decode_token(layers, x, hidden, inter, nq * hd, kvd, nq, nkv, hd, rope)
         ref = x.copy()
         for L in m.layers:
-            ref = oracle.decode_layer(L, ref, T0 + i, hidden, inter, nq, nkv, hd, rope)
+            ref = oracle.decode_layer(L, ref, T0 + i, hidden, inter, nq, nkv, hd, rope, window=window)
         e = rel_err(got, ref)
         errs.append(e)
         print(f"  token {i} pos {T0 + i}: rel_err={e:.3e}", flush=True)
@@ -92,6 +95,22 @@ def test_decode_empty_cache(hip):
 
 def test_decode_gqa_ratio_and_rope_base(hip):
     run_sequence(hip, T0=100, n_tokens=2, n_layers=1, nq=16, nkv=2, hd=128, hidden=1024, inter=512, rope=10000.0)
+
+
+def test_decode_sliding_window(hip):
+    # windows whose first position is not a multiple of 8 (the attention chunks start at
+    # the window start rounded down to 8 and mask the positions before it), one that
+    # covers a whole 64-position chunk, and one longer than the cache (no effect)
+    run_sequence(hip, T0=100, n_tokens=2, n_layers=1, window=41)
+    run_sequence(hip, T0=150, n_tokens=2, n_layers=1, window=70)
+    run_sequence(hip, T0=20, n_tokens=2, n_layers=1, window=64)
+
+
+@pytest.mark.parametrize("nq,nkv,hd,T0", [(24, 8, 96, 70), (2, 2, 256, 130), (16, 2, 32, 65), (8, 1, 160, 9)])
+def test_decode_head_geometries(hip, nq, nkv, hd, T0):
+    # hd a multiple of 32 up to 256, 1..8 query heads per kv head (q_dim a multiple of 256
+    # for the Q4_K output projection)
+    run_sequence(hip, T0=T0, n_tokens=2, n_layers=1, nq=nq, nkv=nkv, hd=hd, hidden=512, inter=512)
 
 
 def test_decode_unsupported_layer_returns_none(hip):

@@ -455,6 +455,33 @@ def test_attention_closed_forms():
         assert np.allclose(out[h * hd:(h + 1) * hd], mean[h // 4], rtol=1e-5, atol=1e-6)
 
 
+def test_attention_window_closed_forms():
+    """Sliding window (LC/src/metal/shaders/kv_attention.rs:35): a window of one position
+    returns that position's V; a window covering the whole cache changes nothing; the
+    window is the attention over the trailing slice of the cache."""
+    rng = np.random.default_rng(13)
+    nq, nkv, hd, T = 6, 2, 32, 9
+    q = rng.standard_normal(nq * hd).astype(np.float32)
+    kc = rng.standard_normal(T * nkv * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(T * nkv * hd).astype(np.float16).view(np.uint16)
+    out = oracle.attend_f16(q, kc, vc, T, nq, nkv, hd, 0.2, t_start=T - 1)
+    v_last = vc.view(np.float16).astype(np.float32).reshape(T, nkv, hd)[T - 1]
+    for h in range(nq):
+        assert np.array_equal(out[h * hd:(h + 1) * hd], v_last[h // 3])
+    full = oracle.attend_f16(q, kc, vc, T, nq, nkv, hd, 0.2)
+    assert np.array_equal(oracle.attend_f16(q, kc, vc, T, nq, nkv, hd, 0.2, t_start=0), full)
+    # softmax over the window only: recompute in f64 from the raw rows
+    t0 = 4
+    k = kc.view(np.float16).astype(np.float64).reshape(T, nkv, hd)
+    v = vc.view(np.float16).astype(np.float64).reshape(T, nkv, hd)
+    win = oracle.attend_f16(q, kc, vc, T, nq, nkv, hd, 0.2, t_start=t0)
+    for h in range(nq):
+        s = k[t0:, h // 3] @ q[h * hd:(h + 1) * hd].astype(np.float64) * 0.2
+        p = np.exp(s - s.max())
+        ref = (p / p.sum()) @ v[t0:, h // 3]
+        assert np.allclose(win[h * hd:(h + 1) * hd], ref, rtol=1e-5, atol=1e-6)
+
+
 def test_silu_closed_form():
     g = np.array([0.0, 1.0, -2.0, 10.0], np.float32)
     u = np.array([3.0, 2.0, 1.0, 0.5], np.float32)
