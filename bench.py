@@ -357,6 +357,11 @@ def bench_configs(be, torch, stream, copies: int):
             "roofline": {"bound": bound, "peak": peak, "unit": unit, "frac": round(t / peak, 4)},
             "note": "f32 scores are canonical fma chains (bit-exact, no MFMA); Q4_0 int32 block dots "
                     "on v_mfma_i32_16x16x64_i8 vs the int8 MFMA peak; walk includes top-32 selection"}
+        if name == "f32":
+            # the published fp32 peak counts packed (two-wide) FMAs; this build disables
+            # packed fp32 (v_pk_fma_f32), so one fma per lane per issue is its ceiling
+            out[f"gate_knn_{name}_34x10240x2560_q256_top32"]["roofline_unpacked"] = {
+                "peak": 78.6, "unit": unit, "frac": round(t / 78.6, 4)}
         log(f"[bench] gate_knn {name}: {out[f'gate_knn_{name}_34x10240x2560_q256_top32']}")
     for h in hf + hq:
         be.release_weight(h)
