@@ -177,8 +177,14 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
                 const uint8_t* lrow = a.qs + row * (static_cast<size_t>(a.cols) >> 1);
                 const uint8_t* hrow = a.qh + row * (static_cast<size_t>(a.cols) >> 2);
                 const int8_t* srow = a.sc + row * (static_cast<size_t>(a.cols) >> 4);
-                B.r[r].l = *reinterpret_cast<const uint4*>(lrow + c * 16u);
-                B.r[r].h = *reinterpret_cast<const uint2*>(hrow + c * 8u);
+                // weights are read once per launch: non-temporal loads keep them from
+                // displacing x and the scales in the caches
+                typedef uint32_t nt4 __attribute__((ext_vector_type(4)));
+                typedef uint32_t nt2 __attribute__((ext_vector_type(2)));
+                const nt4 lv = __builtin_nontemporal_load(reinterpret_cast<const nt4*>(lrow + c * 16u));
+                const nt2 hv = __builtin_nontemporal_load(reinterpret_cast<const nt2*>(hrow + c * 8u));
+                B.r[r].l = make_uint4(lv.x, lv.y, lv.z, lv.w);
+                B.r[r].h = make_uint2(hv.x, hv.y);
                 const uint32_t s2 = *reinterpret_cast<const uint16_t*>(srow + c * 2u);
                 const uint32_t d = (a.d + row * S)[c >> 3];
                 B.r[r].sd = s2 | (d << 16);
