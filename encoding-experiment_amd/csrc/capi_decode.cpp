@@ -21,7 +21,11 @@ using larql::DevWeight;
 using larql::fail;
 
 struct LayerDev {
+    // Q|K|V fused by rows and gate/up interleaved by rows when each pair shares a format;
+    // otherwise separate weights (mixed Q4_K / Q6_K projections, as in Q4_K_M files)
     DevWeight qkv, wo, gateup, down;
+    DevWeight wq, wk, wv, gate, up;
+    bool split_qkv = false, split_gu = false;
     float* input_norm = nullptr;
     float* post_attn_norm = nullptr;
     double eps = 1e-6;
@@ -42,6 +46,7 @@ struct larql_hip_model {
     std::vector<void*> allocs;
     // workspace
     float *h0 = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *xin = nullptr;
+    float* gtmp = nullptr;  // gate projection when gate and up have different formats
     larql::DeviceBuf part;
     // host-pointer decode_token cache key
     std::vector<uint64_t> key;
@@ -124,9 +129,6 @@ void check_supported(const larql_pipeline_layer& L) {
         fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: biases not supported");
     if (L.has_v_norm) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: V-norm not supported");
     if (L.layer_scalar != 0.0f) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: layer scalar not supported");
-    if (L.wq.format != L.wk.format || L.wq.format != L.wv.format)
-        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: mixed Q/K/V formats not supported");
-    if (L.gate.format != L.up.format) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: mixed gate/up formats not supported");
 }
 
 larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t n, size_t hidden,
@@ -163,12 +165,25 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
                 fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: per-layer head geometry must be uniform");
             }
             const size_t qd = static_cast<size_t>(d.nq) * d.hd, kvd = static_cast<size_t>(d.nkv) * d.hd;
-            d.qkv = build_weight(c, m, L.wq.format, hidden,
-                                 {{L.wq.data, L.wq.len, qd}, {L.wk.data, L.wk.len, kvd}, {L.wv.data, L.wv.len, kvd}},
-                                 false, on_device);
+            d.split_qkv = L.wq.format != L.wk.format || L.wq.format != L.wv.format;
+            if (d.split_qkv) {
+                d.wq = build_weight(c, m, L.wq.format, hidden, {{L.wq.data, L.wq.len, qd}}, false, on_device);
+                d.wk = build_weight(c, m, L.wk.format, hidden, {{L.wk.data, L.wk.len, kvd}}, false, on_device);
+                d.wv = build_weight(c, m, L.wv.format, hidden, {{L.wv.data, L.wv.len, kvd}}, false, on_device);
+            } else {
+                d.qkv = build_weight(c, m, L.wq.format, hidden,
+                                     {{L.wq.data, L.wq.len, qd}, {L.wk.data, L.wk.len, kvd}, {L.wv.data, L.wv.len, kvd}},
+                                     false, on_device);
+            }
             d.wo = build_weight(c, m, L.wo.format, qd, {{L.wo.data, L.wo.len, hidden}}, false, on_device);
-            d.gateup = build_weight(c, m, L.gate.format, hidden,
-                                    {{L.gate.data, L.gate.len, inter}, {L.up.data, L.up.len, inter}}, true, on_device);
+            d.split_gu = L.gate.format != L.up.format;
+            if (d.split_gu) {
+                d.gate = build_weight(c, m, L.gate.format, hidden, {{L.gate.data, L.gate.len, inter}}, false, on_device);
+                d.up = build_weight(c, m, L.up.format, hidden, {{L.up.data, L.up.len, inter}}, false, on_device);
+            } else {
+                d.gateup = build_weight(c, m, L.gate.format, hidden,
+                                        {{L.gate.data, L.gate.len, inter}, {L.up.data, L.up.len, inter}}, true, on_device);
+            }
             d.down = build_weight(c, m, L.down.format, inter, {{L.down.data, L.down.len, hidden}}, false, on_device);
             d.input_norm = upload_vec(c, m, L.input_norm, hidden, on_device);
             d.post_attn_norm = upload_vec(c, m, L.post_attn_norm, hidden, on_device);
@@ -182,6 +197,7 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
         m->qkv = static_cast<float*>(dev_alloc(m, (m->q_dim + 2 * m->kv_dim) * 4));
         m->attn = static_cast<float*>(dev_alloc(m, m->q_dim * 4));
         m->act = static_cast<float*>(dev_alloc(m, inter * 4));
+        m->gtmp = static_cast<float*>(dev_alloc(m, inter * 4));
         LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
     } catch (...) {
         for (void* p : m->allocs) (void)hipFree(p);
@@ -293,7 +309,15 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
         a.out = m->qkv;
         a.norm_w = L.input_norm;
         a.eps = L.eps;
-        larql::launch_mv(L.qkv, a, s);
+        if (L.split_qkv) {  // three launches into the [q | k | v] buffer, each with the norm
+            larql::launch_mv(L.wq, a, s);
+            a.out = m->qkv + m->q_dim;
+            larql::launch_mv(L.wk, a, s);
+            a.out = m->qkv + m->q_dim + m->kv_dim;
+            larql::launch_mv(L.wv, a, s);
+        } else {
+            larql::launch_mv(L.qkv, a, s);
+        }
 
         larql::AttnArgs at{};
         at.qkv = m->qkv;
@@ -323,8 +347,17 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
         g.out = m->act;
         g.norm_w = L.post_attn_norm;
         g.eps = L.eps;
-        g.epi = larql::EPI_SILU_PAIR;
-        larql::launch_mv(L.gateup, g, s);
+        if (L.split_gu) {  // gate, then up with silu(gate) * up in its epilogue
+            g.out = m->gtmp;
+            larql::launch_mv(L.gate, g, s);
+            g.out = m->act;
+            g.epi = larql::EPI_SILU_MUL;
+            g.resid = m->gtmp;
+            larql::launch_mv(L.up, g, s);
+        } else {
+            g.epi = larql::EPI_SILU_PAIR;
+            larql::launch_mv(L.gateup, g, s);
+        }
 
         larql::MvArgs d;
         d.x = m->act;

@@ -11,6 +11,7 @@ enum MvEpi : int {
     EPI_STORE = 0,      // out[n] = dot
     EPI_RESID = 1,      // out[n] = resid[n] + dot              (residual add, LI/src/forward/layer.rs:88-92)
     EPI_SILU_PAIR = 2,  // rows interleaved gate/up: out[n/2] = silu(gate) * up  (LI/src/ffn/mod.rs:87-94)
+    EPI_SILU_MUL = 3,   // out[n] = silu(resid[n]) * dot: the up projection after a separate gate
 };
 
 struct MvArgs {
@@ -117,6 +118,13 @@ __device__ __forceinline__ double slot_sum_d(double v, double* scratch, int wave
     return s;
 }
 
+// Output of a non-pair epilogue for a row whose dot is `tot` and resid value `rv`.
+__device__ __forceinline__ float epi_value(const MvArgs& a, float rv, float tot) {
+    if (a.epi == EPI_RESID) return rv + tot;
+    if (a.epi == EPI_SILU_MUL) return silu_mul(rv, tot);
+    return tot;
+}
+
 // Epilogue for a totals vector after the wave reduction.  `tot` is valid in lane
 // (r << rsh) for row row0 + r.  Used when the slot is a single wave.
 template <int RB>
@@ -129,7 +137,7 @@ __device__ __forceinline__ void epilogue_wave(const MvArgs& a, float tot, int la
         const float up = __shfl_down(tot, 1 << rsh, 64);
         if (owner && (r & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
     } else if (owner && row < a.rows) {
-        a.out[row] = a.epi == EPI_RESID ? a.resid[row] + tot : tot;
+        a.out[row] = epi_value(a, a.epi == EPI_STORE ? 0.f : a.resid[row], tot);
     }
 }
 
@@ -140,7 +148,7 @@ __device__ __forceinline__ void epilogue_lanes(const MvArgs& a, float tot, int l
         const float up = __shfl_down(tot, 1, 64);
         if (lane < rb && (lane & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
     } else if (lane < rb && row < a.rows) {
-        a.out[row] = a.epi == EPI_RESID ? a.resid[row] + tot : tot;
+        a.out[row] = epi_value(a, a.epi == EPI_STORE ? 0.f : a.resid[row], tot);
     }
 }
 

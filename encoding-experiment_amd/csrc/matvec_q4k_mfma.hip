@@ -296,7 +296,7 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
             const float up = __shfl_down(tot, 1, 64);  // rows 2i, 2i + 1 sit in adjacent lanes of one tile
             if ((lane & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
         } else if (row < a.rows) {
-            a.out[row] = a.epi == EPI_RESID ? a.resid[row] + tot : tot;
+            a.out[row] = epi_value(a, a.epi == EPI_STORE ? 0.f : a.resid[row], tot);
         }
     }
 }

@@ -78,7 +78,7 @@ __device__ __forceinline__ void epilogue_rv(const MvArgs& a, float tot, float rv
         const float up = __shfl_down(tot, 1 << rsh, 64);
         if (owner && (r & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
     } else if (owner && row < a.rows) {
-        a.out[row] = a.epi == EPI_RESID ? rv + tot : tot;
+        a.out[row] = epi_value(a, rv, tot);
     }
 }
 

@@ -243,7 +243,8 @@ enum { LARQL_ACT_SILU = 0, LARQL_ACT_GELU_TANH = 1 };
 /* FullPipelineLayer — LC/src/pipeline.rs:60-120, same fields in the same order.
  * Optional vectors are NULL when absent.  The HIP decode step implements the
  * Llama family: RMSNorm, gated SiLU FFN, no post-norms, no V-norm, no biases,
- * no layer scalar, Q4_K or Q6_K projections; anything else is reported as
+ * no layer scalar, Q4_K or Q6_K projections (each its own format, as in Q4_K_M files);
+ * anything else is reported as
  * LARQL_HIP_ERR_UNSUPPORTED so the caller falls back (predict.rs:397-430). */
 typedef struct {
     larql_quant_weight wq, wk, wv, wo;

@@ -282,17 +282,20 @@ def attend_f16(q, kc, vc, T: int, num_q: int, num_kv: int, head_dim: int, scale:
     return out
 
 
+_PROJ = ("wq", "wk", "wv", "wo", "gate", "up", "down")
+
+
 class _Layer(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_void_p) for n in
-                ("wq", "wk", "wv", "wo", "gate", "up", "down",
-                 "input_norm", "post_attn_norm", "k_cache", "v_cache")]
+    _fields_ = [(n, ctypes.c_void_p) for n in _PROJ + ("input_norm", "post_attn_norm", "k_cache", "v_cache")] + \
+               [("fmt", ctypes.c_int * 7)]
 
 
 def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, num_kv: int,
                  head_dim: int, rope_base: float, eps: float = 1e-6, window: int = 0):
     """One Llama decoder layer on the CPU.  ``layer`` holds numpy arrays keyed as
     the lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits) are updated in place.
-    window > 0 attends over the last `window` positions only."""
+    window > 0 attends over the last `window` positions only.  ``layer["formats"]``
+    (optional) maps a projection name to "q6_k" for Q6_K bytes (default Q4_K)."""
     keep = {}
     st = _Layer()
     for name, dt in (("wq", np.uint8), ("wk", np.uint8), ("wv", np.uint8), ("wo", np.uint8),
@@ -301,6 +304,9 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
         a = _c(layer[name], dt)
         keep[name] = a
         setattr(st, name, a.ctypes.data)
+    fm = layer.get("formats", {})
+    for i, name in enumerate(_PROJ):
+        st.fmt[i] = 1 if fm.get(name, "q4_k") == "q6_k" else 0
     for name in ("k_cache", "v_cache"):
         a = layer[name]
         assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]

@@ -576,6 +576,12 @@ void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_
     free(sc);
 }
 
+/* A projection in its layer's format: Q4_K (0) or Q6_K (1). */
+static void lo_proj(int fmt, const uint8_t* w, const float* x, float* out, size_t rows, size_t cols) {
+    if (fmt == 1) lo_q6k_matvec(w, x, out, rows, cols);
+    else lo_q4k_matvec(w, x, out, rows, cols);
+}
+
 /* One Llama layer: pre-norm attention + SwiGLU FFN, no post-norms, norm offset 0
  * (LI/src/attention/block.rs:52-157, LI/src/forward/layer.rs:50-94; per-op order of
  * the reference GPU decode LC/src/metal/decode.rs:144-715).  The new K/V row is
@@ -603,9 +609,9 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
     float* a = (float*)malloc(inter * sizeof(float));
 
     lo_rms_norm(h, L->input_norm, 0.0f, eps, xn, hidden);
-    lo_q4k_matvec(L->wq, xn, q, qd, hidden);
-    lo_q4k_matvec(L->wk, xn, k, kvd, hidden);
-    lo_q4k_matvec(L->wv, xn, v, kvd, hidden);
+    lo_proj(L->fmt[0], L->wq, xn, q, qd, hidden);
+    lo_proj(L->fmt[1], L->wk, xn, k, kvd, hidden);
+    lo_proj(L->fmt[2], L->wv, xn, v, kvd, hidden);
     lo_rope_at(q, num_q, head_dim, head_dim, rope_base, pos);
     lo_rope_at(k, num_kv, head_dim, head_dim, rope_base, pos);
     for (size_t i = 0; i < kvd; i++) {
@@ -615,14 +621,14 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
     float scale = (float)(1.0 / sqrt((double)head_dim));
     const size_t T = pos + 1, t0 = (window > 0 && T > window) ? T - window : 0;
     lo_attend_f16(q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, T - t0, num_q, num_kv, head_dim, scale, att);
-    lo_q4k_matvec(L->wo, att, o, hidden, qd);
+    lo_proj(L->fmt[3], L->wo, att, o, hidden, qd);
     for (size_t i = 0; i < hidden; i++) h[i] = h[i] + o[i];
 
     lo_rms_norm(h, L->post_attn_norm, 0.0f, eps, xn, hidden);
-    lo_q4k_matvec(L->gate, xn, g, inter, hidden);
-    lo_q4k_matvec(L->up, xn, u, inter, hidden);
+    lo_proj(L->fmt[4], L->gate, xn, g, inter, hidden);
+    lo_proj(L->fmt[5], L->up, xn, u, inter, hidden);
     lo_silu_gate_up(g, u, a, inter);
-    lo_q4k_matvec(L->down, a, o, hidden, inter);
+    lo_proj(L->fmt[6], L->down, a, o, hidden, inter);
     for (size_t i = 0; i < hidden; i++) h[i] = h[i] + o[i];
 
     free(xn); free(q); free(k); free(v); free(att); free(o); free(g); free(u); free(a);

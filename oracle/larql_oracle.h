@@ -84,9 +84,12 @@ void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_
 /* One Llama decoder layer (Q4_K projections, fp16 KV cache) at position pos.
  * h is updated in place; the new K/V row is written into kc/vc at pos. */
 typedef struct {
-    const uint8_t *wq, *wk, *wv, *wo, *gate, *up, *down;  /* Q4_K 148-byte layout */
+    const uint8_t *wq, *wk, *wv, *wo, *gate, *up, *down;  /* Q4_K 148-byte or Q6_K 210-byte layout */
     const float *input_norm, *post_attn_norm;
     uint16_t *k_cache, *v_cache;                             /* [max_seq][kv_heads][head_dim] fp16 */
+    /* per projection (wq, wk, wv, wo, gate, up, down): 0 = Q4_K, 1 = Q6_K; mixed formats
+     * per projection as the reference's per-layer QuantWeight allows (LC/src/pipeline.rs:22-27) */
+    int fmt[7];
 } lo_layer_t;
 
 void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,

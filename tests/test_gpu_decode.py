@@ -26,34 +26,45 @@ def q4k(rows, cols, seed, std=0.02):
     return oracle.quantize_q4_k(oracle.gauss(seed, rows * cols, 0.0, std))
 
 
+def q6k(rows, cols, seed, std=0.02):
+    return oracle.quantize_q6_k(oracle.gauss(seed, rows * cols, 0.0, std))
+
+
 class SmallModel:
-    def __init__(self, n_layers, hidden, inter, nq, nkv, hd, cap, seed=0):
+    """formats: projection name -> "q6_k" for Q6_K weights (default Q4_K)."""
+
+    def __init__(self, n_layers, hidden, inter, nq, nkv, hd, cap, seed=0, formats=None):
         self.n, self.hidden, self.inter, self.nq, self.nkv, self.hd = n_layers, hidden, inter, nq, nkv, hd
+        self.formats = dict(formats or {})
         self.layers = []
         qd, kvd = nq * hd, nkv * hd
+        shapes = dict(wq=(qd, hidden), wk=(kvd, hidden), wv=(kvd, hidden), wo=(hidden, qd), gate=(inter, hidden),
+                      up=(inter, hidden), down=(hidden, inter))
         for l in range(n_layers):
             s = seed + 100 * l
-            self.layers.append(dict(
-                wq=q4k(qd, hidden, s + 1), wk=q4k(kvd, hidden, s + 2), wv=q4k(kvd, hidden, s + 3),
-                wo=q4k(hidden, qd, s + 4), gate=q4k(inter, hidden, s + 5), up=q4k(inter, hidden, s + 6),
-                down=q4k(hidden, inter, s + 7),
-                input_norm=(1.0 + 0.1 * oracle.gauss(s + 8, hidden)).astype(np.float32),
-                post_attn_norm=(1.0 + 0.1 * oracle.gauss(s + 9, hidden)).astype(np.float32),
-                k_cache=np.zeros(cap * kvd, np.uint16), v_cache=np.zeros(cap * kvd, np.uint16)))
+            L = {}
+            for i, (name, (r, c)) in enumerate(shapes.items()):
+                L[name] = (q6k if self.formats.get(name) == "q6_k" else q4k)(r, c, s + 1 + i)
+            L.update(input_norm=(1.0 + 0.1 * oracle.gauss(s + 8, hidden)).astype(np.float32),
+                     post_attn_norm=(1.0 + 0.1 * oracle.gauss(s + 9, hidden)).astype(np.float32),
+                     k_cache=np.zeros(cap * kvd, np.uint16), v_cache=np.zeros(cap * kvd, np.uint16),
+                     formats=self.formats)
+            self.layers.append(L)
 
     def hip_layers(self, rope_base, window=0):
+        fm = {k: larql_hip.Q6_K for k, v in self.formats.items() if v == "q6_k"}
         return [larql_hip.make_layer(L["wq"], L["wk"], L["wv"], L["wo"], L["gate"], L["up"], L["down"],
                                      L["input_norm"], L["post_attn_norm"], head_dim=self.hd,
                                      num_q_heads=self.nq, num_kv_heads=self.nkv, rope_base=rope_base,
-                                     sliding_window=window)
+                                     sliding_window=window, formats=fm)
                 for L in self.layers]
 
 
 def run_sequence(hip, T0, n_tokens, n_layers=2, hidden=512, inter=1024, nq=8, nkv=2, hd=64, rope=500000.0,
-                 window=0):
+                 window=0, formats=None):
     print(f"[decode] layers={n_layers} hidden={hidden} nq={nq} nkv={nkv} hd={hd} T0={T0} tokens={n_tokens} "
-          f"window={window}", flush=True)
-    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=T0 + n_tokens + 1, seed=T0)
+          f"window={window} formats={formats}", flush=True)
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=T0 + n_tokens + 1, seed=T0, formats=formats)
     kvd = nkv * hd
     hip.reset_kv_cache()
     for l, L in enumerate(m.layers):
@@ -111,6 +122,14 @@ def test_decode_head_geometries(hip, nq, nkv, hd, T0):
     # hd a multiple of 32 up to 256, 1..8 query heads per kv head (q_dim a multiple of 256
     # for the Q4_K output projection)
     run_sequence(hip, T0=T0, n_tokens=2, n_layers=1, nq=nq, nkv=nkv, hd=hd, hidden=512, inter=512)
+
+
+@pytest.mark.parametrize("formats", [{"wv": "q6_k", "down": "q6_k"}, {"wq": "q6_k", "up": "q6_k"},
+                                     {"gate": "q6_k", "wo": "q6_k"}])
+def test_decode_mixed_projection_formats(hip, formats):
+    # Q4_K_M-style layers: some projections Q6_K (split Q|K|V launches, gate then up with
+    # silu(gate) * up in the up epilogue)
+    run_sequence(hip, T0=40, n_tokens=2, n_layers=2, formats=formats)
 
 
 def test_decode_unsupported_layer_returns_none(hip):
