@@ -431,6 +431,36 @@ extern "C" int larql_hip_decode_token(larql_hip_ctx* c, const larql_pipeline_lay
     });
 }
 
+extern "C" int larql_hip_prefill_q4(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t num_layers,
+                                    const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim,
+                                    size_t seq_len, size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
+                                    float rope_base, int use_qk_norm, float softcap, float* out) {
+    return guarded(c, [&] {
+        if (!layers || !x || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        if (use_qk_norm || softcap != 0.f) fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill: QK-norm / softcap not supported");
+        if (num_q_heads * head_dim != q_dim || num_kv_heads * head_dim != kv_dim)
+            fail(LARQL_HIP_ERR_INVALID, "prefill: q_dim/kv_dim do not match the head geometry");
+        (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
+        if (seq_len == 0) return;
+        auto key = layers_key(layers, num_layers, hidden, inter);
+        larql_hip_model*& m = c->trait_model;
+        if (!m || m->key != key) {
+            destroy_model(c, m);
+            m = nullptr;
+            m = build_model(c, layers, num_layers, hidden, inter, false);
+            m->key = key;
+        }
+        if (m->q_dim != q_dim || m->kv_dim != kv_dim)
+            fail(LARQL_HIP_ERR_INVALID, "prefill: layer geometry differs from q_dim/kv_dim");
+        kv_ensure(c, m->layers.size(), m->nkv, m->hd, seq_len);
+        c->kv.current_len = 0;  // a new prompt at positions 0 .. seq_len - 1
+        const float* dx = stage_upload(c, c->stage_in, x, seq_len * hidden);
+        float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, seq_len * hidden * sizeof(float)));
+        for (size_t p = 0; p < seq_len; p++) run_decode(c, m, dx + p * hidden, dout + p * hidden, nullptr, c->stream);
+        download(c, out, dout, seq_len * hidden * sizeof(float));
+    });
+}
+
 extern "C" int larql_hip_populate_kv_layer(larql_hip_ctx* c, size_t layer, const float* k_data, const float* v_data,
                                            size_t seq_len, size_t num_kv_heads, size_t head_dim) {
     return guarded(c, [&] {

@@ -77,6 +77,8 @@ SIGNATURES = {
     "larql_hip_topk_dev": (_I, [_P, _P, _SZ, _SZ, _SZ, _I, _P, _P, _P]),
     # decode step (structs declared below; pointers passed as void*)
     "larql_hip_decode_token": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
+    "larql_hip_prefill_q4": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float,
+                                  ctypes.c_int, ctypes.c_float, _P]),
     "larql_hip_populate_kv_layer": (_I, [_P, _SZ, _P, _P, _SZ, _SZ, _SZ]),
     "larql_hip_reset_kv_cache": (_I, [_P]),
     "larql_hip_kv_cache_len": (_I, [_P, ctypes.POINTER(_SZ)]),
@@ -415,6 +417,20 @@ class HipBackend:
                                               kv_dim, num_q_heads, num_kv_heads, head_dim, rope_base,
                                               out.ctypes.data_as(_P))
         return out if self._ok(rc) else None
+
+    def prefill_q4(self, layers, x, hidden: int, inter: int, q_dim: int, kv_dim: int, seq_len: int,
+                   num_q_heads: int, num_kv_heads: int, head_dim: int, rope_base: float, use_qk_norm: bool = False,
+                   softcap: float = 0.0):
+        """backend.rs:139-152: a prompt [seq_len, hidden] through all layers at positions
+        0..seq_len-1, filling the KV cache; returns the final hidden states [seq_len, hidden]
+        or None."""
+        arr = (PipelineLayer * len(layers))(*layers)
+        xv, xp = _arr(x, np.float32)
+        out = np.empty(seq_len * hidden, dtype=np.float32)
+        rc = self._lib.larql_hip_prefill_q4(self._ctx, ctypes.cast(arr, _P), len(layers), xp, hidden, inter, q_dim,
+                                            kv_dim, seq_len, num_q_heads, num_kv_heads, head_dim, rope_base,
+                                            1 if use_qk_norm else 0, softcap, out.ctypes.data_as(_P))
+        return out.reshape(seq_len, hidden) if self._ok(rc) else None
 
     def populate_kv_layer(self, layer: int, k_data, v_data, seq_len: int, num_kv_heads: int, head_dim: int):
         """backend.rs:103-107 (K/V f32 [seq_len, num_kv*head_dim], stored as fp16)."""

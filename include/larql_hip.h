@@ -285,6 +285,18 @@ int larql_hip_decode_token(larql_hip_ctx* ctx, const larql_pipeline_layer* layer
                            size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float rope_base,
                            float* out);
 
+/* ComputeBackend::prefill_q4 — LC/src/backend.rs:139-152: a prompt of seq_len tokens
+ * (x: host [seq_len][hidden]) through all layers at positions 0 .. seq_len-1, the
+ * post-RoPE K/V of every position stored in the cache (whose length becomes seq_len);
+ * out: host [seq_len][hidden], the final hidden state of every position (before the
+ * final norm).  Positions run in order through the decode-step kernels, as the
+ * reference's Metal prefill runs its projections per position (LC/src/metal/prefill.rs).
+ * use_qk_norm != 0 or softcap != 0 (Gemma-style layers) return UNSUPPORTED. */
+int larql_hip_prefill_q4(larql_hip_ctx* ctx, const larql_pipeline_layer* layers, size_t num_layers,
+                         const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim, size_t seq_len,
+                         size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float rope_base,
+                         int use_qk_norm, float softcap, float* out);
+
 /* ComputeBackend::populate_kv_layer — LC/src/backend.rs:103-107: K/V rows
  * [seq_len][num_kv_heads*head_dim] f32 (stored as fp16, RNE); sets the cache
  * length to seq_len. */

@@ -132,6 +132,35 @@ def test_decode_mixed_projection_formats(hip, formats):
     run_sequence(hip, T0=40, n_tokens=2, n_layers=2, formats=formats)
 
 
+def test_prefill_q4_matches_oracle_and_decode(hip):
+    """prefill_q4 (backend.rs:139-152): a 6-token prompt from positions 0; every
+    position's hidden state against the oracle layers, the cache left at 6 positions,
+    and a following decode_token identical to decoding the prompt token by token."""
+    n_layers, hidden, inter, nq, nkv, hd, seq = 2, 512, 1024, 8, 2, 64, 6
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=77, formats={"wv": "q6_k"})
+    layers = m.hip_layers(10000.0)
+    x = np.stack([oracle.gauss(8000 + p, hidden) for p in range(seq)])
+    hip.reset_kv_cache()
+    got = hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0)
+    assert got is not None and hip.kv_cache_len() == seq
+    for p in range(seq):
+        ref = x[p].copy()
+        for L in m.layers:
+            ref = oracle.decode_layer(L, ref, p, hidden, inter, nq, nkv, hd, 10000.0)
+        e = rel_err(got[p], ref)
+        print(f"  position {p}: rel_err={e:.3e}", flush=True)
+        assert e <= REL_TOL, (p, e)
+    nxt = oracle.gauss(9000, hidden)
+    after_prefill = hip.decode_token(layers, nxt, hidden, inter, nq * hd, nkv * hd, nq, nkv, hd, 10000.0)
+    hip.reset_kv_cache()
+    for p in range(seq):
+        hip.decode_token(layers, x[p], hidden, inter, nq * hd, nkv * hd, nq, nkv, hd, 10000.0)
+    stepwise = hip.decode_token(layers, nxt, hidden, inter, nq * hd, nkv * hd, nq, nkv, hd, 10000.0)
+    assert np.array_equal(after_prefill, stepwise)
+    with pytest.raises(larql_hip.LarqlHipError):  # QK-norm layers: UNSUPPORTED (the trait's None)
+        hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0, use_qk_norm=True)
+
+
 def test_decode_unsupported_layer_returns_none(hip):
     be = larql_hip.HipBackend(0, strict=False)
     try:
