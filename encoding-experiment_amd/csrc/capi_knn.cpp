@@ -125,3 +125,44 @@ extern "C" int larql_hip_gate_knn(larql_hip_ctx* c, int format, const void* gate
         LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
     });
 }
+
+// lm-head KNN (LV/src/index/walk.rs:549-583): quantize_to_q8 of each query, the Q4_0
+// matvec over the vocab, then the signed top-k, all on the device.
+static void run_lm_head_knn(larql_hip_ctx* c, const DevWeight& w, const float* dq, size_t nq, size_t top_k,
+                            uint32_t* di, float* dv, hipStream_t s) {
+    if (w.format != LARQL_Q4_0) fail(LARQL_HIP_ERR_UNSUPPORTED, "lm-head KNN: the head must be Q4_0");
+    if (nq == 0) fail(LARQL_HIP_ERR_INVALID, "lm-head KNN: nq == 0");
+    if (w.rows > 0x7FFFFFFF) fail(LARQL_HIP_ERR_UNSUPPORTED, "lm-head KNN: vocab too large");
+    check_k(top_k, static_cast<int>(w.rows));
+    const size_t hidden = w.cols, nb = hidden / 32;
+    int8_t* q8 = static_cast<int8_t*>(larql::ensure(c, c->knn_q8, nq * hidden));
+    float* q8s = static_cast<float*>(larql::ensure(c, c->knn_q8s, nq * nb * sizeof(float)));
+    larql::launch_quantize_q8(dq, hidden, nq, q8, q8s, s);
+    float* S = static_cast<float*>(larql::ensure(c, c->knn_scores, nq * w.rows * sizeof(float)));
+    larql::launch_q4_0_matvec(w, q8, q8s, S, nq, s);
+    larql::launch_topk(S, nq, w.rows, static_cast<int>(w.rows), static_cast<int>(top_k), 1, di, dv, s);
+}
+
+extern "C" int larql_hip_lm_head_knn(larql_hip_ctx* c, const uint8_t* lm_head_q4, size_t len, const float* query,
+                                     size_t vocab, size_t hidden, size_t top_k, uint32_t* idx, float* scores) {
+    return guarded(c, [&] {
+        if (!lm_head_q4 || !query || !idx || !scores) fail(LARQL_HIP_ERR_INVALID, "lm-head KNN: null pointer");
+        const DevWeight& w = larql::cached_weight(c, LARQL_Q4_0, lm_head_q4, len, nullptr, vocab, hidden);
+        const float* dq = stage_upload(c, c->stage_in, query, hidden);
+        uint32_t* di = static_cast<uint32_t*>(larql::ensure(c, c->knn_idx, top_k * sizeof(uint32_t)));
+        float* dv = static_cast<float*>(larql::ensure(c, c->knn_val, top_k * sizeof(float)));
+        run_lm_head_knn(c, w, dq, 1, top_k, di, dv, c->stream);
+        LARQL_HIP_CHECK(hipMemcpyAsync(idx, di, top_k * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+        LARQL_HIP_CHECK(hipMemcpyAsync(scores, dv, top_k * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
+    });
+}
+
+extern "C" int larql_hip_lm_head_knn_dev(larql_hip_ctx* c, uint64_t handle, const float* queries, size_t nq,
+                                         size_t top_k, uint32_t* idx, float* scores, void* stream) {
+    return guarded(c, [&] {
+        if (!queries || !idx || !scores) fail(LARQL_HIP_ERR_INVALID, "lm-head KNN: null pointer");
+        const DevWeight& w = larql::lookup(c, handle);
+        run_lm_head_knn(c, w, queries, nq, top_k, idx, scores, pick_stream(c, stream));
+    });
+}

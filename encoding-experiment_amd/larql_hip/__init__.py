@@ -75,6 +75,8 @@ SIGNATURES = {
     "larql_hip_gate_knn_dev": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _P, _P, _P]),
     "larql_hip_gate_scores_dev": (_I, [_P, _P, _SZ, _P, _SZ, _P, _P]),
     "larql_hip_topk_dev": (_I, [_P, _P, _SZ, _SZ, _SZ, _I, _P, _P, _P]),
+    "larql_hip_lm_head_knn": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _P, _P]),
+    "larql_hip_lm_head_knn_dev": (_I, [_P, _U64, _P, _SZ, _SZ, _P, _P, _P]),
     # decode step (structs declared below; pointers passed as void*)
     "larql_hip_decode_token": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
     "larql_hip_prefill_q4": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float,
@@ -483,6 +485,21 @@ class HipBackend:
         rc = self._lib.larql_hip_gate_knn(self._ctx, fmt, gp, g.nbytes, features, hidden, q.ctypes.data_as(_P), nq,
                                           top_k, idx.ctypes.data_as(_P), val.ctypes.data_as(_P))
         return (idx, val) if self._ok(rc) else None
+
+    def lm_head_knn(self, lm_head_q4, vocab: int, hidden: int, query, top_k: int):
+        """lm_head_knn_backend's Q4 path (LV/src/index/walk.rs:549-583): top_k (token, score)
+        by signed score descending, ties in index order; None if unsupported."""
+        w, wp = _arr(lm_head_q4, np.uint8)
+        q, qp = _arr(query, np.float32)
+        idx = np.empty(top_k, dtype=np.uint32)
+        val = np.empty(top_k, dtype=np.float32)
+        rc = self._lib.larql_hip_lm_head_knn(self._ctx, wp, w.nbytes, qp, vocab, hidden, top_k,
+                                             idx.ctypes.data_as(_P), val.ctypes.data_as(_P))
+        return (idx, val) if self._ok(rc) else None
+
+    def lm_head_knn_dev(self, handle: int, queries, nq: int, top_k: int, idx, scores, stream=None):
+        self._check(self._lib.larql_hip_lm_head_knn_dev(self._ctx, handle, _dptr(queries), nq, top_k, _dptr(idx),
+                                                        _dptr(scores), _stream_ptr(stream)))
 
     @staticmethod
     def _handle_array(handles):

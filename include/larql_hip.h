@@ -223,6 +223,18 @@ int larql_hip_gate_scores_dev(larql_hip_ctx* ctx, const uint64_t* handles, size_
 int larql_hip_topk_dev(larql_hip_ctx* ctx, const float* scores, size_t rows, size_t n, size_t k, int signed_mode,
                        uint32_t* idx, float* vals, void* stream);
 
+/* lm-head KNN, the Q4 path of VectorIndex::lm_head_knn_backend (LV/src/index/walk.rs:549-583):
+ * query quantized by quantize_to_q8, scores = q4_matvec(lm_head_q4 [vocab][hidden] Q4_0),
+ * the top_k tokens by signed score descending (ties in index order), 1 <= top_k <= 64.
+ * Host-pointer form: lm_head_q4 / query / idx / scores in host memory (the head is
+ * uploaded once and cached like every weight). */
+int larql_hip_lm_head_knn(larql_hip_ctx* ctx, const uint8_t* lm_head_q4, size_t len, const float* query,
+                          size_t vocab, size_t hidden, size_t top_k, uint32_t* idx, float* scores);
+/* Device form: a registered LARQL_Q4_0 head, nq queries f32 [nq][hidden] (device),
+ * idx / scores [nq][top_k] (device). */
+int larql_hip_lm_head_knn_dev(larql_hip_ctx* ctx, uint64_t handle, const float* queries, size_t nq, size_t top_k,
+                              uint32_t* idx, float* scores, void* stream);
+
 /* ── decode step: layers, KV cache, full-pipeline decode ───────────────── */
 
 /* QuantWeight — LC/src/pipeline.rs:22-27.  `data`/`len` are reference-layout

@@ -197,3 +197,41 @@ def test_gate_knn_34_layers_full_size(hip):
     finally:
         for h in handles_f32 + handles_q4:
             hip.release_weight(h)
+
+
+@pytest.mark.parametrize("vocab,hidden,k", [(10007, 512, 5), (32000, 1024, 64), (64, 64, 64)])
+def test_lm_head_knn_q4_bit_exact(hip, vocab, hidden, k):
+    """lm_head_knn_backend's Q4 path (LV/src/index/walk.rs:549-583): quantize_to_q8, the
+    Q4_0 matvec over the vocab, top-k by signed score (ties in index order)."""
+    print(f"[lm-head knn] vocab={vocab} hidden={hidden} k={k}", flush=True)
+    head = oracle.quantize_q4_0(oracle.gauss(51, vocab * hidden, 0.0, 0.02))
+    query = oracle.gauss(52, hidden)
+    got = hip.lm_head_knn(head, vocab, hidden, query, k)
+    q8, q8s = oracle.quantize_to_q8(query)
+    scores = oracle.q4_0_matvec_blockint(head, q8, q8s, vocab, hidden)
+    ref_i, ref_v = oracle.topk_signed(scores, k)
+    np.testing.assert_array_equal(got[0], ref_i)
+    np.testing.assert_array_equal(got[1].view(np.uint32), ref_v.view(np.uint32))
+
+
+def test_lm_head_knn_dev_batch(hip):
+    """Device form over several queries equals the host form query by query."""
+    torch = pytest.importorskip("torch")
+    vocab, hidden, nq, k = 5000, 256, 3, 10
+    head = oracle.quantize_q4_0(oracle.gauss(53, vocab * hidden, 0.0, 0.02))
+    queries = oracle.gauss(54, nq * hidden).reshape(nq, hidden)
+    h = hip.register_weight(larql_hip.Q4_0, head, vocab, hidden)
+    try:
+        dq = torch.from_numpy(queries).cuda()
+        di = torch.empty(nq * k, device="cuda", dtype=torch.int32)
+        dv = torch.empty(nq * k, device="cuda", dtype=torch.float32)
+        hip.lm_head_knn_dev(h, dq, nq, k, di, dv)
+        hip.synchronize()
+        gi = di.cpu().numpy().view(np.uint32).reshape(nq, k)
+        gv = dv.cpu().numpy().reshape(nq, k)
+        for i in range(nq):
+            ri, rv = hip.lm_head_knn(head, vocab, hidden, queries[i], k)
+            np.testing.assert_array_equal(gi[i], ri)
+            np.testing.assert_array_equal(gv[i].view(np.uint32), rv.view(np.uint32))
+    finally:
+        hip.release_weight(h)
