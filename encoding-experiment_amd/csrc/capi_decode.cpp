@@ -11,6 +11,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <algorithm>
 #include <vector>
 
 #include "capi_util.h"
@@ -48,6 +49,7 @@ struct larql_hip_model {
     float *h0 = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *xin = nullptr;
     float* gtmp = nullptr;  // gate projection when gate and up have different formats
     larql::DeviceBuf part;
+    larql::DeviceBuf prompt;  // batched prompt pass: activations of all positions
     // host-pointer decode_token cache key
     std::vector<uint64_t> key;
 };
@@ -212,6 +214,7 @@ void destroy_model(larql_hip_ctx* c, larql_hip_model* m) {
     (void)hipDeviceSynchronize();
     for (void* p : m->allocs) (void)hipFree(p);
     if (m->part.p) (void)hipFree(m->part.p);
+    if (m->prompt.p) (void)hipFree(m->prompt.p);
     (void)c;
     delete m;
 }
@@ -431,6 +434,67 @@ extern "C" int larql_hip_decode_token(larql_hip_ctx* c, const larql_pipeline_lay
     });
 }
 
+// The batched prompt pass takes layers whose projections are all Q4_K with Q|K|V and
+// gate/up fused (every Llama layer of a Q4_K file); others run position by position.
+bool prompt_batchable(const larql_hip_model* m) {
+    for (const LayerDev& L : m->layers)
+        if (L.split_qkv || L.split_gu || L.qkv.format != LARQL_Q4_K || L.wo.format != LARQL_Q4_K ||
+            L.gateup.format != LARQL_Q4_K || L.down.format != LARQL_Q4_K)
+            return false;
+    return true;
+}
+
+// All M positions (0 .. M-1) of a prompt through every layer at once: the projections as
+// Q4_K GEMMs on the matrix cores with f32 operands (fp16 operands' ~1e-4 per projection
+// compounds to >1e-3 of the output over 8+ layers), the attention in prompt mode (each query over its
+// causal prefix, which the RoPE / KV kernel has written to the cache first).
+void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M, float* dout, hipStream_t s) {
+    auto& kv = c->kv;
+    kv_ensure(c, m->layers.size(), m->nkv, m->hd, M);
+    const size_t hidden = m->hidden, inter = m->inter, qd = m->q_dim, kvd = m->kv_dim, ld = qd + 2 * kvd;
+    const size_t wide = std::max({hidden, qd, inter}), gw = std::max(hidden, 2 * inter);
+    const int S = larql::attn_prompt_splits(1, static_cast<int>(M), 0);
+    const size_t part_n = M * static_cast<size_t>(m->nq) * S * (m->hd + 2);
+    const size_t n_f = 2 * M * hidden + M * wide + M * ld + M * qd + M * gw + M * inter + part_n;
+    float* base = static_cast<float*>(larql::ensure(c, m->prompt, n_f * sizeof(float)));
+    float *H0 = base, *H1 = H0 + M * hidden, *XN = H1 + M * hidden, *QKV = XN + M * wide, *ATT = QKV + M * ld;
+    float *G = ATT + M * qd, *ACT = G + M * gw, *PART = ACT + M * inter;
+    larql::launch_copy_f32(dx, H0, M * hidden, s);
+    for (size_t l = 0; l < m->layers.size(); l++) {
+        const LayerDev& L = m->layers[l];
+        larql::launch_rmsnorm_rows(H0, L.input_norm, XN, M, hidden, L.eps, s);
+        larql::launch_q4k_gemm_f32(L.qkv, XN, QKV, M, s);
+        const float2* rope = rope_table(c, L.rope_base, L.rdim, s);
+        larql::launch_rope_kv_rows(QKV, M, 0, qd, kvd, L.hd, L.rdim, rope, kv.k[l], kv.v[l], L.nkv, s);
+        larql::AttnArgs at{};
+        at.qkv = QKV;
+        at.kc = kv.k[l];
+        at.vc = kv.v[l];
+        at.out = ATT;
+        at.part = PART;
+        at.num_q = L.nq;
+        at.num_kv = L.nkv;
+        at.hd = L.hd;
+        at.rdim = L.rdim;
+        at.T = 1;  // query p has T = 1 + p
+        at.scale = L.attn_scale;
+        at.rope = rope;
+        at.batch = static_cast<int>(M);
+        at.window = L.window;
+        at.qkv_ld = static_cast<int>(ld);
+        larql::launch_attention(at, s);
+        larql::launch_q4k_gemm_f32(L.wo, ATT, G, M, s);
+        larql::launch_add_rows(H0, G, H1, M * hidden, s);
+        larql::launch_rmsnorm_rows(H1, L.post_attn_norm, XN, M, hidden, L.eps, s);
+        larql::launch_q4k_gemm_f32(L.gateup, XN, G, M, s);
+        larql::launch_silu_pair_rows(G, ACT, M * inter, s);
+        larql::launch_q4k_gemm_f32(L.down, ACT, G, M, s);
+        larql::launch_add_rows(H1, G, H0, M * hidden, s);
+    }
+    larql::launch_copy_f32(H0, dout, M * hidden, s);
+    kv.current_len = M;
+}
+
 extern "C" int larql_hip_prefill_q4(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t num_layers,
                                     const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim,
                                     size_t seq_len, size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
@@ -456,7 +520,11 @@ extern "C" int larql_hip_prefill_q4(larql_hip_ctx* c, const larql_pipeline_layer
         c->kv.current_len = 0;  // a new prompt at positions 0 .. seq_len - 1
         const float* dx = stage_upload(c, c->stage_in, x, seq_len * hidden);
         float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, seq_len * hidden * sizeof(float)));
-        for (size_t p = 0; p < seq_len; p++) run_decode(c, m, dx + p * hidden, dout + p * hidden, nullptr, c->stream);
+        if (seq_len > 1 && prompt_batchable(m))
+            run_prompt(c, m, dx, seq_len, dout, c->stream);
+        else
+            for (size_t p = 0; p < seq_len; p++)
+                run_decode(c, m, dx + p * hidden, dout + p * hidden, nullptr, c->stream);
         download(c, out, dout, seq_len * hidden * sizeof(float));
     });
 }

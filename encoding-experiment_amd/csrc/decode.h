@@ -15,9 +15,18 @@ struct AttnArgs {
     int T, t_begin, S;  // S is set by launch_attention
     float scale;
     const float2* rope;  // [cap][rdim / 2] cos, sin (launch_rope_table)
+    // Prompt mode (prefill): grid z = query position p of `batch`, T = T + p for query p,
+    // the window start recomputed per query, qkv rows qkv_ld floats apart, every K/V row
+    // (the query's own included) already in the cache, out rows num_q * hd apart and
+    // partials [batch][num_q][S][hd + 2] with S the largest query's split count.
+    int batch = 0, window = 0, qkv_ld = 0;
 };
 
 void launch_attention(const AttnArgs& a, hipStream_t s);
+// Position splits of one query (T positions from t_begin) and the most over a prompt's
+// queries T0 .. T0 + batch - 1 (its partials stride).
+int attn_splits(int T, int t_begin);
+int attn_prompt_splits(int T0, int batch, int window);
 // cos/sin table for positions [0, cap): angle p * base^(-2i/rdim) in f64, as the CPU
 // path computes it (LI/src/attention/rope.rs:22-55), rounded to f32.
 void launch_rope_table(float2* cs, size_t cap, int rdim, double base, hipStream_t s);
@@ -27,6 +36,12 @@ bool attn_supported(int reps, int hd);
 // K/V rows [seq][num_kv][hd] (f32 or fp16 bits) into the V cache layout.
 void launch_v_to_cache(const void* src, bool src_f32, __half* dst, size_t seq, int num_kv, int hd, hipStream_t s);
 void launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s);
+// Row kernels of the batched prompt pass (prompt.hip).
+void launch_rmsnorm_rows(const float* X, const float* w, float* Y, size_t m, size_t n, double eps, hipStream_t s);
+void launch_rope_kv_rows(const float* QKV, size_t m, size_t p0, size_t q_dim, size_t kv_dim, int hd, int rdim,
+                         const float2* rope, __half* kc, __half* vc, int num_kv, hipStream_t s);
+void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipStream_t s);
+void launch_silu_pair_rows(const float* GU, float* act, size_t n, hipStream_t s);
 void launch_f32_to_f16(const float* src, __half* dst, size_t n, hipStream_t s);
 
 }  // namespace larql

@@ -140,8 +140,20 @@ __device__ __forceinline__ v4u split8(const float* x, int part) {
 // The row at pos = T - 1 comes from the fresh projections: RoPE'd, rounded to fp16 and
 // written to the cache by the workgroup that owns it, which uses it from LDS.
 // attn_combine_kernel merges the S softmax partials of each head.
+// Prompt mode: this workgroup's query (grid z) and its view of the arguments.
+__device__ __forceinline__ void attn_select_query(AttnArgs& a, int hd) {
+    if (a.batch == 0) return;
+    const int p = blockIdx.z;
+    a.T += p;
+    a.t_begin = (a.window > 0 && a.T > a.window) ? a.T - a.window : 0;
+    a.qkv += static_cast<size_t>(p) * a.qkv_ld;
+    a.part += static_cast<size_t>(p) * a.num_q * a.S * (hd + 2);
+    a.out += static_cast<size_t>(p) * a.num_q * hd;
+}
+
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
+    attn_select_query(a, HD);
     constexpr int KS = HD / 32;                 // score k-steps
     constexpr int NDT = HD / 16;                // P.V dim tiles
     constexpr int DTW = (NDT + 3) / 4;          // dim tiles per wave (upper bound)
@@ -162,7 +174,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     const int q_dim = a.num_q * HD, kv_dim = a.num_kv * HD;
     const int t0 = (a.t_begin & ~7) + s * kAttnChunk;
     const int pos = a.T - 1;
-    const bool owner = pos < t0 + kAttnChunk;  // the last chunk holds pos
+    if (t0 > pos) return;  // prompt mode: a chunk past this query's position
+    // the last chunk holds pos; outside prompt mode its row comes from the projections
+    const bool owner = pos < t0 + kAttnChunk;
+    const bool fresh = owner && a.batch == 0;
+    const int klim = a.batch ? pos + 1 : pos;  // K rows read from the cache: t < klim
 
     // 1. Global loads, all issued up front.  K rows below pos as score A operands
     // (lane (g, c) of wave w: position t0 + 16 w + c, dims 32 ks + 8 g ..); V blocks at or
@@ -171,7 +187,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     v4u kA[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++)
-        kA[ks] = tk < pos ? *reinterpret_cast<const v4u*>(a.kc + (static_cast<size_t>(tk) * a.num_kv + kvh) * HD +
+        kA[ks] = tk < klim ? *reinterpret_cast<const v4u*>(a.kc + (static_cast<size_t>(tk) * a.num_kv + kvh) * HD +
                                                           32 * ks + 8 * g)
                           : v4u{0u, 0u, 0u, 0u};
     v4u vA[DTW][2];
@@ -189,7 +205,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     }
     for (int i = tid; i < reps * HD; i += kAttnThreads) qr_s[i] = a.qkv[static_cast<size_t>(kvh * reps) * HD + i];
     for (int i = tid; i < half; i += kAttnThreads) cs_s[i] = a.rope[static_cast<size_t>(pos) * half + i];
-    if (owner)
+    if (fresh)
         for (int i = tid; i < HD; i += kAttnThreads) {
             kr_s[i] = a.qkv[q_dim + static_cast<size_t>(kvh) * HD + i];
             vnew[i] = __builtin_bit_cast(uint16_t,
@@ -200,7 +216,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         const int h = i / HD, d = i - h * HD;
         q_s[i] = rope_elem(qr_s + h * HD, d, half, cs_s);
     }
-    if (owner)
+    if (fresh)
         for (int d = tid; d < HD; d += kAttnThreads) {
             const uint16_t kh = __builtin_bit_cast(uint16_t, static_cast<_Float16>(rope_elem(kr_s, d, half, cs_s)));
             knew[d] = kh;
@@ -220,11 +236,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         qop[i] = op;
     }
     if (owner) {
-        if (tk == pos) {
+        if (fresh && tk == pos) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) kA[ks] = *reinterpret_cast<const v4u*>(&knew[32 * ks + 8 * g]);
         }
-        // the block holding pos: the new value at pos, zeros above it (beyond the cache)
+        // the block holding pos: the new value at pos (prompt mode: the cached one), zeros
+        // above it (beyond this query)
 #pragma unroll
         for (int i = 0; i < DTW; i++) {
             const int dt = wave + 4 * i;
@@ -233,12 +250,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
                 const int tv = t0 + 32 * ts + 8 * g;
                 if (dt < NDT && tv <= pos && pos < tv + 8) {
                     const int e = pos - tv;
-                    const uint32_t vn = vnew[16 * dt + c];
+                    const bool sub = fresh;
+                    const uint32_t vn = sub ? vnew[16 * dt + c] : 0u;
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
                         const uint32_t w = vA[i][ts][k];
-                        const uint32_t lo = 2 * k < e ? (w & 0xFFFFu) : (2 * k == e ? vn : 0u);
-                        const uint32_t hi = 2 * k + 1 < e ? (w >> 16) : (2 * k + 1 == e ? vn : 0u);
+                        const uint32_t lo = 2 * k < e ? (w & 0xFFFFu)
+                                                      : (2 * k == e ? (sub ? vn : (w & 0xFFFFu)) : 0u);
+                        const uint32_t hi = 2 * k + 1 < e ? (w >> 16) : (2 * k + 1 == e ? (sub ? vn : (w >> 16)) : 0u);
                         vA[i][ts][k] = lo | (hi << 16);
                     }
                 }
@@ -320,12 +339,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 // merge waits on global memory once.
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a) {
     extern __shared__ float lds[];
+    const int Sst = a.S;  // partial stride per head
+    if (a.batch) {        // prompt mode: query blockIdx.y has its own split count
+        attn_select_query(a, a.hd);
+        a.S = (a.T - (a.t_begin & ~7) + kAttnChunk - 1) / kAttnChunk;
+    }
     const int h = blockIdx.x, tid = threadIdx.x, hd = a.hd, hd2 = hd / 2;
     const int ngrp = kAttnThreads / hd2;                 // split groups
     float* e_s = lds;                                    // S weights
     float2* o_s = reinterpret_cast<float2*>(e_s + a.S);  // ngrp * hd2 partial outputs
     float* red = reinterpret_cast<float*>(o_s + ngrp * hd2);
-    const float* src = a.part + static_cast<size_t>(h) * a.S * (hd + 2);
+    const float* src = a.part + static_cast<size_t>(h) * Sst * (hd + 2);
     const int grp = tid / hd2, j = tid - grp * hd2;
     const bool act = grp < ngrp;
     constexpr int PF = 16;
@@ -449,12 +473,24 @@ void launch_f32_to_f16(const float* src, __half* dst, size_t n, hipStream_t s) {
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
+int attn_splits(int T, int t_begin) { return (T - (t_begin & ~7) + kAttnChunk - 1) / kAttnChunk; }
+
+int attn_prompt_splits(int T0, int batch, int window) {
+    int S = 1;
+    for (int p = 0; p < batch; p++) {
+        const int T = T0 + p, tb = (window > 0 && T > window) ? T - window : 0;
+        S = std::max(S, attn_splits(T, tb));
+    }
+    return S;
+}
+
 void launch_attention(const AttnArgs& a0, hipStream_t s) {
     AttnArgs a = a0;
     const int reps = a.num_q / a.num_kv;
     if (!attn_supported(reps, a.hd)) fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: head geometry");
-    a.S = (a.T - (a.t_begin & ~7) + kAttnChunk - 1) / kAttnChunk;
-    const dim3 grid(a.S, a.num_kv), block(kAttnThreads);
+    a.S = a.batch ? attn_prompt_splits(a.T, a.batch, a.window) : attn_splits(a.T, a.t_begin);
+    const int nz = a.batch ? a.batch : 1;
+    const dim3 grid(a.S, a.num_kv, nz), block(kAttnThreads);
     switch (a.hd) {
         case 32: attn_decode_kernel<32><<<grid, block, 0, s>>>(a); break;
         case 64: attn_decode_kernel<64><<<grid, block, 0, s>>>(a); break;
@@ -469,7 +505,7 @@ void launch_attention(const AttnArgs& a0, hipStream_t s) {
     // combine: S split weights + block-reduction scratch
     const size_t lds2 = sizeof(float) * (static_cast<size_t>(a.S) + 2 * kAttnThreads + kAttnThreads / 64);
     if (lds2 > 64 * 1024) fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: too many position splits");
-    attn_combine_kernel<<<dim3(a.num_q), dim3(kAttnThreads), lds2, s>>>(a);
+    attn_combine_kernel<<<dim3(a.num_q, 1, nz), dim3(kAttnThreads), lds2, s>>>(a);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 

@@ -180,6 +180,9 @@ void launch_q6k_matvec(const DevWeight& w, const float* x, float* out, size_t m,
 // MFMA operands.
 size_t q4k_gemm_ws_bytes(size_t m, size_t cols);
 void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, void* ws, hipStream_t s);
+// The same product with f32 operands (v_mfma_f32_16x16x4f32): ~1e-6 instead of ~1e-4, for
+// chains of projections (the batched prompt pass).
+void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, hipStream_t s);
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
                         size_t m, hipStream_t s);
 void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,

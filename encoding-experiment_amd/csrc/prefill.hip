@@ -241,7 +241,148 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const uint8_t* __res
         }
 }
 
+// ── f32 operands: the accurate variant for chains of projections ────────
+// Same tiling (64 tokens x 320 weight rows per workgroup, 80 rows per wave), with
+// v_mfma_f32_16x16x4f32: weights dequantized to f32 (`fma(q, d sc_j, -dmin m_j)`, one
+// rounding) and X read in f32, so each product is exact and the error is the f32
+// accumulation's (~1e-6) instead of the fp16 operands' (~1e-4 per projection), which
+// compounds through a model's layers.  A k-step of 4 takes element e of the lane's
+// sub-block 4h + g for lane group g, so a lane's 16 nibble bytes feed 32 steps and its A
+// operands are the matching 32 consecutive elements of its token's row of X.
+constexpr int kF32Pitch = 36;  // floats per lane slot in LDS (32 + 4: spread the banks)
+
+__global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* __restrict__ qs,
+                                                                const v4u* __restrict__ hdr,
+                                                                const float* __restrict__ X, float* __restrict__ Y,
+                                                                int M, int N, int K, int ntiles) {
+    __shared__ float As[2][kMt][64][kF32Pitch];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int S = K / 256, n = 2 * S;
+    const int mt0 = blockIdx.y * kMt;
+    const int nt0 = (blockIdx.x * kWaves + wave) * kNT;
+    uint32_t qo[kNT], ho[kNT];
+#pragma unroll
+    for (int j = 0; j < kNT; j++) {
+        const uint32_t t = static_cast<uint32_t>(min(nt0 + j, ntiles - 1));
+        qo[j] = __builtin_amdgcn_readfirstlane(t * S * 2048u);
+        ho[j] = __builtin_amdgcn_readfirstlane(t * S * 256u);
+    }
+    // X staging: thread (tile r = tid / 64, slot l = tid % 64) loads token 16 (mt0 + r) + l % 16,
+    // elements 32 (4h + l / 16) .. + 31 of super-block sb; zeros for tokens past M.
+    const int xr_row = (mt0 + (tid >> 6)) * 16 + (lane & 15);
+    const bool xr_ok = xr_row < M;  // (the select also keeps the compiler from a stack copy of Xu)
+    const float* xrow = X + static_cast<size_t>(min(xr_row, M - 1)) * K + 32 * g;
+    struct Xu {
+        float4 v[8];
+    };
+    auto load_x = [&](int u, Xu& x) __attribute__((always_inline)) {
+        const float4* p = reinterpret_cast<const float4*>(xrow + 256 * (u >> 1) + 128 * (u & 1));
+#pragma unroll
+        for (int k = 0; k < 8; k++) x.v[k] = xr_ok ? p[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto store_x = [&](int b, const Xu& x) __attribute__((always_inline)) {
+        float4* d = reinterpret_cast<float4*>(&As[b][tid >> 6][lane][0]);
+#pragma unroll
+        for (int k = 0; k < 8; k++) d[k] = x.v[k];
+    };
+    struct Wu {
+        v4u q[kNT], hd[kNT];
+    };
+    const uint8_t* hdrb = reinterpret_cast<const uint8_t*>(hdr) + c * 16;
+    auto load_w = [&](int u, Wu& w) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+            w.q[j] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4u*>(qs + qo[j] + static_cast<uint32_t>(u) * 1024u) + lane);
+            w.hd[j] = *reinterpret_cast<const v4u*>(hdrb + ho[j] + static_cast<uint32_t>(u >> 1) * 256u);
+        }
+    };
+    floatx4 acc[kMt][kNT];
+#pragma unroll
+    for (int i = 0; i < kMt; i++)
+#pragma unroll
+        for (int j = 0; j < kNT; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int b, int u, const Wu& w) __attribute__((always_inline)) {
+        const int h = u & 1;
+        float sc[kNT], nmn[kNT];
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+            const float d = h2f(w.hd[j].x & 0xFFFFu), dmin = h2f(w.hd[j].x >> 16);
+            const uint32_t scw = h ? w.hd[j].z : w.hd[j].y;
+            sc[j] = d * static_cast<float>((scw >> (8 * g)) & 0x3Fu);
+            nmn[j] = -(dmin * static_cast<float>((w.hd[j].w >> (8 * g + 4 * h)) & 0xFu));
+        }
+#pragma unroll
+        for (int e4 = 0; e4 < 8; e4++) {  // elements 4 e4 .. 4 e4 + 3 of the lane's sub-block
+            float4 a[kMt];
+#pragma unroll
+            for (int i = 0; i < kMt; i++) a[i] = *reinterpret_cast<const float4*>(&As[b][i][lane][4 * e4]);
+#pragma unroll
+            for (int j = 0; j < kNT; j++) {
+                // byte (4 e4 + t) / 2 of the 16: element 2i in the low nibble, 2i + 1 in the high
+                const uint32_t word = w.q[j][e4 >> 1] >> (16 * (e4 & 1));
+                float wt[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    wt[t] = __builtin_fmaf(static_cast<float>((word >> (4 * t)) & 0xFu), sc[j], nmn[j]);
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < kMt; i++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][t], wt[t], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+
+    // two-unit ring: unit u in LDS buffer u % 2; X and W of unit u + 1 in flight meanwhile
+    Wu w0, w1;
+    Xu x0, x1;
+    load_x(0, x0);
+    load_w(0, w0);
+    load_x(min(1, n - 1), x1);
+    load_w(min(1, n - 1), w1);
+    store_x(0, x0);
+    __syncthreads();
+    for (int u = 0; u < n; u += 2) {
+        store_x(1, x1);
+        load_x(min(u + 2, n - 1), x0);
+        compute(0, u, w0);
+        load_w(min(u + 2, n - 1), w0);
+        __syncthreads();
+        store_x(0, x0);
+        load_x(min(u + 3, n - 1), x1);
+        compute(1, u + 1, w1);
+        load_w(min(u + 3, n - 1), w1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < kMt; i++)
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+            const int col = (nt0 + j) * 16 + c;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = (mt0 + i) * 16 + 4 * g + r;
+                if (m < M && col < N) Y[static_cast<size_t>(m) * N + col] = acc[i][j][r];
+            }
+        }
+}
+
 }  // namespace
+
+void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, hipStream_t s) {
+    if (w.format != LARQL_Q4_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: Q4_K weights only");
+    if (m == 0) return;
+    if (m > 0x7FFFFFFF / w.cols) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: too many tokens");
+    const dim3 grid(static_cast<unsigned>((w.rows + kNwg - 1) / kNwg),
+                    static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)));
+    q4k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(w.qs, reinterpret_cast<const v4u*>(w.hdr), X, Y,
+                                                         static_cast<int>(m), static_cast<int>(w.rows),
+                                                         static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16));
+    LARQL_HIP_CHECK(hipGetLastError());
+}
 
 size_t q4k_gemm_ws_bytes(size_t m, size_t cols) {
     const size_t m_pad = (m + 16 * kMt - 1) / (16 * kMt) * (16 * kMt);

@@ -1,0 +1,98 @@
+// Row kernels of the batched prompt pass (prefill_q4, LC/src/backend.rs:139-152): the
+// per-position operations of a Llama layer applied to all M positions of a prompt at
+// once, around the Q4_K GEMMs (prefill.hip) and the prompt-mode attention (decode.hip).
+// Each follows the decode step's arithmetic for one position:
+//   * RMSNorm  (LI/src/residual.rs:17-33): rms = sqrt(sum(x^2) in f64 / n + eps) rounded
+//     to f32, y = (x * (1 / rms)) * w — the fused-norm prologue of the matvecs;
+//   * RoPE of K (LI/src/attention/rope.rs:22-55) with the cos/sin table, K and V rounded
+//     to fp16 (RNE) into the cache rows of their positions;
+//   * residual add (LI/src/forward/layer.rs:88-92) and silu(gate) * up
+//     (LI/src/ffn/mod.rs:87-94) over gate/up rows interleaved as the fused weight emits them.
+#include "decode.h"
+#include "matvec_common.h"
+
+namespace larql {
+
+namespace {
+
+// Grid M rows; 256 threads.
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ X, const float* __restrict__ w,
+                                                           float* __restrict__ Y, int n, double eps) {
+    __shared__ double red[4];
+    const float* x = X + static_cast<size_t>(blockIdx.x) * n;
+    float* y = Y + static_cast<size_t>(blockIdx.x) * n;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) ss += static_cast<double>(x[i]) * x[i];
+    ss = wave_sum_d(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rms = static_cast<float>(sqrt(tot / static_cast<double>(n) + eps));
+    const float inv = 1.0f / rms;
+    for (int i = threadIdx.x; i < n; i += 256) y[i] = (x[i] * inv) * w[i];
+}
+
+// Thread per (position p, kv element j): K RoPE'd at p, K and V to fp16 in the cache.
+__global__ void rope_kv_rows_kernel(const float* __restrict__ QKV, int M, int p0, int ld, int q_dim, int kv_dim,
+                                    int hd, int half, const float2* __restrict__ rope, __half* __restrict__ kc,
+                                    __half* __restrict__ vc, int num_kv) {
+    const size_t t = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    if (t >= static_cast<size_t>(M) * kv_dim) return;
+    const int p = static_cast<int>(t / kv_dim), j = static_cast<int>(t - static_cast<size_t>(p) * kv_dim);
+    const int kvh = j / hd, d = j - kvh * hd, pos = p0 + p;
+    const float* row = QKV + static_cast<size_t>(p) * ld;
+    const float* k = row + q_dim + kvh * hd;
+    const float2* cs = rope + static_cast<size_t>(pos) * half;
+    float kr = k[d];
+    if (d < half) kr = k[d] * cs[d].x - k[d + half] * cs[d].y;
+    else if (d < 2 * half) kr = k[d - half] * cs[d - half].y + k[d] * cs[d - half].x;
+    kc[(static_cast<size_t>(pos) * num_kv + kvh) * hd + d] = __float2half_rn(kr);
+    vc[((static_cast<size_t>(pos >> 3) * num_kv + kvh) * hd + d) * 8 + (pos & 7)] =
+        __float2half_rn(row[q_dim + kv_dim + j]);
+}
+
+__global__ void add_rows_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
+                                size_t n) {
+    const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+// GU rows [M][2 inter] with gate and up interleaved (2i, 2i + 1) -> act [M][inter].
+__global__ void silu_pair_rows_kernel(const float* __restrict__ GU, float* __restrict__ act, size_t n) {
+    const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    if (i < n) act[i] = silu_mul(GU[2 * i], GU[2 * i + 1]);
+}
+
+unsigned blocks(size_t n) { return static_cast<unsigned>((n + 255) / 256); }
+
+}  // namespace
+
+void launch_rmsnorm_rows(const float* X, const float* w, float* Y, size_t m, size_t n, double eps, hipStream_t s) {
+    if (m == 0) return;
+    rmsnorm_rows_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, w, Y, static_cast<int>(n), eps);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_rope_kv_rows(const float* QKV, size_t m, size_t p0, size_t q_dim, size_t kv_dim, int hd, int rdim,
+                         const float2* rope, __half* kc, __half* vc, int num_kv, hipStream_t s) {
+    const size_t n = m * kv_dim;
+    if (n == 0) return;
+    rope_kv_rows_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(
+        QKV, static_cast<int>(m), static_cast<int>(p0), static_cast<int>(q_dim + 2 * kv_dim), static_cast<int>(q_dim),
+        static_cast<int>(kv_dim), hd, rdim / 2, rope, kc, vc, num_kv);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipStream_t s) {
+    if (n == 0) return;
+    add_rows_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(a, b, out, n);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_silu_pair_rows(const float* GU, float* act, size_t n, hipStream_t s) {
+    if (n == 0) return;
+    silu_pair_rows_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(GU, act, n);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace larql
