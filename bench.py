@@ -153,8 +153,11 @@ def run_decode(be, torch, stream, steps, warmup):
     times = [e0.elapsed_time(e1) for e0, e1 in ev]
     med = statistics.median(times)
     nbytes = decode_algorithmic_bytes(sm.cfg, kv_len)
+    prefill = run_prompt_prefill(torch, stream, sm)
+    be.kv_truncate(0)
     sm.model.close()
     return {
+        "prefill": prefill,
         "tokens_per_s": round(1000.0 / med, 2),
         "ms_per_step_median": round(med, 4),
         "ms_per_step_min": round(min(times), 4),
@@ -162,6 +165,33 @@ def run_decode(be, torch, stream, steps, warmup):
         "bytes_per_step": nbytes,
         "achieved_GBs": round(nbytes / (med * 1e-3) / 1e9, 1),
         "config": "Llama-3-8B shape, Q4_K linears, Q6_K head (vocab 128256), fp16 KV at pos 2048, batch 1",
+    }
+
+
+def run_prompt_prefill(torch, stream, sm, seq=512, reps=4):
+    """A 512-token prompt through the 8B-shape model (larql_hip_model_prefill_dev: per
+    layer, f32-operand Q4_K GEMMs over all positions and prompt-mode attention)."""
+    c = sm.cfg
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(seq, c["hidden"], generator=gen, device="cuda", dtype=torch.float32)
+    out = torch.empty_like(x)
+    sm.model.prefill_dev(x, seq, out, stream=stream)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in ev:
+        e0.record(stream)
+        sm.model.prefill_dev(x, seq, out, stream=stream)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in ev)
+    h, f, q, kv = c["hidden"], c["inter"], c["nq"] * c["hd"], c["nkv"] * c["hd"]
+    gemm_flop = 2.0 * seq * c["n_layers"] * h * (q + 2 * kv + q + 2 * f) + 2.0 * seq * c["n_layers"] * f * h
+    return {
+        "tokens": seq,
+        "ms_median": round(ms, 3),
+        "tokens_per_s": round(seq / (ms * 1e-3), 1),
+        "gemm_TFLOPs": round(gemm_flop / (ms * 1e-3) / 1e12, 1),
+        "gemm_frac_of_fp32_mfma_peak": round(gemm_flop / (ms * 1e-3) / 157.3e12, 3),
     }
 
 

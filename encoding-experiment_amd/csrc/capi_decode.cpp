@@ -436,7 +436,7 @@ extern "C" int larql_hip_decode_token(larql_hip_ctx* c, const larql_pipeline_lay
 
 // The batched prompt pass takes layers whose projections are all Q4_K with Q|K|V and
 // gate/up fused (every Llama layer of a Q4_K file); others run position by position.
-bool prompt_batchable(const larql_hip_model* m) {
+static bool prompt_batchable(const larql_hip_model* m) {
     for (const LayerDev& L : m->layers)
         if (L.split_qkv || L.split_gu || L.qkv.format != LARQL_Q4_K || L.wo.format != LARQL_Q4_K ||
             L.gateup.format != LARQL_Q4_K || L.down.format != LARQL_Q4_K)
@@ -448,22 +448,26 @@ bool prompt_batchable(const larql_hip_model* m) {
 // Q4_K GEMMs on the matrix cores with f32 operands (fp16 operands' ~1e-4 per projection
 // compounds to >1e-3 of the output over 8+ layers), the attention in prompt mode (each query over its
 // causal prefix, which the RoPE / KV kernel has written to the cache first).
-void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M, float* dout, hipStream_t s) {
+static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M, float* dout, hipStream_t s) {
     auto& kv = c->kv;
     kv_ensure(c, m->layers.size(), m->nkv, m->hd, M);
     const size_t hidden = m->hidden, inter = m->inter, qd = m->q_dim, kvd = m->kv_dim, ld = qd + 2 * kvd;
     const size_t wide = std::max({hidden, qd, inter}), gw = std::max(hidden, 2 * inter);
     const int S = larql::attn_prompt_splits(1, static_cast<int>(M), 0);
     const size_t part_n = M * static_cast<size_t>(m->nq) * S * (m->hd + 2);
-    const size_t n_f = 2 * M * hidden + M * wide + M * ld + M * qd + M * gw + M * inter + part_n;
+    size_t split_n = 0;  // K-split partial products of the GEMMs
+    for (const LayerDev& L : m->layers)
+        split_n = std::max({split_n, larql::q4k_gemm_f32_part_floats(L.qkv, M), larql::q4k_gemm_f32_part_floats(L.wo, M),
+                            larql::q4k_gemm_f32_part_floats(L.gateup, M), larql::q4k_gemm_f32_part_floats(L.down, M)});
+    const size_t n_f = 2 * M * hidden + M * wide + M * ld + M * qd + M * gw + M * inter + part_n + split_n;
     float* base = static_cast<float*>(larql::ensure(c, m->prompt, n_f * sizeof(float)));
     float *H0 = base, *H1 = H0 + M * hidden, *XN = H1 + M * hidden, *QKV = XN + M * wide, *ATT = QKV + M * ld;
-    float *G = ATT + M * qd, *ACT = G + M * gw, *PART = ACT + M * inter;
+    float *G = ATT + M * qd, *ACT = G + M * gw, *PART = ACT + M * inter, *SPL = PART + part_n;
     larql::launch_copy_f32(dx, H0, M * hidden, s);
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
         larql::launch_rmsnorm_rows(H0, L.input_norm, XN, M, hidden, L.eps, s);
-        larql::launch_q4k_gemm_f32(L.qkv, XN, QKV, M, s);
+        larql::launch_q4k_gemm_f32(L.qkv, XN, QKV, M, SPL, split_n, s);
         const float2* rope = rope_table(c, L.rope_base, L.rdim, s);
         larql::launch_rope_kv_rows(QKV, M, 0, qd, kvd, L.hd, L.rdim, rope, kv.k[l], kv.v[l], L.nkv, s);
         larql::AttnArgs at{};
@@ -483,12 +487,12 @@ void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M,
         at.window = L.window;
         at.qkv_ld = static_cast<int>(ld);
         larql::launch_attention(at, s);
-        larql::launch_q4k_gemm_f32(L.wo, ATT, G, M, s);
+        larql::launch_q4k_gemm_f32(L.wo, ATT, G, M, SPL, split_n, s);
         larql::launch_add_rows(H0, G, H1, M * hidden, s);
         larql::launch_rmsnorm_rows(H1, L.post_attn_norm, XN, M, hidden, L.eps, s);
-        larql::launch_q4k_gemm_f32(L.gateup, XN, G, M, s);
+        larql::launch_q4k_gemm_f32(L.gateup, XN, G, M, SPL, split_n, s);
         larql::launch_silu_pair_rows(G, ACT, M * inter, s);
-        larql::launch_q4k_gemm_f32(L.down, ACT, G, M, s);
+        larql::launch_q4k_gemm_f32(L.down, ACT, G, M, SPL, split_n, s);
         larql::launch_add_rows(H1, G, H0, M * hidden, s);
     }
     larql::launch_copy_f32(H0, dout, M * hidden, s);
@@ -611,6 +615,22 @@ extern "C" int larql_hip_model_decode_dev(larql_hip_ctx* c, larql_hip_model* m, 
     return guarded(c, [&] {
         if (!m || !x_dev) fail(LARQL_HIP_ERR_INVALID, "null pointer");
         run_decode(c, m, x_dev, hidden_out_dev, logits_dev, pick_stream(c, stream));
+    });
+}
+
+extern "C" int larql_hip_model_prefill_dev(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, size_t seq_len,
+                                           float* out_dev, void* stream) {
+    return guarded(c, [&] {
+        if (!m || !x_dev || !out_dev) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        if (seq_len == 0) return;
+        hipStream_t s = pick_stream(c, stream);
+        kv_ensure(c, m->layers.size(), m->nkv, m->hd, seq_len);
+        c->kv.current_len = 0;
+        if (seq_len > 1 && prompt_batchable(m))
+            run_prompt(c, m, x_dev, seq_len, out_dev, s);
+        else
+            for (size_t p = 0; p < seq_len; p++)
+                run_decode(c, m, x_dev + p * m->hidden, out_dev + p * m->hidden, nullptr, s);
     });
 }
 

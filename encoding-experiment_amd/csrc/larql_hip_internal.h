@@ -181,8 +181,12 @@ void launch_q6k_matvec(const DevWeight& w, const float* x, float* out, size_t m,
 size_t q4k_gemm_ws_bytes(size_t m, size_t cols);
 void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, void* ws, hipStream_t s);
 // The same product with f32 operands (v_mfma_f32_16x16x4f32): ~1e-6 instead of ~1e-4, for
-// chains of projections (the batched prompt pass).
-void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, hipStream_t s);
+// chains of projections (the batched prompt pass).  Small grids split K over up to four
+// workgroups per tile, summed in split order from `part` (floats: q4k_gemm_f32_part_floats;
+// with less, no split).
+size_t q4k_gemm_f32_part_floats(const DevWeight& w, size_t m);
+void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, float* part, size_t part_floats,
+                         hipStream_t s);
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
                         size_t m, hipStream_t s);
 void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,

@@ -254,13 +254,16 @@ constexpr int kF32Pitch = 36;  // floats per lane slot in LDS (32 + 4: spread th
 __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* __restrict__ qs,
                                                                 const v4u* __restrict__ hdr,
                                                                 const float* __restrict__ X, float* __restrict__ Y,
-                                                                int M, int N, int K, int ntiles) {
+                                                                int M, int N, int K, int ntiles, int sb_per) {
     __shared__ float As[2][kMt][64][kF32Pitch];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int S = K / 256, n = 2 * S;
+    const int S = K / 256;
     const int mt0 = blockIdx.y * kMt;
     const int nt0 = (blockIdx.x * kWaves + wave) * kNT;
+    // split blockIdx.z of K: super-blocks [z sb_per, (z + 1) sb_per), partial sums to Y[z]
+    const int u0 = 2 * static_cast<int>(blockIdx.z) * sb_per, u1 = min(2 * S, u0 + 2 * sb_per), last = u1 - 1;
+    Y += static_cast<size_t>(blockIdx.z) * M * N;
     uint32_t qo[kNT], ho[kNT];
 #pragma unroll
     for (int j = 0; j < kNT; j++) {
@@ -339,22 +342,23 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
     // two-unit ring: unit u in LDS buffer u % 2; X and W of unit u + 1 in flight meanwhile
     Wu w0, w1;
     Xu x0, x1;
-    load_x(0, x0);
-    load_w(0, w0);
-    load_x(min(1, n - 1), x1);
-    load_w(min(1, n - 1), w1);
+    // (u1 - u0 is even: the range is whole super-blocks)
+    load_x(u0, x0);
+    load_w(u0, w0);
+    load_x(u0 + 1, x1);
+    load_w(u0 + 1, w1);
     store_x(0, x0);
     __syncthreads();
-    for (int u = 0; u < n; u += 2) {
+    for (int u = u0; u < u1; u += 2) {
         store_x(1, x1);
-        load_x(min(u + 2, n - 1), x0);
+        load_x(min(u + 2, last), x0);
         compute(0, u, w0);
-        load_w(min(u + 2, n - 1), w0);
+        load_w(min(u + 2, last), w0);
         __syncthreads();
         store_x(0, x0);
-        load_x(min(u + 3, n - 1), x1);
+        load_x(min(u + 3, last), x1);
         compute(1, u + 1, w1);
-        load_w(min(u + 3, n - 1), w1);
+        load_w(min(u + 3, last), w1);
         __syncthreads();
     }
 #pragma unroll
@@ -370,18 +374,59 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
         }
 }
 
+// Y = sum over the splits of the partial products, in split order (deterministic).
+__global__ void sum_splits_kernel(const float* __restrict__ P, float* __restrict__ Y, size_t n, int splits) {
+    const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    if (i >= n) return;
+    float a = P[i];
+    for (int z = 1; z < splits; z++) a += P[z * n + i];
+    Y[i] = a;
+}
+
+// K-splits for the f32 GEMM: the count (1..4, whole super-blocks each) that minimises
+// rounds of workgroups over the CUs x units per workgroup (one workgroup per CU at a time).
+struct F32Split {
+    int splits, sb_per;
+};
+F32Split f32_split(const DevWeight& w, size_t m) {
+    const int S = static_cast<int>(w.cols / 256);
+    const long wgs = static_cast<long>((w.rows + kNwg - 1) / kNwg) * static_cast<long>((m + 16 * kMt - 1) / (16 * kMt));
+    const long cus = current_device_cus();
+    F32Split best{1, S};
+    long best_cost = -1;
+    for (int s = 1; s <= 4 && s <= S; s++) {
+        const int per = (S + s - 1) / s, eff = (S + per - 1) / per;
+        const long cost = ((wgs * eff + cus - 1) / cus) * per;
+        if (best_cost < 0 || cost < best_cost) best = {eff, per}, best_cost = cost;
+    }
+    return best;
+}
+
 }  // namespace
 
-void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, hipStream_t s) {
+size_t q4k_gemm_f32_part_floats(const DevWeight& w, size_t m) {
+    const F32Split sp = f32_split(w, m);
+    return sp.splits > 1 ? sp.splits * m * w.rows : 0;
+}
+
+void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, float* part, size_t part_floats,
+                         hipStream_t s) {
     if (w.format != LARQL_Q4_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: Q4_K weights only");
     if (m == 0) return;
     if (m > 0x7FFFFFFF / w.cols) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: too many tokens");
+    F32Split sp = f32_split(w, m);
+    if (sp.splits > 1 && (!part || part_floats < sp.splits * m * w.rows)) sp = {1, static_cast<int>(w.cols / 256)};
     const dim3 grid(static_cast<unsigned>((w.rows + kNwg - 1) / kNwg),
-                    static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)));
-    q4k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(w.qs, reinterpret_cast<const v4u*>(w.hdr), X, Y,
-                                                         static_cast<int>(m), static_cast<int>(w.rows),
-                                                         static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16));
+                    static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)), static_cast<unsigned>(sp.splits));
+    q4k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(
+        w.qs, reinterpret_cast<const v4u*>(w.hdr), X, sp.splits > 1 ? part : Y, static_cast<int>(m),
+        static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per);
     LARQL_HIP_CHECK(hipGetLastError());
+    if (sp.splits > 1) {
+        const size_t n = m * w.rows;
+        sum_splits_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(part, Y, n, sp.splits);
+        LARQL_HIP_CHECK(hipGetLastError());
+    }
 }
 
 size_t q4k_gemm_ws_bytes(size_t m, size_t cols) {

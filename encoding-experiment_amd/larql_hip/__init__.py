@@ -90,6 +90,7 @@ SIGNATURES = {
     "larql_hip_model_set_head": (_I, [_P, _P, _P, _SZ, _P, ctypes.c_float, _I]),
     "larql_hip_model_destroy": (_I, [_P, _P]),
     "larql_hip_model_decode_dev": (_I, [_P, _P, _P, _P, _P, _P]),
+    "larql_hip_model_prefill_dev": (_I, [_P, _P, _P, _SZ, _P, _P]),
 }
 
 NORM_RMS, NORM_LAYER = 0, 1
@@ -549,6 +550,12 @@ class DeviceModel:
     def decode_dev(self, x, hidden_out=None, logits=None, stream=None):
         self.be._check(self.be._lib.larql_hip_model_decode_dev(self.be._ctx, self._h, _dptr(x), _dptr(hidden_out),
                                                                _dptr(logits), _stream_ptr(stream)))
+
+    def prefill_dev(self, x, seq_len: int, out, stream=None):
+        """A prompt [seq_len][hidden] from position 0 (device tensors); resets the KV cache
+        and leaves it at seq_len; out gets every position's hidden state."""
+        self.be._check(self.be._lib.larql_hip_model_prefill_dev(self.be._ctx, self._h, _dptr(x), seq_len,
+                                                                _dptr(out), _stream_ptr(stream)))
 
     def close(self):
         if self._h:

@@ -342,6 +342,12 @@ int larql_hip_model_destroy(larql_hip_ctx* ctx, larql_hip_model* model);
  * K/V at the current cache length and advances it.  Enqueues on `stream`. */
 int larql_hip_model_decode_dev(larql_hip_ctx* ctx, larql_hip_model* model, const float* x_dev,
                                float* hidden_out_dev, float* logits_dev, void* stream);
+/* A prompt on device memory (the trait's prefill_q4, LC/src/backend.rs:139-152, for a
+ * registered model): x_dev [seq_len][hidden] at positions 0 .. seq_len-1 in,
+ * out_dev [seq_len][hidden] (each position's last-layer hidden state) out; the KV
+ * cache is reset and left at seq_len.  Enqueues on `stream`. */
+int larql_hip_model_prefill_dev(larql_hip_ctx* ctx, larql_hip_model* model, const float* x_dev, size_t seq_len,
+                                float* out_dev, void* stream);
 
 #ifdef __cplusplus
 }

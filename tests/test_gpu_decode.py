@@ -219,6 +219,36 @@ def cpu_logits(host):
     return oracle.q6k_matvec(host["head"], hn, c["vocab"], c["hidden"])
 
 
+@pytest.mark.parametrize("formats", [None, {"wv": "q6_k"}])
+def test_model_prefill_dev_matches_trait_prefill(hip, formats):
+    """larql_hip_model_prefill_dev (a registered model, device buffers) gives the trait
+    prefill_q4's hidden states bit for bit (batched pass, or per position for mixed
+    formats), leaves the cache at seq_len, and the next decode_dev continues from it."""
+    torch = pytest.importorskip("torch")
+    n_layers, hidden, inter, nq, nkv, hd, seq = 2, 512, 1024, 8, 2, 64, 20
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=31, formats=formats)
+    layers = m.hip_layers(10000.0)
+    x = np.stack([oracle.gauss(600 + p, hidden) for p in range(seq)])
+    hip.reset_kv_cache()
+    ref = hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0)
+    nxt = oracle.gauss(700, hidden)
+    ref_next = hip.decode_token(layers, nxt, hidden, inter, nq * hd, nkv * hd, nq, nkv, hd, 10000.0)
+    model = hip.model(layers, hidden, inter, weights_on_device=False)
+    try:
+        xd = torch.from_numpy(x.astype(np.float32)).cuda()
+        out = torch.empty_like(xd)
+        model.prefill_dev(xd, seq, out)
+        torch.cuda.synchronize()
+        assert hip.kv_cache_len() == seq
+        assert np.array_equal(out.cpu().numpy(), ref)
+        h = torch.empty(hidden, device="cuda", dtype=torch.float32)
+        model.decode_dev(torch.from_numpy(nxt.astype(np.float32)).cuda(), hidden_out=h)
+        torch.cuda.synchronize()
+        assert np.array_equal(h.cpu().numpy(), ref_next)
+    finally:
+        model.close()
+
+
 def test_decode_8b_step_matches_cpu():
     """Full Llama-3-8B-shape decode step: 32 layers, d=4096, 32q/8kv heads, hd 128,
     FFN 14336, Q4_K projections, fp16 KV with 2048 prefilled positions, Q6_K head over
