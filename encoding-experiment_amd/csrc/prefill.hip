@@ -324,12 +324,17 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
             for (int i = 0; i < kMt; i++) a[i] = *reinterpret_cast<const float4*>(&As[b][i][lane][4 * e4]);
 #pragma unroll
             for (int j = 0; j < kNT; j++) {
-                // byte (4 e4 + t) / 2 of the 16: element 2i in the low nibble, 2i + 1 in the high
-                const uint32_t word = w.q[j][e4 >> 1] >> (16 * (e4 & 1));
+                // byte i of the 16 holds element 2i (low nibble) and 2i + 1 (high): split into
+                // low and high nibble bytes once per dword, then one byte convert per weight
+                const uint32_t word = w.q[j][e4 >> 1];
+                uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+                asm("" : "+v"(lo), "+v"(hi));  // opaque: keeps v_cvt_f32_ubyteN, not bfe + convert
+                const int b0 = 16 * (e4 & 1);
                 float wt[4];
-#pragma unroll
-                for (int t = 0; t < 4; t++)
-                    wt[t] = __builtin_fmaf(static_cast<float>((word >> (4 * t)) & 0xFu), sc[j], nmn[j]);
+                wt[0] = __builtin_fmaf(static_cast<float>((lo >> b0) & 0xFFu), sc[j], nmn[j]);
+                wt[1] = __builtin_fmaf(static_cast<float>((hi >> b0) & 0xFFu), sc[j], nmn[j]);
+                wt[2] = __builtin_fmaf(static_cast<float>((lo >> (b0 + 8)) & 0xFFu), sc[j], nmn[j]);
+                wt[3] = __builtin_fmaf(static_cast<float>((hi >> (b0 + 8)) & 0xFFu), sc[j], nmn[j]);
 #pragma unroll
                 for (int t = 0; t < 4; t++)
 #pragma unroll

@@ -276,3 +276,37 @@ def test_decode_8b_step_matches_cpu():
         sm.model.close()
     finally:
         be.close()
+
+
+@pytest.mark.parametrize("formats", [None, {"wv": "q6_k"}])
+def test_vindex_file_layers_match_direct_layers(hip, tmp_path, formats):
+    """Layers sliced from vindex files (interleaved_q4k.bin [gate|up|down] per layer,
+    attn_weights_q4k.bin + manifest; pipeline_layer.rs:97-152) run prefill_q4 and
+    decode_token bit-identically to the same bytes passed as separate arrays."""
+    from larql_hip import vindex
+
+    n_layers, hidden, inter, nq, nkv, hd, seq = 2, 512, 1024, 8, 2, 64, 5
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=41, formats=formats)
+    (tmp_path / "interleaved_q4k.bin").write_bytes(
+        b"".join(L[n].tobytes() for L in m.layers for n in ("gate", "up", "down")))
+    blob, man = b"", []
+    for L in m.layers:
+        for n in ("wq", "wk", "wv", "wo"):
+            man.append({"offset": len(blob), "length": L[n].nbytes,
+                        "format": "Q6_K" if m.formats.get(n) == "q6_k" else "Q4_K"})
+            blob += L[n].tobytes()
+    (tmp_path / "attn_weights_q4k.bin").write_bytes(blob)
+    (tmp_path / "attn_weights_q4k_manifest.json").write_text(__import__("json").dumps(man))
+    v = vindex.Vindex(str(tmp_path), n_layers, hidden, inter)
+    vl = v.pipeline_layers([(L["input_norm"], L["post_attn_norm"]) for L in m.layers], head_dim=hd,
+                           num_q_heads=nq, num_kv_heads=nkv, rope_base=10000.0)
+    x = np.stack([oracle.gauss(300 + p, hidden) for p in range(seq)])
+    outs = []
+    for layers in (m.hip_layers(10000.0), vl):
+        hip.reset_kv_cache()
+        pre = hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0)
+        nxt = hip.decode_token(layers, oracle.gauss(400, hidden), hidden, inter, nq * hd, nkv * hd, nq, nkv, hd,
+                               10000.0)
+        outs.append((pre, nxt))
+    print(f"[vindex] formats={formats}: prefill and next token compared", flush=True)
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
