@@ -113,7 +113,10 @@ class Vindex:
         self.per_matrix = ffn_per_matrix(inter, hidden, q4k)
         self.attn = _map(os.path.join(path, "attn_weights_q4k.bin"))
         man = os.path.join(path, "attn_weights_q4k_manifest.json")
-        self.manifest = parse_attn_manifest(json.load(open(man))) if os.path.exists(man) else None
+        self.manifest = None
+        if os.path.exists(man):
+            with open(man) as f:
+                self.manifest = parse_attn_manifest(json.load(f))
         self.gates = None
         gp = os.path.join(path, "gate_vectors_q4.bin")
         if os.path.exists(gp):

@@ -173,6 +173,26 @@ def test_prefill_q4_matches_oracle_and_decode(hip, seq, formats, window):
         hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0, use_qk_norm=True)
 
 
+def test_prefill_q4_uneven_k_splits(hip):
+    """hidden 2560 = 10 Q4_K super-blocks: the small Q|K|V grid splits K four ways as 3, 3,
+    3 and 1 super-blocks (the last split shorter), summed in split order; every position
+    stays within the bar."""
+    n_layers, hidden, inter, nq, nkv, hd, seq = 2, 2560, 1024, 8, 2, 64, 20
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=13)
+    layers = m.hip_layers(10000.0)
+    x = np.stack([oracle.gauss(200 + p, hidden) for p in range(seq)])
+    hip.reset_kv_cache()
+    got = hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0)
+    worst = 0.0
+    for p in range(seq):
+        ref = x[p].copy()
+        for L in m.layers:
+            ref = oracle.decode_layer(L, ref, p, hidden, inter, nq, nkv, hd, 10000.0)
+        worst = max(worst, rel_err(got[p], ref))
+    print(f"[prefill splits] hidden {hidden}: worst rel_err={worst:.3e}", flush=True)
+    assert worst <= REL_TOL
+
+
 def test_prefill_q4_deep_model(hip):
     """The batched pass through 16 layers stays within the bar at every position: its
     error must not compound with depth (fp16 GEMM operands reached 1.8e-3 here)."""
