@@ -434,20 +434,28 @@ extern "C" int larql_hip_decode_token(larql_hip_ctx* c, const larql_pipeline_lay
     });
 }
 
-// The batched prompt pass takes layers whose projections are all Q4_K with Q|K|V and
-// gate/up fused (every Llama layer of a Q4_K file); others run position by position.
+// The batched prompt pass takes layers with gate/up fused in Q4_K and every other
+// projection Q4_K or Q6_K (Q4_K and Q4_K_M files); others run position by position.
 static bool prompt_batchable(const larql_hip_model* m) {
-    for (const LayerDev& L : m->layers)
-        if (L.split_qkv || L.split_gu || L.qkv.format != LARQL_Q4_K || L.wo.format != LARQL_Q4_K ||
-            L.gateup.format != LARQL_Q4_K || L.down.format != LARQL_Q4_K)
-            return false;
+    auto ok = [](const larql::DevWeight& w) { return w.format == LARQL_Q4_K || w.format == LARQL_Q6_K; };
+    for (const LayerDev& L : m->layers) {
+        if (L.split_gu || L.gateup.format != LARQL_Q4_K || !ok(L.wo) || !ok(L.down)) return false;
+        if (L.split_qkv ? !(ok(L.wq) && ok(L.wk) && ok(L.wv)) : !ok(L.qkv)) return false;
+    }
     return true;
 }
 
-// All M positions (0 .. M-1) of a prompt through every layer at once: the projections as
-// Q4_K GEMMs on the matrix cores with f32 operands (fp16 operands' ~1e-4 per projection
-// compounds to >1e-3 of the output over 8+ layers), the attention in prompt mode (each query over its
-// causal prefix, which the RoPE / KV kernel has written to the cache first).
+// One projection of all M positions: X rows ldx apart -> Y rows ldy apart.  Q4_K: the
+// f32-operand GEMM; Q6_K: the Q6_K matvec once per position.
+static void prompt_proj(const larql::DevWeight& w, const float* X, size_t ldx, float* Y, size_t ldy, size_t M,
+                        float* spl, size_t split_n, hipStream_t s) {
+    if (w.format == LARQL_Q4_K) {
+        larql::launch_q4k_gemm_f32(w, X, Y, M, spl, split_n, s, ldy);
+        return;
+    }
+    for (size_t p = 0; p < M; p++) larql::launch_q6k_matvec(w, X + p * ldx, Y + p * ldy, 1, s);
+}
+
 static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M, float* dout, hipStream_t s) {
     auto& kv = c->kv;
     kv_ensure(c, m->layers.size(), m->nkv, m->hd, M);
@@ -456,9 +464,14 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
     const int S = larql::attn_prompt_splits(1, static_cast<int>(M), 0);
     const size_t part_n = M * static_cast<size_t>(m->nq) * S * (m->hd + 2);
     size_t split_n = 0;  // K-split partial products of the GEMMs
-    for (const LayerDev& L : m->layers)
-        split_n = std::max({split_n, larql::q4k_gemm_f32_part_floats(L.qkv, M), larql::q4k_gemm_f32_part_floats(L.wo, M),
-                            larql::q4k_gemm_f32_part_floats(L.gateup, M), larql::q4k_gemm_f32_part_floats(L.down, M)});
+    auto need = [&](const larql::DevWeight& w) {
+        if (w.format == LARQL_Q4_K) split_n = std::max(split_n, larql::q4k_gemm_f32_part_floats(w, M));
+    };
+    for (const LayerDev& L : m->layers) {
+        if (L.split_qkv) need(L.wq), need(L.wk), need(L.wv);
+        else need(L.qkv);
+        need(L.wo), need(L.gateup), need(L.down);
+    }
     const size_t n_f = 2 * M * hidden + M * wide + M * ld + M * qd + M * gw + M * inter + part_n + split_n;
     float* base = static_cast<float*>(larql::ensure(c, m->prompt, n_f * sizeof(float)));
     float *H0 = base, *H1 = H0 + M * hidden, *XN = H1 + M * hidden, *QKV = XN + M * wide, *ATT = QKV + M * ld;
@@ -467,7 +480,13 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
         larql::launch_rmsnorm_rows(H0, L.input_norm, XN, M, hidden, L.eps, s);
-        larql::launch_q4k_gemm_f32(L.qkv, XN, QKV, M, SPL, split_n, s);
+        if (L.split_qkv) {  // Q, K, V into their column ranges of the [q | k | v] rows
+            prompt_proj(L.wq, XN, hidden, QKV, ld, M, SPL, split_n, s);
+            prompt_proj(L.wk, XN, hidden, QKV + qd, ld, M, SPL, split_n, s);
+            prompt_proj(L.wv, XN, hidden, QKV + qd + kvd, ld, M, SPL, split_n, s);
+        } else {
+            prompt_proj(L.qkv, XN, hidden, QKV, ld, M, SPL, split_n, s);
+        }
         const float2* rope = rope_table(c, L.rope_base, L.rdim, s);
         larql::launch_rope_kv_rows(QKV, M, 0, qd, kvd, L.hd, L.rdim, rope, kv.k[l], kv.v[l], L.nkv, s);
         larql::AttnArgs at{};
@@ -487,12 +506,12 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
         at.window = L.window;
         at.qkv_ld = static_cast<int>(ld);
         larql::launch_attention(at, s);
-        larql::launch_q4k_gemm_f32(L.wo, ATT, G, M, SPL, split_n, s);
+        prompt_proj(L.wo, ATT, qd, G, hidden, M, SPL, split_n, s);
         larql::launch_add_rows(H0, G, H1, M * hidden, s);
         larql::launch_rmsnorm_rows(H1, L.post_attn_norm, XN, M, hidden, L.eps, s);
-        larql::launch_q4k_gemm_f32(L.gateup, XN, G, M, SPL, split_n, s);
+        prompt_proj(L.gateup, XN, hidden, G, 2 * inter, M, SPL, split_n, s);
         larql::launch_silu_pair_rows(G, ACT, M * inter, s);
-        larql::launch_q4k_gemm_f32(L.down, ACT, G, M, SPL, split_n, s);
+        prompt_proj(L.down, ACT, inter, G, hidden, M, SPL, split_n, s);
         larql::launch_add_rows(H1, G, H0, M * hidden, s);
     }
     larql::launch_copy_f32(H0, dout, M * hidden, s);

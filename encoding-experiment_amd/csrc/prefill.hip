@@ -254,7 +254,7 @@ constexpr int kF32Pitch = 36;  // floats per lane slot in LDS (32 + 4: spread th
 __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* __restrict__ qs,
                                                                 const v4u* __restrict__ hdr,
                                                                 const float* __restrict__ X, float* __restrict__ Y,
-                                                                int M, int N, int K, int ntiles, int sb_per) {
+                                                                int M, int N, int K, int ntiles, int sb_per, int ldy) {
     __shared__ float As[2][kMt][64][kF32Pitch];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
@@ -262,8 +262,9 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
     const int mt0 = blockIdx.y * kMt;
     const int nt0 = (blockIdx.x * kWaves + wave) * kNT;
     // split blockIdx.z of K: super-blocks [z sb_per, (z + 1) sb_per), partial sums to Y[z]
+    // (rows ldy apart; the dense partials of a split launch have ldy = N)
     const int u0 = 2 * static_cast<int>(blockIdx.z) * sb_per, u1 = min(2 * S, u0 + 2 * sb_per), last = u1 - 1;
-    Y += static_cast<size_t>(blockIdx.z) * M * N;
+    Y += static_cast<size_t>(blockIdx.z) * M * ldy;
     uint32_t qo[kNT], ho[kNT];
 #pragma unroll
     for (int j = 0; j < kNT; j++) {
@@ -374,18 +375,19 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = (mt0 + i) * 16 + 4 * g + r;
-                if (m < M && col < N) Y[static_cast<size_t>(m) * N + col] = acc[i][j][r];
+                if (m < M && col < N) Y[static_cast<size_t>(m) * ldy + col] = acc[i][j][r];
             }
         }
 }
 
 // Y = sum over the splits of the partial products, in split order (deterministic).
-__global__ void sum_splits_kernel(const float* __restrict__ P, float* __restrict__ Y, size_t n, int splits) {
+__global__ void sum_splits_kernel(const float* __restrict__ P, float* __restrict__ Y, size_t n, int splits, int N,
+                                  int ldy) {
     const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
     if (i >= n) return;
     float a = P[i];
     for (int z = 1; z < splits; z++) a += P[z * n + i];
-    Y[i] = a;
+    Y[(i / N) * ldy + i % N] = a;
 }
 
 // K-splits for the f32 GEMM: the count (1..4, whole super-blocks each) that minimises
@@ -415,7 +417,9 @@ size_t q4k_gemm_f32_part_floats(const DevWeight& w, size_t m) {
 }
 
 void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, float* part, size_t part_floats,
-                         hipStream_t s) {
+                         hipStream_t s, size_t ldy) {
+    if (ldy == 0) ldy = w.rows;
+    if (ldy < w.rows || ldy > 0x7FFFFFFF) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: bad output row stride");
     if (w.format != LARQL_Q4_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: Q4_K weights only");
     if (m == 0) return;
     if (m > 0x7FFFFFFF / w.cols) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: too many tokens");
@@ -425,11 +429,13 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
                     static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)), static_cast<unsigned>(sp.splits));
     q4k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(
         w.qs, reinterpret_cast<const v4u*>(w.hdr), X, sp.splits > 1 ? part : Y, static_cast<int>(m),
-        static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per);
+        static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per,
+        static_cast<int>(sp.splits > 1 ? w.rows : ldy));
     LARQL_HIP_CHECK(hipGetLastError());
     if (sp.splits > 1) {
         const size_t n = m * w.rows;
-        sum_splits_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(part, Y, n, sp.splits);
+        sum_splits_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(
+            part, Y, n, sp.splits, static_cast<int>(w.rows), static_cast<int>(ldy));
         LARQL_HIP_CHECK(hipGetLastError());
     }
 }

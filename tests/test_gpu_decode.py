@@ -132,14 +132,16 @@ def test_decode_mixed_projection_formats(hip, formats):
     run_sequence(hip, T0=40, n_tokens=2, n_layers=2, formats=formats)
 
 
-@pytest.mark.parametrize("seq,formats,window", [(6, {"wv": "q6_k"}, 0), (6, None, 0), (70, None, 0),
+@pytest.mark.parametrize("seq,formats,window", [(6, {"wv": "q6_k"}, 0), (20, {"wo": "q6_k", "down": "q6_k"}, 0),
+                                                 (6, {"up": "q6_k"}, 0), (6, None, 0), (70, None, 0),
                                                  (70, None, 37)])
 def test_prefill_q4_matches_oracle_and_decode(hip, seq, formats, window):
     """prefill_q4 (backend.rs:139-152): a prompt from position 0; every position's hidden
     state against the oracle layers, the cache left at seq positions, and the next
-    decode_token against decoding the prompt token by token.  All-Q4_K layers take the
-    batched pass (Q4_K GEMMs with f32 operands, prompt-mode attention: within the
-    1e-3 bar); the mixed-format model runs position by position (bit-identical)."""
+    decode_token against decoding the prompt token by token.  Layers with gate/up fused
+    in Q4_K take the batched pass (Q4_K GEMMs with f32 operands, Q6_K projections per
+    position, prompt-mode attention: within the 1e-3 bar); split gate/up runs position
+    by position (bit-identical to token-by-token decode)."""
     n_layers, hidden, inter, nq, nkv, hd = 2, 512, 1024, 8, 2, 64
     print(f"[prefill] seq={seq} formats={formats} window={window}", flush=True)
     m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=77, formats=formats)
@@ -163,7 +165,7 @@ def test_prefill_q4_matches_oracle_and_decode(hip, seq, formats, window):
     for p in range(seq):
         hip.decode_token(layers, x[p], hidden, inter, nq * hd, nkv * hd, nq, nkv, hd, 10000.0)
     stepwise = hip.decode_token(layers, nxt, hidden, inter, nq * hd, nkv * hd, nq, nkv, hd, 10000.0)
-    if formats:
+    if formats and ("gate" in formats or "up" in formats):
         assert np.array_equal(after_prefill, stepwise)
     else:
         e = rel_err(after_prefill, stepwise.astype(np.float64))
