@@ -504,8 +504,8 @@ def main():
         pmc_report(*args.pmc_report)
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this benchmark runs on exactly one GPU; sharding is described in DESIGN.md and "
-                                   "not built (one GPU's share is the full single-GPU shape)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU sharding is not built "
+                                   "(one GPU's share is the full single-GPU shape)", "n_gpus": args.gpus}))
         sys.exit(2)
     if args.pmc_pass:
         pmc_pass(args.pmc_pass, args.pmc_launches)
