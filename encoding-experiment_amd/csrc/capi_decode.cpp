@@ -445,15 +445,12 @@ static bool prompt_batchable(const larql_hip_model* m) {
     return true;
 }
 
-// One projection of all M positions: X rows ldx apart -> Y rows ldy apart.  Q4_K: the
-// f32-operand GEMM; Q6_K: the Q6_K matvec once per position.
+// One projection of all M positions (X rows ldx = w.cols apart) -> Y rows ldy apart: the
+// f32-operand GEMM, Q4_K or Q6_K.
 static void prompt_proj(const larql::DevWeight& w, const float* X, size_t ldx, float* Y, size_t ldy, size_t M,
                         float* spl, size_t split_n, hipStream_t s) {
-    if (w.format == LARQL_Q4_K) {
-        larql::launch_q4k_gemm_f32(w, X, Y, M, spl, split_n, s, ldy);
-        return;
-    }
-    for (size_t p = 0; p < M; p++) larql::launch_q6k_matvec(w, X + p * ldx, Y + p * ldy, 1, s);
+    if (ldx != w.cols) fail(LARQL_HIP_ERR_INVALID, "prompt pass: input rows do not match the weight");
+    larql::launch_q4k_gemm_f32(w, X, Y, M, spl, split_n, s, ldy);
 }
 
 static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M, float* dout, hipStream_t s) {
@@ -465,7 +462,7 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
     const size_t part_n = M * static_cast<size_t>(m->nq) * S * (m->hd + 2);
     size_t split_n = 0;  // K-split partial products of the GEMMs
     auto need = [&](const larql::DevWeight& w) {
-        if (w.format == LARQL_Q4_K) split_n = std::max(split_n, larql::q4k_gemm_f32_part_floats(w, M));
+        split_n = std::max(split_n, larql::q4k_gemm_f32_part_floats(w, M));
     };
     for (const LayerDev& L : m->layers) {
         if (L.split_qkv) need(L.wq), need(L.wk), need(L.wv);

@@ -185,7 +185,8 @@ void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, voi
 // workgroups per tile, summed in split order from `part` (floats: q4k_gemm_f32_part_floats;
 // with less, no split).
 size_t q4k_gemm_f32_part_floats(const DevWeight& w, size_t m);
-// Y rows are ldy floats apart (0: w.rows), so a projection can fill a column slice.
+// Q4_K or Q6_K weights.  Y rows are ldy floats apart (0: w.rows), so a projection can
+// fill a column slice.
 void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, float* part, size_t part_floats,
                          hipStream_t s, size_t ldy = 0);
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,

@@ -380,6 +380,133 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
         }
 }
 
+// Q6_K weights (ql nibble of element e at byte e / 2, its two high bits regrouped per
+// 16-element group G: element 16 G + 8 w + 2 j + p at bits 8 j + 4 w + 2 p of word G; int8
+// scale per group; f16 d per block) with the f32 kernel's X staging and tiling: lane (g, c)
+// of unit (sb, h) takes elements 32 (4h + g) .. + 31 of row c of each tile, i.e. 16 ql
+// bytes, two high-bit words and two scales; w = fma(q, d sc, -32 d sc) = d sc (q - 32).
+__global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* __restrict__ ql,
+                                                                const uint8_t* __restrict__ qh,
+                                                                const int8_t* __restrict__ scl,
+                                                                const uint16_t* __restrict__ dd,
+                                                                const float* __restrict__ X, float* __restrict__ Y,
+                                                                int M, int N, int K, int sb_per, int ldy) {
+    __shared__ float As[2][kMt][64][kF32Pitch];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int S = K / 256;
+    const int mt0 = blockIdx.y * kMt;
+    const int nt0 = (blockIdx.x * kWaves + wave) * kNT;
+    const int u0 = 2 * static_cast<int>(blockIdx.z) * sb_per, u1 = min(2 * S, u0 + 2 * sb_per), last = u1 - 1;
+    Y += static_cast<size_t>(blockIdx.z) * M * ldy;
+    size_t blk[kNT];  // first block of the lane's row in tile j (rows past N re-read row N - 1)
+#pragma unroll
+    for (int j = 0; j < kNT; j++) blk[j] = static_cast<size_t>(min((nt0 + j) * 16 + c, N - 1)) * S;
+    const int xr_row = (mt0 + (tid >> 6)) * 16 + (lane & 15);
+    const bool xr_ok = xr_row < M;
+    const float* xrow = X + static_cast<size_t>(min(xr_row, M - 1)) * K + 32 * g;
+    struct Xu {
+        float4 v[8];
+    };
+    auto load_x = [&](int u, Xu& x) __attribute__((always_inline)) {
+        const float4* p = reinterpret_cast<const float4*>(xrow + 256 * (u >> 1) + 128 * (u & 1));
+#pragma unroll
+        for (int k = 0; k < 8; k++) x.v[k] = xr_ok ? p[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto store_x = [&](int b, const Xu& x) __attribute__((always_inline)) {
+        float4* d = reinterpret_cast<float4*>(&As[b][tid >> 6][lane][0]);
+#pragma unroll
+        for (int k = 0; k < 8; k++) d[k] = x.v[k];
+    };
+    struct Wu {
+        v4u l[kNT];
+        uint2 h[kNT];
+        uint32_t sd[kNT];  // scales of groups G0, G0 + 1 | d << 16
+    };
+    auto load_w = [&](int u, Wu& w) __attribute__((always_inline)) {
+        const int G0 = 8 * (u & 1) + 2 * g;
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+            const size_t o = blk[j] + (u >> 1);
+            w.l[j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(ql + o * 128 + 64 * (u & 1) + 16 * g));
+            w.h[j] = *reinterpret_cast<const uint2*>(qh + o * 64 + 4 * G0);
+            w.sd[j] = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(scl + o * 16 + G0)) |
+                      (static_cast<uint32_t>(dd[o]) << 16);
+        }
+    };
+    floatx4 acc[kMt][kNT];
+#pragma unroll
+    for (int i = 0; i < kMt; i++)
+#pragma unroll
+        for (int j = 0; j < kNT; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int b, const Wu& w) __attribute__((always_inline)) {
+        float ds[kNT][2];
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+            const float d = h2f(w.sd[j] >> 16);
+            ds[j][0] = d * static_cast<float>(static_cast<int8_t>(w.sd[j] & 0xFFu));
+            ds[j][1] = d * static_cast<float>(static_cast<int8_t>((w.sd[j] >> 8) & 0xFFu));
+        }
+#pragma unroll
+        for (int e4 = 0; e4 < 8; e4++) {  // elements 4 e4 .. 4 e4 + 3 of the lane's 32
+            float4 a[kMt];
+#pragma unroll
+            for (int i = 0; i < kMt; i++) a[i] = *reinterpret_cast<const float4*>(&As[b][i][lane][4 * e4]);
+#pragma unroll
+            for (int j = 0; j < kNT; j++) {
+                const float sc = ds[j][e4 >> 2], nb = -32.f * sc;
+                const uint32_t lo = w.l[j][e4 >> 1], hi = (e4 >> 2) ? w.h[j].y : w.h[j].x;
+                float wt[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const uint32_t q4 = (lo >> (16 * (e4 & 1) + 4 * t)) & 0xFu;
+                    const uint32_t q2 =
+                        (hi >> (16 * (e4 & 1) + 8 * (t >> 1) + 4 * ((e4 >> 1) & 1) + 2 * (t & 1))) & 3u;
+                    wt[t] = __builtin_fmaf(static_cast<float>(q4 | (q2 << 4)), sc, nb);
+                }
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < kMt; i++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][t], wt[t], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+
+    Wu w0, w1;
+    Xu x0, x1;
+    load_x(u0, x0);
+    load_w(u0, w0);
+    load_x(u0 + 1, x1);
+    load_w(u0 + 1, w1);
+    store_x(0, x0);
+    __syncthreads();
+    for (int u = u0; u < u1; u += 2) {
+        store_x(1, x1);
+        load_x(min(u + 2, last), x0);
+        compute(0, w0);
+        load_w(min(u + 2, last), w0);
+        __syncthreads();
+        store_x(0, x0);
+        load_x(min(u + 3, last), x1);
+        compute(1, w1);
+        load_w(min(u + 3, last), w1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < kMt; i++)
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+            const int col = (nt0 + j) * 16 + c;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = (mt0 + i) * 16 + 4 * g + r;
+                if (m < M && col < N) Y[static_cast<size_t>(m) * ldy + col] = acc[i][j][r];
+            }
+        }
+}
+
 // Y = sum over the splits of the partial products, in split order (deterministic).
 __global__ void sum_splits_kernel(const float* __restrict__ P, float* __restrict__ Y, size_t n, int splits, int N,
                                   int ldy) {
@@ -420,17 +547,23 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
                          hipStream_t s, size_t ldy) {
     if (ldy == 0) ldy = w.rows;
     if (ldy < w.rows || ldy > 0x7FFFFFFF) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: bad output row stride");
-    if (w.format != LARQL_Q4_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: Q4_K weights only");
+    if (w.format != LARQL_Q4_K && w.format != LARQL_Q6_K)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: Q4_K or Q6_K weights only");
     if (m == 0) return;
     if (m > 0x7FFFFFFF / w.cols) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: too many tokens");
     F32Split sp = f32_split(w, m);
     if (sp.splits > 1 && (!part || part_floats < sp.splits * m * w.rows)) sp = {1, static_cast<int>(w.cols / 256)};
     const dim3 grid(static_cast<unsigned>((w.rows + kNwg - 1) / kNwg),
                     static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)), static_cast<unsigned>(sp.splits));
-    q4k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(
-        w.qs, reinterpret_cast<const v4u*>(w.hdr), X, sp.splits > 1 ? part : Y, static_cast<int>(m),
-        static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per,
-        static_cast<int>(sp.splits > 1 ? w.rows : ldy));
+    const int ld_out = static_cast<int>(sp.splits > 1 ? w.rows : ldy);
+    if (w.format == LARQL_Q4_K)
+        q4k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(
+            w.qs, reinterpret_cast<const v4u*>(w.hdr), X, sp.splits > 1 ? part : Y, static_cast<int>(m),
+            static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per, ld_out);
+    else
+        q6k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(
+            w.qs, w.qh, w.sc, static_cast<const uint16_t*>(w.d), X, sp.splits > 1 ? part : Y, static_cast<int>(m),
+            static_cast<int>(w.rows), static_cast<int>(w.cols), sp.sb_per, ld_out);
     LARQL_HIP_CHECK(hipGetLastError());
     if (sp.splits > 1) {
         const size_t n = m * w.rows;

@@ -139,8 +139,8 @@ def test_prefill_q4_matches_oracle_and_decode(hip, seq, formats, window):
     """prefill_q4 (backend.rs:139-152): a prompt from position 0; every position's hidden
     state against the oracle layers, the cache left at seq positions, and the next
     decode_token against decoding the prompt token by token.  Layers with gate/up fused
-    in Q4_K take the batched pass (Q4_K GEMMs with f32 operands, Q6_K projections per
-    position, prompt-mode attention: within the 1e-3 bar); split gate/up runs position
+    in Q4_K take the batched pass (Q4_K and Q6_K GEMMs with f32 operands, prompt-mode
+    attention: within the 1e-3 bar); split gate/up runs position
     by position (bit-identical to token-by-token decode)."""
     n_layers, hidden, inter, nq, nkv, hd = 2, 512, 1024, 8, 2, 64
     print(f"[prefill] seq={seq} formats={formats} window={window}", flush=True)
