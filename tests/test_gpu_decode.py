@@ -175,12 +175,13 @@ def test_prefill_q4_matches_oracle_and_decode(hip, seq, formats, window):
         hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0, use_qk_norm=True)
 
 
-def test_prefill_q4_uneven_k_splits(hip):
-    """hidden 2560 = 10 Q4_K super-blocks: the small Q|K|V grid splits K four ways as 3, 3,
-    3 and 1 super-blocks (the last split shorter), summed in split order; every position
-    stays within the bar."""
+@pytest.mark.parametrize("formats", [None, {"wv": "q6_k", "down": "q6_k"}])
+def test_prefill_q4_uneven_k_splits(hip, formats):
+    """hidden 2560 = 10 super-blocks: the small Q|K|V grids split K four ways as 3, 3, 3
+    and 1 super-blocks (the last split shorter), summed in split order, for Q4_K and Q6_K
+    weights; every position stays within the bar."""
     n_layers, hidden, inter, nq, nkv, hd, seq = 2, 2560, 1024, 8, 2, 64, 20
-    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=13)
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=13, formats=formats)
     layers = m.hip_layers(10000.0)
     x = np.stack([oracle.gauss(200 + p, hidden) for p in range(seq)])
     hip.reset_kv_cache()
