@@ -59,6 +59,8 @@ def _load():
             "lo_rms_norm": (None, [_P, _P, ctypes.c_float, ctypes.c_double, _P, _SZ]),
             "lo_rope_at": (None, [_P, _SZ, _SZ, _SZ, ctypes.c_double, _SZ]),
             "lo_silu_gate_up": (None, [_P, _P, _P, _SZ]),
+            "lo_gelu_tanh_gate_up": (None, [_P, _P, _P, _SZ]),
+            "lo_rms_norm_heads": (None, [_P, _SZ, _SZ, ctypes.c_double]),
             "lo_attend_f16": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
             "lo_decode_layer": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, ctypes.c_double]),
             "lo_decode_layer_window": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, ctypes.c_double,
@@ -270,6 +272,19 @@ def silu_gate_up(g, u):
     return out
 
 
+def gelu_tanh_gate_up(g, u):
+    g, u = _c(g, np.float32), _c(u, np.float32)
+    out = np.empty_like(g)
+    _load().lo_gelu_tanh_gate_up(_ptr(g), _ptr(u), _ptr(out), g.size)
+    return out
+
+
+def rms_norm_heads(x, num_heads: int, head_dim: int, eps: float = 1e-6):
+    x = np.array(x, dtype=np.float32, copy=True)
+    _load().lo_rms_norm_heads(_ptr(x), num_heads, head_dim, eps)
+    return x
+
+
 def attend_f16(q, kc, vc, T: int, num_q: int, num_kv: int, head_dim: int, scale: float, t_start: int = 0):
     """Attention of the last query row over cache positions t_start .. T-1 (t_start > 0 is
     the sliding window, LC/src/metal/shaders/kv_attention.rs:35)."""
@@ -287,15 +302,23 @@ _PROJ = ("wq", "wk", "wv", "wo", "gate", "up", "down")
 
 class _Layer(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in _PROJ + ("input_norm", "post_attn_norm", "k_cache", "v_cache")] + \
-               [("fmt", ctypes.c_int * 7)]
+               [("fmt", ctypes.c_int * 7),
+                ("pre_ffn_norm", ctypes.c_void_p), ("post_ffn_norm", ctypes.c_void_p),
+                ("norm_offset", ctypes.c_float), ("has_post_norms", ctypes.c_int),
+                ("activation", ctypes.c_int), ("has_v_norm", ctypes.c_int),
+                ("layer_scalar", ctypes.c_float), ("rotary_dim", ctypes.c_size_t),
+                ("attn_scale", ctypes.c_float)]
 
 
 def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, num_kv: int,
                  head_dim: int, rope_base: float, eps: float = 1e-6, window: int = 0):
-    """One Llama decoder layer on the CPU.  ``layer`` holds numpy arrays keyed as
-    the lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits) are updated in place.
+    """One decoder layer on the CPU.  ``layer`` holds numpy arrays keyed as the
+    lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits) are updated in place.
     window > 0 attends over the last `window` positions only.  ``layer["formats"]``
-    (optional) maps a projection name to "q6_k" for Q6_K bytes (default Q4_K)."""
+    (optional) maps a projection name to "q6_k" for Q6_K bytes (default Q4_K).
+    Optional layer variants (FullPipelineLayer, LC/src/pipeline.rs:76-115):
+    pre_ffn_norm / post_ffn_norm (arrays or None), norm_offset, has_post_norms,
+    activation ("silu" | "gelu_tanh"), has_v_norm, layer_scalar, rotary_dim, attn_scale."""
     keep = {}
     st = _Layer()
     for name, dt in (("wq", np.uint8), ("wk", np.uint8), ("wv", np.uint8), ("wo", np.uint8),
@@ -304,6 +327,11 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
         a = _c(layer[name], dt)
         keep[name] = a
         setattr(st, name, a.ctypes.data)
+    for name in ("pre_ffn_norm", "post_ffn_norm"):
+        if layer.get(name) is not None:
+            a = _c(layer[name], np.float32)
+            keep[name] = a
+            setattr(st, name, a.ctypes.data)
     fm = layer.get("formats", {})
     for i, name in enumerate(_PROJ):
         st.fmt[i] = 1 if fm.get(name, "q4_k") == "q6_k" else 0
@@ -311,6 +339,13 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
         a = layer[name]
         assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]
         setattr(st, name, a.ctypes.data)
+    st.norm_offset = float(layer.get("norm_offset", 0.0))
+    st.has_post_norms = int(bool(layer.get("has_post_norms", False)))
+    st.activation = {"silu": 0, "gelu_tanh": 1}[layer.get("activation", "silu")]
+    st.has_v_norm = int(bool(layer.get("has_v_norm", False)))
+    st.layer_scalar = float(layer.get("layer_scalar", 0.0))
+    st.rotary_dim = int(layer.get("rotary_dim", 0))
+    st.attn_scale = float(layer.get("attn_scale", 0.0))
     h = np.array(h, dtype=np.float32, copy=True)
     _load().lo_decode_layer_window(ctypes.byref(st), _ptr(h), pos, hidden, inter, num_q, num_kv,
                                    head_dim, rope_base, eps, window)

@@ -540,6 +540,28 @@ void lo_silu_gate_up(const float* gate, const float* up, float* out, size_t n) {
     }
 }
 
+/* LI/src/ffn/mod.rs:96-103 — gelu_tanh(g) * u with
+ * gelu_tanh(x) = 0.5 x (1 + tanh(0.7978846 (x + 0.044715 x^3))), all in f32. */
+void lo_gelu_tanh_gate_up(const float* gate, const float* up, float* out, size_t n) {
+    const float c = 0.7978846f;
+    for (size_t i = 0; i < n; i++) {
+        float x = gate[i];
+        float inner = c * (x + 0.044715f * x * x * x);
+        out[i] = (0.5f * x * (1.0f + tanhf(inner))) * up[i];
+    }
+}
+
+/* LI/src/residual.rs:86-110 — per head: rms = sqrt(sum(f64 x^2)/hd + eps) as f32, x / rms. */
+void lo_rms_norm_heads(float* x, size_t num_heads, size_t head_dim, double eps) {
+    for (size_t h = 0; h < num_heads; h++) {
+        float* v = x + h * head_dim;
+        double sq = 0.0;
+        for (size_t d = 0; d < head_dim; d++) sq += (double)v[d] * (double)v[d];
+        float rms = (float)sqrt(sq / (double)head_dim + eps);
+        for (size_t d = 0; d < head_dim; d++) v[d] = v[d] / rms;
+    }
+}
+
 /* LI/src/attention/gqa.rs:29-110, last query row only: s = (k.q) * scale;
  * e = exp((s - max) as f64); sum in f64; p = (e as f32) * ((1/sum) as f32); out = V^T p.
  * K/V come from an fp16 cache [t][kv_head][head_dim]; kv_h = h / (num_q / num_kv). */
@@ -582,10 +604,18 @@ static void lo_proj(int fmt, const uint8_t* w, const float* x, float* out, size_
     else lo_q4k_matvec(w, x, out, rows, cols);
 }
 
-/* One Llama layer: pre-norm attention + SwiGLU FFN, no post-norms, norm offset 0
- * (LI/src/attention/block.rs:52-157, LI/src/forward/layer.rs:50-94; per-op order of
- * the reference GPU decode LC/src/metal/decode.rs:144-715).  The new K/V row is
- * appended at pos (LC/src/metal/ops/kv_cache.rs:73-105), stored as fp16 (RNE). */
+/* One decoder layer (LI/src/attention/block.rs:52-157, LI/src/forward/layer.rs:50-94; per-op
+ * order of the reference GPU decode LC/src/metal/decode.rs:144-739):
+ *   xn = norm(h, input_norm); q, k, v = projections; [V-norm]; RoPE(q, k) at pos;
+ *   K/V appended at pos (LC/src/metal/ops/kv_cache.rs:73-105) as fp16 (RNE); attention;
+ *   o = Wo att;
+ *   Llama:       h1 = h + o;                          f = norm(h1, post_attn_norm)
+ *   post-norms:  h1 = h + norm(o, post_attn_norm);    f = norm(h1, pre_ffn_norm)
+ *   a = act(gate f) * (up f); dn = Wd a;
+ *   Llama:       h2 = h1 + dn;   post-norms: h2 = h1 + norm(dn, post_ffn_norm)
+ *   layer_scalar != 0: h2 *= layer_scalar.
+ * norm(x, w) = x / rms * (norm_offset + w) (LI/src/residual.rs:17-33); an absent
+ * pre/post-FFN weight is the weight-free norm (LI/src/forward/layer.rs:65-68, 80-83). */
 void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,
                      size_t hidden, size_t inter, size_t num_q, size_t num_kv, size_t head_dim,
                      double rope_base, double eps) {
@@ -598,6 +628,8 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
                             size_t hidden, size_t inter, size_t num_q, size_t num_kv, size_t head_dim,
                             double rope_base, double eps, size_t window) {
     size_t qd = num_q * head_dim, kvd = num_kv * head_dim;
+    const size_t rdim = L->rotary_dim ? L->rotary_dim : head_dim;
+    const float off = L->norm_offset;
     float* xn = (float*)malloc(hidden * sizeof(float));
     float* q = (float*)malloc(qd * sizeof(float));
     float* k = (float*)malloc(kvd * sizeof(float));
@@ -608,28 +640,42 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
     float* u = (float*)malloc(inter * sizeof(float));
     float* a = (float*)malloc(inter * sizeof(float));
 
-    lo_rms_norm(h, L->input_norm, 0.0f, eps, xn, hidden);
+    lo_rms_norm(h, L->input_norm, off, eps, xn, hidden);
     lo_proj(L->fmt[0], L->wq, xn, q, qd, hidden);
     lo_proj(L->fmt[1], L->wk, xn, k, kvd, hidden);
     lo_proj(L->fmt[2], L->wv, xn, v, kvd, hidden);
-    lo_rope_at(q, num_q, head_dim, head_dim, rope_base, pos);
-    lo_rope_at(k, num_kv, head_dim, head_dim, rope_base, pos);
+    if (L->has_v_norm) lo_rms_norm_heads(v, num_kv, head_dim, eps);
+    lo_rope_at(q, num_q, head_dim, rdim, rope_base, pos);
+    lo_rope_at(k, num_kv, head_dim, rdim, rope_base, pos);
     for (size_t i = 0; i < kvd; i++) {
         L->k_cache[pos * kvd + i] = lo_f32_to_f16_rne(k[i]);
         L->v_cache[pos * kvd + i] = lo_f32_to_f16_rne(v[i]);
     }
-    float scale = (float)(1.0 / sqrt((double)head_dim));
+    float scale = L->attn_scale != 0.0f ? L->attn_scale : (float)(1.0 / sqrt((double)head_dim));
     const size_t T = pos + 1, t0 = (window > 0 && T > window) ? T - window : 0;
     lo_attend_f16(q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, T - t0, num_q, num_kv, head_dim, scale, att);
     lo_proj(L->fmt[3], L->wo, att, o, hidden, qd);
-    for (size_t i = 0; i < hidden; i++) h[i] = h[i] + o[i];
-
-    lo_rms_norm(h, L->post_attn_norm, 0.0f, eps, xn, hidden);
+    if (L->has_post_norms) {
+        lo_rms_norm(o, L->post_attn_norm, off, eps, xn, hidden);
+        for (size_t i = 0; i < hidden; i++) h[i] = h[i] + xn[i];
+        lo_rms_norm(h, L->pre_ffn_norm, off, eps, xn, hidden);
+    } else {
+        for (size_t i = 0; i < hidden; i++) h[i] = h[i] + o[i];
+        lo_rms_norm(h, L->post_attn_norm, off, eps, xn, hidden);
+    }
     lo_proj(L->fmt[4], L->gate, xn, g, inter, hidden);
     lo_proj(L->fmt[5], L->up, xn, u, inter, hidden);
-    lo_silu_gate_up(g, u, a, inter);
+    if (L->activation == 1) lo_gelu_tanh_gate_up(g, u, a, inter);
+    else lo_silu_gate_up(g, u, a, inter);
     lo_proj(L->fmt[6], L->down, a, o, hidden, inter);
-    for (size_t i = 0; i < hidden; i++) h[i] = h[i] + o[i];
+    if (L->has_post_norms) {
+        lo_rms_norm(o, L->post_ffn_norm, off, eps, xn, hidden);
+        for (size_t i = 0; i < hidden; i++) h[i] = h[i] + xn[i];
+    } else {
+        for (size_t i = 0; i < hidden; i++) h[i] = h[i] + o[i];
+    }
+    if (L->layer_scalar != 0.0f)
+        for (size_t i = 0; i < hidden; i++) h[i] = h[i] * L->layer_scalar;
 
     free(xn); free(q); free(k); free(v); free(att); free(o); free(g); free(u); free(a);
 }

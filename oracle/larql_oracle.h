@@ -77,12 +77,18 @@ void lo_rms_norm(const float* x, const float* w, float offset, double eps, float
 void lo_rope_at(float* x, size_t num_heads, size_t head_dim, size_t rotary_dim,
                 double base, size_t pos);                                         /* rope.rs:22-55 */
 void lo_silu_gate_up(const float* gate, const float* up, float* out, size_t n);  /* ffn/mod.rs:87-94 */
+void lo_gelu_tanh_gate_up(const float* gate, const float* up, float* out, size_t n); /* ffn/mod.rs:96-103 */
+/* Per-head parameter-free RMS norm, in place (LI/src/residual.rs:86-110). */
+void lo_rms_norm_heads(float* x, size_t num_heads, size_t head_dim, double eps);
 /* Single-query GQA over an fp16 cache laid out [t][kv_head][head_dim] (gqa.rs:29-110). */
 void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T,
                    size_t num_q, size_t num_kv, size_t head_dim, float scale, float* out);
 
-/* One Llama decoder layer (Q4_K projections, fp16 KV cache) at position pos.
- * h is updated in place; the new K/V row is written into kc/vc at pos. */
+/* One decoder layer (Q4_K / Q6_K projections, fp16 KV cache) at position pos.
+ * h is updated in place; the new K/V row is written into kc/vc at pos.
+ * The fields after fmt are the layer variants of FullPipelineLayer (LC/src/pipeline.rs:76-115);
+ * all zero is the Llama layer: no post-norms, SiLU, offset 0, no V-norm, no layer scalar,
+ * full rotary, attention scale 1/sqrt(head_dim). */
 typedef struct {
     const uint8_t *wq, *wk, *wv, *wo, *gate, *up, *down;  /* Q4_K 148-byte or Q6_K 210-byte layout */
     const float *input_norm, *post_attn_norm;
@@ -90,6 +96,14 @@ typedef struct {
     /* per projection (wq, wk, wv, wo, gate, up, down): 0 = Q4_K, 1 = Q6_K; mixed formats
      * per projection as the reference's per-layer QuantWeight allows (LC/src/pipeline.rs:22-27) */
     int fmt[7];
+    const float *pre_ffn_norm, *post_ffn_norm;  /* NULL: norm without weight (LI/src/forward/layer.rs:65-68) */
+    float norm_offset;                          /* weight = offset + w (LI/src/residual.rs:26-29) */
+    int has_post_norms;
+    int activation;                             /* 0 = SiLU, 1 = GELU-tanh (LI/src/ffn/mod.rs:87-103) */
+    int has_v_norm;                             /* parameter-free RMS norm of V per head */
+    float layer_scalar;                         /* 0 = disabled; else h *= layer_scalar */
+    size_t rotary_dim;                          /* 0 = head_dim */
+    float attn_scale;                           /* 0 = 1/sqrt(head_dim) */
 } lo_layer_t;
 
 void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,

@@ -37,10 +37,6 @@ def test_q4_vecmat_matches_oracle(hip, inter, hidden):
     e = rel_err(got, ref)
     print(f"  rel_err {e:.2e}", flush=True)
     assert e <= REL_TOL, e
-    # the reference's own C kernel, where it was built, agrees with the oracle exactly
-    r2 = oracle.ref_q4_0_vecmat(act, q4, inter, hidden)
-    if r2 is not None:
-        assert np.array_equal(r2.view(np.uint32), ref.view(np.uint32))
 
 
 def test_q4_vecmat_skips_tiny_activations(hip):

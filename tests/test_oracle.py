@@ -18,23 +18,38 @@ What pins each oracle function (reference paths relative to larql-main/crates/):
                                               the committed golden outputs of that build.
   q4_0 matvec (int-block order)               exact integer block dots vs numpy int64 brute
                                               force; ggml.rs:388-418 element known answers.
-  quantize_q4_k / q4k_matvec                  test_metal_shaders.rs:1301-1331 hand block
+  quantize_q4_k                               two hand-derived 148-byte super-blocks as literal
+                                              bytes: d = gmr/63 and dmin = -gmin/15 with the
+                                              truncating f16 (a case where nearest differs), the
+                                              min nibble of sub-block j >= 4 in the high half,
+                                              .5 ties of sc_j, m_j and q rounding half away.
+  q4k_matvec                                  test_metal_shaders.rs:1301-1331 hand block
                                               (closed form); one-hot probes of hand-built
-                                              blocks (closed form per element); dequant
-                                              error bound of the quantizer.
-  quantize_q6_k / q6k_matvec                  test_metal_shaders.rs:1334-1361 hand block;
+                                              blocks (closed form per element).
+  quantize_q6_k                               a hand-derived 210-byte super-block as literal
+                                              bytes (sub-scale .5 tie, qh bit placement, d =
+                                              amax/32) and a truncating-f16 d case.
+  q6k_matvec                                  test_metal_shaders.rs:1334-1361 hand block;
                                               one-hot probes of hand-built qh/ql/scale bytes.
   quantize_weights_q8 / q8_matvec             exact integer block dots vs numpy; the
                                               q8_matvec.rs:290-316 cosine > 0.999 check.
   top-k (abs / signed)                        test_vindex.rs:134-160 known answers; vs
                                               numpy stable argsort on random scores.
   gate_scores_f32 (canonical fma chain)       vs math.fsum-exact f64 dot within f32 bounds.
-  rms_norm / rope / silu / attention          closed forms: rope(pos=0) = identity, pair
-                                              norm preserved; attention over T=1 returns V
+  rms_norm / silu / gelu / attention          closed forms: attention over T=1 returns V
                                               (LC/src/cpu/ops/attention.rs:66-75), equal keys
-                                              give the mean of V; rms of output = 1.
-  decode_layer                                composition of the above; all-zero weights
-                                              leave h unchanged (residual identity).
+                                              give the mean of V; rms of output = 1;
+                                              gelu_tanh vs f64 tanh; per-head norm by hand.
+  rope_at                                     pos 0 = identity; pairs 1 and half-1 against
+                                              theta = pos * base^(-2i/rdim) (full and partial
+                                              rotary; pass-through past rdim).
+  decode_layer                                a float64 restatement from dequantized weights
+                                              (Llama layer; post-norm / offset / GELU / V-norm /
+                                              scalar layer) within 1e-5, while each planted
+                                              mistake (swapped norms, silu(up)*gate, dropped
+                                              residual, RoPE on V, wrong RoPE exponent, wrong
+                                              kv-head map) moves it by > 1e-2; zero weights
+                                              leave h unchanged.
 """
 import json
 import math
@@ -500,3 +515,316 @@ def test_decode_layer_zero_weights_is_identity():
     h = oracle.gauss(13, hidden)
     out = oracle.decode_layer(layer, h, 2, hidden, inter, nq, nkv, hd, 500000.0)
     assert np.array_equal(out, h)
+
+
+# ── pins written from the reference's rules by hand ──────────────────────
+# Q4_K known-answer super-blocks (LC/src/cpu/ops/q4_common.rs:104-170), bytes derived by
+# hand.  Block A, every value exact in binary: sub-block ranges 15.75, 1, 0, 0.625, 4,
+# 1.5, 6.25, 5 and mins -7.5, -1, 0, 0.25, -3, -3.5, -1.25, -2 give
+#   d = 15.75 / 63 = 0.25 (f16 0x3400), dmin = 7.5 / 15 = 0.5 (f16 0x3800),
+#   sc_j = round(range_j / d) = 63, 4, 0, 3 (2.5 rounds half away), 16, 6, 25, 20,
+#   m_j = round(-min_j / dmin) = 15, 2, 0, 0 (-0.5 -> -1 -> clamp 0), 6, 7, 3 (2.5), 4,
+#   min bytes m_j | m_{j+4} << 4 = 0x6F, 0x72, 0x30, 0x40,
+#   nibbles q = round((x + dmin m_j) / (d sc_j)): sub-block 1 has d sc = dmin m = 1, so
+#   x = -0.5 -> 0.5 -> 1 (half away), x = -0.75 -> 0.25 -> 0; sub-block 4 (d sc = 4,
+#   dmin m = 3) x = -1 -> 0.5 -> 1.
+_Q4K_A_SPEC = {0: ([-7.5, 8.25], 0.0), 1: ([-1.0, 0.0, -0.5, -0.25, -0.75], -1.0), 2: ([], 0.0),
+               3: ([0.25, 0.875], 0.5), 4: ([-3.0, 1.0, -1.0], 0.0), 5: ([-3.5, -2.0], -3.0),
+               6: ([-1.25, 5.0], 0.0), 7: ([-2.0, 3.0], 0.0)}
+_Q4K_A_BYTES = bytes([0x00, 0x34, 0x00, 0x38, 63, 4, 0, 3, 16, 6, 25, 20, 0, 0, 0, 0, 0x6F, 0x72, 0x30, 0x40]
+                     + [0x10] + [0] * 15 + [0x10, 0x11] + [0] * 14 + [0] * 16 + [0x10] + [0x11] * 15
+                     + [0x10] + [0x11] * 15 + [0x10] + [0] * 15 + [0x10] + [0] * 15 + [0x10] + [0] * 15)
+# Block B, values at N(0, 0.02) scale where the truncating f16 encoder matters:
+#   gmr = fl(0.03 + 0.1) = 0.13, d = fl(0.13 / 63) = 0.002063492 -> f16 truncated 0x1839
+#   (round-to-nearest would give 0x183A); gmin = -0.1, dmin = fl(0.1 / 15) = 0.006666667
+#   -> 0x1ED3 (nearest: 0x1ED4); -min/dmin = 10.5 and 13.5 for sub-blocks 2 and 5 round
+#   half away to 11 and 14.
+_Q4K_B_SPEC = {0: ([-0.1, 0.03], 0.01), 1: ([0.02, -0.04, 0.05], 0.0), 2: ([-0.07, 0.06], -0.03),
+               3: ([0.011, 0.012], 0.0115), 4: ([-0.02, -0.005], -0.01), 5: ([-0.09, 0.0], -0.045),
+               6: ([0.0, 0.08], 0.04), 7: ([-0.033, 0.066], 0.022)}
+_Q4K_B_BYTES = bytes.fromhex(
+    "3918d31e3f2c3f00072c27300000000" "03fe60b50" + "10" + "11" * 15 + "0101" + "00" * 14 + "10" + "00" * 15
+    + "00" * 16 + "10" + "11" * 15 + "10" + "11" * 15 + "10" + "00" * 15 + "10" + "11" * 15)
+
+
+def _spec_block(spec, sub=32):
+    x = np.zeros(8 * sub, np.float32)
+    for j, (vals, fill) in spec.items():
+        x[sub * j:sub * (j + 1)] = np.float32(fill)
+        for i, v in enumerate(vals):
+            x[sub * j + i] = np.float32(v)
+    return x
+
+
+def test_q4k_quantizer_known_answer_bytes():
+    assert len(_Q4K_A_BYTES) == 148 and len(_Q4K_B_BYTES) == 148
+    assert oracle.quantize_q4_k(_spec_block(_Q4K_A_SPEC)).tobytes() == _Q4K_A_BYTES
+    assert oracle.quantize_q4_k(_spec_block(_Q4K_B_SPEC)).tobytes() == _Q4K_B_BYTES
+    both = np.concatenate([_spec_block(_Q4K_A_SPEC), _spec_block(_Q4K_B_SPEC)])
+    assert oracle.quantize_q4_k(both).tobytes() == _Q4K_A_BYTES + _Q4K_B_BYTES
+
+
+# Q6_K known-answer super-block (q4_common.rs:179-239), by hand: amax = 4 so d = 4/32 =
+# 0.125 (f16 0x3000); sub-block maxima 4, 0.3125, 0, 1, 0 x 11, 2 give sc_j = 32, 3 (2.5
+# rounds half away), 0, 8, ..., 16; q = round(x / (d sc_j)) + 32: x = 4 -> 33, -4 -> 31,
+# +-0.3125 (d sc = 0.375) -> 33 / 31, 0.15625 -> 32, -1 -> 31, 0.5 (d sc = 1) -> 33 (half
+# away), 2 -> 33.  33 = 0b10_0001 (lo4 1, hi2 2), 31 = 0b01_1111 (lo4 15, hi2 1), 32 (lo4 0,
+# hi2 2); hi2 of element i sits in byte 128 + i/4 at bits 2(i%4), so a byte of four 32s
+# is 0xAA, elements (32, 31, 32, 32) give 0xA6 and (31, 32, 32, 32) 0xA9.
+_Q6K_X = {0: 4.0, 1: -4.0, 16: 0.3125, 17: -0.3125, 18: 0.15625, 48: -1.0, 53: 0.5, 255: 2.0}
+
+
+def _q6k_expected():
+    ql = [0] * 128
+    ql[0], ql[8], ql[24], ql[26], ql[127] = 0xF1, 0xF1, 0x0F, 0x10, 0x10
+    qh = [0xAA] * 64
+    qh[0], qh[4], qh[12] = 0xA6, 0xA6, 0xA9
+    sc = [32, 3, 0, 8] + [0] * 11 + [16]
+    return bytes(ql + qh + sc + [0x00, 0x30])
+
+
+def test_q6k_quantizer_known_answer_bytes():
+    x = np.zeros(256, np.float32)
+    for i, v in _Q6K_X.items():
+        x[i] = v
+    assert oracle.quantize_q6_k(x).tobytes() == _q6k_expected()
+    # truncating f16 of d: amax 0.3 -> d = fl(0.3 / 32) = 0.009375 -> 0x20CC (nearest 0x20CD);
+    # sub-block maxima 0.3 -> sc = 32, 0.1 -> fl(0.1 / d) = 10.666667 -> 11, 0.05 -> 5.33 -> 5
+    x = np.zeros(256, np.float32)
+    x[0], x[16], x[40] = np.float32(0.3), np.float32(-0.1), np.float32(0.05)
+    q = oracle.quantize_q6_k(x)
+    assert list(q[208:210]) == [0xCC, 0x20]
+    assert list(q[192:195].view(np.int8)) == [32, 11, 5]
+
+
+def test_rope_pairs_beyond_zero_closed_form():
+    """theta_i = pos * base^(-2i/rdim) for pairs i = 1 and i = half-1 (LI/src/attention/rope.rs:33-51):
+    a wrong exponent (i/rdim, 2i/head_dim with partial rotary) fails here; pair 0 cannot tell."""
+    rng = np.random.default_rng(21)
+    for hd, rdim, pos, base in ((128, 128, 2048, 500000.0), (64, 32, 37, 10000.0), (96, 96, 5, 1e6)):
+        x = rng.standard_normal(3 * hd).astype(np.float32)
+        y = oracle.rope_at(x, 3, hd, base, pos, rotary_dim=rdim)
+        half = rdim // 2
+        for h in range(3):
+            for i in (1, half - 1):
+                theta = pos * math.pow(base, -2.0 * i / rdim)
+                c, s = np.float32(math.cos(theta)), np.float32(math.sin(theta))
+                x0, x1 = x[h * hd + i], x[h * hd + half + i]
+                assert y[h * hd + i] == x0 * c - x1 * s, (hd, rdim, i)
+                assert y[h * hd + half + i] == x0 * s + x1 * c, (hd, rdim, i)
+            # dimensions past the rotary part pass through unchanged
+            assert np.array_equal(y[h * hd + rdim:(h + 1) * hd], x[h * hd + rdim:(h + 1) * hd])
+
+
+def test_gelu_tanh_closed_form():
+    g = np.array([0.0, 1.0, -2.0, 3.0, -0.5], np.float32)
+    u = np.array([3.0, 2.0, 1.0, 0.5, -4.0], np.float32)
+    out = oracle.gelu_tanh_gate_up(g, u)
+    gd = g.astype(np.float64)
+    ref = 0.5 * gd * (1 + np.tanh(math.sqrt(2 / math.pi) * (gd + 0.044715 * gd ** 3))) * u
+    assert out[0] == 0.0 and np.allclose(out, ref, rtol=2e-6)
+    assert abs(out[1] - 0.8411920 * 2) < 1e-5                  # gelu_tanh(1) = 0.841192
+
+
+def test_rms_norm_heads_closed_form():
+    x = np.array([3.0, 4.0, 0.0, 0.0, 1.0, 1.0, 1.0, 1.0], np.float32)
+    y = oracle.rms_norm_heads(x, 2, 4, eps=0.0)
+    assert np.allclose(y[:4], np.array([3, 4, 0, 0]) / 2.5) and np.allclose(y[4:], 1.0)
+
+
+# ── decode layer against a float64 restatement ──────────────────────────
+def _f16(b):
+    return float(np.uint16(b).view(np.float16))
+
+
+def _deq_q4k(q, rows, cols):
+    blk = q.reshape(rows * cols // 256, 148)
+    out = np.empty((blk.shape[0], 256), np.float64)
+    for n, b in enumerate(blk):
+        d, dmin = _f16(int(b[0]) | int(b[1]) << 8), _f16(int(b[2]) | int(b[3]) << 8)
+        for j in range(8):
+            sc, m = int(b[4 + j]) & 63, (int(b[16 + j % 4]) >> (4 * (j // 4))) & 15
+            nib = b[20 + 16 * j:36 + 16 * j]
+            qv = np.empty(32, np.float64)
+            qv[0::2], qv[1::2] = nib & 15, nib >> 4
+            out[n, 32 * j:32 * j + 32] = d * sc * qv - dmin * m
+    return out.reshape(rows, cols)
+
+
+def _deq_q6k(q, rows, cols):
+    blk = q.reshape(rows * cols // 256, 210)
+    out = np.empty((blk.shape[0], 256), np.float64)
+    e = np.arange(256)
+    for n, b in enumerate(blk):
+        lo4 = (b[e // 2] >> (4 * (e % 2))) & 15
+        hi2 = (b[128 + e // 4] >> (2 * (e % 4))) & 3
+        sc = b[192 + e // 16].view(np.int8).astype(np.float64)
+        out[n] = _f16(int(b[208]) | int(b[209]) << 8) * sc * (lo4 + 16.0 * hi2 - 32.0)
+    return out.reshape(rows, cols)
+
+
+def test_deq_helpers_match_oracle_matvecs():
+    rng = np.random.default_rng(22)
+    w = (rng.standard_normal(16 * 512) * 0.05).astype(np.float32)
+    x = rng.standard_normal(512).astype(np.float32)
+    for quant, deq, mv in ((oracle.quantize_q4_k, _deq_q4k, oracle.q4k_matvec),
+                           (oracle.quantize_q6_k, _deq_q6k, oracle.q6k_matvec)):
+        q = quant(w)
+        ref = deq(q, 16, 512) @ x.astype(np.float64)
+        assert np.allclose(mv(q, x, 16, 512), ref, rtol=1e-5, atol=1e-6)
+
+
+def _ref_layer64(P, h, kc, vc, pos, dims, mut=()):
+    """One layer in float64 from dequantized weights, written from the reference formulas:
+    RMSNorm LI/src/residual.rs:17-33 (x / sqrt(mean x^2 + eps) * (offset + w)); RoPE
+    LI/src/attention/rope.rs:22-55 (split-half pairs, theta = pos base^(-2i/rdim)); GQA
+    LI/src/attention/gqa.rs:29-110 (kv head h / reps, softmax of scaled dots); SiLU / GELU
+    gate x up LI/src/ffn/mod.rs:87-103; residual and post-norm order
+    LI/src/attention/block.rs:139-150 and LI/src/forward/layer.rs:54-94; V-norm
+    LI/src/residual.rs:86-110; layer scalar LI/src/forward/layer.rs:98-108.
+    `mut` plants one mistake, to show the comparison would catch it."""
+    hidden, inter, nq, nkv, hd = dims
+    eps, off = 1e-6, P.get("norm_offset", 0.0)
+    rdim = P.get("rotary_dim", 0) or hd
+
+    def norm(x, w):
+        r = np.sqrt(np.sum(x * x) / x.size + eps)
+        return x / r * ((off + w) if w is not None else 1.0)
+
+    W = P["deq"]
+    h = h.astype(np.float64)
+    nin, npost = P["input_norm"], P["post_attn_norm"]
+    if "swap_norms" in mut:
+        nin, npost = npost, nin
+    xn = norm(h, nin)
+    q, k, v = W["wq"] @ xn, W["wk"] @ xn, W["wv"] @ xn
+    if P.get("has_v_norm"):
+        v = v.reshape(nkv, hd)
+        v = (v / np.sqrt((v * v).mean(1, keepdims=True) + eps)).reshape(-1)
+    half = rdim // 2
+    th = pos * np.power(P["rope_base"], -2.0 * np.arange(half) / rdim)
+    if "rope_exp" in mut:
+        th = pos * np.power(P["rope_base"], -1.0 * np.arange(half) / rdim)
+    c, s = np.cos(th), np.sin(th)
+
+    def rope(t, n):
+        t = t.reshape(n, hd).copy()
+        a, b = t[:, :half].copy(), t[:, half:2 * half].copy()
+        t[:, :half], t[:, half:2 * half] = a * c - b * s, a * s + b * c
+        return t.reshape(-1)
+
+    q, k = rope(q, nq), rope(k, nkv)
+    if "rope_v" in mut:
+        v = rope(v, nkv)
+    kvd = nkv * hd
+    K = kc.view(np.float16).astype(np.float64).reshape(-1, kvd)[:pos + 1].copy()
+    V = vc.view(np.float16).astype(np.float64).reshape(-1, kvd)[:pos + 1].copy()
+    K[pos] = k.astype(np.float16)                                  # fp16 cache row, RNE
+    V[pos] = v.astype(np.float16)
+    scale = P.get("attn_scale", 0.0) or 1.0 / math.sqrt(hd)
+    att = np.empty(nq * hd)
+    for qh in range(nq):
+        kvh = qh % nkv if "kv_map" in mut else qh // (nq // nkv)
+        sc = K[:, kvh * hd:(kvh + 1) * hd] @ q[qh * hd:(qh + 1) * hd] * scale
+        p = np.exp(sc - sc.max())
+        att[qh * hd:(qh + 1) * hd] = (p / p.sum()) @ V[:, kvh * hd:(kvh + 1) * hd]
+    o = W["wo"] @ att
+    if P.get("has_post_norms"):
+        h1 = h + norm(o, npost)
+        f = norm(h1, P.get("pre_ffn_norm"))
+    else:
+        h1 = (o if "drop_residual" in mut else h + o)
+        f = norm(h1, npost)
+    g, u = W["gate"] @ f, W["up"] @ f
+    if "gate_up_swap" in mut:
+        g, u = u, g
+    if P.get("activation") == "gelu_tanh":
+        a = 0.5 * g * (1 + np.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g ** 3))) * u
+    else:
+        a = g / (1 + np.exp(-g)) * u
+    dn = W["down"] @ a
+    h2 = h1 + (norm(dn, P.get("post_ffn_norm")) if P.get("has_post_norms") else dn)
+    if P.get("layer_scalar", 0.0) != 0.0:
+        h2 = h2 * P["layer_scalar"]
+    return h2
+
+
+def _tiny_layer(seed, dims, formats, std=0.08, **variant):
+    hidden, inter, nq, nkv, hd = dims
+    rng = np.random.default_rng(seed)
+    shapes = dict(wq=(nq * hd, hidden), wk=(nkv * hd, hidden), wv=(nkv * hd, hidden), wo=(hidden, nq * hd),
+                  gate=(inter, hidden), up=(inter, hidden), down=(hidden, inter))
+    P = dict(deq={}, formats=formats, rope_base=10000.0, **variant)
+    for name, (r, c) in shapes.items():
+        w = (rng.standard_normal(r * c) * std).astype(np.float32)
+        if formats.get(name) == "q6_k":
+            P[name] = oracle.quantize_q6_k(w)
+            P["deq"][name] = _deq_q6k(P[name], r, c)
+        else:
+            P[name] = oracle.quantize_q4_k(w)
+            P["deq"][name] = _deq_q4k(P[name], r, c)
+    P["input_norm"] = (1.0 + 0.5 * rng.standard_normal(hidden)).astype(np.float32)
+    P["post_attn_norm"] = (0.3 + 0.2 * rng.standard_normal(hidden)).astype(np.float32)
+    if variant.get("has_post_norms"):
+        P["pre_ffn_norm"] = (0.7 + 0.3 * rng.standard_normal(hidden)).astype(np.float32)
+        P["post_ffn_norm"] = (1.2 + 0.3 * rng.standard_normal(hidden)).astype(np.float32)
+    return P
+
+
+def _run_layer_case(P, dims, pos, seed):
+    hidden, inter, nq, nkv, hd = dims
+    rng = np.random.default_rng(seed)
+    kvd = nkv * hd
+    kc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
+    h = rng.standard_normal(hidden).astype(np.float32)
+    layer = {k: v for k, v in P.items() if k not in ("deq", "rope_base")}
+    layer["k_cache"], layer["v_cache"] = kc.copy(), vc.copy()
+    got = oracle.decode_layer(layer, h, pos, hidden, inter, nq, nkv, hd, P["rope_base"])
+    return got, (lambda mut=(): _ref_layer64(P, h, kc, vc, pos, dims, mut))
+
+
+def _rel(a, b):
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+def test_decode_layer_llama_matches_float64_composition():
+    """lo_decode_layer (Llama: pre-norm, SiLU, no post-norms) against the float64
+    restatement within 1e-5; each planted mistake moves the output by more than 1e-2."""
+    dims = (256, 512, 4, 2, 64)
+    P = _tiny_layer(31, dims, {"wv": "q6_k", "down": "q6_k"})
+    got, ref = _run_layer_case(P, dims, pos=5, seed=32)
+    assert _rel(got, ref()) <= 1e-5
+    for mut in ("swap_norms", "gate_up_swap", "drop_residual", "rope_v", "rope_exp", "kv_map"):
+        assert _rel(got, ref((mut,))) > 1e-2, mut
+
+
+def test_decode_layer_variants_match_float64_composition():
+    """Post-norms with pre/post-FFN weights, norm offset 1, GELU-tanh, V-norm, a layer scalar,
+    partial rotary and an explicit attention scale (a Gemma-style layer,
+    LC/src/pipeline.rs:76-115), then the same with the pre/post-FFN weights absent."""
+    dims = (256, 512, 4, 2, 64)
+    var = dict(has_post_norms=True, norm_offset=1.0, activation="gelu_tanh", has_v_norm=True,
+               layer_scalar=0.75, rotary_dim=32, attn_scale=0.2)
+    P = _tiny_layer(33, dims, {"wq": "q6_k"}, **var)
+    got, ref = _run_layer_case(P, dims, pos=3, seed=34)
+    assert _rel(got, ref()) <= 1e-5
+    for mut in ("swap_norms", "gate_up_swap", "rope_exp", "kv_map"):
+        assert _rel(got, ref((mut,))) > 1e-2, mut
+    # the same layer under SiLU, offset 0, no V-norm, no scalar is far away
+    for k, v in (("activation", "silu"), ("norm_offset", 0.0), ("has_v_norm", False), ("layer_scalar", 0.0)):
+        Q = dict(P, **{k: v})
+        assert _rel(got, _ref_layer64(Q, *_inputs_of(P, dims, 3, 34))) > 1e-2, k
+    P2 = dict(P, pre_ffn_norm=None, post_ffn_norm=None)
+    got2, ref2 = _run_layer_case(P2, dims, pos=3, seed=34)
+    assert _rel(got2, ref2()) <= 1e-5 and _rel(got2, got) > 1e-2
+
+
+def _inputs_of(P, dims, pos, seed):
+    hidden, inter, nq, nkv, hd = dims
+    rng = np.random.default_rng(seed)
+    kvd = nkv * hd
+    kc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
+    h = rng.standard_normal(hidden).astype(np.float32)
+    return h, kc, vc, pos, dims
