@@ -29,6 +29,15 @@ struct LayerDev {
     bool split_qkv = false, split_gu = false;
     float* input_norm = nullptr;
     float* post_attn_norm = nullptr;
+    // layer variants (LC/src/pipeline.rs:76-115): post-norm layers norm the attention and
+    // FFN outputs before their residual adds and the FFN input with pre_ffn_norm (null
+    // vectors: the weight-free norm)
+    float* pre_ffn_norm = nullptr;
+    float* post_ffn_norm = nullptr;
+    float norm_offset = 0.f;
+    float layer_scalar = 0.f;  // 0 = disabled
+    bool post_norms = false, v_norm = false;
+    int act = LARQL_ACT_SILU;
     double eps = 1e-6;
     float attn_scale = 0.f;
     double rope_base = 10000.0;
@@ -43,11 +52,14 @@ struct larql_hip_model {
     DevWeight head;
     float* final_norm = nullptr;
     double final_eps = 1e-6;
+    float final_offset = 0.f;
     size_t vocab = 0;
     std::vector<void*> allocs;
     // workspace
     float *h0 = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *xin = nullptr;
     float* gtmp = nullptr;  // gate projection when gate and up have different formats
+    float* otmp = nullptr;  // post-norm layers: attention / FFN output before its norm
+    float* ones = nullptr;  // weight of the weight-free norm in a fused matvec prologue
     larql::DeviceBuf part;
     larql::DeviceBuf prompt;  // batched prompt pass: activations of all positions
     // host-pointer decode_token cache key
@@ -119,18 +131,20 @@ float* upload_vec(larql_hip_ctx* c, larql_hip_model* m, const float* v, size_t n
     return d;
 }
 
-// The HIP decode step implements the Llama layer; everything else is reported as
-// unsupported so callers fall back (LI/src/layer_graph/predict.rs:397-430).
+// The HIP decode step implements RMSNorm layers with a gated FFN (SiLU or GELU-tanh), with
+// or without post-norms, norm weight offsets, V-norm and a layer scalar; LayerNorm, the
+// ungated FFN and biases are reported as unsupported so callers fall back
+// (LI/src/layer_graph/predict.rs:397-430).  Run on every call, whether or not the layers
+// match a cached model.
 void check_supported(const larql_pipeline_layer& L) {
     if (L.norm_type != LARQL_NORM_RMS) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: LayerNorm layers not supported");
     if (L.ffn_type != LARQL_FFN_GATED) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: non-gated FFN not supported");
-    if (L.activation != LARQL_ACT_SILU) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: only SiLU FFN supported");
-    if (L.has_post_norms || L.pre_ffn_norm || L.post_ffn_norm)
-        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: post-norm layers not supported");
+    if (L.activation != LARQL_ACT_SILU && L.activation != LARQL_ACT_GELU_TANH)
+        fail(LARQL_HIP_ERR_INVALID, "decode: unknown activation");
     if (L.input_norm_bias || L.post_attn_norm_bias || L.ffn_up_bias || L.ffn_down_bias)
         fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: biases not supported");
-    if (L.has_v_norm) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: V-norm not supported");
-    if (L.layer_scalar != 0.0f) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: layer scalar not supported");
+    if (!std::isfinite(L.norm_offset) || !std::isfinite(L.layer_scalar))
+        fail(LARQL_HIP_ERR_INVALID, "decode: non-finite norm offset or layer scalar");
 }
 
 larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t n, size_t hidden,
@@ -189,6 +203,15 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
             d.down = build_weight(c, m, L.down.format, inter, {{L.down.data, L.down.len, hidden}}, false, on_device);
             d.input_norm = upload_vec(c, m, L.input_norm, hidden, on_device);
             d.post_attn_norm = upload_vec(c, m, L.post_attn_norm, hidden, on_device);
+            d.norm_offset = L.norm_offset;
+            d.layer_scalar = L.layer_scalar;
+            d.post_norms = L.has_post_norms != 0;
+            d.v_norm = L.has_v_norm != 0;
+            d.act = L.activation;
+            if (d.post_norms) {
+                if (L.pre_ffn_norm) d.pre_ffn_norm = upload_vec(c, m, L.pre_ffn_norm, hidden, on_device);
+                if (L.post_ffn_norm) d.post_ffn_norm = upload_vec(c, m, L.post_ffn_norm, hidden, on_device);
+            }
             m->layers.push_back(d);
         }
         m->q_dim = static_cast<size_t>(m->nq) * m->hd;
@@ -200,6 +223,12 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
         m->attn = static_cast<float*>(dev_alloc(m, m->q_dim * 4));
         m->act = static_cast<float*>(dev_alloc(m, inter * 4));
         m->gtmp = static_cast<float*>(dev_alloc(m, inter * 4));
+        m->otmp = static_cast<float*>(dev_alloc(m, hidden * 4));
+        {
+            std::vector<float> one(hidden, 1.0f);
+            m->ones = static_cast<float*>(dev_alloc(m, hidden * 4));
+            LARQL_HIP_CHECK(hipMemcpy(m->ones, one.data(), hidden * 4, hipMemcpyHostToDevice));
+        }
         LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
     } catch (...) {
         for (void* p : m->allocs) (void)hipFree(p);
@@ -311,6 +340,7 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
         a.x = m->h0;
         a.out = m->qkv;
         a.norm_w = L.input_norm;
+        a.norm_offset = L.norm_offset;
         a.eps = L.eps;
         if (L.split_qkv) {  // three launches into the [q | k | v] buffer, each with the norm
             larql::launch_mv(L.wq, a, s);
@@ -321,6 +351,7 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
         } else {
             larql::launch_mv(L.qkv, a, s);
         }
+        if (L.v_norm) larql::launch_vnorm_rows(m->qkv + m->q_dim + m->kv_dim, 1, 0, L.nkv, L.hd, L.eps, s);
 
         larql::AttnArgs at{};
         at.qkv = m->qkv;
@@ -338,36 +369,60 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
         at.rope = rope_table(c, L.rope_base, L.rdim, s);
         larql::launch_attention(at, s);
 
+        // h1 = h + o (Llama), or h + norm(o, post_attn_norm) for post-norm layers
         larql::MvArgs o;
         o.x = m->attn;
-        o.out = m->h1;
-        o.epi = larql::EPI_RESID;
-        o.resid = m->h0;
-        larql::launch_mv(L.wo, o, s);
+        if (L.post_norms) {
+            o.out = m->otmp;
+            larql::launch_mv(L.wo, o, s);
+            larql::launch_resid_norm_rows(m->h0, m->otmp, L.post_attn_norm, L.norm_offset, 1.0f, m->h1, 1, m->hidden,
+                                          L.eps, s);
+        } else {
+            o.out = m->h1;
+            o.epi = larql::EPI_RESID;
+            o.resid = m->h0;
+            larql::launch_mv(L.wo, o, s);
+        }
 
         larql::MvArgs g;
         g.x = m->h1;
         g.out = m->act;
-        g.norm_w = L.post_attn_norm;
+        g.act = L.act;
         g.eps = L.eps;
-        if (L.split_gu) {  // gate, then up with silu(gate) * up in its epilogue
+        g.norm_w = L.post_attn_norm;
+        g.norm_offset = L.norm_offset;
+        if (L.post_norms) {  // FFN input: norm(h1, pre_ffn_norm), weight-free when absent
+            g.norm_w = L.pre_ffn_norm ? L.pre_ffn_norm : m->ones;
+            g.norm_offset = L.pre_ffn_norm ? L.norm_offset : 0.0f;
+        }
+        if (L.split_gu) {  // gate, then up with act(gate) * up in its epilogue
             g.out = m->gtmp;
             larql::launch_mv(L.gate, g, s);
             g.out = m->act;
-            g.epi = larql::EPI_SILU_MUL;
+            g.epi = larql::EPI_GATED_MUL;
             g.resid = m->gtmp;
             larql::launch_mv(L.up, g, s);
         } else {
-            g.epi = larql::EPI_SILU_PAIR;
+            g.epi = larql::EPI_GATED_PAIR;
             larql::launch_mv(L.gateup, g, s);
         }
 
+        // h2 = (h1 + down) or (h1 + norm(down, post_ffn_norm)), times the layer scalar
+        const float scale = L.layer_scalar != 0.0f ? L.layer_scalar : 1.0f;
         larql::MvArgs d;
         d.x = m->act;
-        d.out = m->h0;
-        d.epi = larql::EPI_RESID;
-        d.resid = m->h1;
-        larql::launch_mv(L.down, d, s);
+        if (L.post_norms) {
+            d.out = m->otmp;
+            larql::launch_mv(L.down, d, s);
+            larql::launch_resid_norm_rows(m->h1, m->otmp, L.post_ffn_norm, L.post_ffn_norm ? L.norm_offset : 0.0f,
+                                          scale, m->h0, 1, m->hidden, L.eps, s);
+        } else {
+            d.out = m->h0;
+            d.epi = larql::EPI_RESID;
+            d.resid = m->h1;
+            d.out_scale = scale;
+            larql::launch_mv(L.down, d, s);
+        }
     }
     kv.current_len = static_cast<size_t>(T);
     if (hidden_out) larql::launch_copy_f32(m->h0, hidden_out, m->hidden, s);
@@ -377,13 +432,26 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
         e.x = m->h0;
         e.out = logits;
         e.norm_w = m->final_norm;
+        e.norm_offset = m->final_offset;
         e.eps = m->final_eps;
         larql::launch_mv(m->head, e, s);
     }
 }
 
+uint64_t f32_bits(float v) {
+    uint32_t b;
+    std::memcpy(&b, &v, 4);
+    return b;
+}
+
+// Cache key of a trait-call model: every field of every layer that build_model reads
+// (weights and norm vectors by pointer, length and sampled content; the scalars by value).
 std::vector<uint64_t> layers_key(const larql_pipeline_layer* layers, size_t n, size_t hidden, size_t inter) {
     std::vector<uint64_t> k{n, hidden, inter};
+    auto vec = [&](const float* v) {
+        k.push_back(reinterpret_cast<uint64_t>(v));
+        k.push_back(v ? larql::host_fingerprint(v, hidden * 4) : 0);
+    };
     for (size_t l = 0; l < n; l++) {
         const larql_pipeline_layer& L = layers[l];
         for (const larql_quant_weight* w : {&L.wq, &L.wk, &L.wv, &L.wo, &L.gate, &L.up, &L.down}) {
@@ -392,19 +460,34 @@ std::vector<uint64_t> layers_key(const larql_pipeline_layer* layers, size_t n, s
             k.push_back(static_cast<uint64_t>(w->format));
             k.push_back(w->data ? larql::host_fingerprint(w->data, w->len) : 0);
         }
-        k.push_back(reinterpret_cast<uint64_t>(L.input_norm));
-        k.push_back(reinterpret_cast<uint64_t>(L.post_attn_norm));
-        k.push_back(L.input_norm ? larql::host_fingerprint(L.input_norm, hidden * 4) : 0);
-        k.push_back(L.post_attn_norm ? larql::host_fingerprint(L.post_attn_norm, hidden * 4) : 0);
-        uint32_t bits[3];
-        std::memcpy(&bits[0], &L.eps, 4);
-        std::memcpy(&bits[1], &L.rope_base, 4);
-        std::memcpy(&bits[2], &L.attn_scale, 4);
-        k.push_back((static_cast<uint64_t>(bits[0]) << 32) | bits[1]);
-        k.push_back((static_cast<uint64_t>(bits[2]) << 32) | (L.head_dim << 16) | (L.num_q_heads << 8) | L.num_kv_heads);
+        vec(L.input_norm);
+        vec(L.post_attn_norm);
+        vec(L.has_post_norms ? L.pre_ffn_norm : nullptr);
+        vec(L.has_post_norms ? L.post_ffn_norm : nullptr);
+        k.push_back((f32_bits(L.eps) << 32) | f32_bits(L.rope_base));
+        k.push_back((f32_bits(L.attn_scale) << 32) | f32_bits(L.norm_offset));
+        k.push_back((f32_bits(L.layer_scalar) << 32) | (static_cast<uint64_t>(L.activation & 0xFF) << 16) |
+                    (static_cast<uint64_t>(L.has_post_norms != 0) << 8) | static_cast<uint64_t>(L.has_v_norm != 0));
+        k.push_back((static_cast<uint64_t>(L.head_dim) << 32) | (L.num_q_heads << 16) | L.num_kv_heads);
         k.push_back((static_cast<uint64_t>(L.rotary_dim) << 32) | L.sliding_window);
     }
     return k;
+}
+
+// The trait calls' model: rebuilt when the layers' key differs from the cached one.
+larql_hip_model* trait_model_for(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t n, size_t hidden,
+                                 size_t inter) {
+    if (!layers || n == 0) fail(LARQL_HIP_ERR_INVALID, "decode: no layers");
+    for (size_t l = 0; l < n; l++) check_supported(layers[l]);
+    auto key = layers_key(layers, n, hidden, inter);
+    larql_hip_model*& m = c->trait_model;
+    if (!m || m->key != key) {
+        destroy_model(c, m);
+        m = nullptr;
+        m = build_model(c, layers, n, hidden, inter, false);
+        m->key = key;
+    }
+    return m;
 }
 
 }  // namespace
@@ -418,14 +501,7 @@ extern "C" int larql_hip_decode_token(larql_hip_ctx* c, const larql_pipeline_lay
         if (num_q_heads * head_dim != q_dim || num_kv_heads * head_dim != kv_dim)
             fail(LARQL_HIP_ERR_INVALID, "decode_token: q_dim/kv_dim do not match the head geometry");
         (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
-        auto key = layers_key(layers, num_layers, hidden, inter);
-        larql_hip_model*& m = c->trait_model;  // model of the last host-pointer decode_token
-        if (!m || m->key != key) {
-            destroy_model(c, m);
-            m = nullptr;
-            m = build_model(c, layers, num_layers, hidden, inter, false);
-            m->key = key;
-        }
+        larql_hip_model* m = trait_model_for(c, layers, num_layers, hidden, inter);
         if (m->q_dim != q_dim || m->kv_dim != kv_dim)
             fail(LARQL_HIP_ERR_INVALID, "decode_token: layer geometry differs from q_dim/kv_dim");
         LARQL_HIP_CHECK(hipMemcpyAsync(m->xin, x, hidden * sizeof(float), hipMemcpyHostToDevice, c->stream));
@@ -476,7 +552,7 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
     larql::launch_copy_f32(dx, H0, M * hidden, s);
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
-        larql::launch_rmsnorm_rows(H0, L.input_norm, XN, M, hidden, L.eps, s);
+        larql::launch_rmsnorm_rows(H0, L.input_norm, L.norm_offset, XN, M, hidden, L.eps, s);
         if (L.split_qkv) {  // Q, K, V into their column ranges of the [q | k | v] rows
             prompt_proj(L.wq, XN, hidden, QKV, ld, M, SPL, split_n, s);
             prompt_proj(L.wk, XN, hidden, QKV + qd, ld, M, SPL, split_n, s);
@@ -484,6 +560,7 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
         } else {
             prompt_proj(L.qkv, XN, hidden, QKV, ld, M, SPL, split_n, s);
         }
+        if (L.v_norm) larql::launch_vnorm_rows(QKV + qd + kvd, M, ld, L.nkv, L.hd, L.eps, s);
         const float2* rope = rope_table(c, L.rope_base, L.rdim, s);
         larql::launch_rope_kv_rows(QKV, M, 0, qd, kvd, L.hd, L.rdim, rope, kv.k[l], kv.v[l], L.nkv, s);
         larql::AttnArgs at{};
@@ -504,12 +581,21 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
         at.qkv_ld = static_cast<int>(ld);
         larql::launch_attention(at, s);
         prompt_proj(L.wo, ATT, qd, G, hidden, M, SPL, split_n, s);
-        larql::launch_add_rows(H0, G, H1, M * hidden, s);
-        larql::launch_rmsnorm_rows(H1, L.post_attn_norm, XN, M, hidden, L.eps, s);
+        if (L.post_norms) {
+            larql::launch_resid_norm_rows(H0, G, L.post_attn_norm, L.norm_offset, 1.0f, H1, M, hidden, L.eps, s);
+            larql::launch_rmsnorm_rows(H1, L.pre_ffn_norm, L.norm_offset, XN, M, hidden, L.eps, s);
+        } else {
+            larql::launch_add_rows(H0, G, H1, M * hidden, s);
+            larql::launch_rmsnorm_rows(H1, L.post_attn_norm, L.norm_offset, XN, M, hidden, L.eps, s);
+        }
         prompt_proj(L.gateup, XN, hidden, G, 2 * inter, M, SPL, split_n, s);
-        larql::launch_silu_pair_rows(G, ACT, M * inter, s);
+        larql::launch_gated_pair_rows(G, ACT, M * inter, L.act, s);
         prompt_proj(L.down, ACT, inter, G, hidden, M, SPL, split_n, s);
-        larql::launch_add_rows(H1, G, H0, M * hidden, s);
+        const float scale = L.layer_scalar != 0.0f ? L.layer_scalar : 1.0f;
+        if (L.post_norms)
+            larql::launch_resid_norm_rows(H1, G, L.post_ffn_norm, L.norm_offset, scale, H0, M, hidden, L.eps, s);
+        else
+            larql::launch_add_rows(H1, G, H0, M * hidden, s, scale);
     }
     larql::launch_copy_f32(H0, dout, M * hidden, s);
     kv.current_len = M;
@@ -526,14 +612,7 @@ extern "C" int larql_hip_prefill_q4(larql_hip_ctx* c, const larql_pipeline_layer
             fail(LARQL_HIP_ERR_INVALID, "prefill: q_dim/kv_dim do not match the head geometry");
         (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
         if (seq_len == 0) return;
-        auto key = layers_key(layers, num_layers, hidden, inter);
-        larql_hip_model*& m = c->trait_model;
-        if (!m || m->key != key) {
-            destroy_model(c, m);
-            m = nullptr;
-            m = build_model(c, layers, num_layers, hidden, inter, false);
-            m->key = key;
-        }
+        larql_hip_model* m = trait_model_for(c, layers, num_layers, hidden, inter);
         if (m->q_dim != q_dim || m->kv_dim != kv_dim)
             fail(LARQL_HIP_ERR_INVALID, "prefill: layer geometry differs from q_dim/kv_dim");
         kv_ensure(c, m->layers.size(), m->nkv, m->hd, seq_len);

@@ -60,9 +60,10 @@ void run_scores(larql_hip_ctx* c, const KnnPlan& p, size_t n_layers, const float
     }
 }
 
-void check_k(size_t k, int F) {
-    if (k < 1 || k > static_cast<size_t>(larql::kTopkMaxK) || k > static_cast<size_t>(F))
-        fail(LARQL_HIP_ERR_INVALID, "gate KNN: need 1 <= top_k <= min(features, 64)");
+// top_k above the row length is clamped by the kernels (top_k.min(len), LV/src/index/walk.rs:569).
+void check_k(size_t k) {
+    if (k < 1 || k > static_cast<size_t>(larql::kTopkMaxK))
+        fail(LARQL_HIP_ERR_INVALID, "gate KNN: need 1 <= top_k <= LARQL_HIP_TOPK_MAX");
 }
 
 }  // namespace
@@ -80,7 +81,7 @@ extern "C" int larql_hip_gate_knn_dev(larql_hip_ctx* c, const uint64_t* handles,
                                       void* stream) {
     return guarded(c, [&] {
         const KnnPlan p = plan_layers(c, handles, n_layers);
-        check_k(top_k, p.F);
+        check_k(top_k);
         if (!idx || !scores) fail(LARQL_HIP_ERR_INVALID, "gate KNN: null outputs");
         hipStream_t s = pick_stream(c, stream);
         float* S = static_cast<float*>(larql::ensure(c, c->knn_scores, n_layers * nq * p.F * sizeof(float)));
@@ -94,8 +95,8 @@ extern "C" int larql_hip_topk_dev(larql_hip_ctx* c, const float* scores, size_t 
     return guarded(c, [&] {
         if (!scores || !idx || !vals) fail(LARQL_HIP_ERR_INVALID, "top-k: null pointer");
         if (n == 0 || n > 0x7FFFFFFF) fail(LARQL_HIP_ERR_INVALID, "top-k: bad row length");
-        if (k < 1 || k > static_cast<size_t>(larql::kTopkMaxK) || k > n)
-            fail(LARQL_HIP_ERR_INVALID, "top-k: need 1 <= k <= min(n, 64)");
+        if (k < 1 || k > static_cast<size_t>(larql::kTopkMaxK))
+            fail(LARQL_HIP_ERR_INVALID, "top-k: need 1 <= k <= LARQL_HIP_TOPK_MAX");
         larql::launch_topk(scores, rows, n, static_cast<int>(n), static_cast<int>(k), signed_mode ? 1 : 0, idx, vals,
                            pick_stream(c, stream));
     });
@@ -111,7 +112,7 @@ extern "C" int larql_hip_gate_knn(larql_hip_ctx* c, int format, const void* gate
         const DevWeight& w = larql::cached_weight(c, format, gate, gate_len, nullptr, features, hidden);
         const uint64_t h = w.handle;
         const KnnPlan p = plan_layers(c, &h, 1);
-        check_k(top_k, p.F);
+        check_k(top_k);
         const size_t qbytes = nq * hidden * sizeof(float);
         float* dq = static_cast<float*>(larql::ensure(c, c->stage_in, qbytes));
         LARQL_HIP_CHECK(hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, c->stream));
@@ -127,20 +128,37 @@ extern "C" int larql_hip_gate_knn(larql_hip_ctx* c, int format, const void* gate
 }
 
 // lm-head KNN (LV/src/index/walk.rs:549-583): quantize_to_q8 of each query, the Q4_0
-// matvec over the vocab, then the signed top-k, all on the device.
-static void run_lm_head_knn(larql_hip_ctx* c, const DevWeight& w, const float* dq, size_t nq, size_t top_k,
-                            uint32_t* di, float* dv, hipStream_t s) {
+// matvec over the vocab, then the signed top-k, all on the device.  Work buffers: q8
+// [nq][hidden], q8s [nq][hidden / 32], scores S [nq][vocab].
+struct LmHeadBufs {
+    int8_t* q8;
+    float* q8s;
+    float* S;
+};
+
+static void check_lm_head(const DevWeight& w, size_t nq, size_t top_k) {
     if (w.format != LARQL_Q4_0) fail(LARQL_HIP_ERR_UNSUPPORTED, "lm-head KNN: the head must be Q4_0");
     if (nq == 0) fail(LARQL_HIP_ERR_INVALID, "lm-head KNN: nq == 0");
     if (w.rows > 0x7FFFFFFF) fail(LARQL_HIP_ERR_UNSUPPORTED, "lm-head KNN: vocab too large");
-    check_k(top_k, static_cast<int>(w.rows));
+    check_k(top_k);
+}
+
+static void launch_lm_head_knn(const DevWeight& w, const float* dq, size_t nq, size_t top_k, const LmHeadBufs& b,
+                               uint32_t* di, float* dv, hipStream_t s) {
+    larql::launch_quantize_q8(dq, w.cols, nq, b.q8, b.q8s, s);
+    larql::launch_q4_0_matvec(w, b.q8, b.q8s, b.S, nq, s);
+    larql::launch_topk(b.S, nq, w.rows, static_cast<int>(w.rows), static_cast<int>(top_k), 1, di, dv, s);
+}
+
+static void run_lm_head_knn(larql_hip_ctx* c, const DevWeight& w, const float* dq, size_t nq, size_t top_k,
+                            uint32_t* di, float* dv, hipStream_t s) {
+    check_lm_head(w, nq, top_k);
     const size_t hidden = w.cols, nb = hidden / 32;
-    int8_t* q8 = static_cast<int8_t*>(larql::ensure(c, c->knn_q8, nq * hidden));
-    float* q8s = static_cast<float*>(larql::ensure(c, c->knn_q8s, nq * nb * sizeof(float)));
-    larql::launch_quantize_q8(dq, hidden, nq, q8, q8s, s);
-    float* S = static_cast<float*>(larql::ensure(c, c->knn_scores, nq * w.rows * sizeof(float)));
-    larql::launch_q4_0_matvec(w, q8, q8s, S, nq, s);
-    larql::launch_topk(S, nq, w.rows, static_cast<int>(w.rows), static_cast<int>(top_k), 1, di, dv, s);
+    LmHeadBufs b;
+    b.q8 = static_cast<int8_t*>(larql::ensure(c, c->knn_q8, nq * hidden));
+    b.q8s = static_cast<float*>(larql::ensure(c, c->knn_q8s, nq * nb * sizeof(float)));
+    b.S = static_cast<float*>(larql::ensure(c, c->knn_scores, nq * w.rows * sizeof(float)));
+    launch_lm_head_knn(w, dq, nq, top_k, b, di, dv, s);
 }
 
 extern "C" int larql_hip_lm_head_knn(larql_hip_ctx* c, const uint8_t* lm_head_q4, size_t len, const float* query,
@@ -166,3 +184,4 @@ extern "C" int larql_hip_lm_head_knn_dev(larql_hip_ctx* c, uint64_t handle, cons
         run_lm_head_knn(c, w, queries, nq, top_k, idx, scores, pick_stream(c, stream));
     });
 }
+

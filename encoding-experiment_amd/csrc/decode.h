@@ -37,11 +37,19 @@ bool attn_supported(int reps, int hd);
 void launch_v_to_cache(const void* src, bool src_f32, __half* dst, size_t seq, int num_kv, int hd, hipStream_t s);
 void launch_copy_f32(const float* src, float* dst, size_t n, hipStream_t s);
 // Row kernels of the batched prompt pass (prompt.hip).
-void launch_rmsnorm_rows(const float* X, const float* w, float* Y, size_t m, size_t n, double eps, hipStream_t s);
+// y = x / rms * (off + w) per row of n floats (w null: no weight).
+void launch_rmsnorm_rows(const float* X, const float* w, float off, float* Y, size_t m, size_t n, double eps,
+                         hipStream_t s);
+// out = (h + v / rms(v) * (off + w)) * scale per row (the post-norm residual).
+void launch_resid_norm_rows(const float* H, const float* V, const float* w, float off, float scale, float* out,
+                            size_t m, size_t n, double eps, hipStream_t s);
+// Parameter-free RMS norm of num_heads heads of hd floats, in place, in each of m rows ld apart.
+void launch_vnorm_rows(float* X, size_t m, size_t ld, int num_heads, int hd, double eps, hipStream_t s);
 void launch_rope_kv_rows(const float* QKV, size_t m, size_t p0, size_t q_dim, size_t kv_dim, int hd, int rdim,
                          const float2* rope, __half* kc, __half* vc, int num_kv, hipStream_t s);
-void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipStream_t s);
-void launch_silu_pair_rows(const float* GU, float* act, size_t n, hipStream_t s);
+void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipStream_t s, float scale = 1.0f);
+// act[i] = act(GU[2i]) * GU[2i + 1]; kind 0 = SiLU, 1 = GELU-tanh.
+void launch_gated_pair_rows(const float* GU, float* act, size_t n, int kind, hipStream_t s);
 void launch_f32_to_f16(const float* src, __half* dst, size_t n, hipStream_t s);
 
 }  // namespace larql

@@ -22,7 +22,8 @@ void launch_gate_scores_q4(const KnnLayers& nibbles, const KnnLayers& scales, in
                            const float* XS, uint4* XA, float* XSP, float* S, int F, int K, int Q, hipStream_t s);
 size_t q4_xa_bytes(int K, int Q);
 size_t q4_xsp_bytes(int K, int Q);
-// Top-k of `rows` rows of n scores (row stride row_stride floats).
+// Top-k of `rows` rows of n scores (row stride row_stride floats), 1 <= k <= kTopkMaxK:
+// min(k, n) entries per output row of k slots, the rest index 0xFFFFFFFF and score 0.
 void launch_topk(const float* S, size_t rows, size_t row_stride, int n, int k, int signed_mode, uint32_t* idx,
                  float* val, hipStream_t s);
 

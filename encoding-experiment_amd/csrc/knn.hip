@@ -329,18 +329,22 @@ constexpr int kTopkCap = 2048;  // candidates kept in LDS
 // One workgroup per row.  Order: key descending, index ascending (the composite
 // key << 32 | (0xFFFFFFFF - index), unique per element).  T, the k-th largest of the 256
 // per-thread maximum keys, is a lower bound of the k-th largest key (k distinct threads
-// hold an element >= T), so the elements with key >= T are compacted into LDS (the
-// score magnitudes of a row share their top key bits: a select over every element would
-// spend its passes on them) and the exact select runs there: the k-th largest key K,
-// every element above it, then the elements equal to K in index order.  Rows whose
-// candidates overflow the LDS list run the select over all elements instead.
+// hold an element >= T; with k above the thread count T = 0), so the elements with
+// key >= T are compacted into LDS (the score magnitudes of a row share their top key
+// bits: a select over every element would spend its passes on them) and the exact select
+// runs there: the k-th largest key K, every element above it, then the elements equal to
+// K in index order — when more of them tie than are needed, a second select over their
+// indices finds the largest index kept, so ties cost linear time however many there are
+// (an all-zero row is one big tie).  Rows whose candidates overflow the LDS list run the
+// selects over all elements instead.  k <= n; the output rows are kstride apart and
+// slots k .. kstride - 1 receive index 0xFFFFFFFF and score 0.
 template <int PER>
 __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ S, size_t row_stride, int n, int k,
-                                                        int signed_mode, uint32_t* __restrict__ idx_out,
+                                                        int kstride, int signed_mode, uint32_t* __restrict__ idx_out,
                                                         float* __restrict__ val_out) {
     __shared__ uint32_t hist[kThreads / 64][256];
     __shared__ uint32_t sel[2];
-    __shared__ int cnt, nout;
+    __shared__ int cnt, nout, nties;
     __shared__ uint32_t ckey[kTopkCap], cidx[kTopkCap];
     __shared__ uint64_t out_c[kTopkMaxK];
     __shared__ float out_v[kTopkMaxK];
@@ -374,18 +378,25 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
     };
 
     // 1. T: the k-th largest per-thread maximum key (threads without elements do not vote)
-    uint32_t kmax = 0;
-    bool has = false;
-    each([&](uint32_t kk, int) __attribute__((always_inline)) {
-        kmax = max(kmax, kk);
-        has = true;
-    });
+    uint32_t T = 0;
     int above = 0;
-    const uint32_t T = select_kth32(
-        k, [&](auto visit) __attribute__((always_inline)) { if (has) visit(kmax); }, hist, sel, &above);
+    if (k <= kThreads) {
+        uint32_t kmax = 0;
+        bool has = false;
+        each([&](uint32_t kk, int) __attribute__((always_inline)) {
+            kmax = max(kmax, kk);
+            has = true;
+        });
+        T = select_kth32(
+            k, [&](auto visit) __attribute__((always_inline)) { if (has) visit(kmax); }, hist, sel, &above);
+    }
 
     // 2. candidates (key >= T) into LDS
-    if (tid == 0) cnt = 0;
+    if (tid == 0) {
+        cnt = 0;
+        nout = 0;
+        nties = 0;
+    }
     __syncthreads();
     each([&](uint32_t kk, int i) __attribute__((always_inline)) {
         if (kk >= T) {
@@ -399,57 +410,62 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
     __syncthreads();
     const int nc = cnt;
     const bool inlds = nc <= kTopkCap;
+    // g(key, index) over the candidates: the LDS list, or every element of the row
+    auto cands = [&](auto g) __attribute__((always_inline)) {
+        if (inlds) {
+            for (int p = tid; p < nc; p += kThreads) g(ckey[p], cidx[p]);
+        } else {
+            each([&](uint32_t kk, int i) __attribute__((always_inline)) { g(kk, static_cast<uint32_t>(i)); });
+        }
+    };
 
     // 3. K = the k-th largest key; `above` elements are strictly greater
-    const uint32_t K = inlds ? select_kth32(
-                                   k,
-                                   [&](auto visit) __attribute__((always_inline)) {
-                                       for (int p = tid; p < nc; p += kThreads) visit(ckey[p]);
-                                   },
-                                   hist, sel, &above)
-                             : select_kth32(
-                                   k,
-                                   [&](auto visit) __attribute__((always_inline)) {
-                                       each([&](uint32_t kk, int) __attribute__((always_inline)) { visit(kk); });
-                                   },
-                                   hist, sel, &above);
+    const uint32_t K = select_kth32(
+        k,
+        [&](auto visit) __attribute__((always_inline)) {
+            cands([&](uint32_t kk, uint32_t) __attribute__((always_inline)) { visit(kk); });
+        },
+        hist, sel, &above);
 
-    // 4. the k winners: every key > K, then the (k - above) lowest indices with key == K
-    if (tid == 0) nout = 0;
+    // 4. the k winners: every key > K, then the (k - above) lowest indices with key == K.
+    // imax = the largest index kept among the ties (all of them when no more tie than needed).
+    const int need = k - above;
+    int mine = 0;
+    cands([&](uint32_t kk, uint32_t) __attribute__((always_inline)) { mine += kk == K; });
+    if (mine) atomicAdd(&nties, mine);
     __syncthreads();
-    auto consider = [&](uint32_t kk, uint32_t i) __attribute__((always_inline)) {
-        if (kk > K) {
+    uint32_t imax = 0xFFFFFFFFu;
+    if (nties > need) {
+        int above2 = 0;
+        const uint32_t r = select_kth32(
+            need,
+            [&](auto visit) __attribute__((always_inline)) {
+                cands([&](uint32_t kk, uint32_t i) __attribute__((always_inline)) {
+                    if (kk == K) visit(0xFFFFFFFFu - i);
+                });
+            },
+            hist, sel, &above2);
+        imax = 0xFFFFFFFFu - r;
+    }
+    cands([&](uint32_t kk, uint32_t i) __attribute__((always_inline)) {
+        if (kk > K || (kk == K && i <= imax)) {
             const int p = atomicAdd(&nout, 1);
             out_c[p] = (static_cast<uint64_t>(kk) << 32) | (0xFFFFFFFFu - i);
             out_v[p] = s[i];
-        } else if (kk == K) {
-            // rank among the ties by index; only the first (k - above) are kept
-            int r = 0;
-            if (inlds) {
-                for (int p = 0; p < nc; p++) r += (ckey[p] == K) & (cidx[p] < i);
-            } else {  // more than kTopkCap candidates: count over the row itself
-                for (int i2 = 0; i2 < static_cast<int>(i); i2++) r += order_key(s[i2], signed_mode) == K;
-            }
-            if (r < k - above) {
-                const int p = above + r;
-                out_c[p] = (static_cast<uint64_t>(kk) << 32) | (0xFFFFFFFFu - i);
-                out_v[p] = s[i];
-            }
         }
-    };
-    if (inlds) {
-        for (int p = tid; p < nc; p += kThreads) consider(ckey[p], cidx[p]);
-    } else {
-        each([&](uint32_t kk, int i) __attribute__((always_inline)) { consider(kk, static_cast<uint32_t>(i)); });
-    }
+    });
     __syncthreads();
-    if (tid < k) {
-        const uint64_t me = out_c[tid];
+    const size_t row0 = static_cast<size_t>(blockIdx.x) * kstride;
+    for (int p = tid; p < k; p += kThreads) {
+        const uint64_t me = out_c[p];
         int rank = 0;
         for (int j = 0; j < k; j++) rank += out_c[j] > me;
-        const size_t o = static_cast<size_t>(blockIdx.x) * k + rank;
-        idx_out[o] = 0xFFFFFFFFu - static_cast<uint32_t>(me & 0xFFFFFFFFu);
-        val_out[o] = out_v[tid];
+        idx_out[row0 + rank] = 0xFFFFFFFFu - static_cast<uint32_t>(me & 0xFFFFFFFFu);
+        val_out[row0 + rank] = out_v[p];
+    }
+    for (int p = k + tid; p < kstride; p += kThreads) {
+        idx_out[row0 + p] = 0xFFFFFFFFu;
+        val_out[row0 + p] = 0.0f;
     }
 }
 
@@ -480,11 +496,14 @@ size_t q4_xsp_bytes(int K, int Q) { return static_cast<size_t>(K / 64) * ((Q + 7
 
 void launch_topk(const float* S, size_t rows, size_t row_stride, int n, int k, int signed_mode, uint32_t* idx,
                  float* val, hipStream_t s) {
-    if (k < 1 || k > kTopkMaxK || k > n) fail(LARQL_HIP_ERR_INVALID, "top-k: need 1 <= k <= min(n, 64)");
+    if (k < 1 || k > kTopkMaxK || n < 1) fail(LARQL_HIP_ERR_INVALID, "top-k: need 1 <= k <= 512 and n >= 1");
     if (rows == 0) return;
+    const int ke = std::min(k, n);  // top_k.min(len), LV/src/index/walk.rs:569
     const dim3 grid(static_cast<unsigned>(rows));
-    if (n <= kThreads * 48) topk_kernel<48><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, k, signed_mode, idx, val);
-    else topk_kernel<0><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, k, signed_mode, idx, val);
+    if (n <= kThreads * 48)
+        topk_kernel<48><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, k, signed_mode, idx, val);
+    else
+        topk_kernel<0><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, k, signed_mode, idx, val);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 

@@ -10,8 +10,8 @@ namespace larql {
 enum MvEpi : int {
     EPI_STORE = 0,      // out[n] = dot
     EPI_RESID = 1,      // out[n] = resid[n] + dot              (residual add, LI/src/forward/layer.rs:88-92)
-    EPI_SILU_PAIR = 2,  // rows interleaved gate/up: out[n/2] = silu(gate) * up  (LI/src/ffn/mod.rs:87-94)
-    EPI_SILU_MUL = 3,   // out[n] = silu(resid[n]) * dot: the up projection after a separate gate
+    EPI_GATED_PAIR = 2,  // rows interleaved gate/up: out[n/2] = act(gate) * up  (LI/src/ffn/mod.rs:87-103)
+    EPI_GATED_MUL = 3,   // out[n] = act(resid[n]) * dot: the up projection after a separate gate
 };
 
 struct MvArgs {
@@ -32,6 +32,8 @@ struct MvArgs {
     // epilogue
     int epi = EPI_STORE;
     const float* resid = nullptr;
+    int act = 0;             // gated epilogues: 0 = SiLU, 1 = GELU-tanh (Activation, LC/src/pipeline.rs:48-54)
+    float out_scale = 1.0f;  // EPI_RESID: (resid + dot) * out_scale, the layer scalar (LC/src/metal/decode.rs:717-728)
     // launch shape: waves per row slot, row tiles, tiles per workgroup, CUs on the device,
     // device rows (a multiple of 64; rows past `rows` decode to zero)
     int wpr = 1, tiles = 0, steps = 1, num_cus = 0, rows_pad = 0;
@@ -107,6 +109,17 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g * sig) * u;
 }
 
+// gelu_tanh(g) * u, gelu_tanh(x) = 0.5 x (1 + tanh(0.7978846 (x + 0.044715 x^3)))
+// (LI/src/ffn/mod.rs:96-103).
+__device__ __forceinline__ float gelu_tanh_mul(float g, float u) {
+    const float inner = 0.7978846f * (g + 0.044715f * g * g * g);
+    return (0.5f * g * (1.0f + tanhf(inner))) * u;
+}
+
+__device__ __forceinline__ float gated_act(int act, float g, float u) {
+    return act == 1 ? gelu_tanh_mul(g, u) : silu_mul(g, u);
+}
+
 // Sum over the wpr waves of one row slot through LDS (scratch of >= nwaves doubles).
 __device__ __forceinline__ double slot_sum_d(double v, double* scratch, int wave, int slot, int wpr, int lane) {
     v = wave_sum_d(v);
@@ -120,8 +133,8 @@ __device__ __forceinline__ double slot_sum_d(double v, double* scratch, int wave
 
 // Output of a non-pair epilogue for a row whose dot is `tot` and resid value `rv`.
 __device__ __forceinline__ float epi_value(const MvArgs& a, float rv, float tot) {
-    if (a.epi == EPI_RESID) return rv + tot;
-    if (a.epi == EPI_SILU_MUL) return silu_mul(rv, tot);
+    if (a.epi == EPI_RESID) return (rv + tot) * a.out_scale;
+    if (a.epi == EPI_GATED_MUL) return gated_act(a.act, rv, tot);
     return tot;
 }
 
@@ -133,9 +146,9 @@ __device__ __forceinline__ void epilogue_wave(const MvArgs& a, float tot, int la
     const int r = lane >> rsh;
     const bool owner = (lane & ((1 << rsh) - 1)) == 0;
     const int row = row0 + r;
-    if (a.epi == EPI_SILU_PAIR) {
+    if (a.epi == EPI_GATED_PAIR) {
         const float up = __shfl_down(tot, 1 << rsh, 64);
-        if (owner && (r & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
+        if (owner && (r & 1) == 0 && row < a.rows) a.out[row >> 1] = gated_act(a.act, tot, up);
     } else if (owner && row < a.rows) {
         a.out[row] = epi_value(a, a.epi == EPI_STORE ? 0.f : a.resid[row], tot);
     }
@@ -144,9 +157,9 @@ __device__ __forceinline__ void epilogue_wave(const MvArgs& a, float tot, int la
 // Epilogue when lanes 0..RB-1 hold rows row0 + lane (multi-wave slots).
 __device__ __forceinline__ void epilogue_lanes(const MvArgs& a, float tot, int lane, int row0, int rb) {
     const int row = row0 + lane;
-    if (a.epi == EPI_SILU_PAIR) {
+    if (a.epi == EPI_GATED_PAIR) {
         const float up = __shfl_down(tot, 1, 64);
-        if (lane < rb && (lane & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
+        if (lane < rb && (lane & 1) == 0 && row < a.rows) a.out[row >> 1] = gated_act(a.act, tot, up);
     } else if (lane < rb && row < a.rows) {
         a.out[row] = epi_value(a, a.epi == EPI_STORE ? 0.f : a.resid[row], tot);
     }

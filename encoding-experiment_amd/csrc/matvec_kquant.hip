@@ -212,7 +212,7 @@ void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s) {
     if (stream_mv_supported(w)) return launch_mv_stream(w, a, s);
     a.rows = static_cast<int>(w.rows);
     a.cols = static_cast<int>(w.cols);
-    if (a.epi == EPI_SILU_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "silu pair epilogue needs even rows");
+    if (a.epi == EPI_GATED_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "gated pair epilogue needs even rows");
     const size_t nsub = w.cols / 32;
     const size_t waves1 = (nsub + 63) / 64;
     if (waves1 <= 8) {

@@ -292,9 +292,9 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
         float tot = red[lane];
         for (int w = 1; w < KS; w++) tot += red[w * 16 * T + lane];
         const int row = static_cast<int>(tile0 * 16) + lane;
-        if (a.epi == EPI_SILU_PAIR) {
+        if (a.epi == EPI_GATED_PAIR) {
             const float up = __shfl_down(tot, 1, 64);  // rows 2i, 2i + 1 sit in adjacent lanes of one tile
-            if ((lane & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
+            if ((lane & 1) == 0 && row < a.rows) a.out[row >> 1] = gated_act(a.act, tot, up);
         } else if (row < a.rows) {
             a.out[row] = epi_value(a, a.epi == EPI_STORE ? 0.f : a.resid[row], tot);
         }
@@ -329,7 +329,7 @@ void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s) {
     a.rows_pad = static_cast<int>(w.rows_pad);
     a.qs = w.qs;
     a.hdr = w.hdr;
-    if (a.epi == EPI_SILU_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "silu pair epilogue needs even rows");
+    if (a.epi == EPI_GATED_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "gated pair epilogue needs even rows");
     // Measured (MI355X, 256 CUs, 16 rotating weight copies): [14336 x 4096] 7.5 us with
     // two super-blocks per round and four tiles per workgroup (7.7 with 4 x 2, 8.1 with
     // 4 x 1); [28672 x 4096] 12.8 us, [4096 x 14336] 8.0 us, [6144 x 4096] 4.8 us and

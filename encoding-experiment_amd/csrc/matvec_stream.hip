@@ -74,9 +74,9 @@ __device__ __forceinline__ void epilogue_rv(const MvArgs& a, float tot, float rv
     const int r = lane >> rsh;
     const bool owner = (lane & ((1 << rsh) - 1)) == 0;
     const int row = row0 + r;
-    if (a.epi == EPI_SILU_PAIR) {
+    if (a.epi == EPI_GATED_PAIR) {
         const float up = __shfl_down(tot, 1 << rsh, 64);
-        if (owner && (r & 1) == 0 && row < a.rows) a.out[row >> 1] = silu_mul(tot, up);
+        if (owner && (r & 1) == 0 && row < a.rows) a.out[row >> 1] = gated_act(a.act, tot, up);
     } else if (owner && row < a.rows) {
         a.out[row] = epi_value(a, rv, tot);
     }
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
     // flight over the whole GPU then cover one contiguous window of the weights, which
     // HBM serves far better than one separate stream per wave (measured: 33 MB in
     // ~7 us instead of ~9 us at the same depth).
-    const int pairs = (RB == 1 && a.epi == EPI_SILU_PAIR) ? 2 : 1;
+    const int pairs = (RB == 1 && a.epi == EPI_GATED_PAIR) ? 2 : 1;
     const int NSG = a.rows_pad / (RB * pairs);
     const int nsg = gw < NSG ? (NSG - gw + W - 1) / W : 0;
     const int U = nsg * pairs * npass;
@@ -287,9 +287,9 @@ __global__ __launch_bounds__(NT, OCC) void kq_stream_kernel(MvArgs a) {
             const float tot = multi_row_reduce<RB>(acc, lane);
             if constexpr (RB == 1) {
                 // single-row groups: the gate row's total waits in a register for its up row
-                if (a.epi == EPI_SILU_PAIR) {
+                if (a.epi == EPI_GATED_PAIR) {
                     if ((cg & 1) == 0) gate_tot = tot;
-                    else if (lane == 0 && cg < a.rows) a.out[cg >> 1] = silu_mul(gate_tot, tot);
+                    else if (lane == 0 && cg < a.rows) a.out[cg >> 1] = gated_act(a.act, gate_tot, tot);
                 } else {
                     epilogue_rv<1>(a, tot, B.rs, lane, cg);
                 }
@@ -360,7 +360,7 @@ void launch_mv_stream(const DevWeight& w, MvArgs a, hipStream_t s) {
     a.rows = static_cast<int>(w.rows);
     a.cols = static_cast<int>(w.cols);
     a.rows_pad = static_cast<int>(w.rows_pad);
-    if (a.epi == EPI_SILU_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "silu pair epilogue needs even rows");
+    if (a.epi == EPI_GATED_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "gated pair epilogue needs even rows");
     a.qs = w.qs;
     a.qh = w.qh;
     a.sc = w.sc;

@@ -6,8 +6,13 @@
 //     to f32, y = (x * (1 / rms)) * w — the fused-norm prologue of the matvecs;
 //   * RoPE of K (LI/src/attention/rope.rs:22-55) with the cos/sin table, K and V rounded
 //     to fp16 (RNE) into the cache rows of their positions;
-//   * residual add (LI/src/forward/layer.rs:88-92) and silu(gate) * up
-//     (LI/src/ffn/mod.rs:87-94) over gate/up rows interleaved as the fused weight emits them.
+//   * residual add (LI/src/forward/layer.rs:88-92) and act(gate) * up
+//     (LI/src/ffn/mod.rs:87-103) over gate/up rows interleaved as the fused weight emits them;
+//   * the layer variants of FullPipelineLayer (LC/src/pipeline.rs:76-115): norm weight
+//     offset, the post-norm residual h + norm(v) (LI/src/attention/block.rs:139-150,
+//     LI/src/forward/layer.rs:76-87), the parameter-free per-head V-norm
+//     (LI/src/residual.rs:86-110) and the layer scalar.  These kernels also serve the
+//     decode step (one row).
 #include "decode.h"
 #include "matvec_common.h"
 
@@ -15,21 +20,56 @@ namespace larql {
 
 namespace {
 
-// Grid M rows; 256 threads.
-__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ X, const float* __restrict__ w,
-                                                           float* __restrict__ Y, int n, double eps) {
-    __shared__ double red[4];
-    const float* x = X + static_cast<size_t>(blockIdx.x) * n;
-    float* y = Y + static_cast<size_t>(blockIdx.x) * n;
+// sum(x^2) of n floats in f64 by a 256-thread workgroup -> rms as the CPU path rounds it
+// (LI/src/residual.rs:24).
+__device__ __forceinline__ float row_rms(const float* __restrict__ x, int n, double eps, double* red) {
     double ss = 0.0;
     for (int i = threadIdx.x; i < n; i += 256) ss += static_cast<double>(x[i]) * x[i];
     ss = wave_sum_d(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     const double tot = (red[0] + red[1]) + (red[2] + red[3]);
-    const float rms = static_cast<float>(sqrt(tot / static_cast<double>(n) + eps));
-    const float inv = 1.0f / rms;
-    for (int i = threadIdx.x; i < n; i += 256) y[i] = (x[i] * inv) * w[i];
+    return static_cast<float>(sqrt(tot / static_cast<double>(n) + eps));
+}
+
+// Grid M rows; 256 threads.  y = (x * (1 / rms)) * (off + w), or without a weight
+// (w == null) y = x * (1 / rms) (LI/src/residual.rs:25-29: weight None -> 1.0).
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ X, const float* __restrict__ w,
+                                                           float off, float* __restrict__ Y, int n, double eps) {
+    __shared__ double red[4];
+    const float* x = X + static_cast<size_t>(blockIdx.x) * n;
+    float* y = Y + static_cast<size_t>(blockIdx.x) * n;
+    const float inv = 1.0f / row_rms(x, n, eps, red);
+    if (w) {
+        for (int i = threadIdx.x; i < n; i += 256) y[i] = (x[i] * inv) * (off + w[i]);
+    } else {
+        for (int i = threadIdx.x; i < n; i += 256) y[i] = x[i] * inv;
+    }
+}
+
+// Post-norm residual, grid M rows: out = (h + norm(v, w)) * scale (scale 1 = none).
+__global__ __launch_bounds__(256) void resid_norm_rows_kernel(const float* __restrict__ H, const float* __restrict__ V,
+                                                              const float* __restrict__ w, float off, float scale,
+                                                              float* __restrict__ OUT, int n, double eps) {
+    __shared__ double red[4];
+    const size_t r = static_cast<size_t>(blockIdx.x) * n;
+    const float* v = V + r;
+    const float inv = 1.0f / row_rms(v, n, eps, red);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float nv = w ? (v[i] * inv) * (off + w[i]) : v[i] * inv;
+        OUT[r + i] = (H[r + i] + nv) * scale;
+    }
+}
+
+// Parameter-free RMS norm of each V head in place: grid (M rows, num_kv heads), one wave;
+// head h of row p starts at X + p * ld + h * hd.
+__global__ __launch_bounds__(64) void vnorm_rows_kernel(float* __restrict__ X, int ld, int hd, double eps) {
+    float* v = X + static_cast<size_t>(blockIdx.x) * ld + static_cast<size_t>(blockIdx.y) * hd;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < hd; i += 64) ss += static_cast<double>(v[i]) * v[i];
+    ss = wave_sum_d(ss);
+    const float rms = static_cast<float>(sqrt(ss / static_cast<double>(hd) + eps));
+    for (int i = threadIdx.x; i < hd; i += 64) v[i] = v[i] / rms;
 }
 
 // Thread per (position p, kv element j): K RoPE'd at p, K and V to fp16 in the cache.
@@ -52,24 +92,40 @@ __global__ void rope_kv_rows_kernel(const float* __restrict__ QKV, int M, int p0
 }
 
 __global__ void add_rows_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
-                                size_t n) {
+                                size_t n, float scale) {
     const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
-    if (i < n) out[i] = a[i] + b[i];
+    if (i < n) out[i] = (a[i] + b[i]) * scale;
 }
 
 // GU rows [M][2 inter] with gate and up interleaved (2i, 2i + 1) -> act [M][inter].
-__global__ void silu_pair_rows_kernel(const float* __restrict__ GU, float* __restrict__ act, size_t n) {
+__global__ void gated_pair_rows_kernel(const float* __restrict__ GU, float* __restrict__ act, size_t n, int kind) {
     const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
-    if (i < n) act[i] = silu_mul(GU[2 * i], GU[2 * i + 1]);
+    if (i < n) act[i] = gated_act(kind, GU[2 * i], GU[2 * i + 1]);
 }
 
 unsigned blocks(size_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
 }  // namespace
 
-void launch_rmsnorm_rows(const float* X, const float* w, float* Y, size_t m, size_t n, double eps, hipStream_t s) {
+void launch_rmsnorm_rows(const float* X, const float* w, float off, float* Y, size_t m, size_t n, double eps,
+                         hipStream_t s) {
     if (m == 0) return;
-    rmsnorm_rows_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, w, Y, static_cast<int>(n), eps);
+    rmsnorm_rows_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, w, off, Y, static_cast<int>(n), eps);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_resid_norm_rows(const float* H, const float* V, const float* w, float off, float scale, float* out,
+                            size_t m, size_t n, double eps, hipStream_t s) {
+    if (m == 0) return;
+    resid_norm_rows_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(H, V, w, off, scale, out,
+                                                                                static_cast<int>(n), eps);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_vnorm_rows(float* X, size_t m, size_t ld, int num_heads, int hd, double eps, hipStream_t s) {
+    if (m == 0 || num_heads == 0) return;
+    vnorm_rows_kernel<<<dim3(static_cast<unsigned>(m), static_cast<unsigned>(num_heads)), dim3(64), 0, s>>>(
+        X, static_cast<int>(ld), hd, eps);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
@@ -83,15 +139,15 @@ void launch_rope_kv_rows(const float* QKV, size_t m, size_t p0, size_t q_dim, si
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
-void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipStream_t s) {
+void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipStream_t s, float scale) {
     if (n == 0) return;
-    add_rows_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(a, b, out, n);
+    add_rows_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(a, b, out, n, scale);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
-void launch_silu_pair_rows(const float* GU, float* act, size_t n, hipStream_t s) {
+void launch_gated_pair_rows(const float* GU, float* act, size_t n, int kind, hipStream_t s) {
     if (n == 0) return;
-    silu_pair_rows_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(GU, act, n);
+    gated_pair_rows_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(GU, act, n, kind);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 

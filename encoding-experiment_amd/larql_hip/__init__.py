@@ -25,7 +25,7 @@ LIB_PATH = os.path.join(_HERE, "liblarql_hip.so")
 
 Q4_0, Q4_K, Q4_KF, Q6_K, Q8_0, F32 = 0, 1, 2, 3, 4, 5
 FORMAT_NAMES = {Q4_0: "Q4_0", Q4_K: "Q4_K", Q4_KF: "Q4_KF", Q6_K: "Q6_K", Q8_0: "Q8_0", F32: "F32"}
-TOPK_MAX, KNN_MAX_LAYERS = 64, 64
+TOPK_MAX, KNN_MAX_LAYERS = 512, 64
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_DEVICE, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5
 
@@ -139,9 +139,12 @@ def _nbytes(a):
 
 def make_layer(wq, wk, wv, wo, gate, up, down, input_norm, post_attn_norm, *, head_dim, num_q_heads,
                num_kv_heads, rope_base, eps=1e-6, attn_scale=None, fmt=Q4_K, formats=None,
-               rotary_dim=0, sliding_window=0):
-    """A Llama FullPipelineLayer over numpy (host) or device tensors of reference-layout bytes.
-    Keep the source arrays alive while the struct is in use."""
+               rotary_dim=0, sliding_window=0, norm_offset=0.0, has_post_norms=False, pre_ffn_norm=None,
+               post_ffn_norm=None, activation=ACT_SILU, has_v_norm=False, layer_scalar=0.0):
+    """A FullPipelineLayer over numpy (host) or device tensors of reference-layout bytes:
+    the Llama layer by default, or the variants of larql-compute/src/pipeline.rs:76-115
+    (norm offset, post-norms with pre/post-FFN norm weights, GELU-tanh, V-norm, layer
+    scalar).  Keep the source arrays alive while the struct is in use."""
     L = PipelineLayer()
     names = ("wq", "wk", "wv", "wo", "gate", "up", "down")
     for name, arr in zip(names, (wq, wk, wv, wo, gate, up, down)):
@@ -149,11 +152,16 @@ def make_layer(wq, wk, wv, wo, gate, up, down, input_norm, post_attn_norm, *, he
         setattr(L, name, QuantWeight(_addr(arr), _nbytes(arr), None, f))
     L.input_norm = _addr(input_norm)
     L.post_attn_norm = _addr(post_attn_norm)
-    L.norm_offset = 0.0
+    L.pre_ffn_norm = _addr(pre_ffn_norm)
+    L.post_ffn_norm = _addr(post_ffn_norm)
+    L.norm_offset = norm_offset
+    L.has_post_norms = int(bool(has_post_norms))
+    L.has_v_norm = int(bool(has_v_norm))
+    L.layer_scalar = layer_scalar
     L.eps = eps
     L.norm_type = NORM_RMS
     L.ffn_type = FFN_GATED
-    L.activation = ACT_SILU
+    L.activation = activation
     L.attn_scale = attn_scale if attn_scale is not None else float(1.0 / np.sqrt(head_dim))
     L.head_dim, L.num_q_heads, L.num_kv_heads = head_dim, num_q_heads, num_kv_heads
     L.rope_base = rope_base

@@ -193,8 +193,10 @@ int larql_hip_quantize_weights_dev(larql_hip_ctx* ctx, int format, const float* 
 
 /* ── vindex gate-KNN (vindex code, not trait methods: LV/src/index/gate.rs) ── */
 
-/* Largest top_k and number of layers per call. */
-#define LARQL_HIP_TOPK_MAX 64
+/* Largest top_k and number of layers per call.  A top_k above a row's length returns the
+ * whole row ranked (top_k.min(len), LV/src/index/walk.rs:569): slots past the row length
+ * hold index 0xFFFFFFFF and score 0. */
+#define LARQL_HIP_TOPK_MAX 512
 #define LARQL_HIP_KNN_MAX_LAYERS 64
 
 /* Gate KNN for one layer from host memory: VectorIndex::gate_knn (LV/src/index/gate.rs:108-134)
@@ -219,13 +221,13 @@ int larql_hip_gate_scores_dev(larql_hip_ctx* ctx, const uint64_t* handles, size_
 
 /* Top-k of each row of a device score matrix [rows][n]: signed_mode 0 orders by |score|
  * (gate.rs:307-316), 1 by the signed score (lm-head KNN, LV/src/index/walk.rs:563-580).
- * Ties in index order.  idx / vals [rows][k] (device), 1 <= k <= min(n, 64). */
+ * Ties in index order.  idx / vals [rows][k] (device), 1 <= k <= LARQL_HIP_TOPK_MAX. */
 int larql_hip_topk_dev(larql_hip_ctx* ctx, const float* scores, size_t rows, size_t n, size_t k, int signed_mode,
                        uint32_t* idx, float* vals, void* stream);
 
 /* lm-head KNN, the Q4 path of VectorIndex::lm_head_knn_backend (LV/src/index/walk.rs:549-583):
  * query quantized by quantize_to_q8, scores = q4_matvec(lm_head_q4 [vocab][hidden] Q4_0),
- * the top_k tokens by signed score descending (ties in index order), 1 <= top_k <= 64.
+ * the top_k tokens by signed score descending (ties in index order), 1 <= top_k <= LARQL_HIP_TOPK_MAX.
  * Host-pointer form: lm_head_q4 / query / idx / scores in host memory (the head is
  * uploaded once and cached like every weight). */
 int larql_hip_lm_head_knn(larql_hip_ctx* ctx, const uint8_t* lm_head_q4, size_t len, const float* query,
@@ -253,11 +255,15 @@ enum { LARQL_FFN_GATED = 0, LARQL_FFN_STANDARD = 1 };
 enum { LARQL_ACT_SILU = 0, LARQL_ACT_GELU_TANH = 1 };
 
 /* FullPipelineLayer — LC/src/pipeline.rs:60-120, same fields in the same order.
- * Optional vectors are NULL when absent.  The HIP decode step implements the
- * Llama family: RMSNorm, gated SiLU FFN, no post-norms, no V-norm, no biases,
- * no layer scalar, Q4_K or Q6_K projections (each its own format, as in Q4_K_M files);
- * anything else is reported as
- * LARQL_HIP_ERR_UNSUPPORTED so the caller falls back (predict.rs:397-430). */
+ * Optional vectors are NULL when absent.  The HIP decode step and prompt pass implement
+ * RMSNorm layers with a gated FFN and Q4_K or Q6_K projections (each its own format, as in
+ * Q4_K_M files), with the variants the reference's decode reads per layer
+ * (LC/src/metal/decode.rs:98-739): norm_offset (weight = offset + w), SiLU or GELU-tanh,
+ * has_post_norms (h + norm(o, post_attn_norm); FFN input norm(h, pre_ffn_norm); h +
+ * norm(down, post_ffn_norm); an absent pre/post-FFN weight is the weight-free norm, as the
+ * CPU path has it, LI/src/forward/layer.rs:65-83), has_v_norm, layer_scalar (0 = off),
+ * rotary_dim, sliding_window and attn_scale.  LayerNorm, the ungated FFN and biases are
+ * reported as LARQL_HIP_ERR_UNSUPPORTED so the caller falls back (predict.rs:397-430). */
 typedef struct {
     larql_quant_weight wq, wk, wv, wo;
     larql_quant_weight gate, up, down;

@@ -31,11 +31,17 @@ def q6k(rows, cols, seed, std=0.02):
 
 
 class SmallModel:
-    """formats: projection name -> "q6_k" for Q6_K weights (default Q4_K)."""
+    """formats: projection name -> "q6_k" for Q6_K weights (default Q4_K).  variant: layer
+    variants of FullPipelineLayer (larql-compute/src/pipeline.rs:76-115) in the oracle's
+    keys: norm_offset, has_post_norms (with pre/post-FFN norm weights unless
+    ffn_norm_weights=False), activation ("silu" | "gelu_tanh"), has_v_norm, layer_scalar,
+    rotary_dim."""
 
-    def __init__(self, n_layers, hidden, inter, nq, nkv, hd, cap, seed=0, formats=None):
+    def __init__(self, n_layers, hidden, inter, nq, nkv, hd, cap, seed=0, formats=None, variant=None):
         self.n, self.hidden, self.inter, self.nq, self.nkv, self.hd = n_layers, hidden, inter, nq, nkv, hd
         self.formats = dict(formats or {})
+        self.variant = dict(variant or {})
+        ffn_w = self.variant.pop("ffn_norm_weights", True)
         self.layers = []
         qd, kvd = nq * hd, nkv * hd
         shapes = dict(wq=(qd, hidden), wk=(kvd, hidden), wv=(kvd, hidden), wo=(hidden, qd), gate=(inter, hidden),
@@ -48,23 +54,33 @@ class SmallModel:
             L.update(input_norm=(1.0 + 0.1 * oracle.gauss(s + 8, hidden)).astype(np.float32),
                      post_attn_norm=(1.0 + 0.1 * oracle.gauss(s + 9, hidden)).astype(np.float32),
                      k_cache=np.zeros(cap * kvd, np.uint16), v_cache=np.zeros(cap * kvd, np.uint16),
-                     formats=self.formats)
+                     formats=self.formats, **self.variant)
+            if self.variant.get("has_post_norms") and ffn_w:
+                L.update(pre_ffn_norm=(0.8 + 0.2 * oracle.gauss(s + 10, hidden)).astype(np.float32),
+                         post_ffn_norm=(0.5 + 0.2 * oracle.gauss(s + 11, hidden)).astype(np.float32))
             self.layers.append(L)
 
     def hip_layers(self, rope_base, window=0):
         fm = {k: larql_hip.Q6_K for k, v in self.formats.items() if v == "q6_k"}
+        v = self.variant
+        act = larql_hip.ACT_GELU_TANH if v.get("activation") == "gelu_tanh" else larql_hip.ACT_SILU
         return [larql_hip.make_layer(L["wq"], L["wk"], L["wv"], L["wo"], L["gate"], L["up"], L["down"],
                                      L["input_norm"], L["post_attn_norm"], head_dim=self.hd,
                                      num_q_heads=self.nq, num_kv_heads=self.nkv, rope_base=rope_base,
-                                     sliding_window=window, formats=fm)
+                                     sliding_window=window, formats=fm, norm_offset=v.get("norm_offset", 0.0),
+                                     has_post_norms=v.get("has_post_norms", False),
+                                     pre_ffn_norm=L.get("pre_ffn_norm"), post_ffn_norm=L.get("post_ffn_norm"),
+                                     activation=act, has_v_norm=v.get("has_v_norm", False),
+                                     layer_scalar=v.get("layer_scalar", 0.0), rotary_dim=v.get("rotary_dim", 0))
                 for L in self.layers]
 
 
 def run_sequence(hip, T0, n_tokens, n_layers=2, hidden=512, inter=1024, nq=8, nkv=2, hd=64, rope=500000.0,
-                 window=0, formats=None):
+                 window=0, formats=None, variant=None):
     print(f"[decode] layers={n_layers} hidden={hidden} nq={nq} nkv={nkv} hd={hd} T0={T0} tokens={n_tokens} "
-          f"window={window} formats={formats}", flush=True)
-    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=T0 + n_tokens + 1, seed=T0, formats=formats)
+          f"window={window} formats={formats} variant={variant}", flush=True)
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=T0 + n_tokens + 1, seed=T0, formats=formats,
+                   variant=variant)
     kvd = nkv * hd
     hip.reset_kv_cache()
     for l, L in enumerate(m.layers):
@@ -130,6 +146,49 @@ def test_decode_mixed_projection_formats(hip, formats):
     # Q4_K_M-style layers: some projections Q6_K (split Q|K|V launches, gate then up with
     # silu(gate) * up in the up epilogue)
     run_sequence(hip, T0=40, n_tokens=2, n_layers=2, formats=formats)
+
+
+VARIANTS = [
+    dict(norm_offset=1.0),                                                    # Gemma 2/3 norm weights
+    dict(activation="gelu_tanh"),
+    dict(has_post_norms=True, norm_offset=1.0, activation="gelu_tanh"),       # Gemma-3-style layer
+    dict(has_post_norms=True, ffn_norm_weights=False),                        # weight-free pre/post-FFN norms
+    dict(has_v_norm=True, layer_scalar=0.5, rotary_dim=32),                   # Gemma-4-style V-norm, scalar
+]
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_decode_layer_variants(hip, variant):
+    """FullPipelineLayer variants (larql-compute/src/pipeline.rs:76-115) on the decode step
+    against the oracle layer of the same variant: norm offset, GELU-tanh, post-norms with
+    and without pre/post-FFN weights, V-norm, layer scalar, partial rotary."""
+    run_sequence(hip, T0=40, n_tokens=2, n_layers=2, variant=variant)
+
+
+@pytest.mark.parametrize("variant", VARIANTS[1:3] + VARIANTS[4:])
+def test_decode_layer_variants_mixed_formats(hip, variant):
+    # separate gate and up launches carry the activation in the up epilogue
+    run_sequence(hip, T0=12, n_tokens=2, n_layers=1, formats={"gate": "q6_k", "wv": "q6_k"}, variant=variant)
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_prefill_q4_layer_variants(hip, variant):
+    """The batched prompt pass with each layer variant: every position within the bar."""
+    n_layers, hidden, inter, nq, nkv, hd, seq = 2, 512, 1024, 8, 2, 64, 12
+    print(f"[prefill variant] {variant}", flush=True)
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=91, variant=variant)
+    layers = m.hip_layers(10000.0)
+    x = np.stack([oracle.gauss(850 + p, hidden) for p in range(seq)])
+    hip.reset_kv_cache()
+    got = hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0)
+    worst = 0.0
+    for p in range(seq):
+        ref = x[p].copy()
+        for L in m.layers:
+            ref = oracle.decode_layer(L, ref, p, hidden, inter, nq, nkv, hd, 10000.0)
+        worst = max(worst, rel_err(got[p], ref))
+    print(f"  worst position rel_err={worst:.3e}", flush=True)
+    assert worst <= REL_TOL
 
 
 @pytest.mark.parametrize("seq,formats,window", [(6, {"wv": "q6_k"}, 0), (20, {"wo": "q6_k", "down": "q6_k"}, 0),
@@ -216,14 +275,32 @@ def test_prefill_q4_deep_model(hip):
 
 
 def test_decode_unsupported_layer_returns_none(hip):
+    """A supported layer decodes; the same layer struct flipped to LayerNorm (and then to
+    biased up projections) returns None even though its weights match the cached model,
+    and flipped to GELU-tanh it decodes as the oracle's GELU layer, not the cached SiLU one."""
     be = larql_hip.HipBackend(0, strict=False)
     try:
         m = SmallModel(1, 256, 256, 2, 1, 128, cap=4)
         layers = m.hip_layers(10000.0)
-        layers[0].activation = larql_hip.ACT_GELU_TANH
-        x = np.zeros(256, np.float32)
+        x = oracle.gauss(17, 256)
+        silu = be.decode_token(layers, x, 256, 256, 256, 128, 2, 1, 128, 10000.0)
+        assert silu is not None
+        layers[0].norm_type = larql_hip.NORM_LAYER
         assert be.decode_token(layers, x, 256, 256, 256, 128, 2, 1, 128, 10000.0) is None
-        assert "SiLU" in be.last_error()
+        assert "LayerNorm" in be.last_error()
+        layers[0].norm_type = larql_hip.NORM_RMS
+        bias = np.zeros(256, np.float32)
+        layers[0].ffn_up_bias = bias.ctypes.data
+        assert be.decode_token(layers, x, 256, 256, 256, 128, 2, 1, 128, 10000.0) is None
+        assert "bias" in be.last_error()
+        layers[0].ffn_up_bias = None
+        layers[0].activation = larql_hip.ACT_GELU_TANH
+        be.reset_kv_cache()
+        gelu = be.decode_token(layers, x, 256, 256, 256, 128, 2, 1, 128, 10000.0)
+        L = dict(m.layers[0], activation="gelu_tanh")
+        L["k_cache"], L["v_cache"] = np.zeros_like(L["k_cache"]), np.zeros_like(L["v_cache"])
+        ref = oracle.decode_layer(L, x, 0, 256, 256, 2, 1, 128, 10000.0)
+        assert rel_err(gelu, ref) <= REL_TOL and not np.array_equal(gelu, silu)
     finally:
         be.close()
 

@@ -125,7 +125,7 @@ def test_topk_ties_zeros_and_sizes(hip, signed):
     for n in (64, 12288, 12289, 128256):   # register path limit is 48 * 256 = 12288
         cases.append(rng.standard_normal(n).astype(np.float32))
     for row in cases:
-        for k in (1, 32, 64):
+        for k in (1, 32, 64, 300, 512):
             if k > row.size:
                 continue
             gi, gv = _topk_rows(hip, torch, row[None, :], k, signed)
@@ -134,13 +134,45 @@ def test_topk_ties_zeros_and_sizes(hip, signed):
             np.testing.assert_array_equal(gv[0].view(np.uint32), rv.view(np.uint32))
 
 
+@pytest.mark.parametrize("signed", [False, True])
+def test_topk_mass_ties_linear_time(hip, signed):
+    """More than the 2048 LDS candidates tie at the k-th key: all-zero rows of the lm-head
+    (128256) and gate (10240) widths, and a row with 5000 equal values under 100 larger
+    ones.  Ties resolve in index order by a select over their indices (linear time)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(52)
+    spiky = rng.uniform(-0.5, 0.5, 20000).astype(np.float32)
+    spiky[rng.choice(20000, 5000, replace=False)] = 1.0
+    spiky[rng.choice(20000, 100, replace=False)] = 2.0 + rng.uniform(0, 1, 100).astype(np.float32)
+    for row in (np.zeros(128256, np.float32), np.zeros(10240, np.float32), spiky):
+        for k in (1, 64, 512):
+            print(f"[topk ties] n={row.size} k={k} signed={signed}", flush=True)
+            gi, gv = _topk_rows(hip, torch, np.stack([row, row[::-1].copy()]), k, signed)
+            for r, rr in enumerate((row, row[::-1].copy())):
+                ri, rv = (oracle.topk_signed if signed else oracle.topk_abs)(rr, k)
+                np.testing.assert_array_equal(gi[r], ri, err_msg=f"n={row.size} k={k}")
+                np.testing.assert_array_equal(gv[r].view(np.uint32), rv.view(np.uint32))
+
+
+def test_topk_k_above_row_length_is_clamped(hip):
+    """top_k.min(len) (LV/src/index/walk.rs:569): a request for more entries than the row has
+    returns the whole row ranked; the slots past it hold index 0xFFFFFFFF and score 0."""
+    gate = oracle.gauss(61, 8 * 64).reshape(8, 64)
+    q = oracle.gauss(62, 64)
+    got = hip.gate_knn(gate, 8, 64, q, 11, fmt=larql_hip.F32)
+    ri, rv = oracle_knn_f32(gate, q[None, :], 8, 64, 8)
+    np.testing.assert_array_equal(got[0][0, :8], ri[0])
+    np.testing.assert_array_equal(got[1][0, :8].view(np.uint32), rv[0].view(np.uint32))
+    assert np.all(got[0][0, 8:] == 0xFFFFFFFF) and np.all(got[1][0, 8:] == 0.0)
+
+
 def test_topk_invalid_k_returns_none():
     be = larql_hip.HipBackend(0, strict=False)
     try:
         gate = np.zeros((8, 64), np.float32)
         q = np.zeros(64, np.float32)
-        assert be.gate_knn(gate, 8, 64, q, 9, fmt=larql_hip.F32) is None      # k > features
-        assert be.gate_knn(gate, 8, 64, q, 65, fmt=larql_hip.F32) is None     # k > 64
+        assert be.gate_knn(gate, 8, 64, q, 0, fmt=larql_hip.F32) is None      # k = 0
+        assert be.gate_knn(gate, 8, 64, q, 513, fmt=larql_hip.F32) is None    # k > LARQL_HIP_TOPK_MAX
         assert be.gate_knn(gate, 8, 64, q, 4, fmt=larql_hip.Q4_K) is None     # unsupported format
     finally:
         be.close()
