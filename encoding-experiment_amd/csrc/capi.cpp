@@ -191,6 +191,13 @@ extern "C" int larql_hip_ctx_create(int device, larql_hip_ctx** out) {
     }
     c->num_cus = prop.multiProcessorCount;
     c->device_name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    try {
+        larql::noalloc_scratch_init(device);  // with the device current (hipSetDevice above)
+    } catch (const larql::Error&) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return LARQL_HIP_ERR_DEVICE;
+    }
     *out = c;
     return LARQL_HIP_OK;
 }

@@ -3,6 +3,8 @@
 // LV/src/index/gate.rs:14-29, 108-134, 307-316, 500-537, 711-731.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <string>
 #include <vector>
 
 #include "capi_util.h"
@@ -161,6 +163,35 @@ static void run_lm_head_knn(larql_hip_ctx* c, const DevWeight& w, const float* d
     launch_lm_head_knn(w, dq, nq, top_k, b, di, dv, s);
 }
 
+// ── the allocation-free lm-head KNN ──────────────────────────────────────
+// Its work buffers live in one fixed device array per GPU, held until the process ends.
+// Host code reaches each GPU's copy only through the address hipGetSymbolAddress returns
+// on that GPU (recorded once per device by noalloc_scratch_init, which every context
+// creation runs with its device current): the array's name on the host is a stand-in,
+// not a device address.
+static __device__ __align__(256) uint8_t scratch[LARQL_HIP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+}  // namespace
+
+namespace larql {
+void noalloc_scratch_init(int device) {
+    if (device < 0 || device >= kMaxDevices) fail(LARQL_HIP_ERR_DEVICE, "device index out of range");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        fail(LARQL_HIP_ERR_DEVICE, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[device] = ptr;
+}
+}  // namespace larql
+
 extern "C" int larql_hip_lm_head_knn(larql_hip_ctx* c, const uint8_t* lm_head_q4, size_t len, const float* query,
                                      size_t vocab, size_t hidden, size_t top_k, uint32_t* idx, float* scores) {
     return guarded(c, [&] {
@@ -185,3 +216,30 @@ extern "C" int larql_hip_lm_head_knn_dev(larql_hip_ctx* c, uint64_t handle, cons
     });
 }
 
+extern "C" int larql_hip_lm_head_knn_dev_noalloc(larql_hip_ctx* c, uint64_t handle, const float* queries, size_t nq,
+                                                 size_t top_k, uint32_t* idx, float* scores, void* stream) {
+    return guarded(c, [&] {
+        if (!queries || !idx || !scores) fail(LARQL_HIP_ERR_INVALID, "lm-head KNN: null pointer");
+        const DevWeight& w = larql::lookup(c, handle);
+        check_lm_head(w, nq, top_k);
+        uint8_t* base = nullptr;
+        {
+            std::lock_guard<std::mutex> lk(g_scratch_mu);
+            base = static_cast<uint8_t*>(g_scratch_ptr[c->device]);
+        }
+        if (!base) fail(LARQL_HIP_ERR_STATE, "lm-head KNN (no-alloc): scratch address not set up for this device");
+        const size_t hidden = w.cols, nb = hidden / 32;
+        const size_t need_q8 = align256(nq * hidden), need_q8s = align256(nq * nb * sizeof(float));
+        const size_t need_s = nq * w.rows * sizeof(float);
+        if (need_s / sizeof(float) / nq != w.rows || need_q8 + need_q8s + need_s > LARQL_HIP_NOALLOC_SCRATCH_BYTES)
+            fail(LARQL_HIP_ERR_INVALID, "lm-head KNN (no-alloc): nq * (vocab * 4 + hidden * 9 / 8) needs " +
+                                            std::to_string(need_q8 + need_q8s + need_s) + " bytes; the fixed scratch "
+                                            "holds " + std::to_string(LARQL_HIP_NOALLOC_SCRATCH_BYTES));
+        // every byte the kernels read is written first in the same call: nothing to clear
+        LmHeadBufs b;
+        b.q8 = reinterpret_cast<int8_t*>(base);
+        b.q8s = reinterpret_cast<float*>(base + need_q8);
+        b.S = reinterpret_cast<float*>(base + need_q8 + need_q8s);
+        launch_lm_head_knn(w, queries, nq, top_k, b, idx, scores, pick_stream(c, stream));
+    });
+}

@@ -160,6 +160,12 @@ struct larql_hip_ctx {
     larql_hip_model* trait_model = nullptr;
 };
 
+namespace larql {
+// Records this device's address of the allocation-free entry points' fixed device array
+// (capi_knn.cpp); run once per device by context creation, with the device current.
+void noalloc_scratch_init(int device);
+}  // namespace larql
+
 // Frees the decode-side state of a context (trait model, KV cache).
 void larql_hip_decode_release(larql_hip_ctx* c);
 

@@ -26,6 +26,7 @@ LIB_PATH = os.path.join(_HERE, "liblarql_hip.so")
 Q4_0, Q4_K, Q4_KF, Q6_K, Q8_0, F32 = 0, 1, 2, 3, 4, 5
 FORMAT_NAMES = {Q4_0: "Q4_0", Q4_K: "Q4_K", Q4_KF: "Q4_KF", Q6_K: "Q6_K", Q8_0: "Q8_0", F32: "F32"}
 TOPK_MAX, KNN_MAX_LAYERS = 512, 64
+NOALLOC_SCRATCH_BYTES = 8 << 20
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_DEVICE, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5
 
@@ -77,6 +78,7 @@ SIGNATURES = {
     "larql_hip_topk_dev": (_I, [_P, _P, _SZ, _SZ, _SZ, _I, _P, _P, _P]),
     "larql_hip_lm_head_knn": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _P, _P]),
     "larql_hip_lm_head_knn_dev": (_I, [_P, _U64, _P, _SZ, _SZ, _P, _P, _P]),
+    "larql_hip_lm_head_knn_dev_noalloc": (_I, [_P, _U64, _P, _SZ, _SZ, _P, _P, _P]),
     # decode step (structs declared below; pointers passed as void*)
     "larql_hip_decode_token": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
     "larql_hip_prefill_q4": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float,
@@ -509,6 +511,12 @@ class HipBackend:
     def lm_head_knn_dev(self, handle: int, queries, nq: int, top_k: int, idx, scores, stream=None):
         self._check(self._lib.larql_hip_lm_head_knn_dev(self._ctx, handle, _dptr(queries), nq, top_k, _dptr(idx),
                                                         _dptr(scores), _stream_ptr(stream)))
+
+    def lm_head_knn_dev_noalloc(self, handle: int, queries, nq: int, top_k: int, idx, scores, stream=None):
+        """lm_head_knn_dev with its work buffers in the library's fixed device array (no
+        allocation); nq * (vocab * 4 + hidden * 9 / 8) must fit NOALLOC_SCRATCH_BYTES."""
+        self._check(self._lib.larql_hip_lm_head_knn_dev_noalloc(self._ctx, handle, _dptr(queries), nq, top_k,
+                                                                _dptr(idx), _dptr(scores), _stream_ptr(stream)))
 
     @staticmethod
     def _handle_array(handles):

@@ -237,6 +237,22 @@ int larql_hip_lm_head_knn(larql_hip_ctx* ctx, const uint8_t* lm_head_q4, size_t 
 int larql_hip_lm_head_knn_dev(larql_hip_ctx* ctx, uint64_t handle, const float* queries, size_t nq, size_t top_k,
                               uint32_t* idx, float* scores, void* stream);
 
+/* Bytes of the fixed device array behind larql_hip_lm_head_knn_dev_noalloc (one per GPU). */
+#define LARQL_HIP_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* larql_hip_lm_head_knn_dev without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate — code under HIP graph capture,
+ * per-token serving loops, harnesses that forbid hipMalloc.  Same arguments, kernels and
+ * results as larql_hip_lm_head_knn_dev; the quantized queries and the vocabulary scores
+ * live in a fixed device array of LARQL_HIP_NOALLOC_SCRATCH_BYTES per GPU (8 MiB, held
+ * until the process ends), which limits a call to
+ *   nq * (vocab * 4 + hidden * 9 / 8) (+ alignment) <= 8 MiB
+ * (vocab 128256: up to 16 queries); larger requests return LARQL_HIP_ERR_INVALID.  Every
+ * call on one GPU shares that array: calls that overlap on one GPU (different streams or
+ * contexts) race. */
+int larql_hip_lm_head_knn_dev_noalloc(larql_hip_ctx* ctx, uint64_t handle, const float* queries, size_t nq,
+                                      size_t top_k, uint32_t* idx, float* scores, void* stream);
+
 /* ── decode step: layers, KV cache, full-pipeline decode ───────────────── */
 
 /* QuantWeight — LC/src/pipeline.rs:22-27.  `data`/`len` are reference-layout
