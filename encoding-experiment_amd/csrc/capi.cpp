@@ -58,7 +58,7 @@ const DevWeight& lookup(larql_hip_ctx* c, uint64_t handle) {
     return it->second;
 }
 
-static void check_shape(int format, size_t len, size_t rows, size_t cols) {
+static void check_shape(int format, size_t len, size_t rows, size_t cols, int hf) {
     if (rows == 0 || cols == 0) fail(LARQL_HIP_ERR_INVALID, "rows and cols must be nonzero");
     switch (format) {
         case LARQL_Q4_0:
@@ -66,18 +66,17 @@ static void check_shape(int format, size_t len, size_t rows, size_t cols) {
             if (cols % 32) fail(LARQL_HIP_ERR_INVALID, "hidden must be a multiple of 32");
             break;
         case LARQL_Q4_K:
+        case LARQL_Q4_KF:
         case LARQL_Q6_K:
             if (cols % 256) fail(LARQL_HIP_ERR_INVALID, "hidden must be a multiple of 256");
             break;
-        case LARQL_Q4_KF:
-            fail(LARQL_HIP_ERR_UNSUPPORTED, "Q4_KF is not supported by the HIP backend");
         case LARQL_F32:
             if (cols % 16) fail(LARQL_HIP_ERR_INVALID, "f32 gate hidden must be a multiple of 16");
             break;
         default: fail(LARQL_HIP_ERR_INVALID, "unknown quant format");
     }
     if (rows > 0x7FFFFFFF / 2) fail(LARQL_HIP_ERR_INVALID, "too many rows");
-    const size_t need = rows * ref_row_bytes(format, cols);
+    const size_t need = rows * ref_row_bytes(format, cols, hf);
     if (len < need)
         fail(LARQL_HIP_ERR_INVALID, "weight buffer too small: " + std::to_string(len) + " < " +
                                         std::to_string(need) + " bytes");
@@ -85,20 +84,22 @@ static void check_shape(int format, size_t len, size_t rows, size_t cols) {
 
 static uint64_t register_impl(larql_hip_ctx* c, int format, const void* data, size_t len,
                               const float* q8_scales, size_t rows, size_t cols, bool on_device) {
-    check_shape(format, len, rows, cols);
+    const int hf = format == LARQL_Q4_KF ? q4kf_form(len, rows, cols) : kHdr148;
+    check_shape(format, len, rows, cols, hf);
     if (!data) fail(LARQL_HIP_ERR_INVALID, "null weight pointer");
     if (format == LARQL_Q8_0 && !q8_scales) fail(LARQL_HIP_ERR_INVALID, "Q8_0 weights need scales");
     DevWeight w;
     w.format = format;
+    w.hf = hf;
     w.rows = rows;
     w.rows_pad = pad_rows(rows);
     w.cols = cols;
-    w.bytes = dev_layout_bytes(format, w.rows_pad, cols);
+    w.bytes = dev_layout_bytes(format, w.rows_pad, cols, hf);
     if (hipMalloc(&w.base, w.bytes) != hipSuccess)
         fail(LARQL_HIP_ERR_NOMEM, "hipMalloc of weight (" + std::to_string(w.bytes) + " bytes) failed");
     dev_layout_carve(w);
     if (w.rows_pad != rows) LARQL_HIP_CHECK(hipMemsetAsync(w.base, 0, w.bytes, c->stream));
-    const size_t raw_bytes = rows * ref_row_bytes(format, cols);
+    const size_t raw_bytes = rows * ref_row_bytes(format, cols, hf);
     const size_t sc_bytes = format == LARQL_Q8_0 ? rows * (cols / 32) * sizeof(float) : 0;
     try {
         const uint8_t* raw = static_cast<const uint8_t*>(data);
@@ -445,6 +446,11 @@ extern "C" int larql_hip_matvec_dev(larql_hip_ctx* c, uint64_t handle, const voi
                 larql::launch_q4k_matvec(w, static_cast<const float*>(x), out, m, ws, s);
                 break;
             }
+            case LARQL_Q4_KF:  // one matvec per activation row
+                for (size_t i = 0; i < m; i++)
+                    larql::launch_q4k_matvec(w, static_cast<const float*>(x) + i * w.cols, out + i * w.rows, 1,
+                                             nullptr, s);
+                break;
             case LARQL_Q6_K: larql::launch_q6k_matvec(w, static_cast<const float*>(x), out, m, s); break;
             case LARQL_Q4_0:
                 if (!x_scales) fail(LARQL_HIP_ERR_INVALID, "Q4_0 matvec needs Q8 activation scales");

@@ -85,30 +85,36 @@ struct Src {
 // (stride 1) or interleaved (source i -> rows i, i+n, ...).
 DevWeight build_weight(larql_hip_ctx* c, larql_hip_model* m, int format, size_t cols, const std::vector<Src>& srcs,
                        bool interleave, bool on_device) {
-    if (format != LARQL_Q4_K && format != LARQL_Q6_K)
-        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: projections must be Q4_K or Q6_K");
+    if (format != LARQL_Q4_K && format != LARQL_Q6_K && format != LARQL_Q4_KF)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: projections must be Q4_K, Q4_KF or Q6_K");
     if (cols % 256) fail(LARQL_HIP_ERR_INVALID, "decode: projection input width must be a multiple of 256");
+    // Q4_KF: 144-byte GGUF or 160-byte pre-baked blocks, told apart by length; the sources
+    // of one fused weight must agree
+    const int hf = format == LARQL_Q4_KF ? larql::q4kf_form(srcs[0].len, srcs[0].rows, cols) : larql::kHdr148;
     size_t rows = 0;
     for (const Src& s : srcs) {
         if (!s.data) fail(LARQL_HIP_ERR_INVALID, "decode: null weight");
-        if (s.len < s.rows * larql::ref_row_bytes(format, cols))
+        if (format == LARQL_Q4_KF && larql::q4kf_form(s.len, s.rows, cols) != hf)
+            fail(LARQL_HIP_ERR_INVALID, "decode: fused Q4_KF projections mix the 144- and 160-byte layouts");
+        if (s.len < s.rows * larql::ref_row_bytes(format, cols, hf))
             fail(LARQL_HIP_ERR_INVALID, "decode: weight buffer shorter than its shape");
         if (interleave && s.rows != srcs[0].rows) fail(LARQL_HIP_ERR_INVALID, "decode: gate/up shapes differ");
         rows += s.rows;
     }
     DevWeight w;
     w.format = format;
+    w.hf = hf;
     w.rows = rows;
     w.rows_pad = larql::pad_rows(rows);
     w.cols = cols;
-    w.bytes = larql::dev_layout_bytes(format, w.rows_pad, cols);
+    w.bytes = larql::dev_layout_bytes(format, w.rows_pad, cols, hf);
     w.base = dev_alloc(m, w.bytes);
     larql::dev_layout_carve(w);
     LARQL_HIP_CHECK(hipMemsetAsync(w.base, 0, w.bytes, c->stream));
     size_t row0 = 0;
     for (size_t i = 0; i < srcs.size(); i++) {
         const Src& s = srcs[i];
-        const size_t nbytes = s.rows * larql::ref_row_bytes(format, cols);
+        const size_t nbytes = s.rows * larql::ref_row_bytes(format, cols, hf);
         const uint8_t* raw = static_cast<const uint8_t*>(s.data);
         if (!on_device) {
             uint8_t* stage = static_cast<uint8_t*>(larql::ensure(c, c->stage_raw, nbytes));
@@ -181,7 +187,12 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
                 fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: per-layer head geometry must be uniform");
             }
             const size_t qd = static_cast<size_t>(d.nq) * d.hd, kvd = static_cast<size_t>(d.nkv) * d.hd;
-            d.split_qkv = L.wq.format != L.wk.format || L.wq.format != L.wv.format;
+            // one fused launch needs one format (and, for Q4_KF, one byte layout)
+            auto form = [&](const larql_quant_weight& q, size_t r, size_t k) {
+                return q.format * 4 + (q.format == LARQL_Q4_KF ? larql::q4kf_form(q.len, r, k) : 0);
+            };
+            d.split_qkv = form(L.wq, qd, hidden) != form(L.wk, kvd, hidden) ||
+                          form(L.wq, qd, hidden) != form(L.wv, kvd, hidden);
             if (d.split_qkv) {
                 d.wq = build_weight(c, m, L.wq.format, hidden, {{L.wq.data, L.wq.len, qd}}, false, on_device);
                 d.wk = build_weight(c, m, L.wk.format, hidden, {{L.wk.data, L.wk.len, kvd}}, false, on_device);
@@ -192,7 +203,7 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
                                      false, on_device);
             }
             d.wo = build_weight(c, m, L.wo.format, qd, {{L.wo.data, L.wo.len, hidden}}, false, on_device);
-            d.split_gu = L.gate.format != L.up.format;
+            d.split_gu = form(L.gate, inter, hidden) != form(L.up, inter, hidden);
             if (d.split_gu) {
                 d.gate = build_weight(c, m, L.gate.format, hidden, {{L.gate.data, L.gate.len, inter}}, false, on_device);
                 d.up = build_weight(c, m, L.up.format, hidden, {{L.up.data, L.up.len, inter}}, false, on_device);

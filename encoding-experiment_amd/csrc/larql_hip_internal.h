@@ -76,7 +76,8 @@ struct DevWeight {
     uint8_t* qs = nullptr;   // Q4_K/Q4_0 nibbles, Q6_K ql, Q8_0 int8
     uint8_t* qh = nullptr;   // Q6_K high bits
     int8_t* sc = nullptr;    // Q6_K scales
-    uint4* hdr = nullptr;    // Q4_K headers
+    uint4* hdr = nullptr;    // Q4_K / Q4_KF headers
+    int hf = 0;              // Q4_K-family header form: kHdr148, kHdrGguf or kHdrKf160
     void* d = nullptr;       // Q6_K/Q4_0 f16 scales, Q8_0 f32 scales
     // registry keys
     const void* host_ptr = nullptr;
@@ -90,8 +91,24 @@ struct DevWeight {
 // re-uploads instead of serving stale weights.
 uint64_t host_fingerprint(const void* data, size_t len);
 
-size_t ref_row_bytes(int format, size_t cols);   // bytes per row in the reference layout
-size_t dev_layout_bytes(int format, size_t rows_pad, size_t cols);
+// Q4_K-family header forms in the device layout (DevWeight::hf):
+//   kHdr148  : 148-byte Q4_K: uint4 {d | dmin << 16, sc 0..3, sc 4..7 (6-bit bytes),
+//              min bytes m_j | m_{j+4} << 4}
+//   kHdrGguf : 144-byte GGUF Q4_KF: the same uint4 with 6-bit mins, whose top two bits sit
+//              in the top two bits of the scale bytes (m_j >> 4 above sc_j)
+//   kHdrKf160: 160-byte Q4_KF: two uint4 {8 x f16 d*sc_j} {8 x f16 dmin*m_j} per row and
+//              super-block
+constexpr int kHdr148 = 0, kHdrGguf = 1, kHdrKf160 = 2;
+// Bytes per 256-element block of a Q4_K-family header form in the reference layout.
+inline size_t q4k_family_block_bytes(int hf) { return hf == kHdrKf160 ? 160 : hf == kHdrGguf ? 144 : 148; }
+// Q4_KF carries two byte layouts (LC/src/pipeline.rs:15 says 160 bytes, the GPU decode
+// kernels read 144, LC/src/metal/shaders/q4kf_qkv_proj.rs:46): a buffer of exactly
+// rows x blocks x 160 bytes is the pre-baked form, anything else the GGUF form.
+inline int q4kf_form(size_t len, size_t rows, size_t cols) {
+    return len == rows * (cols / 256) * 160 ? kHdrKf160 : kHdrGguf;
+}
+size_t ref_row_bytes(int format, size_t cols, int hf = kHdr148);   // bytes per row in the reference layout
+size_t dev_layout_bytes(int format, size_t rows_pad, size_t cols, int hf = kHdr148);
 inline size_t pad_rows(size_t rows) { return (rows + 63) & ~size_t(63); }
 
 // Q4_K tile-major layout: byte offset of sub-block j (0..7) of super-block sb of `row`

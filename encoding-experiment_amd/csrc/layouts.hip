@@ -5,14 +5,21 @@
 //   Q4_K 148 B / 256 : [f16 d][f16 dmin][12 B sc (0..7 used)][4 B mins][128 B]  (:104-170)
 //   Q6_K 210 B / 256 : [128 B ql][64 B qh][16 x i8 scales][f16 d]              (:179-239)
 //   Q8_0 trait form  : i8 [rows*cols] + f32 scales [rows*cols/32]          (LC/src/pipeline.rs:22-27)
+//   Q4_KF 144 B / 256: llama.cpp GGUF block [f16 d][f16 dmin][12 B packed 6-bit scales and
+//                      mins][128 B: chunk c of 32 bytes = sub-block 2c low, 2c+1 high
+//                      nibbles]            (LC/src/metal/shaders/q4kf_qkv_proj.rs:87-119)
+//   Q4_KF 160 B / 256: [8 x f16 d*sc_j][8 x f16 dmin*m_j][128 B nibbles as Q4_K] (q4_common.rs:370-413)
+// Both Q4_KF forms land in the Q4_K tile-major nibble layout (sub-blocks in the 148-byte
+// nibble order), so one matvec kernel reads all three, templated on the header form.
 #include "larql_hip_internal.h"
 
 namespace larql {
 
-size_t ref_row_bytes(int format, size_t cols) {
+size_t ref_row_bytes(int format, size_t cols, int hf) {
     switch (format) {
         case LARQL_Q4_0: return cols / 32 * 18;
         case LARQL_Q4_K: return cols / 256 * 148;
+        case LARQL_Q4_KF: return cols / 256 * q4k_family_block_bytes(hf);
         case LARQL_Q6_K: return cols / 256 * 210;
         case LARQL_Q8_0: return cols;
         case LARQL_F32: return cols * 4;
@@ -22,10 +29,11 @@ size_t ref_row_bytes(int format, size_t cols) {
 
 static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-size_t dev_layout_bytes(int format, size_t rows, size_t cols) {
+size_t dev_layout_bytes(int format, size_t rows, size_t cols, int hf) {
     switch (format) {
         case LARQL_Q4_0: return align256(rows * cols / 2) + align256(rows * (cols / 32) * 2);
         case LARQL_Q4_K: return align256(rows * cols / 2) + align256(rows * (cols / 256) * 16);
+        case LARQL_Q4_KF: return align256(rows * cols / 2) + align256(rows * (cols / 256) * (hf == kHdrKf160 ? 32 : 16));
         case LARQL_Q6_K:
             return align256(rows * cols / 2) + align256(rows * cols / 4) + align256(rows * cols / 16) +
                    align256(rows * (cols / 256) * 2);
@@ -44,6 +52,7 @@ void dev_layout_carve(DevWeight& w) {
             w.d = p;
             break;
         case LARQL_Q4_K:
+        case LARQL_Q4_KF:
             w.qs = p; p += align256(R * K / 2);
             w.hdr = reinterpret_cast<uint4*>(p);
             break;
@@ -85,6 +94,69 @@ __global__ void repack_q4k_kernel(const uint32_t* __restrict__ raw, uint8_t* __r
     for (int j = 0; j < 8; j++)
         *reinterpret_cast<uint4*>(qs + q4k_sub_offset(row, sb, j, bpr)) =
             make_uint4(s[5 + 4 * j], s[6 + 4 * j], s[7 + 4 * j], s[8 + 4 * j]);
+}
+
+// One thread per GGUF (144-byte, llama.cpp layout) super-block: scales and 6-bit mins
+// unpacked (get_scale_min_k4: j < 4: sc = q[j] & 63, m = q[j+4] & 63; j >= 4: sc =
+// (q[j+4] & 15) | (q[j-4] >> 6) << 4, m = (q[j+4] >> 4) | (q[j] >> 6) << 4) into the kHdrGguf
+// header, nibbles of sub-block j = 2c + h (nibble h of bytes 32c .. 32c + 31) regrouped into
+// the 148-byte order (element 2i low, 2i + 1 high nibble of byte i).
+__global__ void repack_q4kf_gguf_kernel(const uint32_t* __restrict__ raw, uint8_t* __restrict__ qs,
+                                        uint4* __restrict__ hdr, size_t nblocks, size_t bpr, size_t row0,
+                                        size_t stride) {
+    size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint32_t* s = raw + b * 36;
+    const size_t o = dst_block(b, bpr, row0, stride);
+    const size_t row = o / bpr, sb = o - row * bpr;
+    uint8_t q[12];
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[4 * i + k] = static_cast<uint8_t>(s[1 + i] >> (8 * k));
+    uint32_t scw[2] = {0u, 0u}, mnw = 0u;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t sc = j < 4 ? (q[j] & 63u) : ((q[j + 4] & 15u) | ((q[j - 4] >> 6) << 4));
+        const uint32_t mn = j < 4 ? (q[j + 4] & 63u) : ((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+        scw[j >> 2] |= (sc | ((mn >> 4) << 6)) << (8 * (j & 3));
+        mnw |= (mn & 15u) << (8 * (j & 3) + 4 * (j >> 2));
+    }
+    hdr[q4k_hdr_index(row, sb, bpr)] = make_uint4(s[0], scw[0], scw[1], mnw);
+    const uint8_t* n = reinterpret_cast<const uint8_t*>(s + 4);
+    for (int j = 0; j < 8; j++) {
+        const int c = j >> 1, sh = 4 * (j & 1);
+        uint32_t d4[4];
+        for (int w = 0; w < 4; w++) {
+            uint32_t v = 0;
+            for (int k = 0; k < 4; k++) {
+                const int i = 4 * w + k;  // output byte i = elements 2i, 2i + 1 of the sub-block
+                const uint32_t lo = (n[32 * c + 2 * i] >> sh) & 15u, hi = (n[32 * c + 2 * i + 1] >> sh) & 15u;
+                v |= (lo | (hi << 4)) << (8 * k);
+            }
+            d4[w] = v;
+        }
+        *reinterpret_cast<uint4*>(qs + q4k_sub_offset(row, sb, j, bpr)) = make_uint4(d4[0], d4[1], d4[2], d4[3]);
+    }
+}
+
+// One thread per 160-byte Q4_KF super-block: the two f16 octets (d*sc_j, dmin*m_j) as the
+// kHdrKf160 header pair, nibbles (148-byte order) as Q4_K.
+__global__ void repack_q4kf160_kernel(const uint32_t* __restrict__ raw, uint8_t* __restrict__ qs,
+                                      uint4* __restrict__ hdr, size_t nblocks, size_t bpr, size_t row0,
+                                      size_t stride) {
+    size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint32_t* s = raw + b * 40;
+    const size_t o = dst_block(b, bpr, row0, stride);
+    const size_t row = o / bpr, sb = o - row * bpr;
+    const size_t h = q4k_hdr_index(row, sb, bpr) * 2;
+    hdr[h] = make_uint4(s[0], s[1], s[2], s[3]);
+    hdr[h + 1] = make_uint4(s[4], s[5], s[6], s[7]);
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        *reinterpret_cast<uint4*>(qs + q4k_sub_offset(row, sb, j, bpr)) =
+            make_uint4(s[8 + 4 * j], s[9 + 4 * j], s[10 + 4 * j], s[11 + 4 * j]);
 }
 
 // One thread per Q6_K super-block (210-byte stride: 2-byte aligned source).  The
@@ -139,6 +211,16 @@ void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scale
             const size_t bpr = w.cols / 256, nb = src_rows * bpr;
             repack_q4k_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
                 reinterpret_cast<const uint32_t*>(raw), w.qs, w.hdr, nb, bpr, row0, stride);
+            break;
+        }
+        case LARQL_Q4_KF: {
+            const size_t bpr = w.cols / 256, nb = src_rows * bpr;
+            if (w.hf == kHdrKf160)
+                repack_q4kf160_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
+                    reinterpret_cast<const uint32_t*>(raw), w.qs, w.hdr, nb, bpr, row0, stride);
+            else
+                repack_q4kf_gguf_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
+                    reinterpret_cast<const uint32_t*>(raw), w.qs, w.hdr, nb, bpr, row0, stride);
             break;
         }
         case LARQL_Q6_K: {

@@ -206,7 +206,7 @@ static void launch_mv_t(const DevWeight& w, MvArgs a, hipStream_t s, int nslots,
 }
 
 void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s) {
-    if (w.format == LARQL_Q4_K) return launch_q4k_mfma(w, a, s);
+    if (w.format == LARQL_Q4_K || w.format == LARQL_Q4_KF) return launch_q4k_mfma(w, a, s);
     if (w.format != LARQL_Q6_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "launch_mv: format");
     if (a.num_cus <= 0) a.num_cus = current_device_cus();
     if (stream_mv_supported(w)) return launch_mv_stream(w, a, s);
@@ -229,7 +229,10 @@ void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s) {
 }
 
 void launch_q4k_matvec(const DevWeight& w, const float* x, float* out, size_t m, void* ws, hipStream_t s) {
-    if (m > 1) return launch_q4k_gemm(w, x, out, m, ws, s);  // prefill: m tokens on the matrix cores
+    if (m > 1) {  // prefill: m tokens on the matrix cores (148-byte Q4_K)
+        if (w.format != LARQL_Q4_K) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4k matmul: Q4_K weights only");
+        return launch_q4k_gemm(w, x, out, m, ws, s);
+    }
     MvArgs a;
     a.x = x;
     a.out = out;

@@ -3,7 +3,9 @@
 //   Reference semantics: LC/src/cpu/ops/q4k_matvec.rs:31-90 (trait method
 //   LC/src/backend.rs:126-130): out[n] = sum_sb sum_j sum_i (d*sc_j*q - dmin*m_j) * x,
 //   computed here in the factorised form sc * sum(q x) - mn * sum(x) per 32-element
-//   sub-block (LC/src/metal/shaders/q4k_matvec.rs:13-79).
+//   sub-block (LC/src/metal/shaders/q4k_matvec.rs:13-79).  The two Q4_KF byte layouts
+//   (144-byte GGUF and 160-byte pre-baked, LC/src/pipeline.rs:15) arrive in the same
+//   device nibble layout and differ only in how a header gives the scales and mins.
 //
 // Work split.  A workgroup owns T tiles of 16 consecutive weight rows; its KS waves
 // split the super-blocks of the rows into contiguous parts of P = UR * R super-blocks
@@ -88,7 +90,34 @@ constexpr int max_waves() {
     return UR * T >= 8 ? kMaxKS / 2 : kMaxKS;  // 8 units in flight need more than 128 VGPRs
 }
 
-template <int UR, int T, bool NORM>
+// Scales and mins of sub-blocks g and g + 4 of one row from its header (HF: the header
+// form, kHdr148 / kHdrGguf / kHdrKf160; h2 is the second uint4 of a kHdrKf160 pair).
+template <int HF>
+__device__ __forceinline__ void q4k_scale_min(const uint4& h, const uint4& h2, int g, float& sc0, float& sc1,
+                                              float& mn0, float& mn1) {
+    const int scsh = 8 * g;
+    if constexpr (HF == kHdrKf160) {
+        const uint32_t s0 = (g < 2 ? h.x : h.y) >> (16 * (g & 1)), s1 = (g < 2 ? h.z : h.w) >> (16 * (g & 1));
+        const uint32_t m0 = (g < 2 ? h2.x : h2.y) >> (16 * (g & 1)), m1 = (g < 2 ? h2.z : h2.w) >> (16 * (g & 1));
+        sc0 = h2f(s0);
+        sc1 = h2f(s1);
+        mn0 = h2f(m0);
+        mn1 = h2f(m1);
+    } else {
+        const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+        sc0 = d * static_cast<float>((h.y >> scsh) & 0x3Fu);
+        sc1 = d * static_cast<float>((h.z >> scsh) & 0x3Fu);
+        uint32_t q0 = (h.w >> scsh) & 0xFu, q1 = (h.w >> (scsh + 4)) & 0xFu;
+        if constexpr (HF == kHdrGguf) {  // 6-bit mins: bits 4..5 above the 6-bit scales
+            q0 |= ((h.y >> (scsh + 6)) & 3u) << 4;
+            q1 |= ((h.z >> (scsh + 6)) & 3u) << 4;
+        }
+        mn0 = dmin * static_cast<float>(q0);
+        mn1 = dmin * static_cast<float>(q1);
+    }
+}
+
+template <int UR, int T, bool NORM, int HF>
 __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int EL = 4 * UR;  // x elements per lane and round
@@ -102,14 +131,15 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
     const int g = lane >> 4, c = lane & 15;
     const size_t tile0 = static_cast<size_t>(blockIdx.x) * T;  // < rows_pad / 16: the grid is rows_pad / (16 T)
     const uint8_t* tq = a.qs + tile0 * S * 2048 + lane * 16;
-    const uint4* th = a.hdr + tile0 * S * 16 + c;
+    constexpr int HW = HF == kHdrKf160 ? 2 : 1;  // uint4 header words per row and super-block
+    const uint4* th = a.hdr + (tile0 * S * 16 + c) * HW;
 
     uint8_t* wl = lds + wave * wave_lds_bytes<UR>();
     PlSlot* slots = reinterpret_cast<PlSlot*>(wl + kZeroBytes);
     float* red = reinterpret_cast<float*>(lds + KS * wave_lds_bytes<UR>());  // [KS][16 T], then NORM scratch
 
     float xv[EL], wv[NORM ? EL : 1];
-    uint4 n0[T][UR], n1[T][UR], hd[T][UR];
+    uint4 n0[T][UR], n1[T][UR], hd[T][UR], hd2[HF == kHdrKf160 ? T : 1][HF == kHdrKf160 ? UR : 1];
     // Loads of round r: this lane's x slice (element e0), then the units' weights
     // (super-block indices clamped: a short last round re-reads a real block).  The
     // first PRE units are issued with x; the rest after the planes are built, so that a
@@ -131,7 +161,8 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
                 const uint8_t* q = tq + sb * 2048;
                 n0[t][u] = load_nt(q);
                 n1[t][u] = load_nt(q + 1024);
-                hd[t][u] = load_nt(th + sb * 16);
+                hd[t][u] = load_nt(th + sb * 16 * HW);
+                if constexpr (HF == kHdrKf160) hd2[t][u] = load_nt(th + sb * 32 + 1);
             }
     };
     constexpr int PRE = 1;
@@ -175,7 +206,6 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
     const bool alive = (ia >> 2) == g && (ia & 3) < 3;
     const uint32_t abase = alive ? static_cast<uint32_t>(kZeroBytes + 2 * g * sizeof(PlSlot) + (ia & 3) * 16) : 0u;
     const uint32_t astep = alive ? 8u * sizeof(PlSlot) : 0u;
-    const int scsh = 8 * g;
     float acc[T];
 #pragma unroll
     for (int t = 0; t < T; t++) acc[t] = 0.f;
@@ -259,12 +289,9 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
                 // scales of sub-blocks g and g + 4 of row c
                 const PlSlot* sl = slots + 8 * u + 2 * g;
                 const float4 sa = sl[0].s, sb = sl[1].s;
-                const uint4 h = hd[t][u];
-                const float d = h2f(h.x), dmin = h2f(h.x >> 16);
-                const float sc0 = d * static_cast<float>((h.y >> scsh) & 0x3Fu);
-                const float sc1 = d * static_cast<float>((h.z >> scsh) & 0x3Fu);
-                const float mn0 = dmin * static_cast<float>((h.w >> scsh) & 0xFu);
-                const float mn1 = dmin * static_cast<float>((h.w >> (scsh + 4)) & 0xFu);
+                float sc0, sc1, mn0, mn1;
+                if constexpr (HF == kHdrKf160) q4k_scale_min<HF>(hd[t][u], hd2[t][u], g, sc0, sc1, mn0, mn1);
+                else q4k_scale_min<HF>(hd[t][u], hd[t][u], g, sc0, sc1, mn0, mn1);
                 // s' (65536 a + 256 b + c): 256 b + c is exact in int32 and in f32 (< 2^24)
                 const float dot0 = fmaf(static_cast<float>(Da[2]), sa.y, sa.x * static_cast<float>(Da[1] * 256 + Da[0]));
                 const float dot1 = fmaf(static_cast<float>(Db[2]), sb.y, sb.x * static_cast<float>(Db[1] * 256 + Db[0]));
@@ -303,7 +330,7 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
 
 
 
-template <int UR, int T>
+template <int UR, int T, int HF>
 void launch_q4k_mfma_t(const DevWeight& w, MvArgs a, int R, hipStream_t s) {
     const int S = static_cast<int>(w.cols / 256);
     const int KS = (S + UR * R - 1) / (UR * R);
@@ -312,15 +339,15 @@ void launch_q4k_mfma_t(const DevWeight& w, MvArgs a, int R, hipStream_t s) {
     const size_t shmem = static_cast<size_t>(KS) * (wave_lds_bytes<UR>() + 16 * T * sizeof(float)) +
                          (a.norm_w ? kMaxKS * sizeof(double) : 0);
     const dim3 grid(static_cast<unsigned>(w.rows_pad / (16 * T))), block(64 * KS);
-    if (a.norm_w) q4k_mfma_kernel<UR, T, true><<<grid, block, shmem, s>>>(a);
-    else q4k_mfma_kernel<UR, T, false><<<grid, block, shmem, s>>>(a);
+    if (a.norm_w) q4k_mfma_kernel<UR, T, true, HF><<<grid, block, shmem, s>>>(a);
+    else q4k_mfma_kernel<UR, T, false, HF><<<grid, block, shmem, s>>>(a);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
 }  // namespace
 
 void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s) {
-    if (w.format != LARQL_Q4_K || w.cols % 256 != 0 || w.cols == 0 || w.rows_pad % 16 != 0 ||
+    if ((w.format != LARQL_Q4_K && w.format != LARQL_Q4_KF) || w.cols % 256 != 0 || w.cols == 0 || w.rows_pad % 16 != 0 ||
         w.cols > (size_t{1} << 24) || w.rows_pad / 16 > 0x7FFFFFFFu)
         fail(LARQL_HIP_ERR_UNSUPPORTED, "q4k matvec: shape");
     if (a.num_cus <= 0) a.num_cus = current_device_cus();
@@ -337,10 +364,15 @@ void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s) {
     // waves x 4 super-blocks (K > 16384) take several rounds.
     const size_t S = w.cols / 256;
     const size_t tiles = w.rows_pad / 16, cus = static_cast<size_t>(a.num_cus);
-    if (S <= 16 && tiles >= 3 * cus && tiles < 6 * cus && w.rows_pad % 64 == 0)
-        launch_q4k_mfma_t<2, 4>(w, a, 1, s);
-    else
-        launch_q4k_mfma_t<4, 1>(w, a, static_cast<int>((S + 4 * kMaxKS - 1) / (4 * kMaxKS)), s);
+    const int R4 = static_cast<int>((S + 4 * kMaxKS - 1) / (4 * kMaxKS));
+    if (w.format == LARQL_Q4_KF) {  // the two Q4_KF forms: the general split
+        if (w.hf == kHdrKf160) launch_q4k_mfma_t<4, 1, kHdrKf160>(w, a, R4, s);
+        else launch_q4k_mfma_t<4, 1, kHdrGguf>(w, a, R4, s);
+    } else if (S <= 16 && tiles >= 3 * cus && tiles < 6 * cus && w.rows_pad % 64 == 0) {
+        launch_q4k_mfma_t<2, 4, kHdr148>(w, a, 1, s);
+    } else {
+        launch_q4k_mfma_t<4, 1, kHdr148>(w, a, R4, s);
+    }
 }
 
 }  // namespace larql

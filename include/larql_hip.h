@@ -48,7 +48,15 @@ typedef struct larql_hip_ctx larql_hip_ctx;
 
 /* QuantFormat — LC/src/pipeline.rs:12-19 (same discriminant order).  LARQL_F32 is an
  * extension with no QuantFormat counterpart: plain f32 [rows][cols], the vindex's f32
- * gate vectors (LV/src/index/gate.rs:14-29), usable only by the gate-KNN entry points. */
+ * gate vectors (LV/src/index/gate.rs:14-29), usable only by the gate-KNN entry points.
+ * LARQL_Q4_KF takes both byte layouts the reference gives that name, told apart by the
+ * buffer length: exactly rows x (cols/256) x 160 bytes is the pre-baked form
+ * ([8 x f16 d*sc_j][8 x f16 dmin*m_j][128 B nibbles], q4k_to_q4kf,
+ * LC/src/cpu/ops/q4_common.rs:370-413; pipeline.rs:15); any other length is read as
+ * 144-byte GGUF blocks in the layout the reference's GPU decode reads for Q4_KF
+ * (llama.cpp block_q4_K: 6-bit scales and mins packed in 12 bytes, chunk c of 32 bytes
+ * holding sub-block 2c in its low and 2c + 1 in its high nibbles;
+ * LC/src/metal/shaders/q4kf_qkv_proj.rs:87-119). */
 typedef enum {
     LARQL_Q4_0 = 0,
     LARQL_Q4_K = 1,
@@ -164,6 +172,7 @@ int larql_hip_quantize_weights(larql_hip_ctx* ctx, int format, const float* x, s
  * m = 1); for LARQL_Q4_0 / LARQL_Q8_0 `x` is int8 [m][cols] and x_scales f32
  * [m][cols/32], any m (each output row in the single-row order, bit for bit).
  * out is f32 [m][rows].
+ * LARQL_Q4_KF takes f32 x too (m > 1 runs m matvecs).
  * The prefill GEMM packs x as fp16 into a workspace owned by the context; a call with a
  * larger m than any before on the context grows it (device synchronize + allocation), so
  * device calls on one context must not overlap on different streams.

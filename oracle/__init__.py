@@ -52,6 +52,13 @@ def _load():
             "lo_q4k_matvec": (None, [_P, _P, _P, _SZ, _SZ]),
             "lo_q6k_matvec": (None, [_P, _P, _P, _SZ, _SZ]),
             "lo_q8_matvec": (None, [_P, _P, _P, _P, _P, _SZ, _SZ]),
+            "lo_q4kf_gguf_matvec": (None, [_P, _P, _P, _SZ, _SZ]),
+            "lo_q4kf160_matvec": (None, [_P, _P, _P, _SZ, _SZ]),
+            "lo_gguf_scale_min": (None, [ctypes.c_int, _P, _P, _P]),
+            "lo_q4k_to_gguf": (None, [_P, _SZ, _P]),
+            "lo_quantize_q4_k_gguf": (None, [_P, _SZ, _P]),
+            "lo_q4k_to_q4kf": (None, [_P, _SZ, _P]),
+            "lo_q4k_to_gguf_llamacpp": (None, [_P, _SZ, _P]),
             "lo_q8_block_dots": (None, [_P, _P, _P, _SZ, _SZ]),
             "lo_topk_abs": (None, [_P, _SZ, _SZ, _P, _P]),
             "lo_topk_signed": (None, [_P, _SZ, _SZ, _P, _P]),
@@ -210,6 +217,57 @@ def q6k_matvec(q6k, x, rows: int, hidden: int):
     return out
 
 
+def q4kf_gguf_matvec(w, x, rows: int, hidden: int):
+    """Q4_KF, 144-byte llama.cpp GGUF block (the reference's GPU decode layout)."""
+    w, x = _c(w, np.uint8), _c(x, np.float32)
+    out = np.empty(rows, dtype=np.float32)
+    _load().lo_q4kf_gguf_matvec(_ptr(w), _ptr(x), _ptr(out), rows, hidden)
+    return out
+
+
+def q4kf160_matvec(w, x, rows: int, hidden: int):
+    """Q4_KF, 160-byte block with pre-baked half scales (q4k_to_q4kf)."""
+    w, x = _c(w, np.uint8), _c(x, np.float32)
+    out = np.empty(rows, dtype=np.float32)
+    _load().lo_q4kf160_matvec(_ptr(w), _ptr(x), _ptr(out), rows, hidden)
+    return out
+
+
+def gguf_scale_min(j: int, q12):
+    q12 = _c(q12, np.uint8)
+    sc, mn = ctypes.c_uint8(0), ctypes.c_uint8(0)
+    _load().lo_gguf_scale_min(j, _ptr(q12), ctypes.byref(sc), ctypes.byref(mn))
+    return sc.value, mn.value
+
+
+def _convert(fn, src, nblocks, out_block):
+    src = _c(src, np.uint8)
+    out = np.empty(nblocks * out_block, dtype=np.uint8)
+    getattr(_load(), fn)(_ptr(src), nblocks, _ptr(out))
+    return out
+
+
+def q4k_to_gguf(q4k):
+    return _convert("lo_q4k_to_gguf", q4k, np.asarray(q4k).size // 148, 144)
+
+
+def q4k_to_q4kf(q4k):
+    return _convert("lo_q4k_to_q4kf", q4k, np.asarray(q4k).size // 148, 160)
+
+
+def q4k_to_gguf_llamacpp(q4k):
+    return _convert("lo_q4k_to_gguf_llamacpp", q4k, np.asarray(q4k).size // 148, 144)
+
+
+def quantize_q4_k_gguf(x):
+    x = _c(x, np.float32)
+    if x.size % 256:
+        raise ValueError("length must be a multiple of 256")
+    out = np.empty(x.size // 256 * 144, dtype=np.uint8)
+    _load().lo_quantize_q4_k_gguf(_ptr(x), x.size, _ptr(out))
+    return out
+
+
 def q8_matvec(wq, ws, xq, xs, rows: int, hidden: int):
     wq, ws, xq, xs = _c(wq, np.int8), _c(ws, np.float32), _c(xq, np.int8), _c(xs, np.float32)
     out = np.empty(rows, dtype=np.float32)
@@ -315,7 +373,8 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
     """One decoder layer on the CPU.  ``layer`` holds numpy arrays keyed as the
     lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits) are updated in place.
     window > 0 attends over the last `window` positions only.  ``layer["formats"]``
-    (optional) maps a projection name to "q6_k" for Q6_K bytes (default Q4_K).
+    (optional) maps a projection name to "q6_k" (Q6_K bytes), "q4_kf" (Q4_KF, 144-byte GGUF)
+    or "q4_kf160" (Q4_KF, 160-byte); the default is Q4_K.
     Optional layer variants (FullPipelineLayer, LC/src/pipeline.rs:76-115):
     pre_ffn_norm / post_ffn_norm (arrays or None), norm_offset, has_post_norms,
     activation ("silu" | "gelu_tanh"), has_v_norm, layer_scalar, rotary_dim, attn_scale."""
@@ -333,8 +392,9 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
             keep[name] = a
             setattr(st, name, a.ctypes.data)
     fm = layer.get("formats", {})
+    codes = {"q4_k": 0, "q6_k": 1, "q4_kf": 2, "q4_kf160": 3}
     for i, name in enumerate(_PROJ):
-        st.fmt[i] = 1 if fm.get(name, "q4_k") == "q6_k" else 0
+        st.fmt[i] = codes[fm.get(name, "q4_k")]
     for name in ("k_cache", "v_cache"):
         a = layer[name]
         assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]

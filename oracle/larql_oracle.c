@@ -426,6 +426,185 @@ void lo_q6k_matvec(const uint8_t* q6k, const float* x, float* out, size_t rows, 
     }
 }
 
+/* ── Q4_KF: GGUF 144-byte (llama.cpp layout) and 160-byte pre-baked ─────── */
+
+/* llama.cpp get_scale_min_k4 (the unpack of LM/src/quant/ggml.rs:252-262 and of the
+ * uint16 masks of LC/src/metal/shaders/q4kf_qkv_proj.rs:93-97). */
+void lo_gguf_scale_min(int j, const uint8_t* q, uint8_t* sc, uint8_t* mn) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *mn = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* Element e of a llama.cpp block: chunk c = e / 64 of 32 bytes; the first 32 elements of a
+ * chunk are the low nibbles (sub-block 2c), the next 32 the high nibbles (2c + 1). */
+static int gguf_nibble(const uint8_t* qs, int e) {
+    int c = e / 64, l = e % 64;
+    return l < 32 ? (qs[32 * c + l] & 0xF) : (qs[32 * c + l - 32] >> 4);
+}
+
+void lo_q4kf_gguf_matvec(const uint8_t* w, const float* x, float* out, size_t rows, size_t hidden) {
+    size_t nsb = hidden / 256, bytes = nsb * 144;
+    for (size_t r = 0; r < rows; r++) {
+        float acc = 0.0f;
+        for (size_t sb = 0; sb < nsb; sb++) {
+            const uint8_t* blk = w + r * bytes + sb * 144;
+            float d = lo_f16_to_f32(rd_u16(blk)), dmin = lo_f16_to_f32(rd_u16(blk + 2));
+            for (int e = 0; e < 256; e++) {
+                int j = e / 32;
+                uint8_t sc, mn;
+                lo_gguf_scale_min(j, blk + 4, &sc, &mn);
+                float s = d * (float)sc, m = dmin * (float)mn;
+                acc += (s * (float)gguf_nibble(blk + 16, e) - m) * x[sb * 256 + e];
+            }
+        }
+        out[r] = acc;
+    }
+}
+
+void lo_q4kf160_matvec(const uint8_t* w, const float* x, float* out, size_t rows, size_t hidden) {
+    size_t nsb = hidden / 256, bytes = nsb * 160;
+    for (size_t r = 0; r < rows; r++) {
+        float acc = 0.0f;
+        for (size_t sb = 0; sb < nsb; sb++) {
+            const uint8_t* blk = w + r * bytes + sb * 160;
+            for (int j = 0; j < 8; j++) {
+                float s = lo_f16_to_f32(rd_u16(blk + 2 * j)), m = lo_f16_to_f32(rd_u16(blk + 16 + 2 * j));
+                for (int i = 0; i < 16; i++) {
+                    uint8_t q = blk[32 + j * 16 + i];
+                    size_t xi = sb * 256 + j * 32 + i * 2;
+                    acc += (s * (float)(q & 0x0F) - m) * x[xi];
+                    acc += (s * (float)((q >> 4) & 0x0F) - m) * x[xi + 1];
+                }
+            }
+        }
+        out[r] = acc;
+    }
+}
+
+/* The reference's 12-byte packing of 6-bit scales and mins (q4_common.rs:285-296, 343-352). */
+static void ref_gguf_pack(const uint8_t* sc, const uint8_t* mn, uint8_t* p) {
+    for (int j = 0; j < 4; j++) {
+        p[j] = (uint8_t)((sc[j] & 0x3F) | ((mn[j] & 0x03) << 6));
+        p[j + 4] = (uint8_t)((sc[j + 4] & 0x3F) | ((mn[j + 4] & 0x03) << 6));
+    }
+    for (int j = 0; j < 4; j++)
+        p[8 + j] = (uint8_t)(((mn[2 * j] >> 2) & 0x0F) | (((mn[2 * j + 1] >> 2) & 0x0F) << 4));
+}
+
+/* LC/src/cpu/ops/q4_common.rs:321-361 */
+void lo_q4k_to_gguf(const uint8_t* q4k, size_t nblocks, uint8_t* out) {
+    for (size_t b = 0; b < nblocks; b++) {
+        const uint8_t* blk = q4k + b * 148;
+        uint8_t* o = out + b * 144;
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 4; j++) {
+            sc[j] = blk[4 + j] & 0x3F;
+            sc[j + 4] = blk[8 + j] & 0x3F;
+            mn[j] = blk[16 + j] & 0x0F;
+            mn[j + 4] = (blk[16 + j] >> 4) & 0x0F;
+        }
+        memcpy(o, blk, 4);
+        ref_gguf_pack(sc, mn, o + 4);
+        memcpy(o + 16, blk + 20, 128);
+    }
+}
+
+/* LC/src/cpu/ops/q4_common.rs:248-314 (dmin = -gmin / 63 and 6-bit mins). */
+void lo_quantize_q4_k_gguf(const float* x, size_t n, uint8_t* out) {
+    size_t nsb = n / 256;
+    for (size_t sb = 0; sb < nsb; sb++) {
+        const float* blk = x + sb * 256;
+        uint8_t* o = out + sb * 144;
+        float sub_min[8], sub_max[8];
+        for (int j = 0; j < 8; j++) {
+            float mnv = INFINITY, mxv = -INFINITY;
+            for (int i = 0; i < 32; i++) {
+                mnv = fminf(mnv, blk[j * 32 + i]);
+                mxv = fmaxf(mxv, blk[j * 32 + i]);
+            }
+            sub_min[j] = mnv;
+            sub_max[j] = mxv;
+        }
+        float gmr = 0.0f, gmin = INFINITY;
+        for (int j = 0; j < 8; j++) gmr = fmaxf(gmr, sub_max[j] - sub_min[j]);
+        for (int j = 0; j < 8; j++) gmin = fminf(gmin, sub_min[j]);
+        float d = gmr > 0.0f ? gmr / 63.0f : 0.0f;
+        float dmin = gmin < 0.0f ? -gmin / 63.0f : 0.0f;
+        uint8_t qs[8], qm[8];
+        for (int j = 0; j < 8; j++) {
+            float range = sub_max[j] - sub_min[j];
+            qs[j] = d > 0.0f ? f_to_u8(clampf(roundf(range / d), 0.0f, 63.0f)) : 0;
+            qm[j] = dmin > 0.0f ? f_to_u8(clampf(roundf(-sub_min[j] / dmin), 0.0f, 63.0f)) : 0;
+        }
+        wr_u16(o + 0, lo_f32_to_f16_trunc(d));
+        wr_u16(o + 2, lo_f32_to_f16_trunc(dmin));
+        ref_gguf_pack(qs, qm, o + 4);
+        for (int j = 0; j < 8; j++) {
+            float sc = d * (float)qs[j];
+            float mn = dmin * (float)qm[j];
+            float inv_sc = sc > 0.0f ? 1.0f / sc : 0.0f;
+            const float* sub = blk + j * 32;
+            for (int i = 0; i < 16; i++) {
+                uint8_t v0 = f_to_u8(clampf(roundf((sub[i * 2] + mn) * inv_sc), 0.0f, 15.0f));
+                uint8_t v1 = f_to_u8(clampf(roundf((sub[i * 2 + 1] + mn) * inv_sc), 0.0f, 15.0f));
+                o[16 + j * 16 + i] = (uint8_t)(v0 | (v1 << 4));
+            }
+        }
+    }
+}
+
+/* LC/src/cpu/ops/q4_common.rs:370-413 */
+void lo_q4k_to_q4kf(const uint8_t* q4k, size_t nblocks, uint8_t* out) {
+    for (size_t b = 0; b < nblocks; b++) {
+        const uint8_t* blk = q4k + b * 148;
+        uint8_t* o = out + b * 160;
+        float d = lo_f16_to_f32(rd_u16(blk)), dmin = lo_f16_to_f32(rd_u16(blk + 2));
+        for (int j = 0; j < 4; j++) {
+            wr_u16(o + 2 * j, lo_f32_to_f16_trunc(d * (float)(blk[4 + j] & 0x3F)));
+            wr_u16(o + 2 * (j + 4), lo_f32_to_f16_trunc(d * (float)(blk[8 + j] & 0x3F)));
+            wr_u16(o + 16 + 2 * j, lo_f32_to_f16_trunc(dmin * (float)(blk[16 + j] & 0x0F)));
+            wr_u16(o + 16 + 2 * (j + 4), lo_f32_to_f16_trunc(dmin * (float)((blk[16 + j] >> 4) & 0x0F)));
+        }
+        memcpy(o + 32, blk + 20, 128);
+    }
+}
+
+/* 148 -> llama.cpp 144: scales and mins in the get_scale_min_k4 packing, nibbles moved so
+ * that element 32j + l of sub-block j = 2c + h sits in nibble h of byte 32c + l. */
+void lo_q4k_to_gguf_llamacpp(const uint8_t* q4k, size_t nblocks, uint8_t* out) {
+    for (size_t b = 0; b < nblocks; b++) {
+        const uint8_t* blk = q4k + b * 148;
+        uint8_t* o = out + b * 144;
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 4; j++) {
+            sc[j] = blk[4 + j] & 0x3F;
+            sc[j + 4] = blk[8 + j] & 0x3F;
+            mn[j] = blk[16 + j] & 0x0F;
+            mn[j + 4] = (blk[16 + j] >> 4) & 0x0F;
+        }
+        memcpy(o, blk, 4);
+        uint8_t* p = o + 4;
+        for (int j = 0; j < 4; j++) {
+            p[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+            p[j + 4] = (uint8_t)(mn[j] | ((mn[j + 4] >> 4) << 6));
+            p[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
+        }
+        memset(o + 16, 0, 128);
+        for (int e = 0; e < 256; e++) {
+            int j = e / 32, i = e % 32;
+            uint8_t byte = blk[20 + j * 16 + i / 2];
+            int q = (i & 1) ? (byte >> 4) : (byte & 0xF);
+            int c = j / 2, h = j % 2;
+            o[16 + 32 * c + i] |= (uint8_t)(q << (4 * h));
+        }
+    }
+}
+
 /* LC/src/cpu/ops/q8_matvec.rs:36-62 */
 void lo_q8_matvec(const int8_t* wq, const float* ws, const int8_t* xq, const float* xs,
                   float* out, size_t rows, size_t hidden) {
@@ -598,9 +777,12 @@ void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_
     free(sc);
 }
 
-/* A projection in its layer's format: Q4_K (0) or Q6_K (1). */
+/* A projection in its layer's format: Q4_K (0), Q6_K (1), Q4_KF 144-byte GGUF (2) or
+ * Q4_KF 160-byte (3). */
 static void lo_proj(int fmt, const uint8_t* w, const float* x, float* out, size_t rows, size_t cols) {
     if (fmt == 1) lo_q6k_matvec(w, x, out, rows, cols);
+    else if (fmt == 2) lo_q4kf_gguf_matvec(w, x, out, rows, cols);
+    else if (fmt == 3) lo_q4kf160_matvec(w, x, out, rows, cols);
     else lo_q4k_matvec(w, x, out, rows, cols);
 }
 

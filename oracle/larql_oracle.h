@@ -58,6 +58,29 @@ void lo_q4_0_vecmat(const float* act, const uint8_t* q4, float* out,
 void lo_q4k_matvec(const uint8_t* q4k, const float* x, float* out, size_t rows, size_t hidden);
 /* LC/src/cpu/ops/q6k_matvec.rs:31-90 */
 void lo_q6k_matvec(const uint8_t* q6k, const float* x, float* out, size_t rows, size_t hidden);
+/* Q4_KF in its two byte layouts (the trait's QuantFormat::Q4_KF, LC/src/pipeline.rs:15).
+ * 144-byte GGUF block as the reference's GPU decode reads it (llama.cpp block_q4_K,
+ * LC/src/metal/shaders/q4kf_qkv_proj.rs:87-119): [f16 d][f16 dmin][12 B: 6-bit scales and
+ * mins, llama.cpp packing][128 B: chunk c of 32 bytes holds sub-block 2c in its low and
+ * 2c+1 in its high nibbles].  w = d*sc_j*q - dmin*m_j, accumulated in element order. */
+void lo_q4kf_gguf_matvec(const uint8_t* w, const float* x, float* out, size_t rows, size_t hidden);
+/* 160-byte block with pre-baked half scales (q4k_to_q4kf, LC/src/cpu/ops/q4_common.rs:370-413):
+ * [8 x f16 d*sc_j][8 x f16 dmin*m_j][128 B nibbles in the 148-byte order].  w = sc_j*q - mn_j. */
+void lo_q4kf160_matvec(const uint8_t* w, const float* x, float* out, size_t rows, size_t hidden);
+/* Scale and 6-bit min of sub-block j from the 12 packed bytes of a GGUF block (llama.cpp
+ * get_scale_min_k4, stated in the reference at LM/src/quant/ggml.rs:252-262). */
+void lo_gguf_scale_min(int j, const uint8_t* q12, uint8_t* sc, uint8_t* mn);
+/* The reference's converters and GGUF quantizer (LC/src/cpu/ops/q4_common.rs): byte layouts
+ * as the reference writes them.  q4k_to_gguf and quantize_q4_k_gguf pack scales and mins
+ * their own way (bytes 0..7: sc | (m & 3) << 6, bytes 8..11: m >> 2 nibbles) and keep the
+ * 148-byte nibble order, which the llama.cpp-layout GPU kernels do not read back. */
+void lo_q4k_to_gguf(const uint8_t* q4k, size_t nblocks, uint8_t* out);        /* :321-361 */
+void lo_quantize_q4_k_gguf(const float* x, size_t n, uint8_t* out);           /* :248-314 */
+void lo_q4k_to_q4kf(const uint8_t* q4k, size_t nblocks, uint8_t* out);        /* :370-413 */
+/* Lossless 148-byte Q4_K -> 144-byte llama.cpp layout (the 4-bit mins fit the 6-bit field):
+ * test data for the GGUF path whose dequantized values equal the Q4_K block's. */
+void lo_q4k_to_gguf_llamacpp(const uint8_t* q4k, size_t nblocks, uint8_t* out);
+
 /* LC/src/cpu/ops/q8_matvec.rs:36-62 */
 void lo_q8_matvec(const int8_t* wq, const float* ws, const int8_t* xq, const float* xs,
                   float* out, size_t rows, size_t hidden);
@@ -93,7 +116,8 @@ typedef struct {
     const uint8_t *wq, *wk, *wv, *wo, *gate, *up, *down;  /* Q4_K 148-byte or Q6_K 210-byte layout */
     const float *input_norm, *post_attn_norm;
     uint16_t *k_cache, *v_cache;                             /* [max_seq][kv_heads][head_dim] fp16 */
-    /* per projection (wq, wk, wv, wo, gate, up, down): 0 = Q4_K, 1 = Q6_K; mixed formats
+    /* per projection (wq, wk, wv, wo, gate, up, down): 0 = Q4_K, 1 = Q6_K, 2 = Q4_KF 144-byte
+     * GGUF, 3 = Q4_KF 160-byte; mixed formats
      * per projection as the reference's per-layer QuantWeight allows (LC/src/pipeline.rs:22-27) */
     int fmt[7];
     const float *pre_ffn_norm, *post_ffn_norm;  /* NULL: norm without weight (LI/src/forward/layer.rs:65-68) */

@@ -30,8 +30,26 @@ def q6k(rows, cols, seed, std=0.02):
     return oracle.quantize_q6_k(oracle.gauss(seed, rows * cols, 0.0, std))
 
 
+def q4kf(rows, cols, seed, std=0.02):
+    """Q4_KF, 144-byte GGUF (llama.cpp layout): Q4_K converted losslessly, then bits 4..5 of
+    every 6-bit min set at random so mins above 15 occur."""
+    g = oracle.q4k_to_gguf_llamacpp(q4k(rows, cols, seed, std)).reshape(-1, 144)
+    rng = np.random.default_rng(seed)
+    g[:, 8:12] |= ((rng.integers(0, 4, (g.shape[0], 4)) << 4) | (rng.integers(0, 4, (g.shape[0], 4)) << 6)).astype(np.uint8)
+    return g.reshape(-1)
+
+
+def q4kf160(rows, cols, seed, std=0.02):
+    """Q4_KF, 160-byte pre-baked half scales (the reference's q4k_to_q4kf)."""
+    return oracle.q4k_to_q4kf(q4k(rows, cols, seed, std))
+
+
+MAKERS = {"q4_k": q4k, "q6_k": q6k, "q4_kf": q4kf, "q4_kf160": q4kf160}
+HIP_FORMAT = {"q6_k": larql_hip.Q6_K, "q4_kf": larql_hip.Q4_KF, "q4_kf160": larql_hip.Q4_KF}
+
+
 class SmallModel:
-    """formats: projection name -> "q6_k" for Q6_K weights (default Q4_K).  variant: layer
+    """formats: projection name -> "q6_k" / "q4_kf" / "q4_kf160" (default Q4_K).  variant: layer
     variants of FullPipelineLayer (larql-compute/src/pipeline.rs:76-115) in the oracle's
     keys: norm_offset, has_post_norms (with pre/post-FFN norm weights unless
     ffn_norm_weights=False), activation ("silu" | "gelu_tanh"), has_v_norm, layer_scalar,
@@ -50,7 +68,7 @@ class SmallModel:
             s = seed + 100 * l
             L = {}
             for i, (name, (r, c)) in enumerate(shapes.items()):
-                L[name] = (q6k if self.formats.get(name) == "q6_k" else q4k)(r, c, s + 1 + i)
+                L[name] = MAKERS[self.formats.get(name, "q4_k")](r, c, s + 1 + i)
             L.update(input_norm=(1.0 + 0.1 * oracle.gauss(s + 8, hidden)).astype(np.float32),
                      post_attn_norm=(1.0 + 0.1 * oracle.gauss(s + 9, hidden)).astype(np.float32),
                      k_cache=np.zeros(cap * kvd, np.uint16), v_cache=np.zeros(cap * kvd, np.uint16),
@@ -61,7 +79,7 @@ class SmallModel:
             self.layers.append(L)
 
     def hip_layers(self, rope_base, window=0):
-        fm = {k: larql_hip.Q6_K for k, v in self.formats.items() if v == "q6_k"}
+        fm = {k: HIP_FORMAT[v] for k, v in self.formats.items() if v in HIP_FORMAT}
         v = self.variant
         act = larql_hip.ACT_GELU_TANH if v.get("activation") == "gelu_tanh" else larql_hip.ACT_SILU
         return [larql_hip.make_layer(L["wq"], L["wk"], L["wv"], L["wo"], L["gate"], L["up"], L["down"],
@@ -146,6 +164,38 @@ def test_decode_mixed_projection_formats(hip, formats):
     # Q4_K_M-style layers: some projections Q6_K (split Q|K|V launches, gate then up with
     # silu(gate) * up in the up epilogue)
     run_sequence(hip, T0=40, n_tokens=2, n_layers=2, formats=formats)
+
+
+@pytest.mark.parametrize("formats", [
+    {"gate": "q4_kf", "up": "q4_kf", "down": "q4_kf"},               # Q4_K attention, GGUF FFN
+    {n: "q4_kf" for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")},
+    {n: "q4_kf160" for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")},
+    {"wq": "q4_kf", "wk": "q4_kf160", "wv": "q6_k", "gate": "q4_kf160", "up": "q4_kf"},
+])
+def test_decode_q4kf_layers(hip, formats):
+    """Q4_KF projections in both byte layouts (144-byte GGUF as the reference's GPU decode
+    reads it, 160-byte pre-baked), fused where a group shares format and layout, split
+    otherwise; decode against the oracle layer."""
+    run_sequence(hip, T0=30, n_tokens=2, n_layers=2, formats=formats)
+
+
+def test_prefill_q4_q4kf_layers(hip):
+    """A prompt through Q4_KF layers (run position by position through the decode kernels)."""
+    n_layers, hidden, inter, nq, nkv, hd, seq = 2, 512, 1024, 8, 2, 64, 7
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=19,
+                   formats={"gate": "q4_kf", "up": "q4_kf", "down": "q4_kf", "wo": "q4_kf160"})
+    layers = m.hip_layers(10000.0)
+    x = np.stack([oracle.gauss(880 + p, hidden) for p in range(seq)])
+    hip.reset_kv_cache()
+    got = hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0)
+    worst = 0.0
+    for p in range(seq):
+        ref = x[p].copy()
+        for L in m.layers:
+            ref = oracle.decode_layer(L, ref, p, hidden, inter, nq, nkv, hd, 10000.0)
+        worst = max(worst, rel_err(got[p], ref))
+    print(f"[prefill q4kf] worst rel_err={worst:.3e}", flush=True)
+    assert worst <= REL_TOL
 
 
 VARIANTS = [

@@ -828,3 +828,98 @@ def _inputs_of(P, dims, pos, seed):
     vc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
     h = rng.standard_normal(hidden).astype(np.float32)
     return h, kc, vc, pos, dims
+
+
+# ── Q4_KF: GGUF 144-byte (llama.cpp layout) and 160-byte pre-baked ─────────
+# Scales sc = 1, 2, 3, 4, 33, 47, 50, 63 and mins m = 5, 6, 7, 8, 17, 31, 42, 60 packed by
+# hand in the llama.cpp layout: byte j (j < 4) = sc_j | (sc_{j+4} >> 4) << 6, byte 4 + j =
+# m_j | (m_{j+4} >> 4) << 6, byte 8 + j = (sc_{j+4} & 15) | (m_{j+4} & 15) << 4.
+_GGUF_SC = (1, 2, 3, 4, 33, 47, 50, 63)
+_GGUF_M = (5, 6, 7, 8, 17, 31, 42, 60)
+_GGUF_Q12 = bytes([0x81, 0x82, 0xC3, 0xC4, 0x45, 0x46, 0x87, 0xC8, 0x11, 0xFF, 0xA2, 0xCF])
+
+
+def test_gguf_scale_min_known_answer():
+    q12 = np.frombuffer(_GGUF_Q12, np.uint8)
+    for j in range(8):
+        assert oracle.gguf_scale_min(j, q12) == (_GGUF_SC[j], _GGUF_M[j]), j
+
+
+def test_q4kf_gguf_onehot_probes_closed_form():
+    """Element e of a llama.cpp block: chunk c = e // 64 of 32 bytes, low nibbles first
+    (sub-block 2c), then high nibbles (2c + 1); w = d sc_j q - dmin m_j."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    blk[2:4] = np.array([0.25], np.float16).view(np.uint8)
+    blk[4:16] = np.frombuffer(_GGUF_Q12, np.uint8)
+    blk[16:] = (np.arange(128) * 37 % 256).astype(np.uint8)
+    for e in (0, 1, 31, 32, 33, 63, 64, 95, 96, 130, 191, 192, 224, 255):
+        c, l = divmod(e, 64)
+        q = (blk[16 + 32 * c + l] & 15) if l < 32 else (blk[16 + 32 * c + l - 32] >> 4)
+        j = e // 32
+        want = np.float32(np.float32(0.5) * np.float32(_GGUF_SC[j])) * np.float32(q) - \
+            np.float32(np.float32(0.25) * np.float32(_GGUF_M[j]))
+        x = np.zeros(256, np.float32)
+        x[e] = 1.0
+        assert oracle.q4kf_gguf_matvec(blk, x, 1, 256)[0] == want, e
+
+
+def test_q4k_to_llamacpp_gguf_is_lossless():
+    """The 148 -> llama.cpp-144 converter (test data for the GGUF path) keeps every
+    dequantized value: the GGUF matvec of converted bytes equals the Q4_K matvec bit for
+    bit (same element order), also on fuzzed bytes with the unused scale bits set."""
+    rng = np.random.default_rng(40)
+    rows, cols = 24, 1024
+    q = oracle.quantize_q4_k((rng.standard_normal(rows * cols) * 0.02).astype(np.float32))
+    fz = rng.integers(0, 256, q.size, dtype=np.uint8)
+    fz.reshape(-1, 148)[:, 1] &= 0x3B                              # finite, modest d
+    fz.reshape(-1, 148)[:, 3] &= 0x3B                              # and dmin
+    x = rng.standard_normal(cols).astype(np.float32)
+    for blocks in (q, fz):
+        a = oracle.q4k_matvec(blocks, x, rows, cols)
+        b = oracle.q4kf_gguf_matvec(oracle.q4k_to_gguf_llamacpp(blocks), x, rows, cols)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_q4kf160_known_answer_and_onehot():
+    """q4k_to_q4kf (q4_common.rs:370-413) of the hand block A above: d sc_j = 0.25 x (63, 4,
+    0, 3, 16, 6, 25, 20) and dmin m_j = 0.5 x (15, 2, 0, 0, 6, 7, 3, 4), all exact in f16;
+    the 128 nibble bytes copied."""
+    q4k = np.frombuffer(_Q4K_A_BYTES, np.uint8)
+    kf = oracle.q4k_to_q4kf(q4k)
+    sc = np.array([15.75, 1.0, 0.0, 0.75, 4.0, 1.5, 6.25, 5.0], np.float16)
+    mn = np.array([7.5, 1.0, 0.0, 0.0, 3.0, 3.5, 1.5, 2.0], np.float16)
+    assert kf[:16].tobytes() == sc.tobytes() and kf[16:32].tobytes() == mn.tobytes()
+    assert kf[32:].tobytes() == _Q4K_A_BYTES[20:]
+    for e in (0, 1, 33, 34, 130, 255):
+        j, w = divmod(e, 32)
+        byte = kf[32 + 16 * j + w // 2]
+        q = (byte >> 4) if w % 2 else (byte & 15)
+        x = np.zeros(256, np.float32)
+        x[e] = 1.0
+        assert oracle.q4kf160_matvec(kf, x, 1, 256)[0] == np.float32(sc[j]) * np.float32(q) - np.float32(mn[j])
+
+
+def test_reference_gguf_packing_known_answers():
+    """The reference's own GGUF writers (q4_common.rs:248-361) pack 6-bit mins as byte j =
+    sc_j | (m_j & 3) << 6 and byte 8 + j = (m_2j >> 2) | (m_2j+1 >> 2) << 4, and keep the
+    148-byte nibble order.  Block A (sc 63, 4, 0, 3, 16, 6, 25, 20; m 15, 2, 0, 0, 6, 7, 3, 4)
+    through q4k_to_gguf: FF 84 00 03 90 C6 D9 14 03 00 11 10.  quantize_q4_k_gguf of block A's
+    input: dmin = fl(7.5 / 63) = 0.11904762 -> f16 0x2F9E (truncated), m_j = round(-min_j /
+    dmin) = 63, 8 (8.4), 0, 0 (-2.1), 25 (25.2), 29 (29.4), 11 (10.5 half away), 17 (16.8).
+    Read back with the llama.cpp unpack these bytes give other scales and mins (the
+    reference's GPU kernels and its writers disagree); this build reads Q4_KF as the GPU
+    kernels do."""
+    g = oracle.q4k_to_gguf(np.frombuffer(_Q4K_A_BYTES, np.uint8))
+    assert g[:4].tobytes() == _Q4K_A_BYTES[:4]
+    assert g[4:16].tobytes() == bytes([0xFF, 0x84, 0x00, 0x03, 0x90, 0xC6, 0xD9, 0x14, 0x03, 0x00, 0x11, 0x10])
+    assert g[16:].tobytes() == _Q4K_A_BYTES[20:]
+    assert oracle.gguf_scale_min(4, g[4:16]) != (16, 6)
+    q = oracle.quantize_q4_k_gguf(_spec_block(_Q4K_A_SPEC))
+    assert q[:16].tobytes() == bytes([0x00, 0x34, 0x9E, 0x2F, 0xFF, 0x04, 0x00, 0x03, 0x50, 0x46, 0xD9, 0x54,
+                                      0x2F, 0x00, 0x76, 0x42])
+    # nibbles q = round((x + dmin m_j) / (d sc_j)): sub-block 1 (d sc = 1, dmin m = 0.952):
+    # x = 0 -> 1, -0.5 -> 0.45 -> 0, -0.25 -> 0.70 -> 1; sub-block 4 (d sc = 4, dmin m = 2.976):
+    # x = 1 -> 0.99 -> 1, -1 -> 0.49 -> 0, fill 0 -> 0.74 -> 1
+    assert list(q[32:36]) == [0x10, 0x10, 0x00, 0x00]
+    assert list(q[80:84]) == [0x10, 0x10, 0x11, 0x11]
