@@ -59,6 +59,10 @@ struct larql_hip_model {
     float *h0 = nullptr, *h1 = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *xin = nullptr;
     float* gtmp = nullptr;  // gate projection when gate and up have different formats
     float* otmp = nullptr;  // post-norm layers: attention / FFN output before its norm
+    float* utmp = nullptr;  // up projection of a Q8-input FFN
+    float* xn = nullptr;    // normed input of a Q8-input projection
+    int8_t* q8 = nullptr;   // Q8 activation of a Q8-input projection (quantize_to_q8)
+    float* q8s = nullptr;
     float* ones = nullptr;  // weight of the weight-free norm in a fused matvec prologue
     larql::DeviceBuf part;
     larql::DeviceBuf prompt;  // batched prompt pass: activations of all positions
@@ -79,15 +83,19 @@ struct Src {
     const void* data;
     size_t len;
     size_t rows;
+    const float* scales = nullptr;  // Q8_0: f32 scales [rows][cols / 32]
 };
 
 // One device weight from one or more reference-layout sources: concatenated by rows
 // (stride 1) or interleaved (source i -> rows i, i+n, ...).
 DevWeight build_weight(larql_hip_ctx* c, larql_hip_model* m, int format, size_t cols, const std::vector<Src>& srcs,
                        bool interleave, bool on_device) {
-    if (format != LARQL_Q4_K && format != LARQL_Q6_K && format != LARQL_Q4_KF)
-        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: projections must be Q4_K, Q4_KF or Q6_K");
-    if (cols % 256) fail(LARQL_HIP_ERR_INVALID, "decode: projection input width must be a multiple of 256");
+    const bool int_fmt = format == LARQL_Q8_0 || format == LARQL_Q4_0;
+    if (format != LARQL_Q4_K && format != LARQL_Q6_K && format != LARQL_Q4_KF && !int_fmt)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: projections must be Q4_K, Q4_KF, Q6_K, Q8_0 or Q4_0");
+    if (cols % (int_fmt ? 32 : 256))
+        fail(LARQL_HIP_ERR_INVALID, "decode: projection input width must be a multiple of the block size");
+    if (int_fmt && interleave) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: interleaved Q8_0 / Q4_0 weights");
     // Q4_KF: 144-byte GGUF or 160-byte pre-baked blocks, told apart by length; the sources
     // of one fused weight must agree
     const int hf = format == LARQL_Q4_KF ? larql::q4kf_form(srcs[0].len, srcs[0].rows, cols) : larql::kHdr148;
@@ -98,6 +106,7 @@ DevWeight build_weight(larql_hip_ctx* c, larql_hip_model* m, int format, size_t 
             fail(LARQL_HIP_ERR_INVALID, "decode: fused Q4_KF projections mix the 144- and 160-byte layouts");
         if (s.len < s.rows * larql::ref_row_bytes(format, cols, hf))
             fail(LARQL_HIP_ERR_INVALID, "decode: weight buffer shorter than its shape");
+        if (format == LARQL_Q8_0 && !s.scales) fail(LARQL_HIP_ERR_INVALID, "decode: Q8_0 weight without scales");
         if (interleave && s.rows != srcs[0].rows) fail(LARQL_HIP_ERR_INVALID, "decode: gate/up shapes differ");
         rows += s.rows;
     }
@@ -115,14 +124,21 @@ DevWeight build_weight(larql_hip_ctx* c, larql_hip_model* m, int format, size_t 
     for (size_t i = 0; i < srcs.size(); i++) {
         const Src& s = srcs[i];
         const size_t nbytes = s.rows * larql::ref_row_bytes(format, cols, hf);
+        const size_t sbytes = format == LARQL_Q8_0 ? s.rows * (cols / 32) * sizeof(float) : 0;
         const uint8_t* raw = static_cast<const uint8_t*>(s.data);
+        const float* sc = s.scales;
         if (!on_device) {
-            uint8_t* stage = static_cast<uint8_t*>(larql::ensure(c, c->stage_raw, nbytes));
+            const size_t soff = (nbytes + 255) & ~size_t(255);
+            uint8_t* stage = static_cast<uint8_t*>(larql::ensure(c, c->stage_raw, soff + sbytes));
             LARQL_HIP_CHECK(hipMemcpyAsync(stage, s.data, nbytes, hipMemcpyHostToDevice, c->stream));
+            if (sbytes) {
+                LARQL_HIP_CHECK(hipMemcpyAsync(stage + soff, s.scales, sbytes, hipMemcpyHostToDevice, c->stream));
+                sc = reinterpret_cast<const float*>(stage + soff);
+            }
             raw = stage;
         }
-        if (interleave) larql::launch_repack(w, raw, nullptr, c->stream, s.rows, i, srcs.size());
-        else larql::launch_repack(w, raw, nullptr, c->stream, s.rows, row0, 1);
+        if (interleave) larql::launch_repack(w, raw, sc, c->stream, s.rows, i, srcs.size());
+        else larql::launch_repack(w, raw, sc, c->stream, s.rows, row0, 1);
         row0 += s.rows;
         LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));  // the staging buffer is reused
     }
@@ -194,24 +210,34 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
             d.split_qkv = form(L.wq, qd, hidden) != form(L.wk, kvd, hidden) ||
                           form(L.wq, qd, hidden) != form(L.wv, kvd, hidden);
             if (d.split_qkv) {
-                d.wq = build_weight(c, m, L.wq.format, hidden, {{L.wq.data, L.wq.len, qd}}, false, on_device);
-                d.wk = build_weight(c, m, L.wk.format, hidden, {{L.wk.data, L.wk.len, kvd}}, false, on_device);
-                d.wv = build_weight(c, m, L.wv.format, hidden, {{L.wv.data, L.wv.len, kvd}}, false, on_device);
+                d.wq = build_weight(c, m, L.wq.format, hidden, {{L.wq.data, L.wq.len, qd, L.wq.scales}}, false,
+                                    on_device);
+                d.wk = build_weight(c, m, L.wk.format, hidden, {{L.wk.data, L.wk.len, kvd, L.wk.scales}}, false,
+                                    on_device);
+                d.wv = build_weight(c, m, L.wv.format, hidden, {{L.wv.data, L.wv.len, kvd, L.wv.scales}}, false,
+                                    on_device);
             } else {
                 d.qkv = build_weight(c, m, L.wq.format, hidden,
-                                     {{L.wq.data, L.wq.len, qd}, {L.wk.data, L.wk.len, kvd}, {L.wv.data, L.wv.len, kvd}},
+                                     {{L.wq.data, L.wq.len, qd, L.wq.scales},
+                                      {L.wk.data, L.wk.len, kvd, L.wk.scales},
+                                      {L.wv.data, L.wv.len, kvd, L.wv.scales}},
                                      false, on_device);
             }
-            d.wo = build_weight(c, m, L.wo.format, qd, {{L.wo.data, L.wo.len, hidden}}, false, on_device);
-            d.split_gu = form(L.gate, inter, hidden) != form(L.up, inter, hidden);
+            d.wo = build_weight(c, m, L.wo.format, qd, {{L.wo.data, L.wo.len, hidden, L.wo.scales}}, false, on_device);
+            // the Q8-input formats have no fused gate/up epilogue: their gate and up run apart
+            d.split_gu = form(L.gate, inter, hidden) != form(L.up, inter, hidden) || L.gate.format == LARQL_Q8_0 ||
+                         L.gate.format == LARQL_Q4_0;
             if (d.split_gu) {
-                d.gate = build_weight(c, m, L.gate.format, hidden, {{L.gate.data, L.gate.len, inter}}, false, on_device);
-                d.up = build_weight(c, m, L.up.format, hidden, {{L.up.data, L.up.len, inter}}, false, on_device);
+                d.gate = build_weight(c, m, L.gate.format, hidden, {{L.gate.data, L.gate.len, inter, L.gate.scales}},
+                                      false, on_device);
+                d.up = build_weight(c, m, L.up.format, hidden, {{L.up.data, L.up.len, inter, L.up.scales}}, false,
+                                    on_device);
             } else {
                 d.gateup = build_weight(c, m, L.gate.format, hidden,
                                         {{L.gate.data, L.gate.len, inter}, {L.up.data, L.up.len, inter}}, true, on_device);
             }
-            d.down = build_weight(c, m, L.down.format, inter, {{L.down.data, L.down.len, hidden}}, false, on_device);
+            d.down = build_weight(c, m, L.down.format, inter, {{L.down.data, L.down.len, hidden, L.down.scales}}, false,
+                                  on_device);
             d.input_norm = upload_vec(c, m, L.input_norm, hidden, on_device);
             d.post_attn_norm = upload_vec(c, m, L.post_attn_norm, hidden, on_device);
             d.norm_offset = L.norm_offset;
@@ -235,6 +261,11 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
         m->act = static_cast<float*>(dev_alloc(m, inter * 4));
         m->gtmp = static_cast<float*>(dev_alloc(m, inter * 4));
         m->otmp = static_cast<float*>(dev_alloc(m, hidden * 4));
+        m->utmp = static_cast<float*>(dev_alloc(m, inter * 4));
+        m->xn = static_cast<float*>(dev_alloc(m, hidden * 4));
+        const size_t widest = std::max({hidden, inter, m->q_dim});
+        m->q8 = static_cast<int8_t*>(dev_alloc(m, widest));
+        m->q8s = static_cast<float*>(dev_alloc(m, widest / 32 * 4 + 4));
         {
             std::vector<float> one(hidden, 1.0f);
             m->ones = static_cast<float*>(dev_alloc(m, hidden * 4));
@@ -260,13 +291,15 @@ void destroy_model(larql_hip_ctx* c, larql_hip_model* m) {
 }
 
 // ── KV cache ───────────────────────────────────────────────────────────
-void kv_free(larql_hip_ctx* c) {
+void kv_free_cache(larql::KVCache& kv) {
     (void)hipDeviceSynchronize();
-    for (auto* p : c->kv.k) (void)hipFree(p);
-    for (auto* p : c->kv.v) (void)hipFree(p);
-    for (auto& r : c->kv.rope) (void)hipFree(r.cs);
-    c->kv = larql::KVCache{};
+    for (auto* p : kv.k) (void)hipFree(p);
+    for (auto* p : kv.v) (void)hipFree(p);
+    for (auto& r : kv.rope) (void)hipFree(r.cs);
+    kv = larql::KVCache{};
 }
+
+void kv_free(larql_hip_ctx* c) { kv_free_cache(c->kv); }
 
 // RoPE cos/sin table for (base, rdim) covering the cache capacity; built once per
 // capacity (the cache only grows), on stream s, which is then synchronised so the
@@ -336,6 +369,30 @@ void kv_ensure(larql_hip_ctx* c, size_t layers, size_t num_kv, size_t head_dim, 
     }
 }
 
+// Formats whose kernels take a Q8 activation (quantize_to_q8 of the f32 input): Q8_0, and
+// Q4_0 except as the down projection, which takes the f32 activation
+// (LC/src/metal/decode.rs:262-296, 374-404, 560-690).
+bool takes_q8(const DevWeight& w, bool is_down) {
+    return w.format == LARQL_Q8_0 || (w.format == LARQL_Q4_0 && !is_down);
+}
+
+// The model's Q8 activation: quantize_to_q8 of x[n], or of its norm when norm_w is given.
+void quantize_input(larql_hip_model* m, const float* x, size_t n, const float* norm_w, float off, double eps,
+                    hipStream_t s) {
+    const float* src = x;
+    if (norm_w) {
+        larql::launch_rmsnorm_rows(x, norm_w, off, m->xn, 1, n, eps, s);
+        src = m->xn;
+    }
+    larql::launch_quantize_q8(src, n, 1, m->q8, m->q8s, s);
+}
+
+// out = W . (the model's Q8 activation), blocks accumulated in order (bit-exact int dots).
+void int_proj(const DevWeight& w, larql_hip_model* m, float* out, hipStream_t s) {
+    if (w.format == LARQL_Q8_0) larql::launch_q8_matvec(w, m->q8, m->q8s, out, 1, s);
+    else larql::launch_q4_0_matvec(w, m->q8, m->q8s, out, 1, s);
+}
+
 void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float* hidden_out, float* logits,
                 hipStream_t s) {
     auto& kv = c->kv;
@@ -347,20 +404,30 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
     larql::launch_copy_f32(x_dev, m->h0, m->hidden, s);
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
-        larql::MvArgs a;
-        a.x = m->h0;
-        a.out = m->qkv;
-        a.norm_w = L.input_norm;
-        a.norm_offset = L.norm_offset;
-        a.eps = L.eps;
-        if (L.split_qkv) {  // three launches into the [q | k | v] buffer, each with the norm
-            larql::launch_mv(L.wq, a, s);
-            a.out = m->qkv + m->q_dim;
-            larql::launch_mv(L.wk, a, s);
-            a.out = m->qkv + m->q_dim + m->kv_dim;
-            larql::launch_mv(L.wv, a, s);
+        // Q/K/V: f32-input formats with the input norm fused into the matvec; Q8_0 from the
+        // quantized normed input (one quantization shared by the three)
+        bool have_q8 = false;
+        auto qkv_proj = [&](const DevWeight& w, float* out) {
+            if (takes_q8(w, false)) {
+                if (!have_q8) quantize_input(m, m->h0, m->hidden, L.input_norm, L.norm_offset, L.eps, s);
+                have_q8 = true;
+                int_proj(w, m, out, s);
+            } else {
+                larql::MvArgs a;
+                a.x = m->h0;
+                a.out = out;
+                a.norm_w = L.input_norm;
+                a.norm_offset = L.norm_offset;
+                a.eps = L.eps;
+                larql::launch_mv(w, a, s);
+            }
+        };
+        if (L.split_qkv) {  // three launches into the [q | k | v] buffer
+            qkv_proj(L.wq, m->qkv);
+            qkv_proj(L.wk, m->qkv + m->q_dim);
+            qkv_proj(L.wv, m->qkv + m->q_dim + m->kv_dim);
         } else {
-            larql::launch_mv(L.qkv, a, s);
+            qkv_proj(L.qkv, m->qkv);
         }
         if (L.v_norm) larql::launch_vnorm_rows(m->qkv + m->q_dim + m->kv_dim, 1, 0, L.nkv, L.hd, L.eps, s);
 
@@ -381,32 +448,63 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
         larql::launch_attention(at, s);
 
         // h1 = h + o (Llama), or h + norm(o, post_attn_norm) for post-norm layers
-        larql::MvArgs o;
-        o.x = m->attn;
-        if (L.post_norms) {
-            o.out = m->otmp;
-            larql::launch_mv(L.wo, o, s);
-            larql::launch_resid_norm_rows(m->h0, m->otmp, L.post_attn_norm, L.norm_offset, 1.0f, m->h1, 1, m->hidden,
-                                          L.eps, s);
+        const bool o_q8 = takes_q8(L.wo, false);
+        if (L.post_norms || o_q8) {
+            if (o_q8) {
+                quantize_input(m, m->attn, m->q_dim, nullptr, 0.f, L.eps, s);
+                int_proj(L.wo, m, m->otmp, s);
+            } else {
+                larql::MvArgs o;
+                o.x = m->attn;
+                o.out = m->otmp;
+                larql::launch_mv(L.wo, o, s);
+            }
+            if (L.post_norms)
+                larql::launch_resid_norm_rows(m->h0, m->otmp, L.post_attn_norm, L.norm_offset, 1.0f, m->h1, 1,
+                                              m->hidden, L.eps, s);
+            else
+                larql::launch_add_rows(m->h0, m->otmp, m->h1, m->hidden, s);
         } else {
+            larql::MvArgs o;
+            o.x = m->attn;
             o.out = m->h1;
             o.epi = larql::EPI_RESID;
             o.resid = m->h0;
             larql::launch_mv(L.wo, o, s);
         }
 
+        // FFN input norm: post_attn_norm, or pre_ffn_norm (weight-free when absent) for
+        // post-norm layers
+        const float* fnorm = L.post_attn_norm;
+        float foff = L.norm_offset;
+        if (L.post_norms) {
+            fnorm = L.pre_ffn_norm ? L.pre_ffn_norm : m->ones;
+            foff = L.pre_ffn_norm ? L.norm_offset : 0.0f;
+        }
         larql::MvArgs g;
         g.x = m->h1;
         g.out = m->act;
         g.act = L.act;
         g.eps = L.eps;
-        g.norm_w = L.post_attn_norm;
-        g.norm_offset = L.norm_offset;
-        if (L.post_norms) {  // FFN input: norm(h1, pre_ffn_norm), weight-free when absent
-            g.norm_w = L.pre_ffn_norm ? L.pre_ffn_norm : m->ones;
-            g.norm_offset = L.pre_ffn_norm ? L.norm_offset : 0.0f;
-        }
-        if (L.split_gu) {  // gate, then up with act(gate) * up in its epilogue
+        g.norm_w = fnorm;
+        g.norm_offset = foff;
+        const bool g_q8 = !L.split_gu ? false : takes_q8(L.gate, false), u_q8 = !L.split_gu ? false : takes_q8(L.up, false);
+        if (g_q8 || u_q8) {  // gate and up apart, then act(gate) * up
+            quantize_input(m, m->h1, m->hidden, fnorm, foff, L.eps, s);
+            float* outs[2] = {m->gtmp, m->utmp};
+            const DevWeight* ws[2] = {&L.gate, &L.up};
+            for (int i = 0; i < 2; i++) {
+                if (takes_q8(*ws[i], false)) {
+                    int_proj(*ws[i], m, outs[i], s);
+                } else {
+                    larql::MvArgs gi = g;
+                    gi.out = outs[i];
+                    gi.epi = larql::EPI_STORE;
+                    larql::launch_mv(*ws[i], gi, s);
+                }
+            }
+            larql::launch_gated_mul(m->gtmp, m->utmp, m->act, m->inter, L.act, s);
+        } else if (L.split_gu) {  // gate, then up with act(gate) * up in its epilogue
             g.out = m->gtmp;
             larql::launch_mv(L.gate, g, s);
             g.out = m->act;
@@ -420,14 +518,27 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
 
         // h2 = (h1 + down) or (h1 + norm(down, post_ffn_norm)), times the layer scalar
         const float scale = L.layer_scalar != 0.0f ? L.layer_scalar : 1.0f;
-        larql::MvArgs d;
-        d.x = m->act;
-        if (L.post_norms) {
-            d.out = m->otmp;
-            larql::launch_mv(L.down, d, s);
-            larql::launch_resid_norm_rows(m->h1, m->otmp, L.post_ffn_norm, L.post_ffn_norm ? L.norm_offset : 0.0f,
-                                          scale, m->h0, 1, m->hidden, L.eps, s);
+        const bool d_int = L.down.format == LARQL_Q4_0 || L.down.format == LARQL_Q8_0;
+        if (L.post_norms || d_int) {
+            if (L.down.format == LARQL_Q4_0) {  // f32 activation (the reference's q4_f32_matvec)
+                larql::launch_q4_0_f32_matvec(L.down, m->act, m->otmp, s);
+            } else if (L.down.format == LARQL_Q8_0) {
+                quantize_input(m, m->act, m->inter, nullptr, 0.f, L.eps, s);
+                int_proj(L.down, m, m->otmp, s);
+            } else {
+                larql::MvArgs d;
+                d.x = m->act;
+                d.out = m->otmp;
+                larql::launch_mv(L.down, d, s);
+            }
+            if (L.post_norms)
+                larql::launch_resid_norm_rows(m->h1, m->otmp, L.post_ffn_norm, L.post_ffn_norm ? L.norm_offset : 0.0f,
+                                              scale, m->h0, 1, m->hidden, L.eps, s);
+            else
+                larql::launch_add_rows(m->h1, m->otmp, m->h0, m->hidden, s, scale);
         } else {
+            larql::MvArgs d;
+            d.x = m->act;
             d.out = m->h0;
             d.epi = larql::EPI_RESID;
             d.resid = m->h1;
@@ -639,6 +750,73 @@ extern "C" int larql_hip_prefill_q4(larql_hip_ctx* c, const larql_pipeline_layer
     });
 }
 
+extern "C" int larql_hip_full_pipeline_q4(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t num_layers,
+                                          const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim,
+                                          size_t seq_len, size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
+                                          float rope_base, int use_qk_norm, float softcap, float* out) {
+    return guarded(c, [&] {
+        if (!layers || !x || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        if (use_qk_norm || softcap != 0.f)
+            fail(LARQL_HIP_ERR_UNSUPPORTED, "full pipeline: QK-norm / softcap not supported");
+        if (num_q_heads * head_dim != q_dim || num_kv_heads * head_dim != kv_dim)
+            fail(LARQL_HIP_ERR_INVALID, "full pipeline: q_dim/kv_dim do not match the head geometry");
+        (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
+        if (seq_len == 0) return;
+        larql_hip_model* m = trait_model_for(c, layers, num_layers, hidden, inter);
+        if (m->q_dim != q_dim || m->kv_dim != kv_dim)
+            fail(LARQL_HIP_ERR_INVALID, "full pipeline: layer geometry differs from q_dim/kv_dim");
+        // positions 0 .. seq_len - 1 with causal attention over each other only: run against
+        // the set-aside cache, then restore the decode cache whatever happens
+        std::swap(c->kv, c->kv_aside);
+        struct Restore {
+            larql_hip_ctx* c;
+            ~Restore() { std::swap(c->kv, c->kv_aside); }
+        } restore{c};
+        kv_ensure(c, m->layers.size(), m->nkv, m->hd, seq_len);
+        c->kv.current_len = 0;
+        const float* dx = stage_upload(c, c->stage_in, x, seq_len * hidden);
+        float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, seq_len * hidden * sizeof(float)));
+        if (seq_len > 1 && prompt_batchable(m))
+            run_prompt(c, m, dx, seq_len, dout, c->stream);
+        else
+            for (size_t p = 0; p < seq_len; p++)
+                run_decode(c, m, dx + p * hidden, dout + p * hidden, nullptr, c->stream);
+        download(c, out, dout, seq_len * hidden * sizeof(float));
+    });
+}
+
+extern "C" int larql_hip_multi_layer_q4_ffn(larql_hip_ctx* c, const larql_q4_ffn_layer* layers, size_t num_layers,
+                                           const float* x, size_t inter, size_t hidden, float* out) {
+    return guarded(c, [&] {
+        if (!layers || !x || !out || num_layers == 0) fail(LARQL_HIP_ERR_INVALID, "null pointer or no layers");
+        if (hidden % 32 || inter % 32 || hidden == 0 || inter == 0)
+            fail(LARQL_HIP_ERR_INVALID, "multi-layer FFN: hidden and inter must be multiples of 32");
+        // work: x ping-pong [2][hidden], gate, up, act [inter], Q8 activation
+        const size_t nf = 2 * hidden + 3 * inter + hidden / 32;
+        const size_t q8_off = (nf * sizeof(float) + 255) & ~size_t(255);
+        uint8_t* raw = static_cast<uint8_t*>(larql::ensure(c, c->ffn_work, q8_off + hidden));
+        float* base = reinterpret_cast<float*>(raw);
+        float *X[2] = {base, base + hidden}, *G = base + 2 * hidden, *U = G + inter, *A = U + inter;
+        float* q8s = A + inter;
+        int8_t* q8 = reinterpret_cast<int8_t*>(raw + q8_off);
+        LARQL_HIP_CHECK(hipMemcpyAsync(X[0], x, hidden * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        for (size_t l = 0; l < num_layers; l++) {
+            const larql_q4_ffn_layer& L = layers[l];
+            if (!L.gate || !L.up || !L.down) fail(LARQL_HIP_ERR_INVALID, "multi-layer FFN: null weight");
+            const DevWeight& gw = larql::cached_weight(c, LARQL_Q4_0, L.gate, L.gate_len, nullptr, inter, hidden);
+            const DevWeight& uw = larql::cached_weight(c, LARQL_Q4_0, L.up, L.up_len, nullptr, inter, hidden);
+            const DevWeight& dw = larql::cached_weight(c, LARQL_Q4_0, L.down, L.down_len, nullptr, hidden, inter);
+            float *xin = X[l & 1], *xout = X[(l + 1) & 1];
+            larql::launch_quantize_q8(xin, hidden, 1, q8, q8s, c->stream);
+            larql::launch_q4_0_matvec(gw, q8, q8s, G, 1, c->stream);
+            larql::launch_q4_0_matvec(uw, q8, q8s, U, 1, c->stream);
+            larql::launch_gated_mul(G, U, A, inter, LARQL_ACT_SILU, c->stream);
+            larql::launch_q4_0_f32_matvec(dw, A, xout, c->stream);
+        }
+        download(c, out, X[num_layers & 1], hidden * sizeof(float));
+    });
+}
+
 extern "C" int larql_hip_populate_kv_layer(larql_hip_ctx* c, size_t layer, const float* k_data, const float* v_data,
                                            size_t seq_len, size_t num_kv_heads, size_t head_dim) {
     return guarded(c, [&] {
@@ -745,4 +923,5 @@ void larql_hip_decode_release(larql_hip_ctx* c) {
     destroy_model(c, c->trait_model);
     c->trait_model = nullptr;
     kv_free(c);
+    kv_free_cache(c->kv_aside);
 }

@@ -48,6 +48,8 @@ void launch_vnorm_rows(float* X, size_t m, size_t ld, int num_heads, int hd, dou
 void launch_rope_kv_rows(const float* QKV, size_t m, size_t p0, size_t q_dim, size_t kv_dim, int hd, int rdim,
                          const float2* rope, __half* kc, __half* vc, int num_kv, hipStream_t s);
 void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipStream_t s, float scale = 1.0f);
+// act[i] = act(G[i]) * U[i] (separate gate and up buffers); kind 0 = SiLU, 1 = GELU-tanh.
+void launch_gated_mul(const float* G, const float* U, float* act, size_t n, int kind, hipStream_t s);
 // act[i] = act(GU[2i]) * GU[2i + 1]; kind 0 = SiLU, 1 = GELU-tanh.
 void launch_gated_pair_rows(const float* GU, float* act, size_t n, int kind, hipStream_t s);
 void launch_f32_to_f16(const float* src, __half* dst, size_t n, hipStream_t s);

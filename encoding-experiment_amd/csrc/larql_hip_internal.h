@@ -173,6 +173,11 @@ struct larql_hip_ctx {
     // prefill GEMM: X as fp16 MFMA operands
     larql::DeviceBuf gemm_x16;
     larql::KVCache kv;
+    // the cache-less full pipeline (full_pipeline_q4) runs its positions against this one,
+    // leaving the decode cache `kv` untouched
+    larql::KVCache kv_aside;
+    // multi_layer_q4_ffn work buffer
+    larql::DeviceBuf ffn_work;
     // model built by the last host-pointer decode_token (re-used while its key matches)
     larql_hip_model* trait_model = nullptr;
 };
@@ -216,6 +221,8 @@ void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s,
                         size_t m, hipStream_t s);
 void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
                       size_t m, hipStream_t s);
+// Q4_0 weights x f32 activation (one row of x), the reference GPU's q4_f32_matvec.
+void launch_q4_0_f32_matvec(const DevWeight& w, const float* x, float* out, hipStream_t s);
 void launch_quantize_q8(const float* x, size_t n, size_t m, int8_t* q8, float* scales, hipStream_t s);
 // q4_vecmat: chunks of rows per partial (q4_vecmat_chunks) and the two-pass launch;
 // part holds chunks x cols floats.

@@ -521,6 +521,57 @@ void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s,
     launch_int_mv_batched<LARQL_Q4_0>(w, q8x, q8s, out, m, s);
 }
 
+// ── Q4_0 weights x f32 activation ─────────────────────────────────────────
+// The reference GPU's down projection of a Q4_0 FFN (q4_f32_matvec,
+// LC/src/metal/shaders/q4_f32_matvec.rs:10-38): per block, block_sum = sum over the 16
+// nibble bytes of (lo - 8) x[2j] + (hi - 8) x[2j+1], then acc += block_sum * f16(scale).
+// One wave per row; lane l takes blocks l, l + 64, ... (one 16-byte nibble load each, 1 KB
+// contiguous per wave instruction), x through the caches; the lanes' block sums are then
+// added in a tree, an order within f32 rounding of the reference's serial one.
+namespace {
+__global__ __launch_bounds__(256) void q4_0_f32_mv_kernel(const uint8_t* __restrict__ qs,
+                                                          const uint16_t* __restrict__ d, const float* __restrict__ x,
+                                                          float* __restrict__ out, int rows, int nb) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // whole waves leave together: no barrier below
+    const uint4* q = reinterpret_cast<const uint4*>(qs + static_cast<size_t>(row) * nb * 16);
+    const uint16_t* dr = d + static_cast<size_t>(row) * nb;
+    float acc = 0.f;
+    for (int b = lane; b < nb; b += 64) {
+        const uint4 w = q[b];
+        const float4* xb = reinterpret_cast<const float4*>(x + 32 * b);
+        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+        float bs = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 xa = xb[2 * k], xc = xb[2 * k + 1];
+            const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xc.x, xc.y, xc.z, xc.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t byte = (wd[k] >> (8 * j)) & 0xFFu;
+                const float lo = static_cast<float>(static_cast<int>(byte & 15u) - 8);
+                const float hi = static_cast<float>(static_cast<int>(byte >> 4) - 8);
+                bs += lo * xs[2 * j] + hi * xs[2 * j + 1];
+            }
+        }
+        acc += bs * h2f(dr[b]);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) out[row] = acc;
+}
+}  // namespace
+
+void launch_q4_0_f32_matvec(const DevWeight& w, const float* x, float* out, hipStream_t s) {
+    if (w.format != LARQL_Q4_0) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4_0 f32 matvec: Q4_0 weights only");
+    if (w.rows == 0) return;
+    const dim3 grid(static_cast<unsigned>((w.rows + 3) / 4)), block(256);
+    q4_0_f32_mv_kernel<<<grid, block, 0, s>>>(w.qs, static_cast<const uint16_t*>(w.d), x, out,
+                                             static_cast<int>(w.rows), static_cast<int>(w.cols / 32));
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
 // 1..4 activation rows: the lane-group kernel (one pass over the weights); 5..8: the
 // matrix-core kernel; more: chunks of 8 (a single leftover row takes the one-row
 // kernel).  Measured on Q8_0 [14336 x 4096]: M = 4 16.9 us (lane groups) vs 20.1 us

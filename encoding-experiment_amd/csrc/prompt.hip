@@ -103,6 +103,13 @@ __global__ void gated_pair_rows_kernel(const float* __restrict__ GU, float* __re
     if (i < n) act[i] = gated_act(kind, GU[2 * i], GU[2 * i + 1]);
 }
 
+// act[i] = act(G[i]) * U[i] (gate and up in separate buffers).
+__global__ void gated_mul_kernel(const float* __restrict__ G, const float* __restrict__ U, float* __restrict__ act,
+                                 size_t n, int kind) {
+    const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    if (i < n) act[i] = gated_act(kind, G[i], U[i]);
+}
+
 unsigned blocks(size_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
 }  // namespace
@@ -142,6 +149,12 @@ void launch_rope_kv_rows(const float* QKV, size_t m, size_t p0, size_t q_dim, si
 void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipStream_t s, float scale) {
     if (n == 0) return;
     add_rows_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(a, b, out, n, scale);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_gated_mul(const float* G, const float* U, float* act, size_t n, int kind, hipStream_t s) {
+    if (n == 0) return;
+    gated_mul_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(G, U, act, n, kind);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 

@@ -83,6 +83,9 @@ SIGNATURES = {
     "larql_hip_decode_token": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
     "larql_hip_prefill_q4": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float,
                                   ctypes.c_int, ctypes.c_float, _P]),
+    "larql_hip_full_pipeline_q4": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_float,
+                                        ctypes.c_int, ctypes.c_float, _P]),
+    "larql_hip_multi_layer_q4_ffn": (_I, [_P, _P, _SZ, _P, _SZ, _SZ, _P]),
     "larql_hip_populate_kv_layer": (_I, [_P, _SZ, _P, _P, _SZ, _SZ, _SZ]),
     "larql_hip_reset_kv_cache": (_I, [_P]),
     "larql_hip_kv_cache_len": (_I, [_P, ctypes.POINTER(_SZ)]),
@@ -103,6 +106,11 @@ ACT_SILU, ACT_GELU_TANH = 0, 1
 class QuantWeight(ctypes.Structure):
     """larql_quant_weight / QuantWeight (larql-compute/src/pipeline.rs:22-27)."""
     _fields_ = [("data", _P), ("len", _SZ), ("scales", _P), ("format", _I)]
+
+
+class Q4FfnLayer(ctypes.Structure):
+    """larql_q4_ffn_layer: one (gate, up, down_t) Q4_0 triple of multi_layer_q4_ffn."""
+    _fields_ = [("gate", _P), ("gate_len", _SZ), ("up", _P), ("up_len", _SZ), ("down", _P), ("down_len", _SZ)]
 
 
 class PipelineLayer(ctypes.Structure):
@@ -142,16 +150,17 @@ def _nbytes(a):
 def make_layer(wq, wk, wv, wo, gate, up, down, input_norm, post_attn_norm, *, head_dim, num_q_heads,
                num_kv_heads, rope_base, eps=1e-6, attn_scale=None, fmt=Q4_K, formats=None,
                rotary_dim=0, sliding_window=0, norm_offset=0.0, has_post_norms=False, pre_ffn_norm=None,
-               post_ffn_norm=None, activation=ACT_SILU, has_v_norm=False, layer_scalar=0.0):
+               post_ffn_norm=None, activation=ACT_SILU, has_v_norm=False, layer_scalar=0.0, scales=None):
     """A FullPipelineLayer over numpy (host) or device tensors of reference-layout bytes:
     the Llama layer by default, or the variants of larql-compute/src/pipeline.rs:76-115
     (norm offset, post-norms with pre/post-FFN norm weights, GELU-tanh, V-norm, layer
-    scalar).  Keep the source arrays alive while the struct is in use."""
+    scalar).  scales: projection name -> f32 scales of a Q8_0 weight (QuantWeight.scales).
+    Keep the source arrays alive while the struct is in use."""
     L = PipelineLayer()
     names = ("wq", "wk", "wv", "wo", "gate", "up", "down")
     for name, arr in zip(names, (wq, wk, wv, wo, gate, up, down)):
         f = (formats or {}).get(name, fmt)
-        setattr(L, name, QuantWeight(_addr(arr), _nbytes(arr), None, f))
+        setattr(L, name, QuantWeight(_addr(arr), _nbytes(arr), _addr((scales or {}).get(name)), f))
     L.input_norm = _addr(input_norm)
     L.post_attn_norm = _addr(post_attn_norm)
     L.pre_ffn_norm = _addr(pre_ffn_norm)
@@ -444,6 +453,32 @@ class HipBackend:
                                             kv_dim, seq_len, num_q_heads, num_kv_heads, head_dim, rope_base,
                                             1 if use_qk_norm else 0, softcap, out.ctypes.data_as(_P))
         return out.reshape(seq_len, hidden) if self._ok(rc) else None
+
+    def full_pipeline_q4(self, layers, x, hidden: int, inter: int, q_dim: int, kv_dim: int, seq_len: int,
+                         num_q_heads: int, num_kv_heads: int, head_dim: int, rope_base: float,
+                         use_qk_norm: bool = False, softcap: float = 0.0):
+        """backend.rs:71-84: positions 0..seq_len-1 through all layers with causal attention
+        among them only (the decode cache untouched); returns [seq_len, hidden] or None."""
+        arr = (PipelineLayer * len(layers))(*layers)
+        xv, xp = _arr(x, np.float32)
+        out = np.empty(seq_len * hidden, dtype=np.float32)
+        rc = self._lib.larql_hip_full_pipeline_q4(self._ctx, ctypes.cast(arr, _P), len(layers), xp, hidden, inter,
+                                                  q_dim, kv_dim, seq_len, num_q_heads, num_kv_heads, head_dim,
+                                                  rope_base, 1 if use_qk_norm else 0, softcap,
+                                                  out.ctypes.data_as(_P))
+        return out.reshape(seq_len, hidden) if self._ok(rc) else None
+
+    def multi_layer_q4_ffn(self, layers_q4, x, inter: int, hidden: int):
+        """backend.rs:86-96: layers_q4 = [(gate, up, down_t) Q4_0 byte arrays]; returns the
+        chained FFN output [hidden] or None."""
+        keep = [tuple(np.ascontiguousarray(a, dtype=np.uint8) for a in t) for t in layers_q4]
+        arr = (Q4FfnLayer * len(keep))(*[Q4FfnLayer(g.ctypes.data, g.nbytes, u.ctypes.data, u.nbytes, d.ctypes.data,
+                                                    d.nbytes) for g, u, d in keep])
+        xv, xp = _arr(x, np.float32)
+        out = np.empty(hidden, dtype=np.float32)
+        rc = self._lib.larql_hip_multi_layer_q4_ffn(self._ctx, ctypes.cast(arr, _P), len(keep), xp, inter, hidden,
+                                                    out.ctypes.data_as(_P))
+        return out if self._ok(rc) else None
 
     def populate_kv_layer(self, layer: int, k_data, v_data, seq_len: int, num_kv_heads: int, head_dim: int):
         """backend.rs:103-107 (K/V f32 [seq_len, num_kv*head_dim], stored as fp16)."""

@@ -282,7 +282,10 @@ enum { LARQL_ACT_SILU = 0, LARQL_ACT_GELU_TANH = 1 };
 /* FullPipelineLayer — LC/src/pipeline.rs:60-120, same fields in the same order.
  * Optional vectors are NULL when absent.  The HIP decode step and prompt pass implement
  * RMSNorm layers with a gated FFN and Q4_K or Q6_K projections (each its own format, as in
- * Q4_K_M files), with the variants the reference's decode reads per layer
+ * Q4_K_M files) — and Q8_0 attention / Q4_0 FFN projections (the reference decode's Q8
+ * and Q4_0 paths, LC/src/metal/decode.rs:262-296, 374-404, 560-690; Q8_0 needs
+ * larql_quant_weight.scales), Q4_KF in either byte layout — with the variants the
+ * reference's decode reads per layer
  * (LC/src/metal/decode.rs:98-739): norm_offset (weight = offset + w), SiLU or GELU-tanh,
  * has_post_norms (h + norm(o, post_attn_norm); FFN input norm(h, pre_ffn_norm); h +
  * norm(down, post_ffn_norm); an absent pre/post-FFN weight is the weight-free norm, as the
@@ -339,6 +342,39 @@ int larql_hip_prefill_q4(larql_hip_ctx* ctx, const larql_pipeline_layer* layers,
                          const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim, size_t seq_len,
                          size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float rope_base,
                          int use_qk_norm, float softcap, float* out);
+
+/* ComputeBackend::full_pipeline_q4 — LC/src/backend.rs:71-84 (Metal LC/src/metal/trait_impl.rs:43-76 ->
+ * ops/full_pipeline.rs:201-687): x [seq_len][hidden] at positions 0 .. seq_len-1 through all
+ * layers with causal attention among those positions only (no KV cache: the context's decode
+ * cache is left as it was); out [seq_len][hidden] (host), the last layer's hidden state of
+ * every position.  The trait returns the first `hidden` floats of it (the reference calls it
+ * with seq_len = 1, LI/src/layer_graph/predict.rs:406).  Layers as for decode_token, Q8_0
+ * attention and Q4_0 FFN weights included; use_qk_norm != 0 or softcap != 0 return UNSUPPORTED. */
+int larql_hip_full_pipeline_q4(larql_hip_ctx* ctx, const larql_pipeline_layer* layers, size_t num_layers,
+                               const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim,
+                               size_t seq_len, size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
+                               float rope_base, int use_qk_norm, float softcap, float* out);
+
+/* One layer of multi_layer_q4_ffn: the (gate, up, down_t) Q4_0 slices of the reference's
+ * &[(&[u8], &[u8], &[u8])] with their byte lengths.  gate and up are [inter][hidden], down
+ * [hidden][inter] (the interleaved_q4.bin layout, LI/src/layer_graph/predict.rs:177-191). */
+typedef struct {
+    const uint8_t* gate;
+    size_t gate_len;
+    const uint8_t* up;
+    size_t up_len;
+    const uint8_t* down;
+    size_t down_len;
+} larql_q4_ffn_layer;
+
+/* ComputeBackend::multi_layer_q4_ffn — LC/src/backend.rs:86-96 (Metal LC/src/metal/ops/q4_batched.rs:97-212):
+ * x_0 = x; per layer q = quantize_to_q8(x_l), g = q4_matvec(gate, q), u = q4_matvec(up, q)
+ * (bit-exact block order), a = silu(g) * u, x_{l+1} = down . a with the f32 activation
+ * (q4_f32_matvec, LC/src/metal/shaders/q4_f32_matvec.rs); out [hidden] = x_L (layers chained
+ * without a residual add, as the reference chains them).  Host memory in and out; the Q4_0
+ * slices are cached like every weight. */
+int larql_hip_multi_layer_q4_ffn(larql_hip_ctx* ctx, const larql_q4_ffn_layer* layers, size_t num_layers,
+                                 const float* x, size_t inter, size_t hidden, float* out);
 
 /* ComputeBackend::populate_kv_layer — LC/src/backend.rs:103-107: K/V rows
  * [seq_len][num_kv_heads*head_dim] f32 (stored as fp16, RNE); sets the cache

@@ -53,6 +53,7 @@ def _load():
             "lo_q6k_matvec": (None, [_P, _P, _P, _SZ, _SZ]),
             "lo_q8_matvec": (None, [_P, _P, _P, _P, _P, _SZ, _SZ]),
             "lo_q4kf_gguf_matvec": (None, [_P, _P, _P, _SZ, _SZ]),
+            "lo_q4_0_f32_matvec": (None, [_P, _P, _P, _SZ, _SZ]),
             "lo_q4kf160_matvec": (None, [_P, _P, _P, _SZ, _SZ]),
             "lo_gguf_scale_min": (None, [ctypes.c_int, _P, _P, _P]),
             "lo_q4k_to_gguf": (None, [_P, _SZ, _P]),
@@ -217,6 +218,14 @@ def q6k_matvec(q6k, x, rows: int, hidden: int):
     return out
 
 
+def q4_0_f32_matvec(q4, x, rows: int, hidden: int):
+    """Q4_0 weights x f32 activation (the reference GPU's q4_f32_matvec order)."""
+    q4, x = _c(q4, np.uint8), _c(x, np.float32)
+    out = np.empty(rows, dtype=np.float32)
+    _load().lo_q4_0_f32_matvec(_ptr(q4), _ptr(x), _ptr(out), rows, hidden)
+    return out
+
+
 def q4kf_gguf_matvec(w, x, rows: int, hidden: int):
     """Q4_KF, 144-byte llama.cpp GGUF block (the reference's GPU decode layout)."""
     w, x = _c(w, np.uint8), _c(x, np.float32)
@@ -365,7 +374,7 @@ class _Layer(ctypes.Structure):
                 ("norm_offset", ctypes.c_float), ("has_post_norms", ctypes.c_int),
                 ("activation", ctypes.c_int), ("has_v_norm", ctypes.c_int),
                 ("layer_scalar", ctypes.c_float), ("rotary_dim", ctypes.c_size_t),
-                ("attn_scale", ctypes.c_float)]
+                ("attn_scale", ctypes.c_float)] + [(n + "_s", ctypes.c_void_p) for n in _PROJ]
 
 
 def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, num_kv: int,
@@ -373,8 +382,9 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
     """One decoder layer on the CPU.  ``layer`` holds numpy arrays keyed as the
     lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits) are updated in place.
     window > 0 attends over the last `window` positions only.  ``layer["formats"]``
-    (optional) maps a projection name to "q6_k" (Q6_K bytes), "q4_kf" (Q4_KF, 144-byte GGUF)
-    or "q4_kf160" (Q4_KF, 160-byte); the default is Q4_K.
+    (optional) maps a projection name to "q6_k" (Q6_K bytes), "q4_kf" (Q4_KF, 144-byte GGUF),
+    "q4_kf160" (Q4_KF, 160-byte), "q8_0" (int8 weights, scales under name + "_s") or "q4_0";
+    the default is Q4_K.
     Optional layer variants (FullPipelineLayer, LC/src/pipeline.rs:76-115):
     pre_ffn_norm / post_ffn_norm (arrays or None), norm_offset, has_post_norms,
     activation ("silu" | "gelu_tanh"), has_v_norm, layer_scalar, rotary_dim, attn_scale."""
@@ -392,9 +402,13 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
             keep[name] = a
             setattr(st, name, a.ctypes.data)
     fm = layer.get("formats", {})
-    codes = {"q4_k": 0, "q6_k": 1, "q4_kf": 2, "q4_kf160": 3}
+    codes = {"q4_k": 0, "q6_k": 1, "q4_kf": 2, "q4_kf160": 3, "q8_0": 4, "q4_0": 5}
     for i, name in enumerate(_PROJ):
         st.fmt[i] = codes[fm.get(name, "q4_k")]
+        if st.fmt[i] == 4:   # Q8_0: int8 bytes in layer[name], f32 scales in layer[name + "_s"]
+            a = _c(layer[name + "_s"], np.float32)
+            keep[name + "_s"] = a
+            setattr(st, name + "_s", a.ctypes.data)
     for name in ("k_cache", "v_cache"):
         a = layer[name]
         assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]

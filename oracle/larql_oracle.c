@@ -605,6 +605,27 @@ void lo_q4k_to_gguf_llamacpp(const uint8_t* q4k, size_t nblocks, uint8_t* out) {
     }
 }
 
+/* LC/src/metal/shaders/q4_f32_matvec.rs:10-38 */
+void lo_q4_0_f32_matvec(const uint8_t* q4, const float* x, float* out, size_t rows, size_t hidden) {
+    size_t bpr = hidden / 32, bytes = bpr * 18;
+    for (size_t r = 0; r < rows; r++) {
+        float acc = 0.0f;
+        for (size_t b = 0; b < bpr; b++) {
+            const uint8_t* blk = q4 + r * bytes + b * 18;
+            float scale = lo_decode_f16(rd_u16(blk));
+            const float* xb = x + b * 32;
+            float block_sum = 0.0f;
+            for (int j = 0; j < 16; j++) {
+                uint8_t byte = blk[2 + j];
+                float lo = (float)((int)(byte & 0x0F) - 8), hi = (float)((int)(byte >> 4) - 8);
+                block_sum += lo * xb[j * 2] + hi * xb[j * 2 + 1];
+            }
+            acc += block_sum * scale;
+        }
+        out[r] = acc;
+    }
+}
+
 /* LC/src/cpu/ops/q8_matvec.rs:36-62 */
 void lo_q8_matvec(const int8_t* wq, const float* ws, const int8_t* xq, const float* xs,
                   float* out, size_t rows, size_t hidden) {
@@ -777,13 +798,31 @@ void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_
     free(sc);
 }
 
-/* A projection in its layer's format: Q4_K (0), Q6_K (1), Q4_KF 144-byte GGUF (2) or
- * Q4_KF 160-byte (3). */
-static void lo_proj(int fmt, const uint8_t* w, const float* x, float* out, size_t rows, size_t cols) {
-    if (fmt == 1) lo_q6k_matvec(w, x, out, rows, cols);
-    else if (fmt == 2) lo_q4kf_gguf_matvec(w, x, out, rows, cols);
-    else if (fmt == 3) lo_q4kf160_matvec(w, x, out, rows, cols);
-    else lo_q4k_matvec(w, x, out, rows, cols);
+/* A projection in its layer's format: Q4_K (0), Q6_K (1), Q4_KF 144-byte GGUF (2), Q4_KF
+ * 160-byte (3), Q8_0 (4: int8 weights + f32 scales ws, input quantized by quantize_to_q8) or
+ * Q4_0 (5: q8in = 1 quantizes the input and runs the block matvec, q8in = 0 the f32-input
+ * matvec of the reference's down projection). */
+static void lo_proj_q(int fmt, const uint8_t* w, const float* ws, int q8in, const float* x, float* out, size_t rows,
+                      size_t cols) {
+    if (fmt == 4 || (fmt == 5 && q8in)) {
+        int8_t* q8 = (int8_t*)malloc(cols);
+        float* q8s = (float*)malloc(cols / 32 * sizeof(float));
+        lo_quantize_to_q8(x, cols, q8, q8s);
+        if (fmt == 4) lo_q8_matvec((const int8_t*)w, ws, q8, q8s, out, rows, cols);
+        else lo_q4_0_matvec_blockint(w, q8, q8s, out, rows, cols);
+        free(q8);
+        free(q8s);
+    } else if (fmt == 5) {
+        lo_q4_0_f32_matvec(w, x, out, rows, cols);
+    } else if (fmt == 1) {
+        lo_q6k_matvec(w, x, out, rows, cols);
+    } else if (fmt == 2) {
+        lo_q4kf_gguf_matvec(w, x, out, rows, cols);
+    } else if (fmt == 3) {
+        lo_q4kf160_matvec(w, x, out, rows, cols);
+    } else {
+        lo_q4k_matvec(w, x, out, rows, cols);
+    }
 }
 
 /* One decoder layer (LI/src/attention/block.rs:52-157, LI/src/forward/layer.rs:50-94; per-op
@@ -823,9 +862,9 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
     float* a = (float*)malloc(inter * sizeof(float));
 
     lo_rms_norm(h, L->input_norm, off, eps, xn, hidden);
-    lo_proj(L->fmt[0], L->wq, xn, q, qd, hidden);
-    lo_proj(L->fmt[1], L->wk, xn, k, kvd, hidden);
-    lo_proj(L->fmt[2], L->wv, xn, v, kvd, hidden);
+    lo_proj_q(L->fmt[0], L->wq, L->wq_s, 1, xn, q, qd, hidden);
+    lo_proj_q(L->fmt[1], L->wk, L->wk_s, 1, xn, k, kvd, hidden);
+    lo_proj_q(L->fmt[2], L->wv, L->wv_s, 1, xn, v, kvd, hidden);
     if (L->has_v_norm) lo_rms_norm_heads(v, num_kv, head_dim, eps);
     lo_rope_at(q, num_q, head_dim, rdim, rope_base, pos);
     lo_rope_at(k, num_kv, head_dim, rdim, rope_base, pos);
@@ -836,7 +875,7 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
     float scale = L->attn_scale != 0.0f ? L->attn_scale : (float)(1.0 / sqrt((double)head_dim));
     const size_t T = pos + 1, t0 = (window > 0 && T > window) ? T - window : 0;
     lo_attend_f16(q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, T - t0, num_q, num_kv, head_dim, scale, att);
-    lo_proj(L->fmt[3], L->wo, att, o, hidden, qd);
+    lo_proj_q(L->fmt[3], L->wo, L->wo_s, 1, att, o, hidden, qd);
     if (L->has_post_norms) {
         lo_rms_norm(o, L->post_attn_norm, off, eps, xn, hidden);
         for (size_t i = 0; i < hidden; i++) h[i] = h[i] + xn[i];
@@ -845,11 +884,11 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
         for (size_t i = 0; i < hidden; i++) h[i] = h[i] + o[i];
         lo_rms_norm(h, L->post_attn_norm, off, eps, xn, hidden);
     }
-    lo_proj(L->fmt[4], L->gate, xn, g, inter, hidden);
-    lo_proj(L->fmt[5], L->up, xn, u, inter, hidden);
+    lo_proj_q(L->fmt[4], L->gate, L->gate_s, 1, xn, g, inter, hidden);
+    lo_proj_q(L->fmt[5], L->up, L->up_s, 1, xn, u, inter, hidden);
     if (L->activation == 1) lo_gelu_tanh_gate_up(g, u, a, inter);
     else lo_silu_gate_up(g, u, a, inter);
-    lo_proj(L->fmt[6], L->down, a, o, hidden, inter);
+    lo_proj_q(L->fmt[6], L->down, L->down_s, 0, a, o, hidden, inter);
     if (L->has_post_norms) {
         lo_rms_norm(o, L->post_ffn_norm, off, eps, xn, hidden);
         for (size_t i = 0; i < hidden; i++) h[i] = h[i] + xn[i];

@@ -81,6 +81,11 @@ void lo_q4k_to_q4kf(const uint8_t* q4k, size_t nblocks, uint8_t* out);        /*
  * test data for the GGUF path whose dequantized values equal the Q4_K block's. */
 void lo_q4k_to_gguf_llamacpp(const uint8_t* q4k, size_t nblocks, uint8_t* out);
 
+/* Q4_0 weights x f32 activation, the reference GPU's q4_f32_matvec
+ * (LC/src/metal/shaders/q4_f32_matvec.rs:10-38): per block b, block_sum = sum_j
+ * (lo_j - 8) x[2j] + (hi_j - 8) x[2j+1] in f32, acc += block_sum * f16(scale_b). */
+void lo_q4_0_f32_matvec(const uint8_t* q4, const float* x, float* out, size_t rows, size_t hidden);
+
 /* LC/src/cpu/ops/q8_matvec.rs:36-62 */
 void lo_q8_matvec(const int8_t* wq, const float* ws, const int8_t* xq, const float* xs,
                   float* out, size_t rows, size_t hidden);
@@ -117,7 +122,10 @@ typedef struct {
     const float *input_norm, *post_attn_norm;
     uint16_t *k_cache, *v_cache;                             /* [max_seq][kv_heads][head_dim] fp16 */
     /* per projection (wq, wk, wv, wo, gate, up, down): 0 = Q4_K, 1 = Q6_K, 2 = Q4_KF 144-byte
-     * GGUF, 3 = Q4_KF 160-byte; mixed formats
+     * GGUF, 3 = Q4_KF 160-byte, 4 = Q8_0 (int8 + f32 scales in *_s; its input is
+     * quantize_to_q8 of the f32 input), 5 = Q4_0 (gate / up: Q8-quantized input and the block
+     * matvec; down: lo_q4_0_f32_matvec of the f32 activation) — the reference GPU decode's
+     * Q8 attention and Q4_0 FFN (LC/src/metal/decode.rs:262-296, 374-404, 560-690); mixed formats
      * per projection as the reference's per-layer QuantWeight allows (LC/src/pipeline.rs:22-27) */
     int fmt[7];
     const float *pre_ffn_norm, *post_ffn_norm;  /* NULL: norm without weight (LI/src/forward/layer.rs:65-68) */
@@ -128,6 +136,7 @@ typedef struct {
     float layer_scalar;                         /* 0 = disabled; else h *= layer_scalar */
     size_t rotary_dim;                          /* 0 = head_dim */
     float attn_scale;                           /* 0 = 1/sqrt(head_dim) */
+    const float *wq_s, *wk_s, *wv_s, *wo_s, *gate_s, *up_s, *down_s;  /* Q8_0 weight scales */
 } lo_layer_t;
 
 void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,

@@ -44,8 +44,13 @@ def q4kf160(rows, cols, seed, std=0.02):
     return oracle.q4k_to_q4kf(q4k(rows, cols, seed, std))
 
 
-MAKERS = {"q4_k": q4k, "q6_k": q6k, "q4_kf": q4kf, "q4_kf160": q4kf160}
-HIP_FORMAT = {"q6_k": larql_hip.Q6_K, "q4_kf": larql_hip.Q4_KF, "q4_kf160": larql_hip.Q4_KF}
+def q4_0(rows, cols, seed, std=0.02):
+    return oracle.quantize_q4_0(oracle.gauss(seed, rows * cols, 0.0, std))
+
+
+MAKERS = {"q4_k": q4k, "q6_k": q6k, "q4_kf": q4kf, "q4_kf160": q4kf160, "q4_0": q4_0}
+HIP_FORMAT = {"q6_k": larql_hip.Q6_K, "q4_kf": larql_hip.Q4_KF, "q4_kf160": larql_hip.Q4_KF, "q8_0": larql_hip.Q8_0,
+              "q4_0": larql_hip.Q4_0}
 
 
 class SmallModel:
@@ -68,7 +73,10 @@ class SmallModel:
             s = seed + 100 * l
             L = {}
             for i, (name, (r, c)) in enumerate(shapes.items()):
-                L[name] = MAKERS[self.formats.get(name, "q4_k")](r, c, s + 1 + i)
+                if self.formats.get(name) == "q8_0":   # int8 weights + f32 scales (QuantWeight.scales)
+                    L[name], L[name + "_s"] = oracle.quantize_weights_q8(oracle.gauss(s + 1 + i, r * c, 0.0, 0.02), r, c)
+                else:
+                    L[name] = MAKERS[self.formats.get(name, "q4_k")](r, c, s + 1 + i)
             L.update(input_norm=(1.0 + 0.1 * oracle.gauss(s + 8, hidden)).astype(np.float32),
                      post_attn_norm=(1.0 + 0.1 * oracle.gauss(s + 9, hidden)).astype(np.float32),
                      k_cache=np.zeros(cap * kvd, np.uint16), v_cache=np.zeros(cap * kvd, np.uint16),
@@ -89,7 +97,8 @@ class SmallModel:
                                      has_post_norms=v.get("has_post_norms", False),
                                      pre_ffn_norm=L.get("pre_ffn_norm"), post_ffn_norm=L.get("post_ffn_norm"),
                                      activation=act, has_v_norm=v.get("has_v_norm", False),
-                                     layer_scalar=v.get("layer_scalar", 0.0), rotary_dim=v.get("rotary_dim", 0))
+                                     layer_scalar=v.get("layer_scalar", 0.0), rotary_dim=v.get("rotary_dim", 0),
+                                     scales={n: L[n + "_s"] for n in self.formats if n + "_s" in L})
                 for L in self.layers]
 
 
@@ -177,6 +186,85 @@ def test_decode_q4kf_layers(hip, formats):
     reads it, 160-byte pre-baked), fused where a group shares format and layout, split
     otherwise; decode against the oracle layer."""
     run_sequence(hip, T0=30, n_tokens=2, n_layers=2, formats=formats)
+
+
+@pytest.mark.parametrize("formats,variant", [
+    ({n: "q8_0" for n in ("wq", "wk", "wv", "wo")} | {n: "q4_0" for n in ("gate", "up", "down")}, None),
+    ({"wq": "q8_0", "wv": "q8_0", "down": "q4_0"}, None),                     # mixed with Q4_K
+    ({n: "q8_0" for n in ("wq", "wk", "wv", "wo")} | {n: "q4_0" for n in ("gate", "up", "down")},
+     dict(has_post_norms=True, norm_offset=1.0, activation="gelu_tanh", layer_scalar=0.5)),
+])
+def test_decode_q8_attention_q4_0_ffn(hip, formats, variant):
+    """Q8_0 attention projections and Q4_0 FFN projections (the reference GPU decode's Q8 and
+    Q4_0 paths: the normed input quantized by quantize_to_q8, bit-exact block dots; the Q4_0
+    down projection on the f32 activation), alone, mixed with Q4_K, and in a post-norm layer."""
+    run_sequence(hip, T0=21, n_tokens=2, n_layers=2, formats=formats, variant=variant)
+
+
+def _oracle_positions(m, x, hidden, inter, nq, nkv, hd, rope):
+    out = []
+    for p in range(x.shape[0]):
+        h = x[p].copy()
+        for L in m.layers:
+            h = oracle.decode_layer(L, h, p, hidden, inter, nq, nkv, hd, rope)
+        out.append(h)
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("seq,formats", [(1, None), (6, None),
+                                         (4, {n: "q8_0" for n in ("wq", "wk", "wv", "wo")} |
+                                          {n: "q4_0" for n in ("gate", "up", "down")})])
+def test_full_pipeline_q4_matches_oracle_and_keeps_cache(hip, seq, formats):
+    """full_pipeline_q4 (backend.rs:71-84): positions 0..seq-1 with causal attention among
+    themselves only; every position's hidden state against the oracle, and the decode cache
+    (9 populated positions) neither read nor changed: the next decode_token continues it."""
+    n_layers, hidden, inter, nq, nkv, hd, T0 = 2, 512, 1024, 8, 2, 64, 9
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=T0 + seq + 2, seed=61, formats=formats)
+    layers = m.hip_layers(10000.0)
+    kvd = nkv * hd
+    hip.reset_kv_cache()
+    for l in range(n_layers):
+        k, v = oracle.gauss(960 + l, T0 * kvd), oracle.gauss(970 + l, T0 * kvd)
+        hip.populate_kv_layer(l, k, v, T0, nkv, hd)
+    x = np.stack([oracle.gauss(990 + p, hidden) for p in range(seq)])
+    got = hip.full_pipeline_q4(layers, x, hidden, inter, nq * hd, kvd, seq, nq, nkv, hd, 10000.0)
+    ref = _oracle_positions(m, x, hidden, inter, nq, nkv, hd, 10000.0)
+    e = max(rel_err(got[p], ref[p]) for p in range(seq))
+    print(f"[full pipeline] seq={seq} formats={formats}: worst rel_err={e:.3e}", flush=True)
+    assert e <= REL_TOL
+    assert hip.kv_cache_len() == T0
+    for l, L in enumerate(m.layers):   # the oracle's caches: the populated rows again
+        L["k_cache"][:] = 0
+        L["v_cache"][:] = 0
+        L["k_cache"][: T0 * kvd] = oracle.gauss(960 + l, T0 * kvd).astype(np.float16).view(np.uint16)
+        L["v_cache"][: T0 * kvd] = oracle.gauss(970 + l, T0 * kvd).astype(np.float16).view(np.uint16)
+    nxt = oracle.gauss(999, hidden)
+    got = hip.decode_token(layers, nxt, hidden, inter, nq * hd, kvd, nq, nkv, hd, 10000.0)
+    ref = nxt.copy()
+    for L in m.layers:
+        ref = oracle.decode_layer(L, ref, T0, hidden, inter, nq, nkv, hd, 10000.0)
+    assert rel_err(got, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("n_layers,inter,hidden", [(3, 1024, 512), (2, 10240, 2560)])
+def test_multi_layer_q4_ffn_matches_oracle(hip, n_layers, inter, hidden):
+    """multi_layer_q4_ffn (backend.rs:86-96; Metal ops/q4_batched.rs:97-212): per layer
+    quantize_to_q8, Q4_0 gate and up (block-integer order), silu(gate) * up, Q4_0 down on the
+    f32 activation; layers chained output to input."""
+    layers_q4, x = [], oracle.gauss(1200, hidden)
+    for l in range(n_layers):
+        layers_q4.append((q4_0(inter, hidden, 1210 + l, 0.05), q4_0(inter, hidden, 1220 + l, 0.05),
+                          q4_0(hidden, inter, 1230 + l, 0.05)))
+    got = hip.multi_layer_q4_ffn(layers_q4, x, inter, hidden)
+    ref = x.copy()
+    for g, u, d in layers_q4:
+        q8, q8s = oracle.quantize_to_q8(ref)
+        gs = oracle.q4_0_matvec_blockint(g, q8, q8s, inter, hidden)
+        us = oracle.q4_0_matvec_blockint(u, q8, q8s, inter, hidden)
+        ref = oracle.q4_0_f32_matvec(d, oracle.silu_gate_up(gs, us), hidden, inter)
+    e = rel_err(got, ref)
+    print(f"[multi-layer q4 ffn] {n_layers} x [{inter}x{hidden}]: rel_err={e:.3e}", flush=True)
+    assert e <= REL_TOL
 
 
 def test_prefill_q4_q4kf_layers(hip):

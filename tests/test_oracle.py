@@ -692,12 +692,21 @@ def _ref_layer64(P, h, kc, vc, pos, dims, mut=()):
         return x / r * ((off + w) if w is not None else 1.0)
 
     W = P["deq"]
+    q8in = P.get("q8_input", ())
+
+    def proj(name, x):
+        """W x; projections whose format takes a Q8 input see quantize_to_q8(x) (f32)."""
+        if name in q8in:
+            q, s8 = oracle.quantize_to_q8(x.astype(np.float32))
+            x = q.astype(np.float64) * np.repeat(s8.astype(np.float64), 32)
+        return W[name] @ x
+
     h = h.astype(np.float64)
     nin, npost = P["input_norm"], P["post_attn_norm"]
     if "swap_norms" in mut:
         nin, npost = npost, nin
     xn = norm(h, nin)
-    q, k, v = W["wq"] @ xn, W["wk"] @ xn, W["wv"] @ xn
+    q, k, v = proj("wq", xn), proj("wk", xn), proj("wv", xn)
     if P.get("has_v_norm"):
         v = v.reshape(nkv, hd)
         v = (v / np.sqrt((v * v).mean(1, keepdims=True) + eps)).reshape(-1)
@@ -728,21 +737,21 @@ def _ref_layer64(P, h, kc, vc, pos, dims, mut=()):
         sc = K[:, kvh * hd:(kvh + 1) * hd] @ q[qh * hd:(qh + 1) * hd] * scale
         p = np.exp(sc - sc.max())
         att[qh * hd:(qh + 1) * hd] = (p / p.sum()) @ V[:, kvh * hd:(kvh + 1) * hd]
-    o = W["wo"] @ att
+    o = proj("wo", att)
     if P.get("has_post_norms"):
         h1 = h + norm(o, npost)
         f = norm(h1, P.get("pre_ffn_norm"))
     else:
         h1 = (o if "drop_residual" in mut else h + o)
         f = norm(h1, npost)
-    g, u = W["gate"] @ f, W["up"] @ f
+    g, u = proj("gate", f), proj("up", f)
     if "gate_up_swap" in mut:
         g, u = u, g
     if P.get("activation") == "gelu_tanh":
         a = 0.5 * g * (1 + np.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g ** 3))) * u
     else:
         a = g / (1 + np.exp(-g)) * u
-    dn = W["down"] @ a
+    dn = proj("down", a)
     h2 = h1 + (norm(dn, P.get("post_ffn_norm")) if P.get("has_post_norms") else dn)
     if P.get("layer_scalar", 0.0) != 0.0:
         h2 = h2 * P["layer_scalar"]
@@ -755,11 +764,19 @@ def _tiny_layer(seed, dims, formats, std=0.08, **variant):
     shapes = dict(wq=(nq * hd, hidden), wk=(nkv * hd, hidden), wv=(nkv * hd, hidden), wo=(hidden, nq * hd),
                   gate=(inter, hidden), up=(inter, hidden), down=(hidden, inter))
     P = dict(deq={}, formats=formats, rope_base=10000.0, **variant)
+    P["q8_input"] = tuple(n for n, f in formats.items() if f == "q8_0" or (f == "q4_0" and n != "down"))
     for name, (r, c) in shapes.items():
         w = (rng.standard_normal(r * c) * std).astype(np.float32)
         if formats.get(name) == "q6_k":
             P[name] = oracle.quantize_q6_k(w)
             P["deq"][name] = _deq_q6k(P[name], r, c)
+        elif formats.get(name) == "q8_0":
+            P[name], P[name + "_s"] = oracle.quantize_weights_q8(w, r, c)
+            P["deq"][name] = (P[name].astype(np.float64).reshape(r, -1, 32) *
+                              P[name + "_s"].astype(np.float64).reshape(r, -1, 1)).reshape(r, c)
+        elif formats.get(name) == "q4_0":
+            P[name] = oracle.quantize_q4_0(w)
+            P["deq"][name] = _deq_q4_0(P[name], r * c).astype(np.float64).reshape(r, c)
         else:
             P[name] = oracle.quantize_q4_k(w)
             P["deq"][name] = _deq_q4k(P[name], r, c)
@@ -778,7 +795,7 @@ def _run_layer_case(P, dims, pos, seed):
     kc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
     vc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
     h = rng.standard_normal(hidden).astype(np.float32)
-    layer = {k: v for k, v in P.items() if k not in ("deq", "rope_base")}
+    layer = {k: v for k, v in P.items() if k not in ("deq", "rope_base", "q8_input")}
     layer["k_cache"], layer["v_cache"] = kc.copy(), vc.copy()
     got = oracle.decode_layer(layer, h, pos, hidden, inter, nq, nkv, hd, P["rope_base"])
     return got, (lambda mut=(): _ref_layer64(P, h, kc, vc, pos, dims, mut))
@@ -923,3 +940,42 @@ def test_reference_gguf_packing_known_answers():
     # x = 1 -> 0.99 -> 1, -1 -> 0.49 -> 0, fill 0 -> 0.74 -> 1
     assert list(q[32:36]) == [0x10, 0x10, 0x00, 0x00]
     assert list(q[80:84]) == [0x10, 0x10, 0x11, 0x11]
+
+
+def test_decode_layer_q8_attention_q4_0_ffn_matches_float64_composition():
+    """Q8_0 attention projections and a Q4_0 FFN (the reference GPU decode's Q8 / Q4_0 paths,
+    LC/src/metal/decode.rs:262-296, 374-404, 560-690): the projections that take a Q8 input
+    see quantize_to_q8 of their f32 input, the Q4_0 down projection the f32 activation.  The
+    float64 restatement quantizes the same f32 inputs; 1e-5 as above."""
+    dims = (256, 512, 4, 2, 64)
+    fm = {"wq": "q8_0", "wk": "q8_0", "wv": "q8_0", "wo": "q8_0", "gate": "q4_0", "up": "q4_0", "down": "q4_0"}
+    P = _tiny_layer(35, dims, fm)
+    got, ref = _run_layer_case(P, dims, pos=4, seed=36)
+    print(f"q8/q4_0 layer rel {_rel(got, ref()):.2e}")
+    assert _rel(got, ref()) <= 1e-5
+    for mut in ("swap_norms", "gate_up_swap", "drop_residual", "kv_map"):
+        assert _rel(got, ref((mut,))) > 1e-2, mut
+
+
+def test_q4_0_f32_matvec_closed_form():
+    """q4_f32_matvec (LC/src/metal/shaders/q4_f32_matvec.rs:10-38): one-hot probes give
+    (nib - 8) * f16(scale) per element (element 2j the low, 2j + 1 the high nibble of byte j),
+    and random inputs agree with a float64 dequantized dot within f32 rounding."""
+    blk = np.zeros(2 * 18, np.uint8)
+    blk[0:2] = np.array([0.75], np.float16).view(np.uint8)
+    blk[18:20] = np.array([-2.5], np.float16).view(np.uint8)
+    blk[2:18] = (np.arange(16) * 29 % 256).astype(np.uint8)
+    blk[20:36] = (np.arange(16) * 53 % 256).astype(np.uint8)
+    for e in (0, 1, 2, 31, 32, 33, 50, 63):
+        b, w = divmod(e, 32)
+        byte = blk[18 * b + 2 + w // 2]
+        nib = (byte >> 4) if w % 2 else (byte & 15)
+        x = np.zeros(64, np.float32)
+        x[e] = 1.0
+        assert oracle.q4_0_f32_matvec(blk, x, 1, 64)[0] == np.float32(int(nib) - 8) * np.float32((0.75, -2.5)[b])
+    rng = np.random.default_rng(37)
+    rows, cols = 20, 1024
+    q4 = oracle.quantize_q4_0(rng.standard_normal(rows * cols).astype(np.float32))
+    x = rng.standard_normal(cols).astype(np.float32)
+    ref = _deq_q4_0(q4, rows * cols).astype(np.float64).reshape(rows, cols) @ x.astype(np.float64)
+    assert np.allclose(oracle.q4_0_f32_matvec(q4, x, rows, cols), ref, rtol=1e-5, atol=1e-5)
