@@ -21,12 +21,15 @@ value        = algorithmic bytes of all trio launches / timed wall time (GB/s)
 roofline     = the gate launch alone: algorithmic bytes / its average launch time,
                vs 8 TB/s; traffic from the committed rocprofv3 PMC summary
 cpu_baseline = the oracle's port of the reference CPU q4k_matvec (q4k_matvec.rs),
-               one thread, timed on a bounded sample on this host.
+               rows split over all the host threads given to this process, timed on
+               a bounded sample; cpu_baselines = every workload of the path, one
+               thread and all-core, with the host's facts (nproc, CPU model).
 
 PMC helpers (used to produce profiles/q4k_matvec_traffic.json):
   bench.py --pmc-pass calib   plain 64 MiB device copies (known bytes) for scaling
   bench.py --pmc-pass gate    gate-shape Q4_K matvec launches
-  bench.py --pmc-report CALIB_FETCH CALIB_WRITE GATE_FETCH GATE_WRITE
+  bench.py --pmc-pass floor   the plain-read floor kernel over the same gate weights
+  bench.py --pmc-report CALIB_FETCH CALIB_WRITE GATE_FETCH GATE_WRITE [--pmc-floor FLOOR_FETCH]
 """
 from __future__ import annotations
 
@@ -49,6 +52,8 @@ HBM_PEAK_GBS = 8000.0
 SHAPES = (("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336))
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "q4k_matvec_traffic.json")
 CALIB_BYTES = 64 << 20
+# plain-read floor launch shapes (workgroups, threads); (0, 0) = the matvec's own shape
+READ_FLOOR_SHAPES = ((0, 0), (1024, 256), (2048, 256), (4096, 256))
 
 
 def q4k_algorithmic_bytes(rows: int, cols: int) -> int:
@@ -74,25 +79,202 @@ def log(msg: str):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(raw_u8, x_np, rows, cols, budget_s: float):
-    """Oracle port of LC/src/cpu/ops/q4k_matvec.rs, single thread, bounded sample."""
-    import oracle
+def host_facts(threads: int) -> dict:
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)), "cpu_model": model,
+            "threads_all_core": threads}
 
+
+def all_core_threads() -> int:
+    """Threads for the all-core CPU legs: the CPUs this process may run on, capped by
+    OMP_NUM_THREADS where the host sets it (the CPU share given to one GPU)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(env))) if env.isdigit() and int(env) > 0 else n
+
+
+def _host_blocks(rng, fmt: str, rows: int, cols: int):
+    """Random weight bytes in a reference layout with finite, normal f16 scales (the
+    CPU kernels' time does not depend on the values)."""
+    import numpy as np
+
+    def f16(n, lo, hi):
+        return rng.uniform(lo, hi, n).astype(np.float16).view(np.uint8).reshape(-1, 2)
+
+    if fmt == "q8_0":
+        return rng.integers(-127, 128, rows * cols, dtype=np.int8), rng.uniform(1e-3, 1e-2, rows * cols // 32).astype(np.float32)
+    bpb, per = {"q4_k": (148, 256), "q6_k": (210, 256), "q4_0": (18, 32)}[fmt]
+    b = rng.integers(0, 256, (rows * cols // per, bpb), dtype=np.uint8)
+    if fmt == "q4_k":
+        b[:, 0:2], b[:, 2:4] = f16(len(b), 1e-4, 1e-3), f16(len(b), 1e-4, 1e-3)
+    elif fmt == "q6_k":
+        b[:, 208:210] = f16(len(b), 1e-4, 1e-3)
+    else:
+        b[:, 0:2] = f16(len(b), 1e-3, 1e-2)
+    return b.reshape(-1), None
+
+
+def _timed(fn, budget_s: float):
     runs, t0 = 0, time.perf_counter()
     while True:
-        oracle.q4k_matvec(raw_u8, x_np, rows, cols)
+        fn()
         runs += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
-            break
-    gbs = q4k_algorithmic_bytes(rows, cols) * runs / el / 1e9
-    return {
-        "value": round(gbs, 3),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{runs} x Q4_K matvec [{rows}x{cols}] in {el:.1f} s (oracle port of q4k_matvec.rs, 1 thread)",
-    }
+            return runs, el
+
+
+def cpu_baselines(budget_s: float) -> dict:
+    """Every workload of the path on this host's CPU through the oracle's ports of the
+    reference CPU kernels, one thread and all-core (rows, queries or positions split over
+    threads; each slice runs the one-thread kernel, so the outputs are the same).  Each
+    leg runs for about budget_s on a bounded sample of the workload, scaled to the unit
+    the GPU line reports; `sample` says what ran."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
+    import oracle
+
+    T = all_core_threads()
+    pool = ThreadPoolExecutor(T)
+    rng = np.random.default_rng(7)
+    out = {"host": host_facts(T)}
+
+    def split(rows, fn, nt):
+        """fn(r0, r1) over nt contiguous row slices (ctypes calls run without the GIL)."""
+        if nt == 1:
+            fn(0, rows)
+            return
+        list(pool.map(lambda t: fn(rows * t // nt, rows * (t + 1) // nt), range(nt)))
+
+    def legs(name, unit, per_run, work, sample, per_time=False):
+        """per_run: the unit's amount per call of work(nt) (bytes, flops, walks ...);
+        per_time: report seconds (or ms) per unit of per_run instead of a rate."""
+        d = {"unit": unit, "sample": sample}
+        for label, nt in (("one_thread", 1), ("all_core", T)):
+            work(nt)  # warm
+            runs, el = _timed(lambda: work(nt), budget_s)
+            v = el / (per_run * runs) if per_time else per_run * runs / el
+            d[label] = {"value": round(v, 4), "threads": nt, "runs": runs, "seconds": round(el, 2)}
+        out[name] = d
+        log(f"[bench] cpu {name}: {d}")
+
+    GB = 1e9
+    # Q4_K [14336 x 4096] (q4k_matvec.rs), the headline shape
+    N, K = 14336, 4096
+    w, _ = _host_blocks(rng, "q4_k", N, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    rb = K // 256 * 148
+    legs("q4k_matvec_14336x4096", "GB/s", q4k_algorithmic_bytes(N, K) / GB,
+         lambda nt: split(N, lambda a, b: oracle.q4k_matvec(w[a * rb:b * rb], x, b - a, K), nt),
+         "one matvec per run")
+    # Q4_0 x Q8 [10240 x 2560], the reference's x86 accumulation order (q4_dot.c)
+    N, K = 10240, 2560
+    w, _ = _host_blocks(rng, "q4_0", N, K)
+    xq, xs = oracle.quantize_to_q8(rng.standard_normal(K).astype(np.float32))
+    rb = K // 32 * 18
+    legs("q4_0_matvec_10240x2560", "GB/s", (N * rb + K + K // 32 * 4 + N * 4) / GB,
+         lambda nt: split(N, lambda a, b: oracle.q4_0_matvec_x86(w[a * rb:b * rb], xq, xs, b - a, K), nt),
+         "one matvec per run, x86 block order")
+    # Q4_0 vecmat [10240 x 2560] (q4_vecmat.rs): out[hidden] accumulates over all rows, so
+    # it runs on one thread only
+    act = rng.standard_normal(N).astype(np.float32)
+    runs, el = _timed(lambda: oracle.q4_0_vecmat(act, w, N, K), budget_s)
+    out["q4_0_vecmat_10240x2560"] = {"unit": "GB/s", "sample": "one vecmat per run; one thread (a single "
+                                     "accumulation over all rows)",
+                                     "one_thread": {"value": round((N * rb + N * 4 + K * 4) * runs / el / GB, 4),
+                                                    "threads": 1, "runs": runs, "seconds": round(el, 2)}}
+    log(f"[bench] cpu q4_0_vecmat: {out['q4_0_vecmat_10240x2560']}")
+    # Q8_0 x Q8 [14336 x 4096], M = 1, 4, 8 (q8_matvec.rs): M matvecs per launch
+    N, K = 14336, 4096
+    wq, ws = _host_blocks(rng, "q8_0", N, K)
+    for m in (1, 4, 8):
+        xs8 = [oracle.quantize_to_q8(rng.standard_normal(K).astype(np.float32)) for _ in range(m)]
+
+        def q8run(nt, xs8=xs8):
+            def f(a, b):
+                for xq_, xs_ in xs8:
+                    oracle.q8_matvec(wq[a * K:b * K], ws[a * (K // 32):b * (K // 32)], xq_, xs_, b - a, K)
+            split(N, f, nt)
+
+        legs(f"q8_0_matvec_14336x4096_m{m}", "GB/s",
+             (N * K + N * K // 32 * 4 + m * (K + K // 32 * 4) + m * N * 4) / GB, q8run,
+             f"{m} row(s) per run, bytes counted as the GPU line counts them")
+    del wq, ws
+    # Q6_K [14336 x 4096] (q6k_matvec.rs)
+    w, _ = _host_blocks(rng, "q6_k", N, K)
+    rb = K // 256 * 210
+    legs("q6k_matvec_14336x4096", "GB/s", (N * rb + K * 4 + N * 4) / GB,
+         lambda nt: split(N, lambda a, b: oracle.q6k_matvec(w[a * rb:b * rb], x, b - a, K), nt),
+         "one matvec per run")
+    # gate-KNN walk: 34 layers [10240 x 2560] x 256 queries, top-32 by |score|
+    # (gate_knn.rs); sample: one layer, 8 queries per run, scaled to the whole walk
+    L, F, K, Q, k, q_s = 34, 10240, 2560, 256, 32, 8
+    g = (rng.standard_normal(F * K) * 0.02).astype(np.float32)
+    qs = rng.standard_normal((q_s, K)).astype(np.float32)
+
+    def knn(nt):
+        def f(a, b):
+            for i in range(a, b):
+                oracle.topk_abs(oracle.gate_scores_f32(g, qs[i], F, K), k)
+        split(q_s, f, nt)
+
+    legs("gate_knn_f32_34x10240x2560_q256_top32", "s/walk", q_s / (L * Q), knn,
+         "1 layer x 8 queries per run (f32 scores + top-32), scaled to 34 layers x 256 queries",
+         per_time=True)
+    del g
+    # prefill GEMM 512 x [10240 x 2560] Q4_K: the reference CPU runs one q4k matvec per
+    # position; sample 4 positions per run
+    N, K, M, m_s = 10240, 2560, 512, 4
+    w, _ = _host_blocks(rng, "q4_k", N, K)
+    xs4 = rng.standard_normal((m_s, K)).astype(np.float32)
+    rb = K // 256 * 148
+    legs("prefill_q4k_gemm_512x10240x2560", "GFLOP/s", 2.0 * m_s * N * K / 1e9,
+         lambda nt: split(N, lambda a, b: [oracle.q4k_matvec(w[a * rb:b * rb], xs4[i], b - a, K)
+                                           for i in range(m_s)], nt),
+         "4 positions per run (one Q4_K matvec each), flops 2 M N K")
+    del w
+    # 8B-shape decode step at pos 2048: one Q4_K layer per run (the oracle's decode layer,
+    # projections row-split over the threads) + the Q6_K head [128256 x 4096] timed on a
+    # 16384-row sample; tokens/s = 1 / (32 x layer + head)
+    from larql_hip.synth import LLAMA3_8B
+    c = LLAMA3_8B
+    h, inter, nq, nkv, hd = c["hidden"], c["inter"], c["nq"], c["nkv"], c["hd"]
+    qd, kvd, pos = nq * hd, nkv * hd, 2048
+    layer = {}
+    for name, (r, cc) in dict(wq=(qd, h), wk=(kvd, h), wv=(kvd, h), wo=(h, qd), gate=(inter, h),
+                              up=(inter, h), down=(h, inter)).items():
+        layer[name] = _host_blocks(rng, "q4_k", r, cc)[0]
+    layer["input_norm"] = np.ones(h, np.float32)
+    layer["post_attn_norm"] = np.ones(h, np.float32)
+    layer["k_cache"] = (rng.standard_normal((pos + 1) * kvd) * 0.5).astype(np.float16).view(np.uint16)
+    layer["v_cache"] = (rng.standard_normal((pos + 1) * kvd) * 0.5).astype(np.float16).view(np.uint16)
+    hx = rng.standard_normal(h).astype(np.float32)
+    hr = 16384
+    head, _ = _host_blocks(rng, "q6_k", hr, h)
+    d = {"unit": "tokens/s", "sample": f"1 layer at pos {pos} per run x {c['n_layers']} + Q6_K head "
+                                       f"{hr}-row sample x {c['vocab'] / hr:.2f}"}
+    for label, nt in (("one_thread", 1), ("all_core", T)):
+        oracle.decode_layer(layer, hx, pos, h, inter, nq, nkv, hd, 500000.0, threads=nt)
+        runs, el = _timed(lambda: oracle.decode_layer(layer, hx, pos, h, inter, nq, nkv, hd, 500000.0,
+                                                      threads=nt), budget_s)
+        hruns, hel = _timed(lambda: oracle.proj_rows_mt("q6_k", head, hx, hr, h, nt), budget_s / 2)
+        step = c["n_layers"] * el / runs + (hel / hruns) * c["vocab"] / hr
+        d[label] = {"value": round(1.0 / step, 4), "threads": nt, "s_per_token": round(step, 3),
+                    "layer_ms": round(el / runs * 1e3, 2), "head_ms": round(hel / hruns * c["vocab"] / hr * 1e3, 2)}
+    out["decode_llama3_8b_q4k_pos2048"] = d
+    log(f"[bench] cpu decode: {d}")
+    pool.shutdown()
+    return out
 
 
 def make_weights(be, torch, stream, copies):
@@ -438,8 +620,12 @@ def pmc_pass(which: str, launches: int):
         return
     be = larql_hip.HipBackend(0, strict=True)
     handles, xs, outs, _ = make_weights(be, torch, stream, copies=16)
+    fold = torch.empty(14336 // 16 + 4, device=dev, dtype=torch.int32)
     for i in range(launches):
-        be.matvec_dev(handles["gate"][i % 16], xs["gate"], outs["gate"], stream=stream)
+        if which == "floor":
+            be.read_floor_dev(handles["gate"][i % 16], fold, stream=stream)
+        else:
+            be.matvec_dev(handles["gate"][i % 16], xs["gate"], outs["gate"], stream=stream)
     torch.cuda.synchronize()
     be.close()
 
@@ -455,7 +641,7 @@ def _pmc_values(path: str, counter: str, name_part: str):
     return vals
 
 
-def pmc_report(calib_fetch, calib_write, gate_fetch, gate_write):
+def pmc_report(calib_fetch, calib_write, gate_fetch, gate_write, floor_fetch=None):
     """Scale the gate launches' FETCH_SIZE / WRITE_SIZE (KiB per dispatch) by what the
     same counters read for a plain copy of CALIB_BYTES, and write the traffic summary."""
     kib = CALIB_BYTES / 1024.0
@@ -475,6 +661,11 @@ def pmc_report(calib_fetch, calib_write, gate_fetch, gate_write):
         "algorithmic_bytes_per_launch": alg,
         "traffic_over_algorithmic": round(traffic / alg, 4),
     }
+    if floor_fetch:
+        ff = statistics.median(_pmc_values(floor_fetch, "FETCH_SIZE", "q4k_read_floor_kernel"))
+        out["read_floor"] = {"fetch_kib_raw": ff, "fetch_bytes": int(ff * f_fetch * 1024.0),
+                             "note": "q4k_read_floor_kernel: the gate weight's device bytes read once, "
+                                     "same grid and workgroup size as the matvec"}
     os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
     with open(TRAFFIC_JSON, "w") as f:
         json.dump(out, f, indent=2)
@@ -490,18 +681,19 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=30)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the non-headline workloads")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=1.5, help="per CPU-baseline leg (14 legs)")
     ap.add_argument("--eager", action="store_true", help="time Python-loop launches instead of a HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--pmc-pass", choices=("calib", "gate"))
+    ap.add_argument("--pmc-pass", choices=("calib", "gate", "floor"))
     ap.add_argument("--pmc-launches", type=int, default=50)
     ap.add_argument("--pmc-report", nargs=4, metavar=("CALIB_FETCH", "CALIB_WRITE", "GATE_FETCH", "GATE_WRITE"))
+    ap.add_argument("--pmc-floor", metavar="FLOOR_FETCH", help="with --pmc-report: FETCH_SIZE of the read-floor pass")
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
 
     if args.pmc_report:
-        pmc_report(*args.pmc_report)
+        pmc_report(*args.pmc_report, floor_fetch=args.pmc_floor)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU; multi-GPU sharding is not built "
@@ -541,21 +733,25 @@ def main():
     gbs = bytes_per_step * args.steps / (ms * 1e-3) / 1e9
     log(f"[bench] trio: {args.steps} steps in {ms:.3f} ms: {ms_per_step * 1e3:.2f} us/step, {gbs:.1f} GB/s")
 
-    # the dominant kernel alone: back-to-back gate launches
+    # each shape alone, back-to-back launches; beside it the plain-read floor: the same
+    # device bytes read once in the same launch shape, with no arithmetic
     per_shape = {}
     for name, rows, cols in SHAPES:
         n = args.steps
         ms_s = timer(lambda i: be.matvec_dev(handles[name][i % args.copies], xs[name], outs[name], stream=stream), n)
         us = ms_s * 1e3 / n
+        fold = torch.empty(8192, device=dev, dtype=torch.int32)
+        floors = {}
+        for g, t in READ_FLOOR_SHAPES:
+            ms_f = timer(lambda i: be.read_floor_dev(handles[name][i % args.copies], fold, g, t, stream=stream), n)
+            floors["matvec shape" if g == 0 else f"{g} x {t}"] = round(ms_f * 1e3 / n, 3)
+        fus = floors["matvec shape"]
+        best = min((v, k) for k, v in floors.items())
         per_shape[name] = {"us_per_launch": round(us, 3),
-                           "GBs": round(q4k_algorithmic_bytes(rows, cols) / (us * 1e-6) / 1e9, 1)}
+                           "GBs": round(q4k_algorithmic_bytes(rows, cols) / (us * 1e-6) / 1e9, 1),
+                           "read_floor_us": fus, "over_floor": round(us / fus, 3),
+                           "read_floor_best_us": best[0], "read_floor_best_shape": best[1]}
     log(f"[bench] per shape: {per_shape}")
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        name, rows, cols = SHAPES[0]
-        cpu = cpu_baseline(raws[name].cpu().numpy(), xs[name].cpu().numpy(), rows, cols, args.cpu_seconds)
-        log(f"[bench] cpu baseline: {cpu}")
 
     for name in handles:
         for h in handles[name]:
@@ -571,6 +767,15 @@ def main():
     if not args.no_decode:
         decode = run_decode(be, torch, stream, args.decode_steps, warmup=5)
         log(f"[bench] decode: {decode}")
+
+    cpu, cpu_all = None, None
+    if not args.no_cpu_baseline:
+        cpu_all = cpu_baselines(args.cpu_seconds)
+        q, one = cpu_all["q4k_matvec_14336x4096"]["all_core"], cpu_all["q4k_matvec_14336x4096"]["one_thread"]
+        cpu = {"value": q["value"], "unit": "GB/s", "cores": q["threads"], "kind": "port",
+               "sample": f"{q['runs']} Q4_K matvecs [14336x4096] in {q['seconds']} s, rows split over "
+                         f"{q['threads']} threads (oracle port of q4k_matvec.rs); one thread: {one['value']} GB/s"}
+        log(f"[bench] cpu baseline: {cpu}")
 
     gate_bytes = q4k_algorithmic_bytes(14336, 4096)
     gate_us = per_shape["gate"]["us_per_launch"]
@@ -606,11 +811,16 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "q4k_mfma_kernel<2, 4> gate [14336x4096]",
+            "kernel": "q4k_mfma_kernel<2, 2, false, 0, 2, false> gate [14336x4096]",
             "bytes_per_launch": gate_bytes,
             "avg_launch_us": gate_us,
+            "read_floor_us": per_shape["gate"]["read_floor_us"],
+            "frac_of_read_floor": round(per_shape["gate"]["read_floor_us"] / gate_us, 4),
+            "read_floor_best_us": per_shape["gate"]["read_floor_best_us"],
+            "read_floor_best_shape": per_shape["gate"]["read_floor_best_shape"],
         },
         "cpu_baseline": cpu,
+        "cpu_baselines": cpu_all,
         "decode": decode,
         "configs": configs,
     }

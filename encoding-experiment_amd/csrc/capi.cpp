@@ -363,6 +363,15 @@ extern "C" int larql_hip_vecmat_dev(larql_hip_ctx* c, uint64_t handle, const flo
     });
 }
 
+extern "C" int larql_hip_read_floor_dev(larql_hip_ctx* c, uint64_t handle, unsigned workgroups, unsigned threads,
+                                       uint32_t* out, size_t out_words, void* stream) {
+    return guarded(c, [&] {
+        if (!out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        const DevWeight& w = larql::lookup(c, handle);
+        larql::launch_q4k_read_floor(w, out, out_words, workgroups, threads, c->num_cus, pick_stream(c, stream));
+    });
+}
+
 static void run_pair_batch(larql_hip_ctx* c, const DevWeight& g, const DevWeight& u, const float* x, size_t seq,
                            float* gate_out, float* up_out, hipStream_t s) {
     if (g.format != LARQL_Q4_0 || u.format != LARQL_Q4_0) fail(LARQL_HIP_ERR_UNSUPPORTED, "pair batch: Q4_0 weights");

@@ -204,6 +204,11 @@ const DevWeight& cached_weight(larql_hip_ctx* c, int format, const void* data, s
 // m > 1 runs the prefill GEMM and needs `ws` of q4k_gemm_ws_bytes(m, cols) bytes.
 void launch_q4k_matvec(const DevWeight& w, const float* x, float* out, size_t m, void* ws, hipStream_t s);
 void launch_q6k_matvec(const DevWeight& w, const float* x, float* out, size_t m, hipStream_t s);
+// Plain-read floor of a Q4_K-family weight: its device bytes read once by `groups`
+// workgroups of `threads` (both 0: the matvec's launch shape), one XOR fold per
+// workgroup into out[0 .. groups).
+void launch_q4k_read_floor(const DevWeight& w, uint32_t* out, size_t out_words, unsigned groups, unsigned threads,
+                           int num_cus, hipStream_t s);
 // Y[m][rows] = X[m][cols] . deq(W)^T, Q4_K, on MFMA (prefill.hip); ws holds X as fp16
 // MFMA operands.
 size_t q4k_gemm_ws_bytes(size_t m, size_t cols);

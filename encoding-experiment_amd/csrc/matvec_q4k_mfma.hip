@@ -30,6 +30,8 @@
 // s' = max|x| / (2^22 - 1): the size of one f32 rounding of the sub-block's largest
 // element.  Each wave builds the planes of its own part in its own LDS area (no
 // workgroup barrier before the loop); a fused RMSNorm adds one barrier for sum(x^2).
+#include <type_traits>
+
 #include "kquant_levels.h"
 #include "matvec_common.h"
 
@@ -117,7 +119,10 @@ __device__ __forceinline__ void q4k_scale_min(const uint4& h, const uint4& h2, i
     }
 }
 
-template <int UR, int T, bool NORM, int HF>
+// PRE: units whose loads are issued with x, before the planes are built (the rest after);
+// XB: every wave's x loads are issued before any wave of the workgroup issues a weight
+// load (a bare s_barrier between them), so x is not queued behind the workgroup's weights.
+template <int UR, int T, bool NORM, int HF, int PRE, bool XB>
 __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int EL = 4 * UR;  // x elements per lane and round
@@ -165,8 +170,8 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
                 if constexpr (HF == kHdrKf160) hd2[t][u] = load_nt(th + sb * 32 + 1);
             }
     };
-    constexpr int PRE = 1;
     load_x(0);
+    if constexpr (XB) __builtin_amdgcn_s_barrier();
     load_units(0, 0, PRE);
 
     // Fused RMSNorm (LI/src/residual.rs:17-33): sum(x^2) over all of x, in f64.
@@ -330,7 +335,7 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
 
 
 
-template <int UR, int T, int HF>
+template <int UR, int T, int HF, int PRE, bool XB>
 void launch_q4k_mfma_t(const DevWeight& w, MvArgs a, int R, hipStream_t s) {
     const int S = static_cast<int>(w.cols / 256);
     const int KS = (S + UR * R - 1) / (UR * R);
@@ -339,9 +344,37 @@ void launch_q4k_mfma_t(const DevWeight& w, MvArgs a, int R, hipStream_t s) {
     const size_t shmem = static_cast<size_t>(KS) * (wave_lds_bytes<UR>() + 16 * T * sizeof(float)) +
                          (a.norm_w ? kMaxKS * sizeof(double) : 0);
     const dim3 grid(static_cast<unsigned>(w.rows_pad / (16 * T))), block(64 * KS);
-    if (a.norm_w) q4k_mfma_kernel<UR, T, true, HF><<<grid, block, shmem, s>>>(a);
-    else q4k_mfma_kernel<UR, T, false, HF><<<grid, block, shmem, s>>>(a);
+    if (a.norm_w) q4k_mfma_kernel<UR, T, true, HF, PRE, XB><<<grid, block, shmem, s>>>(a);
+    else q4k_mfma_kernel<UR, T, false, HF, PRE, XB><<<grid, block, shmem, s>>>(a);
     LARQL_HIP_CHECK(hipGetLastError());
+}
+
+// The launch split of a Q4_K-family weight: ur super-blocks per round, t tiles per
+// workgroup, pre units issued with x, xb the x-first barrier, R rounds.
+struct Q4kSplit {
+    int ur, t, pre;
+    bool xb;
+    int R;
+};
+
+// Measured on MI355X (256 CUs, 16 rotating weight copies, back-to-back launches): rows
+// of <= 16 super-blocks with 1.5 .. 6 tiles per CU take two super-blocks per wave and
+// two tiles per workgroup, the first two units' loads issued with x ([14336 x 4096]
+// 7.52 us, against 7.73 with four tiles per workgroup; [6144 x 4096] 4.76 us); the
+// others four super-blocks per wave, one tile per workgroup, x issued by every wave
+// before any weight load ([4096 x 4096] 3.9 us, [28672 x 4096] 12.1 us, [4096 x 14336]
+// 7.5 us, against 8.1 with the loads of one unit issued with x).  Rows longer than
+// 16 waves x 4 super-blocks (K > 16384) take several rounds.  The per-wave phases
+// explain the spread: a wave cannot build its x planes before its x loads return, and
+// those queue behind weight loads already in flight (planes ready 0.7 .. 5.8 us into a
+// 7.5 us launch).
+Q4kSplit pick_q4k_split(const DevWeight& w, int num_cus) {
+    const size_t S = w.cols / 256;
+    const size_t tiles = w.rows_pad / 16, cus = static_cast<size_t>(num_cus);
+    const int R4 = static_cast<int>((S + 4 * kMaxKS - 1) / (4 * kMaxKS));
+    if (S <= 16 && 2 * tiles >= 3 * cus && tiles < 6 * cus && w.rows_pad % 32 == 0) return {2, 2, 2, false, 1};
+    if (S <= 16 && tiles >= 6 * cus) return {4, 1, 4, true, R4};
+    return {4, 1, 2, true, R4};
 }
 
 }  // namespace
@@ -357,22 +390,70 @@ void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s) {
     a.qs = w.qs;
     a.hdr = w.hdr;
     if (a.epi == EPI_GATED_PAIR && (w.rows & 1)) fail(LARQL_HIP_ERR_INVALID, "gated pair epilogue needs even rows");
-    // Measured (MI355X, 256 CUs, 16 rotating weight copies): [14336 x 4096] 7.5 us with
-    // two super-blocks per round and four tiles per workgroup (7.7 with 4 x 2, 8.1 with
-    // 4 x 1); [28672 x 4096] 12.8 us, [4096 x 14336] 8.0 us, [6144 x 4096] 4.8 us and
-    // [4096 x 4096] 4.0 us with 4 x 1 (every other split slower).  Rows longer than 16
-    // waves x 4 super-blocks (K > 16384) take several rounds.
-    const size_t S = w.cols / 256;
-    const size_t tiles = w.rows_pad / 16, cus = static_cast<size_t>(a.num_cus);
-    const int R4 = static_cast<int>((S + 4 * kMaxKS - 1) / (4 * kMaxKS));
-    if (w.format == LARQL_Q4_KF) {  // the two Q4_KF forms: the general split
-        if (w.hf == kHdrKf160) launch_q4k_mfma_t<4, 1, kHdrKf160>(w, a, R4, s);
-        else launch_q4k_mfma_t<4, 1, kHdrGguf>(w, a, R4, s);
-    } else if (S <= 16 && tiles >= 3 * cus && tiles < 6 * cus && w.rows_pad % 64 == 0) {
-        launch_q4k_mfma_t<2, 4, kHdr148>(w, a, 1, s);
-    } else {
-        launch_q4k_mfma_t<4, 1, kHdr148>(w, a, R4, s);
+    const Q4kSplit sp = pick_q4k_split(w, a.num_cus);
+    auto go = [&](auto hf) {
+        constexpr int HF = decltype(hf)::value;
+        if (sp.ur == 2) launch_q4k_mfma_t<2, 2, HF, 2, false>(w, a, sp.R, s);
+        else if (sp.pre == 4) launch_q4k_mfma_t<4, 1, HF, 4, true>(w, a, sp.R, s);
+        else launch_q4k_mfma_t<4, 1, HF, 2, true>(w, a, sp.R, s);
+    };
+    if (w.format == LARQL_Q4_KF && w.hf == kHdrKf160) go(std::integral_constant<int, kHdrKf160>{});
+    else if (w.format == LARQL_Q4_KF) go(std::integral_constant<int, kHdrGguf>{});
+    else go(std::integral_constant<int, kHdr148>{});
+}
+
+namespace {
+
+// Every byte of the weight's device allocation loaded once (16 B non-temporal loads,
+// eight in flight per lane), XOR-folded to one word per workgroup: no arithmetic on the
+// values, so its time is what memory alone allows for these bytes in this launch shape.
+__global__ __launch_bounds__(64 * kMaxKS) void q4k_read_floor_kernel(const uint4* __restrict__ p, size_t n16,
+                                                                      uint32_t* __restrict__ out) {
+    const size_t G = static_cast<size_t>(gridDim.x) * blockDim.x;
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + 7 * G < n16; i += 8 * G) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = load_nt(p + i + u * G);
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
+    for (; i < n16; i += G) {
+        const uint4 v = load_nt(p + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc ^= static_cast<uint32_t>(__shfl_xor(static_cast<int>(acc), m));
+    __shared__ uint32_t wv[kMaxKS];
+    if ((threadIdx.x & 63) == 0) wv[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t f = 0;
+        for (unsigned w = 0; w < blockDim.x / 64; w++) f ^= wv[w];
+        out[blockIdx.x] = f;
+    }
+}
+
+}  // namespace
+
+void launch_q4k_read_floor(const DevWeight& w, uint32_t* out, size_t out_words, unsigned groups, unsigned threads,
+                           int num_cus, hipStream_t s) {
+    if ((w.format != LARQL_Q4_K && w.format != LARQL_Q4_KF) || w.cols % 256 != 0 || w.cols == 0 ||
+        w.rows_pad % 16 != 0 || w.bytes % 16 != 0)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "read floor: Q4_K-family weights only");
+    if (num_cus <= 0) num_cus = current_device_cus();
+    if (groups == 0 && threads == 0) {
+        const Q4kSplit sp = pick_q4k_split(w, num_cus);
+        const size_t S = w.cols / 256;
+        groups = static_cast<unsigned>(w.rows_pad / (16 * sp.t));
+        threads = static_cast<unsigned>(64 * ((S + sp.ur * sp.R - 1) / (sp.ur * sp.R)));
+    }
+    if (groups == 0 || threads == 0 || threads % 64 != 0 || threads > 64 * kMaxKS)
+        fail(LARQL_HIP_ERR_INVALID, "read floor: workgroup size must be 64 .. 1024 in steps of 64");
+    if (out_words < groups) fail(LARQL_HIP_ERR_INVALID, "read floor: out holds fewer words than workgroups");
+    q4k_read_floor_kernel<<<dim3(groups), dim3(threads), 0, s>>>(static_cast<const uint4*>(w.base), w.bytes / 16, out);
+    LARQL_HIP_CHECK(hipGetLastError());
 }
 
 }  // namespace larql

@@ -61,6 +61,7 @@ SIGNATURES = {
     "larql_hip_q4_vecmat": (_I, [_P, _P, _P, _SZ, _P, _SZ, _SZ]),
     "larql_hip_q4_matvec_pair_batch": (_I, [_P, _P, _SZ, _P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ]),
     "larql_hip_vecmat_dev": (_I, [_P, _U64, _P, _P, _P]),
+    "larql_hip_read_floor_dev": (_I, [_P, _U64, ctypes.c_uint, ctypes.c_uint, _P, _SZ, _P]),
     "larql_hip_pair_batch_dev": (_I, [_P, _U64, _U64, _P, _SZ, _P, _P, _P]),
     "larql_hip_q4k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
     "larql_hip_q6k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
@@ -561,6 +562,13 @@ class HipBackend:
     def vecmat_dev(self, handle: int, activation, out, stream=None):
         self._check(self._lib.larql_hip_vecmat_dev(self._ctx, handle, _dptr(activation), _dptr(out),
                                                    _stream_ptr(stream)))
+
+    def read_floor_dev(self, handle: int, out, workgroups: int = 0, threads: int = 0, stream=None):
+        """Plain read of a Q4_K-family weight's device bytes (a measurement of the memory
+        floor): in its matvec's launch shape by default, else `workgroups` x `threads`.
+        out: device int32/uint32 tensor, one XOR fold per workgroup."""
+        self._check(self._lib.larql_hip_read_floor_dev(self._ctx, handle, workgroups, threads, _dptr(out),
+                                                       out.numel(), _stream_ptr(stream)))
 
     def pair_batch_dev(self, gate: int, up: int, x, seq_len: int, gate_out, up_out, stream=None):
         self._check(self._lib.larql_hip_pair_batch_dev(self._ctx, gate, up, _dptr(x), seq_len, _dptr(gate_out),

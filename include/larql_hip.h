@@ -180,6 +180,16 @@ int larql_hip_quantize_weights(larql_hip_ctx* ctx, int format, const float* x, s
 int larql_hip_matvec_dev(larql_hip_ctx* ctx, uint64_t handle, const void* x, const float* x_scales,
                          float* out, size_t m, void* stream);
 
+/* Measurement aid with no counterpart in the reference: reads every device byte of a
+ * registered Q4_K / Q4_KF weight once and does no arithmetic on them, so its duration is
+ * the memory floor for those bytes in that launch shape.  workgroups = threads = 0: the
+ * launch shape of the weight's matvec (4 * ceil(rows / 64) words of out always suffice);
+ * else `workgroups` workgroups of `threads` (64 .. 1024, a multiple of 64).  out: device
+ * uint32 [out_words], out_words >= the workgroup count; receives one XOR fold of the
+ * bytes per workgroup. */
+int larql_hip_read_floor_dev(larql_hip_ctx* ctx, uint64_t handle, unsigned workgroups, unsigned threads,
+                             uint32_t* out, size_t out_words, void* stream);
+
 /* q4_vecmat with a registered Q4_0 weight (rows = intermediate, cols = hidden), device
  * activation f32 [rows] and output f32 [cols].  Uses a partials buffer owned by the
  * context: device calls on one context must not overlap on different streams. */

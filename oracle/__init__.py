@@ -71,6 +71,9 @@ def _load():
             "lo_rms_norm_heads": (None, [_P, _SZ, _SZ, ctypes.c_double]),
             "lo_attend_f16": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
             "lo_decode_layer": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, ctypes.c_double]),
+            "lo_decode_layer_mt": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, ctypes.c_double,
+                                           ctypes.c_int]),
+            "lo_proj_rows_mt": (None, [ctypes.c_int, _P, _P, ctypes.c_int, _P, _P, _SZ, _SZ, ctypes.c_int]),
             "lo_decode_layer_window": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, ctypes.c_double,
                                               _SZ]),
             "lo_gauss_f32": (None, [ctypes.c_uint64, ctypes.c_float, ctypes.c_float, _P, _SZ]),
@@ -378,7 +381,7 @@ class _Layer(ctypes.Structure):
 
 
 def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, num_kv: int,
-                 head_dim: int, rope_base: float, eps: float = 1e-6, window: int = 0):
+                 head_dim: int, rope_base: float, eps: float = 1e-6, window: int = 0, threads: int = 1):
     """One decoder layer on the CPU.  ``layer`` holds numpy arrays keyed as the
     lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits) are updated in place.
     window > 0 attends over the last `window` positions only.  ``layer["formats"]``
@@ -421,9 +424,31 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
     st.rotary_dim = int(layer.get("rotary_dim", 0))
     st.attn_scale = float(layer.get("attn_scale", 0.0))
     h = np.array(h, dtype=np.float32, copy=True)
-    _load().lo_decode_layer_window(ctypes.byref(st), _ptr(h), pos, hidden, inter, num_q, num_kv,
-                                   head_dim, rope_base, eps, window)
+    if threads > 1:
+        assert window == 0
+        _load().lo_decode_layer_mt(ctypes.byref(st), _ptr(h), pos, hidden, inter, num_q, num_kv,
+                                   head_dim, rope_base, eps, threads)
+    else:
+        _load().lo_decode_layer_window(ctypes.byref(st), _ptr(h), pos, hidden, inter, num_q, num_kv,
+                                       head_dim, rope_base, eps, window)
     return h
+
+
+_FMT_CODES = {"q4_k": 0, "q6_k": 1, "q4_kf": 2, "q4_kf160": 3, "q8_0": 4, "q4_0": 5}
+
+
+def proj_rows_mt(fmt: str, w, x, rows: int, cols: int, threads: int, scales=None, q8_input: bool = False):
+    """One projection out = W x with its rows split over `threads` threads (the one-thread
+    kernel on each contiguous slice: identical output).  fmt as decode_layer's formats;
+    Q8_0 takes int8 weights and f32 `scales`; q8_input: Q4_0 against the Q8-quantized x."""
+    code = _FMT_CODES[fmt]
+    w = _c(w, np.int8 if code == 4 else np.uint8)
+    x = _c(x, np.float32)
+    sc = _c(scales, np.float32) if scales is not None else None
+    out = np.empty(rows, dtype=np.float32)
+    _load().lo_proj_rows_mt(code, _ptr(w), _ptr(sc) if sc is not None else None, int(q8_input), _ptr(x),
+                            _ptr(out), rows, cols, threads)
+    return out
 
 
 # ── the reference's own C kernel (x86 scalar path), when built ──────────

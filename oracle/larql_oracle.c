@@ -21,6 +21,7 @@
 #include "larql_oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -765,11 +766,13 @@ void lo_rms_norm_heads(float* x, size_t num_heads, size_t head_dim, double eps) 
 /* LI/src/attention/gqa.rs:29-110, last query row only: s = (k.q) * scale;
  * e = exp((s - max) as f64); sum in f64; p = (e as f32) * ((1/sum) as f32); out = V^T p.
  * K/V come from an fp16 cache [t][kv_head][head_dim]; kv_h = h / (num_q / num_kv). */
-void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T,
-                   size_t num_q, size_t num_kv, size_t head_dim, float scale, float* out) {
-    size_t reps = num_q / num_kv, kvd = num_kv * head_dim;
+/* Query heads [h0, h1): scores, softmax in f64, then the weighted V sum with t outermost
+ * (each output element still accumulates its T terms in ascending t, the same additions
+ * as a t-inner loop, while V is walked row by row). */
+static void lo_attend_heads(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T, size_t h0, size_t h1,
+                            size_t reps, size_t kvd, size_t head_dim, float scale, float* out) {
     float* sc = (float*)malloc(T * sizeof(float));
-    for (size_t h = 0; h < num_q; h++) {
+    for (size_t h = h0; h < h1; h++) {
         size_t kvh = h / reps;
         const float* qh = q + h * head_dim;
         for (size_t t = 0; t < T; t++) {
@@ -789,13 +792,18 @@ void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_
         float inv = (float)(1.0 / sum);
         for (size_t t = 0; t < T; t++) sc[t] *= inv;
         float* oh = out + h * head_dim;
-        for (size_t d = 0; d < head_dim; d++) {
-            float acc = 0.0f;
-            for (size_t t = 0; t < T; t++) acc += lo_f16_to_f32(vc[t * kvd + kvh * head_dim + d]) * sc[t];
-            oh[d] = acc;
+        for (size_t d = 0; d < head_dim; d++) oh[d] = 0.0f;
+        for (size_t t = 0; t < T; t++) {
+            const uint16_t* vr = vc + t * kvd + kvh * head_dim;
+            for (size_t d = 0; d < head_dim; d++) oh[d] += lo_f16_to_f32(vr[d]) * sc[t];
         }
     }
     free(sc);
+}
+
+void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T,
+                   size_t num_q, size_t num_kv, size_t head_dim, float scale, float* out) {
+    lo_attend_heads(q, kc, vc, T, 0, num_q, num_q / num_kv, num_kv * head_dim, head_dim, scale, out);
 }
 
 /* A projection in its layer's format: Q4_K (0), Q6_K (1), Q4_KF 144-byte GGUF (2), Q4_KF
@@ -825,6 +833,96 @@ static void lo_proj_q(int fmt, const uint8_t* w, const float* ws, int q8in, cons
     }
 }
 
+/* Row-split drivers for the CPU baselines: rows of a projection go to threads in
+ * contiguous slices and each slice runs the one-thread kernel, so the output equals the
+ * one-thread output bit for bit (rows are independent). */
+static size_t lo_fmt_row_bytes(int fmt, size_t cols) {
+    switch (fmt) {
+        case 1: return cols / 256 * 210;
+        case 2: return cols / 256 * 144;
+        case 3: return cols / 256 * 160;
+        case 4: return cols;
+        case 5: return cols / 32 * 18;
+        default: return cols / 256 * 148;
+    }
+}
+
+typedef struct {
+    int fmt, q8in;
+    const uint8_t* w;
+    const float *ws, *x;
+    float* out;
+    size_t rows, cols;
+} lo_proj_job;
+
+static void* lo_proj_job_run(void* p) {
+    const lo_proj_job* j = (const lo_proj_job*)p;
+    if (j->rows) lo_proj_q(j->fmt, j->w, j->ws, j->q8in, j->x, j->out, j->rows, j->cols);
+    return NULL;
+}
+
+static void lo_proj_n(int nt, int fmt, const uint8_t* w, const float* ws, int q8in, const float* x, float* out,
+                      size_t rows, size_t cols) {
+    if (nt <= 1 || rows < (size_t)nt) {
+        lo_proj_q(fmt, w, ws, q8in, x, out, rows, cols);
+        return;
+    }
+    if (nt > 256) nt = 256;
+    pthread_t th[256];
+    int started[256];
+    lo_proj_job jb[256];
+    const size_t rb = lo_fmt_row_bytes(fmt, cols);
+    for (int t = 0; t < nt; t++) {
+        const size_t r0 = rows * (size_t)t / (size_t)nt, r1 = rows * (size_t)(t + 1) / (size_t)nt;
+        jb[t] = (lo_proj_job){fmt, q8in, w + r0 * rb, ws ? ws + r0 * (cols / 32) : NULL, x, out + r0, r1 - r0, cols};
+        started[t] = pthread_create(&th[t], NULL, lo_proj_job_run, &jb[t]) == 0;
+        if (!started[t]) lo_proj_job_run(&jb[t]);
+    }
+    for (int t = 0; t < nt; t++)
+        if (started[t]) pthread_join(th[t], NULL);
+}
+
+typedef struct {
+    const float* q;
+    const uint16_t *kc, *vc;
+    size_t T, h0, h1, reps, kvd, head_dim;
+    float scale;
+    float* out;
+} lo_attend_job;
+
+static void* lo_attend_job_run(void* p) {
+    const lo_attend_job* j = (const lo_attend_job*)p;
+    if (j->h1 > j->h0) lo_attend_heads(j->q, j->kc, j->vc, j->T, j->h0, j->h1, j->reps, j->kvd, j->head_dim, j->scale,
+                                       j->out);
+    return NULL;
+}
+
+/* Attention with the query heads split over nt threads (each head is independent). */
+static void lo_attend_n(int nt, const float* q, const uint16_t* kc, const uint16_t* vc, size_t T, size_t num_q,
+                        size_t num_kv, size_t head_dim, float scale, float* out) {
+    if (nt <= 1) {
+        lo_attend_f16(q, kc, vc, T, num_q, num_kv, head_dim, scale, out);
+        return;
+    }
+    if (nt > 256) nt = 256;
+    pthread_t th[256];
+    int started[256];
+    lo_attend_job jb[256];
+    for (int t = 0; t < nt; t++) {
+        jb[t] = (lo_attend_job){q, kc, vc, T, num_q * (size_t)t / (size_t)nt, num_q * (size_t)(t + 1) / (size_t)nt,
+                                num_q / num_kv, num_kv * head_dim, head_dim, scale, out};
+        started[t] = pthread_create(&th[t], NULL, lo_attend_job_run, &jb[t]) == 0;
+        if (!started[t]) lo_attend_job_run(&jb[t]);
+    }
+    for (int t = 0; t < nt; t++)
+        if (started[t]) pthread_join(th[t], NULL);
+}
+
+void lo_proj_rows_mt(int fmt, const uint8_t* w, const float* ws, int q8in, const float* x, float* out, size_t rows,
+                     size_t cols, int nthreads) {
+    lo_proj_n(nthreads, fmt, w, ws, q8in, x, out, rows, cols);
+}
+
 /* One decoder layer (LI/src/attention/block.rs:52-157, LI/src/forward/layer.rs:50-94; per-op
  * order of the reference GPU decode LC/src/metal/decode.rs:144-739):
  *   xn = norm(h, input_norm); q, k, v = projections; [V-norm]; RoPE(q, k) at pos;
@@ -845,9 +943,26 @@ void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,
 
 /* Same, attending over the last `window` positions only when window > 0 and T = pos + 1
  * exceeds it: t_start = T - window (LC/src/metal/shaders/kv_attention.rs:35). */
+static void lo_decode_layer_impl(const lo_layer_t* L, float* h, size_t pos, size_t hidden, size_t inter,
+                                 size_t num_q, size_t num_kv, size_t head_dim, double rope_base, double eps,
+                                 size_t window, int nt);
+
 void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
                             size_t hidden, size_t inter, size_t num_q, size_t num_kv, size_t head_dim,
                             double rope_base, double eps, size_t window) {
+    lo_decode_layer_impl(L, h, pos, hidden, inter, num_q, num_kv, head_dim, rope_base, eps, window, 1);
+}
+
+/* The same layer with each projection's rows split over nthreads threads (identical
+ * output; the CPU baseline's all-core decode). */
+void lo_decode_layer_mt(const lo_layer_t* L, float* h, size_t pos, size_t hidden, size_t inter, size_t num_q,
+                        size_t num_kv, size_t head_dim, double rope_base, double eps, int nthreads) {
+    lo_decode_layer_impl(L, h, pos, hidden, inter, num_q, num_kv, head_dim, rope_base, eps, 0, nthreads);
+}
+
+static void lo_decode_layer_impl(const lo_layer_t* L, float* h, size_t pos, size_t hidden, size_t inter,
+                                 size_t num_q, size_t num_kv, size_t head_dim, double rope_base, double eps,
+                                 size_t window, int nt) {
     size_t qd = num_q * head_dim, kvd = num_kv * head_dim;
     const size_t rdim = L->rotary_dim ? L->rotary_dim : head_dim;
     const float off = L->norm_offset;
@@ -862,9 +977,9 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
     float* a = (float*)malloc(inter * sizeof(float));
 
     lo_rms_norm(h, L->input_norm, off, eps, xn, hidden);
-    lo_proj_q(L->fmt[0], L->wq, L->wq_s, 1, xn, q, qd, hidden);
-    lo_proj_q(L->fmt[1], L->wk, L->wk_s, 1, xn, k, kvd, hidden);
-    lo_proj_q(L->fmt[2], L->wv, L->wv_s, 1, xn, v, kvd, hidden);
+    lo_proj_n(nt, L->fmt[0], L->wq, L->wq_s, 1, xn, q, qd, hidden);
+    lo_proj_n(nt, L->fmt[1], L->wk, L->wk_s, 1, xn, k, kvd, hidden);
+    lo_proj_n(nt, L->fmt[2], L->wv, L->wv_s, 1, xn, v, kvd, hidden);
     if (L->has_v_norm) lo_rms_norm_heads(v, num_kv, head_dim, eps);
     lo_rope_at(q, num_q, head_dim, rdim, rope_base, pos);
     lo_rope_at(k, num_kv, head_dim, rdim, rope_base, pos);
@@ -874,8 +989,8 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
     }
     float scale = L->attn_scale != 0.0f ? L->attn_scale : (float)(1.0 / sqrt((double)head_dim));
     const size_t T = pos + 1, t0 = (window > 0 && T > window) ? T - window : 0;
-    lo_attend_f16(q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, T - t0, num_q, num_kv, head_dim, scale, att);
-    lo_proj_q(L->fmt[3], L->wo, L->wo_s, 1, att, o, hidden, qd);
+    lo_attend_n(nt, q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, T - t0, num_q, num_kv, head_dim, scale, att);
+    lo_proj_n(nt, L->fmt[3], L->wo, L->wo_s, 1, att, o, hidden, qd);
     if (L->has_post_norms) {
         lo_rms_norm(o, L->post_attn_norm, off, eps, xn, hidden);
         for (size_t i = 0; i < hidden; i++) h[i] = h[i] + xn[i];
@@ -884,11 +999,11 @@ void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
         for (size_t i = 0; i < hidden; i++) h[i] = h[i] + o[i];
         lo_rms_norm(h, L->post_attn_norm, off, eps, xn, hidden);
     }
-    lo_proj_q(L->fmt[4], L->gate, L->gate_s, 1, xn, g, inter, hidden);
-    lo_proj_q(L->fmt[5], L->up, L->up_s, 1, xn, u, inter, hidden);
+    lo_proj_n(nt, L->fmt[4], L->gate, L->gate_s, 1, xn, g, inter, hidden);
+    lo_proj_n(nt, L->fmt[5], L->up, L->up_s, 1, xn, u, inter, hidden);
     if (L->activation == 1) lo_gelu_tanh_gate_up(g, u, a, inter);
     else lo_silu_gate_up(g, u, a, inter);
-    lo_proj_q(L->fmt[6], L->down, L->down_s, 0, a, o, hidden, inter);
+    lo_proj_n(nt, L->fmt[6], L->down, L->down_s, 0, a, o, hidden, inter);
     if (L->has_post_norms) {
         lo_rms_norm(o, L->post_ffn_norm, off, eps, xn, hidden);
         for (size_t i = 0; i < hidden; i++) h[i] = h[i] + xn[i];

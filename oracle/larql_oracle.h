@@ -145,6 +145,14 @@ void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,
 void lo_decode_layer_window(const lo_layer_t* L, float* h, size_t pos,
                             size_t hidden, size_t inter, size_t num_q, size_t num_kv, size_t head_dim,
                             double rope_base, double eps, size_t window);
+/* lo_decode_layer (window 0) with each projection's rows split over nthreads threads;
+ * identical output (CPU baseline use). */
+void lo_decode_layer_mt(const lo_layer_t* L, float* h, size_t pos, size_t hidden, size_t inter, size_t num_q,
+                        size_t num_kv, size_t head_dim, double rope_base, double eps, int nthreads);
+/* One projection (format code as lo_layer_t.fmt; q8in: Q8-quantized input for Q4_0),
+ * rows split over nthreads threads; identical output to one thread. */
+void lo_proj_rows_mt(int fmt, const uint8_t* w, const float* ws, int q8in, const float* x, float* out, size_t rows,
+                     size_t cols, int nthreads);
 
 /* ── deterministic inputs (splitmix64 -> Box-Muller in f64 -> f32) ─────── */
 void lo_gauss_f32(uint64_t seed, float mean, float std, float* out, size_t n);

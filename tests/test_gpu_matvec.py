@@ -55,7 +55,8 @@ def fuzz_q6k(rows, cols, seed):
     return b.reshape(-1)
 
 
-Q4K_SHAPES = [(1, 256), (7, 256), (64, 512), (300, 4096), (1000, 2560), (14336, 4096), (4096, 14336), (100, 20480)]
+Q4K_SHAPES = [(1, 256), (7, 256), (64, 512), (300, 4096), (1000, 2560), (14336, 4096), (4096, 14336), (100, 20480),
+              (28672, 4096), (6144, 4096)]
 
 
 @pytest.mark.parametrize("rows,cols", Q4K_SHAPES)
@@ -260,3 +261,47 @@ def test_device_weight_quantizers_bit_exact(hip, fmt):
         q, s = hip.quantize_weights(larql_hip.Q8_0, w)
         rq, rs = oracle.quantize_weights_q8(w, rows, cols)
         assert np.array_equal(q, rq) and np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols", [(300, 4096), (14336, 4096), (4096, 14336), (28672, 4096)])
+def test_read_floor_reads_every_block(hip, rows, cols):
+    """The plain-read floor kernel folds the weight's device bytes by XOR, a linear map:
+    one nibble bit flipped in the first or the last super-block of the host bytes flips
+    exactly one bit of the total fold (so both ends of the allocation are read), the total
+    does not depend on the launch shape (every byte read exactly once in each), and the
+    same bytes give the same fold on every call."""
+    import torch
+
+    print(f"[read floor] rows={rows} cols={cols}", flush=True)
+    q = weights("q4k", rows, cols, seed=7 + rows)
+    words = 4 * ((rows + 63) // 64)
+
+    def fold(raw, shapes=((0, 0),)):
+        h = hip.register_weight(larql_hip.Q4_K, raw, rows, cols)
+        res = []
+        for g, t in shapes:
+            out = torch.zeros(max(words, g), dtype=torch.int32, device="cuda")
+            hip.read_floor_dev(h, out, g, t)
+            hip.read_floor_dev(h, out, g, t)
+            torch.cuda.synchronize()
+            res.append(int(np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))))
+        hip.release_weight(h)
+        hip.forget_host(raw)
+        return res
+
+    base = fold(q.copy(), ((0, 0), (2048, 256), (37, 1024), (7, 192)))
+    assert len(set(base)) == 1, [hex(v) for v in base]
+    assert fold(q.copy())[0] == base[0]
+    for pos in (20 + 5, q.size - 1):
+        m = q.copy()
+        m[pos] ^= 0x10
+        d = fold(m)[0] ^ base[0]
+        assert bin(d).count("1") == 1, (pos, hex(d))
+    h = hip.register_weight(larql_hip.Q4_K, q, rows, cols)
+    try:
+        for g, t, n in ((64, 256, 63), (8, 100, 8), (8, 2048, 8)):
+            with pytest.raises(larql_hip.LarqlHipError):
+                hip.read_floor_dev(h, torch.zeros(n, dtype=torch.int32, device="cuda"), g, t)
+    finally:
+        hip.release_weight(h)
+        hip.forget_host(q)

@@ -957,6 +957,39 @@ def test_decode_layer_q8_attention_q4_0_ffn_matches_float64_composition():
         assert _rel(got, ref((mut,))) > 1e-2, mut
 
 
+def test_threaded_drivers_equal_one_thread():
+    """The row-split drivers of the CPU baselines (lo_proj_rows_mt, lo_decode_layer_mt) run
+    the one-thread kernels on contiguous row slices: identical output for every format,
+    thread counts that do and do not divide the rows, and more threads than rows."""
+    dims = (256, 512, 4, 2, 64)
+    fm = {"wq": "q8_0", "wk": "q6_k", "wv": "q4_k", "wo": "q4_0", "gate": "q4_0", "up": "q4_k", "down": "q4_0"}
+    P = _tiny_layer(41, dims, fm)
+    hidden, inter, nq, nkv, hd = dims
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    for name, rows in (("wq", nq * hd), ("wk", nkv * hd), ("wv", nkv * hd), ("gate", inter), ("up", inter)):
+        f = fm[name]
+        q8in = f == "q4_0"
+        one = oracle.proj_rows_mt(f, P[name], x, rows, hidden, 1, P.get(name + "_s"), q8in)
+        for t in (3, 7, rows + 5):
+            got = oracle.proj_rows_mt(f, P[name], x, rows, hidden, t, P.get(name + "_s"), q8in)
+            assert np.array_equal(one.view(np.uint32), got.view(np.uint32)), (name, t)
+    kvd = nkv * hd
+    pos = 9
+    kc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
+    h = rng.standard_normal(hidden).astype(np.float32)
+    layer = {k: v for k, v in P.items() if k not in ("deq", "rope_base", "q8_input")}
+    outs = []
+    for t in (1, 5):
+        layer["k_cache"], layer["v_cache"] = kc.copy(), vc.copy()
+        outs.append((oracle.decode_layer(layer, h, pos, *dims, 10000.0, threads=t),
+                     layer["k_cache"].copy(), layer["v_cache"].copy()))
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                              b.view(np.uint32) if b.dtype == np.float32 else b)
+
+
 def test_q4_0_f32_matvec_closed_form():
     """q4_f32_matvec (LC/src/metal/shaders/q4_f32_matvec.rs:10-38): one-hot probes give
     (nib - 8) * f16(scale) per element (element 2j the low, 2j + 1 the high nibble of byte j),
