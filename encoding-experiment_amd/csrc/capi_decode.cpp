@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstring>
 #include <algorithm>
+#include <string>
 #include <vector>
 
 #include "capi_util.h"
@@ -86,6 +87,30 @@ struct Src {
     const float* scales = nullptr;  // Q8_0: f32 scales [rows][cols / 32]
 };
 
+// A pointer the caller declares to be device memory: an allocation the GPU addresses
+// (device, managed or pinned host memory) holding `bytes` from p.  Checked on the host
+// before any copy or kernel reads it, so a host address passed by mistake is an error,
+// not a GPU page fault.
+void require_device_range(const void* p, size_t bytes, const char* what) {
+    hipPointerAttribute_t at{};
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+        (void)hipGetLastError();
+        fail(LARQL_HIP_ERR_INVALID, std::string(what) + ": not a device address (weights_on_device is set)");
+    }
+    if (at.type != hipMemoryTypeDevice && at.type != hipMemoryTypeManaged && at.type != hipMemoryTypeUnified &&
+        !(at.type == hipMemoryTypeHost && at.devicePointer))
+        fail(LARQL_HIP_ERR_INVALID, std::string(what) + ": not a device address (weights_on_device is set)");
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) == hipSuccess && base) {
+        const auto b = reinterpret_cast<uintptr_t>(base), q = reinterpret_cast<uintptr_t>(p);
+        if (q < b || q - b > size || bytes > size - (q - b))
+            fail(LARQL_HIP_ERR_INVALID, std::string(what) + ": device buffer shorter than its shape");
+    } else {
+        (void)hipGetLastError();
+    }
+}
+
 // One device weight from one or more reference-layout sources: concatenated by rows
 // (stride 1) or interleaved (source i -> rows i, i+n, ...).
 DevWeight build_weight(larql_hip_ctx* c, larql_hip_model* m, int format, size_t cols, const std::vector<Src>& srcs,
@@ -127,7 +152,10 @@ DevWeight build_weight(larql_hip_ctx* c, larql_hip_model* m, int format, size_t 
         const size_t sbytes = format == LARQL_Q8_0 ? s.rows * (cols / 32) * sizeof(float) : 0;
         const uint8_t* raw = static_cast<const uint8_t*>(s.data);
         const float* sc = s.scales;
-        if (!on_device) {
+        if (on_device) {
+            require_device_range(s.data, nbytes, "decode: weight");
+            if (sbytes) require_device_range(s.scales, sbytes, "decode: Q8_0 weight scales");
+        } else {
             const size_t soff = (nbytes + 255) & ~size_t(255);
             uint8_t* stage = static_cast<uint8_t*>(larql::ensure(c, c->stage_raw, soff + sbytes));
             LARQL_HIP_CHECK(hipMemcpyAsync(stage, s.data, nbytes, hipMemcpyHostToDevice, c->stream));
@@ -147,6 +175,7 @@ DevWeight build_weight(larql_hip_ctx* c, larql_hip_model* m, int format, size_t 
 
 float* upload_vec(larql_hip_ctx* c, larql_hip_model* m, const float* v, size_t n, bool on_device) {
     if (!v) fail(LARQL_HIP_ERR_INVALID, "decode: null norm vector");
+    if (on_device) require_device_range(v, n * sizeof(float), "decode: norm vector");
     float* d = static_cast<float*>(dev_alloc(m, n * sizeof(float)));
     LARQL_HIP_CHECK(hipMemcpyAsync(d, v, n * sizeof(float), on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                                    c->stream));
@@ -393,15 +422,9 @@ void int_proj(const DevWeight& w, larql_hip_model* m, float* out, hipStream_t s)
     else larql::launch_q4_0_matvec(w, m->q8, m->q8s, out, 1, s);
 }
 
-void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float* hidden_out, float* logits,
-                hipStream_t s) {
+// The layer launches of one decode step at T = pos + 1, h0 -> h0.
+void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hipStream_t s) {
     auto& kv = c->kv;
-    kv_ensure(c, m->layers.size(), m->nkv, m->hd, kv.current_len + 1);
-    const int T = static_cast<int>(kv.current_len) + 1;
-    const int S = (T + 63) / 64;
-    float* part = static_cast<float*>(
-        larql::ensure(c, m->part, static_cast<size_t>(m->nq) * S * (m->hd + 2) * sizeof(float)));
-    larql::launch_copy_f32(x_dev, m->h0, m->hidden, s);
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
         // Q/K/V: f32-input formats with the input norm fused into the matvec; Q8_0 from the
@@ -546,6 +569,18 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
             larql::launch_mv(L.down, d, s);
         }
     }
+}
+
+void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float* hidden_out, float* logits,
+                hipStream_t s) {
+    auto& kv = c->kv;
+    kv_ensure(c, m->layers.size(), m->nkv, m->hd, kv.current_len + 1);
+    const int T = static_cast<int>(kv.current_len) + 1;
+    const int S = (T + 63) / 64;
+    float* part = static_cast<float*>(
+        larql::ensure(c, m->part, static_cast<size_t>(m->nq) * S * (m->hd + 2) * sizeof(float)));
+    larql::launch_copy_f32(x_dev, m->h0, m->hidden, s);
+    enqueue_layers(c, m, T, part, s);
     kv.current_len = static_cast<size_t>(T);
     if (hidden_out) larql::launch_copy_f32(m->h0, hidden_out, m->hidden, s);
     if (logits) {

@@ -180,9 +180,24 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     const bool fresh = owner && a.batch == 0;
     const int klim = a.batch ? pos + 1 : pos;  // K rows read from the cache: t < klim
 
-    // 1. Global loads, all issued up front.  K rows below pos as score A operands
-    // (lane (g, c) of wave w: position t0 + 16 w + c, dims 32 ks + 8 g ..); V blocks at or
-    // below pos as P.V A operands (dims 16 dt + c, positions t0 + 32 ts + 8 g ..).
+    // 1. Global loads, all issued up front: first the query heads, the RoPE row and the
+    // new K/V row (needed first, and loads return in order), then K rows below pos as
+    // score A operands (lane (g, c) of wave w: position t0 + 16 w + c, dims 32 ks + 8 g ..)
+    // and V blocks at or below pos as P.V A operands (dims 16 dt + c, positions
+    // t0 + 32 ts + 8 g ..).
+    constexpr int QPT = (8 * HD + kAttnThreads - 1) / kAttnThreads;  // query elements per thread
+    float qv[QPT];
+#pragma unroll
+    for (int u = 0; u < QPT; u++) {
+        const int i = tid + u * kAttnThreads;
+        qv[u] = i < reps * HD ? a.qkv[static_cast<size_t>(kvh * reps) * HD + i] : 0.f;
+    }
+    const float2 csv = tid < half ? a.rope[static_cast<size_t>(pos) * half + tid] : make_float2(0.f, 0.f);
+    float krv = 0.f, vnv = 0.f;
+    if (fresh && tid < HD) {
+        krv = a.qkv[q_dim + static_cast<size_t>(kvh) * HD + tid];
+        vnv = a.qkv[q_dim + kv_dim + static_cast<size_t>(kvh) * HD + tid];
+    }
     const int tk = t0 + 16 * wave + c;
     v4u kA[KS];
 #pragma unroll
@@ -203,14 +218,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
                             : v4u{0u, 0u, 0u, 0u};
         }
     }
-    for (int i = tid; i < reps * HD; i += kAttnThreads) qr_s[i] = a.qkv[static_cast<size_t>(kvh * reps) * HD + i];
-    for (int i = tid; i < half; i += kAttnThreads) cs_s[i] = a.rope[static_cast<size_t>(pos) * half + i];
-    if (fresh)
-        for (int i = tid; i < HD; i += kAttnThreads) {
-            kr_s[i] = a.qkv[q_dim + static_cast<size_t>(kvh) * HD + i];
-            vnew[i] = __builtin_bit_cast(uint16_t,
-                                         static_cast<_Float16>(a.qkv[q_dim + kv_dim + static_cast<size_t>(kvh) * HD + i]));
-        }
+#pragma unroll
+    for (int u = 0; u < QPT; u++) {
+        const int i = tid + u * kAttnThreads;
+        if (i < reps * HD) qr_s[i] = qv[u];
+    }
+    if (tid < half) cs_s[tid] = csv;
+    if (fresh && tid < HD) {
+        kr_s[tid] = krv;
+        vnew[tid] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vnv));
+    }
     __syncthreads();
     for (int i = tid; i < reps * HD; i += kAttnThreads) {
         const int h = i / HD, d = i - h * HD;

@@ -503,7 +503,9 @@ class HipBackend:
     def kv_truncate(self, n: int):
         self._check(self._lib.larql_hip_kv_truncate(self._ctx, n))
 
-    def model(self, layers, hidden: int, inter: int, weights_on_device: bool = True) -> DeviceModel:
+    def model(self, layers, hidden: int, inter: int, weights_on_device: bool = False) -> DeviceModel:
+        """weights_on_device: the layers' weight and norm pointers are device addresses
+        (else host memory, uploaded once)."""
         return DeviceModel(self, layers, hidden, inter, weights_on_device)
 
     # ── device-resident fast path ──────────────────────────────────────
