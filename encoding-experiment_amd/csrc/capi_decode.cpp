@@ -62,6 +62,10 @@ struct larql_hip_model {
     float* otmp = nullptr;  // post-norm layers: attention / FFN output before its norm
     float* utmp = nullptr;  // up projection of a Q8-input FFN
     float* xn = nullptr;    // normed input of a Q8-input projection
+    // Normed input handed from an EPI_RESID projection to the next norm-fused one: x * (offset
+    // + w) and the producer's per-workgroup sums of x^2 (Q4_K MFMA kernels on both sides)
+    float* xw = nullptr;
+    double* psum = nullptr;
     int8_t* q8 = nullptr;   // Q8 activation of a Q8-input projection (quantize_to_q8)
     float* q8s = nullptr;
     float* ones = nullptr;  // weight of the weight-free norm in a fused matvec prologue
@@ -292,6 +296,8 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
         m->otmp = static_cast<float*>(dev_alloc(m, hidden * 4));
         m->utmp = static_cast<float*>(dev_alloc(m, inter * 4));
         m->xn = static_cast<float*>(dev_alloc(m, hidden * 4));
+        m->xw = static_cast<float*>(dev_alloc(m, hidden * 4));
+        m->psum = static_cast<double*>(dev_alloc(m, (hidden / 16 + 64) * sizeof(double)));
         const size_t widest = std::max({hidden, inter, m->q_dim});
         m->q8 = static_cast<int8_t*>(dev_alloc(m, widest));
         m->q8s = static_cast<float*>(dev_alloc(m, widest / 32 * 4 + 4));
@@ -416,6 +422,11 @@ void quantize_input(larql_hip_model* m, const float* x, size_t n, const float* n
     larql::launch_quantize_q8(src, n, 1, m->q8, m->q8s, s);
 }
 
+// Weights whose m = 1 matvec is the Q4_K MFMA kernel (the producer / consumer epilogues).
+bool q4k_mfma(const DevWeight& w) { return w.format == LARQL_Q4_K || w.format == LARQL_Q4_KF; }
+// A Q4_K MFMA consumer able to take n producer partial sums.
+bool takes_psum(const DevWeight& w, int n) { return q4k_mfma(w) && n <= larql::q4k_mfma_max_psum(w, 0); }
+
 // out = W . (the model's Q8 activation), blocks accumulated in order (bit-exact int dots).
 void int_proj(const DevWeight& w, larql_hip_model* m, float* out, hipStream_t s) {
     if (w.format == LARQL_Q8_0) larql::launch_q8_matvec(w, m->q8, m->q8s, out, 1, s);
@@ -425,6 +436,10 @@ void int_proj(const DevWeight& w, larql_hip_model* m, float* out, hipStream_t s)
 // The layer launches of one decode step at T = pos + 1, h0 -> h0.
 void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hipStream_t s) {
     auto& kv = c->kv;
+    // prenormed: m->xw / m->psum hold this layer's normed Q/K/V input (from the previous
+    // layer's down projection), npsum partial sums
+    bool prenormed = false;
+    int npsum = 0;
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
         // Q/K/V: f32-input formats with the input norm fused into the matvec; Q8_0 from the
@@ -439,9 +454,15 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hi
                 larql::MvArgs a;
                 a.x = m->h0;
                 a.out = out;
-                a.norm_w = L.input_norm;
-                a.norm_offset = L.norm_offset;
                 a.eps = L.eps;
+                if (prenormed) {
+                    a.x = m->xw;
+                    a.x_psum = m->psum;
+                    a.x_npsum = npsum;
+                } else {
+                    a.norm_w = L.input_norm;
+                    a.norm_offset = L.norm_offset;
+                }
                 larql::launch_mv(w, a, s);
             }
         };
@@ -487,13 +508,6 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hi
                                               m->hidden, L.eps, s);
             else
                 larql::launch_add_rows(m->h0, m->otmp, m->h1, m->hidden, s);
-        } else {
-            larql::MvArgs o;
-            o.x = m->attn;
-            o.out = m->h1;
-            o.epi = larql::EPI_RESID;
-            o.resid = m->h0;
-            larql::launch_mv(L.wo, o, s);
         }
 
         // FFN input norm: post_attn_norm, or pre_ffn_norm (weight-free when absent) for
@@ -504,14 +518,41 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hi
             fnorm = L.pre_ffn_norm ? L.pre_ffn_norm : m->ones;
             foff = L.pre_ffn_norm ? L.norm_offset : 0.0f;
         }
+        const bool g_q8 = !L.split_gu ? false : takes_q8(L.gate, false), u_q8 = !L.split_gu ? false : takes_q8(L.up, false);
+        // Llama O projection: h1 = h + Wo attn; it also hands the FFN its normed input when
+        // both sides run the Q4_K MFMA kernel
+        const int o_groups = q4k_mfma(L.wo) ? larql::q4k_mfma_groups(L.wo, 0) : 0;
+        const bool ffn_prenormed = !(L.post_norms || o_q8) && q4k_mfma(L.wo) &&
+                                   (L.split_gu ? !g_q8 && !u_q8 && takes_psum(L.gate, o_groups) &&
+                                                     takes_psum(L.up, o_groups)
+                                               : takes_psum(L.gateup, o_groups));
+        if (!(L.post_norms || o_q8)) {
+            larql::MvArgs o;
+            o.x = m->attn;
+            o.out = m->h1;
+            o.epi = larql::EPI_RESID;
+            o.resid = m->h0;
+            if (ffn_prenormed) {
+                o.out2 = m->xw;
+                o.out2_w = fnorm;
+                o.out2_off = foff;
+                o.psum = m->psum;
+            }
+            larql::launch_mv(L.wo, o, s);
+        }
         larql::MvArgs g;
         g.x = m->h1;
         g.out = m->act;
         g.act = L.act;
         g.eps = L.eps;
-        g.norm_w = fnorm;
-        g.norm_offset = foff;
-        const bool g_q8 = !L.split_gu ? false : takes_q8(L.gate, false), u_q8 = !L.split_gu ? false : takes_q8(L.up, false);
+        if (ffn_prenormed) {
+            g.x = m->xw;
+            g.x_psum = m->psum;
+            g.x_npsum = o_groups;
+        } else {
+            g.norm_w = fnorm;
+            g.norm_offset = foff;
+        }
         if (g_q8 || u_q8) {  // gate and up apart, then act(gate) * up
             quantize_input(m, m->h1, m->hidden, fnorm, foff, L.eps, s);
             float* outs[2] = {m->gtmp, m->utmp};
@@ -566,8 +607,24 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hi
             d.epi = larql::EPI_RESID;
             d.resid = m->h1;
             d.out_scale = scale;
+            // the next layer's normed Q/K/V input, when both sides run the Q4_K MFMA kernel
+            const LayerDev* Ln = l + 1 < m->layers.size() ? &m->layers[l + 1] : nullptr;
+            const int d_groups = q4k_mfma(L.down) ? larql::q4k_mfma_groups(L.down, 0) : 0;
+            prenormed = Ln && q4k_mfma(L.down) &&
+                        (Ln->split_qkv ? takes_psum(Ln->wq, d_groups) && takes_psum(Ln->wk, d_groups) &&
+                                             takes_psum(Ln->wv, d_groups)
+                                       : takes_psum(Ln->qkv, d_groups));
+            if (prenormed) {
+                d.out2 = m->xw;
+                d.out2_w = Ln->input_norm;
+                d.out2_off = Ln->norm_offset;
+                d.psum = m->psum;
+                npsum = d_groups;
+            }
             larql::launch_mv(L.down, d, s);
+            continue;
         }
+        prenormed = false;
     }
 }
 

@@ -34,6 +34,18 @@ struct MvArgs {
     const float* resid = nullptr;
     int act = 0;             // gated epilogues: 0 = SiLU, 1 = GELU-tanh (Activation, LC/src/pipeline.rs:48-54)
     float out_scale = 1.0f;  // EPI_RESID: (resid + dot) * out_scale, the layer scalar (LC/src/metal/decode.rs:717-728)
+    // Q4_K MFMA kernel only.  Producer (EPI_RESID): also out2[n] = out[n] * (out2_off +
+    // out2_w[n]), the next matvec's norm-weighted input, and psum[workgroup] = sum of
+    // out[n]^2 over the workgroup's rows (f64).  Consumer: x already carries the norm
+    // weight; x_psum[0 .. x_npsum) are its producer's partial sums of squares, and the row
+    // totals are scaled by 1 / sqrt(sum / cols + eps) (an RMSNorm whose statistics come
+    // with its input).
+    float* out2 = nullptr;
+    const float* out2_w = nullptr;
+    float out2_off = 0.f;
+    double* psum = nullptr;
+    const double* x_psum = nullptr;
+    int x_npsum = 0;
     // launch shape: waves per row slot, row tiles, tiles per workgroup, CUs on the device,
     // device rows (a multiple of 64; rows past `rows` decode to zero)
     int wpr = 1, tiles = 0, steps = 1, num_cus = 0, rows_pad = 0;
@@ -183,5 +195,9 @@ void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s);
 bool stream_mv_supported(const DevWeight& w);
 void launch_mv_stream(const DevWeight& w, MvArgs a, hipStream_t s);
 void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s);
+// Workgroups of launch_q4k_mfma for this weight (the partial sums a producer writes), and
+// the most partial sums its launch can take as a consumer (two per thread).
+int q4k_mfma_groups(const DevWeight& w, int num_cus);
+int q4k_mfma_max_psum(const DevWeight& w, int num_cus);
 
 }  // namespace larql

@@ -173,6 +173,22 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
     load_x(0);
     if constexpr (XB) __builtin_amdgcn_s_barrier();
     load_units(0, 0, PRE);
+    // Loaded now, used at the end (so the epilogue waits on no memory): the producer's
+    // partial sums of squares of a prenormed x, and wave 0's residual and out2 weight rows.
+    double ps0 = 0.0, ps1 = 0.0;
+    float rv_pre = 0.f, w2_pre = 0.f;
+    if constexpr (!NORM) {
+        if (a.x_psum) {
+            const int i0 = static_cast<int>(threadIdx.x), i1 = i0 + static_cast<int>(blockDim.x);
+            if (i0 < a.x_npsum) ps0 = a.x_psum[i0];
+            if (i1 < a.x_npsum) ps1 = a.x_psum[i1];
+        }
+        const int row = static_cast<int>(tile0 * 16) + lane;
+        if (wave == 0 && lane < 16 * T && row < a.rows) {
+            if (a.epi == EPI_RESID || a.epi == EPI_GATED_MUL) rv_pre = a.resid[row];
+            if (a.out2) w2_pre = a.out2_w[row];
+        }
+    }
 
     // Fused RMSNorm (LI/src/residual.rs:17-33): sum(x^2) over all of x, in f64.
     float inv_rms = 1.f;
@@ -319,16 +335,39 @@ __global__ __launch_bounds__((64 * max_waves<UR, T>())) void q4k_mfma_kernel(MvA
         v = swap16_add(v, v);
         if (lane < 16) red[(wave * T + t) * 16 + lane] = v;
     }
+    double* xsq = reinterpret_cast<double*>(red + KS * 16 * T);  // prenormed input: per-wave sums
+    if (!NORM && a.x_psum) {
+        const double v = wave_sum_d(ps0 + ps1);
+        if (lane == 0) xsq[wave] = v;
+    }
     __syncthreads();
-    if (wave == 0 && lane < 16 * T) {
-        float tot = red[lane];
-        for (int w = 1; w < KS; w++) tot += red[w * 16 * T + lane];
+    if (wave == 0) {
         const int row = static_cast<int>(tile0 * 16) + lane;
+        float tot = 0.f;
+        if (lane < 16 * T) {
+            tot = red[lane];
+            for (int w = 1; w < KS; w++) tot += red[w * 16 * T + lane];
+        }
+        if (!NORM && a.x_psum) {
+            double sq = 0.0;
+            for (int w = 0; w < KS; w++) sq += xsq[w];
+            // rms as the CPU path rounds it (LI/src/residual.rs:24)
+            const float rms = static_cast<float>(sqrt(sq / static_cast<double>(a.cols) + a.eps));
+            tot *= 1.0f / rms;
+        }
         if (a.epi == EPI_GATED_PAIR) {
             const float up = __shfl_down(tot, 1, 64);  // rows 2i, 2i + 1 sit in adjacent lanes of one tile
-            if ((lane & 1) == 0 && row < a.rows) a.out[row >> 1] = gated_act(a.act, tot, up);
-        } else if (row < a.rows) {
-            a.out[row] = epi_value(a, a.epi == EPI_STORE ? 0.f : a.resid[row], tot);
+            if (lane < 16 * T && (lane & 1) == 0 && row < a.rows) a.out[row >> 1] = gated_act(a.act, tot, up);
+        } else {
+            const bool live = lane < 16 * T && row < a.rows;
+            const float rv = a.epi == EPI_STORE ? 0.f : (NORM ? (live ? a.resid[row] : 0.f) : rv_pre);
+            const float v = live ? epi_value(a, rv, tot) : 0.f;
+            if (live) a.out[row] = v;
+            if (!NORM && a.out2 && live) a.out2[row] = v * (a.out2_off + w2_pre);
+            if (!NORM && a.psum) {
+                const double q = wave_sum_d(static_cast<double>(v) * static_cast<double>(v));
+                if (lane == 0) a.psum[blockIdx.x] = q;
+            }
         }
     }
 }
@@ -342,7 +381,11 @@ void launch_q4k_mfma_t(const DevWeight& w, MvArgs a, int R, hipStream_t s) {
     a.steps = R;
     if (KS > max_waves<UR, T>()) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4k matvec: row too long for this split");
     const size_t shmem = static_cast<size_t>(KS) * (wave_lds_bytes<UR>() + 16 * T * sizeof(float)) +
-                         (a.norm_w ? kMaxKS * sizeof(double) : 0);
+                         (a.norm_w || a.x_psum ? kMaxKS * sizeof(double) : 0);
+    if (a.x_psum && (a.norm_w || a.x_npsum > 2 * 64 * KS))
+        fail(LARQL_HIP_ERR_INVALID, "q4k matvec: prenormed input with a norm, or too many partial sums");
+    if ((a.out2 || a.psum) && (a.epi != EPI_RESID || a.norm_w))
+        fail(LARQL_HIP_ERR_INVALID, "q4k matvec: out2 / psum need EPI_RESID and no fused norm");
     const dim3 grid(static_cast<unsigned>(w.rows_pad / (16 * T))), block(64 * KS);
     if (a.norm_w) q4k_mfma_kernel<UR, T, true, HF, PRE, XB><<<grid, block, shmem, s>>>(a);
     else q4k_mfma_kernel<UR, T, false, HF, PRE, XB><<<grid, block, shmem, s>>>(a);
@@ -400,6 +443,18 @@ void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s) {
     if (w.format == LARQL_Q4_KF && w.hf == kHdrKf160) go(std::integral_constant<int, kHdrKf160>{});
     else if (w.format == LARQL_Q4_KF) go(std::integral_constant<int, kHdrGguf>{});
     else go(std::integral_constant<int, kHdr148>{});
+}
+
+int q4k_mfma_groups(const DevWeight& w, int num_cus) {
+    if (num_cus <= 0) num_cus = current_device_cus();
+    return static_cast<int>(w.rows_pad / (16 * pick_q4k_split(w, num_cus).t));
+}
+
+int q4k_mfma_max_psum(const DevWeight& w, int num_cus) {
+    if (num_cus <= 0) num_cus = current_device_cus();
+    const Q4kSplit sp = pick_q4k_split(w, num_cus);
+    const size_t S = w.cols / 256;
+    return static_cast<int>(2 * 64 * ((S + sp.ur * sp.R - 1) / (sp.ur * sp.R)));
 }
 
 namespace {
