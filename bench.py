@@ -29,6 +29,7 @@ PMC helpers (used to produce profiles/q4k_matvec_traffic.json):
   bench.py --pmc-pass calib   plain 64 MiB device copies (known bytes) for scaling
   bench.py --pmc-pass gate    gate-shape Q4_K matvec launches
   bench.py --pmc-pass floor   the plain-read floor kernel over the same gate weights
+  bench.py --pmc-pass knn     the Q4_0 gate-KNN walk (34 layers [10240x2560], 256 queries)
   bench.py --pmc-report CALIB_FETCH CALIB_WRITE GATE_FETCH GATE_WRITE [--pmc-floor FLOOR_FETCH]
 """
 from __future__ import annotations
@@ -619,6 +620,27 @@ def pmc_pass(which: str, launches: int):
         torch.cuda.synchronize()
         return
     be = larql_hip.HipBackend(0, strict=True)
+    if which == "knn":  # the Q4_0 gate-KNN walk: 34 layers [10240 x 2560], 256 queries, top-32
+        L, F, K, Q, k = 34, 10240, 2560, 256, 32
+        gen = torch.Generator(device=dev)
+        hq = []
+        for l in range(L):
+            gen.manual_seed(9000 + l)
+            g = torch.randn(F, K, generator=gen, device=dev, dtype=torch.float32) * 0.02
+            raw = torch.empty(F * K // 32 * 18, dtype=torch.uint8, device=dev)
+            be.quantize_weights_dev(larql_hip.Q4_0, g, F * K, raw, stream=stream)
+            torch.cuda.synchronize()
+            hq.append(be.register_weight_device(larql_hip.Q4_0, raw, raw.numel(), F, K))
+            del g, raw
+        gen.manual_seed(4)
+        q = torch.randn(Q, K, generator=gen, device=dev, dtype=torch.float32)
+        di = torch.empty(L * Q * k, device=dev, dtype=torch.int32)
+        dv = torch.empty(L * Q * k, device=dev)
+        for _ in range(max(1, launches // 10)):
+            be.gate_knn_dev(hq, q, Q, k, di, dv, stream=stream)
+        torch.cuda.synchronize()
+        be.close()
+        return
     handles, xs, outs, _ = make_weights(be, torch, stream, copies=16)
     fold = torch.empty(14336 // 16 + 4, device=dev, dtype=torch.int32)
     for i in range(launches):
@@ -684,7 +706,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=1.5, help="per CPU-baseline leg (14 legs)")
     ap.add_argument("--eager", action="store_true", help="time Python-loop launches instead of a HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--pmc-pass", choices=("calib", "gate", "floor"))
+    ap.add_argument("--pmc-pass", choices=("calib", "gate", "floor", "knn"))
     ap.add_argument("--pmc-launches", type=int, default=50)
     ap.add_argument("--pmc-report", nargs=4, metavar=("CALIB_FETCH", "CALIB_WRITE", "GATE_FETCH", "GATE_WRITE"))
     ap.add_argument("--pmc-floor", metavar="FLOOR_FETCH", help="with --pmc-report: FETCH_SIZE of the read-floor pass")

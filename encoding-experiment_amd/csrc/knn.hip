@@ -117,8 +117,11 @@ __global__ __launch_bounds__(kThreads, 3) void gate_scores_f32_kernel(KnnLayers 
 // exactly as the reference's serial loop (product and sum rounded separately).
 // The queries are laid out once per walk (q4_xa_kernel) as the A operands of every
 // (block pair, group of 8 queries), zeros included, plus their block scales; a
-// workgroup (64 features x 128 queries) stages one block pair of them in LDS per step.
-constexpr int kQ4TileF = 64, kQ4TileG = 16;  // features, groups of 8 queries
+// workgroup (128 features x 128 queries) stages one block pair of them in LDS per step,
+// and each wave applies every A operand it reads to two sets of 16 features (two MFMAs
+// per LDS read).  The loop is bound by VALU issue: the reference's accumulate costs four
+// VALU operations per (feature, query, block) (conversion, two products, sum).
+constexpr int kQ4TileF = 128, kQ4TileG = 16;  // features, groups of 8 queries
 
 // XA[bp][G][lane][16 B], XSP[bp][G][8 m][2 h] = xs of query 8G + m, block 2bp + h.
 // One thread per (bp, G, lane).  Element order within a 16-element half block matches
@@ -152,7 +155,8 @@ __device__ __forceinline__ int nib_s8(uint32_t w4) {
     return static_cast<int>(((w4 | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
 }
 
-// Grid (F / 64, ceil(groups / 16), layers); wave w: features f0 + 16 w + c.
+// Grid (F / 128, ceil(groups / 16), layers); wave w: features f0 + 32 w + c (set 0) and
+// f0 + 32 w + 16 + c (set 1).
 __global__ __launch_bounds__(kThreads, 2) void gate_scores_q4_kernel(KnnLayers g, KnnLayers gd,
                                                                   const uint4* __restrict__ XA,
                                                                   const float* __restrict__ XSP, float* __restrict__ S,
@@ -165,17 +169,23 @@ __global__ __launch_bounds__(kThreads, 2) void gate_scores_q4_kernel(KnnLayers g
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int gl = lane >> 4, c = lane & 15;
     const int G0 = blockIdx.y * kQ4TileG, nG = min(kQ4TileG, ng - G0);
-    const int f = min(blockIdx.x * kQ4TileF + 16 * wave + c, F - 1);
+    const int fb = blockIdx.x * kQ4TileF + 32 * wave + c;  // set 0; set 1 is fb + 16
     const int nbp = K / 64, nb = K / 32;
-    const uint8_t* wrow = nib + static_cast<size_t>(f) * (K / 2) + (gl >> 1) * 16 + (gl & 1) * 8;
-    const uint32_t* drow = reinterpret_cast<const uint32_t*>(dsc + static_cast<size_t>(f) * nb);
+    const uint8_t* wrow[2];
+    const uint32_t* drow[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const int f = min(fb + 16 * e, F - 1);
+        wrow[e] = nib + static_cast<size_t>(f) * (K / 2) + (gl >> 1) * 16 + (gl & 1) * 8;
+        drow[e] = reinterpret_cast<const uint32_t*>(dsc + static_cast<size_t>(f) * nb);
+    }
 
     // staging: thread tid covers A items tid + 256 j of the tile's 16 x 64, and (tid < 64)
     // one float4 of the scales
     uint4 ar[4];
     float4 xr = make_float4(0.f, 0.f, 0.f, 0.f);
-    uint2 wr;
-    uint32_t dr;
+    uint2 wr[2];
+    uint32_t dr[2];
     auto gload = [&](int bp) __attribute__((always_inline)) {
         const uint4* src = XA + (static_cast<size_t>(bp) * ng + G0) * 64;
 #pragma unroll
@@ -185,8 +195,11 @@ __global__ __launch_bounds__(kThreads, 2) void gate_scores_q4_kernel(KnnLayers g
         }
         if (tid < 64 && (tid >> 2) < nG)
             xr = reinterpret_cast<const float4*>(XSP + (static_cast<size_t>(bp) * ng + G0) * 16)[tid];
-        wr = *reinterpret_cast<const uint2*>(wrow + static_cast<size_t>(bp) * 32);
-        dr = drow[bp];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            wr[e] = *reinterpret_cast<const uint2*>(wrow[e] + static_cast<size_t>(bp) * 32);
+            dr[e] = drow[e][bp];
+        }
     };
     auto lstore = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
@@ -197,49 +210,62 @@ __global__ __launch_bounds__(kThreads, 2) void gate_scores_q4_kernel(KnnLayers g
         if (tid < 64) Xs[s][tid >> 2][tid & 3] = xr;
     };
 
-    float acc[kQ4TileG][2];
+    float acc[2][kQ4TileG][2];
 #pragma unroll
-    for (int G = 0; G < kQ4TileG; G++) acc[G][0] = acc[G][1] = 0.f;
+    for (int e = 0; e < 2; e++)
+#pragma unroll
+        for (int G = 0; G < kQ4TileG; G++) acc[e][G][0] = acc[e][G][1] = 0.f;
 
     gload(0);
     lstore(0);
     __syncthreads();
     for (int bp = 0; bp < nbp; bp++) {
         const int s = bp & 1;
-        const uint2 w = wr;
-        const uint32_t dw = dr;
-        if (bp + 1 < nbp) gload(bp + 1);
-        const v4i_t B = {nib_s8(w.x & 0x0F0F0F0Fu), nib_s8((w.x >> 4) & 0x0F0F0F0Fu), nib_s8(w.y & 0x0F0F0F0Fu),
+        v4i_t B[2];
+        float d0[2], d1[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const uint2 w = wr[e];
+            B[e] = v4i_t{nib_s8(w.x & 0x0F0F0F0Fu), nib_s8((w.x >> 4) & 0x0F0F0F0Fu), nib_s8(w.y & 0x0F0F0F0Fu),
                          nib_s8((w.y >> 4) & 0x0F0F0F0Fu)};
-        const float d0 = h2f(dw), d1 = h2f(dw >> 16);
+            d0[e] = h2f(dr[e]);
+            d1[e] = h2f(dr[e] >> 16);
+        }
+        if (bp + 1 < nbp) gload(bp + 1);
 #pragma unroll
         for (int G = 0; G < kQ4TileG; G++) {
             if (G < nG) {
                 const uint4 av = As[s][G][lane];
                 const v4i_t A = {static_cast<int>(av.x), static_cast<int>(av.y), static_cast<int>(av.z),
                                  static_cast<int>(av.w)};
-                const v4i_t D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, v4i_t{0, 0, 0, 0}, 0, 0, 0);
                 const float4 xs = Xs[s][G][gl];  // xs of queries 2g, 2g + 1, blocks 2bp, 2bp + 1
-                // reference order: cs = f16(s) * q8s; acc += (float)isum * cs
-                acc[G][0] = acc[G][0] + static_cast<float>(D[0]) * (d0 * xs.x);
-                acc[G][0] = acc[G][0] + static_cast<float>(D[1]) * (d1 * xs.y);
-                acc[G][1] = acc[G][1] + static_cast<float>(D[2]) * (d0 * xs.z);
-                acc[G][1] = acc[G][1] + static_cast<float>(D[3]) * (d1 * xs.w);
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const v4i_t D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[e], v4i_t{0, 0, 0, 0}, 0, 0, 0);
+                    // reference order: cs = f16(s) * q8s; acc += (float)isum * cs
+                    acc[e][G][0] = acc[e][G][0] + static_cast<float>(D[0]) * (d0[e] * xs.x);
+                    acc[e][G][0] = acc[e][G][0] + static_cast<float>(D[1]) * (d1[e] * xs.y);
+                    acc[e][G][1] = acc[e][G][1] + static_cast<float>(D[2]) * (d0[e] * xs.z);
+                    acc[e][G][1] = acc[e][G][1] + static_cast<float>(D[3]) * (d1[e] * xs.w);
+                }
             }
         }
         // buffer s ^ 1 was last read in step bp - 1, before that step's barrier
         if (bp + 1 < nbp) lstore(s ^ 1);
         __syncthreads();
     }
-    const int fo = blockIdx.x * kQ4TileF + 16 * wave + c;
-    if (fo >= F) return;
     float* Sl = S + static_cast<size_t>(l) * Q * F;
 #pragma unroll
-    for (int G = 0; G < kQ4TileG; G++) {
+    for (int e = 0; e < 2; e++) {
+        const int fo = fb + 16 * e;
+        if (fo >= F) continue;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int q = 8 * (G0 + G) + 2 * gl + j;
-            if (G < nG && q < Q) Sl[static_cast<size_t>(q) * F + fo] = acc[G][j];
+        for (int G = 0; G < kQ4TileG; G++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int q = 8 * (G0 + G) + 2 * gl + j;
+                if (G < nG && q < Q) Sl[static_cast<size_t>(q) * F + fo] = acc[e][G][j];
+            }
         }
     }
 }

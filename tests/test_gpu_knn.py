@@ -178,10 +178,25 @@ def test_topk_invalid_k_returns_none():
         be.close()
 
 
+def _pool_map(fn, items):
+    """The oracle's ctypes calls run without the GIL: map them over the host's threads."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
+    n = max(1, min(16, len(os.sched_getaffinity(0))))
+    with ThreadPoolExecutor(n) as pool:
+        return list(pool.map(fn, items))
+
+
 def test_gate_knn_34_layers_full_size(hip):
     """The vindex walk shape: 34 layers x gate [10240 x 2560], 256 queries, top-32, in
-    f32 and Q4_0, one launch each.  Four (layer, query) lists of each are checked against
-    the oracle bit for bit; every list is checked for the selection invariants."""
+    f32 and Q4_0, one launch each.  Every list of layers 0 and 33 (2 x 256 of each format)
+    is checked against the oracle bit for bit; every list of all 34 layers is checked
+    for the selection invariants.  For Q4_0 the same lists are also ranked by the
+    reference's x86 order (per-element accumulation, LC/csrc/q4_dot.c:183-195): lists
+    whose index sets differ must differ only across a near-tie at the k-th score (a gap
+    below twice the largest score difference between the two orders in that row), and
+    the counts are printed."""
     torch = pytest.importorskip("torch")
     L, F, K, Q, k = 34, 10240, 2560, 256, 32
     dev = torch.device("cuda:0")
@@ -203,6 +218,7 @@ def test_gate_knn_34_layers_full_size(hip):
     gen.manual_seed(4)
     queries = torch.randn(Q, K, generator=gen, device=dev, dtype=torch.float32)
     qn = queries.cpu().numpy()
+    q8 = [oracle.quantize_to_q8(qn[qi]) for qi in range(Q)]
     try:
         for fmt, handles in (("f32", handles_f32), ("q4_0", handles_q4)):
             di = torch.empty(L * Q * k, device=dev, dtype=torch.int32)
@@ -217,15 +233,43 @@ def test_gate_knn_34_layers_full_size(hip):
             assert all(len(set(r)) == k for r in gi.reshape(-1, k))
             assert gi.max() < F
             for l, g in gates:
-                for qi in (0, 255):
+                print(f"[knn 34] {fmt}: layer {l}, all {Q} queries against the oracle", flush=True)
+
+                def scores(qi, l=l, g=g):
                     if fmt == "f32":
-                        s = oracle.gate_scores_f32(g, qn[qi], F, K)
-                    else:
-                        q8, q8s = oracle.quantize_to_q8(qn[qi])
-                        s = oracle.q4_0_matvec_blockint(q4_host[l], q8, q8s, F, K)
-                    ri, rv = oracle.topk_abs(s, k)
-                    np.testing.assert_array_equal(gi[l, qi], ri, err_msg=f"{fmt} layer {l} query {qi}")
-                    np.testing.assert_array_equal(gv[l, qi].view(np.uint32), rv.view(np.uint32))
+                        return oracle.gate_scores_f32(g, qn[qi], F, K)
+                    return oracle.q4_0_matvec_blockint(q4_host[l], q8[qi][0], q8[qi][1], F, K)
+
+                def check(qi):
+                    ri, rv = oracle.topk_abs(scores(qi), k)
+                    return (np.array_equal(gi[l, qi], ri) and np.array_equal(gv[l, qi].view(np.uint32), rv.view(np.uint32)))
+
+                ok = _pool_map(check, range(Q))
+                bad = [qi for qi in range(Q) if not ok[qi]]
+                assert not bad, f"{fmt} layer {l}: queries {bad[:8]} differ from the oracle"
+                if fmt != "q4_0":
+                    continue
+
+                def x86_cmp(qi, l=l):
+                    sb = scores(qi)
+                    sx = oracle.q4_0_matvec_x86(q4_host[l], q8[qi][0], q8[qi][1], F, K)
+                    delta = float(np.max(np.abs(sx.astype(np.float64) - sb)))
+                    xi, _ = oracle.topk_abs(sx, k)
+                    srt = np.sort(np.abs(sx.astype(np.float64)))[::-1]
+                    gap = srt[k - 1] - srt[k]
+                    same = set(xi.tolist()) == set(gi[l, qi].tolist())
+                    explained = same
+                    if not same:
+                        diff = set(xi.tolist()) ^ set(gi[l, qi].tolist())
+                        explained = all(abs(abs(float(sx[f])) - srt[k - 1]) <= 2 * delta for f in diff)
+                    return same, explained, gap <= 2 * delta
+
+                res = _pool_map(x86_cmp, range(Q))
+                n_same = sum(r[0] for r in res)
+                n_near = sum(r[2] for r in res)
+                print(f"[knn 34] q4_0 layer {l}: x86-order top-{k} index sets identical in {n_same}/{Q} lists; "
+                      f"near-ties at the k-th score in {n_near}/{Q}", flush=True)
+                assert all(r[1] for r in res), f"layer {l}: an x86-order difference not explained by a near-tie"
     finally:
         for h in handles_f32 + handles_q4:
             hip.release_weight(h)
