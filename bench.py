@@ -339,8 +339,19 @@ def run_decode(be, torch, stream, steps, warmup):
     prefill = run_prompt_prefill(torch, stream, sm)
     be.kv_truncate(0)
     sm.model.close()
+    del sm
+    torch.cuda.empty_cache()
+    # the Q4_K_M mix (V and down projections in Q6_K): the same prompt through the Q6_K GEMM
+    sm = build_llama(be, torch, q6k=("wv", "down"), **LLAMA3_8B)
+    prefill_km = run_prompt_prefill(torch, stream, sm)
+    prefill_km["config"] = "Q4_K_M mix: wv and down in Q6_K, the rest Q4_K"
+    be.kv_truncate(0)
+    sm.model.close()
+    del sm
+    torch.cuda.empty_cache()
     return {
         "prefill": prefill,
+        "prefill_q4_k_m": prefill_km,
         "tokens_per_s": round(1000.0 / med, 2),
         "ms_per_step_median": round(med, 4),
         "ms_per_step_min": round(min(times), 4),

@@ -460,7 +460,15 @@ extern "C" int larql_hip_matvec_dev(larql_hip_ctx* c, uint64_t handle, const voi
                     larql::launch_q4k_matvec(w, static_cast<const float*>(x) + i * w.cols, out + i * w.rows, 1,
                                              nullptr, s);
                 break;
-            case LARQL_Q6_K: larql::launch_q6k_matvec(w, static_cast<const float*>(x), out, m, s); break;
+            case LARQL_Q6_K:
+                if (m > 1) {  // the prompt pass's f32-operand GEMM; K-split partials in the workspace
+                    const size_t pf = larql::q4k_gemm_f32_part_floats(w, m);
+                    float* part = pf ? static_cast<float*>(larql::ensure(c, c->gemm_x16, pf * sizeof(float))) : nullptr;
+                    larql::launch_q4k_gemm_f32(w, static_cast<const float*>(x), out, m, part, pf, s, 0);
+                } else {
+                    larql::launch_q6k_matvec(w, static_cast<const float*>(x), out, m, s);
+                }
+                break;
             case LARQL_Q4_0:
                 if (!x_scales) fail(LARQL_HIP_ERR_INVALID, "Q4_0 matvec needs Q8 activation scales");
                 larql::launch_q4_0_matvec(w, static_cast<const int8_t*>(x), x_scales, out, m, s);

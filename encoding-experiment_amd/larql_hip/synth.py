@@ -42,7 +42,9 @@ def _quantized(be: HipBackend, torch, gen, rows, cols, fmt, std):
 
 def build_llama(be: HipBackend, torch, *, n_layers=32, hidden=4096, inter=14336, nq=32, nkv=8, hd=128,
                 vocab=128256, rope=500000.0, kv_len=2048, token=1, std=0.02, seed=0, keep_host=False,
-                log=None) -> SynthModel:
+                log=None, q6k=()) -> SynthModel:
+    """q6k: projection names quantized to Q6_K instead of Q4_K (("wv", "down") is the
+    Q4_K_M mix of llama.cpp files: attention V and FFN down in Q6_K)."""
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     qd, kvd = nq * hd, nkv * hd
@@ -56,10 +58,10 @@ def build_llama(be: HipBackend, torch, *, n_layers=32, hidden=4096, inter=14336,
         raws = {}
         for i, (name, rows, cols) in enumerate(shapes):
             gen.manual_seed(seed * 1_000_003 + l * 16 + i)
-            raws[name] = _quantized(be, torch, gen, rows, cols, Q4_K, std)
+            raws[name] = _quantized(be, torch, gen, rows, cols, Q6_K if name in q6k else Q4_K, std)
         structs.append(make_layer(raws["wq"], raws["wk"], raws["wv"], raws["wo"], raws["gate"], raws["up"],
                                   raws["down"], ones, ones, head_dim=hd, num_q_heads=nq, num_kv_heads=nkv,
-                                  rope_base=rope))
+                                  rope_base=rope, formats={n: Q6_K for n in q6k}))
         raws_all.append(raws)
         if keep_host:
             host["layers"].append({k: v.cpu().numpy() for k, v in raws.items()})
