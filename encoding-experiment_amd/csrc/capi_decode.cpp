@@ -433,8 +433,16 @@ void int_proj(const DevWeight& w, larql_hip_model* m, float* out, hipStream_t s)
     else larql::launch_q4_0_matvec(w, m->q8, m->q8s, out, 1, s);
 }
 
+// Prompt-attention options of prefill_q4 / full_pipeline_q4 (use_qk_norm, softcap); a
+// decode step takes neither (zero).
+struct PromptAttn {
+    int qk_norm = 0;
+    float softcap = 0.f;
+};
+
 // The layer launches of one decode step at T = pos + 1, h0 -> h0.
-void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hipStream_t s) {
+void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hipStream_t s,
+                    const PromptAttn& pa = {}) {
     auto& kv = c->kv;
     // prenormed: m->xw / m->psum hold this layer's normed Q/K/V input (from the previous
     // layer's down projection), npsum partial sums
@@ -489,6 +497,8 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hi
         at.t_begin = (L.window > 0 && T > L.window) ? T - L.window : 0;
         at.scale = L.attn_scale;
         at.rope = rope_table(c, L.rope_base, L.rdim, s);
+        at.qk_norm = pa.qk_norm;
+        at.softcap = pa.softcap;
         larql::launch_attention(at, s);
 
         // h1 = h + o (Llama), or h + norm(o, post_attn_norm) for post-norm layers
@@ -629,7 +639,7 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hi
 }
 
 void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float* hidden_out, float* logits,
-                hipStream_t s) {
+                hipStream_t s, const PromptAttn& pa = {}) {
     auto& kv = c->kv;
     kv_ensure(c, m->layers.size(), m->nkv, m->hd, kv.current_len + 1);
     const int T = static_cast<int>(kv.current_len) + 1;
@@ -637,7 +647,7 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
     float* part = static_cast<float*>(
         larql::ensure(c, m->part, static_cast<size_t>(m->nq) * S * (m->hd + 2) * sizeof(float)));
     larql::launch_copy_f32(x_dev, m->h0, m->hidden, s);
-    enqueue_layers(c, m, T, part, s);
+    enqueue_layers(c, m, T, part, s, pa);
     kv.current_len = static_cast<size_t>(T);
     if (hidden_out) larql::launch_copy_f32(m->h0, hidden_out, m->hidden, s);
     if (logits) {
@@ -743,7 +753,8 @@ static void prompt_proj(const larql::DevWeight& w, const float* X, size_t ldx, f
     larql::launch_q4k_gemm_f32(w, X, Y, M, spl, split_n, s, ldy);
 }
 
-static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M, float* dout, hipStream_t s) {
+static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M, float* dout, hipStream_t s,
+                       const PromptAttn& pa = {}) {
     auto& kv = c->kv;
     kv_ensure(c, m->layers.size(), m->nkv, m->hd, M);
     const size_t hidden = m->hidden, inter = m->inter, qd = m->q_dim, kvd = m->kv_dim, ld = qd + 2 * kvd;
@@ -793,6 +804,8 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
         at.batch = static_cast<int>(M);
         at.window = L.window;
         at.qkv_ld = static_cast<int>(ld);
+        at.qk_norm = pa.qk_norm;
+        at.softcap = pa.softcap;
         larql::launch_attention(at, s);
         prompt_proj(L.wo, ATT, qd, G, hidden, M, SPL, split_n, s);
         if (L.post_norms) {
@@ -821,7 +834,6 @@ extern "C" int larql_hip_prefill_q4(larql_hip_ctx* c, const larql_pipeline_layer
                                     float rope_base, int use_qk_norm, float softcap, float* out) {
     return guarded(c, [&] {
         if (!layers || !x || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
-        if (use_qk_norm || softcap != 0.f) fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill: QK-norm / softcap not supported");
         if (num_q_heads * head_dim != q_dim || num_kv_heads * head_dim != kv_dim)
             fail(LARQL_HIP_ERR_INVALID, "prefill: q_dim/kv_dim do not match the head geometry");
         (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
@@ -833,11 +845,12 @@ extern "C" int larql_hip_prefill_q4(larql_hip_ctx* c, const larql_pipeline_layer
         c->kv.current_len = 0;  // a new prompt at positions 0 .. seq_len - 1
         const float* dx = stage_upload(c, c->stage_in, x, seq_len * hidden);
         float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, seq_len * hidden * sizeof(float)));
+        const PromptAttn pa{use_qk_norm != 0, softcap};
         if (seq_len > 1 && prompt_batchable(m))
-            run_prompt(c, m, dx, seq_len, dout, c->stream);
+            run_prompt(c, m, dx, seq_len, dout, c->stream, pa);
         else
             for (size_t p = 0; p < seq_len; p++)
-                run_decode(c, m, dx + p * hidden, dout + p * hidden, nullptr, c->stream);
+                run_decode(c, m, dx + p * hidden, dout + p * hidden, nullptr, c->stream, pa);
         download(c, out, dout, seq_len * hidden * sizeof(float));
     });
 }
@@ -848,8 +861,6 @@ extern "C" int larql_hip_full_pipeline_q4(larql_hip_ctx* c, const larql_pipeline
                                           float rope_base, int use_qk_norm, float softcap, float* out) {
     return guarded(c, [&] {
         if (!layers || !x || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
-        if (use_qk_norm || softcap != 0.f)
-            fail(LARQL_HIP_ERR_UNSUPPORTED, "full pipeline: QK-norm / softcap not supported");
         if (num_q_heads * head_dim != q_dim || num_kv_heads * head_dim != kv_dim)
             fail(LARQL_HIP_ERR_INVALID, "full pipeline: q_dim/kv_dim do not match the head geometry");
         (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
@@ -868,11 +879,12 @@ extern "C" int larql_hip_full_pipeline_q4(larql_hip_ctx* c, const larql_pipeline
         c->kv.current_len = 0;
         const float* dx = stage_upload(c, c->stage_in, x, seq_len * hidden);
         float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, seq_len * hidden * sizeof(float)));
+        const PromptAttn pa{use_qk_norm != 0, softcap};
         if (seq_len > 1 && prompt_batchable(m))
-            run_prompt(c, m, dx, seq_len, dout, c->stream);
+            run_prompt(c, m, dx, seq_len, dout, c->stream, pa);
         else
             for (size_t p = 0; p < seq_len; p++)
-                run_decode(c, m, dx + p * hidden, dout + p * hidden, nullptr, c->stream);
+                run_decode(c, m, dx + p * hidden, dout + p * hidden, nullptr, c->stream, pa);
         download(c, out, dout, seq_len * hidden * sizeof(float));
     });
 }

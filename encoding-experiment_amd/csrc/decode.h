@@ -20,6 +20,12 @@ struct AttnArgs {
     // (the query's own included) already in the cache, out rows num_q * hd apart and
     // partials [batch][num_q][S][hd + 2] with S the largest query's split count.
     int batch = 0, window = 0, qkv_ld = 0;
+    // Prompt-attention options of the reference's fused kernel (LC/src/metal/shaders/
+    // fused_attention.rs:79-88, 132-137): qk_norm scales each RoPE'd query head by
+    // 1 / sqrt(sum q^2 + 1e-6) (the cached K is not normed); softcap > 0 maps each scaled
+    // score s to tanh(s / softcap) * softcap before the softmax.
+    int qk_norm = 0;
+    float softcap = 0.f;
 };
 
 void launch_attention(const AttnArgs& a, hipStream_t s);

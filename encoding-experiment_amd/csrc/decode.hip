@@ -242,6 +242,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
             a.vc[((static_cast<size_t>(pos >> 3) * a.num_kv + kvh) * HD + d) * 8 + (pos & 7)] = __ushort_as_half(vnew[d]);
         }
     __syncthreads();
+    if (a.qk_norm) {  // unit-length query heads: one wave per head
+        for (int h = wave; h < reps; h += kAttnThreads / 64) {
+            float ss = 0.f;
+            for (int d = lane; d < HD; d += 64) ss += q_s[h * HD + d] * q_s[h * HD + d];
+            const float r = 1.0f / sqrtf(wave_sum_dpp(ss) + 1e-6f);
+            for (int d = lane; d < HD; d += 64) q_s[h * HD + d] *= r;
+        }
+        __syncthreads();
+    }
     // score B operands: lane (g, col) of k-step ks holds dims 32 ks + 8 g .. of column col
     for (int i = tid; i < KS * 64; i += kAttnThreads) {
         const int ks = i >> 6, l = i & 63, lg = l >> 4, col = l & 15;
@@ -294,7 +303,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int tl = 16 * wave + 4 * g + r, t = t0 + tl;
-            p_s[c][tl] = (t >= a.t_begin && t <= pos) ? sacc[r] * a.scale : -INFINITY;
+            float sv = sacc[r] * a.scale;
+            if (a.softcap > 0.f) sv = tanhf(sv / a.softcap) * a.softcap;
+            p_s[c][tl] = (t >= a.t_begin && t <= pos) ? sv : -INFINITY;
         }
     }
     __syncthreads();

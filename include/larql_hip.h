@@ -345,9 +345,12 @@ int larql_hip_decode_token(larql_hip_ctx* ctx, const larql_pipeline_layer* layer
  * (x: host [seq_len][hidden]) through all layers at positions 0 .. seq_len-1, the
  * post-RoPE K/V of every position stored in the cache (whose length becomes seq_len);
  * out: host [seq_len][hidden], the final hidden state of every position (before the
- * final norm).  Positions run in order through the decode-step kernels, as the
- * reference's Metal prefill runs its projections per position (LC/src/metal/prefill.rs).
- * use_qk_norm != 0 or softcap != 0 (Gemma-style layers) return UNSUPPORTED. */
+ * final norm).  Layers with gate|up in Q4_K and Q4_K / Q6_K elsewhere run once over all
+ * positions; others run position by position through the decode-step kernels.
+ * use_qk_norm != 0 scales each RoPE'd query head by 1 / sqrt(sum q^2 + 1e-6) and
+ * softcap > 0 maps each scaled score s to tanh(s / softcap) * softcap (the reference's
+ * fused attention, LC/src/metal/shaders/fused_attention.rs:79-88, 132-137); the cached K
+ * rows are not normed, and a later decode_token applies neither. */
 int larql_hip_prefill_q4(larql_hip_ctx* ctx, const larql_pipeline_layer* layers, size_t num_layers,
                          const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim, size_t seq_len,
                          size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float rope_base,
@@ -359,7 +362,7 @@ int larql_hip_prefill_q4(larql_hip_ctx* ctx, const larql_pipeline_layer* layers,
  * cache is left as it was); out [seq_len][hidden] (host), the last layer's hidden state of
  * every position.  The trait returns the first `hidden` floats of it (the reference calls it
  * with seq_len = 1, LI/src/layer_graph/predict.rs:406).  Layers as for decode_token, Q8_0
- * attention and Q4_0 FFN weights included; use_qk_norm != 0 or softcap != 0 return UNSUPPORTED. */
+ * attention and Q4_0 FFN weights included; use_qk_norm and softcap as for prefill_q4. */
 int larql_hip_full_pipeline_q4(larql_hip_ctx* ctx, const larql_pipeline_layer* layers, size_t num_layers,
                                const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim,
                                size_t seq_len, size_t num_q_heads, size_t num_kv_heads, size_t head_dim,

@@ -70,6 +70,9 @@ def _load():
             "lo_gelu_tanh_gate_up": (None, [_P, _P, _P, _SZ]),
             "lo_rms_norm_heads": (None, [_P, _SZ, _SZ, ctypes.c_double]),
             "lo_attend_f16": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P]),
+            "lo_attend_f16_opts": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, ctypes.c_int,
+                                          ctypes.c_float, _P]),
+            "lo_qk_norm_heads": (None, [_P, _SZ, _SZ]),
             "lo_decode_layer": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, ctypes.c_double]),
             "lo_decode_layer_mt": (None, [_P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _SZ, ctypes.c_double, ctypes.c_double,
                                            ctypes.c_int]),
@@ -355,16 +358,28 @@ def rms_norm_heads(x, num_heads: int, head_dim: int, eps: float = 1e-6):
     return x
 
 
-def attend_f16(q, kc, vc, T: int, num_q: int, num_kv: int, head_dim: int, scale: float, t_start: int = 0):
+def attend_f16(q, kc, vc, T: int, num_q: int, num_kv: int, head_dim: int, scale: float, t_start: int = 0,
+               qk_norm: bool = False, softcap: float = 0.0):
     """Attention of the last query row over cache positions t_start .. T-1 (t_start > 0 is
-    the sliding window, LC/src/metal/shaders/kv_attention.rs:35)."""
+    the sliding window, LC/src/metal/shaders/kv_attention.rs:35); qk_norm / softcap as the
+    prompt attention's options (LC/src/metal/shaders/fused_attention.rs:79-88, 132-137)."""
     kvd = num_kv * head_dim
     q = _c(q, np.float32)
     kc = _c(np.asarray(kc)[t_start * kvd:T * kvd], np.uint16)
     vc = _c(np.asarray(vc)[t_start * kvd:T * kvd], np.uint16)
     out = np.empty(num_q * head_dim, dtype=np.float32)
-    _load().lo_attend_f16(_ptr(q), _ptr(kc), _ptr(vc), T - t_start, num_q, num_kv, head_dim, scale, _ptr(out))
+    if qk_norm or softcap != 0.0:
+        _load().lo_attend_f16_opts(_ptr(q), _ptr(kc), _ptr(vc), T - t_start, num_q, num_kv, head_dim, scale,
+                                   int(bool(qk_norm)), softcap, _ptr(out))
+    else:
+        _load().lo_attend_f16(_ptr(q), _ptr(kc), _ptr(vc), T - t_start, num_q, num_kv, head_dim, scale, _ptr(out))
     return out
+
+
+def qk_norm_heads(x, num_heads: int, head_dim: int):
+    x = np.array(x, dtype=np.float32, copy=True)
+    _load().lo_qk_norm_heads(_ptr(x), num_heads, head_dim)
+    return x
 
 
 _PROJ = ("wq", "wk", "wv", "wo", "gate", "up", "down")
@@ -377,7 +392,8 @@ class _Layer(ctypes.Structure):
                 ("norm_offset", ctypes.c_float), ("has_post_norms", ctypes.c_int),
                 ("activation", ctypes.c_int), ("has_v_norm", ctypes.c_int),
                 ("layer_scalar", ctypes.c_float), ("rotary_dim", ctypes.c_size_t),
-                ("attn_scale", ctypes.c_float)] + [(n + "_s", ctypes.c_void_p) for n in _PROJ]
+                ("attn_scale", ctypes.c_float)] + [(n + "_s", ctypes.c_void_p) for n in _PROJ] + \
+               [("qk_norm", ctypes.c_int), ("softcap", ctypes.c_float)]
 
 
 def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, num_kv: int,
@@ -390,7 +406,9 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
     the default is Q4_K.
     Optional layer variants (FullPipelineLayer, LC/src/pipeline.rs:76-115):
     pre_ffn_norm / post_ffn_norm (arrays or None), norm_offset, has_post_norms,
-    activation ("silu" | "gelu_tanh"), has_v_norm, layer_scalar, rotary_dim, attn_scale."""
+    activation ("silu" | "gelu_tanh"), has_v_norm, layer_scalar, rotary_dim, attn_scale; and the
+    prompt-attention options qk_norm (bool) and softcap (float, 0 = off) of prefill_q4 /
+    full_pipeline_q4."""
     keep = {}
     st = _Layer()
     for name, dt in (("wq", np.uint8), ("wk", np.uint8), ("wv", np.uint8), ("wo", np.uint8),
@@ -423,6 +441,8 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
     st.layer_scalar = float(layer.get("layer_scalar", 0.0))
     st.rotary_dim = int(layer.get("rotary_dim", 0))
     st.attn_scale = float(layer.get("attn_scale", 0.0))
+    st.qk_norm = int(bool(layer.get("qk_norm", False)))
+    st.softcap = float(layer.get("softcap", 0.0))
     h = np.array(h, dtype=np.float32, copy=True)
     if threads > 1:
         assert window == 0

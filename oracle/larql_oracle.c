@@ -770,7 +770,7 @@ void lo_rms_norm_heads(float* x, size_t num_heads, size_t head_dim, double eps) 
  * (each output element still accumulates its T terms in ascending t, the same additions
  * as a t-inner loop, while V is walked row by row). */
 static void lo_attend_heads(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T, size_t h0, size_t h1,
-                            size_t reps, size_t kvd, size_t head_dim, float scale, float* out) {
+                            size_t reps, size_t kvd, size_t head_dim, float scale, float softcap, float* out) {
     float* sc = (float*)malloc(T * sizeof(float));
     for (size_t h = h0; h < h1; h++) {
         size_t kvh = h / reps;
@@ -780,6 +780,7 @@ static void lo_attend_heads(const float* q, const uint16_t* kc, const uint16_t* 
             float dot = 0.0f;
             for (size_t d = 0; d < head_dim; d++) dot += lo_f16_to_f32(kr[d]) * qh[d];
             sc[t] = dot * scale;
+            if (softcap > 0.0f) sc[t] = tanhf(sc[t] / softcap) * softcap;  /* fused_attention.rs:132-137 */
         }
         float mx = -INFINITY;
         for (size_t t = 0; t < T; t++) mx = fmaxf(mx, sc[t]);
@@ -803,7 +804,28 @@ static void lo_attend_heads(const float* q, const uint16_t* kc, const uint16_t* 
 
 void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T,
                    size_t num_q, size_t num_kv, size_t head_dim, float scale, float* out) {
-    lo_attend_heads(q, kc, vc, T, 0, num_q, num_q / num_kv, num_kv * head_dim, head_dim, scale, out);
+    lo_attend_heads(q, kc, vc, T, 0, num_q, num_q / num_kv, num_kv * head_dim, head_dim, scale, 0.0f, out);
+}
+
+/* LC/src/metal/shaders/fused_attention.rs:79-88: s = sum of squares in element order
+ * (f32), every element times rsqrt(s + 1e-6). */
+void lo_qk_norm_heads(float* x, size_t num_heads, size_t head_dim) {
+    for (size_t h = 0; h < num_heads; h++) {
+        float* v = x + h * head_dim;
+        float s = 0.0f;
+        for (size_t d = 0; d < head_dim; d++) s += v[d] * v[d];
+        const float r = 1.0f / sqrtf(s + 1e-6f);
+        for (size_t d = 0; d < head_dim; d++) v[d] *= r;
+    }
+}
+
+void lo_attend_f16_opts(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T, size_t num_q,
+                        size_t num_kv, size_t head_dim, float scale, int qk_norm, float softcap, float* out) {
+    float* qn = (float*)malloc(num_q * head_dim * sizeof(float));
+    memcpy(qn, q, num_q * head_dim * sizeof(float));
+    if (qk_norm) lo_qk_norm_heads(qn, num_q, head_dim);
+    lo_attend_heads(qn, kc, vc, T, 0, num_q, num_q / num_kv, num_kv * head_dim, head_dim, scale, softcap, out);
+    free(qn);
 }
 
 /* A projection in its layer's format: Q4_K (0), Q6_K (1), Q4_KF 144-byte GGUF (2), Q4_KF
@@ -886,22 +908,22 @@ typedef struct {
     const float* q;
     const uint16_t *kc, *vc;
     size_t T, h0, h1, reps, kvd, head_dim;
-    float scale;
+    float scale, softcap;
     float* out;
 } lo_attend_job;
 
 static void* lo_attend_job_run(void* p) {
     const lo_attend_job* j = (const lo_attend_job*)p;
     if (j->h1 > j->h0) lo_attend_heads(j->q, j->kc, j->vc, j->T, j->h0, j->h1, j->reps, j->kvd, j->head_dim, j->scale,
-                                       j->out);
+                                       j->softcap, j->out);
     return NULL;
 }
 
 /* Attention with the query heads split over nt threads (each head is independent). */
 static void lo_attend_n(int nt, const float* q, const uint16_t* kc, const uint16_t* vc, size_t T, size_t num_q,
-                        size_t num_kv, size_t head_dim, float scale, float* out) {
+                        size_t num_kv, size_t head_dim, float scale, float softcap, float* out) {
     if (nt <= 1) {
-        lo_attend_f16(q, kc, vc, T, num_q, num_kv, head_dim, scale, out);
+        lo_attend_heads(q, kc, vc, T, 0, num_q, num_q / num_kv, num_kv * head_dim, head_dim, scale, softcap, out);
         return;
     }
     if (nt > 256) nt = 256;
@@ -910,7 +932,7 @@ static void lo_attend_n(int nt, const float* q, const uint16_t* kc, const uint16
     lo_attend_job jb[256];
     for (int t = 0; t < nt; t++) {
         jb[t] = (lo_attend_job){q, kc, vc, T, num_q * (size_t)t / (size_t)nt, num_q * (size_t)(t + 1) / (size_t)nt,
-                                num_q / num_kv, num_kv * head_dim, head_dim, scale, out};
+                                num_q / num_kv, num_kv * head_dim, head_dim, scale, softcap, out};
         started[t] = pthread_create(&th[t], NULL, lo_attend_job_run, &jb[t]) == 0;
         if (!started[t]) lo_attend_job_run(&jb[t]);
     }
@@ -983,13 +1005,15 @@ static void lo_decode_layer_impl(const lo_layer_t* L, float* h, size_t pos, size
     if (L->has_v_norm) lo_rms_norm_heads(v, num_kv, head_dim, eps);
     lo_rope_at(q, num_q, head_dim, rdim, rope_base, pos);
     lo_rope_at(k, num_kv, head_dim, rdim, rope_base, pos);
+    if (L->qk_norm) lo_qk_norm_heads(q, num_q, head_dim);  /* after RoPE, Q only: the cache keeps K */
     for (size_t i = 0; i < kvd; i++) {
         L->k_cache[pos * kvd + i] = lo_f32_to_f16_rne(k[i]);
         L->v_cache[pos * kvd + i] = lo_f32_to_f16_rne(v[i]);
     }
     float scale = L->attn_scale != 0.0f ? L->attn_scale : (float)(1.0 / sqrt((double)head_dim));
     const size_t T = pos + 1, t0 = (window > 0 && T > window) ? T - window : 0;
-    lo_attend_n(nt, q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, T - t0, num_q, num_kv, head_dim, scale, att);
+    lo_attend_n(nt, q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, T - t0, num_q, num_kv, head_dim, scale,
+                L->softcap, att);
     lo_proj_n(nt, L->fmt[3], L->wo, L->wo_s, 1, att, o, hidden, qd);
     if (L->has_post_norms) {
         lo_rms_norm(o, L->post_attn_norm, off, eps, xn, hidden);

@@ -111,6 +111,14 @@ void lo_rms_norm_heads(float* x, size_t num_heads, size_t head_dim, double eps);
 /* Single-query GQA over an fp16 cache laid out [t][kv_head][head_dim] (gqa.rs:29-110). */
 void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T,
                    size_t num_q, size_t num_kv, size_t head_dim, float scale, float* out);
+/* The same with the prompt-attention options: qk_norm != 0 L2-normalises each query head
+ * (1 / sqrt(sum q^2 + 1e-6), on a copy of q), softcap > 0 caps every scaled score
+ * (LC/src/metal/shaders/fused_attention.rs:79-88, 132-137). */
+void lo_attend_f16_opts(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T, size_t num_q,
+                        size_t num_kv, size_t head_dim, float scale, int qk_norm, float softcap, float* out);
+/* In place: each of num_heads heads of head_dim floats times 1 / sqrt(sum x^2 + 1e-6)
+ * (fused_attention.rs:79-88: one f32 sum in element order). */
+void lo_qk_norm_heads(float* x, size_t num_heads, size_t head_dim);
 
 /* One decoder layer (Q4_K / Q6_K projections, fp16 KV cache) at position pos.
  * h is updated in place; the new K/V row is written into kc/vc at pos.
@@ -137,6 +145,12 @@ typedef struct {
     size_t rotary_dim;                          /* 0 = head_dim */
     float attn_scale;                           /* 0 = 1/sqrt(head_dim) */
     const float *wq_s, *wk_s, *wv_s, *wo_s, *gate_s, *up_s, *down_s;  /* Q8_0 weight scales */
+    /* prompt-attention options of prefill_q4 / full_pipeline_q4 (LC/src/metal/shaders/
+     * fused_attention.rs:79-88, 132-137): qk_norm != 0 scales each RoPE'd query head by
+     * 1 / sqrt(sum q^2 + 1e-6) (K untouched); softcap > 0 maps each scaled score s to
+     * tanh(s / softcap) * softcap */
+    int qk_norm;
+    float softcap;
 } lo_layer_t;
 
 void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,

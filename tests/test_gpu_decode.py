@@ -368,8 +368,93 @@ def test_prefill_q4_matches_oracle_and_decode(hip, seq, formats, window):
         e = rel_err(after_prefill, stepwise.astype(np.float64))
         print(f"  next token after batched prefill vs stepwise: rel_err={e:.3e}", flush=True)
         assert e <= REL_TOL
-    with pytest.raises(larql_hip.LarqlHipError):  # QK-norm layers: UNSUPPORTED (the trait's None)
-        hip.prefill_q4(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0, use_qk_norm=True)
+
+
+PROMPT_OPTS = [(True, 0.0), (False, 1.5), (True, 1.5)]
+
+
+@pytest.mark.parametrize("entry", ["prefill", "full_pipeline"])
+@pytest.mark.parametrize("formats", [None, {"up": "q6_k"}])
+@pytest.mark.parametrize("qk_norm,softcap", PROMPT_OPTS)
+def test_prompt_attention_options(hip, entry, formats, qk_norm, softcap):
+    """use_qk_norm and softcap of prefill_q4 / full_pipeline_q4 (LC/src/metal/shaders/
+    fused_attention.rs:79-88, 132-137; LC/src/metal/trait_impl.rs:43-76, 150-192): every
+    position against the oracle layers with the same options, on the batched pass (Q4_K
+    layers) and position by position (split gate/up).  After prefill_q4 the next
+    decode_token (no options) continues from the cache, whose K rows are not normed."""
+    n_layers, hidden, inter, nq, nkv, hd, seq = 2, 512, 1024, 8, 2, 64, 10
+    print(f"[prompt options] {entry} formats={formats} qk_norm={qk_norm} softcap={softcap}", flush=True)
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=83, formats=formats,
+                   variant=dict(attn_scale=0.25))
+    for L in m.layers:
+        L.update(qk_norm=qk_norm, softcap=softcap, attn_scale=0.25)
+    layers = m.hip_layers(10000.0)
+    for hl in layers:
+        hl.attn_scale = 0.25
+    x = np.stack([oracle.gauss(870 + p, hidden) for p in range(seq)])
+    hip.reset_kv_cache()
+    call = hip.prefill_q4 if entry == "prefill" else hip.full_pipeline_q4
+    got = call(layers, x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0, use_qk_norm=qk_norm,
+               softcap=softcap)
+    worst = 0.0
+    for p in range(seq):
+        ref = x[p].copy()
+        for L in m.layers:
+            ref = oracle.decode_layer(L, ref, p, hidden, inter, nq, nkv, hd, 10000.0)
+        e = rel_err(got[p], ref)
+        worst = max(worst, e)
+        assert e <= REL_TOL, (p, e)
+    print(f"  worst position rel_err={worst:.3e}", flush=True)
+    if entry == "prefill":
+        assert hip.kv_cache_len() == seq
+        nxt = oracle.gauss(879, hidden)
+        got = hip.decode_token(layers, nxt, hidden, inter, nq * hd, nkv * hd, nq, nkv, hd, 10000.0)
+        ref = nxt.copy()
+        for L in m.layers:
+            ref = oracle.decode_layer(dict(L, qk_norm=False, softcap=0.0), ref, seq, hidden, inter, nq, nkv, hd,
+                                      10000.0)
+        assert rel_err(got, ref) <= REL_TOL
+
+
+def _double_rows_q4k(w, r0, r1, cols):
+    """Q4_K rows r0..r1-1 times exactly 2: the f16 d and dmin of each of their 148-byte
+    super-blocks doubled (every dequantized weight is d * sc * q - dmin * m)."""
+    b = w.reshape(-1, cols // 256, 148).copy()
+    hdr = b[r0:r1, :, 0:4].copy().view(np.float16)
+    b[r0:r1, :, 0:4] = (hdr * np.float16(2)).view(np.uint8)
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("formats", [None, {"up": "q6_k"}])
+def test_qk_norm_is_per_query_head(hip, formats):
+    """A property the oracle does not enter: with QK-norm on, doubling the Q rows of one
+    head leaves every output unchanged (the norm is per query head and comes after the
+    linear RoPE; only the 1e-6 inside the root differs); without it the same change moves
+    the output.  Doubling the K rows of one kv head does move it (K is not normed)."""
+    n_layers, hidden, inter, nq, nkv, hd, seq = 1, 512, 1024, 8, 2, 64, 9
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=seq + 2, seed=87, formats=formats)
+    x = np.stack([oracle.gauss(890 + p, hidden) for p in range(seq)])
+    args = (x, hidden, inter, nq * hd, nkv * hd, seq, nq, nkv, hd, 10000.0)
+
+    def run(qk, wq=None, wk=None):
+        layers = m.hip_layers(10000.0)
+        keep = []
+        for arr, field in ((wq, "wq"), (wk, "wk")):
+            if arr is not None:   # a fresh buffer: the cached model is rebuilt
+                keep.append(arr)
+                getattr(layers[0], field).data = arr.ctypes.data
+        hip.reset_kv_cache()
+        return hip.prefill_q4(layers, *args, use_qk_norm=qk)
+
+    wq2 = _double_rows_q4k(m.layers[0]["wq"], 3 * hd, 4 * hd, hidden)
+    wk2 = _double_rows_q4k(m.layers[0]["wk"], hd, 2 * hd, hidden)
+    base = run(True)
+    e_q = rel_err(run(True, wq=wq2), base.astype(np.float64))
+    e_k = rel_err(run(True, wk=wk2), base.astype(np.float64))
+    e_off = rel_err(run(False, wq=wq2), run(False).astype(np.float64))
+    print(f"[qk-norm invariance] formats={formats}: Q head x2 {e_q:.2e}, K head x2 {e_k:.2e}, "
+          f"Q head x2 without norm {e_off:.2e}", flush=True)
+    assert e_q <= 1e-5 and e_k > 1e-3 and e_off > 1e-3
 
 
 @pytest.mark.parametrize("formats", [None, {"wv": "q6_k", "down": "q6_k"}])

@@ -497,6 +497,45 @@ def test_attention_window_closed_forms():
         assert np.allclose(win[h * hd:(h + 1) * hd], ref, rtol=1e-5, atol=1e-6)
 
 
+def test_attention_qk_norm_softcap_closed_forms():
+    """Prompt-attention options (LC/src/metal/shaders/fused_attention.rs:79-88, 132-137) on two
+    positions, where the softmax is the logistic function of the score difference: q = (3, 4,
+    0, ..) has L2 norm 5; K rows 0 and (5, 0, ..), V rows 0 and e0, scale 0.5, so out[0] =
+    1 / (1 + exp(-s1)) with s1 = 0.5 * 5 * q0 and, with QK-norm, q0 = 3 / sqrt(25 + 1e-6);
+    with softcap c, s1 -> c * tanh(s1 / c).  The RMS norm in place of the L2 norm, the cap
+    applied before the scale, or the cap without its factor c each miss by > 1e-2."""
+    hd = 32
+    q = np.zeros(hd, np.float32)
+    q[:2] = (3.0, 4.0)
+    kc = np.zeros(2 * hd, np.float16)
+    kc[hd] = 5.0
+    vc = np.zeros(2 * hd, np.float16)
+    vc[hd] = 1.0
+    kc, vc = kc.view(np.uint16), vc.view(np.uint16)
+    logistic = lambda s: 1.0 / (1.0 + math.exp(-s))
+    qn0 = 3.0 / math.sqrt(25.0 + 1e-6)
+    cases = {(False, 0.0): 0.5 * 5 * 3.0, (True, 0.0): 0.5 * 5 * qn0,
+             (False, 2.0): 2.0 * math.tanh(0.5 * 5 * 3.0 / 2.0), (True, 2.0): 2.0 * math.tanh(0.5 * 5 * qn0 / 2.0),
+             (True, -1.0): 0.5 * 5 * qn0}                          # a cap <= 0 is off
+    for (qk, cap), s1 in cases.items():
+        out = oracle.attend_f16(q, kc, vc, 2, 1, 1, hd, 0.5, qk_norm=qk, softcap=cap)
+        assert abs(out[0] - logistic(s1)) <= 1e-6, (qk, cap, out[0], logistic(s1))
+        assert not np.any(out[1:])
+    got = oracle.attend_f16(q, kc, vc, 2, 1, 1, hd, 0.5, qk_norm=True, softcap=2.0)[0]
+    rms0 = 3.0 / math.sqrt(25.0 / hd + 1e-6)
+    for wrong in (2.0 * math.tanh(0.5 * 5 * rms0 / 2.0),           # RMS, not L2
+                  0.5 * 2.0 * math.tanh(5 * qn0 / 2.0),            # cap before the scale
+                  math.tanh(0.5 * 5 * qn0 / 2.0)):                 # cap without its factor
+        assert abs(got - logistic(wrong)) > 1e-2
+    # the QK-norm helper: unit heads, each head on its own
+    x = np.random.default_rng(5).standard_normal(3 * hd).astype(np.float32)
+    x[hd:2 * hd] *= 100.0
+    y = oracle.qk_norm_heads(x, 3, hd).reshape(3, hd)
+    assert np.allclose(np.linalg.norm(y.astype(np.float64), axis=1), 1.0, atol=1e-6)
+    assert np.allclose(y * np.linalg.norm(x.reshape(3, hd).astype(np.float64), axis=1, keepdims=True),
+                       x.reshape(3, hd), rtol=1e-5, atol=1e-6)
+
+
 def test_silu_closed_form():
     g = np.array([0.0, 1.0, -2.0, 10.0], np.float32)
     u = np.array([3.0, 2.0, 1.0, 0.5], np.float32)
@@ -723,6 +762,13 @@ def _ref_layer64(P, h, kc, vc, pos, dims, mut=()):
         return t.reshape(-1)
 
     q, k = rope(q, nq), rope(k, nkv)
+    if P.get("qk_norm"):           # per query head, after RoPE; RMS under the planted "qk_rms"
+        qh = q.reshape(nq, hd)
+        ss = (qh * qh).sum(1, keepdims=True) / (hd if "qk_rms" in mut else 1)
+        q = (qh / np.sqrt(ss + 1e-6)).reshape(-1)
+        if "qk_norm_k" in mut:
+            kh = k.reshape(nkv, hd)
+            k = (kh / np.sqrt((kh * kh).sum(1, keepdims=True) + 1e-6)).reshape(-1)
     if "rope_v" in mut:
         v = rope(v, nkv)
     kvd = nkv * hd
@@ -735,6 +781,9 @@ def _ref_layer64(P, h, kc, vc, pos, dims, mut=()):
     for qh in range(nq):
         kvh = qh % nkv if "kv_map" in mut else qh // (nq // nkv)
         sc = K[:, kvh * hd:(kvh + 1) * hd] @ q[qh * hd:(qh + 1) * hd] * scale
+        cap = P.get("softcap", 0.0)
+        if cap > 0:
+            sc = (np.tanh(sc / scale / cap) * cap * scale) if "cap_pre_scale" in mut else np.tanh(sc / cap) * cap
         p = np.exp(sc - sc.max())
         att[qh * hd:(qh + 1) * hd] = (p / p.sum()) @ V[:, kvh * hd:(kvh + 1) * hd]
     o = proj("wo", att)
@@ -835,6 +884,23 @@ def test_decode_layer_variants_match_float64_composition():
     P2 = dict(P, pre_ffn_norm=None, post_ffn_norm=None)
     got2, ref2 = _run_layer_case(P2, dims, pos=3, seed=34)
     assert _rel(got2, ref2()) <= 1e-5 and _rel(got2, got) > 1e-2
+
+
+def test_decode_layer_qk_norm_softcap_match_float64_composition():
+    """The prompt-attention options in the oracle layer (QK-norm of the RoPE'd query heads,
+    the score cap) against the float64 restatement within 1e-5; planted mistakes (K normed
+    too, the RMS norm for the L2 norm, the cap before the scale) each move it by > 1e-2, and
+    each option alone is far from the layer without it."""
+    dims = (256, 512, 4, 2, 64)
+    P = _tiny_layer(35, dims, {}, std=0.3, qk_norm=True, softcap=1.0, attn_scale=0.5)
+    got, ref = _run_layer_case(P, dims, pos=6, seed=36)
+    assert _rel(got, ref()) <= 1e-5
+    for mut in ("qk_norm_k", "qk_rms", "cap_pre_scale"):
+        assert _rel(got, ref((mut,))) > 1e-2, mut
+    for k, v in (("qk_norm", False), ("softcap", 0.0)):
+        Q = dict(P, **{k: v})
+        got_q, ref_q = _run_layer_case(Q, dims, pos=6, seed=36)
+        assert _rel(got_q, ref_q()) <= 1e-5 and _rel(got_q, got) > 1e-2, k
 
 
 def _inputs_of(P, dims, pos, seed):
