@@ -7,12 +7,12 @@
 // GEMM on the matrix cores, v_mfma_f32_16x16x32_f16 with f32 accumulation:
 //   * x16_pack_kernel converts X to fp16 once, laid out as ready-made A operands:
 //     one 1 KB block (64 lanes x 8 halves) per (16 tokens, super-block, half, step);
-//   * the GEMM streams the tile-major Q4_K weights (one coalesced 1 KB load per 16 rows
-//     and half super-block) and dequantizes them in registers into B operands,
-//     w = (1024 + q) * (d sc_j) - (1024 d sc_j + dmin m_j) in one f32 fma per element,
+//   * the GEMM (q4k_gemm_shared_kernel) streams the tile-major Q4_K weights and
+//     dequantizes each 16-row tile and k-step once per 256 tokens into fp16 B operands in
+//     LDS, w = (1024 + q) * (d sc_j) - (1024 d sc_j + dmin m_j) in one f32 fma per element,
 //     rounded to fp16 (the same value as d sc_j q - dmin m_j, to ~2^-14 d sc_j);
-//   * the A blocks of a workgroup's 64 tokens go through LDS, double-buffered, and are
-//     shared by its four waves; each wave owns 80 weight rows.
+//   * each of its eight waves multiplies its own 32 tokens, A operands straight from the
+//     packed X into registers, by the shared B operands of 80 weight rows.
 // The MFMA k order within a step is free as long as A and B agree: lane (g, c) of step s
 // in half h supplies elements 8s + {0,4,1,5,2,6,3,7} of sub-block 4h + g (the order in
 // which the nibble bytes unpack), and x16_pack_kernel writes X in that order.
@@ -29,12 +29,13 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
+// Tiling of the f32-operand GEMMs (q4k_gemm_f32_kernel, q6k_gemm_f32_kernel); the packed
+// X of the fp16 GEMM is padded to kMt tiles of 16 tokens.
 constexpr int kMt = 4;                 // 16-token tiles per workgroup (64 tokens)
 constexpr int kNT = 5;                 // 16-row weight tiles per wave (80 rows)
 constexpr int kWaves = 4;              // waves per workgroup, side by side along N
 constexpr int kThreads = 64 * kWaves;
 constexpr int kNwg = 16 * kNT * kWaves;  // 320 weight rows per workgroup
-constexpr int kXUnit = kMt * 4 * 64;     // uint4 of A operands per unit (16 KB)
 
 // X [M x K] f32 -> XP[mt][sb][h][s][lane] (uint4 = 8 halves); rows >= M are zeros.
 // Workgroup (sb, mt): the 16 x 256 block of X, read row-major into LDS, written out as
@@ -106,144 +107,178 @@ __device__ __forceinline__ half8 deq8(uint32_t u, const SubScale& k, uint32_t m_
     return __builtin_bit_cast(half8, r);
 }
 
-// Grid (ceil(N / 320), ceil(M / 64)): workgroups that share weight rows are 8 apart in
-// launch order when gridDim.x is a multiple of 8, i.e. on one XCD.  One wave per SIMD
-// (the accumulators, three units of staged weights and the operands take ~410 registers).
-__global__ __launch_bounds__(kThreads) void q4k_gemm_kernel(const uint8_t* __restrict__ qs,
-                                                            const v4u* __restrict__ hdr,
-                                                            const v4u* __restrict__ XP, float* __restrict__ Y,
-                                                            int M, int N, int K, int ntiles) {
-    __shared__ v4u As[3 * kXUnit];  // A operands of three units
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// ── fp16 operands with the dequantization shared by the workgroup ─────────
+// 256 tokens x 80 weight rows per workgroup (grid 128 x 2 = one workgroup per CU at
+// M = 512, N = 10240), eight waves, two per SIMD (one wave's loads wait while the other
+// multiplies).  Each unit (half super-block, 128 k, four k-steps of 32) is dequantized
+// once: wave w turns k-step w % 4 of tiles 0-2 (w < 4) or 3-4 (w >= 4) into fp16 B
+// operands in LDS, then every wave multiplies its own 32 tokens (two A tiles from the
+// packed X, straight into registers) by the B operands of all four steps.  Per unit and
+// SIMD: five 8-weight dequantizations and their scales against 80 MFMAs, where a wave that
+// dequantizes its own rows for its own 64 tokens does twenty.
+constexpr int kShTiles = 5;                   // 16-row weight tiles per workgroup
+constexpr int kShWaves = 8;
+constexpr int kShThreads = 64 * kShWaves;
+constexpr int kShMt = 2;                      // 16-token tiles per wave
+constexpr int kShTok = 16 * kShMt * kShWaves;  // 256 tokens per workgroup
+constexpr int kShDq = 3;                      // most tiles one wave dequantizes per unit
+
+__global__ __launch_bounds__(kShThreads) void q4k_gemm_shared_kernel(const uint8_t* __restrict__ qs,
+                                                                     const v4u* __restrict__ hdr,
+                                                                     const v4u* __restrict__ XP, float* __restrict__ Y,
+                                                                     int M, int N, int K, int ntiles, int mtiles) {
+    __shared__ v4u Bs[3][kShTiles][4][64];  // B operands of three units (60 KB)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
     const int S = K / 256;
     const int n = 2 * S;  // units: (super-block u / 2, half u % 2)
-    const int mt0 = blockIdx.y * kMt;
-    const int nt0 = (blockIdx.x * kWaves + wave) * kNT;  // first 16-row weight tile of this wave
+    const int nt0 = blockIdx.x * kShTiles;
+    const int mtw = blockIdx.y * (kShTok / 16) + wave * kShMt;  // first 16-token tile of this wave
+    const int step = wave & 3;                                  // the k-step this wave dequantizes
+    const int dj0 = wave < 4 ? 0 : 3, dn = wave < 4 ? 3 : 2;    // and its tiles dj0 .. dj0 + dn - 1
 
-    // wave-uniform byte offsets of tile j's qs block (sb 0, half 0) and header block;
-    // the lane adds its 16-byte slot (qs) or header row c
-    uint32_t qo[kNT], ho[kNT];
+    // qs block (sb 0, half 0) of dequantized tile jj, offset to this wave's dword of the
+    // lane's 16-byte nibble slot, and the tile's header block
+    uint32_t qo[kShDq], ho[kShDq];
 #pragma unroll
-    for (int j = 0; j < kNT; j++) {
-        const uint32_t t = static_cast<uint32_t>(min(nt0 + j, ntiles - 1));
-        qo[j] = __builtin_amdgcn_readfirstlane(t * S * 2048u);
-        ho[j] = __builtin_amdgcn_readfirstlane(t * S * 256u);
+    for (int jj = 0; jj < kShDq; jj++) {
+        const uint32_t t = static_cast<uint32_t>(min(nt0 + dj0 + min(jj, dn - 1), ntiles - 1));
+        qo[jj] = __builtin_amdgcn_readfirstlane(t * S * 2048u + 4u * step);
+        ho[jj] = __builtin_amdgcn_readfirstlane(t * S * 256u);
     }
-    const v4u* xb = XP + static_cast<size_t>(mt0) * S * 512 + tid;
+    // every load is a wave-uniform base plus the lane's byte offset (scalar base, vector offset)
+    const uint32_t lo16 = lane * 16u, lc16 = c * 16u;
+    // A tile i of this wave: XP[(mt n + u) 256 + s 64 + lane], mt clamped into the packed X
+    // (tiles past it hold tokens >= M, whose rows are not stored)
+    size_t xo[kShMt];
+#pragma unroll
+    for (int i = 0; i < kShMt; i++) xo[i] = static_cast<size_t>(min(mtw + i, mtiles - 1)) * n * 256;
 
-    // A: 1024 uint4 per unit, four per thread: idx = tid + 256 r -> (tile r, step, lane)
-    struct Xu {
-        v4u v[4];
+    struct Au {
+        v4u v[kShMt][4];  // [tile][k-step]
     };
-    auto load_x = [&](int u, Xu& x) __attribute__((always_inline)) {
+    auto load_a = [&](int u, Au& a) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) x.v[r] = xb[static_cast<size_t>(r) * S * 512 + u * 256];
-    };
-    auto store_x = [&](int b, const Xu& x) __attribute__((always_inline)) {
+        for (int i = 0; i < kShMt; i++) {
+            const uint8_t* base = reinterpret_cast<const uint8_t*>(XP + xo[i] + static_cast<size_t>(u) * 256);
 #pragma unroll
-        for (int r = 0; r < 4; r++) As[b * kXUnit + r * 256 + tid] = x.v[r];
+            for (int s = 0; s < 4; s++) a.v[i][s] = *reinterpret_cast<const v4u*>(base + lo16 + s * 1024);
+        }
     };
-    // nibbles and super-block header of the unit (the half's scale word is chosen when
-    // the unit is consumed: selecting at load time would wait for the load)
     struct Wu {
-        v4u q[kNT], hd[kNT];
+        uint32_t q[kShDq];
+        v4u hd[kShDq];
     };
-    const uint8_t* hdrb = reinterpret_cast<const uint8_t*>(hdr) + c * 16;
     auto load_w = [&](int u, Wu& w) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < kNT; j++) {
-            w.q[j] = __builtin_nontemporal_load(
-                reinterpret_cast<const v4u*>(qs + qo[j] + static_cast<uint32_t>(u) * 1024u) + lane);
-            w.hd[j] = *reinterpret_cast<const v4u*>(hdrb + ho[j] + static_cast<uint32_t>(u >> 1) * 256u);
+        for (int jj = 0; jj < kShDq; jj++) {
+            const uint8_t* qb = qs + qo[jj] + static_cast<size_t>(u) * 1024;
+            const uint8_t* hb = reinterpret_cast<const uint8_t*>(hdr) + ho[jj] + static_cast<size_t>(u >> 1) * 256;
+            w.q[jj] = *reinterpret_cast<const uint32_t*>(qb + lo16);
+            w.hd[jj] = *reinterpret_cast<const v4u*>(hb + lc16);
         }
     };
-
-    floatx4 acc[kMt][kNT];
-#pragma unroll
-    for (int i = 0; i < kMt; i++)
-#pragma unroll
-        for (int j = 0; j < kNT; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
     uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u;
     asm volatile("" : "+v"(m_lo), "+v"(m_hi));  // keep the masks in VGPRs
-    auto compute = [&](int b, int u, const Wu& w) __attribute__((always_inline)) {
+    // this wave's k-step of unit u for its tiles -> LDS buffer b
+    auto dequant = [&](int u, const Wu& w, int b) __attribute__((always_inline)) {
         const int h = u & 1;
-        SubScale k[kNT];
 #pragma unroll
-        for (int j = 0; j < kNT; j++) {
-            const float d = h2f(w.hd[j].x & 0xFFFFu), dmin = h2f(w.hd[j].x >> 16);
-            const uint32_t scw = h ? w.hd[j].z : w.hd[j].y;
+        for (int jj = 0; jj < kShDq; jj++) {
+            if (jj >= dn) break;
+            const float d = h2f(w.hd[jj].x & 0xFFFFu), dmin = h2f(w.hd[jj].x >> 16);
+            const uint32_t scw = h ? w.hd[jj].z : w.hd[jj].y;
             const float sc = d * static_cast<float>((scw >> (8 * g)) & 0x3Fu);
-            const float mn = dmin * static_cast<float>((w.hd[j].w >> (8 * g + 4 * h)) & 0xFu);
-            k[j].sc = sc;
-            k[j].c_lo = -__builtin_fmaf(1024.f, sc, mn);
-            k[j].sc16 = sc * 0.0625f;
-            k[j].c_hi = -__builtin_fmaf(64.f, sc, mn);
+            const float mn = dmin * static_cast<float>((w.hd[jj].w >> (8 * g + 4 * h)) & 0xFu);
+            SubScale k;
+            k.sc = sc;
+            k.c_lo = -__builtin_fmaf(1024.f, sc, mn);
+            k.sc16 = sc * 0.0625f;
+            k.c_hi = -__builtin_fmaf(64.f, sc, mn);
+            Bs[b][dj0 + jj][step][lane] = __builtin_bit_cast(v4u, deq8(w.q[jj], k, m_lo, m_hi));
         }
-        const v4u* Ab = As + b * kXUnit;
+    };
+    floatx4 acc[kShMt][kShTiles];
+#pragma unroll
+    for (int i = 0; i < kShMt; i++)
+#pragma unroll
+        for (int j = 0; j < kShTiles; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const bool live = mtw < mtiles;  // wave-uniform: this wave has tokens to multiply
+    // the B operands of step s + 1 are read from LDS before the MFMAs of step s are issued
+    auto mfma = [&](const Au& a, int b) __attribute__((always_inline)) {
+        if (!live) return;
+        v4u bq[2][kShTiles];
+#pragma unroll
+        for (int j = 0; j < kShTiles; j++) bq[0][j] = Bs[b][j][0][lane];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            half8 bq[kNT], aq[kMt];
+            if (s < 3) {
 #pragma unroll
-            for (int j = 0; j < kNT; j++) bq[j] = deq8(w.q[j][s], k[j], m_lo, m_hi);
+                for (int j = 0; j < kShTiles; j++) bq[(s + 1) & 1][j] = Bs[b][j][s + 1][lane];
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep those reads ahead of this step's MFMAs
 #pragma unroll
-            for (int i = 0; i < kMt; i++) aq[i] = __builtin_bit_cast(half8, Ab[(i * 4 + s) * 64 + lane]);
+            for (int i = 0; i < kShMt; i++)
 #pragma unroll
-            for (int i = 0; i < kMt; i++)
-#pragma unroll
-                for (int j = 0; j < kNT; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[i], bq[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < kShTiles; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a.v[i][s]),
+                                                                       __builtin_bit_cast(half8, bq[s & 1][j]),
+                                                                       acc[i][j], 0, 0, 0);
         }
     };
 
-    // Three-stage ring: unit u uses LDS buffer u % 3 and register sets u % 3.  After unit
-    // u is consumed, X of unit u + 1 goes to LDS and X and W of unit u + 3 are requested,
-    // so every load has two units of compute to arrive.  Loads past the last unit re-read
-    // it (unused), keeping the count of loads in flight the same in every stage.
+    // Three-unit ring: unit u multiplies from LDS buffer u % 3 and A registers u % 3 and
+    // was dequantized from weight registers u % 3.  In the stage of unit u the wave first
+    // dequantizes unit u + 1 (its weights were requested two stages before) into buffer
+    // (u + 1) % 3, requests the weights of unit u + 3, multiplies unit u, then requests the
+    // A tiles of unit u + 3 into the registers it just used.  A barrier ends each stage:
+    // buffer (u + 1) % 3 is complete, and the buffer the next stage overwrites was last
+    // read two stages before.  Loads past the last unit re-read it (unused).
+    Au a0, a1, a2;
     Wu w0, w1, w2;
-    Xu x0, x1, x2;
-    load_x(0, x0);
     load_w(0, w0);
-    load_x(min(1, n - 1), x1);
+    load_a(0, a0);
     load_w(min(1, n - 1), w1);
-    load_x(min(2, n - 1), x2);
+    load_a(min(1, n - 1), a1);
     load_w(min(2, n - 1), w2);
-    store_x(0, x0);
+    load_a(min(2, n - 1), a2);
+    dequant(0, w0, 0);
     __syncthreads();
-    auto stage = [&](int u, int b, Wu& w, Xu& xnext, Xu& xload) __attribute__((always_inline)) {
-        compute(b, u, w);
-        store_x(b == 2 ? 0 : b + 1, xnext);
-        load_x(min(u + 3, n - 1), xload);
-        load_w(min(u + 3, n - 1), w);
+    auto stage = [&](int u, int b, Au& a, const Wu& wn, Wu& wr) __attribute__((always_inline)) {
+        if (u + 1 < n) dequant(u + 1, wn, b == 2 ? 0 : b + 1);
+        load_w(min(u + 3, n - 1), wr);
+        mfma(a, b);
+        load_a(min(u + 3, n - 1), a);
         __syncthreads();
     };
     int u = 0;
     for (; u + 3 <= n; u += 3) {
-        stage(u, 0, w0, x1, x0);
-        stage(u + 1, 1, w1, x2, x1);
-        stage(u + 2, 2, w2, x0, x2);
+        stage(u, 0, a0, w1, w0);
+        stage(u + 1, 1, a1, w2, w1);
+        stage(u + 2, 2, a2, w0, w2);
     }
-    if (u < n) stage(u, 0, w0, x1, x0);
-    if (u + 1 < n) stage(u + 1, 1, w1, x2, x1);
+    if (u < n) stage(u, 0, a0, w1, w0);
+    if (u + 1 < n) stage(u + 1, 1, a1, w2, w1);
 
     // D lane (g, c) holds rows 4g .. 4g + 3 of column c of each 16 x 16 tile
+    if (!live) return;
 #pragma unroll
-    for (int i = 0; i < kMt; i++)
+    for (int i = 0; i < kShMt; i++)
 #pragma unroll
-        for (int j = 0; j < kNT; j++) {
+        for (int j = 0; j < kShTiles; j++) {
             const int col = (nt0 + j) * 16 + c;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = (mt0 + i) * 16 + 4 * g + r;
+                const int m = (mtw + i) * 16 + 4 * g + r;
                 if (m < M && col < N) Y[static_cast<size_t>(m) * N + col] = acc[i][j][r];
             }
         }
 }
 
 // ── f32 operands: the accurate variant for chains of projections ────────
-// Same tiling (64 tokens x 320 weight rows per workgroup, 80 rows per wave), with
-// v_mfma_f32_16x16x4f32: weights dequantized to f32 (`fma(q, d sc_j, -dmin m_j)`, one
+// 64 tokens x 320 weight rows per workgroup, 80 rows per wave (each wave dequantizes its
+// own rows for the workgroup's tokens), with v_mfma_f32_16x16x4f32: weights dequantized to f32 (`fma(q, d sc_j, -dmin m_j)`, one
 // rounding) and X read in f32, so each product is exact and the error is the f32
 // accumulation's (~1e-6) instead of the fp16 operands' (~1e-4 per projection), which
 // compounds through a model's layers.  A k-step of 4 takes element e of the lane's
@@ -587,11 +622,12 @@ void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, voi
     x16_pack_kernel<<<dim3(static_cast<unsigned>(w.cols / 256), static_cast<unsigned>(mtiles)), dim3(256), 0, s>>>(
         X, static_cast<v4u*>(ws), static_cast<int>(m), static_cast<int>(w.cols));
     LARQL_HIP_CHECK(hipGetLastError());
-    const dim3 grid(static_cast<unsigned>((w.rows + kNwg - 1) / kNwg), static_cast<unsigned>(mtiles / kMt));
-    q4k_gemm_kernel<<<grid, dim3(kThreads), 0, s>>>(w.qs, reinterpret_cast<const v4u*>(w.hdr),
-                                                     static_cast<const v4u*>(ws), Y, static_cast<int>(m),
-                                                     static_cast<int>(w.rows), static_cast<int>(w.cols),
-                                                     static_cast<int>(w.rows_pad / 16));
+    const size_t ntiles = w.rows_pad / 16;
+    const dim3 grid(static_cast<unsigned>((ntiles + kShTiles - 1) / kShTiles),
+                    static_cast<unsigned>((mtiles * 16 + kShTok - 1) / kShTok));
+    q4k_gemm_shared_kernel<<<grid, dim3(kShThreads), 0, s>>>(
+        w.qs, reinterpret_cast<const v4u*>(w.hdr), static_cast<const v4u*>(ws), Y, static_cast<int>(m),
+        static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(ntiles), static_cast<int>(mtiles));
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
