@@ -309,6 +309,28 @@ extern "C" int larql_hip_q4k_matmul(larql_hip_ctx* c, const uint8_t* q4k_data, s
     });
 }
 
+extern "C" int larql_hip_matmul(larql_hip_ctx* c, const float* a, size_t m, size_t k, const float* b, size_t n,
+                                int transpose_b, float* out) {
+    return guarded(c, [&] {
+        if (m == 0 || n == 0) return;
+        if (!out || (k > 0 && (!a || !b))) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        const float* da = k ? stage_upload(c, c->stage_in, a, m * k) : nullptr;
+        const float* db = k ? stage_upload(c, c->stage_in2, b, n * k) : nullptr;
+        float* dc = static_cast<float*>(larql::ensure(c, c->stage_out, m * n * sizeof(float)));
+        larql::launch_f32_matmul(da, db, dc, m, k, n, transpose_b != 0, c->stream);
+        download(c, out, dc, m * n * sizeof(float));
+    });
+}
+
+extern "C" int larql_hip_matmul_dev(larql_hip_ctx* c, const float* a, size_t m, size_t k, const float* b, size_t n,
+                                    int transpose_b, float* out, void* stream) {
+    return guarded(c, [&] {
+        if (m == 0 || n == 0) return;
+        if (!out || (k > 0 && (!a || !b))) fail(LARQL_HIP_ERR_INVALID, "null pointer");
+        larql::launch_f32_matmul(a, b, out, m, k, n, transpose_b != 0, pick_stream(c, stream));
+    });
+}
+
 extern "C" int larql_hip_q6k_matvec(larql_hip_ctx* c, const uint8_t* q6k_data, size_t q6k_len, const float* x,
                                     float* out, size_t num_rows, size_t hidden) {
     return guarded(c, [&] {

@@ -209,6 +209,10 @@ void launch_q6k_matvec(const DevWeight& w, const float* x, float* out, size_t m,
 // workgroup into out[0 .. groups).
 void launch_q4k_read_floor(const DevWeight& w, uint32_t* out, size_t out_words, unsigned groups, unsigned threads,
                            int num_cus, hipStream_t s);
+// C[m][n] = A[m][k] . B (B [k][n], or [n][k] transposed), f32 fma chains in k order
+// (f32_gemm.hip).
+void launch_f32_matmul(const float* A, const float* B, float* C, size_t m, size_t k, size_t n, bool transpose_b,
+                       hipStream_t s);
 // Y[m][rows] = X[m][cols] . deq(W)^T, Q4_K, on MFMA (prefill.hip); ws holds X as fp16
 // MFMA operands.
 size_t q4k_gemm_ws_bytes(size_t m, size_t cols);

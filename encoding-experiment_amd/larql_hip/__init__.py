@@ -66,6 +66,8 @@ SIGNATURES = {
     "larql_hip_q4k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
     "larql_hip_q6k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
     "larql_hip_q4k_matmul": (_I, [_P, _P, _SZ, _P, _SZ, _P, _SZ, _SZ]),
+    "larql_hip_matmul": (_I, [_P, _P, _SZ, _SZ, _P, _SZ, _I, _P]),
+    "larql_hip_matmul_dev": (_I, [_P, _P, _SZ, _SZ, _P, _SZ, _I, _P, _P]),
     "larql_hip_quantize_to_q8": (_I, [_P, _P, _SZ, _P, _P]),
     "larql_hip_q8_matvec": (_I, [_P, _P, _SZ, _P, _P, _P, _SZ, _P, _SZ, _SZ]),
     "larql_hip_matvec_dev": (_I, [_P, _U64, _P, _P, _P, _SZ, _P]),
@@ -383,6 +385,37 @@ class HipBackend:
         rc = self._lib.larql_hip_q4k_matmul(self._ctx, qp, q.size, xv.ctypes.data_as(_P), m, out.ctypes.data_as(_P),
                                             num_rows, hidden)
         return out if self._ok(rc) else None
+
+    def _matmul(self, a, b, transpose_b: bool):
+        av = np.ascontiguousarray(a, dtype=np.float32)
+        bv = np.ascontiguousarray(b, dtype=np.float32)
+        if av.ndim != 2 or bv.ndim != 2:
+            raise ValueError("matmul takes 2-D arrays")
+        m, k = av.shape
+        n = bv.shape[0] if transpose_b else bv.shape[1]
+        if (bv.shape[1] if transpose_b else bv.shape[0]) != k:
+            raise ValueError(f"matmul: inner dimensions differ ({av.shape} x {bv.shape}, transpose_b={transpose_b})")
+        out = np.empty((m, n), dtype=np.float32)
+        rc = self._lib.larql_hip_matmul(self._ctx, av.ctypes.data_as(_P), m, k, bv.ctypes.data_as(_P), n,
+                                        int(bool(transpose_b)), out.ctypes.data_as(_P))
+        return out if self._ok(rc) else None
+
+    def matmul(self, a, b):
+        """backend.rs:27-28 — C = A [m, k] x B [k, n] (f32)."""
+        return self._matmul(a, b, False)
+
+    def matmul_transb(self, a, b):
+        """backend.rs:30-31 — C = A [m, k] x B [n, k]^T (f32)."""
+        return self._matmul(a, b, True)
+
+    def matmul_batch(self, ops):
+        """backend.rs:33-43 — ops: (a, b, transpose_b) triples, run in order."""
+        return [self._matmul(a, b, tb) for a, b, tb in ops]
+
+    def matmul_dev(self, a, b, out, m: int, k: int, n: int, transpose_b: bool = False, stream=None):
+        """Device form of matmul / matmul_transb: a [m, k], b [k, n] or [n, k], out [m, n]."""
+        self._check(self._lib.larql_hip_matmul_dev(self._ctx, _dptr(a), m, k, _dptr(b), n, int(bool(transpose_b)),
+                                                   _dptr(out), _stream_ptr(stream)))
 
     def q6k_matvec(self, q6k_data, x, num_rows: int, hidden: int):
         """backend.rs:133-137 — scores[N] = Q6_K[N,K] @ f32_x[K]."""

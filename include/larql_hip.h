@@ -85,6 +85,22 @@ int larql_hip_has_kv_cache(larql_hip_ctx* ctx);
 /* Block until all work queued on the context stream has finished. */
 int larql_hip_synchronize(larql_hip_ctx* ctx);
 
+/* ComputeBackend::matmul / matmul_transb — LC/src/backend.rs:27-31 (Metal: tiled sgemm,
+ * LC/src/metal/f32_ops.rs:93-140).  f32, row-major, host pointers:
+ *   transpose_b == 0: c[m][n] = a[m][k] . b[k][n]
+ *   transpose_b != 0: c[m][n] = a[m][k] . b[n][k]^T
+ * Each element of c is one f32 fma chain over k = 0 .. k-1 from +0 (reproducible bit for
+ * bit; the reference CPU sgemm sums in its own blocked order, within f32 rounding).  Both
+ * operands are uploaded on every call (no caching: callers update operands in place, as
+ * the k-means centroids of LV/src/clustering/kmeans.rs:28 are).  k == 0 gives zeros;
+ * m == 0 or n == 0 writes nothing.  ComputeBackend::matmul_batch (:35-43) is these calls
+ * in order. */
+int larql_hip_matmul(larql_hip_ctx* ctx, const float* a, size_t m, size_t k, const float* b, size_t n,
+                     int transpose_b, float* c);
+/* Same on device pointers, enqueued on `stream` (null: the context stream). */
+int larql_hip_matmul_dev(larql_hip_ctx* ctx, const float* a, size_t m, size_t k, const float* b, size_t n,
+                         int transpose_b, float* c, void* stream);
+
 /* ── weight registry (explicit form of the Metal buffer cache) ─────────── */
 
 /* Upload + repack a reference-layout weight from host memory.  q8_scales is
