@@ -97,7 +97,11 @@ void lo_topk_abs(const float* scores, size_t n, size_t k, uint32_t* idx, float* 
 /* Top-k by signed score descending (LV/src/index/walk.rs:563-580); ties -> lower index. */
 void lo_topk_signed(const float* scores, size_t n, size_t k, uint32_t* idx, float* val);
 /* f32 gate scores in the canonical order shared with the HIP kernel:
- * s[f] = one sequential fmaf chain over k = 0..hidden-1 starting from +0.0f. */
+ * s[f] = one sequential fmaf chain over k = 0..hidden-1 starting from +0.0f.
+ * Parity unpinned for the bit patterns: the reference computes these scores in the
+ * third-party matrixmultiply 0.3 sgemm (LV/src/index/gate.rs:14-29 ->
+ * larql-main/crates/larql-tensor/src/sgemm.rs:41-68), whose accumulation order is not in
+ * the reference tree; the value is pinned against an exact f64 dot within f32 bounds. */
 void lo_gate_scores_f32(const float* gate, const float* x, float* out, size_t features, size_t hidden);
 
 /* ── decode-step numerics (LI/src) ──────────────────────────────────────── */
