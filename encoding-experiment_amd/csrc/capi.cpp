@@ -403,8 +403,7 @@ static void run_pair_batch(larql_hip_ctx* c, const DevWeight& g, const DevWeight
     int8_t* q8 = static_cast<int8_t*>(larql::ensure(c, c->pair_q8, seq * hidden));
     float* q8s = static_cast<float*>(larql::ensure(c, c->pair_q8s, seq * (hidden / 32) * sizeof(float)));
     larql::launch_quantize_q8(x, hidden, seq, q8, q8s, s);
-    larql::launch_q4_0_matvec(g, q8, q8s, gate_out, seq, s);
-    larql::launch_q4_0_matvec(u, q8, q8s, up_out, seq, s);
+    larql::launch_q4_0_matvec_pair(g, u, q8, q8s, gate_out, up_out, seq, s);
 }
 
 extern "C" int larql_hip_q4_matvec_pair_batch(larql_hip_ctx* c, const uint8_t* gate_q4, size_t gate_len,

@@ -440,8 +440,9 @@ struct PromptAttn {
     float softcap = 0.f;
 };
 
-// The layer launches of one decode step at T = pos + 1, h0 -> h0.
-void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hipStream_t s,
+// The layer launches of one decode step at T = pos + 1, x0 -> h0 (layer 0 reads its
+// input from x0, which the step does not write; later layers read h0).
+void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, const float* x0, int T, float* part, hipStream_t s,
                     const PromptAttn& pa = {}) {
     auto& kv = c->kv;
     // prenormed: m->xw / m->psum hold this layer's normed Q/K/V input (from the previous
@@ -450,17 +451,18 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hi
     int npsum = 0;
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
+        const float* hin = l == 0 ? x0 : m->h0;
         // Q/K/V: f32-input formats with the input norm fused into the matvec; Q8_0 from the
         // quantized normed input (one quantization shared by the three)
         bool have_q8 = false;
         auto qkv_proj = [&](const DevWeight& w, float* out) {
             if (takes_q8(w, false)) {
-                if (!have_q8) quantize_input(m, m->h0, m->hidden, L.input_norm, L.norm_offset, L.eps, s);
+                if (!have_q8) quantize_input(m, hin, m->hidden, L.input_norm, L.norm_offset, L.eps, s);
                 have_q8 = true;
                 int_proj(w, m, out, s);
             } else {
                 larql::MvArgs a;
-                a.x = m->h0;
+                a.x = hin;
                 a.out = out;
                 a.eps = L.eps;
                 if (prenormed) {
@@ -514,10 +516,10 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hi
                 larql::launch_mv(L.wo, o, s);
             }
             if (L.post_norms)
-                larql::launch_resid_norm_rows(m->h0, m->otmp, L.post_attn_norm, L.norm_offset, 1.0f, m->h1, 1,
+                larql::launch_resid_norm_rows(hin, m->otmp, L.post_attn_norm, L.norm_offset, 1.0f, m->h1, 1,
                                               m->hidden, L.eps, s);
             else
-                larql::launch_add_rows(m->h0, m->otmp, m->h1, m->hidden, s);
+                larql::launch_add_rows(hin, m->otmp, m->h1, m->hidden, s);
         }
 
         // FFN input norm: post_attn_norm, or pre_ffn_norm (weight-free when absent) for
@@ -541,7 +543,7 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, int T, float* part, hi
             o.x = m->attn;
             o.out = m->h1;
             o.epi = larql::EPI_RESID;
-            o.resid = m->h0;
+            o.resid = hin;
             if (ffn_prenormed) {
                 o.out2 = m->xw;
                 o.out2_w = fnorm;
@@ -646,8 +648,8 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
     const int S = (T + 63) / 64;
     float* part = static_cast<float*>(
         larql::ensure(c, m->part, static_cast<size_t>(m->nq) * S * (m->hd + 2) * sizeof(float)));
-    larql::launch_copy_f32(x_dev, m->h0, m->hidden, s);
-    enqueue_layers(c, m, T, part, s, pa);
+    if (m->layers.empty()) larql::launch_copy_f32(x_dev, m->h0, m->hidden, s);
+    else enqueue_layers(c, m, x_dev, T, part, s, pa);
     kv.current_len = static_cast<size_t>(T);
     if (hidden_out) larql::launch_copy_f32(m->h0, hidden_out, m->hidden, s);
     if (logits) {
@@ -912,8 +914,7 @@ extern "C" int larql_hip_multi_layer_q4_ffn(larql_hip_ctx* c, const larql_q4_ffn
             const DevWeight& dw = larql::cached_weight(c, LARQL_Q4_0, L.down, L.down_len, nullptr, hidden, inter);
             float *xin = X[l & 1], *xout = X[(l + 1) & 1];
             larql::launch_quantize_q8(xin, hidden, 1, q8, q8s, c->stream);
-            larql::launch_q4_0_matvec(gw, q8, q8s, G, 1, c->stream);
-            larql::launch_q4_0_matvec(uw, q8, q8s, U, 1, c->stream);
+            larql::launch_q4_0_matvec_pair(gw, uw, q8, q8s, G, U, 1, c->stream);
             larql::launch_gated_mul(G, U, A, inter, LARQL_ACT_SILU, c->stream);
             larql::launch_q4_0_f32_matvec(dw, A, xout, c->stream);
         }

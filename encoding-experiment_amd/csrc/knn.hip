@@ -14,6 +14,7 @@
 #include "knn.h"
 
 #include <algorithm>
+#include <type_traits>
 
 // The Q4_0 path must round the product and the sum separately, as the reference's
 // `acc += (float)isum * cs` does; explicit fmaf() calls (the f32 path) are unaffected.
@@ -276,9 +277,12 @@ __global__ __launch_bounds__(kThreads, 2) void gate_scores_q4_kernel(KnnLayers g
 // pattern of |s| (abs mode; -0 and +0 equal), or an order-preserving map of s
 // (signed mode).  A radix select over 8-bit digits of c (8 passes) finds the k-th
 // largest composite exactly; the k elements at or above it are ranked and written.
-__device__ __forceinline__ uint32_t order_key(float v, int signed_mode) {
+// (A template parameter, not a run-time flag: a branch per element between a load and
+// its use makes the compiler wait for each load before issuing the next.)
+template <bool SG>
+__device__ __forceinline__ uint32_t order_key(float v) {
     uint32_t b = __float_as_uint(v);
-    if (!signed_mode) return b & 0x7FFFFFFFu;
+    if constexpr (!SG) return b & 0x7FFFFFFFu;
     if ((b & 0x7FFFFFFFu) == 0) b = 0;  // -0 == +0
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
@@ -364,9 +368,9 @@ constexpr int kTopkCap = 2048;  // candidates kept in LDS
 // (an all-zero row is one big tie).  Rows whose candidates overflow the LDS list run the
 // selects over all elements instead.  k <= n; the output rows are kstride apart and
 // slots k .. kstride - 1 receive index 0xFFFFFFFF and score 0.
-template <int PER>
+template <int PER, bool SG>
 __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ S, size_t row_stride, int n, int k,
-                                                        int kstride, int signed_mode, uint32_t* __restrict__ idx_out,
+                                                        int kstride, uint32_t* __restrict__ idx_out,
                                                         float* __restrict__ val_out) {
     __shared__ uint32_t hist[kThreads / 64][256];
     __shared__ uint32_t sel[2];
@@ -379,11 +383,12 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
     // element i = tid + kThreads * j (coalesced); held in registers when PER > 0
     uint32_t key[PER > 0 ? PER : 1];
     if constexpr (PER > 0) {
+        // clamped, unpredicated loads first (all in flight together), then the keys
 #pragma unroll
-        for (int j = 0; j < PER; j++) {
-            const int i = tid + kThreads * j;
-            key[j] = i < n ? order_key(s[i], signed_mode) : 0u;
-        }
+        for (int j = 0; j < PER; j++) key[j] = __float_as_uint(s[min(tid + kThreads * j, n - 1)]);
+#pragma unroll
+        for (int j = 0; j < PER; j++)
+            key[j] = tid + kThreads * j < n ? order_key<SG>(__uint_as_float(key[j])) : 0u;
     }
     const int nper = (n + kThreads - 1) / kThreads;
     // f(key, i) for this thread's elements i = tid + kThreads * j < n
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
             for (int j = 0; j < nper; j++) {
                 const int i = tid + kThreads * j;
                 if (i >= n) break;
-                f(order_key(s[i], signed_mode), i);
+                f(order_key<SG>(s[i]), i);
             }
         }
     };
@@ -495,6 +500,270 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
     }
 }
 
+// ── top-k, one wave per row ────────────────────────────────────────────────
+// Rows of n <= 64 PW elements with k <= 64.  Each wave owns one row (element i = lane +
+// 64 j in register j) and runs without workgroup barriers, so a CU works on many rows at
+// once instead of one.  Same order and result as topk_kernel:
+//   1. T = the k-th largest of the 64 lane maxima: k distinct lanes hold an element >= T,
+//      so T bounds the k-th largest key from below;
+//   2. the elements with key >= T go to the wave's LDS list (a wave scan of the lanes'
+//      counts gives each lane its slots);
+//   3. K = the k-th largest key of the list; `above` keys exceed it;
+//   4. ties at K are kept in index order: imax = the (k - above)-th smallest tie index;
+//   5. the k winners are ranked by (key descending, index ascending) and written.
+// A row whose list would overflow (many equal keys) runs steps 3-4 over its registers.
+// Every k-th-largest search is a radix descent over the 32 key bits with wave ballots.
+// Register slots past n hold key 0 with an index >= n: with k <= n they rank below k
+// real elements (no key is below 0, and ties go to the smaller index), so they take
+// part in every step without a validity test.
+constexpr int kWCap = 512;      // list entries per wave
+constexpr int kWWaves = 4;      // rows per workgroup
+
+__device__ __forceinline__ uint64_t wave_ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+__device__ __forceinline__ int wave_popc(bool p) { return __builtin_popcountll(wave_ballot(p)); }
+// Set bits of m below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+}
+
+// The k-th largest of the values v[t] with ok[t] over the wave (the largest x that at
+// least k of them reach); 0 when fewer than k are valid.  Wave-uniform.
+template <int R, class V, class Ok>
+__device__ __forceinline__ uint32_t wave_kth_largest(V v, Ok ok, int k) {
+    uint32_t prefix = 0;
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t c = prefix | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int t = 0; t < R; t++) cnt += wave_popc(ok(t) && v(t) >= c);
+        if (cnt >= k) prefix = c;
+    }
+    return prefix;
+}
+
+template <int PW, bool SG>
+__global__ __launch_bounds__(64 * kWWaves) void topk_wave_kernel(const float* __restrict__ S, size_t row_stride,
+                                                                 int n, int k, int kstride,
+                                                                 uint32_t* __restrict__ idx_out,
+                                                                 float* __restrict__ val_out, int rows) {
+    __shared__ uint32_t lkey[kWWaves][kWCap], lidx[kWWaves][kWCap];
+    __shared__ uint32_t wkey[kWWaves][64], widx[kWWaves][64];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row = blockIdx.x * kWWaves + w;
+    if (row >= rows) return;  // whole wave; the kernel has no workgroup barrier
+    const float* __restrict__ s = S + static_cast<size_t>(row) * row_stride;
+    uint32_t key[PW];
+    if (n == 64 * PW) {  // every register holds an element: one base, immediate offsets
+        const float* __restrict__ sl = s + lane;
+#pragma unroll
+        for (int j = 0; j < PW; j++) key[j] = order_key<SG>(sl[64 * j]);
+    } else {
+        // raw buffer loads over exactly the row's n floats (offsets past it read 0; the
+        // whole offset is in the vector operand, which the range check covers), all in
+        // flight together, then the keys; the mask is all ones for i < n, zero past the row
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(s), 0, n * static_cast<int>(sizeof(float)), 0x00020000);
+#pragma unroll
+        for (int j = 0; j < PW; j++) key[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * lane + 256 * j, 0, 0);
+#pragma unroll
+        for (int j = 0; j < PW; j++) {
+            const uint32_t live = static_cast<uint32_t>((lane + 64 * j - n) >> 31);
+            key[j] = order_key<SG>(__uint_as_float(key[j])) & live;
+        }
+    }
+    // element index of register j; the opaque copy of the lane keeps the compiler from
+    // holding one index register per j
+    auto index_of = [&](int j) __attribute__((always_inline)) {
+        int l = lane;
+        asm volatile("" : "+v"(l));
+        return static_cast<uint32_t>(l + 64 * j);
+    };
+    auto all = [](int) { return true; };
+
+    // 1. T from the lane maxima
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < PW; j++) m = max(m, key[j]);
+    const uint32_t T = wave_kth_largest<1>([&](int) { return m; }, all, k);
+
+    // 2. the list of keys >= T (slots past the capacity are not written)
+    int total = 0;
+#pragma unroll
+    for (int j = 0; j < PW; j++) {
+        const bool c = key[j] >= T;
+        const uint64_t b = wave_ballot(c);
+        if (b) {  // wave-uniform
+            const int q = total + lanes_below(b);
+            if (c && q < kWCap) {
+                lkey[w][q] = key[j];
+                lidx[w][q] = index_of(j);
+            }
+            total += __builtin_popcountll(b);
+        }
+    }
+    uint32_t K, imax = 0xFFFFFFFFu;
+    int nwin = 0;
+    if (total <= kWCap) {
+        // the wave reads what its own lanes wrote: keep the LDS accesses in program order
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        constexpr int R = kWCap / 64;
+        uint32_t ck[R], ci[R];
+#pragma unroll
+        for (int t = 0; t < R; t++) {
+            const int q = lane + 64 * t;
+            ck[t] = q < total ? lkey[w][q] : 0u;
+            ci[t] = q < total ? lidx[w][q] : 0u;
+        }
+        auto cok = [&](int t) __attribute__((always_inline)) { return lane + 64 * t < total; };
+        // 3. K and the keys above it
+        K = wave_kth_largest<R>([&](int t) { return ck[t]; }, cok, k);
+        int above = 0, nt = 0;
+#pragma unroll
+        for (int t = 0; t < R; t++) {
+            above += wave_popc(cok(t) && ck[t] > K);
+            nt += wave_popc(cok(t) && ck[t] == K);
+        }
+        // 4. the (k - above) smallest tie indices: the largest kept is the need-th largest
+        // of the complemented indices
+        const int need = k - above;
+        if (nt > need)
+            imax = ~wave_kth_largest<R>([&](int t) { return ~ci[t]; },
+                                         [&](int t) { return cok(t) && ck[t] == K; }, need);
+        // 5. the winners to the wave's winner list
+#pragma unroll
+        for (int t = 0; t < R; t++) {
+            const bool win = cok(t) && (ck[t] > K || (ck[t] == K && ci[t] <= imax));
+            const uint64_t b = wave_ballot(win);
+            if (win) {
+                const int q = nwin + lanes_below(b);
+                wkey[w][q] = ck[t];
+                widx[w][q] = ci[t];
+            }
+            nwin += __builtin_popcountll(b);
+        }
+    } else {
+        // 3-4 over the keys in the registers (rows with many equal keys): K by four 8-bit
+        // radix passes with a wave histogram in LDS, then the ties in index order (j, then
+        // lane) and the winners, one sweep each.
+        uint32_t* hist = lkey[w];  // 256 bins
+        uint32_t prefix = 0, pmask = 0;
+        int remaining = k;
+        for (int pass = 0; pass < 4; pass++) {
+            const int shift = 24 - 8 * pass;
+#pragma unroll
+            for (int u = 0; u < 4; u++) hist[lane + 64 * u] = 0u;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int j = 0; j < PW; j++)
+                if ((key[j] & pmask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 0xFFu], 1u);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // lane covers digits 255 - 4 lane .. 252 - 4 lane (descending)
+            uint32_t h[4], tot = 0;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                h[u] = hist[255 - 4 * lane - u];
+                tot += h[u];
+            }
+            const uint32_t inc = wave_incl_scan(tot), exc = inc - tot;
+            const bool here = exc < static_cast<uint32_t>(remaining) && inc >= static_cast<uint32_t>(remaining);
+            uint32_t dsel = 0, rem = 0, cum = exc;
+            bool found = false;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (here && !found && cum + h[u] >= static_cast<uint32_t>(remaining)) {
+                    dsel = 255 - 4 * lane - u;
+                    rem = static_cast<uint32_t>(remaining) - cum;
+                    found = true;
+                }
+                cum += h[u];
+            }
+            const uint64_t at = wave_ballot(here);
+            const int src = __builtin_ctzll(at);
+            prefix |= static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(dsel), src)) << shift;
+            remaining = __builtin_amdgcn_readlane(static_cast<int>(rem), src);
+            pmask |= 0xFFu << shift;
+            // the histogram's area is rewritten by the next pass
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        K = prefix;
+        const int need = remaining;  // ties kept; k - need keys exceed K
+        // the two sweeps read the keys again from memory, eight registers at a time (a
+        // loop over the register array would need a ballot per register, all unrolled)
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(s), 0, n * static_cast<int>(sizeof(float)), 0x00020000);
+        auto load8 = [&](int j0, uint32_t (&kk)[8]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) kk[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * (lane + 64 * (j0 + u)), 0, 0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t live = static_cast<uint32_t>((lane + 64 * (j0 + u) - n) >> 31);
+                kk[u] = order_key<SG>(__uint_as_float(kk[u])) & live;
+            }
+        };
+        int run = 0;
+        for (int j0 = 0; j0 < PW && run < need; j0 += 8) {
+            uint32_t kk[8];
+            load8(j0, kk);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const bool tie = kk[u] == K;
+                const uint64_t b = wave_ballot(tie);
+                const int c = __builtin_popcountll(b);
+                if (run < need && run + c >= need) {  // wave-uniform
+                    const uint64_t at = wave_ballot(tie && lanes_below(b) == need - run - 1);
+                    imax = static_cast<uint32_t>(__builtin_ctzll(at) + 64 * (j0 + u));
+                }
+                run += c;
+            }
+        }
+        for (int j0 = 0; j0 < PW; j0 += 8) {
+            uint32_t kk[8];
+            load8(j0, kk);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t i = static_cast<uint32_t>(lane + 64 * (j0 + u));
+                const bool win = kk[u] > K || (kk[u] == K && i <= imax);
+                const uint64_t b = wave_ballot(win);
+                if (win) {
+                    const int q = nwin + lanes_below(b);
+                    wkey[w][q] = kk[u];
+                    widx[w][q] = i;
+                }
+                nwin += __builtin_popcountll(b);
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // 5. rank the k winners: key descending, index ascending
+    const size_t row0 = static_cast<size_t>(row) * kstride;
+    if (lane < k) {
+        const uint32_t mk = wkey[w][lane], mi = widx[w][lane];
+        int rank = 0;
+        for (int j = 0; j < k; j++) {
+            const uint32_t ok = wkey[w][j], oi = widx[w][j];
+            rank += (ok > mk || (ok == mk && oi < mi)) ? 1 : 0;
+        }
+        idx_out[row0 + rank] = mi;
+        val_out[row0 + rank] = s[mi];
+    }
+    for (int p = k + lane; p < kstride; p += 64) {
+        idx_out[row0 + p] = 0xFFFFFFFFu;
+        val_out[row0 + p] = 0.0f;
+    }
+}
+
 }  // namespace
 
 void launch_gate_scores_f32(const KnnLayers& g, int n_layers, const float* X, float* S, int F, int K, int Q,
@@ -525,11 +794,26 @@ void launch_topk(const float* S, size_t rows, size_t row_stride, int n, int k, i
     if (k < 1 || k > kTopkMaxK || n < 1) fail(LARQL_HIP_ERR_INVALID, "top-k: need 1 <= k <= 512 and n >= 1");
     if (rows == 0) return;
     const int ke = std::min(k, n);  // top_k.min(len), LV/src/index/walk.rs:569
-    const dim3 grid(static_cast<unsigned>(rows));
-    if (n <= kThreads * 48)
-        topk_kernel<48><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, k, signed_mode, idx, val);
-    else
-        topk_kernel<0><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, k, signed_mode, idx, val);
+    auto go = [&](auto sg) {
+        constexpr bool SG = decltype(sg)::value;
+        const dim3 grid(static_cast<unsigned>(rows));
+        if (ke <= 64 && n <= 64 * 224 && rows <= 0x7FFFFFFF) {  // a wave per row
+            const dim3 gw(static_cast<unsigned>((rows + kWWaves - 1) / kWWaves)), bw(64 * kWWaves);
+            const int r = static_cast<int>(rows);
+            if (n <= 64 * 64)
+                topk_wave_kernel<64, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, k, idx, val, r);
+            else if (n <= 64 * 160)
+                topk_wave_kernel<160, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, k, idx, val, r);
+            else
+                topk_wave_kernel<224, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, k, idx, val, r);
+        } else if (n <= kThreads * 48) {
+            topk_kernel<48, SG><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, k, idx, val);
+        } else {
+            topk_kernel<0, SG><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, k, idx, val);
+        }
+    };
+    if (signed_mode) go(std::true_type{});
+    else go(std::false_type{});
     LARQL_HIP_CHECK(hipGetLastError());
 }
 

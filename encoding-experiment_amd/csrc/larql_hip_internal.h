@@ -228,6 +228,9 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
                          hipStream_t s, size_t ldy = 0);
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
                         size_t m, hipStream_t s);
+// Two Q4_0 matrices of one shape times the same Q8 rows, in one launch per pass.
+void launch_q4_0_matvec_pair(const DevWeight& w1, const DevWeight& w2, const int8_t* q8x, const float* q8s,
+                             float* out1, float* out2, size_t m, hipStream_t s);
 void launch_q8_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
                       size_t m, hipStream_t s);
 // Q4_0 weights x f32 activation (one row of x), the reference GPU's q4_f32_matvec.

@@ -190,15 +190,22 @@ constexpr size_t x_lds_bytes(int m, int nb) {
     return static_cast<size_t>(m) * nb * (32 + Blk<FMT>::kXAux * 4);
 }
 
-// Grid: one workgroup per 256 / G rows.  x: m <= M activation rows of Q8 values (cols
-// int8 each) and their scales (nb each); out: m rows of `rows` floats.  Rows m..M-1 of
-// the x image are left unset: their sums are formed and discarded.
+// A second weight matrix of the same shape, multiplied by the same activation rows in the
+// same launch (gate and up of a walk FFN): workgroups nwg1 .. 2 nwg1 - 1 take it.
+struct IntMvPair {
+    const uint8_t* qs;
+    const void* dsc;
+    float* out;
+    int nwg1;  // workgroups of the first matrix
+};
+
+// Grid: one workgroup per 256 / G rows (of each matrix).  x: m <= M activation rows of Q8
+// values (cols int8 each) and their scales (nb each); out: m rows of `rows` floats.  Rows
+// m..M-1 of the x image are left unset: their sums are formed and discarded.
 template <int FMT, int M, int G, int D>
-__global__ __launch_bounds__(kThreads) void int_mv_kernel(const uint8_t* __restrict__ qs,
-                                                          const void* __restrict__ dsc,
-                                                          const int8_t* __restrict__ xq,
-                                                          const float* __restrict__ xsc,
-                                                          float* __restrict__ out, int rows, int nb, int m) {
+__device__ __forceinline__ void int_mv_body(const uint8_t* __restrict__ qs, const void* __restrict__ dsc,
+                                            const int8_t* __restrict__ xq, const float* __restrict__ xsc,
+                                            float* __restrict__ out, int rows, int nb, int m, int wg) {
     using B = Blk<FMT>;
     // x image: first and second 16 bytes of every block in separate arrays, so the 16
     // lanes of a group read 256 contiguous bytes (no bank conflicts)
@@ -207,7 +214,7 @@ __global__ __launch_bounds__(kThreads) void int_mv_kernel(const uint8_t* __restr
     uint4* xw1 = lds4 + M * nb;                                    // [M][nb]
     uint32_t* xa = reinterpret_cast<uint32_t*>(lds4 + 2 * M * nb);  // [M][nb][kXAux]
     const int j = threadIdx.x & (G - 1);
-    const int row = blockIdx.x * (kThreads / G) + threadIdx.x / G;
+    const int row = wg * (kThreads / G) + threadIdx.x / G;
     const size_t base = static_cast<size_t>(min(row, rows - 1)) * nb;
     const int steps = (nb + G - 1) / G;
     const int nx = m * nb;
@@ -275,6 +282,29 @@ __global__ __launch_bounds__(kThreads) void int_mv_kernel(const uint8_t* __restr
         for (int mi = 0; mi < M; mi++)
             if (mi < m) out[static_cast<size_t>(mi) * rows + row] = acc[mi];
     }
+}
+
+template <int FMT, int M, int G, int D>
+__global__ __launch_bounds__(kThreads) void int_mv_kernel(const uint8_t* __restrict__ qs,
+                                                          const void* __restrict__ dsc,
+                                                          const int8_t* __restrict__ xq,
+                                                          const float* __restrict__ xsc,
+                                                          float* __restrict__ out, int rows, int nb, int m) {
+    int_mv_body<FMT, M, G, D>(qs, dsc, xq, xsc, out, rows, nb, m, blockIdx.x);
+}
+
+template <int FMT, int M, int G, int D>
+__global__ __launch_bounds__(kThreads) void int_mv_pair_kernel(const uint8_t* __restrict__ qs,
+                                                               const void* __restrict__ dsc,
+                                                               const int8_t* __restrict__ xq,
+                                                               const float* __restrict__ xsc,
+                                                               float* __restrict__ out, int rows, int nb, int m,
+                                                               IntMvPair second) {
+    if (static_cast<int>(blockIdx.x) >= second.nwg1)  // workgroup-uniform
+        int_mv_body<FMT, M, G, D>(second.qs, second.dsc, xq, xsc, second.out, rows, nb, m,
+                                  blockIdx.x - second.nwg1);
+    else
+        int_mv_body<FMT, M, G, D>(qs, dsc, xq, xsc, out, rows, nb, m, blockIdx.x);
 }
 
 // ── Q8_0 x Q8 for 2..8 activation rows on the matrix cores ─────────────
@@ -462,34 +492,49 @@ void launch_q8_mfma(const DevWeight& w, const int8_t* q8x, const float* q8s, flo
 
 constexpr size_t kLdsLimit = 64 * 1024;
 
+// w2 / out2: the optional second matrix of the same shape (one grid over both).
 template <int FMT, int M, int G, int D>
-void launch_int_mv_g(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s) {
+void launch_int_mv_g(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s,
+                     const DevWeight* w2, float* out2) {
     const int nb = static_cast<int>(w.cols / 32);
     const size_t rows_per_wg = kThreads / G;
     const size_t grid = (w.rows + rows_per_wg - 1) / rows_per_wg;
-    int_mv_kernel<FMT, M, G, D><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), x_lds_bytes<FMT>(M, nb), s>>>(
-        w.qs, w.d, q8x, q8s, out, static_cast<int>(w.rows), nb, m);
+    if (w2) {
+        IntMvPair second;
+        second.qs = w2->qs;
+        second.dsc = w2->d;
+        second.out = out2;
+        second.nwg1 = static_cast<int>(grid);
+        int_mv_pair_kernel<FMT, M, G, D>
+            <<<dim3(static_cast<unsigned>(2 * grid)), dim3(kThreads), x_lds_bytes<FMT>(M, nb), s>>>(
+                w.qs, w.d, q8x, q8s, out, static_cast<int>(w.rows), nb, m, second);
+    } else {
+        int_mv_kernel<FMT, M, G, D><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), x_lds_bytes<FMT>(M, nb), s>>>(
+            w.qs, w.d, q8x, q8s, out, static_cast<int>(w.rows), nb, m);
+    }
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
-// Lane groups of 4 when the matrix has enough 64-row workgroups to cover the chip
+// Lane groups of 4 when the launch has enough 64-row workgroups to cover the chip
 // (fewer DPP adds per block), else of 16 (four times the workgroups).  Measured on
 // Q8_0 [14336 x 4096]: 16.1 us (G = 4) vs 17.2 us (G = 16); on Q4_0 [10240 x 2560]:
 // 5.2 us (G = 16) vs 5.3 us (G = 4).
 template <int FMT, int M>
-void launch_int_mv(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s) {
-    if ((w.rows + 63) / 64 * 4 >= static_cast<size_t>(current_device_cus()) * 3)
-        launch_int_mv_g<FMT, M, 4, 4>(w, q8x, q8s, out, m, s);
+void launch_int_mv(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s,
+                   const DevWeight* w2, float* out2) {
+    const size_t nmat = w2 ? 2 : 1;
+    if (nmat * (w.rows + 63) / 64 * 4 >= static_cast<size_t>(current_device_cus()) * 3)
+        launch_int_mv_g<FMT, M, 4, 4>(w, q8x, q8s, out, m, s, w2, out2);
     else
-        launch_int_mv_g<FMT, M, 16, 4>(w, q8x, q8s, out, m, s);
+        launch_int_mv_g<FMT, M, 16, 4>(w, q8x, q8s, out, m, s, w2, out2);
 }
 
 // M activation rows in passes of up to 8 (one pass over the weights per pass): each pass
 // takes the kernel with 1, 2, 4 or 8 x rows that holds the rows left, or the largest
-// whose x image fits LDS.
+// whose x image fits LDS.  With w2, every pass multiplies both matrices in one launch.
 template <int FMT>
 void launch_int_mv_batched(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, size_t m,
-                           hipStream_t s) {
+                           hipStream_t s, const DevWeight* w2 = nullptr, float* out2 = nullptr) {
     const int nb = static_cast<int>(w.cols / 32);
     if (x_lds_bytes<FMT>(1, nb) > kLdsLimit) fail(LARQL_HIP_ERR_UNSUPPORTED, "int matvec: hidden too large for LDS staging");
     size_t done = 0;
@@ -504,11 +549,12 @@ void launch_int_mv_batched(const DevWeight& w, const int8_t* q8x, const float* q
         const int8_t* xq = q8x + done * w.cols;
         const float* xs = q8s + done * nb;
         float* o = out + done * w.rows;
+        float* o2 = w2 ? out2 + done * w.rows : nullptr;
         switch (kern) {
-            case 8: launch_int_mv<FMT, 8>(w, xq, xs, o, take, s); break;
-            case 4: launch_int_mv<FMT, 4>(w, xq, xs, o, take, s); break;
-            case 2: launch_int_mv<FMT, 2>(w, xq, xs, o, take, s); break;
-            default: launch_int_mv<FMT, 1>(w, xq, xs, o, take, s); break;
+            case 8: launch_int_mv<FMT, 8>(w, xq, xs, o, take, s, w2, o2); break;
+            case 4: launch_int_mv<FMT, 4>(w, xq, xs, o, take, s, w2, o2); break;
+            case 2: launch_int_mv<FMT, 2>(w, xq, xs, o, take, s, w2, o2); break;
+            default: launch_int_mv<FMT, 1>(w, xq, xs, o, take, s, w2, o2); break;
         }
         done += take;
     }
@@ -519,6 +565,13 @@ void launch_int_mv_batched(const DevWeight& w, const int8_t* q8x, const float* q
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, size_t m,
                         hipStream_t s) {
     launch_int_mv_batched<LARQL_Q4_0>(w, q8x, q8s, out, m, s);
+}
+
+void launch_q4_0_matvec_pair(const DevWeight& w1, const DevWeight& w2, const int8_t* q8x, const float* q8s,
+                             float* out1, float* out2, size_t m, hipStream_t s) {
+    if (w1.format != LARQL_Q4_0 || w2.format != LARQL_Q4_0 || w1.rows != w2.rows || w1.cols != w2.cols)
+        fail(LARQL_HIP_ERR_INVALID, "q4_0 matvec pair: two Q4_0 matrices of one shape");
+    launch_int_mv_batched<LARQL_Q4_0>(w1, q8x, q8s, out1, m, s, &w2, out2);
 }
 
 // ── Q4_0 weights x f32 activation ─────────────────────────────────────────

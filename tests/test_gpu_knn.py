@@ -154,6 +154,32 @@ def test_topk_mass_ties_linear_time(hip, signed):
                 np.testing.assert_array_equal(gv[r].view(np.uint32), rv.view(np.uint32))
 
 
+@pytest.mark.parametrize("signed", [False, True])
+def test_topk_wave_rows_every_path(hip, signed):
+    """Rows with k <= 64 and n <= 14336 take one wave per row: row lengths that fill the
+    lane registers exactly (4096, 10240, 14336) or leave a partial last register (40, 65,
+    4097, 10241), five rows per launch (a partial last workgroup of four rows), and rows
+    whose candidate list overflows (600 equal largest values; an all-zero row), which
+    select over the whole row again."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(53)
+    for n in (40, 65, 4096, 4097, 10240, 10241, 14336):
+        rows = rng.standard_normal((5, n)).astype(np.float32)
+        rows[1, rng.choice(n, min(n, 600), replace=False)] = 7.0    # > 512 tied candidates
+        rows[2] = 0.0
+        rows[3, ::5] = -rows[3, ::5]                                   # equal magnitudes
+        rows[3, 1::5] = rows[3, ::5][: rows[3, 1::5].size]
+        for k in (1, 7, 32, 64):
+            if k > n:
+                continue
+            print(f"[topk wave] n={n} k={k} signed={signed}", flush=True)
+            gi, gv = _topk_rows(hip, torch, rows, k, signed)
+            for r in range(rows.shape[0]):
+                ri, rv = (oracle.topk_signed if signed else oracle.topk_abs)(rows[r], k)
+                np.testing.assert_array_equal(gi[r], ri, err_msg=f"n={n} k={k} row={r}")
+                np.testing.assert_array_equal(gv[r].view(np.uint32), rv.view(np.uint32))
+
+
 def test_topk_k_above_row_length_is_clamped(hip):
     """top_k.min(len) (LV/src/index/walk.rs:569): a request for more entries than the row has
     returns the whole row ranked; the slots past it hold index 0xFFFFFFFF and score 0."""
