@@ -180,10 +180,13 @@ def test_q8_matvec_ragged_bit_exact(hip, m, rows, cols):
         assert np.array_equal(got[i].view(np.uint32), ref.view(np.uint32)), i
 
 
-@pytest.mark.parametrize("m,rows,cols", [(3, 1000, 2560), (8, 33, 160)])
+@pytest.mark.parametrize("m,rows,cols", [(3, 1000, 2560), (2, 17, 64), (11, 1000, 2560), (9, 300, 4096),
+                                         (5, 64, 4096), (8, 33, 160)])
 def test_q4_0_matvec_batched_dev_bit_exact(hip, m, rows, cols):
     """Q4_0 x Q8 over several activation rows through the device entry point: each row
-    equals the single-row block-integer order."""
+    equals the single-row block-integer order.  Passes of up to 8 rows (11 rows: 8 + 3;
+    9 rows: 8 + 1), a partial workgroup of rows (17), hidden 64 .. 4096, and an odd block
+    count (8, 33, 160)."""
     torch = pytest.importorskip("torch")
     print(f"[q4_0 batched] m={m} rows={rows} cols={cols}", flush=True)
     q = weights("q4_0", rows, cols, seed=520 + rows)

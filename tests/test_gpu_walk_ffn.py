@@ -98,7 +98,11 @@ def test_vecmat_dev_matches_host_entry(hip):
     assert np.array_equal(dev.view(np.uint32), host.view(np.uint32))   # same kernels, same order
 
 
-@pytest.mark.parametrize("seq,rows,hidden", [(6, 10240, 2560), (1, 64, 32), (9, 300, 544)])
+# (6, 10240, 2560), (17, 300, 576), (130, 200, 128): several positions (one launch per pass of
+# up to 8, ragged row tiles); (1, 64, 32): one position; (9, 300, 544): hidden not a multiple
+# of 64
+@pytest.mark.parametrize("seq,rows,hidden", [(6, 10240, 2560), (17, 300, 576), (130, 200, 128), (1, 64, 32),
+                                             (9, 300, 544)])
 def test_pair_batch_bit_exact(hip, seq, rows, hidden):
     print(f"[pair batch] seq={seq} rows={rows} hidden={hidden}", flush=True)
     gate = oracle.quantize_q4_0(oracle.gauss(41 + seq, rows * hidden, 0.0, 0.02))
