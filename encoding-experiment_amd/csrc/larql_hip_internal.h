@@ -73,12 +73,10 @@ struct DevWeight {
     void* base = nullptr;    // one device allocation holding all sub-arrays
     size_t bytes = 0;
     // sub-array pointers into `base`
-    uint8_t* qs = nullptr;   // Q4_K/Q4_0 nibbles, Q6_K ql, Q8_0 int8
-    uint8_t* qh = nullptr;   // Q6_K high bits
-    int8_t* sc = nullptr;    // Q6_K scales
+    uint8_t* qs = nullptr;   // Q4_K/Q4_0 nibbles, Q6_K tile-major blocks (q6k_block), Q8_0 int8
     uint4* hdr = nullptr;    // Q4_K / Q4_KF headers
     int hf = 0;              // Q4_K-family header form: kHdr148, kHdrGguf or kHdrKf160
-    void* d = nullptr;       // Q6_K/Q4_0 f16 scales, Q8_0 f32 scales
+    void* d = nullptr;       // Q4_0 f16 scales, Q8_0 f32 scales
     // registry keys
     const void* host_ptr = nullptr;
     size_t host_len = 0;
@@ -119,6 +117,21 @@ __host__ __device__ inline size_t q4k_sub_offset(size_t row, size_t sb, int j, s
 }
 __host__ __device__ inline size_t q4k_hdr_index(size_t row, size_t sb, size_t S) {
     return ((row >> 4) * S + sb) * 16 + (row & 15);
+}
+
+// Q6_K device layout: one 3360-byte block per (16-row tile, super-block), in tile-major
+// order (tile t, super-block sb at index t S + sb): [ql 2048][qh 1024][scales 256][d 32].
+// Row c (0..15) of the tile, lane group g (0..3) = elements 64 g .. 64 g + 63:
+//   ql bytes 32 g + 16 h .. + 15 (h = 0, 1)  at h * 1024 + (16 g + c) * 16,
+//   qh group words 4 g .. 4 g + 3             at 2048 + (16 g + c) * 16
+//     (word j: element 16 j + 8 w + 2 i + p at bits 8 i + 4 w + 2 p),
+//   int8 scales 4 g .. 4 g + 3                at 3072 + (16 g + c) * 4,
+//   f16 d                                     at 3328 + 2 c,
+// so the load of one part by the 64 lanes (16 g + c) of a wave is one contiguous span.
+constexpr size_t kQ6Block = 3360;
+constexpr size_t kQ6Qh = 2048, kQ6Sc = 3072, kQ6D = 3328;
+__host__ __device__ inline size_t q6k_block(size_t row, size_t sb, size_t S) {
+    return ((row >> 4) * S + sb) * kQ6Block;
 }
 
 // Compute units of the current device (queried once per device, then cached).

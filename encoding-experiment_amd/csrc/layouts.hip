@@ -4,6 +4,7 @@
 //   Q4_0  18 B / 32  : [f16 scale][16 B nibbles]                              (:50-81)
 //   Q4_K 148 B / 256 : [f16 d][f16 dmin][12 B sc (0..7 used)][4 B mins][128 B]  (:104-170)
 //   Q6_K 210 B / 256 : [128 B ql][64 B qh][16 x i8 scales][f16 d]              (:179-239)
+//                      (device: 3360-byte blocks per 16-row tile and super-block, q6k_block)
 //   Q8_0 trait form  : i8 [rows*cols] + f32 scales [rows*cols/32]          (LC/src/pipeline.rs:22-27)
 //   Q4_KF 144 B / 256: llama.cpp GGUF block [f16 d][f16 dmin][12 B packed 6-bit scales and
 //                      mins][128 B: chunk c of 32 bytes = sub-block 2c low, 2c+1 high
@@ -34,9 +35,7 @@ size_t dev_layout_bytes(int format, size_t rows, size_t cols, int hf) {
         case LARQL_Q4_0: return align256(rows * cols / 2) + align256(rows * (cols / 32) * 2);
         case LARQL_Q4_K: return align256(rows * cols / 2) + align256(rows * (cols / 256) * 16);
         case LARQL_Q4_KF: return align256(rows * cols / 2) + align256(rows * (cols / 256) * (hf == kHdrKf160 ? 32 : 16));
-        case LARQL_Q6_K:
-            return align256(rows * cols / 2) + align256(rows * cols / 4) + align256(rows * cols / 16) +
-                   align256(rows * (cols / 256) * 2);
+        case LARQL_Q6_K: return align256(rows * (cols / 256) * 210);  // rows % 16 == 0: kQ6Block per tile
         case LARQL_Q8_0: return align256(rows * cols) + align256(rows * (cols / 32) * 4);
         case LARQL_F32: return align256(rows * cols * 4);
         default: return 0;
@@ -56,11 +55,8 @@ void dev_layout_carve(DevWeight& w) {
             w.qs = p; p += align256(R * K / 2);
             w.hdr = reinterpret_cast<uint4*>(p);
             break;
-        case LARQL_Q6_K:
-            w.qs = p; p += align256(R * K / 2);
-            w.qh = p; p += align256(R * K / 4);
-            w.sc = reinterpret_cast<int8_t*>(p); p += align256(R * K / 16);
-            w.d = p;
+        case LARQL_Q6_K:  // tile-major blocks (q6k_block)
+            w.qs = p;
             break;
         case LARQL_Q8_0:
             w.qs = p; p += align256(R * K);
@@ -159,33 +155,37 @@ __global__ void repack_q4kf160_kernel(const uint32_t* __restrict__ raw, uint8_t*
             make_uint4(s[8 + 4 * j], s[9 + 4 * j], s[10 + 4 * j], s[11 + 4 * j]);
 }
 
-// One thread per Q6_K super-block (210-byte stride: 2-byte aligned source).  The
-// 64 qh bytes (element e at byte e/4, bits 2*(e%4)) are regrouped into 16 words, one
-// per 16-element group g: element 16g + 8w + 2j + p goes to bits 8j + 4w + 2p.
-__global__ void repack_q6k_kernel(const uint16_t* __restrict__ raw, uint8_t* __restrict__ ql,
-                                  uint8_t* __restrict__ qh, int8_t* __restrict__ sc,
-                                  uint16_t* __restrict__ d, size_t nblocks, size_t bpr, size_t row0, size_t stride) {
+// One thread per Q6_K super-block (210-byte stride: 2-byte aligned source) into its row
+// of the tile-major block (q6k_block).  The 64 qh bytes (element e at byte e/4, bits
+// 2*(e%4)) are regrouped into 16 words, one per 16-element group j: element 16j + 8w +
+// 2i + p goes to bits 8i + 4w + 2p.
+__global__ void repack_q6k_kernel(const uint16_t* __restrict__ raw, uint8_t* __restrict__ blocks,
+                                  size_t nblocks, size_t bpr, size_t row0, size_t stride) {
     size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
     const uint16_t* s = raw + b * 105;
     const size_t o = dst_block(b, bpr, row0, stride);
-    uint16_t* l = reinterpret_cast<uint16_t*>(ql + o * 128);
-    uint32_t* h = reinterpret_cast<uint32_t*>(qh + o * 64);
-    uint16_t* c = reinterpret_cast<uint16_t*>(sc + o * 16);
-    for (int i = 0; i < 64; i++) l[i] = s[i];
-    for (int g = 0; g < 16; g++) {
-        // source: 16 elements = 4 bytes = u16 words s[64 + 2g] and s[64 + 2g + 1]
-        const uint32_t src = static_cast<uint32_t>(s[64 + 2 * g]) | (static_cast<uint32_t>(s[64 + 2 * g + 1]) << 16);
+    const size_t row = o / bpr, sb = o - row * bpr, c = row & 15;
+    uint8_t* blk = blocks + q6k_block(row, sb, bpr);
+    for (int g = 0; g < 4; g++)
+        for (int h = 0; h < 2; h++) {
+            uint16_t* l = reinterpret_cast<uint16_t*>(blk + h * 1024 + (16 * g + c) * 16);
+            for (int i = 0; i < 8; i++) l[i] = s[16 * g + 8 * h + i];
+        }
+    for (int j = 0; j < 16; j++) {
+        // source: 16 elements = 4 bytes = u16 words s[64 + 2j] and s[64 + 2j + 1]
+        const uint32_t src = static_cast<uint32_t>(s[64 + 2 * j]) | (static_cast<uint32_t>(s[64 + 2 * j + 1]) << 16);
         uint32_t dst = 0;
         for (int e = 0; e < 16; e++) {
             const uint32_t v = (src >> (2 * e)) & 3u;
-            const int w = e >> 3, j = (e & 7) >> 1, p = e & 1;
-            dst |= v << (8 * j + 4 * w + 2 * p);
+            const int w = e >> 3, i = (e & 7) >> 1, p = e & 1;
+            dst |= v << (8 * i + 4 * w + 2 * p);
         }
-        h[g] = dst;
+        *reinterpret_cast<uint32_t*>(blk + kQ6Qh + (16 * (j >> 2) + c) * 16 + 4 * (j & 3)) = dst;
     }
-    for (int i = 0; i < 8; i++) c[i] = s[96 + i];
-    d[o] = s[104];
+    for (int k = 0; k < 8; k++)  // scales 2k, 2k + 1
+        *reinterpret_cast<uint16_t*>(blk + kQ6Sc + (16 * (k >> 1) + c) * 4 + 2 * (k & 1)) = s[96 + k];
+    *reinterpret_cast<uint16_t*>(blk + kQ6D + 2 * c) = s[104];
 }
 
 // One thread per Q4_0 block (18-byte stride: 2-byte aligned source).
@@ -226,8 +226,7 @@ void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scale
         case LARQL_Q6_K: {
             const size_t bpr = w.cols / 256, nb = src_rows * bpr;
             repack_q6k_kernel<<<dim3((nb + T - 1) / T), dim3(T), 0, s>>>(
-                reinterpret_cast<const uint16_t*>(raw), w.qs, w.qh, w.sc, static_cast<uint16_t*>(w.d), nb, bpr,
-                row0, stride);
+                reinterpret_cast<const uint16_t*>(raw), w.qs, nb, bpr, row0, stride);
             break;
         }
         case LARQL_Q4_0: {

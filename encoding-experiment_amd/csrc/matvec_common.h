@@ -1,5 +1,5 @@
-// Shared pieces of the Q4_K / Q6_K matvec kernels: launch arguments, the fused
-// RMSNorm prologue, the multi-row wave reduction and the epilogues.
+// Shared pieces of the Q4_K / Q6_K matvec kernels: launch arguments, the wave reductions
+// and the epilogues.
 #pragma once
 
 #include "device_common.h"
@@ -16,11 +16,8 @@ enum MvEpi : int {
 
 struct MvArgs {
     // weight (device layout)
-    const uint8_t* qs = nullptr;   // Q4_K nibbles / Q6_K ql
+    const uint8_t* qs = nullptr;   // Q4_K nibbles / Q6_K tile-major blocks
     const uint4* hdr = nullptr;    // Q4_K headers
-    const uint8_t* qh = nullptr;   // Q6_K high bits
-    const int8_t* sc = nullptr;    // Q6_K scales
-    const uint16_t* d = nullptr;   // Q6_K f16 super-block scales
     int rows = 0, cols = 0;
     // activation / output
     const float* x = nullptr;
@@ -46,9 +43,9 @@ struct MvArgs {
     double* psum = nullptr;
     const double* x_psum = nullptr;
     int x_npsum = 0;
-    // launch shape: waves per row slot, row tiles, tiles per workgroup, CUs on the device,
-    // device rows (a multiple of 64; rows past `rows` decode to zero)
-    int wpr = 1, tiles = 0, steps = 1, num_cus = 0, rows_pad = 0;
+    // launch shape: rounds per wave, CUs on the device, device rows (a multiple of 64;
+    // rows past `rows` decode to zero)
+    int steps = 1, num_cus = 0, rows_pad = 0;
 };
 
 // Transposing reduction across 32- and 16-lane halves (gfx950 permlane swaps): after
@@ -66,55 +63,8 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
-constexpr int DPP_ROW_MIRROR = 0x140;       // lane i <- 15 - i within 16 lanes
-constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i <- 7 - i within 8 lanes
-constexpr int DPP_QUAD_REV = 0x1B;          // quad_perm [3,2,1,0]
-constexpr int DPP_QUAD_SWAP = 0xB1;         // quad_perm [1,0,3,2]
-constexpr int DPP_QUAD_1032 = DPP_QUAD_SWAP;
-constexpr int DPP_QUAD_2301 = 0x4E;         // quad_perm [2,3,0,1]
-
-// Reduce RB per-lane partials (RB <= 8) over the 64 lanes of a wave; on return lane
-// (r << (6 - log2 RB)) holds the total of row r (every lane of that 64/RB block does).
-// Each halving step keeps RB/2 registers: rows of the lower half-block in the lower
-// lanes, rows of the upper half-block in the upper lanes.
-template <int RB>
-__device__ __forceinline__ float multi_row_reduce(float (&v)[RB], int lane) {
-    static_assert(RB == 1 || RB == 2 || RB == 4 || RB == 8, "RB must be 1, 2, 4 or 8");
-    float w[4];
-    if constexpr (RB >= 2) {
-#pragma unroll
-        for (int i = 0; i < RB / 2; i++) w[i] = swap32_add(v[i], v[i + RB / 2]);
-    } else {
-        w[0] = swap32_add(v[0], v[0]);
-    }
-    constexpr int n32 = RB >= 2 ? RB / 2 : 1;
-    float u[2];
-    if constexpr (n32 >= 2) {
-#pragma unroll
-        for (int i = 0; i < n32 / 2; i++) u[i] = swap16_add(w[i], w[i + n32 / 2]);
-    } else {
-        u[0] = swap16_add(w[0], w[0]);
-    }
-    constexpr int n16 = n32 >= 2 ? n32 / 2 : 1;
-    float t;
-    if constexpr (n16 == 2) {
-        const bool upper = (lane & 8) != 0;
-        const float keep = upper ? u[1] : u[0];
-        const float send = upper ? u[0] : u[1];
-        t = keep + dpp_f<DPP_ROW_MIRROR>(send);
-    } else {
-        t = u[0] + dpp_f<DPP_ROW_MIRROR>(u[0]);
-    }
-    t += dpp_f<DPP_ROW_HALF_MIRROR>(t);
-    t += dpp_f<DPP_QUAD_REV>(t);
-    t += dpp_f<DPP_QUAD_SWAP>(t);
-    return t;
-}
-
-template <int RB>
-__device__ __forceinline__ constexpr int rb_shift() {
-    return RB == 1 ? 6 : RB == 2 ? 5 : RB == 4 ? 4 : 3;
-}
+constexpr int DPP_QUAD_1032 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_2301 = 0x4E;  // quad_perm [2,3,0,1]
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
     const float sig = 1.0f / (1.0f + expf(-g));
@@ -132,49 +82,11 @@ __device__ __forceinline__ float gated_act(int act, float g, float u) {
     return act == 1 ? gelu_tanh_mul(g, u) : silu_mul(g, u);
 }
 
-// Sum over the wpr waves of one row slot through LDS (scratch of >= nwaves doubles).
-__device__ __forceinline__ double slot_sum_d(double v, double* scratch, int wave, int slot, int wpr, int lane) {
-    v = wave_sum_d(v);
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    double s = 0.0;
-    for (int w = 0; w < wpr; w++) s += scratch[slot * wpr + w];
-    __syncthreads();
-    return s;
-}
-
 // Output of a non-pair epilogue for a row whose dot is `tot` and resid value `rv`.
 __device__ __forceinline__ float epi_value(const MvArgs& a, float rv, float tot) {
     if (a.epi == EPI_RESID) return (rv + tot) * a.out_scale;
     if (a.epi == EPI_GATED_MUL) return gated_act(a.act, rv, tot);
     return tot;
-}
-
-// Epilogue for a totals vector after the wave reduction.  `tot` is valid in lane
-// (r << rsh) for row row0 + r.  Used when the slot is a single wave.
-template <int RB>
-__device__ __forceinline__ void epilogue_wave(const MvArgs& a, float tot, int lane, int row0) {
-    constexpr int rsh = rb_shift<RB>();
-    const int r = lane >> rsh;
-    const bool owner = (lane & ((1 << rsh) - 1)) == 0;
-    const int row = row0 + r;
-    if (a.epi == EPI_GATED_PAIR) {
-        const float up = __shfl_down(tot, 1 << rsh, 64);
-        if (owner && (r & 1) == 0 && row < a.rows) a.out[row >> 1] = gated_act(a.act, tot, up);
-    } else if (owner && row < a.rows) {
-        a.out[row] = epi_value(a, a.epi == EPI_STORE ? 0.f : a.resid[row], tot);
-    }
-}
-
-// Epilogue when lanes 0..RB-1 hold rows row0 + lane (multi-wave slots).
-__device__ __forceinline__ void epilogue_lanes(const MvArgs& a, float tot, int lane, int row0, int rb) {
-    const int row = row0 + lane;
-    if (a.epi == EPI_GATED_PAIR) {
-        const float up = __shfl_down(tot, 1, 64);
-        if (lane < rb && (lane & 1) == 0 && row < a.rows) a.out[row >> 1] = gated_act(a.act, tot, up);
-    } else if (lane < rb && row < a.rows) {
-        a.out[row] = epi_value(a, a.epi == EPI_STORE ? 0.f : a.resid[row], tot);
-    }
 }
 
 // Load N floats starting at base[c0] (N % 4 == 0, 16-byte aligned); zeros when !valid.
@@ -192,9 +104,10 @@ __device__ __forceinline__ void load_slice(const float* __restrict__ base, int c
 }
 
 void launch_mv(const DevWeight& w, MvArgs a, hipStream_t s);
-bool stream_mv_supported(const DevWeight& w);
-void launch_mv_stream(const DevWeight& w, MvArgs a, hipStream_t s);
 void launch_q4k_mfma(const DevWeight& w, MvArgs a, hipStream_t s);
+// Q6_K on the matrix cores (matvec_q6k_mfma.hip); no prenormed input or second output.
+bool q6k_mfma_supported(const DevWeight& w);
+void launch_q6k_mfma(const DevWeight& w, MvArgs a, hipStream_t s);
 // Workgroups of launch_q4k_mfma for this weight (the partial sums a producer writes), and
 // the most partial sums its launch can take as a consumer (two per thread).
 int q4k_mfma_groups(const DevWeight& w, int num_cus);

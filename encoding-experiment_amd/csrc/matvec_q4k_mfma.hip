@@ -34,6 +34,7 @@
 
 #include "kquant_levels.h"
 #include "matvec_common.h"
+#include "mfma_planes.h"
 
 
 namespace larql {
@@ -42,41 +43,15 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// One sub-block's planes in LDS: [MFMA half m][plane p] x 16 bytes, then
-// {s', 65536 s', sum x, 0}.  Within a unit, sub-block j sits in slot 2 (j % 4) + j / 4,
-// so the two sub-blocks of a lane (g and g + 4) are adjacent.
-struct PlSlot {
-    uint4 pl[2][3];
-    float4 s;
-};
-static_assert(sizeof(PlSlot) == 112, "LDS plane slot");
-
+// Within a unit, sub-block j's planes (mfma_planes.h) sit in slot 2 (j % 4) + j / 4, so
+// the two sub-blocks of a lane (g and g + 4) are adjacent; the slot's float4 is
+// {s', 65536 s', sum x, 0}.
 constexpr int kZeroBytes = 256;  // per-wave zero area read by the idle A lanes (offsets < 176)
 constexpr int kMaxKS = 16;
 
 template <int UR>
 __host__ __device__ constexpr int wave_lds_bytes() {
     return kZeroBytes + 8 * UR * static_cast<int>(sizeof(PlSlot));
-}
-
-// Byte b (b = 0, 1, 2) of each of u0..u3 -> dword b, top bits flipped: the signed digit
-// planes of four elements, low to high.
-__device__ __forceinline__ void pack_planes(uint32_t u0, uint32_t u1, uint32_t u2, uint32_t u3, uint32_t (&pl)[3]) {
-    const uint32_t p01 = __builtin_amdgcn_perm(u1, u0, 0x05010400u);  // u0.b0 u1.b0 u0.b1 u1.b1
-    const uint32_t q01 = __builtin_amdgcn_perm(u1, u0, 0x0C0C0602u);  // u0.b2 u1.b2 0 0
-    const uint32_t p23 = __builtin_amdgcn_perm(u3, u2, 0x05010400u);
-    const uint32_t q23 = __builtin_amdgcn_perm(u3, u2, 0x0C0C0602u);
-    pl[0] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;
-    pl[1] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
-    pl[2] = __builtin_amdgcn_perm(q23, q01, 0x05040100u) ^ 0x80808080u;
-}
-
-// Weight bytes are read exactly once: non-temporal loads keep them from displacing x and
-// the planes in the caches (measured: 8.4 -> 7.9 us on [14336 x 4096]).
-__device__ __forceinline__ uint4 load_nt(const void* p) {
-    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-    const v4u v = __builtin_nontemporal_load(static_cast<const v4u*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // Nibble dword (element 2i in the low, 2i + 1 in the high nibble of byte i) -> bytes of

@@ -415,15 +415,13 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
         }
 }
 
-// Q6_K weights (ql nibble of element e at byte e / 2, its two high bits regrouped per
-// 16-element group G: element 16 G + 8 w + 2 j + p at bits 8 j + 4 w + 2 p of word G; int8
-// scale per group; f16 d per block) with the f32 kernel's X staging and tiling: lane (g, c)
-// of unit (sb, h) takes elements 32 (4h + g) .. + 31 of row c of each tile, i.e. 16 ql
-// bytes, two high-bit words and two scales; w = fma(q, d sc, -32 d sc) = d sc (q - 32).
-__global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* __restrict__ ql,
-                                                                const uint8_t* __restrict__ qh,
-                                                                const int8_t* __restrict__ scl,
-                                                                const uint16_t* __restrict__ dd,
+// Q6_K weights (tile-major blocks, q6k_block in larql_hip_internal.h: ql nibble of element
+// e at byte e / 2, its two high bits regrouped per 16-element group G: element 16 G + 8 w +
+// 2 j + p at bits 8 j + 4 w + 2 p of word G; int8 scale per group; f16 d per block) with
+// the f32 kernel's X staging and tiling: lane (g, c) of unit (sb, h) takes elements
+// 32 (4h + g) .. + 31 of row c of each tile, i.e. 16 ql bytes, two high-bit words and two
+// scales; w = fma(q, d sc, -32 d sc) = d sc (q - 32).
+__global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* __restrict__ q6,
                                                                 const float* __restrict__ X, float* __restrict__ Y,
                                                                 int M, int N, int K, int sb_per, int ldy) {
     __shared__ float As[2][kMt][64][kF32Pitch];
@@ -434,9 +432,16 @@ __global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* _
     const int nt0 = (blockIdx.x * kWaves + wave) * kNT;
     const int u0 = 2 * static_cast<int>(blockIdx.z) * sb_per, u1 = min(2 * S, u0 + 2 * sb_per), last = u1 - 1;
     Y += static_cast<size_t>(blockIdx.z) * M * ldy;
-    size_t blk[kNT];  // first block of the lane's row in tile j (rows past N re-read row N - 1)
+    // the lane's row in tile j (rows past N re-read row N - 1): its tile's first block and
+    // its offset in each part of a block (lane group gq = 2h + g / 2 of the unit's half h)
+    size_t blk[kNT];
+    uint32_t rc[kNT];
 #pragma unroll
-    for (int j = 0; j < kNT; j++) blk[j] = static_cast<size_t>(min((nt0 + j) * 16 + c, N - 1)) * S;
+    for (int j = 0; j < kNT; j++) {
+        const size_t row = static_cast<size_t>(min((nt0 + j) * 16 + c, N - 1));
+        blk[j] = q6k_block(row, 0, S);
+        rc[j] = static_cast<uint32_t>(row & 15);
+    }
     const int xr_row = (mt0 + (tid >> 6)) * 16 + (lane & 15);
     const bool xr_ok = xr_row < M;
     const float* xrow = X + static_cast<size_t>(min(xr_row, M - 1)) * K + 32 * g;
@@ -459,14 +464,15 @@ __global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* _
         uint32_t sd[kNT];  // scales of groups G0, G0 + 1 | d << 16
     };
     auto load_w = [&](int u, Wu& w) __attribute__((always_inline)) {
-        const int G0 = 8 * (u & 1) + 2 * g;
+        const uint32_t gq = 2 * (u & 1) + (g >> 1), g1 = g & 1;
 #pragma unroll
         for (int j = 0; j < kNT; j++) {
-            const size_t o = blk[j] + (u >> 1);
-            w.l[j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(ql + o * 128 + 64 * (u & 1) + 16 * g));
-            w.h[j] = *reinterpret_cast<const uint2*>(qh + o * 64 + 4 * G0);
-            w.sd[j] = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(scl + o * 16 + G0)) |
-                      (static_cast<uint32_t>(dd[o]) << 16);
+            const uint8_t* b = q6 + blk[j] + static_cast<size_t>(u >> 1) * kQ6Block;
+            const uint32_t lc = 16 * gq + rc[j];
+            w.l[j] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(b + g1 * 1024 + lc * 16));
+            w.h[j] = *reinterpret_cast<const uint2*>(b + kQ6Qh + lc * 16 + 8 * g1);
+            w.sd[j] = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(b + kQ6Sc + lc * 4 + 2 * g1)) |
+                      (static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(b + kQ6D + 2 * rc[j])) << 16);
         }
     };
     floatx4 acc[kMt][kNT];
@@ -597,8 +603,8 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
             static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per, ld_out);
     else
         q6k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(
-            w.qs, w.qh, w.sc, static_cast<const uint16_t*>(w.d), X, sp.splits > 1 ? part : Y, static_cast<int>(m),
-            static_cast<int>(w.rows), static_cast<int>(w.cols), sp.sb_per, ld_out);
+            w.qs, X, sp.splits > 1 ? part : Y, static_cast<int>(m), static_cast<int>(w.rows), static_cast<int>(w.cols),
+            sp.sb_per, ld_out);
     LARQL_HIP_CHECK(hipGetLastError());
     if (sp.splits > 1) {
         const size_t n = m * w.rows;
