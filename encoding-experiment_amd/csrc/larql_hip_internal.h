@@ -13,13 +13,9 @@
 //     hdr : u32x4 [rows/16][S][16]      {d|dmin<<16, sc[0..3], sc[4..7], min bytes}
 //   so that one wave-wide 16-byte load of a (tile, super-block) reads 1 KB of
 //   contiguous memory (the matrix-core matvec's B operand, one sub-block per lane).
-//   Q6_K (210 B / 256):
-//     ql  : u8 [rows][S*128]      low nibbles (reference order)
-//     qh  : u32 [rows][S*16]      high 2-bit pairs, regrouped per 16 elements: for
-//                                 element 8w + 2j + p of a 16-element group (w, p in
-//                                 {0,1}), bits 8j + 4w + 2p of the group's word
-//     sc  : i8 [rows][S*16]       sub-block scales
-//     d   : f16 [rows][S]         super-block scale
+//   Q6_K (210 B / 256), tile-major over 16-row tiles: one 3360-byte block per
+//     (tile, super-block) holding its 16 rows' ql, regrouped qh, scales and d
+//     (q6k_block below gives the block's offset and its internal layout)
 //   Q4_0 (18 B / 32):
 //     qs  : u8 [rows][B*16]       nibble bytes
 //     d   : f16 [rows][B]         block scale
