@@ -515,8 +515,8 @@ def bench_configs(be, torch, stream, copies: int):
     us = _graph_us(torch, stream,
                    lambda i: be.pair_batch_dev(hs[i % copies], hs[(i + 1) % copies], xs6, seq, g6, u6, stream=stream), 64)
     hbm("q4_0_pair_batch_6x10240x2560", 2 * (N * K // 32 * 18) + seq * K * 4 + 2 * seq * N * 4, us,
-        {"launches": 3, "timing": "HIP graph replay of 64 calls",
-         "note": "quantize 6 rows + gate and up Q4_0 matvecs over all 6 rows (one pass each)"})
+        {"launches": 2, "timing": "HIP graph replay of 64 calls",
+         "note": "quantize 6 rows, then the gate and up Q4_0 matvecs over all 6 rows in one launch"})
     for h in hs:
         be.release_weight(h)
 
