@@ -97,6 +97,59 @@ def test_gate_knn_q4_fuzzed_bytes(hip):
     np.testing.assert_array_equal(got[1].view(np.uint32), ref_v.view(np.uint32))
 
 
+def _q4_scores(hip, torch, q4, queries, features, hidden):
+    h = hip.register_weight(larql_hip.Q4_0, q4, features, hidden)
+    try:
+        nq = queries.shape[0]
+        dq = torch.from_numpy(np.ascontiguousarray(queries, dtype=np.float32)).cuda()
+        ds = torch.empty(nq * features, device="cuda", dtype=torch.float32)
+        hip.gate_scores_dev([h], dq, nq, ds)
+        hip.synchronize()
+        return ds.cpu().numpy().reshape(nq, features)
+    finally:
+        hip.release_weight(h)
+
+
+def _q4_scores_ref(q4, queries, features, hidden):
+    out = []
+    for q in queries:
+        q8, q8s = oracle.quantize_to_q8(q)
+        out.append(oracle.q4_0_matvec_blockint(q4, q8, q8s, features, hidden))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("features,hidden,nq", [(200, 192, 257), (130, 2560, 33), (16, 64, 1), (1000, 512, 129)])
+def test_gate_scores_q4_bit_exact(hip, features, hidden, nq):
+    """Every score: hidden sizes of an odd number of block pairs, partial feature tiles,
+    query counts off the 8-query groups and the 16-group tiles."""
+    torch = pytest.importorskip("torch")
+    print(f"[knn q4 scores] F={features} K={hidden} nq={nq}", flush=True)
+    q4 = oracle.quantize_q4_0(oracle.gauss(61, features * hidden, 0.0, 0.02))
+    queries = oracle.gauss(62, nq * hidden).reshape(nq, hidden)
+    got = _q4_scores(hip, torch, q4, queries, features, hidden)
+    ref = _q4_scores_ref(q4, queries, features, hidden)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("nibble", [0x00, 0xFF, 0x0F])
+def test_gate_scores_q4_extreme_codes(hip, nibble):
+    """Block dots at their largest magnitudes: every code 0 or 15 against queries whose
+    int8 values are all +-127 (constant rows and alternating signs); the int32 dots and
+    their conversion to f32 are exact there."""
+    torch = pytest.importorskip("torch")
+    features, hidden = 48, 2560
+    print(f"[knn q4 extreme] nibble byte {nibble:#x}", flush=True)
+    blocks = np.zeros((features * hidden // 32, 18), dtype=np.uint8)
+    blocks[:, 2:] = nibble
+    blocks[:, 0:2] = np.frombuffer(np.full(blocks.shape[0], 0.03, dtype=np.float16).tobytes(), np.uint8).reshape(-1, 2)
+    q4 = blocks.reshape(-1)
+    queries = np.stack([np.full(hidden, 1.0), np.full(hidden, -2.5), np.tile([3.0, -3.0], hidden // 2),
+                        oracle.gauss(63, hidden)]).astype(np.float32)
+    got = _q4_scores(hip, torch, q4, queries, features, hidden)
+    ref = _q4_scores_ref(q4, queries, features, hidden)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def _topk_rows(hip, torch, rows, k, signed):
     n = rows.shape[1]
     ds = torch.from_numpy(np.ascontiguousarray(rows, dtype=np.float32)).cuda()
