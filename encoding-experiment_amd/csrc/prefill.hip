@@ -147,36 +147,43 @@ __global__ __launch_bounds__(kShThreads) void q4k_gemm_shared_kernel(const uint8
         qo[jj] = __builtin_amdgcn_readfirstlane(t * S * 2048u + 4u * step);
         ho[jj] = __builtin_amdgcn_readfirstlane(t * S * 256u);
     }
-    // every load is a wave-uniform base plus the lane's byte offset (scalar base, vector offset)
+    // Every load is a raw buffer load: the wave-uniform part of the offset in the scalar
+    // operand, the lane's byte offset in the vector operand, so no vector ALU goes to
+    // addresses.  All offsets are in range (tiles clamped, units below n).
     const uint32_t lo16 = lane * 16u, lc16 = c * 16u;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(qs), 0, static_cast<int>(static_cast<uint32_t>(ntiles) * S * 2048u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<v4u*>(hdr), 0, static_cast<int>(static_cast<uint32_t>(ntiles) * S * 256u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<v4u*>(XP), 0, static_cast<int>(static_cast<uint32_t>(mtiles) * n * 4096u), 0x00020000);
     // A tile i of this wave: XP[(mt n + u) 256 + s 64 + lane], mt clamped into the packed X
     // (tiles past it hold tokens >= M, whose rows are not stored)
-    size_t xo[kShMt];
+    uint32_t xo[kShMt];
 #pragma unroll
-    for (int i = 0; i < kShMt; i++) xo[i] = static_cast<size_t>(min(mtw + i, mtiles - 1)) * n * 256;
+    for (int i = 0; i < kShMt; i++)
+        xo[i] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(min(mtw + i, mtiles - 1)) * n * 4096u);
 
     struct Au {
         v4u v[kShMt][4];  // [tile][k-step]
     };
-    auto load_a = [&](int u, Au& a) __attribute__((always_inline)) {
+    auto load_a = [&a_rs = rx, &xo, lo16](int u, Au& a) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < kShMt; i++) {
-            const uint8_t* base = reinterpret_cast<const uint8_t*>(XP + xo[i] + static_cast<size_t>(u) * 256);
+        for (int i = 0; i < kShMt; i++)
 #pragma unroll
-            for (int s = 0; s < 4; s++) a.v[i][s] = *reinterpret_cast<const v4u*>(base + lo16 + s * 1024);
-        }
+            for (int s = 0; s < 4; s++)
+                a.v[i][s] = __builtin_bit_cast(
+                    v4u, __builtin_amdgcn_raw_buffer_load_b128(a_rs, lo16, xo[i] + u * 4096u + s * 1024u, 0));
     };
     struct Wu {
         uint32_t q[kShDq];
         v4u hd[kShDq];
     };
-    auto load_w = [&](int u, Wu& w) __attribute__((always_inline)) {
+    auto load_w = [&qo, &ho, rq, rh, lo16, lc16](int u, Wu& w) __attribute__((always_inline)) {
 #pragma unroll
         for (int jj = 0; jj < kShDq; jj++) {
-            const uint8_t* qb = qs + qo[jj] + static_cast<size_t>(u) * 1024;
-            const uint8_t* hb = reinterpret_cast<const uint8_t*>(hdr) + ho[jj] + static_cast<size_t>(u >> 1) * 256;
-            w.q[jj] = *reinterpret_cast<const uint32_t*>(qb + lo16);
-            w.hd[jj] = *reinterpret_cast<const v4u*>(hb + lc16);
+            w.q[jj] = __builtin_amdgcn_raw_buffer_load_b32(rq, lo16, qo[jj] + u * 1024u, 0);
+            w.hd[jj] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rh, lc16, ho[jj] + (u >> 1) * 256u, 0));
         }
     };
     uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u;
@@ -193,9 +200,10 @@ __global__ __launch_bounds__(kShThreads) void q4k_gemm_shared_kernel(const uint8
             const float mn = dmin * static_cast<float>((w.hd[jj].w >> (8 * g + 4 * h)) & 0xFu);
             SubScale k;
             k.sc = sc;
-            k.c_lo = -__builtin_fmaf(1024.f, sc, mn);
+            // -(1024 sc + mn) as one fma with negated operands (no separate negation)
+            k.c_lo = __builtin_fmaf(-1024.f, sc, -mn);
             k.sc16 = sc * 0.0625f;
-            k.c_hi = -__builtin_fmaf(64.f, sc, mn);
+            k.c_hi = __builtin_fmaf(-64.f, sc, -mn);
             Bs[b][dj0 + jj][step][lane] = __builtin_bit_cast(v4u, deq8(w.q[jj], k, m_lo, m_hi));
         }
     };
@@ -625,6 +633,9 @@ void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, voi
     if (!ws) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: no workspace");
     if (m > 0x7FFFFFFF / w.cols) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: too many tokens");
     const size_t mtiles = (m + 16 * kMt - 1) / (16 * kMt) * kMt;  // 16-token tiles, padded
+    // the kernel addresses X, the nibbles and the headers with 31-bit buffer offsets
+    if (mtiles * 16 * w.cols * 2 > 0x7FFFFFFF || w.rows_pad * (w.cols / 2) > 0x7FFFFFFF)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: operands above 2 GiB");
     x16_pack_kernel<<<dim3(static_cast<unsigned>(w.cols / 256), static_cast<unsigned>(mtiles)), dim3(256), 0, s>>>(
         X, static_cast<v4u*>(ws), static_cast<int>(m), static_cast<int>(w.cols));
     LARQL_HIP_CHECK(hipGetLastError());
