@@ -473,6 +473,22 @@ def bench_configs(be, torch, stream, copies: int):
         out[name] = d
         log(f"[bench] {name}: {d}")
 
+    def read_floor(name, hs, shapes):
+        """The plain read of the same device bytes (no arithmetic) in the kernel's own
+        launch shape (first entry) and in fixed shapes: what memory alone allows."""
+        fold = torch.empty(8192, device=dev, dtype=torch.int32)
+        fl = {}
+        for g, t in shapes:
+            fl[f"{g} x {t}"] = round(_time_us(
+                torch, stream, lambda i: be.read_floor_dev(hs[i % len(hs)], fold, g, t, stream=stream), 200), 3)
+        own = fl[f"{shapes[0][0]} x {shapes[0][1]}"]
+        best = min((v, k) for k, v in fl.items())
+        out[name].update({"read_floor_us": fl, "over_own_shape_floor": round(out[name]["us_per_launch"] / own, 3),
+                          "read_floor_best_us": best[0], "read_floor_best_shape": best[1]})
+        log(f"[bench] {name} read floor: {fl}")
+
+    FIXED_FLOOR_SHAPES = ((1024, 256), (2048, 256), (4096, 256))
+
     # Q4_0 x Q8, [10240 x 2560]
     N, K = 10240, 2560
     w = rnd(N, K, seed=11, std=0.02)
@@ -487,6 +503,8 @@ def bench_configs(be, torch, stream, copies: int):
     y = torch.empty(N, device=dev)
     us = _time_us(torch, stream, lambda i: be.matvec_dev(hs[i % copies], xq, y, x_scales=xs, stream=stream), 200)
     hbm("q4_0_matvec_10240x2560", N * K // 32 * 18 + K + K // 32 * 4 + N * 4, us)
+    # the matvec's shape: 16-lane groups, 16 rows per 256-thread workgroup
+    read_floor("q4_0_matvec_10240x2560", hs, ((N // 16, 256),) + FIXED_FLOOR_SHAPES)
     for h in hs:
         be.release_weight(h)
     del w, raw
@@ -538,6 +556,8 @@ def bench_configs(be, torch, stream, copies: int):
         us = _time_us(torch, stream, lambda i: be.matvec_dev(hs[i % len(hs)], xq, y, m=m, x_scales=xs, stream=stream),
                       200)
         hbm(f"q8_0_matvec_14336x4096_m{m}", N * K + N * K // 32 * 4 + m * (K + K // 32 * 4) + m * N * 4, us)
+        if m == 1:  # the matvec's shape at M = 1: 4-lane groups, 64 rows per 256-thread workgroup
+            read_floor("q8_0_matvec_14336x4096_m1", hs, ((N // 64, 256),) + FIXED_FLOOR_SHAPES)
     for h in hs:
         be.release_weight(h)
     del w, wq, wsc
@@ -553,6 +573,10 @@ def bench_configs(be, torch, stream, copies: int):
         y = torch.empty(N, device=dev)
         us = _time_us(torch, stream, lambda i: be.matvec_dev(hs[i % copies], x, y, stream=stream), 200)
         hbm(f"q6k_matvec_{N}x{K}", N * K // 256 * 210 + K * 4 + N * 4, us)
+        # the matvec's shapes: two 16-row tiles per 512-thread workgroup at [14336 x 4096],
+        # one per 896-thread workgroup at [4096 x 14336]
+        own = (N // 32, 512) if N == 14336 else (N // 16, 896)
+        read_floor(f"q6k_matvec_{N}x{K}", hs, (own,) + FIXED_FLOOR_SHAPES)
         for h in hs:
             be.release_weight(h)
         del w, raw

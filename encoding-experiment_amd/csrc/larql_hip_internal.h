@@ -19,9 +19,8 @@
 //   Q4_0 (18 B / 32):
 //     qs  : u8 [rows][B*16]       nibble bytes
 //     d   : f16 [rows][B]         block scale
-//   Q8_0 (trait form: i8 + separate f32 scales):
-//     qs  : i8 [rows][cols]
-//     d   : f32 [rows][B]
+//   Q8_0 (trait form: i8 + separate f32 scales), tile-major over 16-row tiles and block
+//     pairs (q8_piece / q8_scale_index below)
 // where S = cols/256 and B = cols/32.  Rows are zero-padded to rows_pad (a multiple
 // of 64) so matvec tiles load without row tests; padding rows decode to zero.
 // The algorithmic byte count of every format stays the reference's; the Q4_K
@@ -128,6 +127,20 @@ constexpr size_t kQ6Block = 3360;
 constexpr size_t kQ6Qh = 2048, kQ6Sc = 3072, kQ6D = 3328;
 __host__ __device__ inline size_t q6k_block(size_t row, size_t sb, size_t S) {
     return ((row >> 4) * S + sb) * kQ6Block;
+}
+
+// Q8_0 device layout: one 1 KB chunk per (16-row tile t, block pair p) at (t P + p) * 1024,
+// P = ceil(B / 2): piece g (0, 1 = block 2p bytes 0-15, 16-31; 2, 3 = block 2p + 1) of
+// row c of the tile at g * 256 + c * 16, so one wave-wide 16-byte load of a chunk (lane
+// 16 g + c) or of four pieces (16 rows each) reads contiguous runs of 256 bytes or more.
+// Scales: the pair {d[2p], d[2p + 1]} of row c at float ((t P + p) * 16 + c) * 2.  The
+// second block of a pair past an odd block count is zeros.
+__host__ __device__ inline size_t q8_pairs(size_t nb) { return (nb + 1) / 2; }
+__host__ __device__ inline size_t q8_piece(size_t row, size_t blk, int half, size_t P) {
+    return (((row >> 4) * P + (blk >> 1)) << 10) + ((((blk & 1) * 2 + static_cast<size_t>(half)) * 16 + (row & 15)) << 4);
+}
+__host__ __device__ inline size_t q8_scale_index(size_t row, size_t blk, size_t P) {
+    return (((row >> 4) * P + (blk >> 1)) * 16 + (row & 15)) * 2 + (blk & 1);
 }
 
 // Compute units of the current device (queried once per device, then cached).

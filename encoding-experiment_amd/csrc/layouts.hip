@@ -6,6 +6,7 @@
 //   Q6_K 210 B / 256 : [128 B ql][64 B qh][16 x i8 scales][f16 d]              (:179-239)
 //                      (device: 3360-byte blocks per 16-row tile and super-block, q6k_block)
 //   Q8_0 trait form  : i8 [rows*cols] + f32 scales [rows*cols/32]          (LC/src/pipeline.rs:22-27)
+//                      (device: 1 KB chunks per 16-row tile and block pair, q8_piece)
 //   Q4_KF 144 B / 256: llama.cpp GGUF block [f16 d][f16 dmin][12 B packed 6-bit scales and
 //                      mins][128 B: chunk c of 32 bytes = sub-block 2c low, 2c+1 high
 //                      nibbles]            (LC/src/metal/shaders/q4kf_qkv_proj.rs:87-119)
@@ -36,7 +37,8 @@ size_t dev_layout_bytes(int format, size_t rows, size_t cols, int hf) {
         case LARQL_Q4_K: return align256(rows * cols / 2) + align256(rows * (cols / 256) * 16);
         case LARQL_Q4_KF: return align256(rows * cols / 2) + align256(rows * (cols / 256) * (hf == kHdrKf160 ? 32 : 16));
         case LARQL_Q6_K: return align256(rows * (cols / 256) * 210);  // rows % 16 == 0: kQ6Block per tile
-        case LARQL_Q8_0: return align256(rows * cols) + align256(rows * (cols / 32) * 4);
+        case LARQL_Q8_0:  // rows % 16 == 0: q8_piece / q8_scale_index
+            return align256(rows / 16 * q8_pairs(cols / 32) * 1024) + align256(rows / 16 * q8_pairs(cols / 32) * 128);
         case LARQL_F32: return align256(rows * cols * 4);
         default: return 0;
     }
@@ -59,7 +61,7 @@ void dev_layout_carve(DevWeight& w) {
             w.qs = p;
             break;
         case LARQL_Q8_0:
-            w.qs = p; p += align256(R * K);
+            w.qs = p; p += align256(R / 16 * q8_pairs(K / 32) * 1024);
             w.d = p;
             break;
         case LARQL_F32:
@@ -188,6 +190,33 @@ __global__ void repack_q6k_kernel(const uint16_t* __restrict__ raw, uint8_t* __r
     *reinterpret_cast<uint16_t*>(blk + kQ6D + 2 * c) = s[104];
 }
 
+// One thread per 16-byte piece (source row r, pair p, piece g) of a Q8_0 weight in the
+// trait form (i8 [rows][cols], f32 scales [rows][B]) into the tile-major layout; the
+// thread of piece 0 also moves the pair's two scales.  Byte loads: the source may sit at
+// any offset.
+__global__ void repack_q8_0_kernel(const int8_t* __restrict__ raw, const float* __restrict__ sc,
+                                   uint8_t* __restrict__ qs, float* __restrict__ d, size_t src_rows, size_t nb,
+                                   size_t row0) {
+    const size_t P = q8_pairs(nb);
+    const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    if (i >= src_rows * P * 4) return;
+    const int g = static_cast<int>(i & 3);
+    const size_t p = (i >> 2) % P, r = (i >> 2) / P, row = row0 + r;
+    const size_t blk = 2 * p + (g >> 1);
+    uint32_t v[4] = {0, 0, 0, 0};
+    if (blk < nb) {
+        const int8_t* src = raw + r * nb * 32 + blk * 32 + (g & 1) * 16;
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(src[k])) << (8 * (k & 3));
+    }
+    *reinterpret_cast<uint4*>(qs + q8_piece(row, blk, g & 1, P)) = make_uint4(v[0], v[1], v[2], v[3]);
+    if (g == 0) {
+        float* dst = d + q8_scale_index(row, 2 * p, P);
+        dst[0] = sc[r * nb + 2 * p];
+        dst[1] = 2 * p + 1 < nb ? sc[r * nb + 2 * p + 1] : 0.0f;
+    }
+}
+
 // One thread per Q4_0 block (18-byte stride: 2-byte aligned source).
 __global__ void repack_q4_0_kernel(const uint16_t* __restrict__ raw, uint8_t* __restrict__ qs,
                                    uint16_t* __restrict__ d, size_t nblocks, size_t bpr, size_t row0, size_t stride) {
@@ -237,9 +266,9 @@ void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scale
         }
         case LARQL_Q8_0: {
             if (stride != 1) fail(LARQL_HIP_ERR_UNSUPPORTED, "repack: interleaved Q8_0");
-            LARQL_HIP_CHECK(hipMemcpyAsync(w.qs + row0 * w.cols, raw, src_rows * w.cols, hipMemcpyDeviceToDevice, s));
-            LARQL_HIP_CHECK(hipMemcpyAsync(static_cast<float*>(w.d) + row0 * (w.cols / 32), q8_scales,
-                                           src_rows * (w.cols / 32) * sizeof(float), hipMemcpyDeviceToDevice, s));
+            const size_t nb = w.cols / 32, n = src_rows * q8_pairs(nb) * 4;
+            repack_q8_0_kernel<<<dim3(static_cast<unsigned>((n + T - 1) / T)), dim3(T), 0, s>>>(
+                reinterpret_cast<const int8_t*>(raw), q8_scales, w.qs, static_cast<float*>(w.d), src_rows, nb, row0);
             break;
         }
         case LARQL_F32: {

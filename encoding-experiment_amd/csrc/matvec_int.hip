@@ -111,7 +111,8 @@ struct Blk<LARQL_Q4_0> {
     uint4 q;
     uint32_t d;
     static constexpr int kXAux = 2;
-    __device__ __forceinline__ void load(const uint8_t* qs, const void* dsc, size_t blk) {
+    __device__ __forceinline__ void load(const uint8_t* qs, const void* dsc, int row, int b, int nb) {
+        const size_t blk = static_cast<size_t>(row) * nb + b;
         q = reinterpret_cast<const uint4*>(qs)[blk];
         d = static_cast<const uint16_t*>(dsc)[blk];
     }
@@ -154,18 +155,18 @@ struct Blk<LARQL_Q4_0> {
     }
 };
 
-// Q8_0 (trait form): 32 int8 + an f32 scale.  LDS image: the 8 raw x dwords and the
-// x scale.
+// Q8_0: 32 int8 + an f32 scale, tile-major (q8_piece: a 16-row tile's pieces of one
+// block are 256 contiguous bytes).  LDS image: the 8 raw x dwords and the x scale.
 template <>
 struct Blk<LARQL_Q8_0> {
     uint4 a, c;
     float ws;
     static constexpr int kXAux = 1;
-    __device__ __forceinline__ void load(const uint8_t* qs, const void* dsc, size_t blk) {
-        const uint4* p = reinterpret_cast<const uint4*>(qs) + 2 * blk;
-        a = p[0];
-        c = p[1];
-        ws = static_cast<const float*>(dsc)[blk];
+    __device__ __forceinline__ void load(const uint8_t* qs, const void* dsc, int row, int b, int nb) {
+        const size_t P = q8_pairs(nb), off = q8_piece(row, b, 0, P);
+        a = *reinterpret_cast<const uint4*>(qs + off);
+        c = *reinterpret_cast<const uint4*>(qs + off + 256);
+        ws = static_cast<const float*>(dsc)[q8_scale_index(row, b, P)];
     }
     __device__ __forceinline__ float product(const uint4* xp0, const uint4* xp1, const uint32_t* xa) const {
         const uint4 x0 = *xp0;
@@ -215,7 +216,7 @@ __device__ __forceinline__ void int_mv_body(const uint8_t* __restrict__ qs, cons
     uint32_t* xa = reinterpret_cast<uint32_t*>(lds4 + 2 * M * nb);  // [M][nb][kXAux]
     const int j = threadIdx.x & (G - 1);
     const int row = wg * (kThreads / G) + threadIdx.x / G;
-    const size_t base = static_cast<size_t>(min(row, rows - 1)) * nb;
+    const int rowc = min(row, rows - 1);
     const int steps = (nb + G - 1) / G;
     const int nx = m * nb;
 
@@ -228,7 +229,7 @@ __device__ __forceinline__ void int_mv_body(const uint8_t* __restrict__ qs, cons
     for (int k = 0; k < kXBatch; k++) xr[k].load(xq, xsc, min(static_cast<int>(threadIdx.x) + k * kThreads, nx - 1));
     B ring[D];
 #pragma unroll
-    for (int u = 0; u < D; u++) ring[u].load(qs, dsc, base + min(u * G + j, nb - 1));
+    for (int u = 0; u < D; u++) ring[u].load(qs, dsc, rowc, min(u * G + j, nb - 1), nb);
 #pragma unroll
     for (int k = 0; k < kXBatch; k++) {
         const int i = threadIdx.x + k * kThreads;
@@ -267,7 +268,7 @@ __device__ __forceinline__ void int_mv_body(const uint8_t* __restrict__ qs, cons
             // consume, then refill the same registers (a copy of a slot whose load is
             // still in flight would wait for it)
             consume(ring[u], s0 + u);
-            ring[u].load(qs, dsc, base + min((s0 + u + D) * G + j, nb - 1));
+            ring[u].load(qs, dsc, rowc, min((s0 + u + D) * G + j, nb - 1), nb);
             // keep the refills in ring order: the wait for the next step then leaves the
             // younger steps in flight
             __builtin_amdgcn_sched_barrier(0);
@@ -344,8 +345,7 @@ __global__ __launch_bounds__(64 * WAVES) void q8_mfma_kernel(const uint8_t* __re
     float* xsl = reinterpret_cast<float*>(lds4 + nchunk + 1);   // [npair][8 mi][2 blocks]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
-    const int rbase = (blockIdx.x * WAVES + wave) * 16;
-    const uint32_t wr = static_cast<uint32_t>(min(rbase + c, rows - 1));
+    const int rbase = (blockIdx.x * WAVES + wave) * 16;  // one 16-row tile per wave
 
     // x image item j: pair j >> 5, A row i = (j >> 1) & 15 (mi = i >> 1, block 2bp + (i & 1)),
     // half j & 1 of the block; zero for mi >= m
@@ -379,15 +379,22 @@ __global__ __launch_bounds__(64 * WAVES) void q8_mfma_kernel(const uint8_t* __re
 #pragma unroll
     for (int k = 0; k < kSB; k++) s0[k] = xscale(min(t0 + k * kT, nb * 8 - 1));
 
-    const __amdgpu_buffer_rsrc_t rw =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wq), 0, rows * nb * 32, kBufDword3);
-    const uint32_t voff_w = wr * static_cast<uint32_t>(nb) * 32 + 16 * g;
-    const float2* wsrow = reinterpret_cast<const float2*>(wsc + static_cast<size_t>(wr) * nb);
+    // tile-major weights (q8_piece): the chunk of pair bp is 1 KB, lane 16 g + c's piece at
+    // 16 lane, so one load per pair reads the wave's 16 rows contiguously; tiles past the
+    // last row (the workgroup's last waves) read zeros past the descriptor's end, and their
+    // rows are not stored
+    const uint32_t tile = static_cast<uint32_t>(rbase >> 4);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(wq), 0, static_cast<int>(static_cast<uint32_t>((rows + 15) / 16) * npair * 1024u), kBufDword3);
+    const uint32_t voff_w = tile * static_cast<uint32_t>(npair) * 1024u + 16u * lane;
+    const int tiles = (rows + 15) / 16;
+    const float2* wsrow = reinterpret_cast<const float2*>(wsc) +
+                          static_cast<size_t>(min(static_cast<int>(tile), tiles - 1)) * npair * 16 + c;
     v4i wv[D];
     float2 ws[D];
     auto refill = [&](int u, int bp) __attribute__((always_inline)) {
-        wv[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w + 64 * bp, 0, 0);
-        ws[u] = wsrow[min(bp, npair - 1)];
+        wv[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w + 1024u * bp, 0, 0);
+        ws[u] = wsrow[static_cast<size_t>(min(bp, npair - 1)) * 16];
     };
 #pragma unroll
     for (int u = 0; u < D; u++) refill(u, u);

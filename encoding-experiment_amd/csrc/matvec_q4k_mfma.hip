@@ -469,11 +469,11 @@ __global__ __launch_bounds__(64 * kMaxKS) void q4k_read_floor_kernel(const uint4
 
 void launch_q4k_read_floor(const DevWeight& w, uint32_t* out, size_t out_words, unsigned groups, unsigned threads,
                            int num_cus, hipStream_t s) {
-    if ((w.format != LARQL_Q4_K && w.format != LARQL_Q4_KF) || w.cols % 256 != 0 || w.cols == 0 ||
-        w.rows_pad % 16 != 0 || w.bytes % 16 != 0)
-        fail(LARQL_HIP_ERR_UNSUPPORTED, "read floor: Q4_K-family weights only");
+    if (w.bytes % 16 != 0 || w.bytes == 0) fail(LARQL_HIP_ERR_UNSUPPORTED, "read floor: weight size");
     if (num_cus <= 0) num_cus = current_device_cus();
     if (groups == 0 && threads == 0) {
+        if ((w.format != LARQL_Q4_K && w.format != LARQL_Q4_KF) || w.cols % 256 != 0 || w.rows_pad % 16 != 0)
+            fail(LARQL_HIP_ERR_UNSUPPORTED, "read floor: the matvec launch shape is known for Q4_K-family weights only");
         const Q4kSplit sp = pick_q4k_split(w, num_cus);
         const size_t S = w.cols / 256;
         groups = static_cast<unsigned>(w.rows_pad / (16 * sp.t));

@@ -599,8 +599,9 @@ class HipBackend:
                                                    _stream_ptr(stream)))
 
     def read_floor_dev(self, handle: int, out, workgroups: int = 0, threads: int = 0, stream=None):
-        """Plain read of a Q4_K-family weight's device bytes (a measurement of the memory
-        floor): in its matvec's launch shape by default, else `workgroups` x `threads`.
+        """Plain read of a registered weight's device bytes (a measurement of the memory
+        floor): in its matvec's launch shape by default (Q4_K-family weights), else
+        `workgroups` x `threads` (any format).
         out: device int32/uint32 tensor, one XOR fold per workgroup."""
         self._check(self._lib.larql_hip_read_floor_dev(self._ctx, handle, workgroups, threads, _dptr(out),
                                                        out.numel(), _stream_ptr(stream)))

@@ -197,10 +197,11 @@ int larql_hip_matvec_dev(larql_hip_ctx* ctx, uint64_t handle, const void* x, con
                          float* out, size_t m, void* stream);
 
 /* Measurement aid with no counterpart in the reference: reads every device byte of a
- * registered Q4_K / Q4_KF weight once and does no arithmetic on them, so its duration is
- * the memory floor for those bytes in that launch shape.  workgroups = threads = 0: the
- * launch shape of the weight's matvec (4 * ceil(rows / 64) words of out always suffice);
- * else `workgroups` workgroups of `threads` (64 .. 1024, a multiple of 64).  out: device
+ * registered weight once and does no arithmetic on them, so its duration is the memory
+ * floor for those bytes in that launch shape.  workgroups = threads = 0 (Q4_K / Q4_KF
+ * weights): the launch shape of the weight's matvec (4 * ceil(rows / 64) words of out
+ * always suffice); else, for any format, `workgroups` workgroups of `threads` (64 .. 1024,
+ * a multiple of 64).  out: device
  * uint32 [out_words], out_words >= the workgroup count; receives one XOR fold of the
  * bytes per workgroup. */
 int larql_hip_read_floor_dev(larql_hip_ctx* ctx, uint64_t handle, unsigned workgroups, unsigned threads,
