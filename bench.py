@@ -556,8 +556,8 @@ def bench_configs(be, torch, stream, copies: int):
         us = _time_us(torch, stream, lambda i: be.matvec_dev(hs[i % len(hs)], xq, y, m=m, x_scales=xs, stream=stream),
                       200)
         hbm(f"q8_0_matvec_14336x4096_m{m}", N * K + N * K // 32 * 4 + m * (K + K // 32 * 4) + m * N * 4, us)
-        if m == 1:  # the matvec's shape at M = 1: 4-lane groups, 64 rows per 256-thread workgroup
-            read_floor("q8_0_matvec_14336x4096_m1", hs, ((N // 64, 256),) + FIXED_FLOOR_SHAPES)
+        if m == 1:  # the matvec's shape at M = 1: 4-lane groups, 32 rows per 128-thread workgroup
+            read_floor("q8_0_matvec_14336x4096_m1", hs, ((N // 32, 128),) + FIXED_FLOOR_SHAPES)
     for h in hs:
         be.release_weight(h)
     del w, wq, wsc
