@@ -308,3 +308,36 @@ def test_read_floor_reads_every_block(hip, rows, cols):
     finally:
         hip.release_weight(h)
         hip.forget_host(q)
+
+
+def test_read_floor_other_formats_explicit_shapes(hip):
+    """Weights of the other formats are read in explicit launch shapes only: the fold is
+    the same in every shape (each device byte read once) and changes when one weight byte
+    does; the matvec's own shape (0, 0) is known for Q4_K-family weights alone."""
+    import torch
+
+    rows, cols = 1000, 2560
+    w = oracle.gauss(901, rows * cols, 0.0, 0.02)
+    wq, ws = oracle.quantize_weights_q8(w, rows, cols)
+
+    def folds(qbytes):
+        h = hip.register_weight(larql_hip.Q8_0, qbytes, rows, cols, q8_scales=ws)
+        try:
+            res = []
+            for g, t in ((64, 256), (300, 128), (7, 1024)):
+                out = torch.zeros(g, dtype=torch.int32, device="cuda")
+                hip.read_floor_dev(h, out, g, t)
+                torch.cuda.synchronize()
+                res.append(int(np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))))
+            with pytest.raises(larql_hip.LarqlHipError):
+                hip.read_floor_dev(h, torch.zeros(64, dtype=torch.int32, device="cuda"), 0, 0)
+            return res
+        finally:
+            hip.release_weight(h)
+            hip.forget_host(qbytes)
+
+    base = folds(wq.copy())
+    assert len(set(base)) == 1, [hex(v) for v in base]
+    m = wq.copy()
+    m[12345] ^= 0x04
+    assert bin(folds(m)[0] ^ base[0]).count("1") == 1
