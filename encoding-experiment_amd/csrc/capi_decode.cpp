@@ -645,9 +645,11 @@ void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float*
     auto& kv = c->kv;
     kv_ensure(c, m->layers.size(), m->nkv, m->hd, kv.current_len + 1);
     const int T = static_cast<int>(kv.current_len) + 1;
-    const int S = (T + 63) / 64;
+    // partials for any T up to the cache capacity: the buffer grows only with the cache, so
+    // a step inside the capacity allocates nothing
+    const int S_cap = larql::attn_splits(static_cast<int>(kv.max_seq), 0);
     float* part = static_cast<float*>(
-        larql::ensure(c, m->part, static_cast<size_t>(m->nq) * S * (m->hd + 2) * sizeof(float)));
+        larql::ensure(c, m->part, larql::attn_part_floats(m->nq, S_cap, m->hd) * sizeof(float)));
     if (m->layers.empty()) larql::launch_copy_f32(x_dev, m->h0, m->hidden, s);
     else enqueue_layers(c, m, x_dev, T, part, s, pa);
     kv.current_len = static_cast<size_t>(T);
@@ -762,7 +764,7 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
     const size_t hidden = m->hidden, inter = m->inter, qd = m->q_dim, kvd = m->kv_dim, ld = qd + 2 * kvd;
     const size_t wide = std::max({hidden, qd, inter}), gw = std::max(hidden, 2 * inter);
     const int S = larql::attn_prompt_splits(1, static_cast<int>(M), 0);
-    const size_t part_n = M * static_cast<size_t>(m->nq) * S * (m->hd + 2);
+    const size_t part_n = larql::attn_part_floats(m->nq, S, m->hd, static_cast<int>(M));
     size_t split_n = 0;  // K-split partial products of the GEMMs
     auto need = [&](const larql::DevWeight& w) {
         split_n = std::max(split_n, larql::q4k_gemm_f32_part_floats(w, M));

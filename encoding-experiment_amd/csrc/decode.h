@@ -10,15 +10,16 @@ struct AttnArgs {
     __half* kc;        // this layer's K cache [cap][num_kv][hd]
     __half* vc;        // this layer's V cache [cap / 8][num_kv][hd][8]
     float* out;        // [num_q * hd]
-    float* part;       // [num_q][S][hd + 2]: unnormalised o, chunk max, chunk sum
+    float* part;       // [num_q][S][pst]: unnormalised o[hd], chunk max, chunk sum (attn_part_floats)
     int num_q, num_kv, hd, rdim;
     int T, t_begin, S;  // S is set by launch_attention
+    int pst = 0;        // partial entry stride in floats (attn_partial_stride), set by launch_attention
     float scale;
     const float2* rope;  // [cap][rdim / 2] cos, sin (launch_rope_table)
     // Prompt mode (prefill): grid z = query position p of `batch`, T = T + p for query p,
     // the window start recomputed per query, qkv rows qkv_ld floats apart, every K/V row
     // (the query's own included) already in the cache, out rows num_q * hd apart and
-    // partials [batch][num_q][S][hd + 2] with S the largest query's split count.
+    // partials [batch][num_q][S][pst] with S the largest query's split count.
     int batch = 0, window = 0, qkv_ld = 0;
     // Prompt-attention options of the reference's fused kernel (LC/src/metal/shaders/
     // fused_attention.rs:79-88, 132-137): qk_norm scales each RoPE'd query head by
@@ -33,6 +34,12 @@ void launch_attention(const AttnArgs& a, hipStream_t s);
 // queries T0 .. T0 + batch - 1 (its partials stride).
 int attn_splits(int T, int t_begin);
 int attn_prompt_splits(int T0, int batch, int window);
+// Floats per partial entry (o[hd], max, sum).  A partial buffer holds batch x num_q x S
+// entries.
+int attn_partial_stride(int hd);
+inline size_t attn_part_floats(int num_q, int S, int hd, int batch = 1) {
+    return static_cast<size_t>(batch) * num_q * S * attn_partial_stride(hd);
+}
 // cos/sin table for positions [0, cap): angle p * base^(-2i/rdim) in f64, as the CPU
 // path computes it (LI/src/attention/rope.rs:22-55), rounded to f32.
 void launch_rope_table(float2* cs, size_t cap, int rdim, double base, hipStream_t s);

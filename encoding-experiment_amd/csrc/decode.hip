@@ -63,27 +63,6 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return (a + b) + (c + d);
 }
 
-// Workgroup-wide max / sum through `scratch` (>= kAttnThreads / 64 floats); every
-// thread gets the result.
-__device__ __forceinline__ float block_max(float v, float* scratch) {
-    v = wave_max_dpp(v);
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float r = scratch[0];
-    for (int w = 1; w < kAttnThreads / 64; w++) r = fmaxf(r, scratch[w]);
-    __syncthreads();
-    return r;
-}
-__device__ __forceinline__ float block_sum(float v, float* scratch) {
-    v = wave_sum_dpp(v);
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float r = scratch[0];
-    for (int w = 1; w < kAttnThreads / 64; w++) r += scratch[w];
-    __syncthreads();
-    return r;
-}
-
 // Value of lane (this lane + R) within its row of 16 (row_shl:R).
 template <int R>
 __device__ __forceinline__ float from_lane_plus(float v) {
@@ -139,21 +118,115 @@ __device__ __forceinline__ v4u split8(const float* x, int part) {
 //           eight consecutive positions of one dim are one 16-byte load.
 // The row at pos = T - 1 comes from the fresh projections: RoPE'd, rounded to fp16 and
 // written to the cache by the workgroup that owns it, which uses it from LDS.
-// attn_combine_kernel merges the S softmax partials of each head.
+// attn_combine_kernel merges the S softmax partials of each kv head's query heads.
 // Prompt mode: this workgroup's query (grid z) and its view of the arguments.
-__device__ __forceinline__ void attn_select_query(AttnArgs& a, int hd) {
+__device__ __forceinline__ void attn_select_query(AttnArgs& a) {
     if (a.batch == 0) return;
     const int p = blockIdx.z;
     a.T += p;
     a.t_begin = (a.window > 0 && a.T > a.window) ? a.T - a.window : 0;
     a.qkv += static_cast<size_t>(p) * a.qkv_ld;
-    a.part += static_cast<size_t>(p) * a.num_q * a.S * (hd + 2);
-    a.out += static_cast<size_t>(p) * a.num_q * hd;
+    a.part += static_cast<size_t>(p) * a.num_q * a.S * a.pst;
+    a.out += static_cast<size_t>(p) * a.num_q * a.hd;
+}
+
+// o = sum_s e_s o_s / sum_s e_s l_s with e_s = exp(m_s - max_s m_s), in split order, for
+// nh consecutive query heads: partial entry (head h, split s) at base + (h sst + s) pst =
+// {o[HD], m, l}, outputs at out + h HD.  One workgroup; ml holds 2 nh S floats of LDS.
+// The loads of every (m, l) pair and of the first PF splits of each thread's first output
+// pair are issued together, so for S <= PF (T <= 2176) the merge waits on memory once.
+template <int HD>
+__device__ __forceinline__ void attn_merge_heads(const float* __restrict__ base, int pst, int sst, int S, int nh,
+                                                 float* __restrict__ out, float* ml, float* inv_l) {
+    constexpr int H2 = HD / 2, PF = 34;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nout = nh * H2;  // float2 outputs
+    float2 ov[PF];
+    {
+        const int h = tid / H2, d = 2 * (tid - h * H2);
+        const float* src = base + static_cast<size_t>(h) * sst * pst + d;
+#pragma unroll
+        for (int u = 0; u < PF; u++)
+            ov[u] = tid < nout && u < S ? *reinterpret_cast<const float2*>(src + static_cast<size_t>(u) * pst)
+                                        : make_float2(0.f, 0.f);
+    }
+    for (int k = tid; k < nh * S; k += kAttnThreads) {
+        const int h = k / S, s = k - h * S;
+        const float2 v = *reinterpret_cast<const float2*>(base + (static_cast<size_t>(h) * sst + s) * pst + HD);
+        ml[2 * k] = v.x;
+        ml[2 * k + 1] = v.y;
+    }
+    __syncthreads();
+    for (int h = wave; h < nh; h += kAttnThreads / 64) {  // one wave per head
+        float mx = -INFINITY;
+        for (int s = lane; s < S; s += 64) mx = fmaxf(mx, ml[2 * (h * S + s)]);
+        mx = wave_max_dpp(mx);
+        float L = 0.f;
+        for (int s = lane; s < S; s += 64) {
+            const float e = expf(ml[2 * (h * S + s)] - mx);
+            ml[2 * (h * S + s)] = e;
+            L = fmaf(ml[2 * (h * S + s) + 1], e, L);
+        }
+        L = wave_sum_dpp(L);
+        if (lane == 0) inv_l[h] = 1.0f / L;
+    }
+    __syncthreads();
+    for (int i = tid; i < nout; i += kAttnThreads) {
+        const int h = i / H2, d = 2 * (i - h * H2);
+        const float* e = ml + 2 * h * S;
+        const float* src = base + static_cast<size_t>(h) * sst * pst + d;
+        float2 o = make_float2(0.f, 0.f);
+        int s = 0;
+        if (i == tid) {
+#pragma unroll
+            for (int u = 0; u < PF; u++)
+                if (u < S) {
+                    o.x = fmaf(ov[u].x, e[2 * u], o.x);
+                    o.y = fmaf(ov[u].y, e[2 * u], o.y);
+                }
+            s = PF;
+        }
+        for (; s < S; s += 16) {  // splits past PF: sixteen loads in flight per round
+            float2 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                v[u] = s + u < S ? *reinterpret_cast<const float2*>(src + static_cast<size_t>(s + u) * pst)
+                                 : make_float2(0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (s + u < S) {
+                    o.x = fmaf(v[u].x, e[2 * (s + u)], o.x);
+                    o.y = fmaf(v[u].y, e[2 * (s + u)], o.y);
+                }
+        }
+        const float il = inv_l[h];
+        *reinterpret_cast<float2*>(out + static_cast<size_t>(h) * HD + d) = make_float2(o.x * il, o.y * il);
+    }
+}
+
+// Query heads per merge pass: as many of the kv head's reps as fit kMergeLdsMax.
+constexpr int kMergeLdsMax = 48 * 1024;
+__host__ __device__ inline int merge_heads_per_pass(int reps, int S) {
+    const int fit = (kMergeLdsMax / 4 - 8) / (2 * S);
+    return fit < 1 ? 1 : (fit < reps ? fit : reps);
+}
+
+// The merge of kv head kvh's reps query heads, in passes of merge_heads_per_pass.
+template <int HD>
+__device__ __forceinline__ void attn_merge_group(const float* part, int pst, int sst, int S, int reps, int kvh,
+                                                 float* out, float* lds) {
+    const int hc = merge_heads_per_pass(reps, S);
+    for (int h0 = 0; h0 < reps; h0 += hc) {
+        if (h0) __syncthreads();  // the previous pass's LDS reads are done
+        const int nh = reps - h0 < hc ? reps - h0 : hc;
+        const size_t h = static_cast<size_t>(kvh) * reps + h0;
+        attn_merge_heads<HD>(part + h * sst * pst, pst, sst, S, nh, out + h * HD, lds, lds + 2 * nh * S);
+    }
 }
 
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
-    attn_select_query(a, HD);
+    attn_select_query(a);
     constexpr int KS = HD / 32;                 // score k-steps
     constexpr int NDT = HD / 16;                // P.V dim tiles
     constexpr int DTW = (NDT + 3) / 4;          // dim tiles per wave (upper bound)
@@ -345,98 +418,42 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
                                                        __builtin_bit_cast(half8, pop[ts * 64 + lane]), o, 0, 0, 0);
         o = add_lane_plus(o, reps);
         if (c < reps) {
-            float* dst = a.part + (static_cast<size_t>(kvh * reps + c) * a.S + s) * (HD + 2);
+            float* dst = a.part + (static_cast<size_t>(kvh * reps + c) * a.S + s) * a.pst;
 #pragma unroll
             for (int r = 0; r < 4; r++) dst[16 * dt + 4 * g + r] = o[r];
         }
     }
     if (tid < reps) {
-        float* dst = a.part + (static_cast<size_t>(kvh * reps + tid) * a.S + s) * (HD + 2);
+        float* dst = a.part + (static_cast<size_t>(kvh * reps + tid) * a.S + s) * a.pst;
         dst[HD] = ml_s[2 * tid];
         dst[HD + 1] = ml_s[2 * tid + 1];
     }
 }
 
-// Merge of the S softmax partials of each head (a second launch: the kernel boundary
-// makes every partial visible; a device-scope release/acquire inside the split kernel
-// measured ~25 us per launch here):
-//   o = sum_s e_s o_s / sum_s e_s l_s,   e_s = exp(m_s - max_s m_s).
-// Grid (num_q); thread (group g, dim pair j) sums splits g, g + ngrp, ... with the
-// per-split weights computed once per workgroup in LDS.  The first 16 partial vectors of
-// every thread and the split maxima and sums are loaded before any reduction, so the
-// merge waits on global memory once.
+// Merge of the S softmax partials (a second launch: the kernel boundary makes every
+// partial visible), grid (num_kv, 1, batch): one workgroup per kv head and query.  A merge
+// in the split launch itself (the kv head's last workgroup to finish merging, all of its
+// workgroups placed on one XCD and meeting in its L2 through an atomic arrival count) was
+// measured: 1.5405 against 1.5408 ms per 8B decode step, so the chain of memory round
+// trips, not the launch between them, sets the cost; the merge stays a launch.
+template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a) {
     extern __shared__ float lds[];
-    const int Sst = a.S;  // partial stride per head
-    if (a.batch) {        // prompt mode: query blockIdx.y has its own split count
-        attn_select_query(a, a.hd);
-        a.S = (a.T - (a.t_begin & ~7) + kAttnChunk - 1) / kAttnChunk;
-    }
-    const int h = blockIdx.x, tid = threadIdx.x, hd = a.hd, hd2 = hd / 2;
-    const int ngrp = kAttnThreads / hd2;                 // split groups
-    float* e_s = lds;                                    // S weights
-    float2* o_s = reinterpret_cast<float2*>(e_s + a.S);  // ngrp * hd2 partial outputs
-    float* red = reinterpret_cast<float*>(o_s + ngrp * hd2);
-    const float* src = a.part + static_cast<size_t>(h) * Sst * (hd + 2);
-    const int grp = tid / hd2, j = tid - grp * hd2;
-    const bool act = grp < ngrp;
-    constexpr int PF = 16;
-    float2 ov[PF];
-#pragma unroll
-    for (int u = 0; u < PF; u++) {
-        const int s2 = grp + u * ngrp;
-        ov[u] = act && s2 < a.S ? *reinterpret_cast<const float2*>(src + s2 * (hd + 2) + 2 * j) : make_float2(0.f, 0.f);
-    }
-    float M = -INFINITY, m0 = -INFINITY, l0 = 0.f;
-    if (tid < a.S) {
-        m0 = src[tid * (hd + 2) + hd];
-        l0 = src[tid * (hd + 2) + hd + 1];
-    }
-    M = m0;
-    for (int s2 = tid + kAttnThreads; s2 < a.S; s2 += kAttnThreads) M = fmaxf(M, src[s2 * (hd + 2) + hd]);
-    M = block_max(M, red);
-    float L = 0.f;
-    if (tid < a.S) {
-        const float e = expf(m0 - M);
-        e_s[tid] = e;
-        L = l0 * e;
-    }
-    for (int s2 = tid + kAttnThreads; s2 < a.S; s2 += kAttnThreads) {
-        const float e = expf(src[s2 * (hd + 2) + hd] - M);
-        e_s[s2] = e;
-        L = fmaf(src[s2 * (hd + 2) + hd + 1], e, L);
-    }
-    L = block_sum(L, red);  // also orders the e_s writes before their reads
-    float2 o = make_float2(0.f, 0.f);
-    if (act) {
-#pragma unroll
-        for (int u = 0; u < PF; u++) {
-            const int s2 = grp + u * ngrp;
-            if (s2 < a.S) {
-                o.x = fmaf(ov[u].x, e_s[s2], o.x);
-                o.y = fmaf(ov[u].y, e_s[s2], o.y);
-            }
-        }
-        for (int s2 = grp + PF * ngrp; s2 < a.S; s2 += ngrp) {
-            const float2 v = *reinterpret_cast<const float2*>(src + s2 * (hd + 2) + 2 * j);
-            o.x = fmaf(v.x, e_s[s2], o.x);
-            o.y = fmaf(v.y, e_s[s2], o.y);
-        }
-        o_s[grp * hd2 + j] = o;
-    }
-    __syncthreads();
-    if (tid < hd2) {
-        float2 t = o_s[tid];
-        for (int g = 1; g < ngrp; g++) {
-            t.x += o_s[g * hd2 + tid].x;
-            t.y += o_s[g * hd2 + tid].y;
-        }
-        const float invL = 1.0f / L;
-        *reinterpret_cast<float2*>(a.out + static_cast<size_t>(h) * hd + 2 * tid) = make_float2(t.x * invL, t.y * invL);
-    }
+    const int sst = a.S;  // partial stride per head
+    attn_select_query(a);
+    const int S = (a.T - (a.t_begin & ~7) + kAttnChunk - 1) / kAttnChunk;  // this query's splits
+    const int reps = a.num_q / a.num_kv;
+    attn_merge_group<HD>(a.part, a.pst, sst, S, reps, blockIdx.x, a.out, lds);
 }
 
 bool attn_supported(int reps, int hd) { return reps >= 1 && reps <= 8 && hd % 32 == 0 && hd >= 32 && hd <= 256; }
+
+int attn_partial_stride(int hd) { return hd + 2; }
+
+// The merge's LDS: 2 nh S (m, l) pairs and nh reciprocal sums per pass.
+static size_t merge_lds_bytes(int reps, int S) {
+    return sizeof(float) * (2 * static_cast<size_t>(merge_heads_per_pass(reps, S)) * S + 8);
+}
 
 __global__ void rope_table_kernel(float2* cs, size_t n, int half, int rdim, double base) {
     const size_t idx = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
@@ -517,7 +534,11 @@ void launch_attention(const AttnArgs& a0, hipStream_t s) {
     const int reps = a.num_q / a.num_kv;
     if (!attn_supported(reps, a.hd)) fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: head geometry");
     a.S = a.batch ? attn_prompt_splits(a.T, a.batch, a.window) : attn_splits(a.T, a.t_begin);
+    a.pst = attn_partial_stride(a.hd);
+    if (2 * static_cast<size_t>(a.S) * sizeof(float) + 32 > static_cast<size_t>(kMergeLdsMax))
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: too many position splits");
     const int nz = a.batch ? a.batch : 1;
+    const size_t lds = merge_lds_bytes(reps, a.S);
     const dim3 grid(a.S, a.num_kv, nz), block(kAttnThreads);
     switch (a.hd) {
         case 32: attn_decode_kernel<32><<<grid, block, 0, s>>>(a); break;
@@ -530,10 +551,17 @@ void launch_attention(const AttnArgs& a0, hipStream_t s) {
         default: attn_decode_kernel<256><<<grid, block, 0, s>>>(a); break;
     }
     LARQL_HIP_CHECK(hipGetLastError());
-    // combine: S split weights + block-reduction scratch
-    const size_t lds2 = sizeof(float) * (static_cast<size_t>(a.S) + 2 * kAttnThreads + kAttnThreads / 64);
-    if (lds2 > 64 * 1024) fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: too many position splits");
-    attn_combine_kernel<<<dim3(a.num_q, 1, nz), dim3(kAttnThreads), lds2, s>>>(a);
+    const dim3 g2(a.num_kv, 1, nz);
+    switch (a.hd) {
+        case 32: attn_combine_kernel<32><<<g2, block, lds, s>>>(a); break;
+        case 64: attn_combine_kernel<64><<<g2, block, lds, s>>>(a); break;
+        case 96: attn_combine_kernel<96><<<g2, block, lds, s>>>(a); break;
+        case 128: attn_combine_kernel<128><<<g2, block, lds, s>>>(a); break;
+        case 160: attn_combine_kernel<160><<<g2, block, lds, s>>>(a); break;
+        case 192: attn_combine_kernel<192><<<g2, block, lds, s>>>(a); break;
+        case 224: attn_combine_kernel<224><<<g2, block, lds, s>>>(a); break;
+        default: attn_combine_kernel<256><<<g2, block, lds, s>>>(a); break;
+    }
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
