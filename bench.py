@@ -454,6 +454,8 @@ def bench_configs(be, torch, stream, copies: int):
     Q8_0 x Q8 [14336x4096] at M = 1, 4, 8; Q6_K [14336x4096] and
     [4096x14336]; gate-KNN over 34 layers [10240x2560] x 256 queries, top-32, f32 and
     Q4_0; Q4_K prefill GEMM 512 x [10240x2560]."""
+    import numpy as np
+
     import larql_hip
 
     dev = torch.device("cuda:0")
@@ -476,7 +478,7 @@ def bench_configs(be, torch, stream, copies: int):
     def read_floor(name, hs, shapes):
         """The plain read of the same device bytes (no arithmetic) in the kernel's own
         launch shape (first entry) and in fixed shapes: what memory alone allows."""
-        fold = torch.empty(8192, device=dev, dtype=torch.int32)
+        fold = torch.empty(max(g for g, _ in shapes), device=dev, dtype=torch.int32)
         fl = {}
         for g, t in shapes:
             fl[f"{g} x {t}"] = round(_time_us(
@@ -581,6 +583,123 @@ def bench_configs(be, torch, stream, copies: int):
             be.release_weight(h)
         del w, raw
 
+    # Q4_K at sizes that amortise the launch ramp and at the decode step's fused gate|up:
+    # the Llama-3 vocabulary [128256 x 4096] (295 MB; 2 copies rotate past the 256 MB
+    # Infinity Cache) and [28672 x 4096] (68 MB, 16 copies), each beside its read floor
+    for (N, K), seed, ncopy, fixed in (((128256, 4096), 41, 2, ((2048, 256), (4096, 256), (8192, 256), (16384, 256))),
+                                       ((28672, 4096), 42, copies, FIXED_FLOOR_SHAPES + ((8192, 256),))):
+        w = rnd(N, K, seed=seed, std=0.02)
+        raw = torch.empty(N * K // 256 * 148, dtype=torch.uint8, device=dev)
+        be.quantize_weights_dev(larql_hip.Q4_K, w, N * K, raw, stream=stream)
+        torch.cuda.synchronize()
+        del w
+        hs = [be.register_weight_device(larql_hip.Q4_K, raw, raw.numel(), N, K) for _ in range(ncopy)]
+        del raw
+        x = rnd(K, seed=seed + 100)
+        y = torch.empty(N, device=dev)
+        n = 40 if N > 100000 else 200
+        us = _time_us(torch, stream, lambda i: be.matvec_dev(hs[i % ncopy], x, y, stream=stream), n)
+        sh = be.q4k_launch_shape(hs[0])
+        hbm(f"q4k_matvec_{N}x{K}", q4k_algorithmic_bytes(N, K), us,
+            {"launch": sh, "weight_copies": ncopy})
+        read_floor(f"q4k_matvec_{N}x{K}", hs, ((sh["workgroups"], sh["threads"]),) + fixed)
+        out[f"q4k_matvec_{N}x{K}"]["over_best_floor"] = round(us / out[f"q4k_matvec_{N}x{K}"]["read_floor_best_us"], 3)
+        for h in hs:
+            be.release_weight(h)
+        torch.cuda.empty_cache()
+
+    # lm-head KNN, Q4 path (lm_head_knn_backend, LV/src/index/walk.rs:549-583): Q4_0
+    # [128256 x 4096], one query, top-5 by signed score (quantize_to_q8 + Q4_0 matvec +
+    # top-k); 2 copies of 295 MB rotate past the Infinity Cache
+    N, K, k5 = 128256, 4096, 5
+    w = rnd(N, K, seed=71, std=0.02)
+    raw = torch.empty(N * K // 32 * 18, dtype=torch.uint8, device=dev)
+    be.quantize_weights_dev(larql_hip.Q4_0, w, N * K, raw, stream=stream)
+    torch.cuda.synchronize()
+    del w
+    hs = [be.register_weight_device(larql_hip.Q4_0, raw, raw.numel(), N, K) for _ in range(2)]
+    del raw
+    qv = rnd(K, seed=72)
+    ki = torch.empty(k5, device=dev, dtype=torch.int32)
+    kv_ = torch.empty(k5, device=dev)
+    us = _graph_us(torch, stream, lambda i: be.lm_head_knn_dev(hs[i % 2], qv, 1, k5, ki, kv_, stream=stream), 40)
+    hbm("lm_head_knn_q4_0_128256x4096_top5", N * K // 32 * 18 + K * 4 + N * 4, us,
+        {"launches": 3, "timing": "HIP graph replay of 40 calls",
+         "note": "reference comment: ~1 ms for its Q4 lm-head path (LV/src/index/walk.rs:551)"})
+    for h in hs:
+        be.release_weight(h)
+    torch.cuda.empty_cache()
+
+    # multi_layer_q4_ffn (backend.rs:86-96), the trait call with host buffers: 8 layers of
+    # Q4_0 gate/up [10240 x 2560] and down [2560 x 10240], chained; weights uploaded once
+    # (cached by host pointer), then each call uploads x and downloads the output
+    nl, F, K = 8, 10240, 2560
+    host_layers = []
+    for l in range(nl):
+        t3 = []
+        for j, (r, cc) in enumerate(((F, K), (F, K), (K, F))):
+            w = rnd(r, cc, seed=800 + 3 * l + j, std=0.05)
+            raw = torch.empty(r * cc // 32 * 18, dtype=torch.uint8, device=dev)
+            be.quantize_weights_dev(larql_hip.Q4_0, w, r * cc, raw, stream=stream)
+            torch.cuda.synchronize()
+            t3.append(raw.cpu().numpy())
+            del w, raw
+        host_layers.append(tuple(t3))
+    xh = rnd(K, seed=830).cpu().numpy()
+    for _ in range(3):
+        assert be.multi_layer_q4_ffn(host_layers, xh, F, K) is not None
+    ts = []
+    for _ in range(50):
+        t0 = time.perf_counter()
+        be.multi_layer_q4_ffn(host_layers, xh, F, K)
+        ts.append(time.perf_counter() - t0)
+    us = statistics.median(ts) * 1e6
+    hbm("multi_layer_q4_ffn_8x10240x2560", nl * 3 * (F * K // 32 * 18) + 2 * K * 4, us,
+        {"timing": "host wall clock per trait call (median of 50), including the x upload and output download",
+         "launches_per_call": 4 * nl})
+    del host_layers
+    be.synchronize()
+
+    # full_pipeline_q4 (backend.rs:71-84), the trait call with host buffers: 2 layers of the
+    # Llama-3-8B shape in Q4_K, 16 positions with causal attention among them
+    from larql_hip.synth import LLAMA3_8B
+    c8 = LLAMA3_8B
+    h8, i8, nq8, nkv8, hd8, seq8 = c8["hidden"], c8["inter"], c8["nq"], c8["nkv"], c8["hd"], 16
+    qd8, kvd8 = nq8 * hd8, nkv8 * hd8
+    ones8 = np.ones(h8, np.float32)
+    keep, layers8 = [], []
+    for l in range(2):
+        arrs = []
+        for j, (r, cc) in enumerate(((qd8, h8), (kvd8, h8), (kvd8, h8), (h8, qd8), (i8, h8), (i8, h8), (h8, i8))):
+            w = rnd(r, cc, seed=850 + 8 * l + j, std=0.02)
+            raw = torch.empty(r * cc // 256 * 148, dtype=torch.uint8, device=dev)
+            be.quantize_weights_dev(larql_hip.Q4_K, w, r * cc, raw, stream=stream)
+            torch.cuda.synchronize()
+            arrs.append(raw.cpu().numpy())
+            del w, raw
+        keep.append(arrs)
+        layers8.append(larql_hip.make_layer(*arrs, ones8, ones8, head_dim=hd8, num_q_heads=nq8, num_kv_heads=nkv8,
+                                            rope_base=c8["rope"]))
+    x8 = rnd(seq8, h8, seed=870).cpu().numpy()
+    for _ in range(2):
+        assert be.full_pipeline_q4(layers8, x8, h8, i8, qd8, kvd8, seq8, nq8, nkv8, hd8, c8["rope"]) is not None
+    ts = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        be.full_pipeline_q4(layers8, x8, h8, i8, qd8, kvd8, seq8, nq8, nkv8, hd8, c8["rope"])
+        ts.append(time.perf_counter() - t0)
+    ms = statistics.median(ts) * 1e3
+    wbytes = sum(a.nbytes for arrs in keep for a in arrs)
+    out["full_pipeline_q4_2x_llama3_8b_16pos"] = {
+        "ms_per_call": round(ms, 3), "tokens_per_s": round(seq8 / (ms * 1e-3), 1),
+        "weight_bytes": wbytes, "weight_GBs": round(wbytes / (ms * 1e-3) / 1e9, 1),
+        "timing": "host wall clock per trait call (median of 20), including the activation upload and download",
+        "note": "positions 0..15 through 2 Llama-3-8B-shape Q4_K layers, causal attention among them, the decode "
+                "cache untouched"}
+    log(f"[bench] full_pipeline_q4: {out['full_pipeline_q4_2x_llama3_8b_16pos']}")
+    del keep, layers8
+    torch.cuda.empty_cache()
+
     # gate-KNN: 34 layers [10240 x 2560] x 256 queries, top-32
     L, F, K, Q, k = 34, 10240, 2560, 256, 32
     hf, hq = [], []
@@ -603,13 +722,9 @@ def bench_configs(be, torch, stream, copies: int):
         out[f"gate_knn_{name}_34x10240x2560_q256_top32"] = {
             "ms_per_walk": round(us / 1e3, 3), "ops": flops, "achieved": round(t, 1), "unit": unit,
             "roofline": {"bound": bound, "peak": peak, "unit": unit, "frac": round(t / peak, 4)},
-            "note": "f32 scores are canonical fma chains (bit-exact, no MFMA); Q4_0 int32 block dots "
-                    "on v_mfma_i32_16x16x64_i8 vs the int8 MFMA peak; walk includes top-32 selection"}
-        if name == "f32":
-            # the published fp32 peak counts packed (two-wide) FMAs; this build disables
-            # packed fp32 (v_pk_fma_f32), so one fma per lane per issue is its ceiling
-            out[f"gate_knn_{name}_34x10240x2560_q256_top32"]["roofline_unpacked"] = {
-                "peak": 78.6, "unit": unit, "frac": round(t / 78.6, 4)}
+            "note": "f32 scores are canonical fma chains (bit-exact, no MFMA) on v_fmac_f32, against the "
+                    "published 157.3 TFLOP/s fp32 peak; Q4_0 int32 block dots on v_mfma_i32_16x16x64_i8 vs "
+                    "the int8 MFMA peak; walk includes top-32 selection"}
         log(f"[bench] gate_knn {name}: {out[f'gate_knn_{name}_34x10240x2560_q256_top32']}")
     for h in hf + hq:
         be.release_weight(h)
@@ -806,8 +921,10 @@ def main():
         best = min((v, k) for k, v in floors.items())
         per_shape[name] = {"us_per_launch": round(us, 3),
                            "GBs": round(q4k_algorithmic_bytes(rows, cols) / (us * 1e-6) / 1e9, 1),
-                           "read_floor_us": fus, "over_floor": round(us / fus, 3),
-                           "read_floor_best_us": best[0], "read_floor_best_shape": best[1]}
+                           "read_floor_us": fus, "over_own_shape_floor": round(us / fus, 3),
+                           "read_floor_best_us": best[0], "read_floor_best_shape": best[1],
+                           "over_best_floor": round(us / best[0], 3),
+                           "launch": be.q4k_launch_shape(handles[name][0])}
     log(f"[bench] per shape: {per_shape}")
 
     for name in handles:
@@ -836,6 +953,10 @@ def main():
 
     gate_bytes = q4k_algorithmic_bytes(14336, 4096)
     gate_us = per_shape["gate"]["us_per_launch"]
+    sh = per_shape["gate"]["launch"]
+    gate_kernel = (f"q4k_mfma_kernel<{sh['ur']}, {sh['tiles']}, false, 0, {sh['pre']}, "
+                   f"{'true' if sh['xb'] else 'false'}> gate [14336x4096], {sh['workgroups']} x {sh['threads']} "
+                   f"threads, {sh['rounds']} round(s)")
     achieved = gate_bytes / (gate_us * 1e-6) / 1e9
     traffic = None
     if os.path.exists(TRAFFIC_JSON):
@@ -868,13 +989,14 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "q4k_mfma_kernel<2, 2, false, 0, 2, false> gate [14336x4096]",
+            "kernel": gate_kernel,
             "bytes_per_launch": gate_bytes,
             "avg_launch_us": gate_us,
-            "read_floor_us": per_shape["gate"]["read_floor_us"],
-            "frac_of_read_floor": round(per_shape["gate"]["read_floor_us"] / gate_us, 4),
             "read_floor_best_us": per_shape["gate"]["read_floor_best_us"],
             "read_floor_best_shape": per_shape["gate"]["read_floor_best_shape"],
+            "frac_of_read_floor": round(per_shape["gate"]["read_floor_best_us"] / gate_us, 4),
+            "read_floor_own_shape_us": per_shape["gate"]["read_floor_us"],
+            "frac_of_own_shape_floor": round(per_shape["gate"]["read_floor_us"] / gate_us, 4),
         },
         "cpu_baseline": cpu,
         "cpu_baselines": cpu_all,

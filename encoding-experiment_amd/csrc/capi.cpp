@@ -13,6 +13,7 @@
 #include <new>
 
 #include "larql_hip_internal.h"
+#include "matvec_common.h"
 
 using larql::DevWeight;
 using larql::Error;
@@ -71,7 +72,6 @@ static void check_shape(int format, size_t len, size_t rows, size_t cols, int hf
             if (cols % 256) fail(LARQL_HIP_ERR_INVALID, "hidden must be a multiple of 256");
             break;
         case LARQL_F32:
-            if (cols % 16) fail(LARQL_HIP_ERR_INVALID, "f32 gate hidden must be a multiple of 16");
             break;
         default: fail(LARQL_HIP_ERR_INVALID, "unknown quant format");
     }
@@ -84,7 +84,7 @@ static void check_shape(int format, size_t len, size_t rows, size_t cols, int hf
 
 static uint64_t register_impl(larql_hip_ctx* c, int format, const void* data, size_t len,
                               const float* q8_scales, size_t rows, size_t cols, bool on_device) {
-    const int hf = format == LARQL_Q4_KF ? q4kf_form(len, rows, cols) : kHdr148;
+    const int hf = format == LARQL_Q4_KF && rows && cols % 256 == 0 ? q4kf_form_checked(len, rows, cols) : kHdr148;
     check_shape(format, len, rows, cols, hf);
     if (!data) fail(LARQL_HIP_ERR_INVALID, "null weight pointer");
     if (format == LARQL_Q8_0 && !q8_scales) fail(LARQL_HIP_ERR_INVALID, "Q8_0 weights need scales");
@@ -217,7 +217,8 @@ extern "C" void larql_hip_ctx_destroy(larql_hip_ctx* c) {
         }
         for (auto* b : {&c->stage_in, &c->stage_in2, &c->stage_out, &c->stage_raw, &c->scratch, &c->knn_scores,
                         &c->knn_q8, &c->knn_q8s, &c->knn_idx, &c->knn_val, &c->knn_handles, &c->vecmat_part,
-                        &c->pair_q8, &c->pair_q8s, &c->knn_xa, &c->knn_xsp, &c->gemm_x16, &c->ffn_work})
+                        &c->pair_q8, &c->pair_q8s, &c->knn_xa, &c->knn_xsp, &c->knn_xpad, &c->knn_sort, &c->gemm_x16,
+                        &c->ffn_work})
             if (b->p) (void)hipFree(b->p);
         (void)hipStreamDestroy(c->stream);
     }
@@ -391,6 +392,20 @@ extern "C" int larql_hip_read_floor_dev(larql_hip_ctx* c, uint64_t handle, unsig
         if (!out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
         const DevWeight& w = larql::lookup(c, handle);
         larql::launch_q4k_read_floor(w, out, out_words, workgroups, threads, c->num_cus, pick_stream(c, stream));
+    });
+}
+
+extern "C" int larql_hip_q4k_launch_shape(larql_hip_ctx* c, uint64_t handle, int* ur, int* tiles, int* pre, int* xb,
+                                          int* rounds, unsigned* workgroups, unsigned* threads) {
+    return guarded(c, [&] {
+        const larql::Q4kShape sh = larql::q4k_mfma_shape(larql::lookup(c, handle), c->num_cus);
+        if (ur) *ur = sh.ur;
+        if (tiles) *tiles = sh.tiles;
+        if (pre) *pre = sh.pre;
+        if (xb) *xb = sh.xb;
+        if (rounds) *rounds = sh.rounds;
+        if (workgroups) *workgroups = sh.groups;
+        if (threads) *threads = sh.threads;
     });
 }
 

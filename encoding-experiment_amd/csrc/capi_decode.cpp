@@ -127,11 +127,11 @@ DevWeight build_weight(larql_hip_ctx* c, larql_hip_model* m, int format, size_t 
     if (int_fmt && interleave) fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: interleaved Q8_0 / Q4_0 weights");
     // Q4_KF: 144-byte GGUF or 160-byte pre-baked blocks, told apart by length; the sources
     // of one fused weight must agree
-    const int hf = format == LARQL_Q4_KF ? larql::q4kf_form(srcs[0].len, srcs[0].rows, cols) : larql::kHdr148;
+    const int hf = format == LARQL_Q4_KF ? larql::q4kf_form_checked(srcs[0].len, srcs[0].rows, cols) : larql::kHdr148;
     size_t rows = 0;
     for (const Src& s : srcs) {
         if (!s.data) fail(LARQL_HIP_ERR_INVALID, "decode: null weight");
-        if (format == LARQL_Q4_KF && larql::q4kf_form(s.len, s.rows, cols) != hf)
+        if (format == LARQL_Q4_KF && larql::q4kf_form_checked(s.len, s.rows, cols) != hf)
             fail(LARQL_HIP_ERR_INVALID, "decode: fused Q4_KF projections mix the 144- and 160-byte layouts");
         if (s.len < s.rows * larql::ref_row_bytes(format, cols, hf))
             fail(LARQL_HIP_ERR_INVALID, "decode: weight buffer shorter than its shape");

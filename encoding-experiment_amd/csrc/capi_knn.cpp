@@ -51,7 +51,15 @@ void run_scores(larql_hip_ctx* c, const KnnPlan& p, size_t n_layers, const float
     if (nq > 0x7FFFFFFF / static_cast<size_t>(p.K)) fail(LARQL_HIP_ERR_INVALID, "gate KNN: too many queries");
     const int Q = static_cast<int>(nq);
     if (p.format == LARQL_F32) {
-        larql::launch_gate_scores_f32(p.a, static_cast<int>(n_layers), queries, scores, p.F, p.K, Q, s);
+        // rows of the device gate are f32_row_stride(K) apart; queries are padded to match
+        const size_t Kp = larql::f32_row_stride(static_cast<size_t>(p.K));
+        const float* X = queries;
+        if (Kp != static_cast<size_t>(p.K)) {
+            float* xp = static_cast<float*>(larql::ensure(c, c->knn_xpad, nq * Kp * sizeof(float)));
+            larql::launch_pad_rows_f32(queries, xp, nq, static_cast<size_t>(p.K), Kp, 0.0f, s);
+            X = xp;
+        }
+        larql::launch_gate_scores_f32(p.a, static_cast<int>(n_layers), X, scores, p.F, static_cast<int>(Kp), Q, s);
     } else {
         int8_t* q8 = static_cast<int8_t*>(larql::ensure(c, c->knn_q8, nq * p.K));
         float* q8s = static_cast<float*>(larql::ensure(c, c->knn_q8s, nq * (p.K / 32) * sizeof(float)));
@@ -62,10 +70,23 @@ void run_scores(larql_hip_ctx* c, const KnnPlan& p, size_t n_layers, const float
     }
 }
 
-// top_k above the row length is clamped by the kernels (top_k.min(len), LV/src/index/walk.rs:569).
-void check_k(size_t k) {
-    if (k < 1 || k > static_cast<size_t>(larql::kTopkMaxK))
-        fail(LARQL_HIP_ERR_INVALID, "gate KNN: need 1 <= top_k <= LARQL_HIP_TOPK_MAX");
+// top_k above the row length is clamped by the kernels (top_k.min(len), LV/src/index/walk.rs:569);
+// any k >= 1 is taken (the output holds rows x k slots).
+void check_k(size_t k, size_t rows = 1) {
+    if (k < 1 || rows * k >= (size_t{1} << 31)) fail(LARQL_HIP_ERR_INVALID, "top-k: need top_k >= 1 and rows x top_k < 2^31");
+}
+
+// Top-k of rows of n scores: the selection kernels up to LARQL_HIP_TOPK_MAX, above it the
+// sorted path (same order) with a context work buffer.
+void topk_any(larql_hip_ctx* c, const float* S, size_t rows, size_t stride, int n, size_t k, int signed_mode,
+              uint32_t* idx, float* val, hipStream_t s) {
+    if (k <= static_cast<size_t>(larql::kTopkMaxK)) {
+        larql::launch_topk(S, rows, stride, n, static_cast<int>(k), signed_mode, idx, val, s);
+        return;
+    }
+    const size_t wb = larql::topk_sorted_work_bytes(rows, n);
+    void* w = larql::ensure(c, c->knn_sort, wb);
+    larql::launch_topk_sorted(S, rows, stride, n, k, signed_mode, idx, val, w, wb, s);
 }
 
 }  // namespace
@@ -83,12 +104,12 @@ extern "C" int larql_hip_gate_knn_dev(larql_hip_ctx* c, const uint64_t* handles,
                                       void* stream) {
     return guarded(c, [&] {
         const KnnPlan p = plan_layers(c, handles, n_layers);
-        check_k(top_k);
+        check_k(top_k, n_layers * nq);
         if (!idx || !scores) fail(LARQL_HIP_ERR_INVALID, "gate KNN: null outputs");
         hipStream_t s = pick_stream(c, stream);
         float* S = static_cast<float*>(larql::ensure(c, c->knn_scores, n_layers * nq * p.F * sizeof(float)));
         run_scores(c, p, n_layers, queries, nq, S, s);
-        larql::launch_topk(S, n_layers * nq, static_cast<size_t>(p.F), p.F, static_cast<int>(top_k), 0, idx, scores, s);
+        topk_any(c, S, n_layers * nq, static_cast<size_t>(p.F), p.F, top_k, 0, idx, scores, s);
     });
 }
 
@@ -97,10 +118,8 @@ extern "C" int larql_hip_topk_dev(larql_hip_ctx* c, const float* scores, size_t 
     return guarded(c, [&] {
         if (!scores || !idx || !vals) fail(LARQL_HIP_ERR_INVALID, "top-k: null pointer");
         if (n == 0 || n > 0x7FFFFFFF) fail(LARQL_HIP_ERR_INVALID, "top-k: bad row length");
-        if (k < 1 || k > static_cast<size_t>(larql::kTopkMaxK))
-            fail(LARQL_HIP_ERR_INVALID, "top-k: need 1 <= k <= LARQL_HIP_TOPK_MAX");
-        larql::launch_topk(scores, rows, n, static_cast<int>(n), static_cast<int>(k), signed_mode ? 1 : 0, idx, vals,
-                           pick_stream(c, stream));
+        check_k(k, rows);
+        topk_any(c, scores, rows, n, static_cast<int>(n), k, signed_mode ? 1 : 0, idx, vals, pick_stream(c, stream));
     });
 }
 
@@ -114,7 +133,7 @@ extern "C" int larql_hip_gate_knn(larql_hip_ctx* c, int format, const void* gate
         const DevWeight& w = larql::cached_weight(c, format, gate, gate_len, nullptr, features, hidden);
         const uint64_t h = w.handle;
         const KnnPlan p = plan_layers(c, &h, 1);
-        check_k(top_k);
+        check_k(top_k, nq);
         const size_t qbytes = nq * hidden * sizeof(float);
         float* dq = static_cast<float*>(larql::ensure(c, c->stage_in, qbytes));
         LARQL_HIP_CHECK(hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, c->stream));
@@ -122,7 +141,7 @@ extern "C" int larql_hip_gate_knn(larql_hip_ctx* c, int format, const void* gate
         run_scores(c, p, 1, dq, nq, S, c->stream);
         uint32_t* di = static_cast<uint32_t*>(larql::ensure(c, c->knn_idx, nq * top_k * sizeof(uint32_t)));
         float* dv = static_cast<float*>(larql::ensure(c, c->knn_val, nq * top_k * sizeof(float)));
-        larql::launch_topk(S, nq, static_cast<size_t>(p.F), p.F, static_cast<int>(top_k), 0, di, dv, c->stream);
+        topk_any(c, S, nq, static_cast<size_t>(p.F), p.F, top_k, 0, di, dv, c->stream);
         LARQL_HIP_CHECK(hipMemcpyAsync(idx, di, nq * top_k * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
         LARQL_HIP_CHECK(hipMemcpyAsync(scores, dv, nq * top_k * sizeof(float), hipMemcpyDeviceToHost, c->stream));
         LARQL_HIP_CHECK(hipStreamSynchronize(c->stream));
@@ -142,14 +161,17 @@ static void check_lm_head(const DevWeight& w, size_t nq, size_t top_k) {
     if (w.format != LARQL_Q4_0) fail(LARQL_HIP_ERR_UNSUPPORTED, "lm-head KNN: the head must be Q4_0");
     if (nq == 0) fail(LARQL_HIP_ERR_INVALID, "lm-head KNN: nq == 0");
     if (w.rows > 0x7FFFFFFF) fail(LARQL_HIP_ERR_UNSUPPORTED, "lm-head KNN: vocab too large");
-    check_k(top_k);
+    check_k(top_k, nq);
 }
 
-static void launch_lm_head_knn(const DevWeight& w, const float* dq, size_t nq, size_t top_k, const LmHeadBufs& b,
-                               uint32_t* di, float* dv, hipStream_t s) {
+// Scores then the signed top-k (c: the context whose buffer the sorted path of a k above
+// LARQL_HIP_TOPK_MAX uses; null: k must be within it).
+static void launch_lm_head_knn(larql_hip_ctx* c, const DevWeight& w, const float* dq, size_t nq, size_t top_k,
+                               const LmHeadBufs& b, uint32_t* di, float* dv, hipStream_t s) {
     larql::launch_quantize_q8(dq, w.cols, nq, b.q8, b.q8s, s);
     larql::launch_q4_0_matvec(w, b.q8, b.q8s, b.S, nq, s);
-    larql::launch_topk(b.S, nq, w.rows, static_cast<int>(w.rows), static_cast<int>(top_k), 1, di, dv, s);
+    if (c) topk_any(c, b.S, nq, w.rows, static_cast<int>(w.rows), top_k, 1, di, dv, s);
+    else larql::launch_topk(b.S, nq, w.rows, static_cast<int>(w.rows), static_cast<int>(top_k), 1, di, dv, s);
 }
 
 static void run_lm_head_knn(larql_hip_ctx* c, const DevWeight& w, const float* dq, size_t nq, size_t top_k,
@@ -160,7 +182,7 @@ static void run_lm_head_knn(larql_hip_ctx* c, const DevWeight& w, const float* d
     b.q8 = static_cast<int8_t*>(larql::ensure(c, c->knn_q8, nq * hidden));
     b.q8s = static_cast<float*>(larql::ensure(c, c->knn_q8s, nq * nb * sizeof(float)));
     b.S = static_cast<float*>(larql::ensure(c, c->knn_scores, nq * w.rows * sizeof(float)));
-    launch_lm_head_knn(w, dq, nq, top_k, b, di, dv, s);
+    launch_lm_head_knn(c, w, dq, nq, top_k, b, di, dv, s);
 }
 
 // ── the allocation-free lm-head KNN ──────────────────────────────────────
@@ -222,6 +244,8 @@ extern "C" int larql_hip_lm_head_knn_dev_noalloc(larql_hip_ctx* c, uint64_t hand
         if (!queries || !idx || !scores) fail(LARQL_HIP_ERR_INVALID, "lm-head KNN: null pointer");
         const DevWeight& w = larql::lookup(c, handle);
         check_lm_head(w, nq, top_k);
+        if (top_k > static_cast<size_t>(larql::kTopkMaxK))
+            fail(LARQL_HIP_ERR_INVALID, "lm-head KNN (no-alloc): top_k above LARQL_HIP_TOPK_MAX needs a sort buffer");
         uint8_t* base = nullptr;
         {
             std::lock_guard<std::mutex> lk(g_scratch_mu);
@@ -240,6 +264,6 @@ extern "C" int larql_hip_lm_head_knn_dev_noalloc(larql_hip_ctx* c, uint64_t hand
         b.q8 = reinterpret_cast<int8_t*>(base);
         b.q8s = reinterpret_cast<float*>(base + need_q8);
         b.S = reinterpret_cast<float*>(base + need_q8 + need_q8s);
-        launch_lm_head_knn(w, queries, nq, top_k, b, idx, scores, pick_stream(c, stream));
+        launch_lm_head_knn(nullptr, w, queries, nq, top_k, b, idx, scores, pick_stream(c, stream));
     });
 }

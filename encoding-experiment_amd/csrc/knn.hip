@@ -277,15 +277,9 @@ __global__ __launch_bounds__(kThreads, 2) void gate_scores_q4_kernel(KnnLayers g
 // pattern of |s| (abs mode; -0 and +0 equal), or an order-preserving map of s
 // (signed mode).  A radix select over 8-bit digits of c (8 passes) finds the k-th
 // largest composite exactly; the k elements at or above it are ranked and written.
-// (A template parameter, not a run-time flag: a branch per element between a load and
-// its use makes the compiler wait for each load before issuing the next.)
-template <bool SG>
-__device__ __forceinline__ uint32_t order_key(float v) {
-    uint32_t b = __float_as_uint(v);
-    if constexpr (!SG) return b & 0x7FFFFFFFu;
-    if ((b & 0x7FFFFFFFu) == 0) b = 0;  // -0 == +0
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
+// (The sign mode is a template parameter, not a run-time flag: a branch per element
+// between a load and its use makes the compiler wait for each load before issuing the
+// next.)  k32 is order_key<SG> (knn.h).
 
 // Inclusive scan of one value per lane over the wave (DPP within rows of 16, then the
 // row totals through SGPRs).

@@ -95,12 +95,29 @@ constexpr int kHdr148 = 0, kHdrGguf = 1, kHdrKf160 = 2;
 // Bytes per 256-element block of a Q4_K-family header form in the reference layout.
 inline size_t q4k_family_block_bytes(int hf) { return hf == kHdrKf160 ? 160 : hf == kHdrGguf ? 144 : 148; }
 // Q4_KF carries two byte layouts (LC/src/pipeline.rs:15 says 160 bytes, the GPU decode
-// kernels read 144, LC/src/metal/shaders/q4kf_qkv_proj.rs:46): a buffer of exactly
-// rows x blocks x 160 bytes is the pre-baked form, anything else the GGUF form.
+// kernels read 144, LC/src/metal/shaders/q4kf_qkv_proj.rs:46), told apart by length: a
+// buffer of exactly rows x blocks x 160 bytes is the pre-baked form, exactly x 144 the GGUF
+// form; any other length is ambiguous (a 160-byte buffer with slack would read as GGUF
+// blocks) and is refused (q4kf_form_checked).
 inline int q4kf_form(size_t len, size_t rows, size_t cols) {
-    return len == rows * (cols / 256) * 160 ? kHdrKf160 : kHdrGguf;
+    const size_t blocks = rows * (cols / 256);
+    return len == blocks * 160 ? kHdrKf160 : len == blocks * 144 ? kHdrGguf : -1;
+}
+inline int q4kf_form_checked(size_t len, size_t rows, size_t cols) {
+    const int hf = q4kf_form(len, rows, cols);
+    if (hf < 0)
+        fail(LARQL_HIP_ERR_INVALID, "Q4_KF buffer of " + std::to_string(len) + " bytes: must be exactly rows x " +
+                                        std::to_string(cols / 256) + " blocks x 144 (GGUF) or x 160 (pre-baked)");
+    return hf;
 }
 size_t ref_row_bytes(int format, size_t cols, int hf = kHdr148);   // bytes per row in the reference layout
+// f32 gate rows on the device: cols rounded up to a multiple of 16 (the score kernel's
+// k-stage), the extra columns -0.0; a query row is padded with +0.0 to match, so every
+// padded term of a score's fma chain adds -0.0 (the additive identity) and the scores
+// keep their bits.
+inline size_t f32_row_stride(size_t cols) { return (cols + 15) & ~size_t(15); }
+// dst[r][k] = src[r][k] for k < K, `pad` for K <= k < Kp (rows x Kp floats).
+void launch_pad_rows_f32(const float* src, float* dst, size_t rows, size_t K, size_t Kp, float pad, hipStream_t s);
 size_t dev_layout_bytes(int format, size_t rows_pad, size_t cols, int hf = kHdr148);
 inline size_t pad_rows(size_t rows) { return (rows + 63) & ~size_t(63); }
 
@@ -188,8 +205,9 @@ struct larql_hip_ctx {
     std::map<std::pair<const void*, size_t>, uint64_t> by_host;
     // reusable device staging buffers for host-pointer calls
     larql::DeviceBuf stage_in, stage_in2, stage_out, stage_raw, scratch;
-    // gate-KNN work buffers: scores [layers][nq][features], quantized queries
-    larql::DeviceBuf knn_scores, knn_q8, knn_q8s, knn_idx, knn_val, knn_handles, knn_xa, knn_xsp;
+    // gate-KNN work buffers: scores [layers][nq][features], quantized queries, f32 queries
+    // padded to the gate row stride
+    larql::DeviceBuf knn_scores, knn_q8, knn_q8s, knn_idx, knn_val, knn_handles, knn_xa, knn_xsp, knn_xpad, knn_sort;
     // q4_vecmat chunk partials; pair-batch quantized activations
     larql::DeviceBuf vecmat_part, pair_q8, pair_q8s;
     // prefill GEMM: X as fp16 MFMA operands

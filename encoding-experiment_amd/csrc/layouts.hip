@@ -39,9 +39,24 @@ size_t dev_layout_bytes(int format, size_t rows, size_t cols, int hf) {
         case LARQL_Q6_K: return align256(rows * (cols / 256) * 210);  // rows % 16 == 0: kQ6Block per tile
         case LARQL_Q8_0:  // rows % 16 == 0: q8_piece / q8_scale_index
             return align256(rows / 16 * q8_pairs(cols / 32) * 1024) + align256(rows / 16 * q8_pairs(cols / 32) * 128);
-        case LARQL_F32: return align256(rows * cols * 4);
+        case LARQL_F32: return align256(rows * f32_row_stride(cols) * 4);
         default: return 0;
     }
+}
+
+__global__ void pad_rows_f32_kernel(const float* __restrict__ src, float* __restrict__ dst, size_t rows, size_t K,
+                                    size_t Kp, float pad) {
+    const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    if (i >= rows * Kp) return;
+    const size_t r = i / Kp, k = i - r * Kp;
+    dst[i] = k < K ? src[r * K + k] : pad;
+}
+
+void launch_pad_rows_f32(const float* src, float* dst, size_t rows, size_t K, size_t Kp, float pad, hipStream_t s) {
+    const size_t n = rows * Kp;
+    if (n == 0) return;
+    pad_rows_f32_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(src, dst, rows, K, Kp, pad);
+    LARQL_HIP_CHECK(hipGetLastError());
 }
 
 void dev_layout_carve(DevWeight& w) {
@@ -273,8 +288,13 @@ void launch_repack(const DevWeight& w, const uint8_t* raw, const float* q8_scale
         }
         case LARQL_F32: {
             if (stride != 1) fail(LARQL_HIP_ERR_UNSUPPORTED, "repack: interleaved f32");
-            LARQL_HIP_CHECK(hipMemcpyAsync(w.qs + row0 * w.cols * 4, raw, src_rows * w.cols * 4,
-                                           hipMemcpyDeviceToDevice, s));
+            const size_t Kp = f32_row_stride(w.cols);
+            if (Kp == w.cols)
+                LARQL_HIP_CHECK(hipMemcpyAsync(w.qs + row0 * w.cols * 4, raw, src_rows * w.cols * 4,
+                                               hipMemcpyDeviceToDevice, s));
+            else
+                launch_pad_rows_f32(reinterpret_cast<const float*>(raw), reinterpret_cast<float*>(w.qs) + row0 * Kp,
+                                    src_rows, w.cols, Kp, -0.0f, s);
             break;
         }
         default: fail(LARQL_HIP_ERR_UNSUPPORTED, "repack: unsupported format");

@@ -112,5 +112,11 @@ void launch_q6k_mfma(const DevWeight& w, MvArgs a, hipStream_t s);
 // the most partial sums its launch can take as a consumer (two per thread).
 int q4k_mfma_groups(const DevWeight& w, int num_cus);
 int q4k_mfma_max_psum(const DevWeight& w, int num_cus);
+// The launch split of the weight's m = 1 matvec (pick_q4k_split) and its grid.
+struct Q4kShape {
+    int ur, tiles, pre, xb, rounds;
+    unsigned groups, threads;
+};
+Q4kShape q4k_mfma_shape(const DevWeight& w, int num_cus);
 
 }  // namespace larql

@@ -427,6 +427,17 @@ int q4k_mfma_groups(const DevWeight& w, int num_cus) {
     return static_cast<int>(w.rows_pad / (16 * pick_q4k_split(w, num_cus).t));
 }
 
+Q4kShape q4k_mfma_shape(const DevWeight& w, int num_cus) {
+    if ((w.format != LARQL_Q4_K && w.format != LARQL_Q4_KF) || w.cols % 256 != 0 || w.cols == 0 || w.rows_pad % 16 != 0)
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "q4k launch shape: not a Q4_K-family weight");
+    if (num_cus <= 0) num_cus = current_device_cus();
+    const Q4kSplit sp = pick_q4k_split(w, num_cus);
+    const size_t S = w.cols / 256;
+    const unsigned waves = static_cast<unsigned>((S + sp.ur * sp.R - 1) / (sp.ur * sp.R));
+    return Q4kShape{sp.ur, sp.t, sp.pre, sp.xb ? 1 : 0, sp.R, static_cast<unsigned>(w.rows_pad / (16 * sp.t)),
+                    64 * waves};
+}
+
 int q4k_mfma_max_psum(const DevWeight& w, int num_cus) {
     if (num_cus <= 0) num_cus = current_device_cus();
     const Q4kSplit sp = pick_q4k_split(w, num_cus);

@@ -62,6 +62,7 @@ SIGNATURES = {
     "larql_hip_q4_matvec_pair_batch": (_I, [_P, _P, _SZ, _P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ]),
     "larql_hip_vecmat_dev": (_I, [_P, _U64, _P, _P, _P]),
     "larql_hip_read_floor_dev": (_I, [_P, _U64, ctypes.c_uint, ctypes.c_uint, _P, _SZ, _P]),
+    "larql_hip_q4k_launch_shape": (_I, [_P, _U64, _P, _P, _P, _P, _P, _P, _P]),
     "larql_hip_pair_batch_dev": (_I, [_P, _U64, _U64, _P, _SZ, _P, _P, _P]),
     "larql_hip_q4k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
     "larql_hip_q6k_matvec": (_I, [_P, _P, _SZ, _P, _P, _SZ, _SZ]),
@@ -605,6 +606,17 @@ class HipBackend:
         out: device int32/uint32 tensor, one XOR fold per workgroup."""
         self._check(self._lib.larql_hip_read_floor_dev(self._ctx, handle, workgroups, threads, _dptr(out),
                                                        out.numel(), _stream_ptr(stream)))
+
+    def q4k_launch_shape(self, handle: int) -> dict:
+        """The launch configuration of a registered Q4_K / Q4_KF weight's matvec: ur, tiles,
+        pre, xb, rounds (q4k_mfma_kernel<ur, tiles, norm, header, pre, xb>) and its grid."""
+        v = [ctypes.c_int() for _ in range(5)]
+        g, t = ctypes.c_uint(), ctypes.c_uint()
+        self._check(self._lib.larql_hip_q4k_launch_shape(self._ctx, handle, *[ctypes.byref(x) for x in v],
+                                                         ctypes.byref(g), ctypes.byref(t)))
+        d = dict(zip(("ur", "tiles", "pre", "xb", "rounds"), (x.value for x in v)))
+        d.update(workgroups=g.value, threads=t.value)
+        return d
 
     def pair_batch_dev(self, gate: int, up: int, x, seq_len: int, gate_out, up_out, stream=None):
         self._check(self._lib.larql_hip_pair_batch_dev(self._ctx, gate, up, _dptr(x), seq_len, _dptr(gate_out),

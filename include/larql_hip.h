@@ -47,16 +47,18 @@ typedef struct larql_hip_ctx larql_hip_ctx;
 #define LARQL_HIP_ERR_STATE (-5)       /* e.g. KV cache not initialised */
 
 /* QuantFormat — LC/src/pipeline.rs:12-19 (same discriminant order).  LARQL_F32 is an
- * extension with no QuantFormat counterpart: plain f32 [rows][cols], the vindex's f32
- * gate vectors (LV/src/index/gate.rs:14-29), usable only by the gate-KNN entry points.
+ * extension with no QuantFormat counterpart: plain f32 [rows][cols] (any cols), the
+ * vindex's f32 gate vectors (LV/src/index/gate.rs:14-29), usable only by the gate-KNN
+ * entry points.
  * LARQL_Q4_KF takes both byte layouts the reference gives that name, told apart by the
  * buffer length: exactly rows x (cols/256) x 160 bytes is the pre-baked form
  * ([8 x f16 d*sc_j][8 x f16 dmin*m_j][128 B nibbles], q4k_to_q4kf,
- * LC/src/cpu/ops/q4_common.rs:370-413; pipeline.rs:15); any other length is read as
- * 144-byte GGUF blocks in the layout the reference's GPU decode reads for Q4_KF
+ * LC/src/cpu/ops/q4_common.rs:370-413; pipeline.rs:15); exactly rows x (cols/256) x 144
+ * bytes is read as GGUF blocks in the layout the reference's GPU decode reads for Q4_KF
  * (llama.cpp block_q4_K: 6-bit scales and mins packed in 12 bytes, chunk c of 32 bytes
  * holding sub-block 2c in its low and 2c + 1 in its high nibbles;
- * LC/src/metal/shaders/q4kf_qkv_proj.rs:87-119). */
+ * LC/src/metal/shaders/q4kf_qkv_proj.rs:87-119).  Any other length, trailing bytes
+ * included, is LARQL_HIP_ERR_INVALID (it could not be told apart). */
 typedef enum {
     LARQL_Q4_0 = 0,
     LARQL_Q4_K = 1,
@@ -207,6 +209,14 @@ int larql_hip_matvec_dev(larql_hip_ctx* ctx, uint64_t handle, const void* x, con
 int larql_hip_read_floor_dev(larql_hip_ctx* ctx, uint64_t handle, unsigned workgroups, unsigned threads,
                              uint32_t* out, size_t out_words, void* stream);
 
+/* Measurement aid with no counterpart in the reference: the launch configuration of a
+ * registered Q4_K / Q4_KF weight's m = 1 matvec (q4k_mfma_kernel<ur, tiles, norm, header,
+ * pre, xb>): super-blocks per wave and round (ur), 16-row tiles per workgroup, units whose
+ * loads are issued with x (pre), the x-first barrier (xb, 0 or 1), rounds per wave, and
+ * the grid (workgroups x threads per workgroup).  Any pointer may be NULL. */
+int larql_hip_q4k_launch_shape(larql_hip_ctx* ctx, uint64_t handle, int* ur, int* tiles, int* pre, int* xb,
+                               int* rounds, unsigned* workgroups, unsigned* threads);
+
 /* q4_vecmat with a registered Q4_0 weight (rows = intermediate, cols = hidden), device
  * activation f32 [rows] and output f32 [cols].  Uses a partials buffer owned by the
  * context: device calls on one context must not overlap on different streams. */
@@ -229,9 +239,12 @@ int larql_hip_quantize_weights_dev(larql_hip_ctx* ctx, int format, const float* 
 
 /* ── vindex gate-KNN (vindex code, not trait methods: LV/src/index/gate.rs) ── */
 
-/* Largest top_k and number of layers per call.  A top_k above a row's length returns the
- * whole row ranked (top_k.min(len), LV/src/index/walk.rs:569): slots past the row length
- * hold index 0xFFFFFFFF and score 0. */
+/* Largest top_k of the selection kernels, and the most layers per call.  The entry points
+ * that allocate take any top_k >= 1 (rows x top_k < 2^31), as the reference does: above
+ * LARQL_HIP_TOPK_MAX a row is ranked by a sort (same order, more time and a work buffer);
+ * the allocation-free entry point keeps the bound.  A top_k above a row's length returns
+ * the whole row ranked (top_k.min(len), LV/src/index/walk.rs:569): slots past the row
+ * length hold index 0xFFFFFFFF and score 0. */
 #define LARQL_HIP_TOPK_MAX 512
 #define LARQL_HIP_KNN_MAX_LAYERS 64
 
@@ -257,13 +270,13 @@ int larql_hip_gate_scores_dev(larql_hip_ctx* ctx, const uint64_t* handles, size_
 
 /* Top-k of each row of a device score matrix [rows][n]: signed_mode 0 orders by |score|
  * (gate.rs:307-316), 1 by the signed score (lm-head KNN, LV/src/index/walk.rs:563-580).
- * Ties in index order.  idx / vals [rows][k] (device), 1 <= k <= LARQL_HIP_TOPK_MAX. */
+ * Ties in index order.  idx / vals [rows][k] (device), k >= 1. */
 int larql_hip_topk_dev(larql_hip_ctx* ctx, const float* scores, size_t rows, size_t n, size_t k, int signed_mode,
                        uint32_t* idx, float* vals, void* stream);
 
 /* lm-head KNN, the Q4 path of VectorIndex::lm_head_knn_backend (LV/src/index/walk.rs:549-583):
  * query quantized by quantize_to_q8, scores = q4_matvec(lm_head_q4 [vocab][hidden] Q4_0),
- * the top_k tokens by signed score descending (ties in index order), 1 <= top_k <= LARQL_HIP_TOPK_MAX.
+ * the top_k tokens by signed score descending (ties in index order), top_k >= 1.
  * Host-pointer form: lm_head_q4 / query / idx / scores in host memory (the head is
  * uploaded once and cached like every weight). */
 int larql_hip_lm_head_knn(larql_hip_ctx* ctx, const uint8_t* lm_head_q4, size_t len, const float* query,
@@ -283,7 +296,8 @@ int larql_hip_lm_head_knn_dev(larql_hip_ctx* ctx, uint64_t handle, const float* 
  * live in a fixed device array of LARQL_HIP_NOALLOC_SCRATCH_BYTES per GPU (8 MiB, held
  * until the process ends), which limits a call to
  *   nq * (vocab * 4 + hidden * 9 / 8) (+ alignment) <= 8 MiB
- * (vocab 128256: up to 16 queries); larger requests return LARQL_HIP_ERR_INVALID.  Every
+ * (vocab 128256: up to 16 queries), and top_k <= LARQL_HIP_TOPK_MAX (a larger top_k
+ * needs a sort buffer); larger requests return LARQL_HIP_ERR_INVALID.  Every
  * call on one GPU shares that array: calls that overlap on one GPU (different streams or
  * contexts) race. */
 int larql_hip_lm_head_knn_dev_noalloc(larql_hip_ctx* ctx, uint64_t handle, const float* queries, size_t nq,

@@ -2,6 +2,11 @@
 
   known_answers.json  Known-answer data copied (as data) from the reference's own
                       unit tests, each entry citing its source file:line.
+  ui_walk_trace_vindex.npz
+                      The f32 gate vectors [2 layers][4 features][hidden 8] and the
+                      embeddings [16][8] of the reference's fixture vindex
+                      (larql-python/tests/fixtures/ui_walk_trace_vindex/, gate_vectors.bin
+                      and embeddings.bin as index.json lays them out), copied as data.
   q4_0_ref.npz        Inputs and outputs of the reference's own C kernel
                       (larql-compute/csrc/q4_dot.c, x86 scalar path), compiled in
                       place by oracle/Makefile into oracle/_ref/libq4dot_ref.so.
@@ -89,13 +94,38 @@ KNOWN = {
             {"layer": 0, "query": [1, 0, 0, 0], "k": 1, "idx": [0], "score": [1.0]},
             {"layer": 0, "query": [0.8, 0.6, 0, 0], "k": 3, "idx_prefix": [0, 1]},
         ],
+        # gate_walk_matches_gate_knn (test_vindex.rs:2474-2488): the same features in the
+        # same order as gate_knn, scores within 1e-5
+        "walk_case": {"source": "larql-vindex/tests/test_vindex.rs:2474-2488", "layer": 0,
+                      "query": [1.0, 0.5, 0.0, 0.0], "k": 3},
     },
 }
+
+FIXTURE_VINDEX = "/root/reference/larql-main/crates/larql-python/tests/fixtures/ui_walk_trace_vindex"
+
+
+def fixture_vindex():
+    """The fixture vindex's gate vectors and embeddings (f32 files laid out by index.json:
+    layer l's gates at its byte offset, num_features x hidden_size; embeddings vocab x
+    hidden), or None when the reference tree is absent."""
+    if not os.path.isdir(FIXTURE_VINDEX):
+        return None
+    with open(os.path.join(FIXTURE_VINDEX, "index.json")) as f:
+        idx = json.load(f)
+    hidden, vocab = idx["hidden_size"], idx["vocab_size"]
+    raw = np.fromfile(os.path.join(FIXTURE_VINDEX, "gate_vectors.bin"), dtype=np.float32)
+    gates = np.stack([raw[L["offset"] // 4: (L["offset"] + L["length"]) // 4].reshape(L["num_features"], hidden)
+                      for L in idx["layers"]])
+    emb = np.fromfile(os.path.join(FIXTURE_VINDEX, "embeddings.bin"), dtype=np.float32).reshape(vocab, hidden)
+    return {"gates": gates, "embeddings": emb, "hidden": np.int64(hidden)}
 
 
 def main():
     with open(os.path.join(HERE, "known_answers.json"), "w") as f:
         json.dump(KNOWN, f, indent=1)
+    fv = fixture_vindex()
+    if fv is not None:
+        np.savez_compressed(os.path.join(HERE, "ui_walk_trace_vindex.npz"), **fv)
 
     if oracle.ref_lib() is None:
         print("oracle/_ref/libq4dot_ref.so not built; skipping q4_0_ref.npz")

@@ -633,3 +633,47 @@ def test_vindex_file_layers_match_direct_layers(hip, tmp_path, formats):
         outs.append((pre, nxt))
     print(f"[vindex] formats={formats}: prefill and next token compared", flush=True)
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+
+
+def test_decode_step_inside_cache_capacity_captures_without_allocating(hip):
+    """A decode step inside the KV capacity allocates nothing and synchronises nothing, so it
+    records into a HIP graph: here the captured step is the first at T = 65, one more
+    position split than any step before it (the attention partials are sized by the
+    cache capacity, not by T).  Three replays, with eager work and synchronisations
+    between them, give the eager step's hidden state bit for bit."""
+    torch = pytest.importorskip("torch")
+    n_layers, hidden, inter, nq, nkv, hd, T0 = 2, 512, 1024, 8, 2, 64, 63
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=T0 + 3, seed=33)
+    kvd = nkv * hd
+    hip.reset_kv_cache()
+    for l in range(n_layers):
+        hip.populate_kv_layer(l, oracle.gauss(7000 + l, T0 * kvd), oracle.gauss(7100 + l, T0 * kvd), T0, nkv, hd)
+    model = hip.model(m.hip_layers(10000.0), hidden, inter)
+    try:
+        side = torch.cuda.Stream()
+        x1 = torch.from_numpy(oracle.gauss(7200, hidden)).cuda()
+        x2 = torch.from_numpy(oracle.gauss(7201, hidden)).cuda()
+        h1 = torch.empty(hidden, device="cuda")
+        hg = torch.full((hidden,), 7.0, device="cuda")
+        href = torch.empty(hidden, device="cuda")
+        model.decode_dev(x1, hidden_out=h1, stream=side)   # T = 64: one position split
+        side.synchronize()
+        print("[decode-graph] capturing the step at T = 65", flush=True)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            model.decode_dev(x2, hidden_out=hg, stream=side)   # T = 65: two splits
+        hip.kv_truncate(T0 + 1)
+        model.decode_dev(x2, hidden_out=href, stream=side)
+        side.synchronize()
+        ref = href.cpu().numpy()
+        for rep in range(3):
+            hip.kv_truncate(T0 + 1)
+            hg.fill_(7.0)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(hg.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+        del graph
+    finally:
+        model.close()
+        hip.reset_kv_cache()

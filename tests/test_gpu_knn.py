@@ -245,14 +245,76 @@ def test_topk_k_above_row_length_is_clamped(hip):
     assert np.all(got[0][0, 8:] == 0xFFFFFFFF) and np.all(got[1][0, 8:] == 0.0)
 
 
+@pytest.mark.parametrize("signed", [False, True])
+def test_topk_k_above_selection_bound_sorts(hip, signed):
+    """A top_k above LARQL_HIP_TOPK_MAX (512) is taken, as the reference clamps k only to the
+    row length (gate.rs:307-316; range-filtered callers ask for top_k * 10, gate.rs:300):
+    rows are ranked by a stable sort in the same order (key descending, index ascending).
+    Random rows of the gate and lm-head widths, rows with mass ties and +-0, k up to and
+    past the row length."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(54)
+    for n in (10240, 128256, 700):
+        rows = rng.standard_normal((3, n)).astype(np.float32)
+        rows[1, ::3] = 0.0
+        rows[1, 1::7] = -0.0
+        rows[2, rng.choice(n, n // 2, replace=False)] = 1.25   # ties across the k-th place
+        rows[2, ::11] = -1.25
+        for k in (513, 600, 1000, n, n + 37):
+            print(f"[topk sort] n={n} k={k} signed={signed}", flush=True)
+            gi, gv = _topk_rows(hip, torch, rows, k, signed)
+            for r in range(rows.shape[0]):
+                ri, rv = (oracle.topk_signed if signed else oracle.topk_abs)(rows[r], k)
+                m = min(k, n)
+                np.testing.assert_array_equal(gi[r, :m], ri, err_msg=f"n={n} k={k} row={r}")
+                np.testing.assert_array_equal(gv[r, :m].view(np.uint32), rv.view(np.uint32))
+                assert np.all(gi[r, m:] == 0xFFFFFFFF) and np.all(gv[r, m:] == 0.0)
+
+
+def test_gate_knn_k_above_selection_bound(hip):
+    """gate_knn with top_k = 320 and 1000 (the reference's top_k * 10 fallback sizes) through
+    the host and device entry points, f32 and Q4_0, bit-exact with the oracle."""
+    torch = pytest.importorskip("torch")
+    features, hidden, nq = 4000, 256, 5
+    gate = oracle.gauss(91, features * hidden, 0.0, 0.02).reshape(features, hidden)
+    queries = oracle.gauss(92, nq * hidden).reshape(nq, hidden)
+    q4 = oracle.quantize_q4_0(gate.reshape(-1))
+    for k in (320, 1000):
+        print(f"[knn sort] F={features} K={hidden} nq={nq} k={k}", flush=True)
+        got = hip.gate_knn(gate, features, hidden, queries, k, fmt=larql_hip.F32)
+        ri, rv = oracle_knn_f32(gate, queries, features, hidden, k)
+        np.testing.assert_array_equal(got[0], ri)
+        np.testing.assert_array_equal(got[1].view(np.uint32), rv.view(np.uint32))
+        got = hip.gate_knn(q4, features, hidden, queries, k, fmt=larql_hip.Q4_0)
+        ri, rv = oracle_knn_q4(q4, queries, features, hidden, k)
+        np.testing.assert_array_equal(got[0], ri)
+        np.testing.assert_array_equal(got[1].view(np.uint32), rv.view(np.uint32))
+    h = hip.register_weight(larql_hip.Q4_0, q4, features, hidden)
+    try:
+        dq = torch.from_numpy(np.ascontiguousarray(queries, dtype=np.float32)).cuda()
+        k = 777
+        di = torch.empty(2 * nq * k, device="cuda", dtype=torch.int32)
+        dv = torch.empty(2 * nq * k, device="cuda", dtype=torch.float32)
+        hip.gate_knn_dev([h, h], dq, nq, k, di, dv)
+        hip.synchronize()
+        ri, rv = oracle_knn_q4(q4, queries, features, hidden, k)
+        gi = di.cpu().numpy().view(np.uint32).reshape(2, nq, k)
+        gv = dv.cpu().numpy().reshape(2, nq, k)
+        for l in range(2):
+            np.testing.assert_array_equal(gi[l], ri)
+            np.testing.assert_array_equal(gv[l].view(np.uint32), rv.view(np.uint32))
+    finally:
+        hip.release_weight(h)
+
+
 def test_topk_invalid_k_returns_none():
     be = larql_hip.HipBackend(0, strict=False)
     try:
         gate = np.zeros((8, 64), np.float32)
         q = np.zeros(64, np.float32)
-        assert be.gate_knn(gate, 8, 64, q, 0, fmt=larql_hip.F32) is None      # k = 0
-        assert be.gate_knn(gate, 8, 64, q, 513, fmt=larql_hip.F32) is None    # k > LARQL_HIP_TOPK_MAX
-        assert be.gate_knn(gate, 8, 64, q, 4, fmt=larql_hip.Q4_K) is None     # unsupported format
+        assert be.gate_knn(gate, 8, 64, q, 0, fmt=larql_hip.F32) is None          # k = 0
+        assert be.gate_knn(gate, 8, 64, q, 1 << 31, fmt=larql_hip.F32) is None    # rows x k >= 2^31
+        assert be.gate_knn(gate, 8, 64, q, 4, fmt=larql_hip.Q4_K) is None         # unsupported format
     finally:
         be.close()
 

@@ -96,11 +96,15 @@ def test_q4kf_gguf_equals_q4k_on_converted_blocks(hip):
     assert np.array_equal(a, b)
 
 
-def test_q4kf_wrong_length_is_an_error():
+@pytest.mark.parametrize("nbytes", [10 * 143, 10 * 160 + 16, 10 * 144 + 16, 10 * 160 + 160, 10 * 152])
+def test_q4kf_wrong_length_is_an_error(nbytes):
+    """A Q4_KF buffer is exactly 144 or exactly 160 bytes per block: shorter, or either form
+    with trailing slack (which would otherwise read a 160-byte buffer as GGUF blocks), is an
+    error, not a silent misread."""
     be = larql_hip.HipBackend(0, strict=False)
     try:
-        raw = np.zeros(10 * 143, np.uint8)   # neither 144 nor 160 bytes per block
-        with pytest.raises(larql_hip.LarqlHipError):
+        raw = np.zeros(nbytes, np.uint8)   # 10 rows of one 256-element block
+        with pytest.raises(larql_hip.LarqlHipError, match="Q4_KF buffer"):
             be.register_weight(larql_hip.Q4_KF, raw, 10, 256)
     finally:
         be.close()

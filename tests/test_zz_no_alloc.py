@@ -60,3 +60,45 @@ def test_lm_head_knn_noalloc_rejects_oversized_requests():
         be.release_weight(h)
     finally:
         be.close()
+
+
+def test_lm_head_knn_noalloc_first_call_is_captured_without_allocating():
+    """On a fresh context the allocation-free entry point runs before any allocating KNN
+    call, and inside a stream capture, where a device allocation or synchronisation would
+    fail the capture.  The captured graph, replayed three times with eager work and
+    synchronisations between the replays, gives the allocating entry point's indices and
+    scores bit for bit (that one runs after the capture, so nothing it allocates can have
+    served the captured call)."""
+    torch = pytest.importorskip("torch")
+    be = larql_hip.HipBackend(0, strict=True)
+    try:
+        vocab, hidden, nq, k = 32768, 512, 2, 16
+        head = oracle.quantize_q4_0(oracle.gauss(81, vocab * hidden, 0.0, 0.02))
+        h = be.register_weight(larql_hip.Q4_0, head, vocab, hidden)
+        queries = oracle.gauss(82, nq * hidden).reshape(nq, hidden)
+        dq = torch.from_numpy(np.ascontiguousarray(queries, dtype=np.float32)).cuda()
+        gi = torch.full((nq * k,), -7, device="cuda", dtype=torch.int32)
+        gv = torch.full((nq * k,), 7.0, device="cuda", dtype=torch.float32)
+        side = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        print(f"[noalloc] capture: vocab={vocab} hidden={hidden} nq={nq} k={k}", flush=True)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            be.lm_head_knn_dev_noalloc(h, dq, nq, k, gi, gv, stream=side)
+        ri = torch.empty_like(gi)
+        rv = torch.empty_like(gv)
+        be.lm_head_knn_dev(h, dq, nq, k, ri, rv)
+        be.synchronize()
+        ref_i, ref_v = ri.cpu().numpy(), rv.cpu().numpy()
+        for rep in range(3):
+            gi.fill_(-7)
+            gv.fill_(7.0)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(gi.cpu().numpy(), ref_i)
+            np.testing.assert_array_equal(gv.cpu().numpy().view(np.uint32), ref_v.view(np.uint32))
+        del graph
+        be.release_weight(h)
+    finally:
+        be.close()
