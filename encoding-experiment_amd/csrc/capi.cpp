@@ -217,7 +217,7 @@ extern "C" void larql_hip_ctx_destroy(larql_hip_ctx* c) {
         }
         for (auto* b : {&c->stage_in, &c->stage_in2, &c->stage_out, &c->stage_raw, &c->scratch, &c->knn_scores,
                         &c->knn_q8, &c->knn_q8s, &c->knn_idx, &c->knn_val, &c->knn_handles, &c->vecmat_part,
-                        &c->pair_q8, &c->pair_q8s, &c->knn_xa, &c->knn_xsp, &c->knn_xpad, &c->knn_sort, &c->gemm_x16,
+                        &c->pair_q8, &c->pair_q8s, &c->knn_xa, &c->knn_xsp, &c->knn_xpad, &c->knn_sort, &c->knn_cand, &c->gemm_x16,
                         &c->ffn_work})
             if (b->p) (void)hipFree(b->p);
         (void)hipStreamDestroy(c->stream);

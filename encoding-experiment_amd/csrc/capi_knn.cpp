@@ -81,7 +81,14 @@ void check_k(size_t k, size_t rows = 1) {
 void topk_any(larql_hip_ctx* c, const float* S, size_t rows, size_t stride, int n, size_t k, int signed_mode,
               uint32_t* idx, float* val, hipStream_t s) {
     if (k <= static_cast<size_t>(larql::kTopkMaxK)) {
-        larql::launch_topk(S, rows, stride, n, static_cast<int>(k), signed_mode, idx, val, s);
+        const size_t slots = larql::topk_candidate_slots(rows, n, static_cast<int>(k));
+        uint32_t* ci = nullptr;
+        float* cv = nullptr;
+        if (slots) {  // long rows: chunks on many CUs, then their candidates
+            ci = static_cast<uint32_t*>(larql::ensure(c, c->knn_cand, 2 * slots * sizeof(uint32_t)));
+            cv = reinterpret_cast<float*>(ci + slots);
+        }
+        larql::launch_topk(S, rows, stride, n, static_cast<int>(k), signed_mode, idx, val, s, ci, cv);
         return;
     }
     const size_t wb = larql::topk_sorted_work_bytes(rows, n);
@@ -155,6 +162,8 @@ struct LmHeadBufs {
     int8_t* q8;
     float* q8s;
     float* S;
+    uint32_t* ci = nullptr;  // top-k chunk candidates (topk_candidate_slots)
+    float* cv = nullptr;
 };
 
 static void check_lm_head(const DevWeight& w, size_t nq, size_t top_k) {
@@ -164,14 +173,14 @@ static void check_lm_head(const DevWeight& w, size_t nq, size_t top_k) {
     check_k(top_k, nq);
 }
 
-// Scores then the signed top-k (c: the context whose buffer the sorted path of a k above
-// LARQL_HIP_TOPK_MAX uses; null: k must be within it).
+// Scores then the signed top-k (c: the context whose buffers the top-k uses; null: k within
+// LARQL_HIP_TOPK_MAX and the chunk candidates in b.ci / b.cv).
 static void launch_lm_head_knn(larql_hip_ctx* c, const DevWeight& w, const float* dq, size_t nq, size_t top_k,
                                const LmHeadBufs& b, uint32_t* di, float* dv, hipStream_t s) {
     larql::launch_quantize_q8(dq, w.cols, nq, b.q8, b.q8s, s);
     larql::launch_q4_0_matvec(w, b.q8, b.q8s, b.S, nq, s);
     if (c) topk_any(c, b.S, nq, w.rows, static_cast<int>(w.rows), top_k, 1, di, dv, s);
-    else larql::launch_topk(b.S, nq, w.rows, static_cast<int>(w.rows), static_cast<int>(top_k), 1, di, dv, s);
+    else larql::launch_topk(b.S, nq, w.rows, static_cast<int>(w.rows), static_cast<int>(top_k), 1, di, dv, s, b.ci, b.cv);
 }
 
 static void run_lm_head_knn(larql_hip_ctx* c, const DevWeight& w, const float* dq, size_t nq, size_t top_k,
@@ -254,16 +263,23 @@ extern "C" int larql_hip_lm_head_knn_dev_noalloc(larql_hip_ctx* c, uint64_t hand
         if (!base) fail(LARQL_HIP_ERR_STATE, "lm-head KNN (no-alloc): scratch address not set up for this device");
         const size_t hidden = w.cols, nb = hidden / 32;
         const size_t need_q8 = align256(nq * hidden), need_q8s = align256(nq * nb * sizeof(float));
-        const size_t need_s = nq * w.rows * sizeof(float);
-        if (need_s / sizeof(float) / nq != w.rows || need_q8 + need_q8s + need_s > LARQL_HIP_NOALLOC_SCRATCH_BYTES)
-            fail(LARQL_HIP_ERR_INVALID, "lm-head KNN (no-alloc): nq * (vocab * 4 + hidden * 9 / 8) needs " +
-                                            std::to_string(need_q8 + need_q8s + need_s) + " bytes; the fixed scratch "
-                                            "holds " + std::to_string(LARQL_HIP_NOALLOC_SCRATCH_BYTES));
+        const size_t need_s = align256(nq * w.rows * sizeof(float));
+        const size_t slots = larql::topk_candidate_slots(nq, static_cast<int>(w.rows), static_cast<int>(top_k));
+        const size_t need_c = 2 * slots * sizeof(uint32_t);
+        const size_t need = need_q8 + need_q8s + need_s + need_c;
+        if (nq * w.rows * sizeof(float) / sizeof(float) / nq != w.rows || need > LARQL_HIP_NOALLOC_SCRATCH_BYTES)
+            fail(LARQL_HIP_ERR_INVALID, "lm-head KNN (no-alloc): nq * (vocab * 4 + hidden * 9 / 8) plus the top-k "
+                                        "candidates needs " + std::to_string(need) + " bytes; the fixed scratch "
+                                        "holds " + std::to_string(LARQL_HIP_NOALLOC_SCRATCH_BYTES));
         // every byte the kernels read is written first in the same call: nothing to clear
         LmHeadBufs b;
         b.q8 = reinterpret_cast<int8_t*>(base);
         b.q8s = reinterpret_cast<float*>(base + need_q8);
         b.S = reinterpret_cast<float*>(base + need_q8 + need_q8s);
+        if (slots) {
+            b.ci = reinterpret_cast<uint32_t*>(base + need_q8 + need_q8s + need_s);
+            b.cv = reinterpret_cast<float*>(b.ci + slots);
+        }
         launch_lm_head_knn(nullptr, w, queries, nq, top_k, b, idx, scores, pick_stream(c, stream));
     });
 }

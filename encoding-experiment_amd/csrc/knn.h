@@ -35,8 +35,12 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 
 // Top-k of `rows` rows of n scores (row stride row_stride floats), 1 <= k <= kTopkMaxK:
 // min(k, n) entries per output row of k slots, the rest index 0xFFFFFFFF and score 0.
+// Rows longer than one selection kernel's registers run in chunks on many CUs when
+// candidate buffers of topk_candidate_slots(rows, n, k) entries are given (else one
+// workgroup streams each row).
 void launch_topk(const float* S, size_t rows, size_t row_stride, int n, int k, int signed_mode, uint32_t* idx,
-                 float* val, hipStream_t s);
+                 float* val, hipStream_t s, uint32_t* cand_idx = nullptr, float* cand_val = nullptr);
+size_t topk_candidate_slots(size_t rows, int n, int k);
 // The same order for any k >= 1 (topk_sort.hip): a stable segmented radix sort of every
 // row's keys, descending, then the first min(k, n) of each row.  work: work_bytes of
 // device memory, at least topk_sorted_work_bytes(rows, n); rows * n < 2^31.

@@ -272,6 +272,19 @@ __global__ __launch_bounds__(kThreads, 2) void gate_scores_q4_kernel(KnnLayers g
 }
 
 // ── top-k ──────────────────────────────────────────────────────────────────
+// Row views of the selection kernels.  C > 1 (chunks): output row i is chunk i % C of
+// input row i / C, elements [chunk (i % C), min(n, chunk (i % C + 1))), indices relative to
+// the chunk.  cand set (a selection over chunk candidates): output index p of row i is
+// written as (p / ck) chunk + cand[i * crow + p], the row index of candidate p.
+struct TopkView {
+    int C = 1, chunk = 0;
+    const uint32_t* cand = nullptr;
+    int ck = 0, crow = 0;
+};
+__device__ __forceinline__ uint32_t topk_out_index(const TopkView& v, size_t row, uint32_t p) {
+    return v.cand ? (p / v.ck) * static_cast<uint32_t>(v.chunk) + v.cand[row * v.crow + p] : p;
+}
+
 // Order key: (k32(score) descending, index ascending) as one 64-bit composite
 // c = k32 << 32 | (0xFFFFFFFF - index), unique per element.  k32 is the f32 bit
 // pattern of |s| (abs mode; -0 and +0 equal), or an order-preserving map of s
@@ -362,10 +375,11 @@ constexpr int kTopkCap = 2048;  // candidates kept in LDS
 // (an all-zero row is one big tie).  Rows whose candidates overflow the LDS list run the
 // selects over all elements instead.  k <= n; the output rows are kstride apart and
 // slots k .. kstride - 1 receive index 0xFFFFFFFF and score 0.
+// v: the row view (TopkView).
 template <int PER, bool SG>
 __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ S, size_t row_stride, int n, int k,
                                                         int kstride, uint32_t* __restrict__ idx_out,
-                                                        float* __restrict__ val_out) {
+                                                        float* __restrict__ val_out, TopkView v) {
     __shared__ uint32_t hist[kThreads / 64][256];
     __shared__ uint32_t sel[2];
     __shared__ int cnt, nout, nties;
@@ -374,6 +388,12 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
     __shared__ float out_v[kTopkMaxK];
     const int tid = threadIdx.x;
     const float* __restrict__ s = S + static_cast<size_t>(blockIdx.x) * row_stride;
+    if (v.C > 1) {
+        const int r = blockIdx.x / v.C, c = blockIdx.x - r * v.C;
+        s = S + static_cast<size_t>(r) * row_stride + static_cast<size_t>(c) * v.chunk;
+        n = min(v.chunk, n - c * v.chunk);
+        k = min(k, n);
+    }
     // element i = tid + kThreads * j (coalesced); held in registers when PER > 0
     uint32_t key[PER > 0 ? PER : 1];
     if constexpr (PER > 0) {
@@ -485,7 +505,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
         const uint64_t me = out_c[p];
         int rank = 0;
         for (int j = 0; j < k; j++) rank += out_c[j] > me;
-        idx_out[row0 + rank] = 0xFFFFFFFFu - static_cast<uint32_t>(me & 0xFFFFFFFFu);
+        idx_out[row0 + rank] = topk_out_index(v, blockIdx.x, 0xFFFFFFFFu - static_cast<uint32_t>(me & 0xFFFFFFFFu));
         val_out[row0 + rank] = out_v[p];
     }
     for (int p = k + tid; p < kstride; p += kThreads) {
@@ -511,6 +531,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
 // real elements (no key is below 0, and ties go to the smaller index), so they take
 // part in every step without a validity test.
 constexpr int kWCap = 512;      // list entries per wave
+constexpr int kWSmallK = 8;     // k up to this (and rows up to 4096) take k rounds of a wave arg-max
 constexpr int kWWaves = 4;      // rows per workgroup
 
 __device__ __forceinline__ uint64_t wave_ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
@@ -536,11 +557,34 @@ __device__ __forceinline__ uint32_t wave_kth_largest(V v, Ok ok, int k) {
     return prefix;
 }
 
+// 64-bit wave maximum: DPP butterflies within rows of 16 lanes, then the four row results.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v)), CTRL, 0xF, 0xF, false));
+    const uint32_t hi = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v >> 32)), CTRL, 0xF, 0xF, false));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), l));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = max(v, dpp_u64<0xB1>(v));   // quad_perm 1,0,3,2
+    v = max(v, dpp_u64<0x4E>(v));   // quad_perm 2,3,0,1
+    v = max(v, dpp_u64<0x141>(v));  // row_half_mirror
+    v = max(v, dpp_u64<0x140>(v));  // row_mirror
+    return max(max(readlane_u64(v, 0), readlane_u64(v, 16)), max(readlane_u64(v, 32), readlane_u64(v, 48)));
+}
+
 template <int PW, bool SG>
 __global__ __launch_bounds__(64 * kWWaves) void topk_wave_kernel(const float* __restrict__ S, size_t row_stride,
                                                                  int n, int k, int kstride,
                                                                  uint32_t* __restrict__ idx_out,
-                                                                 float* __restrict__ val_out, int rows) {
+                                                                 float* __restrict__ val_out, int rows,
+                                                                 TopkView v) {
     __shared__ uint32_t lkey[kWWaves][kWCap], lidx[kWWaves][kWCap];
     __shared__ uint32_t wkey[kWWaves][64], widx[kWWaves][64];
     const int lane = threadIdx.x & 63;
@@ -548,6 +592,12 @@ __global__ __launch_bounds__(64 * kWWaves) void topk_wave_kernel(const float* __
     const int row = blockIdx.x * kWWaves + w;
     if (row >= rows) return;  // whole wave; the kernel has no workgroup barrier
     const float* __restrict__ s = S + static_cast<size_t>(row) * row_stride;
+    if (v.C > 1) {  // chunk view, as topk_kernel
+        const int r = row / v.C, c = row - r * v.C;
+        s = S + static_cast<size_t>(r) * row_stride + static_cast<size_t>(c) * v.chunk;
+        n = min(v.chunk, n - c * v.chunk);
+        k = min(k, n);
+    }
     uint32_t key[PW];
     if (n == 64 * PW) {  // every register holds an element: one base, immediate offsets
         const float* __restrict__ sl = s + lane;
@@ -575,6 +625,41 @@ __global__ __launch_bounds__(64 * kWWaves) void topk_wave_kernel(const float* __
         return static_cast<uint32_t>(l + 64 * j);
     };
     auto all = [](int) { return true; };
+
+    if (PW <= 64 && k <= kWSmallK) {
+        // A few winners: round r takes the largest composite key << 32 | ~index below the
+        // previous winner (composites are unique per element, so nothing is taken twice);
+        // slots past n hold key 0 with an index >= n, below every real element.
+        uint64_t win[kWSmallK];
+        uint64_t prev = ~uint64_t{0};
+#pragma unroll
+        for (int r = 0; r < kWSmallK; r++) {
+            if (r >= k) break;  // wave-uniform
+            uint64_t best = 0;
+#pragma unroll
+            for (int j = 0; j < PW; j++) {
+                const uint64_t c = (static_cast<uint64_t>(key[j]) << 32) | (0xFFFFFFFFu - index_of(j));
+                if (c < prev && c > best) best = c;
+            }
+            prev = wave_max_u64(best);
+            win[r] = prev;
+        }
+        const size_t row0 = static_cast<size_t>(row) * kstride;
+        uint64_t mine = 0;
+#pragma unroll
+        for (int r = 0; r < kWSmallK; r++)
+            if (r == lane) mine = win[r];
+        if (lane < k) {
+            const uint32_t mi = 0xFFFFFFFFu - static_cast<uint32_t>(mine);
+            idx_out[row0 + lane] = topk_out_index(v, row, mi);
+            val_out[row0 + lane] = s[mi];
+        }
+        for (int p = k + lane; p < kstride; p += 64) {
+            idx_out[row0 + p] = 0xFFFFFFFFu;
+            val_out[row0 + p] = 0.0f;
+        }
+        return;
+    }
 
     // 1. T from the lane maxima
     uint32_t m = 0;
@@ -749,7 +834,7 @@ __global__ __launch_bounds__(64 * kWWaves) void topk_wave_kernel(const float* __
             const uint32_t ok = wkey[w][j], oi = widx[w][j];
             rank += (ok > mk || (ok == mk && oi < mi)) ? 1 : 0;
         }
-        idx_out[row0 + rank] = mi;
+        idx_out[row0 + rank] = topk_out_index(v, row, mi);
         val_out[row0 + rank] = s[mi];
     }
     for (int p = k + lane; p < kstride; p += 64) {
@@ -783,32 +868,89 @@ void launch_gate_scores_q4(const KnnLayers& nib, const KnnLayers& scales, int n_
 size_t q4_xa_bytes(int K, int Q) { return static_cast<size_t>(K / 64) * ((Q + 7) / 8) * 64 * sizeof(uint4); }
 size_t q4_xsp_bytes(int K, int Q) { return static_cast<size_t>(K / 64) * ((Q + 7) / 8) * 16 * sizeof(float); }
 
-void launch_topk(const float* S, size_t rows, size_t row_stride, int n, int k, int signed_mode, uint32_t* idx,
-                 float* val, hipStream_t s) {
-    if (k < 1 || k > kTopkMaxK || n < 1) fail(LARQL_HIP_ERR_INVALID, "top-k: need 1 <= k <= 512 and n >= 1");
-    if (rows == 0) return;
-    const int ke = std::min(k, n);  // top_k.min(len), LV/src/index/walk.rs:569
+// The selection kernels over `nrows` rows (v.C > 1: chunk views, rows = input rows x C) of
+// at most nmax elements, k requested per row (kstride output slots).
+static void topk_select(const float* S, size_t nrows, size_t row_stride, int n, int nmax, int k, int kstride,
+                        const TopkView& v, int signed_mode, uint32_t* idx, float* val, hipStream_t s) {
+    const int ke = std::min(k, nmax);  // top_k.min(len), LV/src/index/walk.rs:569 (per chunk in the kernels)
     auto go = [&](auto sg) {
         constexpr bool SG = decltype(sg)::value;
-        const dim3 grid(static_cast<unsigned>(rows));
-        if (ke <= 64 && n <= 64 * 224 && rows <= 0x7FFFFFFF) {  // a wave per row
-            const dim3 gw(static_cast<unsigned>((rows + kWWaves - 1) / kWWaves)), bw(64 * kWWaves);
-            const int r = static_cast<int>(rows);
-            if (n <= 64 * 64)
-                topk_wave_kernel<64, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, k, idx, val, r);
-            else if (n <= 64 * 160)
-                topk_wave_kernel<160, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, k, idx, val, r);
+        const dim3 grid(static_cast<unsigned>(nrows));
+        if (ke <= 64 && nmax <= 64 * 224 && nrows <= 0x7FFFFFFF) {  // a wave per row
+            const dim3 gw(static_cast<unsigned>((nrows + kWWaves - 1) / kWWaves)), bw(64 * kWWaves);
+            const int r = static_cast<int>(nrows);
+            // register slots per lane: the fewest that hold the row (every slot costs time)
+            if (nmax <= 64 * 4)
+                topk_wave_kernel<4, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, kstride, idx, val, r, v);
+            else if (nmax <= 64 * 16)
+                topk_wave_kernel<16, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, kstride, idx, val, r, v);
+            else if (nmax <= 64 * 64)
+                topk_wave_kernel<64, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, kstride, idx, val, r, v);
+            else if (nmax <= 64 * 160)
+                topk_wave_kernel<160, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, kstride, idx, val, r, v);
             else
-                topk_wave_kernel<224, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, k, idx, val, r);
-        } else if (n <= kThreads * 48) {
-            topk_kernel<48, SG><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, k, idx, val);
+                topk_wave_kernel<224, SG><<<gw, bw, 0, s>>>(S, row_stride, n, ke, kstride, idx, val, r, v);
+        } else if (nmax <= kThreads * 48) {
+            topk_kernel<48, SG><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, kstride, idx, val, v);
         } else {
-            topk_kernel<0, SG><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, k, idx, val);
+            topk_kernel<0, SG><<<grid, dim3(kThreads), 0, s>>>(S, row_stride, n, ke, kstride, idx, val, v);
         }
     };
     if (signed_mode) go(std::true_type{});
     else go(std::false_type{});
     LARQL_HIP_CHECK(hipGetLastError());
+}
+
+// Long rows are split into chunks whose selection runs in registers: 1024 elements for k
+// <= 64 (a wave per chunk), 12288 above; a row of n elements has C = ceil(n / chunk).
+static int topk_chunk_len(int k) { return k <= 64 ? 1024 : kThreads * 48; }
+static bool topk_chunked(int n, int k) { return n > (k <= 64 ? 64 * 224 : kThreads * 48); }
+
+size_t topk_candidate_slots(size_t rows, int n, int k) {
+    if (!topk_chunked(n, k)) return 0;
+    const int chunk = topk_chunk_len(k);
+    return rows * static_cast<size_t>((n + chunk - 1) / chunk) * static_cast<size_t>(k);
+}
+
+namespace {
+// Slots a chunk left empty (index 0xFFFFFFFF) take the lowest key of the signed order, so
+// the second selection ranks them after every real score (in abs mode their 0 is already
+// the lowest key, and they sit after all real candidates of the row).
+__global__ void topk_cand_fix_kernel(const uint32_t* __restrict__ ci, float* __restrict__ cv, size_t n) {
+    const size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    if (i < n && ci[i] == 0xFFFFFFFFu) cv[i] = -INFINITY;
+}
+}  // namespace
+
+void launch_topk(const float* S, size_t rows, size_t row_stride, int n, int k, int signed_mode, uint32_t* idx,
+                 float* val, hipStream_t s, uint32_t* cand_idx, float* cand_val) {
+    if (k < 1 || k > kTopkMaxK || n < 1) fail(LARQL_HIP_ERR_INVALID, "top-k: need 1 <= k <= 512 and n >= 1");
+    if (rows == 0) return;
+    if (!cand_idx || !cand_val || !topk_chunked(n, k)) {
+        topk_select(S, rows, row_stride, n, n, k, k, TopkView{}, signed_mode, idx, val, s);
+        return;
+    }
+    // Stage 1: the top k of every chunk, [rows][C][k] candidates with chunk-relative
+    // indices.  Stage 2: the top k of each row's C k candidates.  An element of a row's top
+    // k is within its chunk's top k (else k elements of its chunk outrank it), and the
+    // candidates sit in chunk order, each chunk's in rank order, so equal keys still
+    // resolve by ascending row index.
+    const int chunk = topk_chunk_len(k), C = (n + chunk - 1) / chunk;
+    TopkView v1;
+    v1.C = C;
+    v1.chunk = chunk;
+    topk_select(S, rows * C, row_stride, n, chunk, k, k, v1, signed_mode, cand_idx, cand_val, s);
+    const size_t nc = rows * static_cast<size_t>(C) * k;
+    if (signed_mode && n % chunk != 0 && n % chunk < k) {
+        topk_cand_fix_kernel<<<dim3(static_cast<unsigned>((nc + 255) / 256)), dim3(256), 0, s>>>(cand_idx, cand_val, nc);
+        LARQL_HIP_CHECK(hipGetLastError());
+    }
+    TopkView v2;  // candidate positions written as row indices
+    v2.chunk = chunk;
+    v2.cand = cand_idx;
+    v2.ck = k;
+    v2.crow = C * k;
+    topk_select(cand_val, rows, static_cast<size_t>(C) * k, C * k, C * k, k, k, v2, signed_mode, idx, val, s);
 }
 
 }  // namespace larql

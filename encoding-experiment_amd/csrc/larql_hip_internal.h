@@ -207,7 +207,7 @@ struct larql_hip_ctx {
     larql::DeviceBuf stage_in, stage_in2, stage_out, stage_raw, scratch;
     // gate-KNN work buffers: scores [layers][nq][features], quantized queries, f32 queries
     // padded to the gate row stride
-    larql::DeviceBuf knn_scores, knn_q8, knn_q8s, knn_idx, knn_val, knn_handles, knn_xa, knn_xsp, knn_xpad, knn_sort;
+    larql::DeviceBuf knn_scores, knn_q8, knn_q8s, knn_idx, knn_val, knn_handles, knn_xa, knn_xsp, knn_xpad, knn_sort, knn_cand;
     // q4_vecmat chunk partials; pair-batch quantized activations
     larql::DeviceBuf vecmat_part, pair_q8, pair_q8s;
     // prefill GEMM: X as fp16 MFMA operands

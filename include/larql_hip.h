@@ -294,10 +294,12 @@ int larql_hip_lm_head_knn_dev(larql_hip_ctx* ctx, uint64_t handle, const float* 
  * per-token serving loops, harnesses that forbid hipMalloc.  Same arguments, kernels and
  * results as larql_hip_lm_head_knn_dev; the quantized queries and the vocabulary scores
  * live in a fixed device array of LARQL_HIP_NOALLOC_SCRATCH_BYTES per GPU (8 MiB, held
- * until the process ends), which limits a call to
- *   nq * (vocab * 4 + hidden * 9 / 8) (+ alignment) <= 8 MiB
- * (vocab 128256: up to 16 queries), and top_k <= LARQL_HIP_TOPK_MAX (a larger top_k
- * needs a sort buffer); larger requests return LARQL_HIP_ERR_INVALID.  Every
+ * until the process ends), with the top-k candidates of a vocabulary ranked in chunks
+ * (above 14336 entries for top_k <= 64, chunks of 4096; above 12288 for larger top_k,
+ * chunks of 12288), which limits a call to
+ *   nq * (vocab * 4 + hidden * 9 / 8 + chunks * top_k * 8) (+ alignment) <= 8 MiB
+ * (vocab 128256, top_k 5: up to 16 queries), and top_k <= LARQL_HIP_TOPK_MAX (a larger
+ * top_k needs a sort buffer); larger requests return LARQL_HIP_ERR_INVALID.  Every
  * call on one GPU shares that array: calls that overlap on one GPU (different streams or
  * contexts) race. */
 int larql_hip_lm_head_knn_dev_noalloc(larql_hip_ctx* ctx, uint64_t handle, const float* queries, size_t nq,

@@ -271,6 +271,28 @@ def test_topk_k_above_selection_bound_sorts(hip, signed):
                 assert np.all(gi[r, m:] == 0xFFFFFFFF) and np.all(gv[r, m:] == 0.0)
 
 
+@pytest.mark.parametrize("signed", [False, True])
+def test_topk_long_rows_in_chunks(hip, signed):
+    """Rows longer than one selection kernel's registers are ranked in chunks on many CUs and
+    then over the chunks' candidates: row lengths whose last chunk is shorter than k (its
+    empty slots must rank after every real score, also when all scores are negative),
+    exact multiples of the chunk, mass ties across chunk boundaries, k = 1 .. 512."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(55)
+    for n, k in ((4096 * 4 + 3, 32), (4096 * 4, 64), (12288 * 2 + 5, 100), (12288 * 3, 512), (128256, 5),
+                 (14337, 1), (40000, 300)):
+        rows = rng.standard_normal((3, n)).astype(np.float32)
+        rows[1] = -np.abs(rows[1]) - 1.0                  # every score negative
+        rows[2, rng.choice(n, n // 3, replace=False)] = -3.0
+        rows[2, rng.choice(n, 50, replace=False)] = 3.0    # ties straddle chunk boundaries
+        print(f"[topk chunks] n={n} k={k} signed={signed}", flush=True)
+        gi, gv = _topk_rows(hip, torch, rows, k, signed)
+        for r in range(rows.shape[0]):
+            ri, rv = (oracle.topk_signed if signed else oracle.topk_abs)(rows[r], k)
+            np.testing.assert_array_equal(gi[r], ri, err_msg=f"n={n} k={k} row={r}")
+            np.testing.assert_array_equal(gv[r].view(np.uint32), rv.view(np.uint32))
+
+
 def test_gate_knn_k_above_selection_bound(hip):
     """gate_knn with top_k = 320 and 1000 (the reference's top_k * 10 fallback sizes) through
     the host and device entry points, f32 and Q4_0, bit-exact with the oracle."""
