@@ -393,13 +393,15 @@ class _Layer(ctypes.Structure):
                 ("activation", ctypes.c_int), ("has_v_norm", ctypes.c_int),
                 ("layer_scalar", ctypes.c_float), ("rotary_dim", ctypes.c_size_t),
                 ("attn_scale", ctypes.c_float)] + [(n + "_s", ctypes.c_void_p) for n in _PROJ] + \
-               [("qk_norm", ctypes.c_int), ("softcap", ctypes.c_float)]
+               [("qk_norm", ctypes.c_int), ("softcap", ctypes.c_float),
+                ("k_cache32", ctypes.c_void_p), ("v_cache32", ctypes.c_void_p)]
 
 
 def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, num_kv: int,
                  head_dim: int, rope_base: float, eps: float = 1e-6, window: int = 0, threads: int = 1):
     """One decoder layer on the CPU.  ``layer`` holds numpy arrays keyed as the
-    lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits) are updated in place.
+    lo_layer_t fields; k_cache / v_cache (uint16 fp16 bits, or float32 for the reference's f32
+    cache: the new row stored unrounded) are updated in place.
     window > 0 attends over the last `window` positions only.  ``layer["formats"]``
     (optional) maps a projection name to "q6_k" (Q6_K bytes), "q4_kf" (Q4_KF, 144-byte GGUF),
     "q4_kf160" (Q4_KF, 160-byte), "q8_0" (int8 weights, scales under name + "_s") or "q4_0";
@@ -432,8 +434,9 @@ def decode_layer(layer: dict, h, pos: int, hidden: int, inter: int, num_q: int, 
             setattr(st, name + "_s", a.ctypes.data)
     for name in ("k_cache", "v_cache"):
         a = layer[name]
-        assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]
-        setattr(st, name, a.ctypes.data)
+        assert a.dtype in (np.uint16, np.float32) and a.flags["C_CONTIGUOUS"]
+        # uint16: fp16 bits; float32: the f32 cache (the new row stored unrounded)
+        setattr(st, name + ("32" if a.dtype == np.float32 else ""), a.ctypes.data)
     st.norm_offset = float(layer.get("norm_offset", 0.0))
     st.has_post_norms = int(bool(layer.get("has_post_norms", False)))
     st.activation = {"silu": 0, "gelu_tanh": 1}[layer.get("activation", "silu")]

@@ -765,42 +765,47 @@ void lo_rms_norm_heads(float* x, size_t num_heads, size_t head_dim, double eps) 
 
 /* LI/src/attention/gqa.rs:29-110, last query row only: s = (k.q) * scale;
  * e = exp((s - max) as f64); sum in f64; p = (e as f32) * ((1/sum) as f32); out = V^T p.
- * K/V come from an fp16 cache [t][kv_head][head_dim]; kv_h = h / (num_q / num_kv). */
+ * K/V come from a cache [t][kv_head][head_dim] of fp16 (lo_attend_heads) or f32
+ * (lo_attend_heads32) elements; kv_h = h / (num_q / num_kv). */
 /* Query heads [h0, h1): scores, softmax in f64, then the weighted V sum with t outermost
  * (each output element still accumulates its T terms in ascending t, the same additions
  * as a t-inner loop, while V is walked row by row). */
-static void lo_attend_heads(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T, size_t h0, size_t h1,
-                            size_t reps, size_t kvd, size_t head_dim, float scale, float softcap, float* out) {
-    float* sc = (float*)malloc(T * sizeof(float));
-    for (size_t h = h0; h < h1; h++) {
-        size_t kvh = h / reps;
-        const float* qh = q + h * head_dim;
-        for (size_t t = 0; t < T; t++) {
-            const uint16_t* kr = kc + t * kvd + kvh * head_dim;
-            float dot = 0.0f;
-            for (size_t d = 0; d < head_dim; d++) dot += lo_f16_to_f32(kr[d]) * qh[d];
-            sc[t] = dot * scale;
-            if (softcap > 0.0f) sc[t] = tanhf(sc[t] / softcap) * softcap;  /* fused_attention.rs:132-137 */
-        }
-        float mx = -INFINITY;
-        for (size_t t = 0; t < T; t++) mx = fmaxf(mx, sc[t]);
-        double sum = 0.0;
-        for (size_t t = 0; t < T; t++) {
-            double e = exp((double)(sc[t] - mx));
-            sc[t] = (float)e;
-            sum += e;
-        }
-        float inv = (float)(1.0 / sum);
-        for (size_t t = 0; t < T; t++) sc[t] *= inv;
-        float* oh = out + h * head_dim;
-        for (size_t d = 0; d < head_dim; d++) oh[d] = 0.0f;
-        for (size_t t = 0; t < T; t++) {
-            const uint16_t* vr = vc + t * kvd + kvh * head_dim;
-            for (size_t d = 0; d < head_dim; d++) oh[d] += lo_f16_to_f32(vr[d]) * sc[t];
-        }
+#define LO_ATTEND_HEADS(NAME, ELEM, LOAD)                                                                    \
+    static void NAME(const float* q, const ELEM* kc, const ELEM* vc, size_t T, size_t h0, size_t h1,          \
+                     size_t reps, size_t kvd, size_t head_dim, float scale, float softcap, float* out) {     \
+        float* sc = (float*)malloc(T * sizeof(float));                                                        \
+        for (size_t h = h0; h < h1; h++) {                                                                    \
+            size_t kvh = h / reps;                                                                            \
+            const float* qh = q + h * head_dim;                                                               \
+            for (size_t t = 0; t < T; t++) {                                                                  \
+                const ELEM* kr = kc + t * kvd + kvh * head_dim;                                               \
+                float dot = 0.0f;                                                                             \
+                for (size_t d = 0; d < head_dim; d++) dot += LOAD(kr[d]) * qh[d];                             \
+                sc[t] = dot * scale;                                                                          \
+                if (softcap > 0.0f) sc[t] = tanhf(sc[t] / softcap) * softcap; /* fused_attention.rs:132-137 */\
+            }                                                                                                 \
+            float mx = -INFINITY;                                                                             \
+            for (size_t t = 0; t < T; t++) mx = fmaxf(mx, sc[t]);                                             \
+            double sum = 0.0;                                                                                 \
+            for (size_t t = 0; t < T; t++) {                                                                  \
+                double e = exp((double)(sc[t] - mx));                                                         \
+                sc[t] = (float)e;                                                                             \
+                sum += e;                                                                                     \
+            }                                                                                                 \
+            float inv = (float)(1.0 / sum);                                                                   \
+            for (size_t t = 0; t < T; t++) sc[t] *= inv;                                                      \
+            float* oh = out + h * head_dim;                                                                   \
+            for (size_t d = 0; d < head_dim; d++) oh[d] = 0.0f;                                               \
+            for (size_t t = 0; t < T; t++) {                                                                  \
+                const ELEM* vr = vc + t * kvd + kvh * head_dim;                                               \
+                for (size_t d = 0; d < head_dim; d++) oh[d] += LOAD(vr[d]) * sc[t];                           \
+            }                                                                                                 \
+        }                                                                                                     \
+        free(sc);                                                                                             \
     }
-    free(sc);
-}
+#define LO_F32_ELEM(x) (x)
+LO_ATTEND_HEADS(lo_attend_heads, uint16_t, lo_f16_to_f32)
+LO_ATTEND_HEADS(lo_attend_heads32, float, LO_F32_ELEM)
 
 void lo_attend_f16(const float* q, const uint16_t* kc, const uint16_t* vc, size_t T,
                    size_t num_q, size_t num_kv, size_t head_dim, float scale, float* out) {
@@ -907,6 +912,7 @@ static void lo_proj_n(int nt, int fmt, const uint8_t* w, const float* ws, int q8
 typedef struct {
     const float* q;
     const uint16_t *kc, *vc;
+    const float *kc32, *vc32;  /* non-NULL: the f32 cache */
     size_t T, h0, h1, reps, kvd, head_dim;
     float scale, softcap;
     float* out;
@@ -914,16 +920,25 @@ typedef struct {
 
 static void* lo_attend_job_run(void* p) {
     const lo_attend_job* j = (const lo_attend_job*)p;
-    if (j->h1 > j->h0) lo_attend_heads(j->q, j->kc, j->vc, j->T, j->h0, j->h1, j->reps, j->kvd, j->head_dim, j->scale,
-                                       j->softcap, j->out);
+    if (j->h1 <= j->h0) return NULL;
+    if (j->kc32)
+        lo_attend_heads32(j->q, j->kc32, j->vc32, j->T, j->h0, j->h1, j->reps, j->kvd, j->head_dim, j->scale,
+                          j->softcap, j->out);
+    else
+        lo_attend_heads(j->q, j->kc, j->vc, j->T, j->h0, j->h1, j->reps, j->kvd, j->head_dim, j->scale, j->softcap,
+                        j->out);
     return NULL;
 }
 
-/* Attention with the query heads split over nt threads (each head is independent). */
-static void lo_attend_n(int nt, const float* q, const uint16_t* kc, const uint16_t* vc, size_t T, size_t num_q,
-                        size_t num_kv, size_t head_dim, float scale, float softcap, float* out) {
+/* Attention with the query heads split over nt threads (each head is independent); kc32 /
+ * vc32 non-NULL: the f32 cache instead of kc / vc. */
+static void lo_attend_n(int nt, const float* q, const uint16_t* kc, const uint16_t* vc, const float* kc32,
+                        const float* vc32, size_t T, size_t num_q, size_t num_kv, size_t head_dim, float scale,
+                        float softcap, float* out) {
     if (nt <= 1) {
-        lo_attend_heads(q, kc, vc, T, 0, num_q, num_q / num_kv, num_kv * head_dim, head_dim, scale, softcap, out);
+        lo_attend_job j = {q, kc, vc, kc32, vc32, T, 0, num_q, num_q / num_kv, num_kv * head_dim, head_dim, scale,
+                           softcap, out};
+        lo_attend_job_run(&j);
         return;
     }
     if (nt > 256) nt = 256;
@@ -931,8 +946,9 @@ static void lo_attend_n(int nt, const float* q, const uint16_t* kc, const uint16
     int started[256];
     lo_attend_job jb[256];
     for (int t = 0; t < nt; t++) {
-        jb[t] = (lo_attend_job){q, kc, vc, T, num_q * (size_t)t / (size_t)nt, num_q * (size_t)(t + 1) / (size_t)nt,
-                                num_q / num_kv, num_kv * head_dim, head_dim, scale, softcap, out};
+        jb[t] = (lo_attend_job){q, kc, vc, kc32, vc32, T, num_q * (size_t)t / (size_t)nt,
+                                num_q * (size_t)(t + 1) / (size_t)nt, num_q / num_kv, num_kv * head_dim, head_dim,
+                                scale, softcap, out};
         started[t] = pthread_create(&th[t], NULL, lo_attend_job_run, &jb[t]) == 0;
         if (!started[t]) lo_attend_job_run(&jb[t]);
     }
@@ -948,7 +964,8 @@ void lo_proj_rows_mt(int fmt, const uint8_t* w, const float* ws, int q8in, const
 /* One decoder layer (LI/src/attention/block.rs:52-157, LI/src/forward/layer.rs:50-94; per-op
  * order of the reference GPU decode LC/src/metal/decode.rs:144-739):
  *   xn = norm(h, input_norm); q, k, v = projections; [V-norm]; RoPE(q, k) at pos;
- *   K/V appended at pos (LC/src/metal/ops/kv_cache.rs:73-105) as fp16 (RNE); attention;
+ *   K/V appended at pos (LC/src/metal/ops/kv_cache.rs:73-105) as fp16 (RNE), or unrounded
+ *   into the f32 cache (k_cache32); attention;
  *   o = Wo att;
  *   Llama:       h1 = h + o;                          f = norm(h1, post_attn_norm)
  *   post-norms:  h1 = h + norm(o, post_attn_norm);    f = norm(h1, pre_ffn_norm)
@@ -1006,14 +1023,24 @@ static void lo_decode_layer_impl(const lo_layer_t* L, float* h, size_t pos, size
     lo_rope_at(q, num_q, head_dim, rdim, rope_base, pos);
     lo_rope_at(k, num_kv, head_dim, rdim, rope_base, pos);
     if (L->qk_norm) lo_qk_norm_heads(q, num_q, head_dim);  /* after RoPE, Q only: the cache keeps K */
+    const int f32kv = L->k_cache32 != NULL;
     for (size_t i = 0; i < kvd; i++) {
-        L->k_cache[pos * kvd + i] = lo_f32_to_f16_rne(k[i]);
-        L->v_cache[pos * kvd + i] = lo_f32_to_f16_rne(v[i]);
+        if (f32kv) {
+            L->k_cache32[pos * kvd + i] = k[i];
+            L->v_cache32[pos * kvd + i] = v[i];
+        } else {
+            L->k_cache[pos * kvd + i] = lo_f32_to_f16_rne(k[i]);
+            L->v_cache[pos * kvd + i] = lo_f32_to_f16_rne(v[i]);
+        }
     }
     float scale = L->attn_scale != 0.0f ? L->attn_scale : (float)(1.0 / sqrt((double)head_dim));
     const size_t T = pos + 1, t0 = (window > 0 && T > window) ? T - window : 0;
-    lo_attend_n(nt, q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, T - t0, num_q, num_kv, head_dim, scale,
-                L->softcap, att);
+    if (f32kv)
+        lo_attend_n(nt, q, NULL, NULL, L->k_cache32 + t0 * kvd, L->v_cache32 + t0 * kvd, T - t0, num_q, num_kv,
+                    head_dim, scale, L->softcap, att);
+    else
+        lo_attend_n(nt, q, L->k_cache + t0 * kvd, L->v_cache + t0 * kvd, NULL, NULL, T - t0, num_q, num_kv, head_dim,
+                    scale, L->softcap, att);
     lo_proj_n(nt, L->fmt[3], L->wo, L->wo_s, 1, att, o, hidden, qd);
     if (L->has_post_norms) {
         lo_rms_norm(o, L->post_attn_norm, off, eps, xn, hidden);

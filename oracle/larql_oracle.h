@@ -155,6 +155,11 @@ typedef struct {
      * tanh(s / softcap) * softcap */
     int qk_norm;
     float softcap;
+    /* non-NULL: f32 K/V caches [max_seq][kv_heads][head_dim] in place of k_cache / v_cache,
+     * the reference's cache element type (LC/src/metal/ops/kv_cache.rs:13-14, populate_kv_layer
+     * takes f32 rows, LC/src/metal/trait_impl.rs:197-225; the CPU attention works in f32,
+     * LI/src/attention/gqa.rs:29-110): the new K/V row is stored unrounded */
+    float *k_cache32, *v_cache32;
 } lo_layer_t;
 
 void lo_decode_layer(const lo_layer_t* L, float* h, size_t pos,

@@ -133,6 +133,44 @@ def run_sequence(hip, T0, n_tokens, n_layers=2, hidden=512, inter=1024, nq=8, nk
     return errs
 
 
+def test_decode_fp16_cache_drift_against_f32_cache(hip):
+    """The reference keeps K/V in f32 (LC/src/metal/ops/kv_cache.rs:13-14; populate_kv_layer
+    takes f32 rows, LC/src/metal/trait_impl.rs:197-225; the CPU attention is f32,
+    LI/src/attention/gqa.rs:29-110); this backend stores them in fp16.  After a 512-position
+    cache populated from f32 rows, 64 tokens are decoded through 4 layers: every step's
+    hidden state stays within 1e-3 of the oracle run with f32 caches (populated and new
+    rows unrounded), so the fp16 cache's drift is inside the bar over a generation.  The
+    same steps against the oracle's fp16 cache measure the kernels alone."""
+    n_layers, hidden, inter, nq, nkv, hd, T0, n = 4, 512, 1024, 8, 2, 64, 512, 64
+    m = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=T0 + n + 1, seed=77)
+    m16 = SmallModel(n_layers, hidden, inter, nq, nkv, hd, cap=T0 + n + 1, seed=77)
+    kvd = nkv * hd
+    hip.reset_kv_cache()
+    for l, (L, L16) in enumerate(zip(m.layers, m16.layers)):
+        k, v = oracle.gauss(5100 + l, T0 * kvd), oracle.gauss(5200 + l, T0 * kvd)
+        hip.populate_kv_layer(l, k, v, T0, nkv, hd)
+        L["k_cache"] = np.zeros((T0 + n + 1) * kvd, np.float32)
+        L["v_cache"] = np.zeros((T0 + n + 1) * kvd, np.float32)
+        L["k_cache"][: T0 * kvd], L["v_cache"][: T0 * kvd] = k, v
+        L16["k_cache"][: T0 * kvd] = k.astype(np.float16).view(np.uint16)
+        L16["v_cache"][: T0 * kvd] = v.astype(np.float16).view(np.uint16)
+    layers = m.hip_layers(500000.0)
+    drift, kern = [], []
+    for i in range(n):
+        x = oracle.gauss(7100 + i, hidden)
+        got = hip.decode_token(layers, x, hidden, inter, nq * hd, kvd, nq, nkv, hd, 500000.0)
+        ref, ref16 = x.copy(), x.copy()
+        for L, L16 in zip(m.layers, m16.layers):
+            ref = oracle.decode_layer(L, ref, T0 + i, hidden, inter, nq, nkv, hd, 500000.0)
+            ref16 = oracle.decode_layer(L16, ref16, T0 + i, hidden, inter, nq, nkv, hd, 500000.0)
+        drift.append(rel_err(got, ref))
+        kern.append(rel_err(got, ref16))
+    print(f"[kv drift] {n} tokens after {T0}: vs f32 cache max {max(drift):.3e} (last {drift[-1]:.3e}); "
+          f"vs fp16 cache max {max(kern):.3e}", flush=True)
+    assert max(kern) <= REL_TOL
+    assert max(drift) <= REL_TOL
+
+
 def test_decode_short_cache(hip):
     run_sequence(hip, T0=5, n_tokens=3)
 

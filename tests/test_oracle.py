@@ -772,10 +772,17 @@ def _ref_layer64(P, h, kc, vc, pos, dims, mut=()):
     if "rope_v" in mut:
         v = rope(v, nkv)
     kvd = nkv * hd
-    K = kc.view(np.float16).astype(np.float64).reshape(-1, kvd)[:pos + 1].copy()
-    V = vc.view(np.float16).astype(np.float64).reshape(-1, kvd)[:pos + 1].copy()
-    K[pos] = k.astype(np.float16)                                  # fp16 cache row, RNE
-    V[pos] = v.astype(np.float16)
+    if kc.dtype == np.float32:   # the reference's f32 cache (kv_cache.rs:13-14): the new row unrounded
+        K = kc.astype(np.float64).reshape(-1, kvd)[:pos + 1].copy()
+        V = vc.astype(np.float64).reshape(-1, kvd)[:pos + 1].copy()
+        K[pos], V[pos] = k.astype(np.float32), v.astype(np.float32)
+        if "kv_fp16" in mut:     # planted: the new row rounded as an fp16 cache rounds it
+            K[pos], V[pos] = k.astype(np.float16), v.astype(np.float16)
+    else:
+        K = kc.view(np.float16).astype(np.float64).reshape(-1, kvd)[:pos + 1].copy()
+        V = vc.view(np.float16).astype(np.float64).reshape(-1, kvd)[:pos + 1].copy()
+        K[pos] = k.astype(np.float16)                              # fp16 cache row, RNE
+        V[pos] = v.astype(np.float16)
     scale = P.get("attn_scale", 0.0) or 1.0 / math.sqrt(hd)
     att = np.empty(nq * hd)
     for qh in range(nq):
@@ -837,12 +844,15 @@ def _tiny_layer(seed, dims, formats, std=0.08, **variant):
     return P
 
 
-def _run_layer_case(P, dims, pos, seed):
+def _run_layer_case(P, dims, pos, seed, f32_kv=False):
     hidden, inter, nq, nkv, hd = dims
     rng = np.random.default_rng(seed)
     kvd = nkv * hd
     kc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
     vc = rng.standard_normal((pos + 2) * kvd).astype(np.float16).view(np.uint16)
+    if f32_kv:   # f32 cache rows that no fp16 holds exactly
+        kc = rng.standard_normal((pos + 2) * kvd).astype(np.float32)
+        vc = rng.standard_normal((pos + 2) * kvd).astype(np.float32)
     h = rng.standard_normal(hidden).astype(np.float32)
     layer = {k: v for k, v in P.items() if k not in ("deq", "rope_base", "q8_input")}
     layer["k_cache"], layer["v_cache"] = kc.copy(), vc.copy()
@@ -862,6 +872,24 @@ def test_decode_layer_llama_matches_float64_composition():
     got, ref = _run_layer_case(P, dims, pos=5, seed=32)
     assert _rel(got, ref()) <= 1e-5
     for mut in ("swap_norms", "gate_up_swap", "drop_residual", "rope_v", "rope_exp", "kv_map"):
+        assert _rel(got, ref((mut,))) > 1e-2, mut
+
+
+def test_decode_layer_f32_kv_matches_float64_composition():
+    """The f32-cache mode (the reference's cache, LC/src/metal/ops/kv_cache.rs:13-14; CPU
+    attention in f32, LI/src/attention/gqa.rs:29-110): cached rows read as f32 and the new
+    row stored unrounded.  Within 3e-6 of the float64 restatement (measured <= 1e-6);
+    rounding the new row to fp16 (what an fp16 cache does) moves it by more than 5e-5
+    (measured >= 2.2e-4), and the Llama mistakes still move it by more than 1e-2."""
+    dims = (256, 512, 4, 2, 64)
+    P = _tiny_layer(35, dims, {"wv": "q6_k"})
+    for pos in (0, 1, 3):
+        got, ref = _run_layer_case(P, dims, pos=pos, seed=36 + pos, f32_kv=True)
+        e, e16 = _rel(got, ref()), _rel(got, ref(("kv_fp16",)))
+        print(f"f32 kv pos={pos}: vs float64 {e:.2e}, vs fp16-rounded new row {e16:.2e}")
+        assert e <= 3e-6
+        assert e16 > 5e-5
+    for mut in ("swap_norms", "gate_up_swap", "drop_residual", "rope_v", "kv_map"):
         assert _rel(got, ref((mut,))) > 1e-2, mut
 
 
