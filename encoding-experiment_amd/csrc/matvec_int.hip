@@ -34,6 +34,18 @@
 namespace larql {
 
 // ── activation quantizer ───────────────────────────────────────────────
+// Block scale from the block's largest |x| (a fold of fmaxf from 0, which skips NaNs, so
+// any order gives it), the inverse used for the codes, and one code: round half away from
+// zero, clamp, NaN -> 0 (Rust's `as i8`: v * inv is NaN for a NaN v, or an infinite v in a
+// block whose scale is infinite).  Shared by the quantizer and the Q4_0 matrix-core kernel
+// that quantizes its own activation rows.
+__device__ __forceinline__ float q8_block_scale(float amax) { return amax / 127.0f; }
+__device__ __forceinline__ float q8_block_inv(float scale) { return scale > 0.0f ? 1.0f / scale : 0.0f; }
+__device__ __forceinline__ int q8_code(float v, float inv) {
+    const float q = roundf(v * inv);
+    return isnan(q) ? 0 : static_cast<int>(fminf(fmaxf(q, -128.0f), 127.0f));
+}
+
 // 32 threads per 32-element block; 8 blocks per 256-thread workgroup.
 __global__ __launch_bounds__(256) void quantize_q8_kernel(const float* __restrict__ x,
                                                           int8_t* __restrict__ q8,
@@ -43,14 +55,11 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float* __restric
     const int j = threadIdx.x & 31;
     if (b >= nblocks) return;  // whole 32-lane group exits together
     const float v = x[b * 32 + j];
-    float amax = fabsf(v);
+    float amax = fmaxf(0.0f, fabsf(v));
 #pragma unroll
     for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-    const float scale = amax / 127.0f;
-    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-    float q = roundf(v * inv);
-    q = fminf(fmaxf(q, -128.0f), 127.0f);
-    q8[b * 32 + j] = static_cast<int8_t>(isnan(q) ? 0.0f : q);
+    const float scale = q8_block_scale(amax);
+    q8[b * 32 + j] = static_cast<int8_t>(q8_code(v, q8_block_inv(scale)));
     if (j == 0) scales[b] = scale;
 }
 
@@ -483,6 +492,242 @@ __global__ __launch_bounds__(64 * WAVES) void q8_mfma_kernel(const uint8_t* __re
     }
 }
 
+// ── Q4_0 x Q8 on the matrix cores, 2 .. 8 activation rows ───────────────
+// Same exact int32 block dots and in-order f32 accumulation as int_mv_kernel (per block b
+// in order: cs = f16(d_b) * xs_b; acc += (float)isum_b * cs, LC/csrc/q4_dot.c:58-89), over
+// the row-major Q4_0 layout.  One wave owns a 16-row tile and walks the row in quads of
+// four blocks; per quad and group of four activation rows (TG groups), two
+// v_mfma_i32_16x16x64_i8 (block halves 0 and 1, the second accumulating onto the first)
+// with A row i = 4 t + j = activation row t of the group, block 4 q + j, live only in
+// k-group j, and B column c = weight row c, k-group g = half of block 4 q + g.  D lane
+// (g, c) then holds, in registers r = 0 .. 3, the exact int32 dots of blocks 4 q + r of
+// activation row g with weight row c: four consecutive blocks of one chain, added in order
+// in the lane (no cross-lane traffic).  Each lane loads its weight row's whole block
+// 4 q + g (16 bytes; the wave reads 64 contiguous bytes of each of its 16 rows) and its
+// four f16 scales.  The nibble codes become int8 code - 8 (bytes without borrows); the
+// activation bytes are staged in LDS in the order the nibbles unpack (even elements, then
+// odd, per 16).  Requires hidden % 128 == 0.  The weight loads are plain (cached): a wave
+// reads half of a 128-byte line of each row per quad and the next quad the other half,
+// which a nontemporal load fetched from HBM twice (pair batch [10240 x 2560] x 6: 15.4
+// against 19.6 us with the quantization launch).  W tiles per workgroup, chosen per shape
+// so the busiest CU holds the fewest tiles (640 + 640 tiles on 256 CUs: five per
+// workgroup, one workgroup per CU; with four, 64 CUs hold two).
+constexpr int kQ40MfmaD = 8;  // quads of weights in flight per wave
+
+constexpr size_t q40_mfma_lds_bytes(int nb) {
+    return (static_cast<size_t>(nb / 4) * 64 + 1) * 16 + static_cast<size_t>(nb / 4) * 32 * 4;
+}
+
+__device__ __forceinline__ uint32_t nib_minus8(uint32_t v) { return ((v | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+
+template <int TG, int W>
+__global__ __launch_bounds__(64 * W) void q4_0_mfma_kernel(const uint8_t* __restrict__ qs,
+                                                           const uint16_t* __restrict__ dsc,
+                                                           const int8_t* __restrict__ xq,
+                                                           const float* __restrict__ xsc,
+                                                           float* __restrict__ out, int rows, int nb, int m,
+                                                           IntMvPair second) {
+    constexpr int kT = 64 * W, D = kQ40MfmaD;
+    extern __shared__ uint4 lds4[];
+    int wg = blockIdx.x;
+    if (second.nwg1 > 0 && wg >= second.nwg1) {  // workgroup-uniform: the second matrix
+        qs = second.qs;
+        dsc = static_cast<const uint16_t*>(second.dsc);
+        out = second.out;
+        wg -= second.nwg1;
+    }
+    const int nq = nb >> 2;
+    const int nchunk = nq * 64;
+    uint4* xl = lds4;                                          // [nq][8 t][4 j][2 h], then a zero chunk
+    float* xsl = reinterpret_cast<float*>(lds4 + nchunk + 1);  // [nq][8 t][4 j]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int rbase = (wg * W + wave) * 16;  // < rows_pad: the grid covers rows_pad / 16 tiles exactly
+
+    // x image: job bj = (q, t, j) stages activation row t, block 4 q + j: chunks 2 bj + h
+    // (bytes 16 h .. of its 32 codes in the unpack order, even elements of the 16, then odd)
+    // and its scale xsl[bj]; zero for t >= m.  Loads return in issue order, so the x of the
+    // first PX passes is requested before the weights (a pass requested after them would
+    // wait an HBM round trip); any further pass loads and stages in turn.
+    constexpr int PX = 2, XV = 3;  // 16-byte values per job: 32 codes + the scale
+    const int njob = nq * 32;
+    auto xload = [&](int bj, uint4(&v)[XV]) __attribute__((always_inline)) {
+        const int q = bj >> 5, t = (bj >> 2) & 7, j = bj & 3;
+        const size_t blk = static_cast<size_t>(min(t, m - 1)) * nb + 4 * q + j;
+        const uint4* src = reinterpret_cast<const uint4*>(xq + blk * 32);
+        v[0] = src[0];
+        v[1] = src[1];
+        v[2].x = __float_as_uint(xsc[blk]);
+    };
+    auto xstage = [&](int bj, const uint4(&v)[XV]) __attribute__((always_inline)) {
+        const bool live = ((bj >> 2) & 7) < m;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint4 r = v[h];
+            const uint4 cv = make_uint4(__builtin_amdgcn_perm(r.y, r.x, 0x06040200u), __builtin_amdgcn_perm(r.w, r.z, 0x06040200u),
+                                        __builtin_amdgcn_perm(r.y, r.x, 0x07050301u), __builtin_amdgcn_perm(r.w, r.z, 0x07050301u));
+            xl[2 * bj + h] = live ? cv : make_uint4(0u, 0u, 0u, 0u);
+        }
+        xsl[bj] = live ? __uint_as_float(v[2].x) : 0.0f;
+    };
+    uint4 xv[PX][XV];
+#pragma unroll
+    for (int p = 0; p < PX; p++)
+        if (static_cast<int>(threadIdx.x) + p * kT < njob) xload(threadIdx.x + p * kT, xv[p]);
+
+    // then the weights, two quads (2 p, 2 p + 1) at a time: lane (g, c) loads block g of
+    // quad 2 p + (c >> 3) of rows c & 7 (wa) and 8 + (c & 7) (wb), so each load instruction
+    // reads 128 contiguous bytes of each of 8 rows (whole cache lines when the row length is
+    // a multiple of 128 bytes); one DPP rotation by 8 lanes then gives every lane both quads
+    // of its own row c.  Block scales: row c's four of each quad.
+    constexpr int DP = D / 2;  // pairs of quads in flight
+    const int np = (nq + 1) >> 1, qh = c >> 3;
+    const uint8_t* wa_row = qs + static_cast<size_t>(rbase + (c & 7)) * nb * 16 + g * 16;
+    const uint8_t* wb_row = wa_row + static_cast<size_t>(8) * nb * 16;
+    const uint2* srow = reinterpret_cast<const uint2*>(dsc + static_cast<size_t>(rbase + c) * nb);
+    uint4 wa[DP], wb[DP];
+    uint2 sa[DP], sb[DP];
+    auto refill = [&](int u, int p) __attribute__((always_inline)) {
+        // past the end (an odd quad count's last pair, or a pair beyond it): the last quad
+        // again, never used
+        const size_t qo = static_cast<size_t>(min(2 * p + qh, nq - 1)) * 64;
+        wa[u] = *reinterpret_cast<const uint4*>(wa_row + qo);
+        wb[u] = *reinterpret_cast<const uint4*>(wb_row + qo);
+        sa[u] = srow[min(2 * p, nq - 1)];
+        sb[u] = srow[min(2 * p + 1, nq - 1)];
+    };
+#pragma unroll
+    for (int u = 0; u < DP; u++) refill(u, u);
+
+#pragma unroll
+    for (int p = 0; p < PX; p++)
+        if (static_cast<int>(threadIdx.x) + p * kT < njob) xstage(threadIdx.x + p * kT, xv[p]);
+    for (int bj = threadIdx.x + PX * kT; bj < njob; bj += kT) {
+        uint4 v[XV];
+        xload(bj, v);
+        xstage(bj, v);
+    }
+    if (threadIdx.x == 0) xl[nchunk] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+
+    // A operand of this lane for group tg, half h: row c = 4 t + j live in k-group j only
+    const bool a_on = (c & 3) == g;
+    auto a_of = [&](int q, int tg, int h) __attribute__((always_inline)) {
+        const int t = 4 * tg + (c >> 2);
+        const uint4 v = xl[a_on ? ((q * 8 + t) * 4 + g) * 2 + h : nchunk];
+        return v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+    };
+    float acc[TG];
+#pragma unroll
+    for (int tg = 0; tg < TG; tg++) acc[tg] = 0.0f;
+    auto quad = [&](int q, const uint4& w, const uint2& s2) __attribute__((always_inline)) {
+        const v4i b0 = {static_cast<int>(nib_minus8(w.x & 0x0F0F0F0Fu)), static_cast<int>(nib_minus8(w.y & 0x0F0F0F0Fu)),
+                        static_cast<int>(nib_minus8((w.x >> 4) & 0x0F0F0F0Fu)),
+                        static_cast<int>(nib_minus8((w.y >> 4) & 0x0F0F0F0Fu))};
+        const v4i b1 = {static_cast<int>(nib_minus8(w.z & 0x0F0F0F0Fu)), static_cast<int>(nib_minus8(w.w & 0x0F0F0F0Fu)),
+                        static_cast<int>(nib_minus8((w.z >> 4) & 0x0F0F0F0Fu)),
+                        static_cast<int>(nib_minus8((w.w >> 4) & 0x0F0F0F0Fu))};
+        const float wsc[4] = {h2f(s2.x), h2f(s2.x >> 16), h2f(s2.y), h2f(s2.y >> 16)};
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) {
+            v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_of(q, tg, 0), b0, v4i{0, 0, 0, 0}, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_of(q, tg, 1), b1, d, 0, 0, 0);
+            const float4 xs4 = *reinterpret_cast<const float4*>(xsl + (q * 8 + 4 * tg + g) * 4);
+            const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {  // blocks 4 q + r in order
+                const float cs = wsc[r] * xs[r];
+                const float p = static_cast<float>(d[r]) * cs;
+                acc[tg] = acc[tg] + p;
+            }
+        }
+    };
+    // lane c < 8 holds (row c, quad 2 p) in wa and passes wb (row c + 8, quad 2 p) to lane
+    // c + 8; lane c >= 8 holds (row c, quad 2 p + 1) in wb and passes wa (row c - 8,
+    // quad 2 p + 1) to lane c - 8.  DPP row_ror:8 swaps the two halves of each 16-lane row.
+    auto pair = [&](int p, int u) __attribute__((always_inline)) {
+        const uint4 give = qh ? wa[u] : wb[u];
+        uint4 got;
+        got.x = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(give.x), 0x128, 0xF, 0xF, false));
+        got.y = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(give.y), 0x128, 0xF, 0xF, false));
+        got.z = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(give.z), 0x128, 0xF, 0xF, false));
+        got.w = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(give.w), 0x128, 0xF, 0xF, false));
+        quad(2 * p, qh ? got : wa[u], sa[u]);
+        if (2 * p + 1 < nq) quad(2 * p + 1, qh ? wb[u] : got, sb[u]);
+    };
+    int p0 = 0;
+    for (; p0 + DP <= np; p0 += DP) {
+#pragma unroll
+        for (int u = 0; u < DP; u++) {
+            pair(p0 + u, u);
+            refill(u, p0 + u + DP);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < DP; u++)
+        if (p0 + u < np) pair(p0 + u, u);
+
+    const int row = rbase + c;
+    if (row < rows) {
+#pragma unroll
+        for (int tg = 0; tg < TG; tg++) {
+            const int t = 4 * tg + g;
+            if (t < m) out[static_cast<size_t>(t) * rows + row] = acc[tg];
+        }
+    }
+}
+
+// Q4_0 with up to 8 activation rows (w2 / out2: a second matrix of the same shape in the
+// same grid).
+template <int W>
+void launch_q4_0_mfma_w(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s,
+                        const DevWeight* w2, float* out2) {
+    const int nb = static_cast<int>(w.cols / 32);
+    const unsigned grid1 = static_cast<unsigned>(w.rows_pad / 16 / W);
+    IntMvPair second{};
+    unsigned grid = grid1;
+    if (w2) {
+        second.qs = w2->qs;
+        second.dsc = w2->d;
+        second.out = out2;
+        second.nwg1 = static_cast<int>(grid1);
+        grid = 2 * grid1;
+    }
+    const size_t lds = q40_mfma_lds_bytes(nb);
+    if (m <= 4)
+        q4_0_mfma_kernel<1, W><<<dim3(grid), dim3(64 * W), lds, s>>>(
+            w.qs, static_cast<const uint16_t*>(w.d), q8x, q8s, out, static_cast<int>(w.rows), nb, m, second);
+    else
+        q4_0_mfma_kernel<2, W><<<dim3(grid), dim3(64 * W), lds, s>>>(
+            w.qs, static_cast<const uint16_t*>(w.d), q8x, q8s, out, static_cast<int>(w.rows), nb, m, second);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+// m (2 .. 8) rows through the matrix-core kernel; false when the weight does not fit it
+// (hidden % 128, the x image in LDS, rows padded to 64).
+bool launch_q4_0_mfma(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s,
+                      const DevWeight* w2, float* out2) {
+    const int nb = static_cast<int>(w.cols / 32);
+    if (m < 2 || m > 8 || nb % 4 != 0 || q40_mfma_lds_bytes(nb) > 64 * 1024 || w.rows_pad % 64 != 0) return false;
+    // tiles per workgroup: of those that divide the tile count (so every wave owns a tile
+    // in the allocation), the one whose busiest CU holds the fewest tiles; ties to the
+    // larger workgroup (fewer x images staged)
+    const size_t tiles = w.rows_pad / 16, mats = w2 ? 2 : 1, cus = static_cast<size_t>(current_device_cus());
+    int best = 4;
+    size_t best_cost = ~size_t{0};
+    for (int W : {8, 5, 4}) {
+        if (tiles % W != 0) continue;
+        const size_t cost = (mats * tiles / W + cus - 1) / cus * W;
+        if (cost < best_cost) best = W, best_cost = cost;
+    }
+    switch (best) {
+        case 8: launch_q4_0_mfma_w<8>(w, q8x, q8s, out, m, s, w2, out2); break;
+        case 5: launch_q4_0_mfma_w<5>(w, q8x, q8s, out, m, s, w2, out2); break;
+        default: launch_q4_0_mfma_w<4>(w, q8x, q8s, out, m, s, w2, out2); break;
+    }
+    return true;
+}
+
 template <int D, int WAVES>
 void launch_q8_mfma_t(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s) {
     const int nb = static_cast<int>(w.cols / 32);
@@ -553,6 +798,14 @@ void launch_int_mv_batched(const DevWeight& w, const int8_t* q8x, const float* q
     size_t done = 0;
     while (done < m) {
         const size_t left = m - done;
+        if constexpr (FMT == LARQL_Q4_0) {  // 2 .. 8 rows of a pass on the matrix cores
+            const int take = static_cast<int>(std::min<size_t>(left, 8));
+            if (launch_q4_0_mfma(w, q8x + done * w.cols, q8s + done * nb, out + done * w.rows, take, s, w2,
+                                 w2 ? out2 + done * w.rows : nullptr)) {
+                done += take;
+                continue;
+            }
+        }
         int cap = 1;  // the largest kernel whose x image fits
         for (int c : {8, 4, 2})
             if (x_lds_bytes<FMT>(c, nb) <= kLdsLimit) { cap = c; break; }

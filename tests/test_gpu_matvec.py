@@ -213,6 +213,11 @@ def test_quantize_to_q8_bit_exact(hip):
     x[64:96] = np.float32(1e-30)
     x[96:128] *= np.float32(1e4)
     x[128] = 2.5
+    x[160:192] = np.nan                              # all-NaN block -> scale 0 (the fold starts at 0)
+    x[200] = np.nan                                  # one NaN -> code 0, the scale from the rest
+    x[224:256] = np.float32(3.0)
+    x[230] = np.inf                                  # scale inf, inv 0: finite -> 0, inf * 0 = NaN -> 0
+    x[262] = -np.inf
     q, s = hip.quantize_to_q8(x)
     rq, rs = oracle.quantize_to_q8(x)
     assert np.array_equal(q, rq) and np.array_equal(s.view(np.uint32), rs.view(np.uint32))

@@ -100,9 +100,9 @@ def test_vecmat_dev_matches_host_entry(hip):
 
 # (6, 10240, 2560), (17, 300, 576), (130, 200, 128): several positions (one launch per pass of
 # up to 8, ragged row tiles); (1, 64, 32): one position; (9, 300, 544): hidden not a multiple
-# of 64
+# of 64; (9, 640, 256): the matrix-core kernel, passes of 8 and 1 rows
 @pytest.mark.parametrize("seq,rows,hidden", [(6, 10240, 2560), (17, 300, 576), (130, 200, 128), (1, 64, 32),
-                                             (9, 300, 544)])
+                                             (9, 300, 544), (9, 640, 256)])
 def test_pair_batch_bit_exact(hip, seq, rows, hidden):
     print(f"[pair batch] seq={seq} rows={rows} hidden={hidden}", flush=True)
     gate = oracle.quantize_q4_0(oracle.gauss(41 + seq, rows * hidden, 0.0, 0.02))
@@ -140,6 +140,47 @@ def test_pair_batch_dev(hip):
         q8, q8s = oracle.quantize_to_q8(x[s])
         assert np.array_equal(g[s].view(np.uint32), oracle.q4_0_matvec_blockint(gate, q8, q8s, rows, hidden).view(np.uint32))
         assert np.array_equal(u[s].view(np.uint32), oracle.q4_0_matvec_blockint(up, q8, q8s, rows, hidden).view(np.uint32))
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+def test_pair_batch_dev_quantizes_like_quantize_to_q8(hip, offset):
+    """The device pair batch quantizes f32 rows inside the matrix-core kernel (x 16-byte
+    aligned) or through the separate quantizer (offset 1: x one float past an aligned
+    address): both bit-exact with quantize_to_q8 + the block-integer matvec, over zero, NaN,
+    tiny, huge and half-way activations."""
+    torch = pytest.importorskip("torch")
+    seq, rows, hidden = 7, 1280, 512
+    gate = oracle.quantize_q4_0(oracle.gauss(55, rows * hidden, 0.0, 0.02))
+    up = oracle.quantize_q4_0(oracle.gauss(56, rows * hidden, 0.0, 0.02))
+    x = oracle.gauss(57, seq * hidden).reshape(seq, hidden)
+    x[0, :32] = 0.0
+    x[1, 32:64] = np.nan
+    x[1, 70] = np.nan
+    x[2, :32] = np.float32(1e-30)
+    x[3, 96:128] *= np.float32(1e4)
+    x[4, :32] = np.arange(-16, 16, dtype=np.float32) + np.float32(0.5)
+    x[4, 31] = np.float32(127.0)                     # scale 1: the others are rounding ties
+    x[5, 64:96] = np.float32(127.0)
+    x[6, :] = -x[6, :]
+    hg = hip.register_weight(larql_hip.Q4_0, gate, rows, hidden)
+    hu = hip.register_weight(larql_hip.Q4_0, up, rows, hidden)
+    try:
+        buf = torch.zeros(seq * hidden + 4, device="cuda", dtype=torch.float32)
+        buf[offset:offset + seq * hidden] = torch.from_numpy(x.reshape(-1)).cuda()
+        dx = buf[offset:offset + seq * hidden]
+        dg = torch.empty(seq * rows, device="cuda", dtype=torch.float32)
+        du = torch.empty(seq * rows, device="cuda", dtype=torch.float32)
+        hip.pair_batch_dev(hg, hu, dx, seq, dg, du)
+        hip.synchronize()
+        g = dg.cpu().numpy().reshape(seq, rows)
+        u = du.cpu().numpy().reshape(seq, rows)
+    finally:
+        hip.release_weight(hg)
+        hip.release_weight(hu)
+    for s in range(seq):
+        q8, q8s = oracle.quantize_to_q8(x[s])
+        assert np.array_equal(g[s].view(np.uint32), oracle.q4_0_matvec_blockint(gate, q8, q8s, rows, hidden).view(np.uint32)), s
+        assert np.array_equal(u[s].view(np.uint32), oracle.q4_0_matvec_blockint(up, q8, q8s, rows, hidden).view(np.uint32)), s
 
 
 def test_pair_batch_shape_mismatch_is_an_error():
