@@ -512,7 +512,7 @@ __global__ __launch_bounds__(64 * WAVES) void q8_mfma_kernel(const uint8_t* __re
 // against 19.6 us with the quantization launch).  W tiles per workgroup, chosen per shape
 // so the busiest CU holds the fewest tiles (640 + 640 tiles on 256 CUs: five per
 // workgroup, one workgroup per CU; with four, 64 CUs hold two).
-constexpr int kQ40MfmaD = 8;  // quads of weights in flight per wave
+constexpr int kQ40MfmaD = 4;  // quads of weights in flight per wave (2, 4, 6, 8 tried: 4 is fastest)
 
 constexpr size_t q40_mfma_lds_bytes(int nb) {
     return (static_cast<size_t>(nb / 4) * 64 + 1) * 16 + static_cast<size_t>(nb / 4) * 32 * 4;

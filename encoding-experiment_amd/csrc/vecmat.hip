@@ -11,13 +11,19 @@
 // the chunk partials in a fixed grouping — so the result is deterministic and within
 // f32 rounding of the reference (the bar is relative, 1e-3).
 //
-// Pass 1 (q4_vecmat_part_kernel): workgroup (tile, chunk) = 512 output columns x one
-// chunk of rows, four waves each owning a quarter of the chunk's rows.  Lane l holds
-// dword l % 4 of block l / 4 of the tile (8 outputs), so one row is a 256-byte
-// contiguous read per wave.  The row's activation is wave-uniform (a scalar load),
-// which makes the skip a uniform branch.
+// Pass 1 (q4_vecmat_part_kernel): workgroup (tile, chunk) = the output columns of 8
+// blocks (256 outputs) x one chunk of rows.  Thread (g, b) owns block b of the tile (16
+// bytes, 32 outputs) in rows g, g + G, g + 2 G, ... of the chunk, so a load instruction
+// reads one whole 128-byte line of each of 8 rows.  Rows whose activation is skipped
+// contribute a zero scale.  The G lane sums of each column are added in row-group order
+// through LDS.  Narrow tiles keep the partials small (chunks x hidden floats, written and
+// read once): whole-row workgroups need several times the chunks to fill the GPU, and at
+// [10240 x 2560] their partials cost more than the row pieces save (14.4 us against 11.0).
 // Pass 2 (q4_vecmat_sum_kernel): out[k] = sum over chunks of part[chunk][k], chunk
-// groups in parallel and their totals added in a fixed order.
+// groups in parallel and their totals added in a fixed order.  Folding it into pass 1
+// (the last workgroup of a tile sums the tile, found by a device counter) measured
+// slower: 14.9 us, the counter and the partial loads adding round trips after the last
+// partial lands.
 #include "device_common.h"
 #include "larql_hip_internal.h"
 
@@ -26,84 +32,87 @@ namespace larql {
 
 namespace {
 
-constexpr int kVmThreads = 256;
-constexpr int kVmWaves = kVmThreads / 64;
-constexpr int kVmTileCols = 512;   // 64 lanes x 8 outputs
-constexpr int kVmRowsPerWave = 32;  // rows in flight per wave (all loaded before any arithmetic)
+constexpr int kVmTileBlocks = 8;     // blocks (of 32 columns) per tile
+constexpr int kVmThreadsWant = 256;  // threads per workgroup
+constexpr int kVmMaxThreads = 512;
+constexpr int kVmR = 8;              // rows in flight per thread
 
-// Grid (ceil(hidden / 512), chunks).  part: [chunks][hidden].
-__global__ __launch_bounds__(kVmThreads) void q4_vecmat_part_kernel(const uint32_t* __restrict__ qs,
-                                                                    const uint16_t* __restrict__ dsc,
-                                                                    const float* __restrict__ act,
-                                                                    float* __restrict__ part, int inter, int hidden,
-                                                                    int rows_per_chunk) {
-    __shared__ float red[kVmWaves - 1][8][64];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+// Tile width and row groups for a row of nb blocks; the LDS partial sums (G x 33 x tile
+// floats) stay within 64 KB.
+struct VmShape {
+    int tb, groups, threads;
+};
+VmShape vecmat_shape(int nb) {
+    VmShape v;
+    v.tb = std::min(nb, kVmTileBlocks);
+    v.groups = std::max(1, std::min(kVmThreadsWant / v.tb, 496 / v.tb));
+    v.threads = (v.tb * v.groups + 63) / 64 * 64;
+    return v;
+}
+
+// Grid (tiles, chunks), vecmat_shape threads.  part: [chunks][hidden].
+__global__ __launch_bounds__(kVmMaxThreads) void q4_vecmat_part_kernel(const uint4* __restrict__ qs,
+                                                                       const uint16_t* __restrict__ dsc,
+                                                                       const float* __restrict__ act,
+                                                                       float* __restrict__ part, int inter, int hidden,
+                                                                       int rows_per_chunk, int tb, int groups) {
+    extern __shared__ float red[];  // [groups][33 tb]: block b's 32 sums at 33 b
+    const int t = threadIdx.x;
     const int nb = hidden >> 5;
-    const int col0 = blockIdx.x * kVmTileCols + 8 * lane;  // first output of this lane
-    const bool active = col0 < hidden;
-    const int blk = min(col0, hidden - 8) >> 5;            // block column
-    const int dw = (min(col0, hidden - 8) >> 3) & 3;       // dword within the block's 16 bytes
-    // rows of this wave: a contiguous quarter of the chunk
+    const int b = t % tb, g = t / tb;
+    const int blk = min(static_cast<int>(blockIdx.x) * tb + b, nb - 1);  // past the edge: a real block, unused
     const int c0 = blockIdx.y * rows_per_chunk;
     const int c1 = min(inter, c0 + rows_per_chunk);
-    const int per = (c1 - c0 + kVmWaves - 1) / kVmWaves;
-    const int r0 = min(c1, c0 + wave * per), r1 = min(c1, r0 + per);
 
-    float acc[8], ssum = 0.0f;
+    if (g < groups) {
+        float acc[32], ssum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-    for (int rb = r0; rb < r1; rb += kVmRowsPerWave) {
-        uint32_t q[kVmRowsPerWave];
-        uint32_t d[kVmRowsPerWave];
-        float a[kVmRowsPerWave];
+        for (int i = 0; i < 32; i++) acc[i] = 0.0f;
+        for (int rb = c0 + g; rb < c1; rb += groups * kVmR) {
+            uint4 q[kVmR];
+            uint32_t d[kVmR];
+            float a[kVmR];
 #pragma unroll
-        for (int k = 0; k < kVmRowsPerWave; k++) {
-            const int row = min(rb + k, r1 - 1);
-            const size_t b = static_cast<size_t>(row) * nb + blk;
-            q[k] = qs[b * 4 + dw];
-            d[k] = dsc[b];
-            a[k] = act[row];
+            for (int k = 0; k < kVmR; k++) {
+                const int row = min(rb + k * groups, c1 - 1);
+                const size_t bi = static_cast<size_t>(row) * nb + blk;
+                q[k] = qs[bi];
+                d[k] = dsc[bi];
+                a[k] = act[row];
+            }
+#pragma unroll
+            for (int k = 0; k < kVmR; k++) {
+                const float av = a[k];
+                const bool use = rb + k * groups < c1 && !(av > -1e-10f && av < 1e-10f);
+                const float scale = use ? h2f(d[k]) * av : 0.0f;
+                const uint32_t w4[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t lo4 = w4[i] & 0x0F0F0F0Fu, hi4 = (w4[i] >> 4) & 0x0F0F0F0Fu;
+                    acc[8 * i + 0] = __builtin_fmaf(ubyte0(lo4), scale, acc[8 * i + 0]);
+                    acc[8 * i + 1] = __builtin_fmaf(ubyte0(hi4), scale, acc[8 * i + 1]);
+                    acc[8 * i + 2] = __builtin_fmaf(ubyte1(lo4), scale, acc[8 * i + 2]);
+                    acc[8 * i + 3] = __builtin_fmaf(ubyte1(hi4), scale, acc[8 * i + 3]);
+                    acc[8 * i + 4] = __builtin_fmaf(ubyte2(lo4), scale, acc[8 * i + 4]);
+                    acc[8 * i + 5] = __builtin_fmaf(ubyte2(hi4), scale, acc[8 * i + 5]);
+                    acc[8 * i + 6] = __builtin_fmaf(ubyte3(lo4), scale, acc[8 * i + 6]);
+                    acc[8 * i + 7] = __builtin_fmaf(ubyte3(hi4), scale, acc[8 * i + 7]);
+                }
+                ssum = ssum + scale;
+            }
         }
+        float* my = red + static_cast<size_t>(g) * 33 * tb + 33 * b;
 #pragma unroll
-        for (int k = 0; k < kVmRowsPerWave; k++) {
-            const float av = a[k];
-            if (rb + k >= r1 || (av > -1e-10f && av < 1e-10f)) continue;  // wave-uniform
-            const float scale = h2f(d[k]) * av;
-            // sum((nib - 8) * scale) as fma(nib, scale, acc) and 8 * sum(scale) once
-            const uint32_t lo4 = q[k] & 0x0F0F0F0Fu, hi4 = (q[k] >> 4) & 0x0F0F0F0Fu;
-            acc[0] = __builtin_fmaf(ubyte0(lo4), scale, acc[0]);
-            acc[1] = __builtin_fmaf(ubyte0(hi4), scale, acc[1]);
-            acc[2] = __builtin_fmaf(ubyte1(lo4), scale, acc[2]);
-            acc[3] = __builtin_fmaf(ubyte1(hi4), scale, acc[3]);
-            acc[4] = __builtin_fmaf(ubyte2(lo4), scale, acc[4]);
-            acc[5] = __builtin_fmaf(ubyte2(hi4), scale, acc[5]);
-            acc[6] = __builtin_fmaf(ubyte3(lo4), scale, acc[6]);
-            acc[7] = __builtin_fmaf(ubyte3(hi4), scale, acc[7]);
-            ssum = ssum + scale;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = __builtin_fmaf(-8.0f, ssum, acc[i]);
-    // the four waves' sums in wave order
-    if (wave > 0) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) red[wave - 1][i][lane] = acc[i];
+        for (int i = 0; i < 32; i++) my[i] = __builtin_fmaf(-8.0f, ssum, acc[i]);
     }
     __syncthreads();
-    if (wave == 0 && active) {
-        float o[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float v = acc[i];
-#pragma unroll
-            for (int w = 0; w < kVmWaves - 1; w++) v = v + red[w][i][lane];
-            o[i] = v;
-        }
-        float4* dst = reinterpret_cast<float4*>(part + static_cast<size_t>(blockIdx.y) * hidden + col0);
-        dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-        dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+    // column c of the tile (block c / 32, element c % 32): its row groups' sums in order
+    const int ncol = min(32 * tb, hidden - static_cast<int>(blockIdx.x) * 32 * tb);
+    for (int c = t; c < ncol; c += blockDim.x) {
+        const int li = 33 * (c >> 5) + (c & 31);
+        float v = red[li];
+        for (int r = 1; r < groups; r++) v = v + red[static_cast<size_t>(r) * 33 * tb + li];
+        part[static_cast<size_t>(blockIdx.y) * hidden + static_cast<size_t>(blockIdx.x) * 32 * tb + c] = v;
     }
 }
 
@@ -138,15 +147,14 @@ __global__ __launch_bounds__(256) void q4_vecmat_sum_kernel(const float* __restr
 
 }  // namespace
 
-// Chunks: two workgroups per CU (about 8 waves per CU) without letting the partials
-// (4 bytes x chunks x hidden, written and read once) pass ~1/8 of the weight bytes
-// (18/32 bytes per weight).  Measured on [10240 x 2560]: 14.0 / 10.9 / 12.5 us for one,
-// two and four workgroups per CU.
+// Chunks: two workgroups per CU, each at least one row per row group, the partials at
+// most 1/8 of the weight bytes.
 size_t q4_vecmat_chunks(size_t inter, size_t hidden) {
-    const size_t tiles = (hidden + kVmTileCols - 1) / kVmTileCols;
+    const VmShape v = vecmat_shape(static_cast<int>(hidden / 32));
+    const size_t tiles = (hidden / 32 + v.tb - 1) / v.tb;
     const size_t want = std::max<size_t>(1, (static_cast<size_t>(current_device_cus()) * 2 + tiles - 1) / tiles);
     const size_t cap = std::max<size_t>(1, inter * 18 / (32 * 4 * 8));  // partials <= weights / 8
-    return std::max<size_t>(1, std::min({want, cap, (inter + kVmWaves - 1) / kVmWaves}));
+    return std::max<size_t>(1, std::min({want, cap, inter / static_cast<size_t>(v.groups)}));
 }
 
 void launch_q4_vecmat(const DevWeight& w, const float* act, float* out, float* part, size_t chunks, hipStream_t s) {
@@ -154,12 +162,14 @@ void launch_q4_vecmat(const DevWeight& w, const float* act, float* out, float* p
     if (w.cols % 32 || w.cols == 0 || w.rows == 0) fail(LARQL_HIP_ERR_INVALID, "q4_vecmat: shape");
     if (w.rows > 0x7FFFFFFF / (w.cols / 32)) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4_vecmat: matrix too large");
     const int inter = static_cast<int>(w.rows), hidden = static_cast<int>(w.cols);
+    const VmShape v = vecmat_shape(hidden / 32);
     const int rows_per_chunk = static_cast<int>((w.rows + chunks - 1) / chunks);
     const int nch = (inter + rows_per_chunk - 1) / rows_per_chunk;
-    const dim3 g1(static_cast<unsigned>((hidden + kVmTileCols - 1) / kVmTileCols), static_cast<unsigned>(nch));
-    q4_vecmat_part_kernel<<<g1, dim3(kVmThreads), 0, s>>>(reinterpret_cast<const uint32_t*>(w.qs),
-                                                          static_cast<const uint16_t*>(w.d), act, part, inter, hidden,
-                                                          rows_per_chunk);
+    const dim3 g1(static_cast<unsigned>((hidden / 32 + v.tb - 1) / v.tb), static_cast<unsigned>(nch));
+    const size_t lds = static_cast<size_t>(v.groups) * 33 * v.tb * sizeof(float);
+    q4_vecmat_part_kernel<<<g1, dim3(v.threads), lds, s>>>(reinterpret_cast<const uint4*>(w.qs),
+                                                           static_cast<const uint16_t*>(w.d), act, part, inter, hidden,
+                                                           rows_per_chunk, v.tb, v.groups);
     LARQL_HIP_CHECK(hipGetLastError());
     q4_vecmat_sum_kernel<<<dim3(static_cast<unsigned>((hidden + kSumCols - 1) / kSumCols)), dim3(256), 0, s>>>(
         part, out, hidden, nch);

@@ -26,7 +26,9 @@ def rel_err(got, ref):
     return float(np.max(np.abs(got.astype(np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
 
 
-@pytest.mark.parametrize("inter,hidden", [(10240, 2560), (1, 32), (7, 64), (300, 544), (14336, 4096), (4099, 1056)])
+# (20000, 8192): 32 column tiles, few chunks of many rows
+@pytest.mark.parametrize("inter,hidden", [(10240, 2560), (1, 32), (7, 64), (300, 544), (14336, 4096), (4099, 1056),
+                                          (20000, 8192)])
 def test_q4_vecmat_matches_oracle(hip, inter, hidden):
     print(f"[vecmat] inter={inter} hidden={hidden}", flush=True)
     q4 = oracle.quantize_q4_0(oracle.gauss(900 + inter, inter * hidden, 0.0, 0.02))
@@ -96,6 +98,51 @@ def test_vecmat_dev_matches_host_entry(hip):
         hip.release_weight(h)
     host = hip.q4_vecmat(act, q4, inter, hidden)
     assert np.array_equal(dev.view(np.uint32), host.view(np.uint32))   # same kernels, same order
+
+
+def test_vecmat_dev_graph_replays_and_shape_changes(hip):
+    """The vecmat's chunk partials live in one context buffer that grows with the shape:
+    eager calls over shapes with more and fewer column tiles and chunks, then a captured
+    graph of two calls replayed three times with eager calls between, all bit-identical
+    to the first eager results (the summation order is fixed)."""
+    torch = pytest.importorskip("torch")
+    shapes = [(4096, 1024), (2048, 8192), (10240, 2560)]
+    hs, acts, outs, ref = [], [], [], []
+    try:
+        for i, (inter, hidden) in enumerate(shapes):
+            q4 = oracle.quantize_q4_0(oracle.gauss(60 + i, inter * hidden, 0.0, 0.02))
+            hs.append(hip.register_weight(larql_hip.Q4_0, q4, inter, hidden))
+            acts.append(torch.from_numpy(oracle.gauss(70 + i, inter)).cuda())
+            outs.append(torch.empty(hidden, device="cuda", dtype=torch.float32))
+            hip.vecmat_dev(hs[-1], acts[-1], outs[-1])
+            hip.synchronize()
+            ref.append(outs[-1].cpu().numpy().copy())
+            e = rel_err(ref[-1], oracle.q4_0_vecmat(acts[-1].cpu().numpy(), q4, inter, hidden))
+            assert e <= REL_TOL, (inter, hidden, e)
+        for i in (1, 0, 2):   # again, in another order
+            outs[i].fill_(7.0)
+            hip.vecmat_dev(hs[i], acts[i], outs[i])
+            hip.synchronize()
+            assert np.array_equal(outs[i].cpu().numpy().view(np.uint32), ref[i].view(np.uint32)), i
+        side = torch.cuda.Stream()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            hip.vecmat_dev(hs[2], acts[2], outs[2], stream=side)
+            hip.vecmat_dev(hs[0], acts[0], outs[0], stream=side)
+        for rep in range(3):
+            outs[0].fill_(7.0)
+            outs[2].fill_(7.0)
+            hip.vecmat_dev(hs[1], acts[1], outs[1])
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for i in range(3):
+                assert np.array_equal(outs[i].cpu().numpy().view(np.uint32), ref[i].view(np.uint32)), (rep, i)
+        del graph
+    finally:
+        for h in hs:
+            hip.release_weight(h)
 
 
 # (6, 10240, 2560), (17, 300, 576), (130, 200, 128): several positions (one launch per pass of
