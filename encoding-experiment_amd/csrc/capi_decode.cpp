@@ -47,8 +47,11 @@ struct LayerDev {
 
 struct larql_hip_model {
     std::vector<LayerDev> layers;
-    size_t hidden = 0, inter = 0, q_dim = 0, kv_dim = 0;
-    int nq = 0, nkv = 0, hd = 0;
+    size_t hidden = 0, inter = 0;
+    // the largest over the layers (each layer has its own head geometry,
+    // LC/src/metal/decode.rs:101-110): q and kv widths, q|k|v width, attention partial
+    // floats per position split
+    size_t q_dim = 0, kv_dim = 0, qkv_dim = 0, part_per_split = 0;
     bool has_head = false;
     DevWeight head;
     float* final_norm = nullptr;
@@ -220,7 +223,7 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
             if (d.hd <= 0 || d.nq <= 0 || d.nkv <= 0 || d.nq % d.nkv || d.hd % 8)
                 fail(LARQL_HIP_ERR_INVALID, "decode: bad head geometry");
             if (!larql::attn_supported(d.nq / d.nkv, d.hd))
-                fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: attention takes head_dim a multiple of 32 up to 256 and "
+                fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: attention takes head_dim a multiple of 32 up to 512 and "
                                                 "1..8 query heads per kv head");
             d.rdim = L.rotary_dim ? static_cast<int>(L.rotary_dim) : d.hd;
             if (d.rdim > d.hd || d.rdim % 2) fail(LARQL_HIP_ERR_INVALID, "decode: bad rotary_dim");
@@ -228,14 +231,11 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
             d.eps = L.eps > 0.f ? static_cast<double>(L.eps) : 1e-6;
             d.attn_scale = L.attn_scale != 0.f ? L.attn_scale : static_cast<float>(1.0 / std::sqrt(double(d.hd)));
             d.rope_base = L.rope_base;
-            if (l == 0) {
-                m->nq = d.nq;
-                m->nkv = d.nkv;
-                m->hd = d.hd;
-            } else if (d.nq != m->nq || d.nkv != m->nkv || d.hd != m->hd) {
-                fail(LARQL_HIP_ERR_UNSUPPORTED, "decode: per-layer head geometry must be uniform");
-            }
             const size_t qd = static_cast<size_t>(d.nq) * d.hd, kvd = static_cast<size_t>(d.nkv) * d.hd;
+            m->q_dim = std::max(m->q_dim, qd);
+            m->kv_dim = std::max(m->kv_dim, kvd);
+            m->qkv_dim = std::max(m->qkv_dim, qd + 2 * kvd);
+            m->part_per_split = std::max(m->part_per_split, larql::attn_part_floats(d.nq, 1, d.hd));
             // one fused launch needs one format (and, for Q4_KF, one byte layout)
             auto form = [&](const larql_quant_weight& q, size_t r, size_t k) {
                 return q.format * 4 + (q.format == LARQL_Q4_KF ? larql::q4kf_form(q.len, r, k) : 0);
@@ -284,12 +284,10 @@ larql_hip_model* build_model(larql_hip_ctx* c, const larql_pipeline_layer* layer
             }
             m->layers.push_back(d);
         }
-        m->q_dim = static_cast<size_t>(m->nq) * m->hd;
-        m->kv_dim = static_cast<size_t>(m->nkv) * m->hd;
         m->h0 = static_cast<float*>(dev_alloc(m, hidden * 4));
         m->h1 = static_cast<float*>(dev_alloc(m, hidden * 4));
         m->xin = static_cast<float*>(dev_alloc(m, hidden * 4));
-        m->qkv = static_cast<float*>(dev_alloc(m, (m->q_dim + 2 * m->kv_dim) * 4));
+        m->qkv = static_cast<float*>(dev_alloc(m, m->qkv_dim * 4));
         m->attn = static_cast<float*>(dev_alloc(m, m->q_dim * 4));
         m->act = static_cast<float*>(dev_alloc(m, inter * 4));
         m->gtmp = static_cast<float*>(dev_alloc(m, inter * 4));
@@ -361,47 +359,86 @@ const float2* rope_table(larql_hip_ctx* c, double base, int rdim, hipStream_t s)
     return t.cs;
 }
 
-// Make room for `layers` layers of [cap][num_kv][head_dim] with cap >= need (initial
-// capacity 4096 as in the reference, LC/src/metal/trait_impl.rs:163; doubled on demand,
-// so attention is not limited in T).
-void kv_ensure(larql_hip_ctx* c, size_t layers, size_t num_kv, size_t head_dim, size_t need) {
+// Capacity >= need positions for every layer held (initial capacity 4096 as in the
+// reference, LC/src/metal/trait_impl.rs:163; doubled on demand, so attention is not
+// limited in T); growth copies the rows in use.
+void kv_reserve(larql_hip_ctx* c, size_t need) {
     auto& kv = c->kv;
-    if (kv.num_layers && (kv.num_kv != num_kv || kv.head_dim != head_dim)) kv_free(c);
-    const size_t row = num_kv * head_dim;
-    if (kv.num_layers == 0) {
-        kv.num_kv = num_kv;
-        kv.head_dim = head_dim;
+    if (kv.num_layers == 0 && kv.max_seq == 0) {
         kv.max_seq = need > 4096 ? (need + 7) & ~size_t(7) : 4096;  // V blocks of 8 positions
         kv.current_len = 0;
     }
-    if (need > kv.max_seq) {
-        size_t cap = kv.max_seq * 2;
-        while (cap < need) cap *= 2;
-        (void)hipDeviceSynchronize();
-        for (size_t l = 0; l < kv.num_layers; l++) {
-            for (auto* vec : {&kv.k, &kv.v}) {
-                __half* p = nullptr;
-                if (hipMalloc(&p, cap * row * sizeof(__half)) != hipSuccess) fail(LARQL_HIP_ERR_NOMEM, "KV grow failed");
-                // V blocks hold 8 positions: copy whole blocks (K rows up to the same bound)
-                const size_t len8 = (kv.current_len + 7) & ~size_t(7);
-                LARQL_HIP_CHECK(hipMemcpy(p, (*vec)[l], len8 * row * sizeof(__half), hipMemcpyDeviceToDevice));
-                (void)hipFree((*vec)[l]);
-                (*vec)[l] = p;
-            }
+    if (need <= kv.max_seq) return;
+    size_t cap = kv.max_seq * 2;
+    while (cap < need) cap *= 2;
+    (void)hipDeviceSynchronize();
+    for (size_t l = 0; l < kv.num_layers; l++) {
+        const size_t row = kv.num_kv[l] * kv.head_dim[l];
+        for (auto* vec : {&kv.k, &kv.v}) {
+            __half* p = nullptr;
+            if (hipMalloc(&p, cap * row * sizeof(__half)) != hipSuccess) fail(LARQL_HIP_ERR_NOMEM, "KV grow failed");
+            // V blocks hold 8 positions: copy whole blocks (K rows up to the same bound)
+            const size_t len8 = (kv.current_len + 7) & ~size_t(7);
+            LARQL_HIP_CHECK(hipMemcpy(p, (*vec)[l], len8 * row * sizeof(__half), hipMemcpyDeviceToDevice));
+            (void)hipFree((*vec)[l]);
+            (*vec)[l] = p;
         }
-        kv.max_seq = cap;
     }
-    while (kv.num_layers < layers) {
-        __half *k = nullptr, *v = nullptr;
+    kv.max_seq = cap;
+}
+
+// Layer l held with geometry [cap][num_kv][head_dim]: layers below it that are missing
+// are made with the same geometry; a layer held with another geometry is made again (its
+// rows dropped).  Returns whether a held layer was made again.
+bool kv_layer(larql_hip_ctx* c, size_t l, size_t num_kv, size_t head_dim) {
+    auto& kv = c->kv;
+    const size_t row = num_kv * head_dim;
+    auto make = [&](__half*& k, __half*& v) {
         if (hipMalloc(&k, kv.max_seq * row * sizeof(__half)) != hipSuccess ||
             hipMalloc(&v, kv.max_seq * row * sizeof(__half)) != hipSuccess) {
             if (k) (void)hipFree(k);
+            k = v = nullptr;
             fail(LARQL_HIP_ERR_NOMEM, "KV cache allocation failed");
         }
+    };
+    bool remade = false;
+    if (l < kv.num_layers && (kv.num_kv[l] != num_kv || kv.head_dim[l] != head_dim)) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(kv.k[l]);
+        (void)hipFree(kv.v[l]);
+        kv.k[l] = kv.v[l] = nullptr;
+        make(kv.k[l], kv.v[l]);
+        kv.num_kv[l] = num_kv;
+        kv.head_dim[l] = head_dim;
+        remade = true;
+    }
+    while (kv.num_layers <= l) {
+        __half *k = nullptr, *v = nullptr;
+        make(k, v);
         kv.k.push_back(k);
         kv.v.push_back(v);
+        kv.num_kv.push_back(num_kv);
+        kv.head_dim.push_back(head_dim);
         kv.num_layers++;
     }
+    return remade;
+}
+
+// populate_kv_layer: layer `layer` (and any missing below it) with this geometry.
+void kv_ensure_layer(larql_hip_ctx* c, size_t layer, size_t num_kv, size_t head_dim, size_t need) {
+    kv_reserve(c, need);
+    kv_layer(c, layer, num_kv, head_dim);
+}
+
+// A model's layers with their own geometries and room for `need` positions; when a held
+// layer's geometry differs (another model), its rows are gone and the cache restarts at
+// length 0.
+void kv_ensure_model(larql_hip_ctx* c, const larql_hip_model* m, size_t need) {
+    kv_reserve(c, need);
+    bool remade = false;
+    for (size_t l = 0; l < m->layers.size(); l++)
+        remade |= kv_layer(c, l, static_cast<size_t>(m->layers[l].nkv), static_cast<size_t>(m->layers[l].hd));
+    if (remade) c->kv.current_len = 0;
 }
 
 // Formats whose kernels take a Q8 activation (quantize_to_q8 of the f32 input): Q8_0, and
@@ -452,6 +489,7 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, const float* x0, int T
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
         const float* hin = l == 0 ? x0 : m->h0;
+        const size_t qd = static_cast<size_t>(L.nq) * L.hd, kvd = static_cast<size_t>(L.nkv) * L.hd;
         // Q/K/V: f32-input formats with the input norm fused into the matvec; Q8_0 from the
         // quantized normed input (one quantization shared by the three)
         bool have_q8 = false;
@@ -478,12 +516,12 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, const float* x0, int T
         };
         if (L.split_qkv) {  // three launches into the [q | k | v] buffer
             qkv_proj(L.wq, m->qkv);
-            qkv_proj(L.wk, m->qkv + m->q_dim);
-            qkv_proj(L.wv, m->qkv + m->q_dim + m->kv_dim);
+            qkv_proj(L.wk, m->qkv + qd);
+            qkv_proj(L.wv, m->qkv + qd + kvd);
         } else {
             qkv_proj(L.qkv, m->qkv);
         }
-        if (L.v_norm) larql::launch_vnorm_rows(m->qkv + m->q_dim + m->kv_dim, 1, 0, L.nkv, L.hd, L.eps, s);
+        if (L.v_norm) larql::launch_vnorm_rows(m->qkv + qd + kvd, 1, 0, L.nkv, L.hd, L.eps, s);
 
         larql::AttnArgs at{};
         at.qkv = m->qkv;
@@ -507,7 +545,7 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, const float* x0, int T
         const bool o_q8 = takes_q8(L.wo, false);
         if (L.post_norms || o_q8) {
             if (o_q8) {
-                quantize_input(m, m->attn, m->q_dim, nullptr, 0.f, L.eps, s);
+                quantize_input(m, m->attn, qd, nullptr, 0.f, L.eps, s);
                 int_proj(L.wo, m, m->otmp, s);
             } else {
                 larql::MvArgs o;
@@ -643,13 +681,12 @@ void enqueue_layers(larql_hip_ctx* c, larql_hip_model* m, const float* x0, int T
 void run_decode(larql_hip_ctx* c, larql_hip_model* m, const float* x_dev, float* hidden_out, float* logits,
                 hipStream_t s, const PromptAttn& pa = {}) {
     auto& kv = c->kv;
-    kv_ensure(c, m->layers.size(), m->nkv, m->hd, kv.current_len + 1);
+    kv_ensure_model(c, m, kv.current_len + 1);
     const int T = static_cast<int>(kv.current_len) + 1;
     // partials for any T up to the cache capacity: the buffer grows only with the cache, so
     // a step inside the capacity allocates nothing
     const int S_cap = larql::attn_splits(static_cast<int>(kv.max_seq), 0);
-    float* part = static_cast<float*>(
-        larql::ensure(c, m->part, larql::attn_part_floats(m->nq, S_cap, m->hd) * sizeof(float)));
+    float* part = static_cast<float*>(larql::ensure(c, m->part, m->part_per_split * S_cap * sizeof(float)));
     if (m->layers.empty()) larql::launch_copy_f32(x_dev, m->h0, m->hidden, s);
     else enqueue_layers(c, m, x_dev, T, part, s, pa);
     kv.current_len = static_cast<size_t>(T);
@@ -718,6 +755,13 @@ larql_hip_model* trait_model_for(larql_hip_ctx* c, const larql_pipeline_layer* l
     return m;
 }
 
+// q_dim / kv_dim of a trait call: the widest layer's, the width the reference sizes its
+// per-token buffers by (LC/src/metal/decode.rs:72-76); for uniform layers, every layer's.
+void check_dims(const larql_hip_model* m, size_t q_dim, size_t kv_dim, const char* what) {
+    if (m->q_dim != q_dim || m->kv_dim != kv_dim)
+        fail(LARQL_HIP_ERR_INVALID, std::string(what) + ": q_dim/kv_dim differ from the widest layer's");
+}
+
 }  // namespace
 
 extern "C" int larql_hip_decode_token(larql_hip_ctx* c, const larql_pipeline_layer* layers, size_t num_layers,
@@ -726,12 +770,11 @@ extern "C" int larql_hip_decode_token(larql_hip_ctx* c, const larql_pipeline_lay
                                       float* out) {
     return guarded(c, [&] {
         if (!layers || !x || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
-        if (num_q_heads * head_dim != q_dim || num_kv_heads * head_dim != kv_dim)
-            fail(LARQL_HIP_ERR_INVALID, "decode_token: q_dim/kv_dim do not match the head geometry");
-        (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
+        // per-layer rope_base and head geometry are authoritative (FullPipelineLayer.rope_base,
+        // head_dim, num_q_heads, num_kv_heads; LC/src/metal/decode.rs:101-110)
+        (void)rope_base, (void)num_q_heads, (void)num_kv_heads, (void)head_dim;
         larql_hip_model* m = trait_model_for(c, layers, num_layers, hidden, inter);
-        if (m->q_dim != q_dim || m->kv_dim != kv_dim)
-            fail(LARQL_HIP_ERR_INVALID, "decode_token: layer geometry differs from q_dim/kv_dim");
+        check_dims(m, q_dim, kv_dim, "decode_token");
         LARQL_HIP_CHECK(hipMemcpyAsync(m->xin, x, hidden * sizeof(float), hipMemcpyHostToDevice, c->stream));
         run_decode(c, m, m->xin, m->xin, nullptr, c->stream);
         download(c, out, m->xin, hidden * sizeof(float));
@@ -760,11 +803,11 @@ static void prompt_proj(const larql::DevWeight& w, const float* X, size_t ldx, f
 static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M, float* dout, hipStream_t s,
                        const PromptAttn& pa = {}) {
     auto& kv = c->kv;
-    kv_ensure(c, m->layers.size(), m->nkv, m->hd, M);
-    const size_t hidden = m->hidden, inter = m->inter, qd = m->q_dim, kvd = m->kv_dim, ld = qd + 2 * kvd;
-    const size_t wide = std::max({hidden, qd, inter}), gw = std::max(hidden, 2 * inter);
+    kv_ensure_model(c, m, M);
+    const size_t hidden = m->hidden, inter = m->inter, qmax = m->q_dim, ldmax = m->qkv_dim;
+    const size_t wide = std::max({hidden, qmax, inter}), gw = std::max(hidden, 2 * inter);
     const int S = larql::attn_prompt_splits(1, static_cast<int>(M), 0);
-    const size_t part_n = larql::attn_part_floats(m->nq, S, m->hd, static_cast<int>(M));
+    const size_t part_n = m->part_per_split * S * M;
     size_t split_n = 0;  // K-split partial products of the GEMMs
     auto need = [&](const larql::DevWeight& w) {
         split_n = std::max(split_n, larql::q4k_gemm_f32_part_floats(w, M));
@@ -774,13 +817,15 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
         else need(L.qkv);
         need(L.wo), need(L.gateup), need(L.down);
     }
-    const size_t n_f = 2 * M * hidden + M * wide + M * ld + M * qd + M * gw + M * inter + part_n + split_n;
+    const size_t n_f = 2 * M * hidden + M * wide + M * ldmax + M * qmax + M * gw + M * inter + part_n + split_n;
     float* base = static_cast<float*>(larql::ensure(c, m->prompt, n_f * sizeof(float)));
-    float *H0 = base, *H1 = H0 + M * hidden, *XN = H1 + M * hidden, *QKV = XN + M * wide, *ATT = QKV + M * ld;
-    float *G = ATT + M * qd, *ACT = G + M * gw, *PART = ACT + M * inter, *SPL = PART + part_n;
+    float *H0 = base, *H1 = H0 + M * hidden, *XN = H1 + M * hidden, *QKV = XN + M * wide, *ATT = QKV + M * ldmax;
+    float *G = ATT + M * qmax, *ACT = G + M * gw, *PART = ACT + M * inter, *SPL = PART + part_n;
     larql::launch_copy_f32(dx, H0, M * hidden, s);
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
+        // this layer's [q | k | v] rows, ld floats apart, and attention rows qd apart
+        const size_t qd = static_cast<size_t>(L.nq) * L.hd, kvd = static_cast<size_t>(L.nkv) * L.hd, ld = qd + 2 * kvd;
         larql::launch_rmsnorm_rows(H0, L.input_norm, L.norm_offset, XN, M, hidden, L.eps, s);
         if (L.split_qkv) {  // Q, K, V into their column ranges of the [q | k | v] rows
             prompt_proj(L.wq, XN, hidden, QKV, ld, M, SPL, split_n, s);
@@ -838,14 +883,13 @@ extern "C" int larql_hip_prefill_q4(larql_hip_ctx* c, const larql_pipeline_layer
                                     float rope_base, int use_qk_norm, float softcap, float* out) {
     return guarded(c, [&] {
         if (!layers || !x || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
-        if (num_q_heads * head_dim != q_dim || num_kv_heads * head_dim != kv_dim)
-            fail(LARQL_HIP_ERR_INVALID, "prefill: q_dim/kv_dim do not match the head geometry");
-        (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
+        // per-layer rope_base and head geometry are authoritative (FullPipelineLayer.rope_base,
+        // head_dim, num_q_heads, num_kv_heads; LC/src/metal/decode.rs:101-110)
+        (void)rope_base, (void)num_q_heads, (void)num_kv_heads, (void)head_dim;
         if (seq_len == 0) return;
         larql_hip_model* m = trait_model_for(c, layers, num_layers, hidden, inter);
-        if (m->q_dim != q_dim || m->kv_dim != kv_dim)
-            fail(LARQL_HIP_ERR_INVALID, "prefill: layer geometry differs from q_dim/kv_dim");
-        kv_ensure(c, m->layers.size(), m->nkv, m->hd, seq_len);
+        check_dims(m, q_dim, kv_dim, "prefill");
+        kv_ensure_model(c, m, seq_len);
         c->kv.current_len = 0;  // a new prompt at positions 0 .. seq_len - 1
         const float* dx = stage_upload(c, c->stage_in, x, seq_len * hidden);
         float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, seq_len * hidden * sizeof(float)));
@@ -865,13 +909,12 @@ extern "C" int larql_hip_full_pipeline_q4(larql_hip_ctx* c, const larql_pipeline
                                           float rope_base, int use_qk_norm, float softcap, float* out) {
     return guarded(c, [&] {
         if (!layers || !x || !out) fail(LARQL_HIP_ERR_INVALID, "null pointer");
-        if (num_q_heads * head_dim != q_dim || num_kv_heads * head_dim != kv_dim)
-            fail(LARQL_HIP_ERR_INVALID, "full pipeline: q_dim/kv_dim do not match the head geometry");
-        (void)rope_base;  // per-layer rope_base is authoritative (FullPipelineLayer.rope_base)
+        // per-layer rope_base and head geometry are authoritative (FullPipelineLayer.rope_base,
+        // head_dim, num_q_heads, num_kv_heads; LC/src/metal/decode.rs:101-110)
+        (void)rope_base, (void)num_q_heads, (void)num_kv_heads, (void)head_dim;
         if (seq_len == 0) return;
         larql_hip_model* m = trait_model_for(c, layers, num_layers, hidden, inter);
-        if (m->q_dim != q_dim || m->kv_dim != kv_dim)
-            fail(LARQL_HIP_ERR_INVALID, "full pipeline: layer geometry differs from q_dim/kv_dim");
+        check_dims(m, q_dim, kv_dim, "full pipeline");
         // positions 0 .. seq_len - 1 with causal attention over each other only: run against
         // the set-aside cache, then restore the decode cache whatever happens
         std::swap(c->kv, c->kv_aside);
@@ -879,7 +922,7 @@ extern "C" int larql_hip_full_pipeline_q4(larql_hip_ctx* c, const larql_pipeline
             larql_hip_ctx* c;
             ~Restore() { std::swap(c->kv, c->kv_aside); }
         } restore{c};
-        kv_ensure(c, m->layers.size(), m->nkv, m->hd, seq_len);
+        kv_ensure_model(c, m, seq_len);
         c->kv.current_len = 0;
         const float* dx = stage_upload(c, c->stage_in, x, seq_len * hidden);
         float* dout = static_cast<float*>(larql::ensure(c, c->stage_out, seq_len * hidden * sizeof(float)));
@@ -929,7 +972,7 @@ extern "C" int larql_hip_populate_kv_layer(larql_hip_ctx* c, size_t layer, const
     return guarded(c, [&] {
         if (!k_data || !v_data) fail(LARQL_HIP_ERR_INVALID, "null pointer");
         if (num_kv_heads == 0 || head_dim == 0) fail(LARQL_HIP_ERR_INVALID, "zero kv geometry");
-        kv_ensure(c, layer + 1, num_kv_heads, head_dim, seq_len);
+        kv_ensure_layer(c, layer, num_kv_heads, head_dim, seq_len);
         const size_t n = seq_len * num_kv_heads * head_dim;
         const float* dk = stage_upload(c, c->stage_in, k_data, n);
         larql::launch_f32_to_f16(dk, c->kv.k[layer], n, c->stream);
@@ -947,7 +990,7 @@ extern "C" int larql_hip_populate_kv_layer_f16_dev(larql_hip_ctx* c, size_t laye
     return guarded(c, [&] {
         if (!k_dev || !v_dev) fail(LARQL_HIP_ERR_INVALID, "null pointer");
         if (num_kv_heads == 0 || head_dim == 0) fail(LARQL_HIP_ERR_INVALID, "zero kv geometry");
-        kv_ensure(c, layer + 1, num_kv_heads, head_dim, seq_len);
+        kv_ensure_layer(c, layer, num_kv_heads, head_dim, seq_len);
         const size_t bytes = seq_len * num_kv_heads * head_dim * sizeof(__half);
         LARQL_HIP_CHECK(hipMemcpyAsync(c->kv.k[layer], k_dev, bytes, hipMemcpyDeviceToDevice, c->stream));
         larql::launch_v_to_cache(v_dev, false, c->kv.v[layer], seq_len, static_cast<int>(num_kv_heads),
@@ -1015,7 +1058,7 @@ extern "C" int larql_hip_model_prefill_dev(larql_hip_ctx* c, larql_hip_model* m,
         if (!m || !x_dev || !out_dev) fail(LARQL_HIP_ERR_INVALID, "null pointer");
         if (seq_len == 0) return;
         hipStream_t s = pick_stream(c, stream);
-        kv_ensure(c, m->layers.size(), m->nkv, m->hd, seq_len);
+        kv_ensure_model(c, m, seq_len);
         c->kv.current_len = 0;
         if (seq_len > 1 && prompt_batchable(m))
             run_prompt(c, m, x_dev, seq_len, out_dev, s);

@@ -14,6 +14,7 @@
 #include "matvec_common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 #include <vector>
 
@@ -266,10 +267,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         qv[u] = i < reps * HD ? a.qkv[static_cast<size_t>(kvh * reps) * HD + i] : 0.f;
     }
     const float2 csv = tid < half ? a.rope[static_cast<size_t>(pos) * half + tid] : make_float2(0.f, 0.f);
-    float krv = 0.f, vnv = 0.f;
-    if (fresh && tid < HD) {
-        krv = a.qkv[q_dim + static_cast<size_t>(kvh) * HD + tid];
-        vnv = a.qkv[q_dim + kv_dim + static_cast<size_t>(kvh) * HD + tid];
+    constexpr int KPT = (HD + kAttnThreads - 1) / kAttnThreads;  // new K/V elements per thread
+    float krv[KPT], vnv[KPT];
+#pragma unroll
+    for (int u = 0; u < KPT; u++) {
+        const int d = tid + u * kAttnThreads;
+        krv[u] = fresh && d < HD ? a.qkv[q_dim + static_cast<size_t>(kvh) * HD + d] : 0.f;
+        vnv[u] = fresh && d < HD ? a.qkv[q_dim + kv_dim + static_cast<size_t>(kvh) * HD + d] : 0.f;
     }
     const int tk = t0 + 16 * wave + c;
     v4u kA[KS];
@@ -296,10 +300,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         const int i = tid + u * kAttnThreads;
         if (i < reps * HD) qr_s[i] = qv[u];
     }
-    if (tid < half) cs_s[tid] = csv;
-    if (fresh && tid < HD) {
-        kr_s[tid] = krv;
-        vnew[tid] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vnv));
+    if (tid < half) cs_s[tid] = csv;  // half <= HD / 2 <= kAttnThreads
+#pragma unroll
+    for (int u = 0; u < KPT; u++) {
+        const int d = tid + u * kAttnThreads;
+        if (fresh && d < HD) {
+            kr_s[d] = krv[u];
+            vnew[d] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vnv[u]));
+        }
     }
     __syncthreads();
     for (int i = tid; i < reps * HD; i += kAttnThreads) {
@@ -446,7 +454,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a) 
     attn_merge_group<HD>(a.part, a.pst, sst, S, reps, blockIdx.x, a.out, lds);
 }
 
-bool attn_supported(int reps, int hd) { return reps >= 1 && reps <= 8 && hd % 32 == 0 && hd >= 32 && hd <= 256; }
+bool attn_supported(int reps, int hd) { return reps >= 1 && reps <= 8 && hd % 32 == 0 && hd >= 32 && hd <= 512; }
 
 int attn_partial_stride(int hd) { return hd + 2; }
 
@@ -529,6 +537,18 @@ int attn_prompt_splits(int T0, int batch, int window) {
     return S;
 }
 
+// f(std::integral_constant<int, hd>) for the instantiated head dims, the multiples of 32
+// from HD up to 512; false for any other hd.
+template <int HD, typename F>
+bool dispatch_head_dim(int hd, F&& f) {
+    if (hd == HD) {
+        f(std::integral_constant<int, HD>{});
+        return true;
+    }
+    if constexpr (HD < 512) return dispatch_head_dim<HD + 32>(hd, f);
+    return false;
+}
+
 void launch_attention(const AttnArgs& a0, hipStream_t s) {
     AttnArgs a = a0;
     const int reps = a.num_q / a.num_kv;
@@ -540,28 +560,11 @@ void launch_attention(const AttnArgs& a0, hipStream_t s) {
     const int nz = a.batch ? a.batch : 1;
     const size_t lds = merge_lds_bytes(reps, a.S);
     const dim3 grid(a.S, a.num_kv, nz), block(kAttnThreads);
-    switch (a.hd) {
-        case 32: attn_decode_kernel<32><<<grid, block, 0, s>>>(a); break;
-        case 64: attn_decode_kernel<64><<<grid, block, 0, s>>>(a); break;
-        case 96: attn_decode_kernel<96><<<grid, block, 0, s>>>(a); break;
-        case 128: attn_decode_kernel<128><<<grid, block, 0, s>>>(a); break;
-        case 160: attn_decode_kernel<160><<<grid, block, 0, s>>>(a); break;
-        case 192: attn_decode_kernel<192><<<grid, block, 0, s>>>(a); break;
-        case 224: attn_decode_kernel<224><<<grid, block, 0, s>>>(a); break;
-        default: attn_decode_kernel<256><<<grid, block, 0, s>>>(a); break;
-    }
+    if (!dispatch_head_dim<32>(a.hd, [&](auto h) { attn_decode_kernel<decltype(h)::value><<<grid, block, 0, s>>>(a); }))
+        fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: head_dim");
     LARQL_HIP_CHECK(hipGetLastError());
     const dim3 g2(a.num_kv, 1, nz);
-    switch (a.hd) {
-        case 32: attn_combine_kernel<32><<<g2, block, lds, s>>>(a); break;
-        case 64: attn_combine_kernel<64><<<g2, block, lds, s>>>(a); break;
-        case 96: attn_combine_kernel<96><<<g2, block, lds, s>>>(a); break;
-        case 128: attn_combine_kernel<128><<<g2, block, lds, s>>>(a); break;
-        case 160: attn_combine_kernel<160><<<g2, block, lds, s>>>(a); break;
-        case 192: attn_combine_kernel<192><<<g2, block, lds, s>>>(a); break;
-        case 224: attn_combine_kernel<224><<<g2, block, lds, s>>>(a); break;
-        default: attn_combine_kernel<256><<<g2, block, lds, s>>>(a); break;
-    }
+    dispatch_head_dim<32>(a.hd, [&](auto h) { attn_combine_kernel<decltype(h)::value><<<g2, block, lds, s>>>(a); });
     LARQL_HIP_CHECK(hipGetLastError());
 }
 

@@ -179,9 +179,10 @@ struct RopeTable {
 };
 
 struct KVCache {
-    size_t num_layers = 0, max_seq = 0, num_kv = 0, head_dim = 0;
+    size_t num_layers = 0, max_seq = 0;
     size_t current_len = 0;
     std::vector<__half*> k, v;   // per layer: K [max_seq][num_kv][head_dim], V [max_seq / 8][num_kv][head_dim][8]
+    std::vector<size_t> num_kv, head_dim;  // per layer (layers may differ, LC/src/metal/ops/kv_cache.rs:12-19)
     std::vector<RopeTable> rope;  // one per (rope_base, rdim) in use, cap >= max_seq
 };
 

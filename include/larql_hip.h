@@ -368,7 +368,12 @@ typedef struct {
  * through all layers with the KV cache (fp16 on the device, appended at the
  * current length, which then advances by one; attention is not limited in T).
  * x and out are host vectors of `hidden` floats (out = final hidden state,
- * before the final norm, as the reference returns it). */
+ * before the final norm, as the reference returns it).  Each layer's own head_dim,
+ * num_q_heads and num_kv_heads are used (layers may differ, as the reference's decode
+ * reads them per layer, LC/src/metal/decode.rs:101-110): head_dim a multiple of 32 up to
+ * 512, 1..8 query heads per kv head.  q_dim and kv_dim are the widest layer's (the
+ * reference's buffer widths); num_q_heads, num_kv_heads, head_dim and rope_base are
+ * unused, as in the reference. */
 int larql_hip_decode_token(larql_hip_ctx* ctx, const larql_pipeline_layer* layers, size_t num_layers,
                            const float* x, size_t hidden, size_t inter, size_t q_dim, size_t kv_dim,
                            size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float rope_base,
@@ -424,7 +429,9 @@ int larql_hip_multi_layer_q4_ffn(larql_hip_ctx* ctx, const larql_q4_ffn_layer* l
 
 /* ComputeBackend::populate_kv_layer — LC/src/backend.rs:103-107: K/V rows
  * [seq_len][num_kv_heads*head_dim] f32 (stored as fp16, RNE); sets the cache
- * length to seq_len. */
+ * length to seq_len.  The layer takes this geometry (layers below it not yet held
+ * take it too); a decode whose layer geometry differs from a held layer's drops the
+ * cache's rows. */
 int larql_hip_populate_kv_layer(larql_hip_ctx* ctx, size_t layer, const float* k_data, const float* v_data,
                                 size_t seq_len, size_t num_kv_heads, size_t head_dim);
 /* ComputeBackend::reset_kv_cache — LC/src/backend.rs:110 (drops the cache). */

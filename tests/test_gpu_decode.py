@@ -198,11 +198,76 @@ def test_decode_sliding_window(hip):
     run_sequence(hip, T0=20, n_tokens=2, n_layers=1, window=64)
 
 
-@pytest.mark.parametrize("nq,nkv,hd,T0", [(24, 8, 96, 70), (2, 2, 256, 130), (16, 2, 32, 65), (8, 1, 160, 9)])
+@pytest.mark.parametrize("nq,nkv,hd,T0", [(24, 8, 96, 70), (2, 2, 256, 130), (16, 2, 32, 65), (8, 1, 160, 9),
+                                          (4, 1, 512, 70), (8, 2, 384, 9), (4, 4, 448, 130)])
 def test_decode_head_geometries(hip, nq, nkv, hd, T0):
-    # hd a multiple of 32 up to 256, 1..8 query heads per kv head (q_dim a multiple of 256
-    # for the Q4_K output projection)
+    # hd a multiple of 32 up to 512 (beyond 256 the new K/V row takes two elements per
+    # thread), 1..8 query heads per kv head (q_dim a multiple of 256 for the Q4_K output
+    # projection)
     run_sequence(hip, T0=T0, n_tokens=2, n_layers=1, nq=nq, nkv=nkv, hd=hd, hidden=512, inter=512)
+
+
+# per-layer head geometry: a head_dim-512 layer with one kv head between 128- and 64-wide
+# ones (Gemma-4's global layers, LC/src/pipeline.rs:100-101)
+MIXED_GEOMS = [(8, 4, 128), (4, 1, 512), (8, 2, 64)]
+
+
+def _mixed_layers(hidden, inter, cap, seed, formats=None):
+    parts = [SmallModel(1, hidden, inter, nq, nkv, hd, cap=cap, seed=seed + 10 * i, formats=formats)
+             for i, (nq, nkv, hd) in enumerate(MIXED_GEOMS)]
+    return parts, [p.hip_layers(10000.0)[0] for p in parts]
+
+
+def _mixed_oracle(parts, x, pos, hidden, inter):
+    h = x.copy()
+    for (nq, nkv, hd), p in zip(MIXED_GEOMS, parts):
+        h = oracle.decode_layer(p.layers[0], h, pos, hidden, inter, nq, nkv, hd, 10000.0)
+    return h
+
+
+@pytest.mark.parametrize("formats", [None, {"wv": "q6_k", "down": "q6_k"}])
+def test_per_layer_head_geometry(hip, formats):
+    """Layers with their own head geometry (the reference decode reads it per layer,
+    LC/src/metal/decode.rs:101-110): caches populated at each layer's width, decode_token
+    steps, then prefill_q4 and full_pipeline_q4 of a prompt from position 0, every result
+    against the oracle's layers at their own geometry.  q_dim / kv_dim are the widest
+    layer's; any other width is an error."""
+    hidden, inter, T0, n_tok, seq = 512, 1024, 37, 3, 6
+    parts, layers = _mixed_layers(hidden, inter, cap=T0 + n_tok + seq + 2, seed=300, formats=formats)
+    qmax = max(nq * hd for nq, _, hd in MIXED_GEOMS)
+    kvmax = max(nkv * hd for _, nkv, hd in MIXED_GEOMS)
+    print(f"[per-layer geometry] {MIXED_GEOMS} formats={formats} q_dim={qmax} kv_dim={kvmax}", flush=True)
+    hip.reset_kv_cache()
+    for l, ((nq, nkv, hd), p) in enumerate(zip(MIXED_GEOMS, parts)):
+        kvd = nkv * hd
+        k, v = oracle.gauss(400 + l, T0 * kvd), oracle.gauss(410 + l, T0 * kvd)
+        hip.populate_kv_layer(l, k, v, T0, nkv, hd)
+        p.layers[0]["k_cache"][: T0 * kvd] = k.astype(np.float16).view(np.uint16)
+        p.layers[0]["v_cache"][: T0 * kvd] = v.astype(np.float16).view(np.uint16)
+    for i in range(n_tok):
+        x = oracle.gauss(500 + i, hidden)
+        got = hip.decode_token(layers, x, hidden, inter, qmax, kvmax, 8, 2, 64, 10000.0)
+        e = rel_err(got, _mixed_oracle(parts, x, T0 + i, hidden, inter))
+        print(f"  decode pos {T0 + i}: rel_err={e:.3e}", flush=True)
+        assert e <= REL_TOL, (i, e)
+    assert hip.kv_cache_len() == T0 + n_tok
+    be = larql_hip.HipBackend(0, strict=False)
+    try:
+        assert be.decode_token(layers, oracle.gauss(1, hidden), hidden, inter, qmax // 2, kvmax, 8, 2, 64,
+                               10000.0) is None
+        assert "widest layer" in be.last_error()
+    finally:
+        be.close()
+    xs = np.stack([oracle.gauss(600 + q, hidden) for q in range(seq)])
+    ref = [_mixed_oracle(parts, xs[q], q, hidden, inter) for q in range(seq)]
+    for entry in ("prefill", "full_pipeline"):
+        hip.reset_kv_cache()
+        fn = hip.prefill_q4 if entry == "prefill" else hip.full_pipeline_q4
+        got = fn(layers, xs, hidden, inter, qmax, kvmax, seq, 8, 2, 64, 10000.0)
+        e = max(rel_err(got[q], ref[q]) for q in range(seq))
+        print(f"  {entry} seq={seq}: worst rel_err={e:.3e}", flush=True)
+        assert e <= REL_TOL, (entry, e)
+    assert hip.kv_cache_len() == 0   # full_pipeline left the (reset) decode cache alone
 
 
 @pytest.mark.parametrize("formats", [{"wv": "q6_k", "down": "q6_k"}, {"wq": "q6_k", "up": "q6_k"},
