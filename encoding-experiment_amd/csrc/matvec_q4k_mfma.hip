@@ -375,23 +375,24 @@ struct Q4kSplit {
     int R;
 };
 
-// Measured on MI355X (256 CUs, 16 rotating weight copies, back-to-back launches): rows
-// of <= 16 super-blocks with 1.5 .. 6 tiles per CU take two super-blocks per wave and
-// two tiles per workgroup, the first two units' loads issued with x ([14336 x 4096]
-// 7.52 us, against 7.73 with four tiles per workgroup; [6144 x 4096] 4.76 us); the
-// others four super-blocks per wave, one tile per workgroup, x issued by every wave
-// before any weight load ([4096 x 4096] 3.9 us, [28672 x 4096] 12.1 us, [4096 x 14336]
-// 7.5 us, against 8.1 with the loads of one unit issued with x).  Rows longer than
-// 16 waves x 4 super-blocks (K > 16384) take several rounds.  The per-wave phases
-// explain the spread: a wave cannot build its x planes before its x loads return, and
-// those queue behind weight loads already in flight (planes ready 0.7 .. 5.8 us into a
-// 7.5 us launch).
+// Measured on MI355X (256 CUs, rotating weight copies, back-to-back launches): rows of
+// <= 16 super-blocks with 1.5 .. 8 tiles per CU take two super-blocks per wave and two
+// tiles per workgroup, the first two units' loads issued with x ([14336 x 4096] 7.2 us,
+// against 7.73 with four tiles per workgroup; [6144 x 4096] 4.76 us; [28672 x 4096], 7
+// tiles per CU: 12.30 us standalone against 12.15 with the split below, but in the 8B
+// decode step, where it is the fused gate|up, 1.5368 against 1.5394 ms per step, five
+// medians of 30 steps each way on one box, spread 0.001 ms); longer tile counts at <= 16 super-blocks take four super-blocks
+// per wave, one tile per workgroup and four units issued with x, and the rest ([4096 x
+// 4096] 3.9 us, [4096 x 14336] 7.5 us, against 8.1 with the loads of one unit issued
+// with x) four super-blocks per wave, one tile per workgroup, x issued by every wave
+// before any weight load.  Rows longer than 16 waves x 4 super-blocks (K > 16384) take
+// several rounds.  The per-wave phases explain the spread: a wave cannot build its x
+// planes before its x loads return, and those queue behind weight loads already in
+// flight (planes ready 0.7 .. 5.8 us into a 7.5 us launch).
 Q4kSplit pick_q4k_split(const DevWeight& w, int num_cus) {
     const size_t S = w.cols / 256;
     const size_t tiles = w.rows_pad / 16, cus = static_cast<size_t>(num_cus);
     const int R4 = static_cast<int>((S + 4 * kMaxKS - 1) / (4 * kMaxKS));
-    // (up to 8 tiles per CU: the decode step's fused gate|up [28672 x 4096], 7 per CU, runs
-    // 1.4775 against 1.4808 ms per step with <4, 1, 4>)
     if (S <= 16 && 2 * tiles >= 3 * cus && tiles < 8 * cus && w.rows_pad % 32 == 0) return {2, 2, 2, false, 1};
     if (S <= 16 && tiles >= 6 * cus) return {4, 1, 4, true, R4};
     return {4, 1, 2, true, R4};
