@@ -791,6 +791,34 @@ def pmc_pass(which: str, launches: int):
         torch.cuda.synchronize()
         be.close()
         return
+    if which == "walk":  # the Q4_0 walk-FFN kernels over [10240 x 2560]: vecmat, 6-position pair batch, matvec
+        N, K, copies = 10240, 2560, 8
+        gen = torch.Generator(device=dev)
+        hs = []
+        for i in range(copies):
+            gen.manual_seed(90 + i)
+            g = torch.randn(N, K, generator=gen, device=dev, dtype=torch.float32) * 0.02
+            raw = torch.empty(N * K // 32 * 18, dtype=torch.uint8, device=dev)
+            be.quantize_weights_dev(larql_hip.Q4_0, g, N * K, raw, stream=stream)
+            torch.cuda.synchronize()
+            hs.append(be.register_weight_device(larql_hip.Q4_0, raw, raw.numel(), N, K))
+            del g, raw
+        act = torch.randn(N, generator=gen, device=dev)
+        y = torch.empty(K, device=dev)
+        x6 = torch.randn(6, K, generator=gen, device=dev)
+        g6 = torch.empty(6 * N, device=dev)
+        u6 = torch.empty(6 * N, device=dev)
+        xq = torch.empty(K, dtype=torch.int8, device=dev)
+        xsc = torch.empty(K // 32, device=dev)
+        be.quantize_to_q8_dev(torch.randn(K, generator=gen, device=dev), K, 1, xq, xsc, stream=stream)
+        y2 = torch.empty(N, device=dev)
+        for i in range(launches):
+            be.vecmat_dev(hs[i % copies], act, y, stream=stream)
+            be.pair_batch_dev(hs[i % copies], hs[(i + 1) % copies], x6, 6, g6, u6, stream=stream)
+            be.matvec_dev(hs[i % copies], xq, y2, x_scales=xsc, stream=stream)
+        torch.cuda.synchronize()
+        be.close()
+        return
     handles, xs, outs, _ = make_weights(be, torch, stream, copies=16)
     fold = torch.empty(14336 // 16 + 4, device=dev, dtype=torch.int32)
     for i in range(launches):
@@ -856,7 +884,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=1.5, help="per CPU-baseline leg (14 legs)")
     ap.add_argument("--eager", action="store_true", help="time Python-loop launches instead of a HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--pmc-pass", choices=("calib", "gate", "floor", "knn"))
+    ap.add_argument("--pmc-pass", choices=("calib", "gate", "floor", "knn", "walk"))
     ap.add_argument("--pmc-launches", type=int, default=50)
     ap.add_argument("--pmc-report", nargs=4, metavar=("CALIB_FETCH", "CALIB_WRITE", "GATE_FETCH", "GATE_WRITE"))
     ap.add_argument("--pmc-floor", metavar="FLOOR_FETCH", help="with --pmc-report: FETCH_SIZE of the read-floor pass")

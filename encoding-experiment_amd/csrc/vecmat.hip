@@ -50,18 +50,33 @@ VmShape vecmat_shape(int nb) {
     return v;
 }
 
-// Grid (tiles, chunks), vecmat_shape threads.  part: [chunks][hidden].
+// Grid tiles x chunks (one dimension), vecmat_shape threads.  part: [chunks][hidden].
+// Workgroup i runs on XCD i % 8; with the chunk count a multiple of 8 every tile of a
+// chunk runs on one XCD (chunk x + 8 k on XCD x), so the rows' scale lines, which the
+// tiles of a row share (160 bytes per [.. x 2560] row), are fetched into one L2 instead
+// of up to eight.
 __global__ __launch_bounds__(kVmMaxThreads) void q4_vecmat_part_kernel(const uint4* __restrict__ qs,
                                                                        const uint16_t* __restrict__ dsc,
                                                                        const float* __restrict__ act,
                                                                        float* __restrict__ part, int inter, int hidden,
-                                                                       int rows_per_chunk, int tb, int groups) {
+                                                                       int rows_per_chunk, int tb, int groups,
+                                                                       int tiles, int nch) {
     extern __shared__ float red[];  // [groups][33 tb]: block b's 32 sums at 33 b
     const int t = threadIdx.x;
     const int nb = hidden >> 5;
     const int b = t % tb, g = t / tb;
-    const int blk = min(static_cast<int>(blockIdx.x) * tb + b, nb - 1);  // past the edge: a real block, unused
-    const int c0 = blockIdx.y * rows_per_chunk;
+    const int wg = static_cast<int>(blockIdx.x);
+    int tile, chunk;
+    if (nch % 8 == 0) {
+        const int x = wg & 7, slot = wg >> 3;
+        chunk = x + 8 * (slot / tiles);
+        tile = slot % tiles;
+    } else {
+        chunk = wg / tiles;
+        tile = wg % tiles;
+    }
+    const int blk = min(tile * tb + b, nb - 1);  // past the edge: a real block, unused
+    const int c0 = chunk * rows_per_chunk;
     const int c1 = min(inter, c0 + rows_per_chunk);
 
     if (g < groups) {
@@ -107,12 +122,12 @@ __global__ __launch_bounds__(kVmMaxThreads) void q4_vecmat_part_kernel(const uin
     }
     __syncthreads();
     // column c of the tile (block c / 32, element c % 32): its row groups' sums in order
-    const int ncol = min(32 * tb, hidden - static_cast<int>(blockIdx.x) * 32 * tb);
+    const int ncol = min(32 * tb, hidden - tile * 32 * tb);
     for (int c = t; c < ncol; c += blockDim.x) {
         const int li = 33 * (c >> 5) + (c & 31);
         float v = red[li];
         for (int r = 1; r < groups; r++) v = v + red[static_cast<size_t>(r) * 33 * tb + li];
-        part[static_cast<size_t>(blockIdx.y) * hidden + static_cast<size_t>(blockIdx.x) * 32 * tb + c] = v;
+        part[static_cast<size_t>(chunk) * hidden + static_cast<size_t>(tile) * 32 * tb + c] = v;
     }
 }
 
@@ -147,12 +162,13 @@ __global__ __launch_bounds__(256) void q4_vecmat_sum_kernel(const float* __restr
 
 }  // namespace
 
-// Chunks: two workgroups per CU, each at least one row per row group, the partials at
-// most 1/8 of the weight bytes.
+// Chunks: about two workgroups per CU, a multiple of 8 (one XCD per chunk), each at least
+// one row per row group, the partials at most 1/8 of the weight bytes.
 size_t q4_vecmat_chunks(size_t inter, size_t hidden) {
     const VmShape v = vecmat_shape(static_cast<int>(hidden / 32));
     const size_t tiles = (hidden / 32 + v.tb - 1) / v.tb;
-    const size_t want = std::max<size_t>(1, (static_cast<size_t>(current_device_cus()) * 2 + tiles - 1) / tiles);
+    const size_t want =
+        std::max<size_t>(1, ((static_cast<size_t>(current_device_cus()) * 2 + tiles - 1) / tiles + 7) / 8 * 8);
     const size_t cap = std::max<size_t>(1, inter * 18 / (32 * 4 * 8));  // partials <= weights / 8
     return std::max<size_t>(1, std::min({want, cap, inter / static_cast<size_t>(v.groups)}));
 }
@@ -165,11 +181,12 @@ void launch_q4_vecmat(const DevWeight& w, const float* act, float* out, float* p
     const VmShape v = vecmat_shape(hidden / 32);
     const int rows_per_chunk = static_cast<int>((w.rows + chunks - 1) / chunks);
     const int nch = (inter + rows_per_chunk - 1) / rows_per_chunk;
-    const dim3 g1(static_cast<unsigned>((hidden / 32 + v.tb - 1) / v.tb), static_cast<unsigned>(nch));
+    const int tiles = (hidden / 32 + v.tb - 1) / v.tb;
+    const dim3 g1(static_cast<unsigned>(tiles * nch));
     const size_t lds = static_cast<size_t>(v.groups) * 33 * v.tb * sizeof(float);
     q4_vecmat_part_kernel<<<g1, dim3(v.threads), lds, s>>>(reinterpret_cast<const uint4*>(w.qs),
                                                            static_cast<const uint16_t*>(w.d), act, part, inter, hidden,
-                                                           rows_per_chunk, v.tb, v.groups);
+                                                           rows_per_chunk, v.tb, v.groups, tiles, nch);
     LARQL_HIP_CHECK(hipGetLastError());
     q4_vecmat_sum_kernel<<<dim3(static_cast<unsigned>((hidden + kSumCols - 1) / kSumCols)), dim3(256), 0, s>>>(
         part, out, hidden, nch);
