@@ -775,7 +775,10 @@ template <int FMT, int M>
 void launch_int_mv(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s,
                    const DevWeight* w2, float* out2) {
     const size_t nmat = w2 ? 2 : 1;
-    if (nmat * (w.rows + 63) / 64 * 4 >= static_cast<size_t>(current_device_cus()) * 3) {
+    // Q4_0 always takes 16-lane groups: a step of 4 lanes reads 64 bytes of a row, half a
+    // cache line (the lm-head [128256 x 4096] 78.7 -> 52 us, the pair [10240 x 2560] x 2
+    // 8.9 -> 7.7 us with 16).  A Q8_0 block is 32 bytes, so 4 lanes read a whole line.
+    if (FMT != LARQL_Q4_0 && nmat * (w.rows + 63) / 64 * 4 >= static_cast<size_t>(current_device_cus()) * 3) {
         // one activation row: 32 rows per 128-thread workgroup (twice the workgroups; the x
         // image each stages is small).  Q8_0 [14336 x 4096]: 13.6 us against 14.6 with 64
         // rows per 256 threads; with 4 rows the doubled staging costs more (17.3 vs 15.1 us).
@@ -844,50 +847,82 @@ void launch_q4_0_matvec_pair(const DevWeight& w1, const DevWeight& w2, const int
 // The reference GPU's down projection of a Q4_0 FFN (q4_f32_matvec,
 // LC/src/metal/shaders/q4_f32_matvec.rs:10-38): per block, block_sum = sum over the 16
 // nibble bytes of (lo - 8) x[2j] + (hi - 8) x[2j+1], then acc += block_sum * f16(scale).
-// One wave per row; lane l takes blocks l, l + 64, ... (one 16-byte nibble load each, 1 KB
-// contiguous per wave instruction), x through the caches; the lanes' block sums are then
-// added in a tree, an order within f32 rounding of the reference's serial one.
+// Workgroup = kQfRows rows x the whole row: wave w covers blocks 64 w .. 64 w + 63, lane l
+// block 64 w + l of each of the rows, so the lane loads its 32 x values once for all
+// kQfRows rows (x crosses the caches once per workgroup, not once per row: 40 KB per
+// [.. x 10240] row otherwise).  The lanes' and then the waves' partial sums are added in a
+// tree, an order within f32 rounding of the reference's serial one.  [2560 x 10240]: 16.5
+// us with one row per wave; 10.3 / 11.8 / 10.4 / 13.2 us with 4 / 8 / 10 / 16 rows per
+// workgroup.
 namespace {
-__global__ __launch_bounds__(256) void q4_0_f32_mv_kernel(const uint8_t* __restrict__ qs,
-                                                          const uint16_t* __restrict__ d, const float* __restrict__ x,
-                                                          float* __restrict__ out, int rows, int nb) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;  // whole waves leave together: no barrier below
-    const uint4* q = reinterpret_cast<const uint4*>(qs + static_cast<size_t>(row) * nb * 16);
-    const uint16_t* dr = d + static_cast<size_t>(row) * nb;
-    float acc = 0.f;
-    for (int b = lane; b < nb; b += 64) {
-        const uint4 w = q[b];
-        const float4* xb = reinterpret_cast<const float4*>(x + 32 * b);
-        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+constexpr int kQfRows = 4;
+
+__global__ __launch_bounds__(1024) void q4_0_f32_mv_kernel(const uint8_t* __restrict__ qs,
+                                                           const uint16_t* __restrict__ d, const float* __restrict__ x,
+                                                           float* __restrict__ out, int rows, int nb) {
+    __shared__ float part[16][kQfRows];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int r0 = blockIdx.x * kQfRows;
+    const int b = 64 * wave + lane;
+    const bool on = b < nb;
+    const int bc = on ? b : nb - 1;  // past the row's end: a real block, contributing 0
+    float xs[32];
+    {
+        const float4* xb = reinterpret_cast<const float4*>(x + 32 * static_cast<size_t>(bc));
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 v = xb[k];
+            xs[4 * k] = v.x, xs[4 * k + 1] = v.y, xs[4 * k + 2] = v.z, xs[4 * k + 3] = v.w;
+        }
+    }
+    uint4 w[kQfRows];
+    uint32_t dv[kQfRows];
+#pragma unroll
+    for (int r = 0; r < kQfRows; r++) {
+        const size_t row = static_cast<size_t>(min(r0 + r, rows - 1));
+        w[r] = reinterpret_cast<const uint4*>(qs + row * nb * 16)[bc];
+        dv[r] = d[row * nb + bc];
+    }
+    float acc[kQfRows];
+#pragma unroll
+    for (int r = 0; r < kQfRows; r++) {
+        const uint32_t wd[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
         float bs = 0.f;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float4 xa = xb[2 * k], xc = xb[2 * k + 1];
-            const float xs[8] = {xa.x, xa.y, xa.z, xa.w, xc.x, xc.y, xc.z, xc.w};
+        for (int k = 0; k < 4; k++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const uint32_t byte = (wd[k] >> (8 * j)) & 0xFFu;
                 const float lo = static_cast<float>(static_cast<int>(byte & 15u) - 8);
                 const float hi = static_cast<float>(static_cast<int>(byte >> 4) - 8);
-                bs += lo * xs[2 * j] + hi * xs[2 * j + 1];
+                bs += lo * xs[8 * k + 2 * j] + hi * xs[8 * k + 2 * j + 1];
             }
-        }
-        acc += bs * h2f(dr[b]);
+        acc[r] = on ? bs * h2f(dv[r]) : 0.f;
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (lane == 0) out[row] = acc;
+    for (int r = 0; r < kQfRows; r++)
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) acc[r] += __shfl_xor(acc[r], off, 64);
+    if (lane == 0)
+#pragma unroll
+        for (int r = 0; r < kQfRows; r++) part[wave][r] = acc[r];
+    __syncthreads();
+    if (threadIdx.x < kQfRows && r0 + static_cast<int>(threadIdx.x) < rows) {
+        float v = part[0][threadIdx.x];
+        for (int i = 1; i < nw; i++) v += part[i][threadIdx.x];
+        out[r0 + threadIdx.x] = v;
+    }
 }
 }  // namespace
 
 void launch_q4_0_f32_matvec(const DevWeight& w, const float* x, float* out, hipStream_t s) {
     if (w.format != LARQL_Q4_0) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4_0 f32 matvec: Q4_0 weights only");
     if (w.rows == 0) return;
-    const dim3 grid(static_cast<unsigned>((w.rows + 3) / 4)), block(256);
+    const int nb = static_cast<int>(w.cols / 32);
+    if (nb > 16 * 64) fail(LARQL_HIP_ERR_UNSUPPORTED, "q4_0 f32 matvec: rows longer than 32768");
+    const dim3 grid(static_cast<unsigned>((w.rows + kQfRows - 1) / kQfRows)), block(64 * ((nb + 63) / 64));
     q4_0_f32_mv_kernel<<<grid, block, 0, s>>>(w.qs, static_cast<const uint16_t*>(w.d), x, out,
-                                             static_cast<int>(w.rows), static_cast<int>(w.cols / 32));
+                                             static_cast<int>(w.rows), nb);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
