@@ -883,21 +883,30 @@ __global__ __launch_bounds__(1024) void q4_0_f32_mv_kernel(const uint8_t* __rest
         w[r] = reinterpret_cast<const uint4*>(qs + row * nb * 16)[bc];
         dv[r] = d[row * nb + bc];
     }
+    // sum((nib - 8) x) as sum(nib x) - 8 sum(x): sum(x) once per block for all the rows,
+    // then one byte conversion and one fma per weight
+    float xsum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) xsum += xs[k];
     float acc[kQfRows];
 #pragma unroll
     for (int r = 0; r < kQfRows; r++) {
         const uint32_t wd[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
         float bs = 0.f;
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t byte = (wd[k] >> (8 * j)) & 0xFFu;
-                const float lo = static_cast<float>(static_cast<int>(byte & 15u) - 8);
-                const float hi = static_cast<float>(static_cast<int>(byte >> 4) - 8);
-                bs += lo * xs[8 * k + 2 * j] + hi * xs[8 * k + 2 * j + 1];
-            }
-        acc[r] = on ? bs * h2f(dv[r]) : 0.f;
+        for (int k = 0; k < 4; k++) {
+            uint32_t lo4 = wd[k] & 0x0F0F0F0Fu, hi4 = (wd[k] >> 4) & 0x0F0F0F0Fu;
+            asm volatile("" : "+v"(lo4), "+v"(hi4));  // byte conversions, not field extracts
+            bs = __builtin_fmaf(ubyte0(lo4), xs[8 * k + 0], bs);
+            bs = __builtin_fmaf(ubyte0(hi4), xs[8 * k + 1], bs);
+            bs = __builtin_fmaf(ubyte1(lo4), xs[8 * k + 2], bs);
+            bs = __builtin_fmaf(ubyte1(hi4), xs[8 * k + 3], bs);
+            bs = __builtin_fmaf(ubyte2(lo4), xs[8 * k + 4], bs);
+            bs = __builtin_fmaf(ubyte2(hi4), xs[8 * k + 5], bs);
+            bs = __builtin_fmaf(ubyte3(lo4), xs[8 * k + 6], bs);
+            bs = __builtin_fmaf(ubyte3(hi4), xs[8 * k + 7], bs);
+        }
+        acc[r] = on ? __builtin_fmaf(-8.0f, xsum, bs) * h2f(dv[r]) : 0.f;
     }
 #pragma unroll
     for (int r = 0; r < kQfRows; r++)

@@ -103,7 +103,10 @@ __global__ __launch_bounds__(kVmMaxThreads) void q4_vecmat_part_kernel(const uin
                 const uint32_t w4[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const uint32_t lo4 = w4[i] & 0x0F0F0F0Fu, hi4 = (w4[i] >> 4) & 0x0F0F0F0Fu;
+                    uint32_t lo4 = w4[i] & 0x0F0F0F0Fu, hi4 = (w4[i] >> 4) & 0x0F0F0F0Fu;
+                    // opaque to the compiler: with the masks known it extracts bytes 1-3 with a
+                    // v_bfe_u32 before each conversion instead of v_cvt_f32_ubyte1..3
+                    asm volatile("" : "+v"(lo4), "+v"(hi4));
                     acc[8 * i + 0] = __builtin_fmaf(ubyte0(lo4), scale, acc[8 * i + 0]);
                     acc[8 * i + 1] = __builtin_fmaf(ubyte0(hi4), scale, acc[8 * i + 1]);
                     acc[8 * i + 2] = __builtin_fmaf(ubyte1(lo4), scale, acc[8 * i + 2]);
