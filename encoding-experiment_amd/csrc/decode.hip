@@ -132,13 +132,14 @@ __device__ __forceinline__ void attn_select_query(AttnArgs& a) {
 }
 
 // o = sum_s e_s o_s / sum_s e_s l_s with e_s = exp(m_s - max_s m_s), in split order, for
-// nh consecutive query heads: partial entry (head h, split s) at base + (h sst + s) pst =
-// {o[HD], m, l}, outputs at out + h HD.  One workgroup; ml holds 2 nh S floats of LDS.
+// HD dims of nh consecutive query heads: partial entry (head h, split s) at
+// base + (h sst + s) pst = {o[HD], ...}, its (m, l) pair mlo floats further, outputs at
+// out + h HD.  One workgroup; ml holds 2 nh S floats of LDS.
 // The loads of every (m, l) pair and of the first PF splits of each thread's first output
 // pair are issued together, so for S <= PF (T <= 2176) the merge waits on memory once.
 template <int HD>
-__device__ __forceinline__ void attn_merge_heads(const float* __restrict__ base, int pst, int sst, int S, int nh,
-                                                 float* __restrict__ out, float* ml, float* inv_l) {
+__device__ __forceinline__ void attn_merge_heads(const float* __restrict__ base, int mlo, int pst, int sst, int S,
+                                                 int nh, float* __restrict__ out, float* ml, float* inv_l) {
     constexpr int H2 = HD / 2, PF = 34;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nout = nh * H2;  // float2 outputs
@@ -153,7 +154,7 @@ __device__ __forceinline__ void attn_merge_heads(const float* __restrict__ base,
     }
     for (int k = tid; k < nh * S; k += kAttnThreads) {
         const int h = k / S, s = k - h * S;
-        const float2 v = *reinterpret_cast<const float2*>(base + (static_cast<size_t>(h) * sst + s) * pst + HD);
+        const float2 v = *reinterpret_cast<const float2*>(base + (static_cast<size_t>(h) * sst + s) * pst + mlo);
         ml[2 * k] = v.x;
         ml[2 * k + 1] = v.y;
     }
@@ -205,25 +206,10 @@ __device__ __forceinline__ void attn_merge_heads(const float* __restrict__ base,
     }
 }
 
-// Query heads per merge pass: as many of the kv head's reps as fit kMergeLdsMax.
+// LDS of one head's merge: S (m, l) pairs and its reciprocal sum.
 constexpr int kMergeLdsMax = 48 * 1024;
-__host__ __device__ inline int merge_heads_per_pass(int reps, int S) {
-    const int fit = (kMergeLdsMax / 4 - 8) / (2 * S);
-    return fit < 1 ? 1 : (fit < reps ? fit : reps);
-}
-
-// The merge of kv head kvh's reps query heads, in passes of merge_heads_per_pass.
-template <int HD>
-__device__ __forceinline__ void attn_merge_group(const float* part, int pst, int sst, int S, int reps, int kvh,
-                                                 float* out, float* lds) {
-    const int hc = merge_heads_per_pass(reps, S);
-    for (int h0 = 0; h0 < reps; h0 += hc) {
-        if (h0) __syncthreads();  // the previous pass's LDS reads are done
-        const int nh = reps - h0 < hc ? reps - h0 : hc;
-        const size_t h = static_cast<size_t>(kvh) * reps + h0;
-        attn_merge_heads<HD>(part + h * sst * pst, pst, sst, S, nh, out + h * HD, lds, lds + 2 * nh * S);
-    }
-}
+constexpr int kMergeParts = 1;  // workgroups per query head, each merging HD / kMergeParts dims
+inline size_t merge_lds_bytes(int S) { return sizeof(float) * (2 * static_cast<size_t>(S) + 8); }
 
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
@@ -439,7 +425,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 }
 
 // Merge of the S softmax partials (a second launch: the kernel boundary makes every
-// partial visible), grid (num_kv, 1, batch): one workgroup per kv head and query.  A merge
+// partial visible), grid (num_q, 1, batch): one workgroup per query head and query (one
+// per kv head, merging its query heads in turn, was 1.5275 against 1.4915 ms per 8B decode
+// step: 8 workgroups each reading 4 heads' partials, against 32 reading one).  A merge
 // in the split launch itself (the kv head's last workgroup to finish merging, all of its
 // workgroups placed on one XCD and meeting in its L2 through an atomic arrival count) was
 // measured: 1.5405 against 1.5408 ms per 8B decode step, so the chain of memory round
@@ -450,18 +438,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a) 
     const int sst = a.S;  // partial stride per head
     attn_select_query(a);
     const int S = (a.T - (a.t_begin & ~7) + kAttnChunk - 1) / kAttnChunk;  // this query's splits
-    const int reps = a.num_q / a.num_kv;
-    attn_merge_group<HD>(a.part, a.pst, sst, S, reps, blockIdx.x, a.out, lds);
+    // query head h, dims [p DH, (p + 1) DH)
+    constexpr int DH = HD / kMergeParts;
+    const size_t h = blockIdx.x / kMergeParts;
+    const int d0 = (blockIdx.x % kMergeParts) * DH;
+    attn_merge_heads<DH>(a.part + h * sst * a.pst + d0, HD - d0, a.pst, sst, S, 1, a.out + h * HD + d0, lds,
+                         lds + 2 * S);
 }
 
 bool attn_supported(int reps, int hd) { return reps >= 1 && reps <= 8 && hd % 32 == 0 && hd >= 32 && hd <= 512; }
 
 int attn_partial_stride(int hd) { return hd + 2; }
-
-// The merge's LDS: 2 nh S (m, l) pairs and nh reciprocal sums per pass.
-static size_t merge_lds_bytes(int reps, int S) {
-    return sizeof(float) * (2 * static_cast<size_t>(merge_heads_per_pass(reps, S)) * S + 8);
-}
 
 __global__ void rope_table_kernel(float2* cs, size_t n, int half, int rdim, double base) {
     const size_t idx = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
@@ -558,12 +545,12 @@ void launch_attention(const AttnArgs& a0, hipStream_t s) {
     if (2 * static_cast<size_t>(a.S) * sizeof(float) + 32 > static_cast<size_t>(kMergeLdsMax))
         fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: too many position splits");
     const int nz = a.batch ? a.batch : 1;
-    const size_t lds = merge_lds_bytes(reps, a.S);
+    const size_t lds = merge_lds_bytes(a.S);
     const dim3 grid(a.S, a.num_kv, nz), block(kAttnThreads);
     if (!dispatch_head_dim<32>(a.hd, [&](auto h) { attn_decode_kernel<decltype(h)::value><<<grid, block, 0, s>>>(a); }))
         fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: head_dim");
     LARQL_HIP_CHECK(hipGetLastError());
-    const dim3 g2(a.num_kv, 1, nz);
+    const dim3 g2(a.num_q * kMergeParts, 1, nz);
     dispatch_head_dim<32>(a.hd, [&](auto h) { attn_combine_kernel<decltype(h)::value><<<g2, block, lds, s>>>(a); });
     LARQL_HIP_CHECK(hipGetLastError());
 }
