@@ -502,14 +502,14 @@ __global__ __launch_bounds__(64 * WAVES) void q8_mfma_kernel(const uint8_t* __re
 // k-group j, and B column c = weight row c, k-group g = half of block 4 q + g.  D lane
 // (g, c) then holds, in registers r = 0 .. 3, the exact int32 dots of blocks 4 q + r of
 // activation row g with weight row c: four consecutive blocks of one chain, added in order
-// in the lane (no cross-lane traffic).  Each lane loads its weight row's whole block
-// 4 q + g (16 bytes; the wave reads 64 contiguous bytes of each of its 16 rows) and its
-// four f16 scales.  The nibble codes become int8 code - 8 (bytes without borrows); the
-// activation bytes are staged in LDS in the order the nibbles unpack (even elements, then
-// odd, per 16).  Requires hidden % 128 == 0.  The weight loads are plain (cached): a wave
-// reads half of a 128-byte line of each row per quad and the next quad the other half,
-// which a nontemporal load fetched from HBM twice (pair batch [10240 x 2560] x 6: 15.4
-// against 19.6 us with the quantization launch).  W tiles per workgroup, chosen per shape
+// in the lane (no cross-lane traffic).  The weights are loaded two quads at a time (below)
+// so that each load instruction reads whole 128-byte lines; the nibble codes become int8
+// code - 8 (bytes without borrows); the activation bytes are staged in LDS in the order the
+// nibbles unpack (even elements, then odd, per 16).  Requires hidden % 128 == 0.  The
+// weight loads are plain (cached): with one quad per load a wave read half of a 128-byte
+// line of each row and the next quad the other half, which a nontemporal load fetched
+// from HBM twice (pair batch [10240 x 2560] x 6: 15.4 against 19.6 us with the
+// quantization launch).  W tiles per workgroup, chosen per shape
 // so the busiest CU holds the fewest tiles (640 + 640 tiles on 256 CUs: five per
 // workgroup, one workgroup per CU; with four, 64 CUs hold two).
 constexpr int kQ40MfmaD = 4;  // quads of weights in flight per wave (2, 4, 6, 8 tried: 4 is fastest)
