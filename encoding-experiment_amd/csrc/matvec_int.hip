@@ -503,22 +503,34 @@ __global__ __launch_bounds__(64 * WAVES) void q8_mfma_kernel(const uint8_t* __re
 // (g, c) then holds, in registers r = 0 .. 3, the exact int32 dots of blocks 4 q + r of
 // activation row g with weight row c: four consecutive blocks of one chain, added in order
 // in the lane (no cross-lane traffic).  The weights are loaded two quads at a time (below)
-// so that each load instruction reads whole 128-byte lines; the nibble codes become int8
-// code - 8 (bytes without borrows); the activation bytes are staged in LDS in the order the
-// nibbles unpack (even elements, then odd, per 16).  Requires hidden % 128 == 0.  The
+// so that each load instruction reads whole 128-byte lines.  The B operands are the raw
+// nibble codes 0 .. 15 (one mask per byte group); the -8 offset enters as the first
+// MFMA's accumulator input, -8 sum(x) of the block for each activation row, staged with
+// the x image, so D is still exactly sum((code - 8) x).  The activation bytes are staged
+// in LDS in the order the nibbles unpack (even elements, then odd, per 16).  Requires
+// hidden % 128 == 0.  The
 // weight loads are plain (cached): with one quad per load a wave read half of a 128-byte
 // line of each row and the next quad the other half, which a nontemporal load fetched
 // from HBM twice (pair batch [10240 x 2560] x 6: 15.4 against 19.6 us with the
 // quantization launch).  W tiles per workgroup, chosen per shape
 // so the busiest CU holds the fewest tiles (640 + 640 tiles on 256 CUs: five per
 // workgroup, one workgroup per CU; with four, 64 CUs hold two).
-constexpr int kQ40MfmaD = 4;  // quads of weights in flight per wave (2, 4, 6, 8 tried: 4 is fastest)
+constexpr int kQ40MfmaD = 4;  // quads of weights in flight per wave (2, 4, 6, 8 tried: 4 is fastest; 6 equal)
+
+// zero chunks after the x image: the A operand reads of lanes outside their k-group land
+// there (offsets up to one activation-row group + one half: 32 + 1 chunks past the base)
+constexpr int kQ40Zero = 34;
 
 constexpr size_t q40_mfma_lds_bytes(int nb) {
-    return (static_cast<size_t>(nb / 4) * 64 + 1) * 16 + static_cast<size_t>(nb / 4) * 32 * 4;
+    return (static_cast<size_t>(nb / 4) * 64 + kQ40Zero) * 16 + static_cast<size_t>(nb / 4) * 32 * 4 * 2;
 }
 
-__device__ __forceinline__ uint32_t nib_minus8(uint32_t v) { return ((v | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+// keep in the lanes outside BANKS, the DPP row_ror:8 partner's `from` in those inside
+template <int BANKS>
+__device__ __forceinline__ uint32_t swap_half(uint32_t keep, uint32_t from) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(keep), static_cast<int>(from), 0x128, 0xF, BANKS, false));
+}
 
 template <int TG, int W>
 __global__ __launch_bounds__(64 * W) void q4_0_mfma_kernel(const uint8_t* __restrict__ qs,
@@ -538,8 +550,9 @@ __global__ __launch_bounds__(64 * W) void q4_0_mfma_kernel(const uint8_t* __rest
     }
     const int nq = nb >> 2;
     const int nchunk = nq * 64;
-    uint4* xl = lds4;                                          // [nq][8 t][4 j][2 h], then a zero chunk
-    float* xsl = reinterpret_cast<float*>(lds4 + nchunk + 1);  // [nq][8 t][4 j]
+    uint4* xl = lds4;  // [nq][8 t][4 j][2 h], then kQ40Zero zero chunks
+    float* xsl = reinterpret_cast<float*>(lds4 + nchunk + kQ40Zero);  // [nq][8 t][4 j]
+    int* xcl = reinterpret_cast<int*>(xsl + nq * 32);          // [nq][8 t][4 j]: -8 sum of the codes
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
     const int rbase = (wg * W + wave) * 16;  // < rows_pad: the grid covers rows_pad / 16 tiles exactly
@@ -561,6 +574,15 @@ __global__ __launch_bounds__(64 * W) void q4_0_mfma_kernel(const uint8_t* __rest
     };
     auto xstage = [&](int bj, const uint4(&v)[XV]) __attribute__((always_inline)) {
         const bool live = ((bj >> 2) & 7) < m;
+        int cs = 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            cs = __builtin_amdgcn_sdot4(static_cast<int>(v[h].x), 0x01010101, cs, false);
+            cs = __builtin_amdgcn_sdot4(static_cast<int>(v[h].y), 0x01010101, cs, false);
+            cs = __builtin_amdgcn_sdot4(static_cast<int>(v[h].z), 0x01010101, cs, false);
+            cs = __builtin_amdgcn_sdot4(static_cast<int>(v[h].w), 0x01010101, cs, false);
+        }
+        xcl[bj] = live ? -8 * cs : 0;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint4 r = v[h];
@@ -579,22 +601,39 @@ __global__ __launch_bounds__(64 * W) void q4_0_mfma_kernel(const uint8_t* __rest
     // quad 2 p + (c >> 3) of rows c & 7 (wa) and 8 + (c & 7) (wb), so each load instruction
     // reads 128 contiguous bytes of each of 8 rows (whole cache lines when the row length is
     // a multiple of 128 bytes); one DPP rotation by 8 lanes then gives every lane both quads
-    // of its own row c.  Block scales: row c's four of each quad.
+    // of its own row c.  Block scales: row c's four of each quad.  Both through buffer
+    // descriptors over the padded matrix (rows_pad = the tiles of the grid x 16): the pair
+    // index is a uniform offset, and a load past the matrix's end (a prefetch past the last
+    // pair of the last row) reads 0; past a row's end it reads the next row's bytes, never
+    // used.
     constexpr int DP = D / 2;  // pairs of quads in flight
     const int np = (nq + 1) >> 1, qh = c >> 3;
-    const uint8_t* wa_row = qs + static_cast<size_t>(rbase + (c & 7)) * nb * 16 + g * 16;
-    const uint8_t* wb_row = wa_row + static_cast<size_t>(8) * nb * 16;
-    const uint2* srow = reinterpret_cast<const uint2*>(dsc + static_cast<size_t>(rbase + c) * nb);
+    const uint32_t rows_pad = static_cast<uint32_t>(second.nwg1 > 0 ? second.nwg1 : gridDim.x) * W * 16;
+    const uint32_t rowb = static_cast<uint32_t>(nb) * 16;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(qs), 0,
+                                                                        static_cast<int>(rows_pad * rowb), kBufDword3);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(dsc), 0, static_cast<int>(rows_pad * static_cast<uint32_t>(nb) * 2), kBufDword3);
+    const uint32_t wa_off = static_cast<uint32_t>(rbase + (c & 7)) * rowb + g * 16 + qh * 64;
+    const uint32_t wb_off = wa_off + 8 * rowb;
+    const uint32_t s_off = static_cast<uint32_t>(rbase + c) * static_cast<uint32_t>(nb) * 2;
     uint4 wa[DP], wb[DP];
     uint2 sa[DP], sb[DP];
+    // The three loads of a pair are issued in one fixed order everywhere (scheduling
+    // barriers around each): the wait counts at the loop head merge the order of the loads
+    // before the loop with that of the loop body, and with the prologue's loads interleaved
+    // the compiler waited for the next pair's data while the current pair was computed.
     auto refill = [&](int u, int p) __attribute__((always_inline)) {
-        // past the end (an odd quad count's last pair, or a pair beyond it): the last quad
-        // again, never used
-        const size_t qo = static_cast<size_t>(min(2 * p + qh, nq - 1)) * 64;
-        wa[u] = *reinterpret_cast<const uint4*>(wa_row + qo);
-        wb[u] = *reinterpret_cast<const uint4*>(wb_row + qo);
-        sa[u] = srow[min(2 * p, nq - 1)];
-        sb[u] = srow[min(2 * p + 1, nq - 1)];
+        const int po = p * 128;
+        __builtin_amdgcn_sched_barrier(0);
+        wa[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, wa_off, po, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        wb[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, wb_off, po, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        const uint4 s4 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rd, s_off, p * 16, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        sa[u] = make_uint2(s4.x, s4.y);
+        sb[u] = make_uint2(s4.z, s4.w);
     };
 #pragma unroll
     for (int u = 0; u < DP; u++) refill(u, u);
@@ -607,31 +646,34 @@ __global__ __launch_bounds__(64 * W) void q4_0_mfma_kernel(const uint8_t* __rest
         xload(bj, v);
         xstage(bj, v);
     }
-    if (threadIdx.x == 0) xl[nchunk] = make_uint4(0u, 0u, 0u, 0u);
+    if (static_cast<int>(threadIdx.x) < kQ40Zero) xl[nchunk + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
 
-    // A operand of this lane for group tg, half h: row c = 4 t + j live in k-group j only
+    // A operand of this lane for group tg, half h: row c = 4 t + j live in k-group j only.
+    // A live lane reads chunk ((q 8 + t) 4 + g) 2 + h, i.e. its base + 64 q + 32 tg + h; the
+    // others read the zero chunks (stride 0), so one multiply-add per quad gives the address.
     const bool a_on = (c & 3) == g;
-    auto a_of = [&](int q, int tg, int h) __attribute__((always_inline)) {
-        const int t = 4 * tg + (c >> 2);
-        const uint4 v = xl[a_on ? ((q * 8 + t) * 4 + g) * 2 + h : nchunk];
+    const uint32_t a_base = a_on ? static_cast<uint32_t>(((c >> 2) * 4 + g) * 2) * 16u : static_cast<uint32_t>(nchunk) * 16u;
+    const uint32_t a_step = a_on ? 1024u : 0u;
+    auto a_of = [&](uint32_t qa, int tg, int h) __attribute__((always_inline)) {
+        const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(xl) + qa + tg * 512 + h * 16);
         return v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
     };
     float acc[TG];
 #pragma unroll
     for (int tg = 0; tg < TG; tg++) acc[tg] = 0.0f;
     auto quad = [&](int q, const uint4& w, const uint2& s2) __attribute__((always_inline)) {
-        const v4i b0 = {static_cast<int>(nib_minus8(w.x & 0x0F0F0F0Fu)), static_cast<int>(nib_minus8(w.y & 0x0F0F0F0Fu)),
-                        static_cast<int>(nib_minus8((w.x >> 4) & 0x0F0F0F0Fu)),
-                        static_cast<int>(nib_minus8((w.y >> 4) & 0x0F0F0F0Fu))};
-        const v4i b1 = {static_cast<int>(nib_minus8(w.z & 0x0F0F0F0Fu)), static_cast<int>(nib_minus8(w.w & 0x0F0F0F0Fu)),
-                        static_cast<int>(nib_minus8((w.z >> 4) & 0x0F0F0F0Fu)),
-                        static_cast<int>(nib_minus8((w.w >> 4) & 0x0F0F0F0Fu))};
+        const v4i b0 = {static_cast<int>(w.x & 0x0F0F0F0Fu), static_cast<int>(w.y & 0x0F0F0F0Fu),
+                        static_cast<int>((w.x >> 4) & 0x0F0F0F0Fu), static_cast<int>((w.y >> 4) & 0x0F0F0F0Fu)};
+        const v4i b1 = {static_cast<int>(w.z & 0x0F0F0F0Fu), static_cast<int>(w.w & 0x0F0F0F0Fu),
+                        static_cast<int>((w.z >> 4) & 0x0F0F0F0Fu), static_cast<int>((w.w >> 4) & 0x0F0F0F0Fu)};
         const float wsc[4] = {h2f(s2.x), h2f(s2.x >> 16), h2f(s2.y), h2f(s2.y >> 16)};
+        const uint32_t qa = a_base + static_cast<uint32_t>(q) * a_step;
 #pragma unroll
         for (int tg = 0; tg < TG; tg++) {
-            v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_of(q, tg, 0), b0, v4i{0, 0, 0, 0}, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_of(q, tg, 1), b1, d, 0, 0, 0);
+            const int4 c4 = *reinterpret_cast<const int4*>(xcl + (q * 8 + 4 * tg + g) * 4);
+            v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_of(qa, tg, 0), b0, v4i{c4.x, c4.y, c4.z, c4.w}, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_of(qa, tg, 1), b1, d, 0, 0, 0);
             const float4 xs4 = *reinterpret_cast<const float4*>(xsl + (q * 8 + 4 * tg + g) * 4);
             const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
 #pragma unroll
@@ -644,16 +686,17 @@ __global__ __launch_bounds__(64 * W) void q4_0_mfma_kernel(const uint8_t* __rest
     };
     // lane c < 8 holds (row c, quad 2 p) in wa and passes wb (row c + 8, quad 2 p) to lane
     // c + 8; lane c >= 8 holds (row c, quad 2 p + 1) in wb and passes wa (row c - 8,
-    // quad 2 p + 1) to lane c - 8.  DPP row_ror:8 swaps the two halves of each 16-lane row.
+    // quad 2 p + 1) to lane c - 8.  DPP row_ror:8 swaps the two halves of each 16-lane row;
+    // its bank mask writes only the receiving half (lanes 0-7: banks 0-1, lanes 8-15: banks
+    // 2-3), the other half keeping the old value, its own quad.
     auto pair = [&](int p, int u) __attribute__((always_inline)) {
-        const uint4 give = qh ? wa[u] : wb[u];
-        uint4 got;
-        got.x = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(give.x), 0x128, 0xF, 0xF, false));
-        got.y = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(give.y), 0x128, 0xF, 0xF, false));
-        got.z = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(give.z), 0x128, 0xF, 0xF, false));
-        got.w = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(give.w), 0x128, 0xF, 0xF, false));
-        quad(2 * p, qh ? got : wa[u], sa[u]);
-        if (2 * p + 1 < nq) quad(2 * p + 1, qh ? wb[u] : got, sb[u]);
+        const uint4 a = wa[u], b = wb[u];
+        const uint4 x0 = {swap_half<0xC>(a.x, b.x), swap_half<0xC>(a.y, b.y), swap_half<0xC>(a.z, b.z),
+                          swap_half<0xC>(a.w, b.w)};
+        const uint4 x1 = {swap_half<0x3>(b.x, a.x), swap_half<0x3>(b.y, a.y), swap_half<0x3>(b.z, a.z),
+                          swap_half<0x3>(b.w, a.w)};
+        quad(2 * p, x0, sa[u]);
+        if (2 * p + 1 < nq) quad(2 * p + 1, x1, sb[u]);
     };
     int p0 = 0;
     for (; p0 + DP <= np; p0 += DP) {
@@ -708,7 +751,9 @@ void launch_q4_0_mfma_w(const DevWeight& w, const int8_t* q8x, const float* q8s,
 bool launch_q4_0_mfma(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out, int m, hipStream_t s,
                       const DevWeight* w2, float* out2) {
     const int nb = static_cast<int>(w.cols / 32);
-    if (m < 2 || m > 8 || nb % 4 != 0 || q40_mfma_lds_bytes(nb) > 64 * 1024 || w.rows_pad % 64 != 0) return false;
+    if (m < 2 || m > 8 || nb % 4 != 0 || q40_mfma_lds_bytes(nb) > 64 * 1024 || w.rows_pad % 64 != 0 ||
+        w.rows_pad * w.cols / 2 > 0x7FFFFFFF)  // buffer descriptors: byte offsets below 2^31
+        return false;
     // tiles per workgroup: of those that divide the tile count (so every wave owns a tile
     // in the allocation), the one whose busiest CU holds the fewest tiles; ties to the
     // larger workgroup (fewer x images staged)
