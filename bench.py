@@ -30,6 +30,8 @@ PMC helpers (used to produce profiles/q4k_matvec_traffic.json):
   bench.py --pmc-pass gate    gate-shape Q4_K matvec launches
   bench.py --pmc-pass floor   the plain-read floor kernel over the same gate weights
   bench.py --pmc-pass knn     the Q4_0 gate-KNN walk (34 layers [10240x2560], 256 queries)
+  bench.py --pmc-pass walk    the Q4_0 walk-FFN kernels over [10240x2560]
+  bench.py --pmc-pass prefill [--pmc-tokens M]  the Q4_K GEMM over [10240x2560] at M tokens
   bench.py --pmc-report CALIB_FETCH CALIB_WRITE GATE_FETCH GATE_WRITE [--pmc-floor FLOOR_FETCH]
 """
 from __future__ import annotations
@@ -753,7 +755,7 @@ def bench_configs(be, torch, stream, copies: int):
     return out
 
 
-def pmc_pass(which: str, launches: int):
+def pmc_pass(which: str, launches: int, tokens: int = 512):
     """Kernels only, for a rocprofv3 --pmc run (no timing output)."""
     import torch
 
@@ -788,6 +790,25 @@ def pmc_pass(which: str, launches: int):
         dv = torch.empty(L * Q * k, device=dev)
         for _ in range(max(1, launches // 10)):
             be.gate_knn_dev(hq, q, Q, k, di, dv, stream=stream)
+        torch.cuda.synchronize()
+        be.close()
+        return
+    if which == "prefill":  # the Q4_K GEMM (pack + MFMA) over [10240 x 2560] at `tokens` rows, 8 weight copies
+        N, K, copies = 10240, 2560, 8
+        gen = torch.Generator(device=dev)
+        hs = []
+        for i in range(copies):
+            gen.manual_seed(50 + i)
+            g = torch.randn(N, K, generator=gen, device=dev, dtype=torch.float32) * 0.02
+            raw = torch.empty(N * K // 256 * 148, dtype=torch.uint8, device=dev)
+            be.quantize_weights_dev(larql_hip.Q4_K, g, N * K, raw, stream=stream)
+            torch.cuda.synchronize()
+            hs.append(be.register_weight_device(larql_hip.Q4_K, raw, raw.numel(), N, K))
+            del g, raw
+        x = torch.randn(tokens, K, generator=gen, device=dev)
+        y = torch.empty(tokens * N, device=dev)
+        for i in range(launches):
+            be.matvec_dev(hs[i % copies], x, y, m=tokens, stream=stream)
         torch.cuda.synchronize()
         be.close()
         return
@@ -884,7 +905,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=1.5, help="per CPU-baseline leg (14 legs)")
     ap.add_argument("--eager", action="store_true", help="time Python-loop launches instead of a HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--pmc-pass", choices=("calib", "gate", "floor", "knn", "walk"))
+    ap.add_argument("--pmc-pass", choices=("calib", "gate", "floor", "knn", "walk", "prefill"))
+    ap.add_argument("--pmc-tokens", type=int, default=512, help="tokens of the prefill PMC pass")
     ap.add_argument("--pmc-launches", type=int, default=50)
     ap.add_argument("--pmc-report", nargs=4, metavar=("CALIB_FETCH", "CALIB_WRITE", "GATE_FETCH", "GATE_WRITE"))
     ap.add_argument("--pmc-floor", metavar="FLOOR_FETCH", help="with --pmc-report: FETCH_SIZE of the read-floor pass")
@@ -900,7 +922,7 @@ def main():
                                    "(one GPU's share is the full single-GPU shape)", "n_gpus": args.gpus}))
         sys.exit(2)
     if args.pmc_pass:
-        pmc_pass(args.pmc_pass, args.pmc_launches)
+        pmc_pass(args.pmc_pass, args.pmc_launches, args.pmc_tokens)
         return
 
     import torch
