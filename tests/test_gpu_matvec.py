@@ -181,12 +181,16 @@ def test_q8_matvec_ragged_bit_exact(hip, m, rows, cols):
 
 
 @pytest.mark.parametrize("m,rows,cols", [(3, 1000, 2560), (2, 17, 64), (11, 1000, 2560), (9, 300, 4096),
-                                         (5, 64, 4096), (8, 33, 160)])
+                                         (5, 64, 4096), (8, 33, 160), (2, 200, 384), (6, 100, 1152),
+                                         (7, 4100, 2688), (4, 1, 512), (3, 70, 8192)])
 def test_q4_0_matvec_batched_dev_bit_exact(hip, m, rows, cols):
     """Q4_0 x Q8 over several activation rows through the device entry point: each row
     equals the single-row block-integer order.  Passes of up to 8 rows (11 rows: 8 + 3;
-    9 rows: 8 + 1), a partial workgroup of rows (17), hidden 64 .. 4096, and an odd block
-    count (8, 33, 160)."""
+    9 rows: 8 + 1), a partial workgroup of rows (17), hidden 64 .. 8192, an odd block
+    count (8, 33, 160), and on the matrix-core kernel (hidden a multiple of 128) odd
+    counts of four-block quads (3, 9, 21: the last pair of quads half past the row), a
+    single row and a padded row count; hidden 8192 has an x image too large for its LDS
+    and takes the lane-group kernel."""
     torch = pytest.importorskip("torch")
     print(f"[q4_0 batched] m={m} rows={rows} cols={cols}", flush=True)
     q = weights("q4_0", rows, cols, seed=520 + rows)

@@ -147,9 +147,11 @@ def test_vecmat_dev_graph_replays_and_shape_changes(hip):
 
 # (6, 10240, 2560), (17, 300, 576), (130, 200, 128): several positions (one launch per pass of
 # up to 8, ragged row tiles); (1, 64, 32): one position; (9, 300, 544): hidden not a multiple
-# of 64; (9, 640, 256): the matrix-core kernel, passes of 8 and 1 rows
+# of 64; (9, 640, 256): the matrix-core kernel, passes of 8 and 1 rows; (5, 1000, 1152),
+# (3, 130, 384): the matrix-core kernel with an odd count of four-block quads (9, 3) over
+# both matrices of one launch
 @pytest.mark.parametrize("seq,rows,hidden", [(6, 10240, 2560), (17, 300, 576), (130, 200, 128), (1, 64, 32),
-                                             (9, 300, 544), (9, 640, 256)])
+                                             (9, 300, 544), (9, 640, 256), (5, 1000, 1152), (3, 130, 384)])
 def test_pair_batch_bit_exact(hip, seq, rows, hidden):
     print(f"[pair batch] seq={seq} rows={rows} hidden={hidden}", flush=True)
     gate = oracle.quantize_q4_0(oracle.gauss(41 + seq, rows * hidden, 0.0, 0.02))
