@@ -497,7 +497,7 @@ extern "C" int larql_hip_matvec_dev(larql_hip_ctx* c, uint64_t handle, const voi
                                              nullptr, s);
                 break;
             case LARQL_Q6_K:
-                if (m > 1) {  // the prompt pass's f32-operand GEMM; K-split partials in the workspace
+                if (m > 1) {  // the prompt pass's f32-accuracy GEMM; row exponents and K-split partials in the workspace
                     const size_t pf = larql::q4k_gemm_f32_part_floats(w, m);
                     float* part = pf ? static_cast<float*>(larql::ensure(c, c->gemm_x16, pf * sizeof(float))) : nullptr;
                     larql::launch_q4k_gemm_f32(w, static_cast<const float*>(x), out, m, part, pf, s, 0);

@@ -793,7 +793,7 @@ static bool prompt_batchable(const larql_hip_model* m) {
 }
 
 // One projection of all M positions (X rows ldx = w.cols apart) -> Y rows ldy apart: the
-// f32-operand GEMM, Q4_K or Q6_K.
+// f32-accuracy GEMM, Q4_K or Q6_K.
 static void prompt_proj(const larql::DevWeight& w, const float* X, size_t ldx, float* Y, size_t ldy, size_t M,
                         float* spl, size_t split_n, hipStream_t s) {
     if (ldx != w.cols) fail(LARQL_HIP_ERR_INVALID, "prompt pass: input rows do not match the weight");
@@ -808,7 +808,7 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
     const size_t wide = std::max({hidden, qmax, inter}), gw = std::max(hidden, 2 * inter);
     const int S = larql::attn_prompt_splits(1, static_cast<int>(M), 0);
     const size_t part_n = m->part_per_split * S * M;
-    size_t split_n = 0;  // K-split partial products of the GEMMs
+    size_t split_n = 0;  // GEMM workspace: row exponents and K-split partial products
     auto need = [&](const larql::DevWeight& w) {
         split_n = std::max(split_n, larql::q4k_gemm_f32_part_floats(w, M));
     };

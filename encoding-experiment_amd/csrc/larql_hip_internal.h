@@ -258,10 +258,11 @@ void launch_f32_matmul(const float* A, const float* B, float* C, size_t m, size_
 // MFMA operands.
 size_t q4k_gemm_ws_bytes(size_t m, size_t cols);
 void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, void* ws, hipStream_t s);
-// The same product with f32 operands (v_mfma_f32_16x16x4f32): ~1e-6 instead of ~1e-4, for
-// chains of projections (the batched prompt pass).  Small grids split K over up to four
-// workgroups per tile, summed in split order from `part` (floats: q4k_gemm_f32_part_floats;
-// with less, no split).
+// The same product from f32 X at f32 accuracy (fp16 operand pairs, three products each,
+// X rows scaled into range by per-token powers of two): ~1e-6 instead of ~1e-4, for
+// chains of projections (the batched prompt pass).  `part` is the workspace (floats:
+// q4k_gemm_f32_part_floats): the m row exponents, and the partial products when small
+// grids split K over up to four workgroups per tile (summed in split order).
 size_t q4k_gemm_f32_part_floats(const DevWeight& w, size_t m);
 // Q4_K or Q6_K weights.  Y rows are ldy floats apart (0: w.rows), so a projection can
 // fill a column slice.

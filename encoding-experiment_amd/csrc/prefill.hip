@@ -29,7 +29,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-// Tiling of the f32-operand GEMMs (q4k_gemm_f32_kernel, q6k_gemm_f32_kernel); the packed
+// Tiling of the f32-accuracy GEMMs (q4k_gemm_hp_kernel, q6k_gemm_hp_kernel); the packed
 // X of the fp16 GEMM is padded to kMt tiles of 16 tokens.
 constexpr int kMt = 4;                 // 16-token tiles per workgroup (64 tokens)
 constexpr int kNT = 5;                 // 16-row weight tiles per wave (80 rows)
@@ -284,21 +284,113 @@ __global__ __launch_bounds__(kShThreads) void q4k_gemm_shared_kernel(const uint8
         }
 }
 
-// ── f32 operands: the accurate variant for chains of projections ────────
-// 64 tokens x 320 weight rows per workgroup, 80 rows per wave (each wave dequantizes its
-// own rows for the workgroup's tokens), with v_mfma_f32_16x16x4f32: weights dequantized to f32 (`fma(q, d sc_j, -dmin m_j)`, one
-// rounding) and X read in f32, so each product is exact and the error is the f32
-// accumulation's (~1e-6) instead of the fp16 operands' (~1e-4 per projection), which
-// compounds through a model's layers.  A k-step of 4 takes element e of the lane's
-// sub-block 4h + g for lane group g, so a lane's 16 nibble bytes feed 32 steps and its A
-// operands are the matching 32 consecutive elements of its token's row of X.
-constexpr int kF32Pitch = 36;  // floats per lane slot in LDS (32 + 4: spread the banks)
+// ── f32 inputs to f32 accuracy: fp16 operand pairs on the matrix cores ────
+// The accurate variant for chains of projections (the batched prompt pass; Q6_K with
+// m > 1).  64 tokens x 320 weight rows per workgroup, 80 rows per wave (each wave
+// dequantizes its own rows for the workgroup's tokens), two-unit ring of X staged in LDS.
+// Every f32 operand v is split into two fp16 parts, hi = fp16(v) and lo = fp16(v - hi)
+// (v - hi exact in f32), so v = hi + lo to ~2^-22, and each product runs as three
+// v_mfma_f32_16x16x32_f16 with f32 accumulation: x_hi w_hi + x_hi w_lo + x_lo w_hi (the
+// dropped x_lo w_lo is ~2^-22 of it).  Through 16 and 32 layers this is as close to the
+// oracle as exact f32 products on v_mfma_f32_16x16x4f32 were, at 2.4x the speed; single
+// fp16 operands (2^-11) compounded past the bar, and bf16 pairs (hi = 8 bits, 2^-16 per
+// product) doubled the error.  fp16's range is made safe per token: row_exp_kernel gives
+// each X row the power of two that puts its largest |x| in [2^14, 2^15), the staging
+// scales the row by it and the epilogue divides it out, both exact; weights are used
+// unscaled (|w| must stay below 65504: a Q4_K super-block scale d below ~69, far above
+// real weights).  The weights are dequantized as before, w = fma(q, d sc_j, -dmin m_j) in
+// f32, then split.  A k-step of 32 takes elements 8 s .. 8 s + 7 of the lane's sub-block
+// 4 h + g for lane group g, in the order the nibbles unpack (0, 2, 4, 6, 1, 3, 5, 7), and
+// the X staging writes its fp16 pairs in that order.  An infinite operand gives NaN (its lo
+// part is inf - inf).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-__global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* __restrict__ qs,
-                                                                const v4u* __restrict__ hdr,
-                                                                const float* __restrict__ X, float* __restrict__ Y,
-                                                                int M, int N, int K, int ntiles, int sb_per, int ldy) {
-    __shared__ float As[2][kMt][64][kF32Pitch];
+// {a, b} -> hi pair {fp16(a), fp16(b)} and lo pair {fp16(a - hi_a), fp16(b - hi_b)}
+__device__ __forceinline__ void hp_split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+    const f16x2 h = __builtin_convertvector((f32x2){a, b}, f16x2);
+    hi = __builtin_bit_cast(uint32_t, h);
+    const float la = a - static_cast<float>(h.x), lb = b - static_cast<float>(h.y);
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){la, lb}, f16x2));
+}
+
+// Eight f32 values in the k-step order -> the step's hi and lo operands.
+__device__ __forceinline__ void hp_split8(const float (&v)[8], v4u& hi, v4u& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) hp_split2(v[2 * i], v[2 * i + 1], h[i], l[i]);
+    hi = v4u{h[0], h[1], h[2], h[3]};
+    lo = v4u{l[0], l[1], l[2], l[3]};
+}
+
+constexpr int kHpPitch = 36;  // dwords per lane slot in LDS: 16 hi + 16 lo + 4 (spread the banks)
+
+// X staging: the thread's 32 elements (8 float4) times its token's power of two -> hi
+// dwords 0..15 and lo dwords 16..31 of its LDS slot, step s at dwords 4 s .. 4 s + 3 in
+// the order (0, 2), (4, 6), (1, 3), (5, 7) of elements 8 s + ...
+__device__ __forceinline__ void hp_store_x(uint32_t* d, const float4 (&v)[8], float scale) {
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const float4 a = v[2 * s], b = v[2 * s + 1];
+        const float e[8] = {a.x * scale, a.z * scale, b.x * scale, b.z * scale,
+                            a.y * scale, a.w * scale, b.y * scale, b.w * scale};
+        v4u hi, lo;
+        hp_split8(e, hi, lo);
+        *reinterpret_cast<v4u*>(d + 4 * s) = hi;
+        *reinterpret_cast<v4u*>(d + 16 + 4 * s) = lo;
+    }
+}
+
+// acc[i] += A_i . B for the three operand-pair products of one k-step
+template <int MT>
+__device__ __forceinline__ void hp3_mfma(floatx4 (&acc)[MT], const v4u (&ah)[MT], const v4u (&al)[MT], const v4u& bh,
+                                         const v4u& bl) {
+    const half8 Bh = __builtin_bit_cast(half8, bh), Bl = __builtin_bit_cast(half8, bl);
+#pragma unroll
+    for (int i = 0; i < MT; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ah[i]), Bh, acc[i], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MT; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ah[i]), Bl, acc[i], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MT; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, al[i]), Bh, acc[i], 0, 0, 0);
+}
+
+// e[row] = the power of two that puts max |X[row]| in [2^14, 2^15) (0 for a row of zeros
+// or a non-finite maximum).  One workgroup per row; K a multiple of 4.
+__global__ __launch_bounds__(256) void row_exp_kernel(const float* __restrict__ X, int K, int* __restrict__ e) {
+    __shared__ float wm[4];
+    const float* row = X + static_cast<size_t>(blockIdx.x) * K;
+    float m = 0.f;
+    for (int i = 4 * static_cast<int>(threadIdx.x); i < K; i += 4 * 256) {
+        const float4 v = *reinterpret_cast<const float4*>(row + i);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+        e[blockIdx.x] = (m > 0.f && m <= 3.4e38f) ? min(120, max(-120, 14 - ilogbf(m))) : 0;
+    }
+}
+
+// The staging thread's token scale and the workgroup's per-token inverses (the first 64
+// threads), from the row exponents.
+__device__ __forceinline__ float hp_token_scales(const int* __restrict__ xe, int M, int mt0, int xr_row, float* inv) {
+    if (threadIdx.x < 16 * kMt) {
+        const int t = mt0 * 16 + static_cast<int>(threadIdx.x);
+        inv[threadIdx.x] = t < M ? ldexpf(1.0f, -xe[t]) : 1.0f;
+    }
+    return ldexpf(1.0f, xe[min(xr_row, M - 1)]);
+}
+
+__global__ __launch_bounds__(kThreads) void q4k_gemm_hp_kernel(const uint8_t* __restrict__ qs,
+                                                               const v4u* __restrict__ hdr,
+                                                               const float* __restrict__ X, const int* __restrict__ xe,
+                                                               float* __restrict__ Y, int M, int N, int K, int ntiles,
+                                                               int sb_per, int ldy) {
+    __shared__ uint32_t As[2][kMt][64][kHpPitch];
+    __shared__ float tok_inv[16 * kMt];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int S = K / 256;
@@ -320,6 +412,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
     const int xr_row = (mt0 + (tid >> 6)) * 16 + (lane & 15);
     const bool xr_ok = xr_row < M;  // (the select also keeps the compiler from a stack copy of Xu)
     const float* xrow = X + static_cast<size_t>(min(xr_row, M - 1)) * K + 32 * g;
+    const float xscale = hp_token_scales(xe, M, mt0, xr_row, tok_inv);
     struct Xu {
         float4 v[8];
     };
@@ -329,9 +422,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
         for (int k = 0; k < 8; k++) x.v[k] = xr_ok ? p[k] : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     auto store_x = [&](int b, const Xu& x) __attribute__((always_inline)) {
-        float4* d = reinterpret_cast<float4*>(&As[b][tid >> 6][lane][0]);
-#pragma unroll
-        for (int k = 0; k < 8; k++) d[k] = x.v[k];
+        hp_store_x(&As[b][tid >> 6][lane][0], x.v, xscale);
     };
     struct Wu {
         v4u q[kNT], hd[kNT];
@@ -345,11 +436,11 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
             w.hd[j] = *reinterpret_cast<const v4u*>(hdrb + ho[j] + static_cast<uint32_t>(u >> 1) * 256u);
         }
     };
-    floatx4 acc[kMt][kNT];
+    floatx4 acc[kNT][kMt];
 #pragma unroll
-    for (int i = 0; i < kMt; i++)
+    for (int j = 0; j < kNT; j++)
 #pragma unroll
-        for (int j = 0; j < kNT; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < kMt; i++) acc[j][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     auto compute = [&](int b, int u, const Wu& w) __attribute__((always_inline)) {
         const int h = u & 1;
@@ -362,28 +453,26 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
             nmn[j] = -(dmin * static_cast<float>((w.hd[j].w >> (8 * g + 4 * h)) & 0xFu));
         }
 #pragma unroll
-        for (int e4 = 0; e4 < 8; e4++) {  // elements 4 e4 .. 4 e4 + 3 of the lane's sub-block
-            float4 a[kMt];
+        for (int s = 0; s < 4; s++) {  // elements 8 s .. 8 s + 7 of the lane's sub-block
+            v4u ah[kMt], al[kMt];
 #pragma unroll
-            for (int i = 0; i < kMt; i++) a[i] = *reinterpret_cast<const float4*>(&As[b][i][lane][4 * e4]);
+            for (int i = 0; i < kMt; i++) {
+                ah[i] = *reinterpret_cast<const v4u*>(&As[b][i][lane][4 * s]);
+                al[i] = *reinterpret_cast<const v4u*>(&As[b][i][lane][16 + 4 * s]);
+            }
 #pragma unroll
             for (int j = 0; j < kNT; j++) {
-                // byte i of the 16 holds element 2i (low nibble) and 2i + 1 (high): split into
-                // low and high nibble bytes once per dword, then one byte convert per weight
-                const uint32_t word = w.q[j][e4 >> 1];
+                // bytes 4 s .. 4 s + 3: elements 8 s + 2 i (low nibble), 8 s + 2 i + 1 (high)
+                const uint32_t word = w.q[j][s];
                 uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
                 asm("" : "+v"(lo), "+v"(hi));  // opaque: keeps v_cvt_f32_ubyteN, not bfe + convert
-                const int b0 = 16 * (e4 & 1);
-                float wt[4];
-                wt[0] = __builtin_fmaf(static_cast<float>((lo >> b0) & 0xFFu), sc[j], nmn[j]);
-                wt[1] = __builtin_fmaf(static_cast<float>((hi >> b0) & 0xFFu), sc[j], nmn[j]);
-                wt[2] = __builtin_fmaf(static_cast<float>((lo >> (b0 + 8)) & 0xFFu), sc[j], nmn[j]);
-                wt[3] = __builtin_fmaf(static_cast<float>((hi >> (b0 + 8)) & 0xFFu), sc[j], nmn[j]);
-#pragma unroll
-                for (int t = 0; t < 4; t++)
-#pragma unroll
-                    for (int i = 0; i < kMt; i++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][t], wt[t], acc[i][j], 0, 0, 0);
+                const float wt[8] = {__builtin_fmaf(ubyte0(lo), sc[j], nmn[j]), __builtin_fmaf(ubyte1(lo), sc[j], nmn[j]),
+                                     __builtin_fmaf(ubyte2(lo), sc[j], nmn[j]), __builtin_fmaf(ubyte3(lo), sc[j], nmn[j]),
+                                     __builtin_fmaf(ubyte0(hi), sc[j], nmn[j]), __builtin_fmaf(ubyte1(hi), sc[j], nmn[j]),
+                                     __builtin_fmaf(ubyte2(hi), sc[j], nmn[j]), __builtin_fmaf(ubyte3(hi), sc[j], nmn[j])};
+                v4u bh, bl;
+                hp_split8(wt, bh, bl);
+                hp3_mfma<kMt>(acc[j], ah, al, bh, bl);
             }
         }
     };
@@ -410,6 +499,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
         load_w(min(u + 3, last), w1);
         __syncthreads();
     }
+    // D lane (g, c) holds tokens 4g .. 4g + 3 of weight row c of each 16 x 16 tile
 #pragma unroll
     for (int i = 0; i < kMt; i++)
 #pragma unroll
@@ -418,7 +508,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = (mt0 + i) * 16 + 4 * g + r;
-                if (m < M && col < N) Y[static_cast<size_t>(m) * ldy + col] = acc[i][j][r];
+                if (m < M && col < N) Y[static_cast<size_t>(m) * ldy + col] = acc[j][i][r] * tok_inv[i * 16 + 4 * g + r];
             }
         }
 }
@@ -426,13 +516,15 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_f32_kernel(const uint8_t* _
 // Q6_K weights (tile-major blocks, q6k_block in larql_hip_internal.h: ql nibble of element
 // e at byte e / 2, its two high bits regrouped per 16-element group G: element 16 G + 8 w +
 // 2 j + p at bits 8 j + 4 w + 2 p of word G; int8 scale per group; f16 d per block) with
-// the f32 kernel's X staging and tiling: lane (g, c) of unit (sb, h) takes elements
+// the same X staging and tiling: lane (g, c) of unit (sb, h) takes elements
 // 32 (4h + g) .. + 31 of row c of each tile, i.e. 16 ql bytes, two high-bit words and two
 // scales; w = fma(q, d sc, -32 d sc) = d sc (q - 32).
-__global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* __restrict__ q6,
-                                                                const float* __restrict__ X, float* __restrict__ Y,
-                                                                int M, int N, int K, int sb_per, int ldy) {
-    __shared__ float As[2][kMt][64][kF32Pitch];
+__global__ __launch_bounds__(kThreads) void q6k_gemm_hp_kernel(const uint8_t* __restrict__ q6,
+                                                               const float* __restrict__ X, const int* __restrict__ xe,
+                                                               float* __restrict__ Y, int M, int N, int K, int sb_per,
+                                                               int ldy) {
+    __shared__ uint32_t As[2][kMt][64][kHpPitch];
+    __shared__ float tok_inv[16 * kMt];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int S = K / 256;
@@ -453,6 +545,7 @@ __global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* _
     const int xr_row = (mt0 + (tid >> 6)) * 16 + (lane & 15);
     const bool xr_ok = xr_row < M;
     const float* xrow = X + static_cast<size_t>(min(xr_row, M - 1)) * K + 32 * g;
+    const float xscale = hp_token_scales(xe, M, mt0, xr_row, tok_inv);
     struct Xu {
         float4 v[8];
     };
@@ -462,9 +555,7 @@ __global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* _
         for (int k = 0; k < 8; k++) x.v[k] = xr_ok ? p[k] : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     auto store_x = [&](int b, const Xu& x) __attribute__((always_inline)) {
-        float4* d = reinterpret_cast<float4*>(&As[b][tid >> 6][lane][0]);
-#pragma unroll
-        for (int k = 0; k < 8; k++) d[k] = x.v[k];
+        hp_store_x(&As[b][tid >> 6][lane][0], x.v, xscale);
     };
     struct Wu {
         v4u l[kNT];
@@ -483,12 +574,21 @@ __global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* _
                       (static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(b + kQ6D + 2 * rc[j])) << 16);
         }
     };
-    floatx4 acc[kMt][kNT];
+    floatx4 acc[kNT][kMt];
 #pragma unroll
-    for (int i = 0; i < kMt; i++)
+    for (int j = 0; j < kNT; j++)
 #pragma unroll
-        for (int j = 0; j < kNT; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < kMt; i++) acc[j][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    // element e (0 .. 31) of the lane's part: the 6-bit code from its ql nibble and two
+    // regrouped high bits, d sc (q - 32) as one fma
+    auto q6w = [](const Wu& w, int j, int e, float sc, float nb) __attribute__((always_inline)) {
+        const int e4 = e >> 2, t = e & 3;
+        const uint32_t lo = w.l[j][e4 >> 1], hi = (e4 >> 2) ? w.h[j].y : w.h[j].x;
+        const uint32_t q4 = (lo >> (16 * (e4 & 1) + 4 * t)) & 0xFu;
+        const uint32_t q2 = (hi >> (16 * (e4 & 1) + 8 * (t >> 1) + 4 * ((e4 >> 1) & 1) + 2 * (t & 1))) & 3u;
+        return __builtin_fmaf(static_cast<float>(q4 | (q2 << 4)), sc, nb);
+    };
     auto compute = [&](int b, const Wu& w) __attribute__((always_inline)) {
         float ds[kNT][2];
 #pragma unroll
@@ -498,27 +598,23 @@ __global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* _
             ds[j][1] = d * static_cast<float>(static_cast<int8_t>((w.sd[j] >> 8) & 0xFFu));
         }
 #pragma unroll
-        for (int e4 = 0; e4 < 8; e4++) {  // elements 4 e4 .. 4 e4 + 3 of the lane's 32
-            float4 a[kMt];
+        for (int s = 0; s < 4; s++) {
+            v4u ah[kMt], al[kMt];
 #pragma unroll
-            for (int i = 0; i < kMt; i++) a[i] = *reinterpret_cast<const float4*>(&As[b][i][lane][4 * e4]);
+            for (int i = 0; i < kMt; i++) {
+                ah[i] = *reinterpret_cast<const v4u*>(&As[b][i][lane][4 * s]);
+                al[i] = *reinterpret_cast<const v4u*>(&As[b][i][lane][16 + 4 * s]);
+            }
 #pragma unroll
             for (int j = 0; j < kNT; j++) {
-                const float sc = ds[j][e4 >> 2], nb = -32.f * sc;
-                const uint32_t lo = w.l[j][e4 >> 1], hi = (e4 >> 2) ? w.h[j].y : w.h[j].x;
-                float wt[4];
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const uint32_t q4 = (lo >> (16 * (e4 & 1) + 4 * t)) & 0xFu;
-                    const uint32_t q2 =
-                        (hi >> (16 * (e4 & 1) + 8 * (t >> 1) + 4 * ((e4 >> 1) & 1) + 2 * (t & 1))) & 3u;
-                    wt[t] = __builtin_fmaf(static_cast<float>(q4 | (q2 << 4)), sc, nb);
-                }
-#pragma unroll
-                for (int t = 0; t < 4; t++)
-#pragma unroll
-                    for (int i = 0; i < kMt; i++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][t], wt[t], acc[i][j], 0, 0, 0);
+                const float sc = ds[j][s >> 1], nb = -32.f * sc;
+                const int e0 = 8 * s;
+                const float wt[8] = {q6w(w, j, e0 + 0, sc, nb), q6w(w, j, e0 + 2, sc, nb), q6w(w, j, e0 + 4, sc, nb),
+                                     q6w(w, j, e0 + 6, sc, nb), q6w(w, j, e0 + 1, sc, nb), q6w(w, j, e0 + 3, sc, nb),
+                                     q6w(w, j, e0 + 5, sc, nb), q6w(w, j, e0 + 7, sc, nb)};
+                v4u bh, bl;
+                hp_split8(wt, bh, bl);
+                hp3_mfma<kMt>(acc[j], ah, al, bh, bl);
             }
         }
     };
@@ -551,7 +647,7 @@ __global__ __launch_bounds__(kThreads) void q6k_gemm_f32_kernel(const uint8_t* _
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = (mt0 + i) * 16 + 4 * g + r;
-                if (m < M && col < N) Y[static_cast<size_t>(m) * ldy + col] = acc[i][j][r];
+                if (m < M && col < N) Y[static_cast<size_t>(m) * ldy + col] = acc[j][i][r] * tok_inv[i * 16 + 4 * g + r];
             }
         }
 }
@@ -566,7 +662,7 @@ __global__ void sum_splits_kernel(const float* __restrict__ P, float* __restrict
     Y[(i / N) * ldy + i % N] = a;
 }
 
-// K-splits for the f32 GEMM: the count (1..4, whole super-blocks each) that minimises
+// K-splits for the f32-accuracy GEMM: the count (1..4, whole super-blocks each) that minimises
 // rounds of workgroups over the CUs x units per workgroup (one workgroup per CU at a time).
 struct F32Split {
     int splits, sb_per;
@@ -587,9 +683,10 @@ F32Split f32_split(const DevWeight& w, size_t m) {
 
 }  // namespace
 
+// workspace: the K-split partials (when split), then the m row exponents (ints)
 size_t q4k_gemm_f32_part_floats(const DevWeight& w, size_t m) {
     const F32Split sp = f32_split(w, m);
-    return sp.splits > 1 ? sp.splits * m * w.rows : 0;
+    return (sp.splits > 1 ? sp.splits * m * w.rows : 0) + m;
 }
 
 void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, float* part, size_t part_floats,
@@ -600,18 +697,22 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
         fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: Q4_K or Q6_K weights only");
     if (m == 0) return;
     if (m > 0x7FFFFFFF / w.cols) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: too many tokens");
+    if (!part || part_floats < m) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: no workspace for the row exponents");
     F32Split sp = f32_split(w, m);
-    if (sp.splits > 1 && (!part || part_floats < sp.splits * m * w.rows)) sp = {1, static_cast<int>(w.cols / 256)};
+    if (sp.splits > 1 && part_floats < sp.splits * m * w.rows + m) sp = {1, static_cast<int>(w.cols / 256)};
+    int* xe = reinterpret_cast<int*>(part + (sp.splits > 1 ? sp.splits * m * w.rows : 0));
+    row_exp_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, static_cast<int>(w.cols), xe);
+    LARQL_HIP_CHECK(hipGetLastError());
     const dim3 grid(static_cast<unsigned>((w.rows + kNwg - 1) / kNwg),
                     static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)), static_cast<unsigned>(sp.splits));
     const int ld_out = static_cast<int>(sp.splits > 1 ? w.rows : ldy);
     if (w.format == LARQL_Q4_K)
-        q4k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(
-            w.qs, reinterpret_cast<const v4u*>(w.hdr), X, sp.splits > 1 ? part : Y, static_cast<int>(m),
+        q4k_gemm_hp_kernel<<<grid, dim3(kThreads), 0, s>>>(
+            w.qs, reinterpret_cast<const v4u*>(w.hdr), X, xe, sp.splits > 1 ? part : Y, static_cast<int>(m),
             static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per, ld_out);
     else
-        q6k_gemm_f32_kernel<<<grid, dim3(kThreads), 0, s>>>(
-            w.qs, X, sp.splits > 1 ? part : Y, static_cast<int>(m), static_cast<int>(w.rows), static_cast<int>(w.cols),
+        q6k_gemm_hp_kernel<<<grid, dim3(kThreads), 0, s>>>(
+            w.qs, X, xe, sp.splits > 1 ? part : Y, static_cast<int>(m), static_cast<int>(w.rows), static_cast<int>(w.cols),
             sp.sb_per, ld_out);
     LARQL_HIP_CHECK(hipGetLastError());
     if (sp.splits > 1) {

@@ -91,18 +91,24 @@ def test_q4k_matmul_m1_equals_matvec(hip):
     np.testing.assert_array_equal(a, b)
 
 
-@pytest.mark.parametrize("rows,cols,m", [(4096, 14336, 64), (300, 512, 37)])
-def test_q6k_gemm_rows_match_matvec_oracle(hip, rows, cols, m):
-    """The Q6_K f32-operand GEMM of the prompt pass (matvec_dev with m > 1 on a Q6_K handle)
+# (4096, 14336, 64): the Llama-3-8B down projection; (300, 512, 37): a ragged tile; (70, 1024,
+# 9, scaled): token rows scaled by 1e6 .. 1e-30, far outside fp16 (the GEMM's operand pairs
+# are fp16: each row must be brought into range by its own power of two), and a zero row
+@pytest.mark.parametrize("rows,cols,m,scaled", [(4096, 14336, 64, False), (300, 512, 37, False), (70, 1024, 9, True)])
+def test_q6k_gemm_rows_match_matvec_oracle(hip, rows, cols, m, scaled):
+    """The Q6_K f32-accuracy GEMM of the prompt pass (matvec_dev with m > 1 on a Q6_K handle)
     at the Llama-3-8B down-projection shape: every token row against the oracle's Q6_K
-    matvec (LC/src/cpu/ops/q6k_matvec.rs), within 1e-3 (f32 operands: measured ~1e-6)."""
+    matvec (LC/src/cpu/ops/q6k_matvec.rs), within 1e-3 (fp16 operand pairs: measured ~1e-6)."""
     import os
     from concurrent.futures import ThreadPoolExecutor
 
     torch = pytest.importorskip("torch")
-    print(f"[q6k gemm] rows={rows} cols={cols} m={m}", flush=True)
+    print(f"[q6k gemm] rows={rows} cols={cols} m={m} scaled={scaled}", flush=True)
     q6k = oracle.quantize_q6_k(oracle.gauss(91, rows * cols, 0.0, 0.02))
     x = oracle.gauss(92, m * cols).reshape(m, cols)
+    if scaled:
+        f = np.array([1e6, 1e3, 3e4, 1.0, 1e-3, 1e-8, 1e-20, 1e-30, 0.0], np.float32)
+        x = (x * f[:, None]).astype(np.float32)
     h = hip.register_weight(larql_hip.Q6_K, q6k, rows, cols)
     try:
         dx = torch.from_numpy(x).cuda()
@@ -111,7 +117,8 @@ def test_q6k_gemm_rows_match_matvec_oracle(hip, rows, cols, m):
         hip.synchronize()
         got = dy.cpu().numpy().reshape(m, rows)
         with ThreadPoolExecutor(max(1, min(16, len(os.sched_getaffinity(0))))) as pool:
-            errs = list(pool.map(lambda t: rel_err(got[t], oracle.q6k_matvec(q6k, x[t], rows, cols)), range(m)))
+            refs = list(pool.map(lambda t: oracle.q6k_matvec(q6k, x[t], rows, cols), range(m)))
+        errs = [rel_err(got[t], refs[t]) if np.any(refs[t]) else float(np.max(np.abs(got[t]))) for t in range(m)]
         e = max(errs)
         print(f"  rel_err max over all {m} tokens = {e:.3e}", flush=True)
         assert e <= REL_TOL, e
