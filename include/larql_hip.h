@@ -187,7 +187,7 @@ int larql_hip_quantize_weights(larql_hip_ctx* ctx, int format, const float* x, s
 
 /* One matvec with a registered weight.  For LARQL_Q4_K / LARQL_Q6_K `x` is f32
  * [m][cols] and x_scales is unused (m > 1: Q4_K runs the fp16-operand prefill GEMM, Q6_K
- * the f32-operand GEMM of the prompt pass); for LARQL_Q4_0 / LARQL_Q8_0 `x` is int8 [m][cols] and x_scales f32
+ * the f32-accuracy GEMM of the prompt pass); for LARQL_Q4_0 / LARQL_Q8_0 `x` is int8 [m][cols] and x_scales f32
  * [m][cols/32], any m (each output row in the single-row order, bit for bit).
  * out is f32 [m][rows].
  * LARQL_Q4_KF takes f32 x too (m > 1 runs m matvecs).
