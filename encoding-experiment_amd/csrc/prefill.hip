@@ -306,11 +306,23 @@ __global__ __launch_bounds__(kShThreads) void q4k_gemm_shared_kernel(const uint8
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+// v - (f32) the low / high f16 half of h2, one v_fma_mix_f32 (the half widened inside the
+// instruction; written out because the compiler otherwise emits a conversion and a subtract)
+__device__ __forceinline__ float sub_f16_lo(float v, uint32_t h2) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(v));
+    return r;
+}
+__device__ __forceinline__ float sub_f16_hi(float v, uint32_t h2) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(v));
+    return r;
+}
+
 // {a, b} -> hi pair {fp16(a), fp16(b)} and lo pair {fp16(a - hi_a), fp16(b - hi_b)}
 __device__ __forceinline__ void hp_split2(float a, float b, uint32_t& hi, uint32_t& lo) {
-    const f16x2 h = __builtin_convertvector((f32x2){a, b}, f16x2);
-    hi = __builtin_bit_cast(uint32_t, h);
-    const float la = a - static_cast<float>(h.x), lb = b - static_cast<float>(h.y);
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+    const float la = sub_f16_lo(a, hi), lb = sub_f16_hi(b, hi);
     lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){la, lb}, f16x2));
 }
 
