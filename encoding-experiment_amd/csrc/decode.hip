@@ -446,6 +446,211 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(AttnArgs a) 
                          lds + 2 * S);
 }
 
+// ── Prompt attention in one pass per block of queries ────────────────────
+// Prompt mode (a.batch queries, every K/V row already in the cache): one workgroup per
+// (block of queries, kv head) instead of one per (query, kv head, 64-position split) plus
+// a merge launch, so each K/V row is read once per block of queries, not once per query.
+// Wave w owns 16 score columns: queries q0 + w QPW .. q0 + (w + 1) QPW - 1 (QPW = 16 /
+// reps) times the reps query heads of the kv head, column c = query c / reps, head c % reps.
+// It walks its causal key range (from its first query's window start to its last query's
+// position) in blocks of 64 positions with an online softmax: per 16-key tile the scores
+// D[t][c] = K[t] . q_c on v_mfma_f32_16x16x32_f16 (K fp16 from the cache; each RoPE'd
+// query split into an fp16 part and its residue, two products, as in attn_decode_kernel),
+// masked outside [t_begin(q), pos(q)], scaled and capped; the block's column maxima and
+// sums across the four lane groups of a column by two lane swaps; the probabilities go
+// through LDS into the P.V operand order and are split the same way; O[d][c] +=
+// V[t][d] P[t][c] with V read as 8-position fp16 runs.  Positions past the wave's last
+// query read zeros (never stale cache rows).  The order of the sums differs from the split
+// kernel's (within f32 rounding).  Head dims up to 256 and reps in {1, 2, 4, 8}.
+constexpr int kPaBlock = 64;  // positions per online-softmax step
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_prompt_kernel(AttnArgs a) {
+    constexpr int KS = HD / 32, NDT = HD / 16;
+    __shared__ float qraw[4][16][HD];
+    __shared__ __attribute__((aligned(16))) float pblk[4][2 * 4 * 16 * 8];  // [ts][g][c][8 e] per wave
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int kvh = blockIdx.y;
+    const int reps = a.num_q / a.num_kv, qpw = 16 / reps, half = a.rdim / 2;
+    const int q_first = (blockIdx.x * 4 + wave) * qpw;      // this wave's first query
+    const int q_last = min(q_first + qpw, a.batch) - 1;     // and its last (< q_first: none)
+    const int qc = q_first + c / reps, hc = c % reps;       // column c's query and head
+    const bool col_ok = c < qpw * reps && qc <= q_last;
+    const int pos_c = a.T - 1 + qc;                          // column c's position
+    const int tb_c = (a.window > 0 && pos_c + 1 > a.window) ? pos_c + 1 - a.window : 0;
+
+    // 1. The wave's query rows (raw), RoPE'd per lane for its dims, QK-normed, split.
+    for (int i = lane; i < 16 * HD; i += 64) {
+        const int col = i / HD, d = i - col * HD, q = q_first + col / reps;
+        qraw[wave][col][d] = (col < qpw * reps && q <= q_last)
+                                 ? a.qkv[static_cast<size_t>(q) * a.qkv_ld + static_cast<size_t>(kvh * reps + col % reps) * HD + d]
+                                 : 0.f;
+    }
+    __syncthreads();
+    float qv[KS][8];
+    {
+        const float2* cs = a.rope + static_cast<size_t>(col_ok ? pos_c : 0) * half;
+        float ss = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int d = 32 * ks + 8 * g + e;
+                const float* x = qraw[wave][c];
+                const float v = d < half ? x[d] * cs[d].x - x[d + half] * cs[d].y
+                                         : (d < 2 * half ? x[d - half] * cs[d - half].y + x[d] * cs[d - half].x : x[d]);
+                qv[ks][e] = v;
+                ss += v * v;
+            }
+        if (a.qk_norm) {  // 1 / sqrt(sum q^2 + 1e-6) over the head: the four lane groups of column c
+            ss += __shfl_xor(ss, 16, 64);
+            ss += __shfl_xor(ss, 32, 64);
+            const float r = 1.0f / sqrtf(ss + 1e-6f);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) qv[ks][e] *= r;
+        }
+    }
+    v4u qh[KS], ql[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+        qh[ks] = split8(qv[ks], 0);
+        ql[ks] = split8(qv[ks], 1);
+    }
+
+    floatx4 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+    if (q_last >= q_first) {
+        const int pos_hi = a.T - 1 + q_last;  // the wave's last position
+        const int tq0 = a.T - 1 + q_first + 1;
+        const int t_lo = ((a.window > 0 && tq0 > a.window) ? tq0 - a.window : 0) & ~7;
+        float* pw = pblk[wave];
+        for (int kb = t_lo; kb <= pos_hi; kb += kPaBlock) {
+            // every K and V load of the block issued together, the K tiles first (loads
+            // return in order): A operand lane (g, c) of tile kt = position kb + 16 kt + c,
+            // dims 32 ks + 8 g ..; of V = dim 16 dt + c, positions kb + 32 ts + 8 g ..
+            v4u ka[4][KS], vb[NDT][2];
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                const int tk = kb + 16 * kt + c;
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++)
+                    ka[kt][ks] = tk <= pos_hi ? *reinterpret_cast<const v4u*>(a.kc + (static_cast<size_t>(tk) * a.num_kv + kvh) * HD +
+                                                                              32 * ks + 8 * g)
+                                              : v4u{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int ts = 0; ts < 2; ts++) {
+                    const int tv = kb + 32 * ts + 8 * g;
+                    vb[dt][ts] = tv <= pos_hi ? *reinterpret_cast<const v4u*>(
+                                                    a.vc + ((static_cast<size_t>(tv >> 3) * a.num_kv + kvh) * HD + 16 * dt + c) * 8)
+                                              : v4u{0u, 0u, 0u, 0u};
+                }
+            // scores of 4 tiles of 16 positions: lane (g, c) holds positions kb + 16 kt + 4 g + r
+            float sv[4][4];
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                floatx4 d4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    d4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ka[kt][ks]), __builtin_bit_cast(half8, qh[ks]),
+                                                                d4, 0, 0, 0);
+                    d4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, ka[kt][ks]), __builtin_bit_cast(half8, ql[ks]),
+                                                                d4, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int t = kb + 16 * kt + 4 * g + r;
+                    float v = d4[r] * a.scale;
+                    if (a.softcap > 0.f) v = tanhf(v / a.softcap) * a.softcap;
+                    sv[kt][r] = (col_ok && t >= tb_c && t <= pos_c) ? v : -INFINITY;
+                }
+            }
+            // online softmax over the block, column c
+            float mb = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) mb = fmaxf(mb, sv[kt][r]);
+            mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+            const float m_new = fmaxf(m_run, mb);
+            const float alpha = m_new == -INFINITY ? 1.f : expf(m_run - m_new);
+            float ls = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                float p4[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    p4[r] = sv[kt][r] == -INFINITY ? 0.f : expf(sv[kt][r] - m_new);
+                    ls += p4[r];
+                }
+                // positions 16 kt + 4 g .. + 3 -> P.V step ts, lane group gp, elements e0 .. e0 + 3
+                const int k0 = 16 * kt + 4 * g, ts = k0 >> 5, gp = (k0 & 31) >> 3, e0 = k0 & 7;
+                *reinterpret_cast<float4*>(pw + ((ts * 4 + gp) * 16 + c) * 8 + e0) = make_float4(p4[0], p4[1], p4[2], p4[3]);
+            }
+            ls += __shfl_xor(ls, 16, 64);
+            ls += __shfl_xor(ls, 32, 64);
+            l_run = l_run * alpha + ls;
+            m_run = m_new;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) o[dt] *= alpha;
+            // the wave reads what its lanes wrote: keep the LDS accesses in program order
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            v4u ph[2], pl[2];
+#pragma unroll
+            for (int ts = 0; ts < 2; ts++) {
+                const float4* src = reinterpret_cast<const float4*>(pw + ((ts * 4 + g) * 16 + c) * 8);
+                const float4 u0 = src[0], u1 = src[1];
+                const float pv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+                ph[ts] = split8(pv, 0);
+                pl[ts] = split8(pv, 1);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // O[d][c] += sum_t V[t][d] P[t][c]: A lane (g, c) = dim 16 dt + c, positions kb + 32 ts + 8 g ..
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+#pragma unroll
+                for (int ts = 0; ts < 2; ts++) {
+                    const int tv = kb + 32 * ts + 8 * g;
+                    v4u va = vb[dt][ts];
+                    if (tv + 7 > pos_hi) {  // the run holding pos_hi: zeros past it (rows not written)
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            const uint32_t lo = 2 * k <= pos_hi - tv ? (va[k] & 0xFFFFu) : 0u;
+                            const uint32_t hi = 2 * k + 1 <= pos_hi - tv ? (va[k] >> 16) : 0u;
+                            va[k] = lo | (hi << 16);
+                        }
+                    }
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, va), __builtin_bit_cast(half8, ph[ts]),
+                                                                   o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, va), __builtin_bit_cast(half8, pl[ts]),
+                                                                   o[dt], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // out[q][(kvh reps + h) HD + d] = O / l: lane (g, c) holds dims 16 dt + 4 g + r of column c
+    if (col_ok) {
+        const float inv = 1.0f / l_run;
+        float* dst = a.out + static_cast<size_t>(qc) * a.num_q * HD + static_cast<size_t>(kvh * reps + hc) * HD;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) dst[16 * dt + 4 * g + r] = o[dt][r] * inv;
+    }
+}
+
 bool attn_supported(int reps, int hd) { return reps >= 1 && reps <= 8 && hd % 32 == 0 && hd >= 32 && hd <= 512; }
 
 int attn_partial_stride(int hd) { return hd + 2; }
@@ -540,6 +745,17 @@ void launch_attention(const AttnArgs& a0, hipStream_t s) {
     AttnArgs a = a0;
     const int reps = a.num_q / a.num_kv;
     if (!attn_supported(reps, a.hd)) fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: head geometry");
+    if (a.batch && a.hd <= 256 && 16 % reps == 0) {  // prompt mode: one pass per block of queries
+        const int qpb = 4 * (16 / reps);
+        const dim3 gp(static_cast<unsigned>((a.batch + qpb - 1) / qpb), a.num_kv), bp(kAttnThreads);
+        if (!dispatch_head_dim<32>(a.hd, [&](auto h) {
+                constexpr int H = decltype(h)::value;
+                if constexpr (H <= 256) attn_prompt_kernel<H><<<gp, bp, 0, s>>>(a);
+            }))
+            fail(LARQL_HIP_ERR_UNSUPPORTED, "attention: head_dim");
+        LARQL_HIP_CHECK(hipGetLastError());
+        return;
+    }
     a.S = a.batch ? attn_prompt_splits(a.T, a.batch, a.window) : attn_splits(a.T, a.t_begin);
     a.pst = attn_partial_stride(a.hd);
     if (2 * static_cast<size_t>(a.S) * sizeof(float) + 32 > static_cast<size_t>(kMergeLdsMax))
