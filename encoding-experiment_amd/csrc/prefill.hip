@@ -18,6 +18,8 @@
 // which the nibble bytes unpack), and x16_pack_kernel writes X in that order.
 // fp16 operands carry 11 significant bits: over K = 2560 random terms the error is
 // ~1e-4 of max|Y|, inside the 1e-3 bar.
+#include <type_traits>
+
 #include "device_common.h"
 #include "larql_hip_internal.h"
 
@@ -29,7 +31,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-// Tiling of the f32-accuracy GEMMs (q4k_gemm_hp_kernel, q6k_gemm_hp_kernel); the packed
+// Tiling of the f32-accuracy GEMMs (q4k_gemm_sq_kernel, q6k_gemm_hp_kernel); the packed
 // X of the fp16 GEMM is padded to kMt tiles of 16 tokens.
 constexpr int kMt = 4;                 // 16-token tiles per workgroup (64 tokens)
 constexpr int kNT = 5;                 // 16-row weight tiles per wave (80 rows)
@@ -285,24 +287,22 @@ __global__ __launch_bounds__(kShThreads) void q4k_gemm_shared_kernel(const uint8
 }
 
 // ── f32 inputs to f32 accuracy: fp16 operand pairs on the matrix cores ────
-// The accurate variant for chains of projections (the batched prompt pass; Q6_K with
-// m > 1).  64 tokens x 320 weight rows per workgroup, 80 rows per wave (each wave
-// dequantizes its own rows for the workgroup's tokens), two-unit ring of X staged in LDS.
-// Every f32 operand v is split into two fp16 parts, hi = fp16(v) and lo = fp16(v - hi)
-// (v - hi exact in f32), so v = hi + lo to ~2^-22, and each product runs as three
-// v_mfma_f32_16x16x32_f16 with f32 accumulation: x_hi w_hi + x_hi w_lo + x_lo w_hi (the
-// dropped x_lo w_lo is ~2^-22 of it).  Through 16 and 32 layers this is as close to the
-// oracle as exact f32 products on v_mfma_f32_16x16x4f32 were, at 2.4x the speed; single
-// fp16 operands (2^-11) compounded past the bar, and bf16 pairs (hi = 8 bits, 2^-16 per
-// product) doubled the error.  fp16's range is made safe per token: row_exp_kernel gives
-// each X row the power of two that puts its largest |x| in [2^14, 2^15), the staging
-// scales the row by it and the epilogue divides it out, both exact; weights are used
-// unscaled (|w| must stay below 65504: a Q4_K super-block scale d below ~69, far above
-// real weights).  The weights are dequantized as before, w = fma(q, d sc_j, -dmin m_j) in
-// f32, then split.  A k-step of 32 takes elements 8 s .. 8 s + 7 of the lane's sub-block
-// 4 h + g for lane group g, in the order the nibbles unpack (0, 2, 4, 6, 1, 3, 5, 7), and
-// the X staging writes its fp16 pairs in that order.  An infinite operand gives NaN (its lo
-// part is inf - inf).
+// The accurate GEMMs for chains of projections (the batched prompt pass; Q6_K with m > 1):
+// q4k_gemm_sq_kernel (Q4_K) and q6k_gemm_hp_kernel (Q6_K).  64 tokens x 320 weight rows per
+// workgroup, 80 rows per wave (each wave prepares its own rows' operands for the
+// workgroup's tokens), two-unit ring of X staged in LDS.  Every f32 operand v is split into
+// two fp16 parts, hi = fp16(v) and lo = fp16(v - hi) (v - hi exact in f32), so v = hi + lo
+// to ~2^-22; a product of two split operands runs as three v_mfma_f32_16x16x32_f16 with f32
+// accumulation, x_hi w_hi + x_hi w_lo + x_lo w_hi (the dropped x_lo w_lo is ~2^-22 of it),
+// one with an exact fp16 weight operand as two.  Single fp16 operands (2^-11) compounded
+// past the bar through 8 and 16 layers, and bf16 pairs (hi = 8 bits, 2^-16 per product)
+// doubled the error.  fp16's range is made safe per token: row_exp_kernel gives each X row
+// the power of two that puts its largest |x| in [2^14, 2^15), the staging scales the row by
+// it and the epilogue divides it out, both exact.  Q6_K weights are dequantized,
+// w = d sc (q - 32) in f32, then split (|w| must stay below 65504).  A k-step of 32 takes
+// elements 8 s .. 8 s + 7 of the lane's sub-block 4 h + g for lane group g (Q6_K), in the
+// order the nibbles unpack (0, 2, 4, 6, 1, 3, 5, 7), and the X staging writes its fp16
+// pairs in that order.  An infinite operand gives NaN (its lo part is inf - inf).
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -340,6 +340,9 @@ constexpr int kHpPitch = 36;  // dwords per lane slot in LDS: 16 hi + 16 lo + 4 
 // X staging: the thread's 32 elements (8 float4) times its token's power of two -> hi
 // dwords 0..15 and lo dwords 16..31 of its LDS slot, step s at dwords 4 s .. 4 s + 3 in
 // the order (0, 2), (4, 6), (1, 3), (5, 7) of elements 8 s + ...
+// (STEP, LO: dwords from step s to s + 1 and from a step's hi to its lo dwords; the
+// defaults are the slot layout above)
+template <int STEP = 4, int LO = 16>
 __device__ __forceinline__ void hp_store_x(uint32_t* d, const float4 (&v)[8], float scale) {
 #pragma unroll
     for (int s = 0; s < 4; s++) {
@@ -348,8 +351,8 @@ __device__ __forceinline__ void hp_store_x(uint32_t* d, const float4 (&v)[8], fl
                             a.y * scale, a.w * scale, b.y * scale, b.w * scale};
         v4u hi, lo;
         hp_split8(e, hi, lo);
-        *reinterpret_cast<v4u*>(d + 4 * s) = hi;
-        *reinterpret_cast<v4u*>(d + 16 + 4 * s) = lo;
+        *reinterpret_cast<v4u*>(d + STEP * s) = hi;
+        *reinterpret_cast<v4u*>(d + STEP * s + LO) = lo;
     }
 }
 
@@ -367,9 +370,13 @@ __device__ __forceinline__ void hp3_mfma(floatx4 (&acc)[MT], const v4u (&ah)[MT]
 }
 
 // e[row] = the power of two that puts max |X[row]| in [2^14, 2^15) (0 for a row of zeros
-// or a non-finite maximum).  One workgroup per row; K a multiple of 4.
-__global__ __launch_bounds__(256) void row_exp_kernel(const float* __restrict__ X, int K, int* __restrict__ e) {
+// or a non-finite maximum).  With xs, also xs[row][j] = 2^(e - 5) times the sum of the 32
+// elements of sub-block j, summed in f64 and rounded once (|xs| < 2^15).  One workgroup per
+// row; K a multiple of 4 (of 32 with xs).
+__global__ __launch_bounds__(256) void row_exp_kernel(const float* __restrict__ X, int K, int* __restrict__ e,
+                                                      float* __restrict__ xs) {
     __shared__ float wm[4];
+    __shared__ int es;
     const float* row = X + static_cast<size_t>(blockIdx.x) * K;
     float m = 0.f;
     for (int i = 4 * static_cast<int>(threadIdx.x); i < K; i += 4 * 256) {
@@ -382,7 +389,24 @@ __global__ __launch_bounds__(256) void row_exp_kernel(const float* __restrict__ 
     __syncthreads();
     if (threadIdx.x == 0) {
         m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-        e[blockIdx.x] = (m > 0.f && m <= 3.4e38f) ? min(120, max(-120, 14 - ilogbf(m))) : 0;
+        const int ev = (m > 0.f && m <= 3.4e38f) ? min(120, max(-120, 14 - ilogbf(m))) : 0;
+        e[blockIdx.x] = ev;
+        es = ev;
+    }
+    if (!xs) return;  // (uniform)
+    __syncthreads();
+    const double sc = ldexp(1.0, es - 5);
+    const int nsb = K / 32;
+    for (int j = static_cast<int>(threadIdx.x); j < nsb; j += 256) {
+        const float4* p = reinterpret_cast<const float4*>(row + 32 * j);
+        double sum[2] = {0.0, 0.0};  // f64: the sum is rounded once, to f32
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 v = p[k];
+            sum[k & 1] += (static_cast<double>(v.x) + static_cast<double>(v.y)) +
+                          (static_cast<double>(v.z) + static_cast<double>(v.w));
+        }
+        xs[static_cast<size_t>(blockIdx.x) * nsb + j] = static_cast<float>((sum[0] + sum[1]) * sc);
     }
 }
 
@@ -396,12 +420,41 @@ __device__ __forceinline__ float hp_token_scales(const int* __restrict__ xe, int
     return ldexpf(1.0f, xe[min(xr_row, M - 1)]);
 }
 
-__global__ __launch_bounds__(kThreads) void q4k_gemm_hp_kernel(const uint8_t* __restrict__ qs,
+// ── Q4_K prompt GEMM on exact integer weight operands ─────────────────────
+// The Q4_K form of the f32-accuracy GEMM.  A Q4_K weight is w = d s_j q - dmin m_j (q the
+// 4-bit code, s_j and m_j the 6-bit scale and 4-bit min of its 32-element sub-block j, d
+// and dmin f16 per super-block), so per super-block and token
+//   sum_k x_k w_k = d sum_j s_j (sum_{k in j} x_k q_k) - dmin sum_j m_j X_j,  X_j = sum_{k in j} x_k.
+// s_j q <= 945 is an exact fp16 integer: the first sum runs on v_mfma_f32_16x16x32_f16 with
+// the weight operand s_j q and the token operand split into fp16 hi and lo parts (two
+// products, both exact in f32; only the split's 2^-22 is lost), one k-step per sub-block
+// and a fresh accumulator per super-block, added into the total times d.  The min term
+// comes after the K loop: the sub-block sums X_j 2^(e - 5) (row_exp_kernel) against
+// -32 dmin m_j per row, both as fp16 pairs (three products), 32 sub-blocks per k-step.
+// Tiling and X staging as the other f32-accuracy GEMMs; a lane's 16-byte nibble load holds one
+// sub-block (lane group g: sub-block 4 h + g), so a 4 x 4 transpose of its words across the
+// lane groups (two v_permlane32_swap, two v_permlane16_swap) gives lane group g word g
+// (elements 8 g .. 8 g + 7) of each of the unit's four sub-blocks.  The weight operand is
+// built as fp16 pairs: 0x64 above each code byte is 1024 + q, and
+// fma(1024 + q, s, -1024 s) = s q exactly.  Weights need dmin below ~136 (fp16 range of
+// 32 dmin m_j); d has no limit.
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+constexpr int kSqPitch = 12;  // dwords per staged cell: 4 hi + 4 lo + 4 (spread the banks)
+
+__device__ __forceinline__ uint32_t sq_pair(uint32_t codes, uint32_t sel, h2v s, h2v ns) {
+    const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, codes, sel));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(b, s, ns));
+}
+
+__global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __restrict__ qs,
                                                                const v4u* __restrict__ hdr,
                                                                const float* __restrict__ X, const int* __restrict__ xe,
-                                                               float* __restrict__ Y, int M, int N, int K, int ntiles,
-                                                               int sb_per, int ldy) {
-    __shared__ uint32_t As[2][kMt][64][kHpPitch];
+                                                               const float* __restrict__ xs, float* __restrict__ Y,
+                                                               int M, int N, int K, int ntiles, int sb_per, int ldy) {
+    // staged X by k-step: cell [t][16 s + token] holds step s (elements 8 s .. 8 s + 7) of
+    // sub-block 4h + t, hi dwords 0..3 and lo 4..7, so the k-step t operand of lane l is
+    // cell [t][l] (12-dword pitch: no bank conflicts for the reads or the writes)
+    __shared__ uint32_t Aq[2][kMt][4][64][kSqPitch];
     __shared__ float tok_inv[16 * kMt];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
@@ -409,7 +462,6 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_hp_kernel(const uint8_t* __
     const int mt0 = blockIdx.y * kMt;
     const int nt0 = (blockIdx.x * kWaves + wave) * kNT;
     // split blockIdx.z of K: super-blocks [z sb_per, (z + 1) sb_per), partial sums to Y[z]
-    // (rows ldy apart; the dense partials of a split launch have ldy = N)
     const int u0 = 2 * static_cast<int>(blockIdx.z) * sb_per, u1 = min(2 * S, u0 + 2 * sb_per), last = u1 - 1;
     Y += static_cast<size_t>(blockIdx.z) * M * ldy;
     uint32_t qo[kNT], ho[kNT];
@@ -419,10 +471,10 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_hp_kernel(const uint8_t* __
         qo[j] = __builtin_amdgcn_readfirstlane(t * S * 2048u);
         ho[j] = __builtin_amdgcn_readfirstlane(t * S * 256u);
     }
-    // X staging: thread (tile r = tid / 64, slot l = tid % 64) loads token 16 (mt0 + r) + l % 16,
-    // elements 32 (4h + l / 16) .. + 31 of super-block sb; zeros for tokens past M.
+    // X staging: slot l of tile r holds sub-block 4h + l / 16 of
+    // token 16 (mt0 + r) + l % 16
     const int xr_row = (mt0 + (tid >> 6)) * 16 + (lane & 15);
-    const bool xr_ok = xr_row < M;  // (the select also keeps the compiler from a stack copy of Xu)
+    const bool xr_ok = xr_row < M;
     const float* xrow = X + static_cast<size_t>(min(xr_row, M - 1)) * K + 32 * g;
     const float xscale = hp_token_scales(xe, M, mt0, xr_row, tok_inv);
     struct Xu {
@@ -434,7 +486,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_hp_kernel(const uint8_t* __
         for (int k = 0; k < 8; k++) x.v[k] = xr_ok ? p[k] : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     auto store_x = [&](int b, const Xu& x) __attribute__((always_inline)) {
-        hp_store_x(&As[b][tid >> 6][lane][0], x.v, xscale);
+        hp_store_x<16 * kSqPitch, 4>(&Aq[b][tid >> 6][lane >> 4][lane & 15][0], x.v, xscale);
     };
     struct Wu {
         v4u q[kNT], hd[kNT];
@@ -448,43 +500,65 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_hp_kernel(const uint8_t* __
             w.hd[j] = *reinterpret_cast<const v4u*>(hdrb + ho[j] + static_cast<uint32_t>(u >> 1) * 256u);
         }
     };
-    floatx4 acc[kNT][kMt];
+    floatx4 acc[kNT][kMt], dp[kNT][kMt];
 #pragma unroll
     for (int j = 0; j < kNT; j++)
 #pragma unroll
-        for (int i = 0; i < kMt; i++) acc[j][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < kMt; i++) acc[j][i] = dp[j][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](int b, int u, const Wu& w) __attribute__((always_inline)) {
-        const int h = u & 1;
-        float sc[kNT], nmn[kNT];
+    // unit (sb, h) of buffer b: k-step t = sub-block 4h + t, lane (g, token c) takes its
+    // elements 8 g .. 8 g + 7 (step g of the staging thread of token c, sub-block 4h + t)
+    auto compute = [&](int b, auto hc, const Wu& w) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value;
+        v4u n[kNT];
+        uint32_t s6[kNT];
 #pragma unroll
         for (int j = 0; j < kNT; j++) {
-            const float d = h2f(w.hd[j].x & 0xFFFFu), dmin = h2f(w.hd[j].x >> 16);
-            const uint32_t scw = h ? w.hd[j].z : w.hd[j].y;
-            sc[j] = d * static_cast<float>((scw >> (8 * g)) & 0x3Fu);
-            nmn[j] = -(dmin * static_cast<float>((w.hd[j].w >> (8 * g + 4 * h)) & 0xFu));
+            const auto a02 = __builtin_amdgcn_permlane32_swap(w.q[j].x, w.q[j].z, false, false);
+            const auto a13 = __builtin_amdgcn_permlane32_swap(w.q[j].y, w.q[j].w, false, false);
+            const auto r01 = __builtin_amdgcn_permlane16_swap(a02[0], a13[0], false, false);
+            const auto r23 = __builtin_amdgcn_permlane16_swap(a02[1], a13[1], false, false);
+            n[j] = v4u{r01[0], r01[1], r23[0], r23[1]};
+            s6[j] = (h ? w.hd[j].z : w.hd[j].y) & 0x3F3F3F3Fu;
         }
 #pragma unroll
-        for (int s = 0; s < 4; s++) {  // elements 8 s .. 8 s + 7 of the lane's sub-block
+        for (int t = 0; t < 4; t++) {
             v4u ah[kMt], al[kMt];
 #pragma unroll
             for (int i = 0; i < kMt; i++) {
-                ah[i] = *reinterpret_cast<const v4u*>(&As[b][i][lane][4 * s]);
-                al[i] = *reinterpret_cast<const v4u*>(&As[b][i][lane][16 + 4 * s]);
+                ah[i] = *reinterpret_cast<const v4u*>(&Aq[b][i][t][lane][0]);
+                al[i] = *reinterpret_cast<const v4u*>(&Aq[b][i][t][lane][4]);
             }
 #pragma unroll
             for (int j = 0; j < kNT; j++) {
-                // bytes 4 s .. 4 s + 3: elements 8 s + 2 i (low nibble), 8 s + 2 i + 1 (high)
-                const uint32_t word = w.q[j][s];
-                uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
-                asm("" : "+v"(lo), "+v"(hi));  // opaque: keeps v_cvt_f32_ubyteN, not bfe + convert
-                const float wt[8] = {__builtin_fmaf(ubyte0(lo), sc[j], nmn[j]), __builtin_fmaf(ubyte1(lo), sc[j], nmn[j]),
-                                     __builtin_fmaf(ubyte2(lo), sc[j], nmn[j]), __builtin_fmaf(ubyte3(lo), sc[j], nmn[j]),
-                                     __builtin_fmaf(ubyte0(hi), sc[j], nmn[j]), __builtin_fmaf(ubyte1(hi), sc[j], nmn[j]),
-                                     __builtin_fmaf(ubyte2(hi), sc[j], nmn[j]), __builtin_fmaf(ubyte3(hi), sc[j], nmn[j])};
-                v4u bh, bl;
-                hp_split8(wt, bh, bl);
-                hp3_mfma<kMt>(acc[j], ah, al, bh, bl);
+                // s = scale of sub-block 4h + t (both halves), ns = -1024 s
+                const h2v sv = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, s6[j], 0x04000400u + 0x00010001u * t)) -
+                               h2v{1024.0f16, 1024.0f16};
+                const h2v ns = sv * h2v{-1024.0f16, -1024.0f16};
+                const uint32_t word = n[j][t];
+                const uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+                // elements (0, 2), (4, 6), (1, 3), (5, 7) of the eight, the staging's order
+                const v4u bq = {sq_pair(lo, 0x04010400u, sv, ns), sq_pair(lo, 0x04030402u, sv, ns),
+                                sq_pair(hi, 0x04010400u, sv, ns), sq_pair(hi, 0x04030402u, sv, ns)};
+                const half8 B = __builtin_bit_cast(half8, bq);
+#pragma unroll
+                for (int i = 0; i < kMt; i++)
+                    dp[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(half8, ah[i]), B, (h == 0 && t == 0) ? floatx4{0.f, 0.f, 0.f, 0.f} : dp[j][i],
+                        0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < kMt; i++)
+                    dp[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, al[i]), B, dp[j][i], 0, 0, 0);
+            }
+        }
+        if constexpr (h == 1) {  // the super-block's sum times d (row c)
+#pragma unroll
+            for (int j = 0; j < kNT; j++) {
+                const float d = h2f(w.hd[j].x & 0xFFFFu);
+#pragma unroll
+                for (int i = 0; i < kMt; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[j][i][r] = fmaf(d, dp[j][i][r], acc[j][i][r]);
             }
         }
     };
@@ -502,15 +576,68 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_hp_kernel(const uint8_t* __
     for (int u = u0; u < u1; u += 2) {
         store_x(1, x1);
         load_x(min(u + 2, last), x0);
-        compute(0, u, w0);
+        compute(0, std::integral_constant<int, 0>{}, w0);
         load_w(min(u + 2, last), w0);
         __syncthreads();
         store_x(0, x0);
         load_x(min(u + 3, last), x1);
-        compute(1, u + 1, w1);
+        compute(1, std::integral_constant<int, 1>{}, w1);
         load_w(min(u + 3, last), w1);
         __syncthreads();
     }
+
+    // min term over super-blocks [SB0, SB1), four per k-step: lane group g takes super-block
+    // q + g, its eight sub-blocks in order (token side: scaled sums; row side: -32 dmin m_j)
+    const int SB0 = u0 >> 1, SB1 = u1 >> 1, nsb = K / 32;
+    struct Mu {
+        float4 x[kMt][2];
+        v4u hd[kNT];
+    };
+    auto load_m = [&](int q, Mu& mu) __attribute__((always_inline)) {
+        const int sb = q + g;
+        const bool sv = sb < SB1;
+#pragma unroll
+        for (int i = 0; i < kMt; i++) {
+            const int tok = (mt0 + i) * 16 + c;
+            const bool ok = sv && tok < M;
+            const float4* p = reinterpret_cast<const float4*>(xs + static_cast<size_t>(min(tok, M - 1)) * nsb + 8 * min(sb, S - 1));
+            mu.x[i][0] = ok ? p[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+            mu.x[i][1] = ok ? p[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < kNT; j++)
+            mu.hd[j] = sv ? *reinterpret_cast<const v4u*>(hdrb + ho[j] + static_cast<uint32_t>(sb) * 256u)
+                          : v4u{0u, 0u, 0u, 0u};
+    };
+    auto apply_m = [&](const Mu& mu) __attribute__((always_inline)) {
+        v4u ah[kMt], al[kMt];
+#pragma unroll
+        for (int i = 0; i < kMt; i++) {
+            const float v[8] = {mu.x[i][0].x, mu.x[i][0].y, mu.x[i][0].z, mu.x[i][0].w,
+                                mu.x[i][1].x, mu.x[i][1].y, mu.x[i][1].z, mu.x[i][1].w};
+            hp_split8(v, ah[i], al[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < kNT; j++) {
+            const float nd = -32.0f * h2f(mu.hd[j].x >> 16);
+            float cm[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) cm[k] = nd * static_cast<float>((mu.hd[j].w >> (8 * (k & 3) + 4 * (k >> 2))) & 0xFu);
+            v4u bh, bl;
+            hp_split8(cm, bh, bl);
+            hp3_mfma<kMt>(acc[j], ah, al, bh, bl);
+        }
+    };
+    Mu m0, m1;
+    load_m(SB0, m0);
+    for (int q = SB0; q < SB1; q += 8) {
+        load_m(q + 4, m1);
+        apply_m(m0);
+        if (q + 4 >= SB1) break;
+        load_m(q + 8, m0);
+        apply_m(m1);
+    }
+
     // D lane (g, c) holds tokens 4g .. 4g + 3 of weight row c of each 16 x 16 tile
 #pragma unroll
     for (int i = 0; i < kMt; i++)
@@ -695,10 +822,11 @@ F32Split f32_split(const DevWeight& w, size_t m) {
 
 }  // namespace
 
-// workspace: the K-split partials (when split), then the m row exponents (ints)
+// workspace: the K-split partials (when split), the m row exponents (ints), then for Q4_K
+// the m x K / 32 scaled sub-block sums
 size_t q4k_gemm_f32_part_floats(const DevWeight& w, size_t m) {
     const F32Split sp = f32_split(w, m);
-    return (sp.splits > 1 ? sp.splits * m * w.rows : 0) + m;
+    return (sp.splits > 1 ? sp.splits * m * w.rows : 0) + m + (w.format == LARQL_Q4_K ? 4 + m * (w.cols / 32) : 0);
 }
 
 void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, float* part, size_t part_floats,
@@ -709,18 +837,26 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
         fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: Q4_K or Q6_K weights only");
     if (m == 0) return;
     if (m > 0x7FFFFFFF / w.cols) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: too many tokens");
-    if (!part || part_floats < m) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: no workspace for the row exponents");
+    // row exponents, then for Q4_K the sub-block sums from a 16-byte boundary (float4 reads)
+    const size_t extra = m + (w.format == LARQL_Q4_K ? 4 + m * (w.cols / 32) : 0);
+    if (!part || part_floats < extra) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: no workspace for the row exponents");
     F32Split sp = f32_split(w, m);
-    if (sp.splits > 1 && part_floats < sp.splits * m * w.rows + m) sp = {1, static_cast<int>(w.cols / 256)};
-    int* xe = reinterpret_cast<int*>(part + (sp.splits > 1 ? sp.splits * m * w.rows : 0));
-    row_exp_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, static_cast<int>(w.cols), xe);
+    if (sp.splits > 1 && part_floats < sp.splits * m * w.rows + extra) sp = {1, static_cast<int>(w.cols / 256)};
+    const size_t xe_at = sp.splits > 1 ? sp.splits * m * w.rows : 0;
+    int* xe = reinterpret_cast<int*>(part + xe_at);
+    float* xs = nullptr;
+    if (w.format == LARQL_Q4_K) {
+        const uintptr_t at = reinterpret_cast<uintptr_t>(part + xe_at + m);
+        xs = reinterpret_cast<float*>((at + 15) & ~uintptr_t{15});
+    }
+    row_exp_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, static_cast<int>(w.cols), xe, xs);
     LARQL_HIP_CHECK(hipGetLastError());
     const dim3 grid(static_cast<unsigned>((w.rows + kNwg - 1) / kNwg),
                     static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)), static_cast<unsigned>(sp.splits));
     const int ld_out = static_cast<int>(sp.splits > 1 ? w.rows : ldy);
     if (w.format == LARQL_Q4_K)
-        q4k_gemm_hp_kernel<<<grid, dim3(kThreads), 0, s>>>(
-            w.qs, reinterpret_cast<const v4u*>(w.hdr), X, xe, sp.splits > 1 ? part : Y, static_cast<int>(m),
+        q4k_gemm_sq_kernel<<<grid, dim3(kThreads), 0, s>>>(
+            w.qs, reinterpret_cast<const v4u*>(w.hdr), X, xe, xs, sp.splits > 1 ? part : Y, static_cast<int>(m),
             static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per, ld_out);
     else
         q6k_gemm_hp_kernel<<<grid, dim3(kThreads), 0, s>>>(
