@@ -34,10 +34,9 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 // Tiling of the f32-accuracy GEMMs (q4k_gemm_sq_kernel, q6k_gemm_hp_kernel); the packed
 // X of the fp16 GEMM is padded to kMt tiles of 16 tokens.
 constexpr int kMt = 4;                 // 16-token tiles per workgroup (64 tokens)
-constexpr int kNT = 5;                 // 16-row weight tiles per wave (80 rows)
+constexpr int kNT = 5;                 // 16-row weight tiles per wave (80 rows; Q4_K: 4 or 5)
 constexpr int kWaves = 4;              // waves per workgroup, side by side along N
 constexpr int kThreads = 64 * kWaves;
-constexpr int kNwg = 16 * kNT * kWaves;  // 320 weight rows per workgroup
 
 // X [M x K] f32 -> XP[mt][sb][h][s][lane] (uint4 = 8 halves); rows >= M are zeros.
 // Workgroup (sb, mt): the 16 x 256 block of X, read row-major into LDS, written out as
@@ -446,6 +445,7 @@ __device__ __forceinline__ uint32_t sq_pair(uint32_t codes, uint32_t sel, h2v s,
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(b, s, ns));
 }
 
+template <int NT>
 __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __restrict__ qs,
                                                                const v4u* __restrict__ hdr,
                                                                const float* __restrict__ X, const int* __restrict__ xe,
@@ -460,13 +460,13 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
     const int g = lane >> 4, c = lane & 15;
     const int S = K / 256;
     const int mt0 = blockIdx.y * kMt;
-    const int nt0 = (blockIdx.x * kWaves + wave) * kNT;
+    const int nt0 = (blockIdx.x * kWaves + wave) * NT;
     // split blockIdx.z of K: super-blocks [z sb_per, (z + 1) sb_per), partial sums to Y[z]
     const int u0 = 2 * static_cast<int>(blockIdx.z) * sb_per, u1 = min(2 * S, u0 + 2 * sb_per), last = u1 - 1;
     Y += static_cast<size_t>(blockIdx.z) * M * ldy;
-    uint32_t qo[kNT], ho[kNT];
+    uint32_t qo[NT], ho[NT];
 #pragma unroll
-    for (int j = 0; j < kNT; j++) {
+    for (int j = 0; j < NT; j++) {
         const uint32_t t = static_cast<uint32_t>(min(nt0 + j, ntiles - 1));
         qo[j] = __builtin_amdgcn_readfirstlane(t * S * 2048u);
         ho[j] = __builtin_amdgcn_readfirstlane(t * S * 256u);
@@ -489,20 +489,20 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
         hp_store_x<16 * kSqPitch, 4>(&Aq[b][tid >> 6][lane >> 4][lane & 15][0], x.v, xscale);
     };
     struct Wu {
-        v4u q[kNT], hd[kNT];
+        v4u q[NT], hd[NT];
     };
     const uint8_t* hdrb = reinterpret_cast<const uint8_t*>(hdr) + c * 16;
     auto load_w = [&](int u, Wu& w) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < kNT; j++) {
+        for (int j = 0; j < NT; j++) {
             w.q[j] = __builtin_nontemporal_load(
                 reinterpret_cast<const v4u*>(qs + qo[j] + static_cast<uint32_t>(u) * 1024u) + lane);
             w.hd[j] = *reinterpret_cast<const v4u*>(hdrb + ho[j] + static_cast<uint32_t>(u >> 1) * 256u);
         }
     };
-    floatx4 acc[kNT][kMt], dp[kNT][kMt];
+    floatx4 acc[NT][kMt], dp[NT][kMt];
 #pragma unroll
-    for (int j = 0; j < kNT; j++)
+    for (int j = 0; j < NT; j++)
 #pragma unroll
         for (int i = 0; i < kMt; i++) acc[j][i] = dp[j][i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
@@ -510,10 +510,10 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
     // elements 8 g .. 8 g + 7 (step g of the staging thread of token c, sub-block 4h + t)
     auto compute = [&](int b, auto hc, const Wu& w) __attribute__((always_inline)) {
         constexpr int h = decltype(hc)::value;
-        v4u n[kNT];
-        uint32_t s6[kNT];
+        v4u n[NT];
+        uint32_t s6[NT];
 #pragma unroll
-        for (int j = 0; j < kNT; j++) {
+        for (int j = 0; j < NT; j++) {
             const auto a02 = __builtin_amdgcn_permlane32_swap(w.q[j].x, w.q[j].z, false, false);
             const auto a13 = __builtin_amdgcn_permlane32_swap(w.q[j].y, w.q[j].w, false, false);
             const auto r01 = __builtin_amdgcn_permlane16_swap(a02[0], a13[0], false, false);
@@ -530,7 +530,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
                 al[i] = *reinterpret_cast<const v4u*>(&Aq[b][i][t][lane][4]);
             }
 #pragma unroll
-            for (int j = 0; j < kNT; j++) {
+            for (int j = 0; j < NT; j++) {
                 // s = scale of sub-block 4h + t (both halves), ns = -1024 s
                 const h2v sv = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, s6[j], 0x04000400u + 0x00010001u * t)) -
                                h2v{1024.0f16, 1024.0f16};
@@ -553,7 +553,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
         }
         if constexpr (h == 1) {  // the super-block's sum times d (row c)
 #pragma unroll
-            for (int j = 0; j < kNT; j++) {
+            for (int j = 0; j < NT; j++) {
                 const float d = h2f(w.hd[j].x & 0xFFFFu);
 #pragma unroll
                 for (int i = 0; i < kMt; i++)
@@ -591,7 +591,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
     const int SB0 = u0 >> 1, SB1 = u1 >> 1, nsb = K / 32;
     struct Mu {
         float4 x[kMt][2];
-        v4u hd[kNT];
+        v4u hd[NT];
     };
     auto load_m = [&](int q, Mu& mu) __attribute__((always_inline)) {
         const int sb = q + g;
@@ -605,7 +605,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
             mu.x[i][1] = ok ? p[1] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
-        for (int j = 0; j < kNT; j++)
+        for (int j = 0; j < NT; j++)
             mu.hd[j] = sv ? *reinterpret_cast<const v4u*>(hdrb + ho[j] + static_cast<uint32_t>(sb) * 256u)
                           : v4u{0u, 0u, 0u, 0u};
     };
@@ -618,7 +618,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
             hp_split8(v, ah[i], al[i]);
         }
 #pragma unroll
-        for (int j = 0; j < kNT; j++) {
+        for (int j = 0; j < NT; j++) {
             const float nd = -32.0f * h2f(mu.hd[j].x >> 16);
             float cm[8];
 #pragma unroll
@@ -642,7 +642,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
 #pragma unroll
     for (int i = 0; i < kMt; i++)
 #pragma unroll
-        for (int j = 0; j < kNT; j++) {
+        for (int j = 0; j < NT; j++) {
             const int col = (nt0 + j) * 16 + c;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
@@ -801,21 +801,32 @@ __global__ void sum_splits_kernel(const float* __restrict__ P, float* __restrict
     Y[(i / N) * ldy + i % N] = a;
 }
 
-// K-splits for the f32-accuracy GEMM: the count (1..4, whole super-blocks each) that minimises
-// rounds of workgroups over the CUs x units per workgroup (one workgroup per CU at a time).
+// K-splits for the f32-accuracy GEMM (1..4, whole super-blocks each) and, for Q4_K, the
+// 16-row weight tiles per wave (4 or 5; a workgroup's rows are 64 nt): the choice with the
+// least modelled time, rounds of workgroups over the CUs (one workgroup per CU at a time)
+// x units per workgroup (super-blocks x tiles, ~1.35 us each on MI355X), plus, when split,
+// the partial sums written and summed ((splits + 1) m N floats at ~5 TB/s).  Measured at
+// the 8B shape and 512 tokens: 4 tiles take the 4096-row projections from 63.6 to 55.7 us
+// and [1024 x 4096] from 35.7 to 32.8 us; the [28672 x 4096] gate|up keeps 5 (323 us, 1
+// split, against 370 + 31.5 us for 4 tiles, 2 splits and their sum).
 struct F32Split {
-    int splits, sb_per;
+    int splits, sb_per, nt;
 };
 F32Split f32_split(const DevWeight& w, size_t m) {
     const int S = static_cast<int>(w.cols / 256);
-    const long wgs = static_cast<long>((w.rows + kNwg - 1) / kNwg) * static_cast<long>((m + 16 * kMt - 1) / (16 * kMt));
     const long cus = current_device_cus();
-    F32Split best{1, S};
-    long best_cost = -1;
-    for (int s = 1; s <= 4 && s <= S; s++) {
-        const int per = (S + s - 1) / s, eff = (S + per - 1) / per;
-        const long cost = ((wgs * eff + cus - 1) / cus) * per;
-        if (best_cost < 0 || cost < best_cost) best = {eff, per}, best_cost = cost;
+    const double unit_ns = 1350.0, sum_ns_per_float = 4.0 / 5000.0;  // 5 TB/s = 5000 bytes per ns
+    F32Split best{1, S, kNT};
+    double best_cost = -1.0;
+    for (int nt = (w.format == LARQL_Q4_K ? 4 : kNT); nt <= kNT; nt++) {
+        const long rows_wg = 16L * nt * kWaves;
+        const long wgs = static_cast<long>((w.rows + rows_wg - 1) / rows_wg) * static_cast<long>((m + 16 * kMt - 1) / (16 * kMt));
+        for (int s = 1; s <= 4 && s <= S; s++) {
+            const int per = (S + s - 1) / s, eff = (S + per - 1) / per;
+            double cost = static_cast<double>((wgs * eff + cus - 1) / cus) * per * nt * unit_ns;
+            if (eff > 1) cost += static_cast<double>(eff + 1) * static_cast<double>(m) * static_cast<double>(w.rows) * sum_ns_per_float;
+            if (best_cost < 0 || cost < best_cost) best = {eff, per, nt}, best_cost = cost;
+        }
     }
     return best;
 }
@@ -841,7 +852,7 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
     const size_t extra = m + (w.format == LARQL_Q4_K ? 4 + m * (w.cols / 32) : 0);
     if (!part || part_floats < extra) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: no workspace for the row exponents");
     F32Split sp = f32_split(w, m);
-    if (sp.splits > 1 && part_floats < sp.splits * m * w.rows + extra) sp = {1, static_cast<int>(w.cols / 256)};
+    if (sp.splits > 1 && part_floats < sp.splits * m * w.rows + extra) sp = {1, static_cast<int>(w.cols / 256), sp.nt};
     const size_t xe_at = sp.splits > 1 ? sp.splits * m * w.rows : 0;
     int* xe = reinterpret_cast<int*>(part + xe_at);
     float* xs = nullptr;
@@ -851,13 +862,19 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
     }
     row_exp_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, static_cast<int>(w.cols), xe, xs);
     LARQL_HIP_CHECK(hipGetLastError());
-    const dim3 grid(static_cast<unsigned>((w.rows + kNwg - 1) / kNwg),
+    const unsigned rows_wg = 16u * static_cast<unsigned>(sp.nt) * kWaves;
+    const dim3 grid(static_cast<unsigned>((w.rows + rows_wg - 1) / rows_wg),
                     static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)), static_cast<unsigned>(sp.splits));
     const int ld_out = static_cast<int>(sp.splits > 1 ? w.rows : ldy);
-    if (w.format == LARQL_Q4_K)
-        q4k_gemm_sq_kernel<<<grid, dim3(kThreads), 0, s>>>(
-            w.qs, reinterpret_cast<const v4u*>(w.hdr), X, xe, xs, sp.splits > 1 ? part : Y, static_cast<int>(m),
-            static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per, ld_out);
+    if (w.format == LARQL_Q4_K) {
+        auto go = [&](auto ntc) {
+            q4k_gemm_sq_kernel<decltype(ntc)::value><<<grid, dim3(kThreads), 0, s>>>(
+                w.qs, reinterpret_cast<const v4u*>(w.hdr), X, xe, xs, sp.splits > 1 ? part : Y, static_cast<int>(m),
+                static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per, ld_out);
+        };
+        if (sp.nt == 4) go(std::integral_constant<int, 4>{});
+        else go(std::integral_constant<int, kNT>{});
+    }
     else
         q6k_gemm_hp_kernel<<<grid, dim3(kThreads), 0, s>>>(
             w.qs, X, xe, sp.splits > 1 ? part : Y, static_cast<int>(m), static_cast<int>(w.rows), static_cast<int>(w.cols),
