@@ -32,6 +32,7 @@ PMC helpers (used to produce profiles/q4k_matvec_traffic.json):
   bench.py --pmc-pass knn     the Q4_0 gate-KNN walk (34 layers [10240x2560], 256 queries)
   bench.py --pmc-pass walk    the Q4_0 walk-FFN kernels over [10240x2560]
   bench.py --pmc-pass prefill [--pmc-tokens M]  the Q4_K GEMM over [10240x2560] at M tokens
+  bench.py --pmc-pass prompt [--pmc-tokens M]   M-token prompt passes through 4 layers of the 8B shape
   bench.py --pmc-report CALIB_FETCH CALIB_WRITE GATE_FETCH GATE_WRITE [--pmc-floor FLOOR_FETCH]
 """
 from __future__ import annotations
@@ -345,7 +346,7 @@ def run_decode(be, torch, stream, steps, warmup):
     torch.cuda.empty_cache()
     # the Q4_K_M mix (V and down projections in Q6_K): the same prompt through the Q6_K GEMM
     sm = build_llama(be, torch, q6k=("wv", "down"), **LLAMA3_8B)
-    prefill_km = run_prompt_prefill(torch, stream, sm)
+    prefill_km = run_prompt_prefill(torch, stream, sm, q6k=("wv", "down"))
     prefill_km["config"] = "Q4_K_M mix: wv and down in Q6_K, the rest Q4_K"
     be.kv_truncate(0)
     sm.model.close()
@@ -364,11 +365,13 @@ def run_decode(be, torch, stream, steps, warmup):
     }
 
 
-def run_prompt_prefill(torch, stream, sm, seq=512, reps=4):
+def run_prompt_prefill(torch, stream, sm, seq=512, reps=4, q6k=()):
     """A 512-token prompt through the 8B-shape model (larql_hip_model_prefill_dev: per
-    layer, f32-accuracy Q4_K GEMMs over all positions and prompt-mode attention).  The
-    GEMMs run each product as three fp16 matrix-core products (operand pairs), so their
-    matrix-core peak for these f32 flops is a third of the dense fp16 peak."""
+    layer, f32-accuracy GEMMs over all positions and prompt-mode attention).  The Q4_K
+    GEMMs issue two fp16 matrix-core products per f32 product (exact integer weight
+    operands against the token operand's fp16 pair), the Q6_K GEMMs three (both operands
+    as fp16 pairs); `gemm_mfma_frac` is the fp16 MFMA work those imply, over the pass's
+    time, against the 2.5 PFLOP/s dense fp16 peak.  q6k: the projections in Q6_K."""
     c = sm.cfg
     gen = torch.Generator(device="cuda").manual_seed(3)
     x = torch.randn(seq, c["hidden"], generator=gen, device="cuda", dtype=torch.float32)
@@ -383,13 +386,15 @@ def run_prompt_prefill(torch, stream, sm, seq=512, reps=4):
     torch.cuda.synchronize()
     ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in ev)
     h, f, q, kv = c["hidden"], c["inter"], c["nq"] * c["hd"], c["nkv"] * c["hd"]
-    gemm_flop = 2.0 * seq * c["n_layers"] * h * (q + 2 * kv + q + 2 * f) + 2.0 * seq * c["n_layers"] * f * h
+    per_layer = {"wq": h * q, "wk": h * kv, "wv": h * kv, "wo": q * h, "gate": h * f, "up": h * f, "down": f * h}
+    gemm_flop = 2.0 * seq * c["n_layers"] * sum(per_layer.values())
+    mfma_flop = 2.0 * seq * c["n_layers"] * sum(n * (3 if k in q6k else 2) for k, n in per_layer.items())
     return {
         "tokens": seq,
         "ms_median": round(ms, 3),
         "tokens_per_s": round(seq / (ms * 1e-3), 1),
         "gemm_TFLOPs": round(gemm_flop / (ms * 1e-3) / 1e12, 1),
-        "gemm_frac_of_fp16_pair_peak": round(gemm_flop / (ms * 1e-3) / (2500e12 / 3), 3),
+        "gemm_mfma_frac": round(mfma_flop / (ms * 1e-3) / 2500e12, 3),
     }
 
 
@@ -814,6 +819,19 @@ def pmc_pass(which: str, launches: int, tokens: int = 512):
         torch.cuda.synchronize()
         be.close()
         return
+    if which == "prompt":  # `launches` 512-token prompt passes through 4 layers of the 8B shape (Q4_K)
+        from larql_hip.synth import LLAMA3_8B, build_llama
+        sm = build_llama(be, torch, **dict(LLAMA3_8B, n_layers=4))
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(3)
+        x = torch.randn(tokens, sm.cfg["hidden"], generator=gen, device=dev)
+        out = torch.empty_like(x)
+        for _ in range(launches):
+            sm.model.prefill_dev(x, tokens, out, stream=stream)
+        torch.cuda.synchronize()
+        sm.model.close()
+        be.close()
+        return
     if which == "walk":  # the Q4_0 walk-FFN kernels over [10240 x 2560]: vecmat, 6-position pair batch, matvec
         N, K, copies = 10240, 2560, 8
         gen = torch.Generator(device=dev)
@@ -907,7 +925,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=1.5, help="per CPU-baseline leg (14 legs)")
     ap.add_argument("--eager", action="store_true", help="time Python-loop launches instead of a HIP graph replay")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--pmc-pass", choices=("calib", "gate", "floor", "knn", "walk", "prefill"))
+    ap.add_argument("--pmc-pass", choices=("calib", "gate", "floor", "knn", "walk", "prefill", "prompt"))
     ap.add_argument("--pmc-tokens", type=int, default=512, help="tokens of the prefill PMC pass")
     ap.add_argument("--pmc-launches", type=int, default=50)
     ap.add_argument("--pmc-report", nargs=4, metavar=("CALIB_FETCH", "CALIB_WRITE", "GATE_FETCH", "GATE_WRITE"))

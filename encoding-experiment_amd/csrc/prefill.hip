@@ -450,7 +450,8 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
                                                                const v4u* __restrict__ hdr,
                                                                const float* __restrict__ X, const int* __restrict__ xe,
                                                                const float* __restrict__ xs, float* __restrict__ Y,
-                                                               int M, int N, int K, int ntiles, int sb_per, int ldy) {
+                                                               int M, int N, int K, int ntiles, int sb_per, int ldy,
+                                                               int gx, int gy, int gz) {
     // staged X by k-step: cell [t][16 s + token] holds step s (elements 8 s .. 8 s + 7) of
     // sub-block 4h + t, hi dwords 0..3 and lo 4..7, so the k-step t operand of lane l is
     // cell [t][l] (12-dword pitch: no bank conflicts for the reads or the writes)
@@ -459,11 +460,19 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int S = K / 256;
-    const int mt0 = blockIdx.y * kMt;
-    const int nt0 = (blockIdx.x * kWaves + wave) * NT;
-    // split blockIdx.z of K: super-blocks [z sb_per, (z + 1) sb_per), partial sums to Y[z]
-    const int u0 = 2 * static_cast<int>(blockIdx.z) * sb_per, u1 = min(2 * S, u0 + 2 * sb_per), last = u1 - 1;
-    Y += static_cast<size_t>(blockIdx.z) * M * ldy;
+    // Workgroup -> (weight block bx, token block by, K split bz), a 1-D grid: the gy token
+    // blocks of one (bx, bz) get consecutive ids that are equal mod 8, i.e. one XCD (ids go
+    // round-robin over the 8) at about the same time, so a weight block is fetched into
+    // that XCD's L2 once for all tokens; ids past the gx gz pairs (rounded up to 8) exit.
+    const int L = static_cast<int>(blockIdx.x), slot = L >> 3, by = slot % gy;
+    const int grp = (slot / gy) * 8 + (L & 7);
+    if (grp >= gx * gz) return;
+    const int bx = grp % gx, bz = grp / gx;
+    const int mt0 = by * kMt;
+    const int nt0 = (bx * kWaves + wave) * NT;
+    // split bz of K: super-blocks [bz sb_per, (bz + 1) sb_per), partial sums to Y[bz]
+    const int u0 = 2 * bz * sb_per, u1 = min(2 * S, u0 + 2 * sb_per), last = u1 - 1;
+    Y += static_cast<size_t>(bz) * M * ldy;
     uint32_t qo[NT], ho[NT];
 #pragma unroll
     for (int j = 0; j < NT; j++) {
@@ -867,10 +876,12 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
                     static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)), static_cast<unsigned>(sp.splits));
     const int ld_out = static_cast<int>(sp.splits > 1 ? w.rows : ldy);
     if (w.format == LARQL_Q4_K) {
+        const unsigned pairs = grid.x * grid.z, lin = (pairs + 7) / 8 * 8 * grid.y;
         auto go = [&](auto ntc) {
-            q4k_gemm_sq_kernel<decltype(ntc)::value><<<grid, dim3(kThreads), 0, s>>>(
+            q4k_gemm_sq_kernel<decltype(ntc)::value><<<dim3(lin), dim3(kThreads), 0, s>>>(
                 w.qs, reinterpret_cast<const v4u*>(w.hdr), X, xe, xs, sp.splits > 1 ? part : Y, static_cast<int>(m),
-                static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per, ld_out);
+                static_cast<int>(w.rows), static_cast<int>(w.cols), static_cast<int>(w.rows_pad / 16), sp.sb_per, ld_out,
+                static_cast<int>(grid.x), static_cast<int>(grid.y), static_cast<int>(grid.z));
         };
         if (sp.nt == 4) go(std::integral_constant<int, 4>{});
         else go(std::integral_constant<int, kNT>{});
