@@ -419,6 +419,11 @@ __device__ __forceinline__ float hp_token_scales(const int* __restrict__ xe, int
     return ldexpf(1.0f, xe[min(xr_row, M - 1)]);
 }
 
+// Workgroup barrier for LDS only: the wave's LDS accesses complete, then s_barrier.
+// __syncthreads() is a workgroup-scope release as well, which also waits for every global
+// load in flight (vmcnt(0)) and so drains the next units' prefetches at each barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ── Q4_K prompt GEMM on exact integer weight operands ─────────────────────
 // The Q4_K form of the f32-accuracy GEMM.  A Q4_K weight is w = d s_j q - dmin m_j (q the
 // 4-bit code, s_j and m_j the 6-bit scale and 4-bit min of its 32-element sub-block j, d
@@ -480,36 +485,64 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
         qo[j] = __builtin_amdgcn_readfirstlane(t * S * 2048u);
         ho[j] = __builtin_amdgcn_readfirstlane(t * S * 256u);
     }
-    // X staging: slot l of tile r holds sub-block 4h + l / 16 of
-    // token 16 (mt0 + r) + l % 16
+    // X staging: slot l of tile r holds sub-block 4h + l / 16 of token 16 (mt0 + r) + l % 16;
+    // a token past M re-reads row M - 1 (its D rows are never stored, and MFMA rows do not
+    // mix; no branch around the loads)
     const int xr_row = (mt0 + (tid >> 6)) * 16 + (lane & 15);
-    const bool xr_ok = xr_row < M;
-    const float* xrow = X + static_cast<size_t>(min(xr_row, M - 1)) * K + 32 * g;
+    // raw buffer loads: the wave-uniform part of each offset in the scalar operand, the
+    // lane's in the vector operand (the launcher keeps X, the nibbles and the headers below
+    // 2 GiB)
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X), 0, static_cast<int>(static_cast<uint32_t>(M) * K * 4u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(qs), 0, static_cast<int>(static_cast<uint32_t>(ntiles) * S * 2048u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<v4u*>(hdr), 0, static_cast<int>(static_cast<uint32_t>(ntiles) * S * 256u), 0x00020000);
+    const uint32_t xoff = (static_cast<uint32_t>(min(xr_row, M - 1)) * K + 32u * g) * 4u;
+    const uint32_t lo16 = lane * 16u, lc16 = c * 16u;
     const float xscale = hp_token_scales(xe, M, mt0, xr_row, tok_inv);
     struct Xu {
         float4 v[8];
     };
+    // (each group of loads kept whole and in program order, so that the wait before a
+    // group's first use counts just the loads issued after it)
     auto load_x = [&](int u, Xu& x) __attribute__((always_inline)) {
-        const float4* p = reinterpret_cast<const float4*>(xrow + 256 * (u >> 1) + 128 * (u & 1));
+        const uint32_t so = static_cast<uint32_t>(u) * 512u;  // (256 (u >> 1) + 128 (u & 1)) floats
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < 8; k++) x.v[k] = xr_ok ? p[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int k = 0; k < 8; k++)
+            x.v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff + 16u * k, so, 0));
+        __builtin_amdgcn_sched_barrier(0);
     };
     auto store_x = [&](int b, const Xu& x) __attribute__((always_inline)) {
         hp_store_x<16 * kSqPitch, 4>(&Aq[b][tid >> 6][lane >> 4][lane & 15][0], x.v, xscale);
     };
+    // a unit's nibbles and the header words it uses: h = 0 (the first half of a super-block)
+    // d | dmin and the scales of sub-blocks 0..3, h = 1 the scales of 4..7
     struct Wu {
-        v4u q[NT], hd[NT];
+        v4u q[NT];
+        uint32_t hx[NT], hs[NT];
     };
     const uint8_t* hdrb = reinterpret_cast<const uint8_t*>(hdr) + c * 16;
     auto load_w = [&](int u, Wu& w) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < NT; j++) {
-            w.q[j] = __builtin_nontemporal_load(
-                reinterpret_cast<const v4u*>(qs + qo[j] + static_cast<uint32_t>(u) * 1024u) + lane);
-            w.hd[j] = *reinterpret_cast<const v4u*>(hdrb + ho[j] + static_cast<uint32_t>(u >> 1) * 256u);
+            w.q[j] = __builtin_bit_cast(
+                v4u, __builtin_amdgcn_raw_buffer_load_b128(rq, lo16, qo[j] + static_cast<uint32_t>(u) * 1024u, 2));
+            const uint32_t hso = ho[j] + static_cast<uint32_t>(u >> 1) * 256u;
+            if (u & 1) {
+                w.hs[j] = __builtin_amdgcn_raw_buffer_load_b32(rh, lc16, hso + 8u, 0);
+            } else {
+                const auto h2 = __builtin_amdgcn_raw_buffer_load_b64(rh, lc16, hso, 0);
+                w.hx[j] = h2[0];
+                w.hs[j] = h2[1];
+            }
         }
+        __builtin_amdgcn_sched_barrier(0);
     };
     floatx4 acc[NT][kMt], dp[NT][kMt];
+    float dsb[NT];  // d of the super-block in progress, per tile (row c)
 #pragma unroll
     for (int j = 0; j < NT; j++)
 #pragma unroll
@@ -528,7 +561,8 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
             const auto r01 = __builtin_amdgcn_permlane16_swap(a02[0], a13[0], false, false);
             const auto r23 = __builtin_amdgcn_permlane16_swap(a02[1], a13[1], false, false);
             n[j] = v4u{r01[0], r01[1], r23[0], r23[1]};
-            s6[j] = (h ? w.hd[j].z : w.hd[j].y) & 0x3F3F3F3Fu;
+            s6[j] = w.hs[j] & 0x3F3F3F3Fu;
+            if constexpr (h == 0) dsb[j] = h2f(w.hx[j] & 0xFFFFu);
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -563,7 +597,7 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
         if constexpr (h == 1) {  // the super-block's sum times d (row c)
 #pragma unroll
             for (int j = 0; j < NT; j++) {
-                const float d = h2f(w.hd[j].x & 0xFFFFu);
+                const float d = dsb[j];
 #pragma unroll
                 for (int i = 0; i < kMt; i++)
 #pragma unroll
@@ -581,18 +615,18 @@ __global__ __launch_bounds__(kThreads) void q4k_gemm_sq_kernel(const uint8_t* __
     load_x(u0 + 1, x1);
     load_w(u0 + 1, w1);
     store_x(0, x0);
-    __syncthreads();
+    lds_barrier();
     for (int u = u0; u < u1; u += 2) {
         store_x(1, x1);
         load_x(min(u + 2, last), x0);
         compute(0, std::integral_constant<int, 0>{}, w0);
         load_w(min(u + 2, last), w0);
-        __syncthreads();
+        lds_barrier();
         store_x(0, x0);
         load_x(min(u + 3, last), x1);
         compute(1, std::integral_constant<int, 1>{}, w1);
         load_w(min(u + 3, last), w1);
-        __syncthreads();
+        lds_barrier();
     }
 
     // min term over super-blocks [SB0, SB1), four per k-step: lane group g takes super-block
@@ -876,6 +910,9 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
                     static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)), static_cast<unsigned>(sp.splits));
     const int ld_out = static_cast<int>(sp.splits > 1 ? w.rows : ldy);
     if (w.format == LARQL_Q4_K) {
+        // (raw buffer offsets: X, the nibbles and the headers below 2 GiB)
+        if (m * w.cols * 4 > 0x7FFFFFFF || (w.rows_pad / 16) * (w.cols / 256) * 2048 > 0x7FFFFFFF)
+            fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: operands above 2 GiB");
         const unsigned pairs = grid.x * grid.z, lin = (pairs + 7) / 8 * 8 * grid.y;
         auto go = [&](auto ntc) {
             q4k_gemm_sq_kernel<decltype(ntc)::value><<<dim3(lin), dim3(kThreads), 0, s>>>(
