@@ -265,9 +265,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     v4u kA[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ks++)
-        kA[ks] = tk < klim ? *reinterpret_cast<const v4u*>(a.kc + (static_cast<size_t>(tk) * a.num_kv + kvh) * HD +
-                                                          32 * ks + 8 * g)
-                          : v4u{0u, 0u, 0u, 0u};
+    {   // (unconditional loads from a row inside the cache, then a select: no branch around
+        // the loads, so each later wait counts only the loads issued after the one it needs)
+        const v4u kv = *reinterpret_cast<const v4u*>(
+            a.kc + (static_cast<size_t>(max(min(tk, klim - 1), 0)) * a.num_kv + kvh) * HD + 32 * ks + 8 * g);
+        kA[ks] = tk < klim ? kv : v4u{0u, 0u, 0u, 0u};
+    }
     v4u vA[DTW][2];
 #pragma unroll
     for (int i = 0; i < DTW; i++) {
@@ -275,10 +278,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int ts = 0; ts < 2; ts++) {
             const int tv = t0 + 32 * ts + 8 * g;
-            vA[i][ts] = (dt < NDT && tv <= pos)
-                            ? *reinterpret_cast<const v4u*>(
-                                  a.vc + ((static_cast<size_t>(tv >> 3) * a.num_kv + kvh) * HD + 16 * dt + c) * 8)
-                            : v4u{0u, 0u, 0u, 0u};
+            const v4u vv = *reinterpret_cast<const v4u*>(
+                a.vc + ((static_cast<size_t>(min(tv, pos) >> 3) * a.num_kv + kvh) * HD + 16 * min(dt, NDT - 1) + c) * 8);
+            vA[i][ts] = (dt < NDT && tv <= pos) ? vv : v4u{0u, 0u, 0u, 0u};
         }
     }
 #pragma unroll
@@ -295,7 +297,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
             vnew[d] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vnv[u]));
         }
     }
-    __syncthreads();
+    lds_barrier();
     for (int i = tid; i < reps * HD; i += kAttnThreads) {
         const int h = i / HD, d = i - h * HD;
         q_s[i] = rope_elem(qr_s + h * HD, d, half, cs_s);
@@ -308,7 +310,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
             a.kc[(static_cast<size_t>(pos) * a.num_kv + kvh) * HD + d] = __ushort_as_half(kh);
             a.vc[((static_cast<size_t>(pos >> 3) * a.num_kv + kvh) * HD + d) * 8 + (pos & 7)] = __ushort_as_half(vnew[d]);
         }
-    __syncthreads();
+    lds_barrier();
     if (a.qk_norm) {  // unit-length query heads: one wave per head
         for (int h = wave; h < reps; h += kAttnThreads / 64) {
             float ss = 0.f;
@@ -316,7 +318,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
             const float r = 1.0f / sqrtf(wave_sum_dpp(ss) + 1e-6f);
             for (int d = lane; d < HD; d += 64) q_s[h * HD + d] *= r;
         }
-        __syncthreads();
+        lds_barrier();
     }
     // score B operands: lane (g, col) of k-step ks holds dims 32 ks + 8 g .. of column col
     for (int i = tid; i < KS * 64; i += kAttnThreads) {
@@ -357,7 +359,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // 2. Scores of positions t0 + 16 w + 4 g + r for lanes (g, col < reps).
     floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
             p_s[c][tl] = (t >= a.t_begin && t <= pos) ? sv : -INFINITY;
         }
     }
-    __syncthreads();
+    lds_barrier();
     // 3. Softmax partials of the chunk: one wave per head.
     for (int h = wave; h < reps; h += kAttnThreads / 64) {
         const float sc = p_s[h][lane];
@@ -388,7 +390,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
             ml_s[2 * h + 1] = l;
         }
     }
-    __syncthreads();
+    lds_barrier();
     // P.V B operands: lane (g, col) of position step ts holds positions 32 ts + 8 g ..
     if (tid < 2 * 64) {
         const int ts = tid >> 6, lg = (tid >> 4) & 3, col = tid & 15;
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         }
         pop[tid] = op;
     }
-    __syncthreads();
+    lds_barrier();
     // 4. Unnormalised P.V: dims 16 dt + 4 g + r for lanes (g, col < reps).
 #pragma unroll
     for (int i = 0; i < DTW; i++) {

@@ -9,6 +9,12 @@ namespace larql {
 
 // IEEE binary16 -> binary32 (exact; subnormal inputs are decoded, as the
 // reference decoders LC/src/cpu/ops/q4_common.rs:426-442 and q4_dot.c:9-35 do).
+// Workgroup barrier for data exchanged through LDS only: the wave's LDS accesses complete,
+// then s_barrier.  __syncthreads() is also a workgroup-scope release, which waits for every
+// global load in flight (vmcnt(0)): in a kernel that keeps loads in flight across its
+// barriers (prefetch, or operands used after later LDS phases) that exposes their latency.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float h2f(uint32_t bits16) {
     return __half2float(__ushort_as_half(static_cast<unsigned short>(bits16 & 0xFFFFu)));
 }

@@ -419,11 +419,6 @@ __device__ __forceinline__ float hp_token_scales(const int* __restrict__ xe, int
     return ldexpf(1.0f, xe[min(xr_row, M - 1)]);
 }
 
-// Workgroup barrier for LDS only: the wave's LDS accesses complete, then s_barrier.
-// __syncthreads() is a workgroup-scope release as well, which also waits for every global
-// load in flight (vmcnt(0)) and so drains the next units' prefetches at each barrier.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // ── Q4_K prompt GEMM on exact integer weight operands ─────────────────────
 // The Q4_K form of the f32-accuracy GEMM.  A Q4_K weight is w = d s_j q - dmin m_j (q the
 // 4-bit code, s_j and m_j the 6-bit scale and 4-bit min of its 32-element sub-block j, d
