@@ -795,9 +795,10 @@ static bool prompt_batchable(const larql_hip_model* m) {
 // One projection of all M positions (X rows ldx = w.cols apart) -> Y rows ldy apart: the
 // f32-accuracy GEMM, Q4_K or Q6_K.
 static void prompt_proj(const larql::DevWeight& w, const float* X, size_t ldx, float* Y, size_t ldy, size_t M,
-                        float* spl, size_t split_n, hipStream_t s) {
+                        float* spl, size_t split_n, hipStream_t s, const larql::GemmRowStats* pre = nullptr,
+                        larql::GemmSplits* defer = nullptr) {
     if (ldx != w.cols) fail(LARQL_HIP_ERR_INVALID, "prompt pass: input rows do not match the weight");
-    larql::launch_q4k_gemm_f32(w, X, Y, M, spl, split_n, s, ldy);
+    larql::launch_q4k_gemm_f32(w, X, Y, M, spl, split_n, s, ldy, pre, defer);
 }
 
 static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, size_t M, float* dout, hipStream_t s,
@@ -817,22 +818,34 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
         else need(L.qkv);
         need(L.wo), need(L.gateup), need(L.down);
     }
-    const size_t n_f = 2 * M * hidden + M * wide + M * ldmax + M * qmax + M * gw + M * inter + part_n + split_n;
+    // row statistics of the normed hidden rows and of the activation rows, computed by the
+    // kernels that produce those rows (two separate regions: a producer may still read
+    // the previous GEMM's partial products in SPL)
+    const size_t st_h = larql::gemm_row_stats_floats(M, hidden), st_a = larql::gemm_row_stats_floats(M, inter);
+    const size_t n_f = 2 * M * hidden + M * wide + M * ldmax + M * qmax + M * gw + M * inter + part_n + split_n +
+                       st_h + st_a + 8;
     float* base = static_cast<float*>(larql::ensure(c, m->prompt, n_f * sizeof(float)));
     float *H0 = base, *H1 = H0 + M * hidden, *XN = H1 + M * hidden, *QKV = XN + M * wide, *ATT = QKV + M * ldmax;
     float *G = ATT + M * qmax, *ACT = G + M * gw, *PART = ACT + M * inter, *SPL = PART + part_n;
+    const larql::GemmRowStats xn_st = larql::gemm_row_stats_at(SPL + split_n, M, hidden);
+    const larql::GemmRowStats act_st = larql::gemm_row_stats_at(SPL + split_n + st_h + 4, M, inter);
     larql::launch_copy_f32(dx, H0, M * hidden, s);
+    bool xn_ready = false;  // XN holds this layer's normed input and xn_st its statistics
     for (size_t l = 0; l < m->layers.size(); l++) {
         const LayerDev& L = m->layers[l];
         // this layer's [q | k | v] rows, ld floats apart, and attention rows qd apart
         const size_t qd = static_cast<size_t>(L.nq) * L.hd, kvd = static_cast<size_t>(L.nkv) * L.hd, ld = qd + 2 * kvd;
-        larql::launch_rmsnorm_rows(H0, L.input_norm, L.norm_offset, XN, M, hidden, L.eps, s);
+        if (!xn_ready) {
+            larql::launch_rmsnorm_rows(H0, L.input_norm, L.norm_offset, XN, M, hidden, L.eps, s);
+            larql::launch_gemm_row_stats(XN, M, hidden, xn_st, s);
+        }
+        xn_ready = false;
         if (L.split_qkv) {  // Q, K, V into their column ranges of the [q | k | v] rows
-            prompt_proj(L.wq, XN, hidden, QKV, ld, M, SPL, split_n, s);
-            prompt_proj(L.wk, XN, hidden, QKV + qd, ld, M, SPL, split_n, s);
-            prompt_proj(L.wv, XN, hidden, QKV + qd + kvd, ld, M, SPL, split_n, s);
+            prompt_proj(L.wq, XN, hidden, QKV, ld, M, SPL, split_n, s, &xn_st);
+            prompt_proj(L.wk, XN, hidden, QKV + qd, ld, M, SPL, split_n, s, &xn_st);
+            prompt_proj(L.wv, XN, hidden, QKV + qd + kvd, ld, M, SPL, split_n, s, &xn_st);
         } else {
-            prompt_proj(L.qkv, XN, hidden, QKV, ld, M, SPL, split_n, s);
+            prompt_proj(L.qkv, XN, hidden, QKV, ld, M, SPL, split_n, s, &xn_st);
         }
         if (L.v_norm) larql::launch_vnorm_rows(QKV + qd + kvd, M, ld, L.nkv, L.hd, L.eps, s);
         const float2* rope = rope_table(c, L.rope_base, L.rdim, s);
@@ -856,22 +869,31 @@ static void run_prompt(larql_hip_ctx* c, larql_hip_model* m, const float* dx, si
         at.qk_norm = pa.qk_norm;
         at.softcap = pa.softcap;
         larql::launch_attention(at, s);
-        prompt_proj(L.wo, ATT, qd, G, hidden, M, SPL, split_n, s);
-        if (L.post_norms) {
+        const float scale = L.layer_scalar != 0.0f ? L.layer_scalar : 1.0f;
+        if (L.post_norms || hidden > larql::kFusedRowMax || inter > larql::kFusedRowMax) {
+            prompt_proj(L.wo, ATT, qd, G, hidden, M, SPL, split_n, s);
             larql::launch_resid_norm_rows(H0, G, L.post_attn_norm, L.norm_offset, 1.0f, H1, M, hidden, L.eps, s);
             larql::launch_rmsnorm_rows(H1, L.pre_ffn_norm, L.norm_offset, XN, M, hidden, L.eps, s);
-        } else {
-            larql::launch_add_rows(H0, G, H1, M * hidden, s);
-            larql::launch_rmsnorm_rows(H1, L.post_attn_norm, L.norm_offset, XN, M, hidden, L.eps, s);
-        }
-        prompt_proj(L.gateup, XN, hidden, G, 2 * inter, M, SPL, split_n, s);
-        larql::launch_gated_pair_rows(G, ACT, M * inter, L.act, s);
-        prompt_proj(L.down, ACT, inter, G, hidden, M, SPL, split_n, s);
-        const float scale = L.layer_scalar != 0.0f ? L.layer_scalar : 1.0f;
-        if (L.post_norms)
+            prompt_proj(L.gateup, XN, hidden, G, 2 * inter, M, SPL, split_n, s);
+            larql::launch_gated_pair_rows(G, ACT, M * inter, L.act, s);
+            prompt_proj(L.down, ACT, inter, G, hidden, M, SPL, split_n, s);
             larql::launch_resid_norm_rows(H1, G, L.post_ffn_norm, L.norm_offset, scale, H0, M, hidden, L.eps, s);
-        else
-            larql::launch_add_rows(H1, G, H0, M * hidden, s, scale);
+            continue;
+        }
+        // the split sums of wo and down, the residual adds, the next norm and the row
+        // statistics of the next GEMM's input: one row kernel after each projection
+        larql::GemmSplits sp{};
+        prompt_proj(L.wo, ATT, qd, G, hidden, M, SPL, split_n, s, nullptr, &sp);
+        larql::launch_resid_norm_stats_rows(sp.splits > 1 ? sp.part : G, M * hidden, sp.splits, H0, 1.0f, H1,
+                                            L.post_attn_norm, L.norm_offset, XN, M, hidden, L.eps, xn_st, s);
+        prompt_proj(L.gateup, XN, hidden, G, 2 * inter, M, SPL, split_n, s, &xn_st);
+        larql::launch_gated_pair_stats_rows(G, ACT, M, inter, L.act, act_st, s);
+        prompt_proj(L.down, ACT, inter, G, hidden, M, SPL, split_n, s, &act_st, &sp);
+        const LayerDev* nx = l + 1 < m->layers.size() ? &m->layers[l + 1] : nullptr;
+        larql::launch_resid_norm_stats_rows(sp.splits > 1 ? sp.part : G, M * hidden, sp.splits, H1, scale, H0,
+                                            nx ? nx->input_norm : nullptr, nx ? nx->norm_offset : 0.0f,
+                                            nx ? XN : nullptr, M, hidden, nx ? nx->eps : 0.0, xn_st, s);
+        xn_ready = nx != nullptr;
     }
     larql::launch_copy_f32(H0, dout, M * hidden, s);
     kv.current_len = M;

@@ -65,6 +65,18 @@ void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipSt
 void launch_gated_mul(const float* G, const float* U, float* act, size_t n, int kind, hipStream_t s);
 // act[i] = act(GU[2i]) * GU[2i + 1]; kind 0 = SiLU, 1 = GELU-tanh.
 void launch_gated_pair_rows(const float* GU, float* act, size_t n, int kind, hipStream_t s);
+// Fused forms of the prompt pass, per row of n floats (n a multiple of 32, at most
+// kFusedRowMax: the row is held in LDS), each value
+// as the separate kernels compute it: hout = (hin + the projection row, its `splits`
+// partial products summed in split order, pstride floats apart) * scale; then, with xn,
+// xn = hout / rms(hout) * (off + w) and xn's GEMM row statistics into st.
+constexpr int kFusedRowMax = 16384;
+void launch_resid_norm_stats_rows(const float* P, size_t pstride, int splits, const float* hin, float scale,
+                                  float* hout, const float* w, float off, float* xn, size_t m, size_t n, double eps,
+                                  const GemmRowStats& st, hipStream_t s);
+// act rows (m x n) as launch_gated_pair_rows, with their GEMM row statistics into st.
+void launch_gated_pair_stats_rows(const float* GU, float* act, size_t m, size_t n, int kind, const GemmRowStats& st,
+                                  hipStream_t s);
 void launch_f32_to_f16(const float* src, __half* dst, size_t n, hipStream_t s);
 
 }  // namespace larql

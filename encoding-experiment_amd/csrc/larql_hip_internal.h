@@ -264,10 +264,29 @@ void launch_q4k_gemm(const DevWeight& w, const float* X, float* Y, size_t m, voi
 // q4k_gemm_f32_part_floats): the m row exponents, and the partial products when small
 // grids split K over up to four workgroups per tile (summed in split order).
 size_t q4k_gemm_f32_part_floats(const DevWeight& w, size_t m);
+// Row statistics of an f32-accuracy GEMM input (row exponents; the scaled sub-block sums
+// that Q4_K weights use, m x cols / 32 floats from a 16-byte boundary), computed by a
+// caller that fuses them into the kernel producing the input: the floats of workspace
+// for m rows of `cols`, their place in it, and the standalone computation.
+struct GemmRowStats {
+    int* xe;
+    float* xs;
+};
+size_t gemm_row_stats_floats(size_t m, size_t cols);
+GemmRowStats gemm_row_stats_at(float* ws, size_t m, size_t cols);
+void launch_gemm_row_stats(const float* X, size_t m, size_t cols, const GemmRowStats& st, hipStream_t s);
+// K-split partial products left to the caller to sum in split order (splits 1: part null,
+// Y was written): split z of row r at part + (z m + r) rows.
+struct GemmSplits {
+    const float* part;
+    int splits;
+};
 // Q4_K or Q6_K weights.  Y rows are ldy floats apart (0: w.rows), so a projection can
-// fill a column slice.
+// fill a column slice.  pre: X's row statistics, already computed (for Q4_K weights with
+// the sub-block sums).  defer: leave the split partial products unsummed (ldy = w.rows).
 void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, float* part, size_t part_floats,
-                         hipStream_t s, size_t ldy = 0);
+                         hipStream_t s, size_t ldy = 0, const GemmRowStats* pre = nullptr,
+                         GemmSplits* defer = nullptr);
 void launch_q4_0_matvec(const DevWeight& w, const int8_t* q8x, const float* q8s, float* out,
                         size_t m, hipStream_t s);
 // Two Q4_0 matrices of one shape times the same Q8 rows, in one launch per pass.

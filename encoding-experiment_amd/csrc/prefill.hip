@@ -368,45 +368,12 @@ __device__ __forceinline__ void hp3_mfma(floatx4 (&acc)[MT], const v4u (&ah)[MT]
     for (int i = 0; i < MT; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, al[i]), Bh, acc[i], 0, 0, 0);
 }
 
-// e[row] = the power of two that puts max |X[row]| in [2^14, 2^15) (0 for a row of zeros
-// or a non-finite maximum).  With xs, also xs[row][j] = 2^(e - 5) times the sum of the 32
-// elements of sub-block j, summed in f64 and rounded once (|xs| < 2^15).  One workgroup per
-// row; K a multiple of 4 (of 32 with xs).
+// One workgroup per row: the row's exponent and (with xs) scaled sub-block sums
+// (gemm_row_stats).
 __global__ __launch_bounds__(256) void row_exp_kernel(const float* __restrict__ X, int K, int* __restrict__ e,
                                                       float* __restrict__ xs) {
-    __shared__ float wm[4];
-    __shared__ int es;
-    const float* row = X + static_cast<size_t>(blockIdx.x) * K;
-    float m = 0.f;
-    for (int i = 4 * static_cast<int>(threadIdx.x); i < K; i += 4 * 256) {
-        const float4 v = *reinterpret_cast<const float4*>(row + i);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-        const int ev = (m > 0.f && m <= 3.4e38f) ? min(120, max(-120, 14 - ilogbf(m))) : 0;
-        e[blockIdx.x] = ev;
-        es = ev;
-    }
-    if (!xs) return;  // (uniform)
-    __syncthreads();
-    const double sc = ldexp(1.0, es - 5);
-    const int nsb = K / 32;
-    for (int j = static_cast<int>(threadIdx.x); j < nsb; j += 256) {
-        const float4* p = reinterpret_cast<const float4*>(row + 32 * j);
-        double sum[2] = {0.0, 0.0};  // f64: the sum is rounded once, to f32
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float4 v = p[k];
-            sum[k & 1] += (static_cast<double>(v.x) + static_cast<double>(v.y)) +
-                          (static_cast<double>(v.z) + static_cast<double>(v.w));
-        }
-        xs[static_cast<size_t>(blockIdx.x) * nsb + j] = static_cast<float>((sum[0] + sum[1]) * sc);
-    }
+    gemm_row_stats(X + static_cast<size_t>(blockIdx.x) * K, K, e + blockIdx.x,
+                   xs ? xs + static_cast<size_t>(blockIdx.x) * (K / 32) : nullptr);
 }
 
 // The staging thread's token scale and the workgroup's per-token inverses (the first 64
@@ -878,28 +845,52 @@ size_t q4k_gemm_f32_part_floats(const DevWeight& w, size_t m) {
     return (sp.splits > 1 ? sp.splits * m * w.rows : 0) + m + (w.format == LARQL_Q4_K ? 4 + m * (w.cols / 32) : 0);
 }
 
+size_t gemm_row_stats_floats(size_t m, size_t cols) { return m + 4 + m * (cols / 32); }
+
+GemmRowStats gemm_row_stats_at(float* ws, size_t m, size_t /*cols*/) {
+    // the exponents, then the sub-block sums from a 16-byte boundary (float4 reads)
+    const uintptr_t at = reinterpret_cast<uintptr_t>(ws + m);
+    return {reinterpret_cast<int*>(ws), reinterpret_cast<float*>((at + 15) & ~uintptr_t{15})};
+}
+
+void launch_gemm_row_stats(const float* X, size_t m, size_t cols, const GemmRowStats& st, hipStream_t s) {
+    if (m == 0) return;
+    if (cols % 32 != 0 || cols > 0x7FFFFFFF) fail(LARQL_HIP_ERR_INVALID, "GEMM row statistics: cols must be a multiple of 32");
+    row_exp_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, static_cast<int>(cols), st.xe, st.xs);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
 void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m, float* part, size_t part_floats,
-                         hipStream_t s, size_t ldy) {
+                         hipStream_t s, size_t ldy, const GemmRowStats* pre, GemmSplits* defer) {
     if (ldy == 0) ldy = w.rows;
     if (ldy < w.rows || ldy > 0x7FFFFFFF) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: bad output row stride");
+    if (defer && ldy != w.rows) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: deferred split sums need dense output rows");
     if (w.format != LARQL_Q4_K && w.format != LARQL_Q6_K)
         fail(LARQL_HIP_ERR_UNSUPPORTED, "prefill GEMM: Q4_K or Q6_K weights only");
+    if (pre && (!pre->xe || (w.format == LARQL_Q4_K && !pre->xs)))
+        fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: incomplete row statistics");
     if (m == 0) return;
     if (m > 0x7FFFFFFF / w.cols) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: too many tokens");
-    // row exponents, then for Q4_K the sub-block sums from a 16-byte boundary (float4 reads)
-    const size_t extra = m + (w.format == LARQL_Q4_K ? 4 + m * (w.cols / 32) : 0);
-    if (!part || part_floats < extra) fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: no workspace for the row exponents");
+    // row exponents, then for Q4_K the sub-block sums from a 16-byte boundary (float4 reads),
+    // unless the caller computed them
+    const size_t extra = pre ? 0 : m + (w.format == LARQL_Q4_K ? 4 + m * (w.cols / 32) : 0);
+    if (extra && (!part || part_floats < extra))
+        fail(LARQL_HIP_ERR_INVALID, "prefill GEMM: no workspace for the row exponents");
     F32Split sp = f32_split(w, m);
-    if (sp.splits > 1 && part_floats < sp.splits * m * w.rows + extra) sp = {1, static_cast<int>(w.cols / 256), sp.nt};
+    if (sp.splits > 1 && (!part || part_floats < sp.splits * m * w.rows + extra))
+        sp = {1, static_cast<int>(w.cols / 256), sp.nt};
     const size_t xe_at = sp.splits > 1 ? sp.splits * m * w.rows : 0;
-    int* xe = reinterpret_cast<int*>(part + xe_at);
-    float* xs = nullptr;
-    if (w.format == LARQL_Q4_K) {
-        const uintptr_t at = reinterpret_cast<uintptr_t>(part + xe_at + m);
-        xs = reinterpret_cast<float*>((at + 15) & ~uintptr_t{15});
+    GemmRowStats st;
+    if (pre) {
+        st = {pre->xe, w.format == LARQL_Q4_K ? pre->xs : nullptr};
+    } else {
+        st = gemm_row_stats_at(part + xe_at, m, w.cols);
+        if (w.format != LARQL_Q4_K) st.xs = nullptr;
+        row_exp_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, static_cast<int>(w.cols), st.xe, st.xs);
+        LARQL_HIP_CHECK(hipGetLastError());
     }
-    row_exp_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(X, static_cast<int>(w.cols), xe, xs);
-    LARQL_HIP_CHECK(hipGetLastError());
+    const int* xe = st.xe;
+    const float* xs = st.xs;
     const unsigned rows_wg = 16u * static_cast<unsigned>(sp.nt) * kWaves;
     const dim3 grid(static_cast<unsigned>((w.rows + rows_wg - 1) / rows_wg),
                     static_cast<unsigned>((m + 16 * kMt - 1) / (16 * kMt)), static_cast<unsigned>(sp.splits));
@@ -923,7 +914,8 @@ void launch_q4k_gemm_f32(const DevWeight& w, const float* X, float* Y, size_t m,
             w.qs, X, xe, sp.splits > 1 ? part : Y, static_cast<int>(m), static_cast<int>(w.rows), static_cast<int>(w.cols),
             sp.sb_per, ld_out);
     LARQL_HIP_CHECK(hipGetLastError());
-    if (sp.splits > 1) {
+    if (defer) *defer = {sp.splits > 1 ? part : nullptr, sp.splits};
+    if (sp.splits > 1 && !defer) {
         const size_t n = m * w.rows;
         sum_splits_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(
             part, Y, n, sp.splits, static_cast<int>(w.rows), static_cast<int>(ldy));

@@ -110,6 +110,140 @@ __global__ void gated_mul_kernel(const float* __restrict__ G, const float* __res
     if (i < n) act[i] = gated_act(kind, G[i], U[i]);
 }
 
+// ── Fused row kernels of the prompt pass ─────────────────────────────────
+// One workgroup per row; the row stays in LDS (kFusedRowMax floats at most) between the
+// steps, and each thread's loads of a chunk are issued together (indices clamped into
+// the row, so no load sits under a branch), so a row costs one round trip to memory per
+// chunk and two workgroup barriers instead of a dependent load per element.
+constexpr int kRowChunk = 16;  // elements per thread per chunk
+
+// The row's exponent (every thread gets it; thread 0 stores it) and, with xs, its scaled
+// sub-block sums from the row in LDS: the arithmetic of gemm_row_stats, whose maximum is
+// order-free and whose sums run per sub-block in one thread.  m: this thread's max |x|;
+// wm: one float per wave.
+template <int NT>
+__device__ __forceinline__ void lds_row_stats(const float* row, int n, float m, float* wm, int* __restrict__ e,
+                                              float* __restrict__ xs) {
+    const int t = threadIdx.x;
+    m = wave_max(m);
+    if ((t & 63) == 0) wm[t >> 6] = m;
+    __syncthreads();
+    m = wm[0];
+#pragma unroll
+    for (int k = 1; k < NT / 64; k++) m = fmaxf(m, wm[k]);
+    const int ev = (m > 0.f && m <= 3.4e38f) ? min(120, max(-120, 14 - ilogbf(m))) : 0;
+    if (t == 0) *e = ev;
+    if (!xs) return;
+    const double sc = ldexp(1.0, ev - 5);
+    for (int j = t; j < n / 32; j += NT) {
+        const float4* p = reinterpret_cast<const float4*>(row + 32 * j);
+        double sum[2] = {0.0, 0.0};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 v = p[k];
+            sum[k & 1] += (static_cast<double>(v.x) + static_cast<double>(v.y)) +
+                          (static_cast<double>(v.z) + static_cast<double>(v.w));
+        }
+        xs[j] = static_cast<float>((sum[0] + sum[1]) * sc);
+    }
+}
+
+// Grid M rows; 256 threads.  The residual step after a projection and the next
+// projection's input, per row of n floats, in the arithmetic of the separate kernels:
+//   y = the projection row, its `splits` partial products summed in split order (split z
+//       at P + z pstride; splits 1: P is the row itself)             (sum_splits_kernel);
+//   hout = (hin + y) * scale                                          (add_rows_kernel);
+//   and with xn: xn = (hout * (1 / rms(hout))) * (off + w)            (rmsnorm_rows_kernel,
+//   the f64 sum of squares over the same 256 threads, element i in thread i % 256, in the
+//   same order) with its row statistics for the next GEMM             (gemm_row_stats).
+__global__ __launch_bounds__(256) void resid_norm_stats_rows_kernel(
+    const float* __restrict__ P, size_t pstride, int splits, const float* __restrict__ hin, float scale,
+    float* __restrict__ hout, const float* __restrict__ w, float off, float* __restrict__ xn, int n, double eps,
+    int* __restrict__ xe, float* __restrict__ xs) {
+    __shared__ __align__(16) float row[kFusedRowMax];
+    __shared__ double red[4];
+    __shared__ float wm[4];
+    const int t = threadIdx.x;
+    const size_t r = static_cast<size_t>(blockIdx.x) * n;
+    double ss = 0.0;
+    for (int c0 = 0; c0 < n; c0 += 256 * kRowChunk) {
+        float a[kRowChunk], h[kRowChunk];
+#pragma unroll
+        for (int q = 0; q < kRowChunk; q++) {
+            const size_t i = r + min(c0 + t + 256 * q, n - 1);
+            a[q] = P[i];
+            h[q] = hin[i];
+        }
+        for (int z = 1; z < splits; z++) {
+#pragma unroll
+            for (int q = 0; q < kRowChunk; q++) a[q] += P[z * pstride + r + min(c0 + t + 256 * q, n - 1)];
+        }
+#pragma unroll
+        for (int q = 0; q < kRowChunk; q++) {
+            const int i = c0 + t + 256 * q;
+            if (i < n) {
+                const float hv = (h[q] + a[q]) * scale;
+                hout[r + i] = hv;
+                row[i] = hv;
+                ss += static_cast<double>(hv) * hv;
+            }
+        }
+    }
+    if (!xn) return;  // (uniform)
+    ss = wave_sum_d(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / static_cast<float>(sqrt(tot / static_cast<double>(n) + eps));
+    float m = 0.f;
+    for (int c0 = 0; c0 < n; c0 += 256 * kRowChunk) {
+        float wv[kRowChunk];
+#pragma unroll
+        for (int q = 0; q < kRowChunk; q++) wv[q] = w ? w[min(c0 + t + 256 * q, n - 1)] : 0.f;
+#pragma unroll
+        for (int q = 0; q < kRowChunk; q++) {
+            const int i = c0 + t + 256 * q;
+            if (i < n) {  // (the thread's own elements of `row`: no barrier needed)
+                const float x = w ? (row[i] * inv) * (off + wv[q]) : row[i] * inv;
+                xn[r + i] = x;
+                row[i] = x;
+                m = fmaxf(m, fabsf(x));
+            }
+        }
+    }
+    lds_row_stats<256>(row, n, m, wm, xe + blockIdx.x, xs ? xs + static_cast<size_t>(blockIdx.x) * (n / 32) : nullptr);
+}
+
+// Grid M rows; 1024 threads.  act = act(gate) * up over a row of n outputs from the
+// gate/up row (pairs interleaved, as gated_pair_rows_kernel), with act's row statistics
+// for the down GEMM.
+__global__ __launch_bounds__(1024) void gated_pair_stats_rows_kernel(const float* __restrict__ GU,
+                                                                     float* __restrict__ act, int n, int kind,
+                                                                     int* __restrict__ xe, float* __restrict__ xs) {
+    __shared__ __align__(16) float row[kFusedRowMax];
+    __shared__ float wm[16];
+    const int t = threadIdx.x;
+    const size_t r = static_cast<size_t>(blockIdx.x) * n;
+    const float2* gu = reinterpret_cast<const float2*>(GU) + r;
+    float m = 0.f;
+    for (int c0 = 0; c0 < n; c0 += 1024 * kRowChunk) {
+        float2 v[kRowChunk];
+#pragma unroll
+        for (int q = 0; q < kRowChunk; q++) v[q] = gu[min(c0 + t + 1024 * q, n - 1)];
+#pragma unroll
+        for (int q = 0; q < kRowChunk; q++) {
+            const int i = c0 + t + 1024 * q;
+            if (i < n) {
+                const float a = gated_act(kind, v[q].x, v[q].y);
+                act[r + i] = a;
+                row[i] = a;
+                m = fmaxf(m, fabsf(a));
+            }
+        }
+    }
+    lds_row_stats<1024>(row, n, m, wm, xe + blockIdx.x, xs ? xs + static_cast<size_t>(blockIdx.x) * (n / 32) : nullptr);
+}
+
 unsigned blocks(size_t n) { return static_cast<unsigned>((n + 255) / 256); }
 
 }  // namespace
@@ -155,6 +289,27 @@ void launch_add_rows(const float* a, const float* b, float* out, size_t n, hipSt
 void launch_gated_mul(const float* G, const float* U, float* act, size_t n, int kind, hipStream_t s) {
     if (n == 0) return;
     gated_mul_kernel<<<dim3(blocks(n)), dim3(256), 0, s>>>(G, U, act, n, kind);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_resid_norm_stats_rows(const float* P, size_t pstride, int splits, const float* hin, float scale,
+                                  float* hout, const float* w, float off, float* xn, size_t m, size_t n, double eps,
+                                  const GemmRowStats& st, hipStream_t s) {
+    if (m == 0) return;
+    if (splits < 1 || n % 32 != 0 || n > static_cast<size_t>(kFusedRowMax) || (xn && !st.xe))
+        fail(LARQL_HIP_ERR_INVALID, "fused residual and norm rows: bad arguments");
+    resid_norm_stats_rows_kernel<<<dim3(static_cast<unsigned>(m)), dim3(256), 0, s>>>(
+        P, pstride, splits, hin, scale, hout, w, off, xn, static_cast<int>(n), eps, st.xe, st.xs);
+    LARQL_HIP_CHECK(hipGetLastError());
+}
+
+void launch_gated_pair_stats_rows(const float* GU, float* act, size_t m, size_t n, int kind, const GemmRowStats& st,
+                                  hipStream_t s) {
+    if (m == 0) return;
+    if (n % 32 != 0 || n > static_cast<size_t>(kFusedRowMax) || !st.xe)
+        fail(LARQL_HIP_ERR_INVALID, "fused gated rows: bad arguments");
+    gated_pair_stats_rows_kernel<<<dim3(static_cast<unsigned>(m)), dim3(1024), 0, s>>>(GU, act, static_cast<int>(n),
+                                                                                       kind, st.xe, st.xs);
     LARQL_HIP_CHECK(hipGetLastError());
 }
 
