@@ -482,17 +482,40 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prompt_kernel(AttnArgs a) {
     const int pos_c = a.T - 1 + qc;                          // column c's position
     const int tb_c = (a.window > 0 && pos_c + 1 > a.window) ? pos_c + 1 - a.window : 0;
 
-    // 1. The wave's query rows (raw), RoPE'd per lane for its dims, QK-normed, split.
-    for (int i = lane; i < 16 * HD; i += 64) {
-        const int col = i / HD, d = i - col * HD, q = q_first + col / reps;
-        qraw[wave][col][d] = (col < qpw * reps && q <= q_last)
-                                 ? a.qkv[static_cast<size_t>(q) * a.qkv_ld + static_cast<size_t>(kvh * reps + col % reps) * HD + d]
-                                 : 0.f;
+    // 1. The wave's query rows (raw), RoPE'd per lane for its dims, QK-normed, split.  All
+    // of a lane's loads are issued before the first is used (rows clamped into the batch,
+    // then zeros selected for columns without a query), not one round trip each.
+    {
+        constexpr int QL = 16 * HD / 64;
+        float qt[QL];
+#pragma unroll
+        for (int k = 0; k < QL; k++) {
+            const int i = lane + 64 * k, col = i / HD, d = i - col * HD;
+            const int q = max(0, min(q_first + col / reps, a.batch - 1));
+            qt[k] = a.qkv[static_cast<size_t>(q) * a.qkv_ld + static_cast<size_t>(kvh * reps + col % reps) * HD + d];
+        }
+#pragma unroll
+        for (int k = 0; k < QL; k++) {
+            const int i = lane + 64 * k, col = i / HD, d = i - col * HD, q = q_first + col / reps;
+            qraw[wave][col][d] = (col < qpw * reps && q <= q_last) ? qt[k] : 0.f;
+        }
     }
     __syncthreads();
     float qv[KS][8];
     {
+        // the (cos, sin) pair of each of the lane's dims, loaded together (dims past the
+        // rotated ones read pair 0 and do not use it; no table when nothing rotates)
         const float2* cs = a.rope + static_cast<size_t>(col_ok ? pos_c : 0) * half;
+        float2 csv[KS][8];
+        if (half > 0) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int d = 32 * ks + 8 * g + e;
+                    csv[ks][e] = cs[d < half ? d : (d < 2 * half ? d - half : 0)];
+                }
+        }
         float ss = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++)
@@ -500,8 +523,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prompt_kernel(AttnArgs a) {
             for (int e = 0; e < 8; e++) {
                 const int d = 32 * ks + 8 * g + e;
                 const float* x = qraw[wave][c];
-                const float v = d < half ? x[d] * cs[d].x - x[d + half] * cs[d].y
-                                         : (d < 2 * half ? x[d - half] * cs[d - half].y + x[d] * cs[d - half].x : x[d]);
+                const float2 p = csv[ks][e];
+                const float v = d < half ? x[d] * p.x - x[d + half] * p.y
+                                         : (d < 2 * half ? x[d - half] * p.y + x[d] * p.x : x[d]);
                 qv[ks][e] = v;
                 ss += v * v;
             }
@@ -534,25 +558,26 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prompt_kernel(AttnArgs a) {
         for (int kb = t_lo; kb <= pos_hi; kb += kPaBlock) {
             // every K and V load of the block issued together, the K tiles first (loads
             // return in order): A operand lane (g, c) of tile kt = position kb + 16 kt + c,
-            // dims 32 ks + 8 g ..; of V = dim 16 dt + c, positions kb + 32 ts + 8 g ..
+            // dims 32 ks + 8 g ..; of V = dim 16 dt + c, positions kb + 32 ts + 8 g ..  Rows
+            // past pos_hi read row pos_hi instead, unconditionally, so no load sits under a
+            // branch: their scores are masked below and their V runs replaced by zeros.
             v4u ka[4][KS], vb[NDT][2];
 #pragma unroll
             for (int kt = 0; kt < 4; kt++) {
-                const int tk = kb + 16 * kt + c;
+                const int tk = min(kb + 16 * kt + c, pos_hi);
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++)
-                    ka[kt][ks] = tk <= pos_hi ? *reinterpret_cast<const v4u*>(a.kc + (static_cast<size_t>(tk) * a.num_kv + kvh) * HD +
-                                                                              32 * ks + 8 * g)
-                                              : v4u{0u, 0u, 0u, 0u};
+                    ka[kt][ks] = *reinterpret_cast<const v4u*>(a.kc + (static_cast<size_t>(tk) * a.num_kv + kvh) * HD +
+                                                               32 * ks + 8 * g);
             }
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
                 for (int ts = 0; ts < 2; ts++) {
                     const int tv = kb + 32 * ts + 8 * g;
-                    vb[dt][ts] = tv <= pos_hi ? *reinterpret_cast<const v4u*>(
-                                                    a.vc + ((static_cast<size_t>(tv >> 3) * a.num_kv + kvh) * HD + 16 * dt + c) * 8)
-                                              : v4u{0u, 0u, 0u, 0u};
+                    const v4u v = *reinterpret_cast<const v4u*>(
+                        a.vc + ((static_cast<size_t>(min(tv, pos_hi) >> 3) * a.num_kv + kvh) * HD + 16 * dt + c) * 8);
+                    vb[dt][ts] = tv <= pos_hi ? v : v4u{0u, 0u, 0u, 0u};
                 }
             // scores of 4 tiles of 16 positions: lane (g, c) holds positions kb + 16 kt + 4 g + r
             float sv[4][4];
