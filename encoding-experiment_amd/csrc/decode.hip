@@ -143,22 +143,33 @@ __device__ __forceinline__ void attn_merge_heads(const float* __restrict__ base,
     constexpr int H2 = HD / 2, PF = 34;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nout = nh * H2;  // float2 outputs
+    // the first (m, l) pair of each thread first: loads complete in order, so storing it
+    // to LDS then waits for it alone, not for the prefetch behind it
+    const int nk = nh * S, k0 = min(tid, nk - 1);
+    const float2 ml0 = [&] {
+        const int h = k0 / S, s = k0 - h * S;
+        return *reinterpret_cast<const float2*>(base + (static_cast<size_t>(h) * sst + s) * pst + mlo);
+    }();
+    __builtin_amdgcn_sched_barrier(0);
     float2 ov[PF];
     {
-        const int h = tid / H2, d = 2 * (tid - h * H2);
+        // unconditional loads (thread and split clamped into range; a load under a
+        // condition becomes a branch, and the loads would then wait one by one): threads
+        // past nout and splits past S load data they do not use
+        const int t = min(tid, nout - 1), h = t / H2, d = 2 * (t - h * H2);
         const float* src = base + static_cast<size_t>(h) * sst * pst + d;
 #pragma unroll
-        for (int u = 0; u < PF; u++)
-            ov[u] = tid < nout && u < S ? *reinterpret_cast<const float2*>(src + static_cast<size_t>(u) * pst)
-                                        : make_float2(0.f, 0.f);
+        for (int u = 0; u < PF; u++) ov[u] = *reinterpret_cast<const float2*>(src + static_cast<size_t>(min(u, S - 1)) * pst);
     }
-    for (int k = tid; k < nh * S; k += kAttnThreads) {
+    ml[2 * k0] = ml0.x;  // (threads past nk write pair nk - 1's value again)
+    ml[2 * k0 + 1] = ml0.y;
+    for (int k = tid + kAttnThreads; k < nk; k += kAttnThreads) {
         const int h = k / S, s = k - h * S;
         const float2 v = *reinterpret_cast<const float2*>(base + (static_cast<size_t>(h) * sst + s) * pst + mlo);
         ml[2 * k] = v.x;
         ml[2 * k + 1] = v.y;
     }
-    __syncthreads();
+    lds_barrier();
     for (int h = wave; h < nh; h += kAttnThreads / 64) {  // one wave per head
         float mx = -INFINITY;
         for (int s = lane; s < S; s += 64) mx = fmaxf(mx, ml[2 * (h * S + s)]);
@@ -172,7 +183,7 @@ __device__ __forceinline__ void attn_merge_heads(const float* __restrict__ base,
         L = wave_sum_dpp(L);
         if (lane == 0) inv_l[h] = 1.0f / L;
     }
-    __syncthreads();
+    lds_barrier();
     for (int i = tid; i < nout; i += kAttnThreads) {
         const int h = i / H2, d = 2 * (i - h * H2);
         const float* e = ml + 2 * h * S;
@@ -180,12 +191,16 @@ __device__ __forceinline__ void attn_merge_heads(const float* __restrict__ base,
         float2 o = make_float2(0.f, 0.f);
         int s = 0;
         if (i == tid) {
+            // every weight read from LDS before the first is used; splits past S keep o
+            float ev[PF];
 #pragma unroll
-            for (int u = 0; u < PF; u++)
-                if (u < S) {
-                    o.x = fmaf(ov[u].x, e[2 * u], o.x);
-                    o.y = fmaf(ov[u].y, e[2 * u], o.y);
-                }
+            for (int u = 0; u < PF; u++) ev[u] = e[2 * min(u, S - 1)];
+#pragma unroll
+            for (int u = 0; u < PF; u++) {
+                const float x = fmaf(ov[u].x, ev[u], o.x), y = fmaf(ov[u].y, ev[u], o.y);
+                o.x = u < S ? x : o.x;
+                o.y = u < S ? y : o.y;
+            }
             s = PF;
         }
         for (; s < S; s += 16) {  // splits past PF: sixteen loads in flight per round
