@@ -166,6 +166,7 @@ __global__ __launch_bounds__(256) void resid_norm_stats_rows_kernel(
     const int t = threadIdx.x;
     const size_t r = static_cast<size_t>(blockIdx.x) * n;
     double ss = 0.0;
+    float w0[kRowChunk];  // the norm weights of the first chunk, requested with its rows
     for (int c0 = 0; c0 < n; c0 += 256 * kRowChunk) {
         float a[kRowChunk], h[kRowChunk];
 #pragma unroll
@@ -173,6 +174,10 @@ __global__ __launch_bounds__(256) void resid_norm_stats_rows_kernel(
             const size_t i = r + min(c0 + t + 256 * q, n - 1);
             a[q] = P[i];
             h[q] = hin[i];
+        }
+        if (c0 == 0) {
+#pragma unroll
+            for (int q = 0; q < kRowChunk; q++) w0[q] = w && xn ? w[min(t + 256 * q, n - 1)] : 0.f;
         }
         for (int z = 1; z < splits; z++) {
 #pragma unroll
@@ -199,7 +204,7 @@ __global__ __launch_bounds__(256) void resid_norm_stats_rows_kernel(
     for (int c0 = 0; c0 < n; c0 += 256 * kRowChunk) {
         float wv[kRowChunk];
 #pragma unroll
-        for (int q = 0; q < kRowChunk; q++) wv[q] = w ? w[min(c0 + t + 256 * q, n - 1)] : 0.f;
+        for (int q = 0; q < kRowChunk; q++) wv[q] = c0 == 0 ? w0[q] : (w ? w[min(c0 + t + 256 * q, n - 1)] : 0.f);
 #pragma unroll
         for (int q = 0; q < kRowChunk; q++) {
             const int i = c0 + t + 256 * q;
